@@ -1,0 +1,194 @@
+/*
+ * obsidian_hip.h — C ABI of the MI355X (gfx950) MoE expert hot path.
+ *
+ * This is the kernel-dispatch boundary of the obsidian engine re-expressed as
+ * plain C: the Rust host (src/executor.rs, src/router.rs, src/forward.rs in the
+ * reference) binds these functions with `extern "C"` instead of building Metal
+ * pipelines. Every entry point names the reference interface it replaces.
+ *
+ * Conventions
+ *   - All tensor arguments are DEVICE pointers (HBM), caller-owned, unless a
+ *     comment says "host". Nothing here allocates on the hot path.
+ *   - bf16 values travel as uint16_t bit patterns, fp32 as float.
+ *   - Quantized tensors use the MLX affine layout (tools/split_experts.py:9-19):
+ *       weight uint32 [rows, cols*bits/32]: element c is bits-wide field c%(32/bits)
+ *         of word c/(32/bits), low bits first;
+ *       scales, biases bf16 [rows, cols/group];  w = q*scale + bias.
+ *     Expert tensors are stacked on a leading expert axis, as in the checkpoint's
+ *     model.layers.{l}.mlp.switch_mlp.{gate,up,down}_proj.{weight,scales,biases}.
+ *   - Calls are asynchronous and ordered on the context's stream (the Metal
+ *     same-queue FIFO order, forward.rs:2-3). obs_sync() is the drain.
+ *   - Return value: OBS_OK (0) or a negative OBS_E_* code; obs_last_error()
+ *     holds the message (the reference's Result<_, String>). Arguments are
+ *     validated before any launch; on error nothing is launched.
+ *   - One context per host thread; a context is not internally locked.
+ */
+#ifndef OBSIDIAN_HIP_H
+#define OBSIDIAN_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct obs_ctx obs_ctx;
+
+enum {
+  OBS_OK = 0,
+  OBS_E_INVALID = -1,     /* null pointer / bad enum / bad count */
+  OBS_E_SHAPE = -2,       /* shape not supported (e.g. cols % group != 0) */
+  OBS_E_ALIGN = -3,       /* pointer alignment requirement not met */
+  OBS_E_HIP = -4,         /* HIP runtime error */
+  OBS_E_NOMEM = -5,       /* allocation failed / workspace too small */
+  OBS_E_UNSUPPORTED = -6, /* no HIP device of the supported architecture */
+};
+
+/* ------------------------------------------------------------------ */
+/* Context / executor — replaces ObsidianExecutor (src/executor.rs:39-70) */
+/* ------------------------------------------------------------------ */
+
+/* Bind device `device`, check it is gfx950, create the context's stream.
+ * Replaces ObsidianExecutor::new (executor.rs:39-58): kernels are compiled
+ * offline into this library, so there is no runtime shader compilation. */
+int obs_create(int device, obs_ctx** out);
+void obs_destroy(obs_ctx* ctx);
+/* Last error message of this context (never NULL). Result<_, String>. */
+const char* obs_last_error(const obs_ctx* ctx);
+/* Message of the last failed obs_create on this thread. */
+const char* obs_create_error(void);
+/* Use a caller-owned hipStream_t (e.g. a graph-capturing stream) instead of
+ * the context's own; NULL restores the own stream. executor.rs:60-66 queue(). */
+int obs_set_stream(obs_ctx* ctx, void* hip_stream);
+void* obs_get_stream(const obs_ctx* ctx);
+
+/* ------------------------------------------------------------------ */
+/* Buffers — replace device().new_buffer / contents() / drain          */
+/* (forward.rs:264-286). HBM is not host-visible, so copies are explicit. */
+/* ------------------------------------------------------------------ */
+int obs_alloc(obs_ctx* ctx, size_t bytes, void** dptr);
+int obs_free(obs_ctx* ctx, void* dptr);
+/* host -> device, stream-ordered; returns when the host buffer may be reused */
+int obs_upload(obs_ctx* ctx, void* dst_dev, const void* src_host, size_t bytes);
+/* device -> host; waits for prior work on the stream (Buffer::contents after drain) */
+int obs_download(obs_ctx* ctx, void* dst_host, const void* src_dev, size_t bytes);
+int obs_memset(obs_ctx* ctx, void* dst_dev, int value, size_t bytes);
+/* Model::drain (forward.rs:282-286): wait for all work queued on the stream. */
+int obs_sync(obs_ctx* ctx);
+
+/* Stream-ordered timing with HIP events on the context's stream (no
+ * reference counterpart; the reference times with std::time::Instant,
+ * main.rs:102-115). obs_timer_stop waits and returns elapsed milliseconds. */
+int obs_timer_start(obs_ctx* ctx);
+int obs_timer_stop(obs_ctx* ctx, float* ms);
+
+/* ------------------------------------------------------------------ */
+/* Quantized tensor kernels                                            */
+/* ------------------------------------------------------------------ */
+
+/* Dequantize an MLX affine tensor (mx.dequantize, validate_dequant.py:21;
+ * the unpack of fused_dequant_matvec_4bit.metal:39-42 and forward.rs:451-457).
+ * bits 4 or 8; out_f32 [rows, cols] gets fl32(q*scale+bias) exactly;
+ * out_bf16 (optional, may be NULL) gets its round-to-nearest-even bf16.
+ * Either output may be NULL, not both. */
+int obs_dequant(obs_ctx* ctx, int bits, const uint32_t* w, const uint16_t* scales,
+                const uint16_t* biases, float* out_f32, uint16_t* out_bf16,
+                uint32_t rows, uint32_t cols, uint32_t group);
+
+/* y = dequant(W) . x for one token — Model::dequant (forward.rs:303-310) /
+ * fused_dequant_matvec_4bit.metal. W 4-bit [out, in]; x bf16 [in];
+ * y_f32 [out] (fp32 result, may be NULL) and/or y_bf16 [out] (may be NULL).
+ * fp32 accumulation; requires in % group == 0, in % 64 == 0. */
+int obs_q4_matvec(obs_ctx* ctx, const uint32_t* w, const uint16_t* scales,
+                  const uint16_t* biases, const uint16_t* x, float* y_f32,
+                  uint16_t* y_bf16, uint32_t in, uint32_t out, uint32_t group);
+
+/* Y[T, out] = X[T, in] . dequant(W)^T, bf16 in/out, fp32 accumulate — Model::matmul_raw
+ * (forward.rs:313-321) / matmul_dequant_4bit.metal. Runs the grouped
+ * dequant-to-LDS bf16 MFMA GEMM with a single group. */
+int obs_q4_matmul(obs_ctx* ctx, const uint32_t* w, const uint16_t* scales,
+                  const uint16_t* biases, const uint16_t* X, uint16_t* Y,
+                  uint32_t T, uint32_t in, uint32_t out, uint32_t group);
+
+/* ------------------------------------------------------------------ */
+/* Router — Model::gate_gpu (forward.rs:386-397) + MoeRouter (router.rs) */
+/* ------------------------------------------------------------------ */
+
+/* logits[T, n_exp] (fp32) = dequant8(Wg) . x[t] for T tokens — dequant_matvec_8bit.metal.
+ * Fixed reduction order: 64 lanes each own in/64 contiguous columns
+ * (serial fma), combined by an xor butterfly; bit-reproducible. */
+int obs_q8_gate_logits(obs_ctx* ctx, const uint32_t* w8, const uint16_t* scales,
+                       const uint16_t* biases, const uint16_t* x, float* logits,
+                       uint32_t T, uint32_t in, uint32_t n_exp, uint32_t group);
+
+/* Softmax over n_exp logits, top-k by repeated argmax (ties -> lower expert
+ * id), optional renormalisation — moe_routing_topk.metal:24-56 and
+ * MoeRouter::route_dispatch (router.rs:62-83). ids int32 [T, k], weights fp32 [T, k].
+ * n_exp <= 256 (the reference kernel's limit), 1 <= k <= min(n_exp, 64).
+ * A slot with no selectable expert (NaN logits) gets id -1 and weight 0.
+ * The synchronous MoeRouter::route (router.rs:25-56) is this call followed by
+ * obs_sync + obs_download. */
+int obs_route_topk(obs_ctx* ctx, const float* logits, int32_t* ids, float* weights,
+                   uint32_t T, uint32_t n_exp, uint32_t k, int norm_topk);
+
+/* ------------------------------------------------------------------ */
+/* Elementwise — ops.metal ew_swiglu / ew_scaled_add (forward.rs:370-380) */
+/* ------------------------------------------------------------------ */
+/* h = silu(g) * u, bf16 in/out, fp32 math */
+int obs_swiglu(obs_ctx* ctx, const uint16_t* g, const uint16_t* u, uint16_t* h, uint32_t n);
+/* acc = acc + scale * y in place, bf16, fp32 math */
+int obs_scaled_add(obs_ctx* ctx, uint16_t* acc, const uint16_t* y, float scale, uint32_t n);
+
+/* ------------------------------------------------------------------ */
+/* HBM-resident expert table + fused MoE layer                         */
+/* (replaces ExpertIndex / read_experts_parallel / expert_pool,        */
+/*  disk_io.rs:36-102, forward.rs:79-104)                              */
+/* ------------------------------------------------------------------ */
+
+typedef struct obs_moe_config {
+  uint32_t n_exp;    /* num_experts (model.rs:15), <= 256 */
+  uint32_t top_k;    /* num_experts_per_tok (model.rs:16) */
+  uint32_t hidden;   /* hidden_size */
+  uint32_t inter;    /* moe_intermediate_size (model.rs:17) */
+  uint32_t group;    /* quantization group size (64) */
+  int32_t norm_topk; /* norm_topk_prob (model.rs:22) */
+} obs_moe_config;
+
+/* One layer's MoE weights, all device pointers, stacked on the expert axis. */
+typedef struct obs_moe_layer {
+  const uint32_t* gate_w; const uint16_t* gate_s; const uint16_t* gate_b; /* [E, I, H/8], [E, I, H/G] */
+  const uint32_t* up_w;   const uint16_t* up_s;   const uint16_t* up_b;   /* [E, I, H/8], [E, I, H/G] */
+  const uint32_t* down_w; const uint16_t* down_s; const uint16_t* down_b; /* [E, H, I/8], [E, H, I/G] */
+  const uint32_t* router_w; const uint16_t* router_s; const uint16_t* router_b; /* 8-bit [E, H/4], [E, H/G] */
+} obs_moe_layer;
+
+/* Decode MoE half of one layer for one token (forward.rs:421-441):
+ * logits -> top-k -> per selected expert silu(gate x) * (up x) -> down ->
+ * weighted sum in rank order. x, y bf16 [hidden]. If residual is non-NULL,
+ * y = residual + sum (forward.rs:440 accumulates into the residual stream x1).
+ * ids_out [top_k] / w_out [top_k] (may be NULL) receive the routing.
+ * Workspace comes from the context (allocated once, on first use). */
+int obs_moe_decode(obs_ctx* ctx, const obs_moe_config* cfg, const obs_moe_layer* layer,
+                   const uint16_t* x, const uint16_t* residual, uint16_t* y,
+                   int32_t* ids_out, float* w_out);
+
+/* Workspace bytes obs_moe_prefill needs for T tokens. */
+size_t obs_moe_prefill_workspace(const obs_moe_config* cfg, uint32_t T);
+
+/* Grouped prefill MoE for T tokens (forward.rs:164-247): routing either
+ * computed from X (ids == NULL: router as obs_q8_gate_logits + obs_route_topk)
+ * or injected (ids, weights [T, top_k] device arrays; ids must be in range and
+ * distinct per token). Tokens are permuted into per-expert groups on the GPU,
+ * gate/up/down run as grouped dequant-to-LDS bf16 MFMA GEMMs with a SwiGLU
+ * epilogue, and outputs are combined per token in rank order in fp32.
+ * X, Y bf16 [T, hidden]; residual (nullable) as in obs_moe_decode.
+ * ws: caller-owned device workspace of obs_moe_prefill_workspace() bytes. */
+int obs_moe_prefill(obs_ctx* ctx, const obs_moe_config* cfg, const obs_moe_layer* layer,
+                    const uint16_t* X, const uint16_t* residual, uint16_t* Y, uint32_t T,
+                    const int32_t* ids, const float* weights, void* ws, size_t ws_bytes);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* OBSIDIAN_HIP_H */

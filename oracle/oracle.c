@@ -1,0 +1,583 @@
+/*
+ * oracle.c — CPU restatement of the obsidian MoE expert hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY (see oracle.h). Built with -ffp-contract=off so the
+ * rounding sequence is exactly the one written here; fused multiply-adds are
+ * spelled out with fmaf()/fma() where a documented order uses them.
+ *
+ * How each function is pinned (tests/test_oracle.py, tests/test_golden.py):
+ *   orc_bf16/f16 conversions .... exhaustive round trips over all 65536 patterns,
+ *                                 numpy float16 (RNE) on random floats, ties.
+ *   orc_dequant ................. known-answer words (0x76543210 -> q 0..7, all-0,
+ *                                 all-0xF), group boundaries 63/64, a numpy restatement
+ *                                 of validate_dequant.py:26-30 (independent code),
+ *                                 committed golden fixtures.
+ *   orc_qmatvec_* ............... one-hot x picks a column; fp64 brute force with
+ *                                 the bound |y - y64| <= gamma_K * sum|w x|;
+ *                                 _lanes with lanes=1 equals the serial fma loop.
+ *   orc_exp ..................... against libm expf/exp (<= 2 ulp on a dense grid),
+ *                                 exp(0) = 1 exactly, monotone on the grid.
+ *   orc_route_topk .............. brute force on tiny cases (sort by (-p, id)),
+ *                                 forced ties -> lowest id, permutation of logits
+ *                                 permutes ids, renormalised weights sum to 1,
+ *                                 closed form w_i = e_i / sum_sel e_j.
+ *   orc_moe_decode / _prefill ... one-hot routing weight reproduces one expert;
+ *                                 prefill with T=1 equals decode; linearity in the
+ *                                 routing weights; grouping invariants.
+ */
+#include "oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* ------------------------------------------------------------------------- */
+/* 16-bit floats                                                              */
+/* ------------------------------------------------------------------------- */
+
+static inline uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static inline float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+float orc_bf16_to_f32(uint16_t h) { return u2f((uint32_t)h << 16); }
+
+uint16_t orc_f32_to_bf16(float f) {
+  uint32_t u = f2u(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x0040u); /* quiet NaN */
+  u += 0x7fffu + ((u >> 16) & 1u);                                                 /* RNE */
+  return (uint16_t)(u >> 16);
+}
+
+float orc_f16_to_f32(uint16_t h) {
+  uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  uint32_t exp = (h >> 10) & 0x1fu, man = h & 0x3ffu;
+  if (exp == 0x1f) return u2f(sign | 0x7f800000u | (man << 13));
+  if (exp == 0) {
+    if (man == 0) return u2f(sign);
+    /* subnormal: value = man * 2^-24 (exact in fp32) */
+    float v = (float)man * 5.9604644775390625e-08f;
+    return (sign ? -v : v);
+  }
+  return u2f(sign | ((exp + 112u) << 23) | (man << 13));
+}
+
+uint16_t orc_f32_to_f16(float f) {
+  uint32_t u = f2u(f);
+  uint16_t sign = (uint16_t)((u >> 16) & 0x8000u);
+  uint32_t au = u & 0x7fffffffu;
+  if (au > 0x7f800000u) return (uint16_t)(sign | 0x7e00u | ((au >> 13) & 0x3ffu));
+  if (au >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u); /* >= 65520 rounds to inf */
+  if (au < 0x38800000u) {
+    /* result is f16-subnormal or zero: round |f| / 2^-24 to an integer, RNE */
+    float a = u2f(au) * 16777216.0f; /* exact scaling by 2^24 */
+    float r = rintf(a);              /* default rounding mode: nearest-even */
+    return (uint16_t)(sign | (uint16_t)r);
+  }
+  /* normal: drop 13 mantissa bits with RNE (carry may bump the exponent) */
+  uint32_t v = au - (112u << 23);
+  v += 0xfffu + ((v >> 13) & 1u);
+  return (uint16_t)(sign | (uint16_t)(v >> 13));
+}
+
+void orc_bf16_to_f32_n(const uint16_t* in, float* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = orc_bf16_to_f32(in[i]);
+}
+void orc_f32_to_bf16_n(const float* in, uint16_t* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = orc_f32_to_bf16(in[i]);
+}
+
+static inline float sb_to_f32(uint16_t v, int sb_type) {
+  return sb_type == ORC_SB_F16 ? orc_f16_to_f32(v) : orc_bf16_to_f32(v);
+}
+
+/* ------------------------------------------------------------------------- */
+/* dequant                                                                    */
+/* ------------------------------------------------------------------------- */
+
+/* Element c of a row: nibble c%8 of word c/8 (4-bit) or byte c%4 of word c/4
+ * (8-bit), low bits first — validate_dequant.py:26-29 and
+ * fused_dequant_matvec_4bit.metal:39-42 (byte view, little-endian). */
+static inline uint32_t q_at(int bits, const uint32_t* row, int64_t c) {
+  if (bits == 4) return (row[c >> 3] >> (4u * (uint32_t)(c & 7))) & 0xfu;
+  return (row[c >> 2] >> (8u * (uint32_t)(c & 3))) & 0xffu;
+}
+
+/* w = q*scale + bias in fp32. q*scale is exact (<= 8 bits x 11 bits), so this
+ * equals the fma form used by the shaders: one rounding, at the add. */
+static inline float dq(uint32_t q, float sc, float bi) { return (float)q * sc + bi; }
+
+static int check_shape(int bits, int64_t in, int group) {
+  if (bits != 4 && bits != 8) return -1;
+  if (group <= 0 || in <= 0 || in % group != 0) return -2;
+  if (in % (32 / bits) != 0) return -3;
+  return 0;
+}
+
+int orc_dequant(int bits, const uint32_t* w, const uint16_t* s, const uint16_t* b, int sb_type,
+                float* out, int64_t rows, int64_t cols, int group) {
+  int rc = check_shape(bits, cols, group);
+  if (rc) return rc;
+  const int64_t words = cols * bits / 32, groups = cols / group;
+  for (int64_t r = 0; r < rows; ++r) {
+    const uint32_t* wr = w + r * words;
+    for (int64_t c = 0; c < cols; ++c) {
+      const int64_t g = r * groups + c / group;
+      out[r * cols + c] = dq(q_at(bits, wr, c), sb_to_f32(s[g], sb_type), sb_to_f32(b[g], sb_type));
+    }
+  }
+  return 0;
+}
+
+/* ------------------------------------------------------------------------- */
+/* mat-vec                                                                    */
+/* ------------------------------------------------------------------------- */
+
+/* Reference shader order: acc += fl(w*x), columns 0..in-1
+ * (fused_dequant_matvec_4bit.metal:29-52: `acc += fma(w, x, 0.0f)`). */
+static float row_dot_shader(int bits, const uint32_t* wr, const uint16_t* sr, const uint16_t* br,
+                            int sb_type, const float* x, int64_t in, int group) {
+  float acc = 0.0f;
+  for (int64_t g = 0; g < in / group; ++g) {
+    const float sc = sb_to_f32(sr[g], sb_type), bi = sb_to_f32(br[g], sb_type);
+    for (int64_t j = 0; j < group; ++j) {
+      const int64_t c = g * group + j;
+      const float prod = dq(q_at(bits, wr, c), sc, bi) * x[c];
+      acc = acc + prod;
+    }
+  }
+  return acc;
+}
+
+int orc_qmatvec_shader(int bits, const uint32_t* w, const uint16_t* s, const uint16_t* b, int sb_type,
+                       const float* x, float* y, int64_t in, int64_t out, int group) {
+  int rc = check_shape(bits, in, group);
+  if (rc) return rc;
+  const int64_t words = in * bits / 32, groups = in / group;
+#pragma omp parallel for schedule(static)
+  for (int64_t o = 0; o < out; ++o)
+    y[o] = row_dot_shader(bits, w + o * words, s + o * groups, b + o * groups, sb_type, x, in, group);
+  return 0;
+}
+
+/* The documented lane order: lane l owns columns [l*in/L, (l+1)*in/L), serial
+ * fmaf accumulation; lanes combined by an xor butterfly with offsets L/2..1
+ * (every lane ends with the same value; lane 0's is returned). */
+static float row_dot_lanes(int bits, const uint32_t* wr, const uint16_t* sr, const uint16_t* br,
+                           int sb_type, const float* x, int64_t in, int group, int lanes) {
+  float part[256];
+  const int64_t chunk = in / lanes;
+  for (int l = 0; l < lanes; ++l) {
+    float acc = 0.0f;
+    for (int64_t c = l * chunk; c < (l + 1) * chunk; ++c) {
+      const int64_t g = c / group;
+      const float wv = dq(q_at(bits, wr, c), sb_to_f32(sr[g], sb_type), sb_to_f32(br[g], sb_type));
+      acc = fmaf(wv, x[c], acc);
+    }
+    part[l] = acc;
+  }
+  for (int off = lanes / 2; off >= 1; off >>= 1) {
+    float nxt[256];
+    for (int l = 0; l < lanes; ++l) nxt[l] = part[l] + part[l ^ off];
+    memcpy(part, nxt, sizeof(float) * (size_t)lanes);
+  }
+  return part[0];
+}
+
+int orc_qmatvec_lanes(int bits, const uint32_t* w, const uint16_t* s, const uint16_t* b, int sb_type,
+                      const float* x, float* y, int64_t in, int64_t out, int group, int lanes) {
+  int rc = check_shape(bits, in, group);
+  if (rc) return rc;
+  if (lanes < 1 || lanes > 256 || (lanes & (lanes - 1)) || in % lanes) return -4;
+  const int64_t words = in * bits / 32, groups = in / group;
+#pragma omp parallel for schedule(static)
+  for (int64_t o = 0; o < out; ++o)
+    y[o] = row_dot_lanes(bits, w + o * words, s + o * groups, b + o * groups, sb_type, x, in, group, lanes);
+  return 0;
+}
+
+int orc_qmatvec_f64(int bits, const uint32_t* w, const uint16_t* s, const uint16_t* b, int sb_type,
+                    const float* x, double* y, double* absbound, int64_t in, int64_t out, int group) {
+  int rc = check_shape(bits, in, group);
+  if (rc) return rc;
+  const int64_t words = in * bits / 32, groups = in / group;
+#pragma omp parallel for schedule(static)
+  for (int64_t o = 0; o < out; ++o) {
+    const uint32_t* wr = w + o * words;
+    double acc = 0.0, ab = 0.0;
+    for (int64_t c = 0; c < in; ++c) {
+      const int64_t g = o * groups + c / group;
+      const double t = (double)dq(q_at(bits, wr, c), sb_to_f32(s[g], sb_type), sb_to_f32(b[g], sb_type)) * (double)x[c];
+      acc += t;
+      ab += fabs(t);
+    }
+    y[o] = acc;
+    if (absbound) absbound[o] = ab;
+  }
+  return 0;
+}
+
+/* ------------------------------------------------------------------------- */
+/* router                                                                     */
+/* ------------------------------------------------------------------------- */
+
+/* exp(x) for the routing softmax and SwiGLU, written from the textbook method:
+ *   n = rint(x * log2(e)),  r = x - n*ln2 (Cody-Waite: ln2 = hi + lo, each
+ *   step one fma), exp(r) by the degree-7 Taylor polynomial in Horner form
+ *   (|r| <= ln2/2, truncation < 6e-9 relative), result = p * 2^n.
+ * Domain conventions: x < -86 -> +0 (keeps 2^n normal), x > 88.5 -> +inf,
+ * NaN -> NaN. Both the HIP kernels and this oracle evaluate exactly these
+ * operations, so their results are bit-identical. */
+float orc_exp(float x) {
+  if (x != x) return x;
+  if (x < -86.0f) return 0.0f;
+  if (x > 88.5f) return INFINITY;
+  const float LOG2E = 1.44269502162933349609375f;   /* fl32(1/ln 2) */
+  const float LN2_HI = 0.693145751953125f;           /* ln2 rounded to 16 significant bits */
+  const float LN2_LO = 1.428606765330187045e-06f;    /* fl32(ln2 - LN2_HI) */
+  const float n = rintf(x * LOG2E);
+  float r = fmaf(-n, LN2_HI, x);
+  r = fmaf(-n, LN2_LO, r);
+  float p = 1.98412698e-04f;                 /* 1/7! */
+  p = fmaf(p, r, 1.38888889e-03f);           /* 1/6! */
+  p = fmaf(p, r, 8.33333333e-03f);           /* 1/5! */
+  p = fmaf(p, r, 4.16666667e-02f);           /* 1/4! */
+  p = fmaf(p, r, 1.66666667e-01f);           /* 1/3! */
+  p = fmaf(p, r, 0.5f);
+  p = fmaf(p, r, 1.0f);
+  p = fmaf(p, r, 1.0f);
+  int ni = (int)n;
+  if (ni > 127) { p = p * 2.0f; ni -= 1; }
+  return p * u2f((uint32_t)(ni + 127) << 23);
+}
+
+/* moe_routing_topk.metal:31-56 for one token. */
+static void route_one(const float* l, int n, int k, int norm_topk, int sum_order, int emulate_f16,
+                      int32_t* ids, float* w) {
+  float p[1024];
+  float mx = -INFINITY;
+  for (int i = 0; i < n; ++i) mx = fmaxf(mx, l[i]);
+  for (int i = 0; i < n; ++i) p[i] = orc_exp(l[i] - mx);
+  float sum = 0.0f;
+  if (sum_order == ORC_SUM_SERIAL) {
+    for (int i = 0; i < n; ++i) sum = sum + p[i];
+  } else {
+    float part[64];
+    for (int ln = 0; ln < 64; ++ln) {
+      float a = 0.0f;
+      for (int j = ln; j < n; j += 64) a = a + p[j];
+      part[ln] = a;
+    }
+    for (int off = 32; off >= 1; off >>= 1) {
+      float nxt[64];
+      for (int ln = 0; ln < 64; ++ln) nxt[ln] = part[ln] + part[ln ^ off];
+      memcpy(part, nxt, sizeof part);
+    }
+    sum = part[0];
+  }
+  for (int i = 0; i < n; ++i) p[i] = p[i] / sum;
+  float wsum = 0.0f;
+  for (int kk = 0; kk < k; ++kk) {
+    float best = -INFINITY;
+    int bi = -1;
+    for (int i = 0; i < n; ++i)
+      if (p[i] > best) { best = p[i]; bi = i; }
+    if (bi < 0) { ids[kk] = -1; w[kk] = 0.0f; continue; }
+    ids[kk] = bi;
+    w[kk] = emulate_f16 ? orc_f16_to_f32(orc_f32_to_f16(best)) : best;
+    wsum = wsum + best;
+    p[bi] = -INFINITY;
+  }
+  if (norm_topk && wsum > 0.0f) {
+    for (int kk = 0; kk < k; ++kk) {
+      if (ids[kk] < 0) continue;
+      const float q = w[kk] / wsum;
+      w[kk] = emulate_f16 ? orc_f16_to_f32(orc_f32_to_f16(q)) : q;
+    }
+  }
+}
+
+int orc_route_topk(const float* logits, int64_t T, int n_exp, int k, int norm_topk,
+                   int sum_order, int emulate_f16, int32_t* ids, float* w) {
+  if (n_exp < 1 || n_exp > 256 || k < 1 || k > n_exp) return -1;
+  if (sum_order != ORC_SUM_SERIAL && sum_order != ORC_SUM_WAVE) return -2;
+  for (int64_t t = 0; t < T; ++t)
+    route_one(logits + t * n_exp, n_exp, k, norm_topk, sum_order, emulate_f16, ids + t * k, w + t * k);
+  return 0;
+}
+
+/* ------------------------------------------------------------------------- */
+/* elementwise                                                                */
+/* ------------------------------------------------------------------------- */
+
+/* ops.metal:21: silu(g)*u = (g / (1 + exp(-g))) * u */
+float orc_silu_mul(float g, float u) { return (g / (1.0f + orc_exp(-g))) * u; }
+
+void orc_swiglu(const float* g, const float* u, float* h, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) h[i] = orc_silu_mul(g[i], u[i]);
+}
+
+/* ops.metal:28: acc = acc + scale*y */
+void orc_scaled_add(float* acc, const float* y, float scale, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) acc[i] = acc[i] + scale * y[i];
+}
+
+/* ------------------------------------------------------------------------- */
+/* layer compositions                                                         */
+/* ------------------------------------------------------------------------- */
+
+static inline double silu_mul_d(double g, double u) { return g / (1.0 + exp(-g)) * u; }
+
+int orc_router(const orc_layer* L, const uint16_t* x_bf16, int64_t T, int k, int norm_topk,
+               float* logits_out, int32_t* ids, float* w) {
+  const int E = L->n_exp, H = L->hidden;
+  float* x = (float*)malloc(sizeof(float) * (size_t)H);
+  float* lg = (float*)malloc(sizeof(float) * (size_t)E * (size_t)T);
+  int rc = 0;
+  for (int64_t t = 0; t < T && !rc; ++t) {
+    orc_bf16_to_f32_n(x_bf16 + t * H, x, H);
+    rc = orc_qmatvec_lanes(8, L->router_w, L->router_s, L->router_b, ORC_SB_BF16, x, lg + t * E, H, E, L->group, 64);
+  }
+  if (!rc) rc = orc_route_topk(lg, T, E, k, norm_topk, ORC_SUM_WAVE, 0, ids, w);
+  if (!rc && logits_out) memcpy(logits_out, lg, sizeof(float) * (size_t)E * (size_t)T);
+  free(x);
+  free(lg);
+  return rc;
+}
+
+/* One expert's FFN in fp64 on the exact fp32 weights: y = Wd (silu(Wg x) * (Wu x)). */
+static void expert_f64(const orc_layer* L, int e, const float* x, double* y) {
+  const int H = L->hidden, I = L->inter, G = L->group;
+  const size_t gw = (size_t)I * H / 8, gs = (size_t)I * H / G, dw = (size_t)H * I / 8, ds = (size_t)H * I / G;
+  double* g = (double*)malloc(sizeof(double) * I);
+  double* u = (double*)malloc(sizeof(double) * I);
+  float* h = (float*)malloc(sizeof(float) * I);
+  double* hd = (double*)malloc(sizeof(double) * I);
+  orc_qmatvec_f64(4, L->gate_w + e * gw, L->gate_s + e * gs, L->gate_b + e * gs, ORC_SB_BF16, x, g, NULL, H, I, G);
+  orc_qmatvec_f64(4, L->up_w + e * gw, L->up_s + e * gs, L->up_b + e * gs, ORC_SB_BF16, x, u, NULL, H, I, G);
+  for (int i = 0; i < I; ++i) hd[i] = silu_mul_d(g[i], u[i]);
+  /* down projection on the fp64 h: accumulate exactly in fp64 */
+  const uint32_t* W = L->down_w + e * dw;
+  const uint16_t* S = L->down_s + e * ds;
+  const uint16_t* B = L->down_b + e * ds;
+  for (int o = 0; o < H; ++o) {
+    double acc = 0.0;
+    for (int c = 0; c < I; ++c) {
+      const int64_t gi = (int64_t)o * (I / G) + c / G;
+      const float wv = dq(q_at(4, W + (size_t)o * (I / 8), c), orc_bf16_to_f32(S[gi]), orc_bf16_to_f32(B[gi]));
+      acc += (double)wv * hd[c];
+    }
+    y[o] = acc;
+  }
+  (void)h;
+  free(g); free(u); free(h); free(hd);
+}
+
+/* One expert in the reference engine's rounding sequence (forward.rs:436-440):
+ * g,u = f16(serial fp32 dot); h = f16(silu(g)*u); y = f16(serial fp32 dot). */
+static void expert_shader_f16(const orc_layer* L, int e, const float* x, float* y) {
+  const int H = L->hidden, I = L->inter, G = L->group;
+  const size_t gw = (size_t)I * H / 8, gs = (size_t)I * H / G, dw = (size_t)H * I / 8, ds = (size_t)H * I / G;
+  float* g = (float*)malloc(sizeof(float) * I);
+  float* u = (float*)malloc(sizeof(float) * I);
+  float* h = (float*)malloc(sizeof(float) * I);
+  orc_qmatvec_shader(4, L->gate_w + e * gw, L->gate_s + e * gs, L->gate_b + e * gs, ORC_SB_BF16, x, g, H, I, G);
+  orc_qmatvec_shader(4, L->up_w + e * gw, L->up_s + e * gs, L->up_b + e * gs, ORC_SB_BF16, x, u, H, I, G);
+  for (int i = 0; i < I; ++i) {
+    const float gf = orc_f16_to_f32(orc_f32_to_f16(g[i])), uf = orc_f16_to_f32(orc_f32_to_f16(u[i]));
+    h[i] = orc_f16_to_f32(orc_f32_to_f16(orc_silu_mul(gf, uf)));
+  }
+  orc_qmatvec_shader(4, L->down_w + e * dw, L->down_s + e * ds, L->down_b + e * ds, ORC_SB_BF16, h, y, I, H, G);
+  for (int o = 0; o < H; ++o) y[o] = orc_f16_to_f32(orc_f32_to_f16(y[o]));
+  free(g); free(u); free(h);
+}
+
+int orc_moe_decode(const orc_layer* L, const uint16_t* x_bf16, int64_t T, int k, int norm_topk,
+                   const int32_t* ids_in, const float* w_in, int32_t* ids_out, float* w_out,
+                   int mode, double* y_out) {
+  const int H = L->hidden, E = L->n_exp;
+  if (mode != ORC_MODE_F64 && mode != ORC_MODE_SHADER_F16) return -1;
+  const int32_t* ids = ids_in;
+  const float* w = w_in;
+  if (!ids_in) {
+    int rc = orc_router(L, x_bf16, T, k, norm_topk, NULL, ids_out, w_out);
+    if (rc) return rc;
+    ids = ids_out;
+    w = w_out;
+  }
+  float* x = (float*)malloc(sizeof(float) * H);
+  double* yd = (double*)malloc(sizeof(double) * H);
+  float* yf = (float*)malloc(sizeof(float) * H);
+  float* acc = (float*)malloc(sizeof(float) * H);
+  for (int64_t t = 0; t < T; ++t) {
+    orc_bf16_to_f32_n(x_bf16 + t * H, x, H);
+    double* out = y_out + t * H;
+    for (int o = 0; o < H; ++o) { out[o] = 0.0; acc[o] = 0.0f; }
+    for (int r = 0; r < k; ++r) {
+      const int e = ids[t * k + r];
+      if (e < 0 || e >= E) continue;
+      const float wr = w[t * k + r];
+      if (mode == ORC_MODE_F64) {
+        expert_f64(L, e, x, yd);
+        for (int o = 0; o < H; ++o) out[o] += (double)wr * yd[o];
+      } else {
+        expert_shader_f16(L, e, x, yf);
+        /* ew_scaled_add into an f16 accumulator, ranks in order (forward.rs:440) */
+        for (int o = 0; o < H; ++o) acc[o] = orc_f16_to_f32(orc_f32_to_f16(acc[o] + wr * yf[o]));
+      }
+    }
+    if (mode == ORC_MODE_SHADER_F16)
+      for (int o = 0; o < H; ++o) out[o] = acc[o];
+  }
+  free(x); free(yd); free(yf); free(acc);
+  return 0;
+}
+
+int orc_group_rows(const int32_t* ids, int64_t T, int k, int n_exp,
+                   int32_t* counts, int32_t* offsets, int32_t* row_token, int32_t* slot_row) {
+  for (int e = 0; e < n_exp; ++e) counts[e] = 0;
+  for (int64_t i = 0; i < T * k; ++i) {
+    if (ids[i] < 0 || ids[i] >= n_exp) return -1;
+    counts[ids[i]]++;
+  }
+  offsets[0] = 0;
+  for (int e = 0; e < n_exp; ++e) offsets[e + 1] = offsets[e] + counts[e];
+  int32_t* fill = (int32_t*)calloc((size_t)n_exp, sizeof(int32_t));
+  /* tokens in ascending order within each expert (forward.rs:203-204) */
+  for (int64_t t = 0; t < T; ++t)
+    for (int r = 0; r < k; ++r) {
+      const int e = ids[t * k + r];
+      const int row = offsets[e] + fill[e]++;
+      row_token[row] = (int32_t)t;
+      slot_row[t * k + r] = row;
+    }
+  free(fill);
+  return 0;
+}
+
+int orc_moe_prefill(const orc_layer* L, const uint16_t* x_bf16, int64_t T, int k,
+                    const int32_t* ids, const float* w, int mode, double* y_out) {
+  const int H = L->hidden, I = L->inter, E = L->n_exp, G = L->group;
+  if (mode != ORC_MODE_F64 && mode != ORC_MODE_MFMA_BF16) return -1;
+  const size_t gw = (size_t)I * H / 8, gs = (size_t)I * H / G, dw = (size_t)H * I / 8, ds = (size_t)H * I / G;
+  int32_t* counts = (int32_t*)malloc(sizeof(int32_t) * E);
+  int32_t* offsets = (int32_t*)malloc(sizeof(int32_t) * (E + 1));
+  int32_t* row_token = (int32_t*)malloc(sizeof(int32_t) * (size_t)(T * k));
+  int32_t* slot_row = (int32_t*)malloc(sizeof(int32_t) * (size_t)(T * k));
+  if (orc_group_rows(ids, T, k, E, counts, offsets, row_token, slot_row)) {
+    free(counts); free(offsets); free(row_token); free(slot_row);
+    return -2;
+  }
+  const int64_t R = T * k;
+  /* per-row expert outputs [R, H] */
+  double* Y = (double*)malloc(sizeof(double) * (size_t)R * H);
+  const int bf = (mode == ORC_MODE_MFMA_BF16);
+#pragma omp parallel
+  {
+    float* x = (float*)malloc(sizeof(float) * H);
+    double* g = (double*)malloc(sizeof(double) * I);
+    double* u = (double*)malloc(sizeof(double) * I);
+    double* h = (double*)malloc(sizeof(double) * I);
+    float* wrow = (float*)malloc(sizeof(float) * (H > I ? H : I));
+#pragma omp for schedule(dynamic, 4)
+    for (int64_t row = 0; row < R; ++row) {
+      int e = 0;
+      while (offsets[e + 1] <= row) ++e;
+      const int64_t t = row_token[row];
+      orc_bf16_to_f32_n(x_bf16 + t * H, x, H);
+      for (int pj = 0; pj < 2; ++pj) {
+        const uint32_t* W = (pj ? L->up_w : L->gate_w) + e * gw;
+        const uint16_t* S = (pj ? L->up_s : L->gate_s) + e * gs;
+        const uint16_t* B = (pj ? L->up_b : L->gate_b) + e * gs;
+        double* dst = pj ? u : g;
+        for (int o = 0; o < I; ++o) {
+          orc_dequant(4, W + (size_t)o * (H / 8), S + (size_t)o * (H / G), B + (size_t)o * (H / G), ORC_SB_BF16, wrow, 1, H, G);
+          double acc = 0.0;
+          for (int c = 0; c < H; ++c) {
+            const float wv = bf ? orc_bf16_to_f32(orc_f32_to_bf16(wrow[c])) : wrow[c];
+            acc += (double)wv * (double)x[c];
+          }
+          dst[o] = acc;
+        }
+      }
+      for (int i = 0; i < I; ++i) {
+        if (bf) {
+          const float hv = orc_silu_mul((float)g[i], (float)u[i]);
+          h[i] = (double)orc_bf16_to_f32(orc_f32_to_bf16(hv));
+        } else {
+          h[i] = silu_mul_d(g[i], u[i]);
+        }
+      }
+      const uint32_t* W = L->down_w + e * dw;
+      const uint16_t* S = L->down_s + e * ds;
+      const uint16_t* B = L->down_b + e * ds;
+      for (int o = 0; o < H; ++o) {
+        orc_dequant(4, W + (size_t)o * (I / 8), S + (size_t)o * (I / G), B + (size_t)o * (I / G), ORC_SB_BF16, wrow, 1, I, G);
+        double acc = 0.0;
+        for (int c = 0; c < I; ++c) {
+          const float wv = bf ? orc_bf16_to_f32(orc_f32_to_bf16(wrow[c])) : wrow[c];
+          acc += (double)wv * h[c];
+        }
+        Y[row * H + o] = bf ? (double)orc_bf16_to_f32(orc_f32_to_bf16((float)acc)) : acc;
+      }
+    }
+    free(x); free(g); free(u); free(h); free(wrow);
+  }
+  /* un-permute and combine in rank order (forward.rs:225-232) */
+  for (int64_t t = 0; t < T; ++t) {
+    for (int o = 0; o < H; ++o) {
+      if (bf) {
+        float acc = 0.0f;
+        for (int r = 0; r < k; ++r) acc = fmaf(w[t * k + r], (float)Y[(int64_t)slot_row[t * k + r] * H + o], acc);
+        y_out[t * H + o] = acc;
+      } else {
+        double acc = 0.0;
+        for (int r = 0; r < k; ++r) acc += (double)w[t * k + r] * Y[(int64_t)slot_row[t * k + r] * H + o];
+        y_out[t * H + o] = acc;
+      }
+    }
+  }
+  free(Y); free(counts); free(offsets); free(row_token); free(slot_row);
+  return 0;
+}
+
+/* ------------------------------------------------------------------------- */
+/* CPU baseline: decode MoE half of one token, reference shader semantics    */
+/* ------------------------------------------------------------------------- */
+
+int orc_moe_decode_baseline(const orc_layer* L, const uint16_t* x_bf16, int k, int norm_topk,
+                            int nthreads, int32_t* ids, float* w, float* y) {
+#ifdef _OPENMP
+  if (nthreads > 0) omp_set_num_threads(nthreads);
+#else
+  (void)nthreads;
+#endif
+  const int H = L->hidden, I = L->inter, E = L->n_exp, G = L->group;
+  const size_t gw = (size_t)I * H / 8, gs = (size_t)I * H / G, dw = (size_t)H * I / 8, ds = (size_t)H * I / G;
+  float x[8192], lg[256], g[4096], u[4096], h[4096], ye[8192];
+  if (H > 8192 || I > 4096 || E > 256) return -1;
+  orc_bf16_to_f32_n(x_bf16, x, H);
+  /* dequant_matvec_8bit (serial per row) then moe_routing_topk */
+  orc_qmatvec_shader(8, L->router_w, L->router_s, L->router_b, ORC_SB_BF16, x, lg, H, E, G);
+  orc_route_topk(lg, 1, E, k, norm_topk, ORC_SUM_SERIAL, 0, ids, w);
+  for (int o = 0; o < H; ++o) y[o] = 0.0f;
+  for (int r = 0; r < k; ++r) {
+    const int e = ids[r];
+    if (e < 0) continue;
+    orc_qmatvec_shader(4, L->gate_w + e * gw, L->gate_s + e * gs, L->gate_b + e * gs, ORC_SB_BF16, x, g, H, I, G);
+    orc_qmatvec_shader(4, L->up_w + e * gw, L->up_s + e * gs, L->up_b + e * gs, ORC_SB_BF16, x, u, H, I, G);
+    orc_swiglu(g, u, h, I);
+    orc_qmatvec_shader(4, L->down_w + e * dw, L->down_s + e * ds, L->down_b + e * ds, ORC_SB_BF16, h, ye, I, H, G);
+    orc_scaled_add(y, ye, w[r], H);
+  }
+  return 0;
+}
+
+int orc_omp_max_threads(void) {
+#ifdef _OPENMP
+  return omp_get_max_threads();
+#else
+  return 1;
+#endif
+}

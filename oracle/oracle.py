@@ -1,0 +1,232 @@
+"""ctypes wrapper of liboracle.so — the CPU restatement of the MoE hot path.
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, by the smoke check and by the
+CPU-baseline leg of bench.py, never by the product library.
+
+Also holds `dequant_numpy`, an independent NumPy restatement of the reference's
+own replica (validate_dequant.py:26-30), used to pin the C dequant.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+from typing import Dict, Optional, Tuple
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+
+SB_BF16, SB_F16 = 0, 1
+SUM_SERIAL, SUM_WAVE = 0, 1
+MODE_F64, MODE_SHADER_F16, MODE_MFMA_BF16 = 0, 1, 2
+
+
+def build() -> None:
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+class OrcLayer(C.Structure):
+    _fields_ = [("n_exp", C.c_int32), ("hidden", C.c_int32), ("inter", C.c_int32), ("group", C.c_int32)] + [
+        (n, C.c_void_p) for n in ("gate_w", "gate_s", "gate_b", "up_w", "up_s", "up_b", "down_w", "down_s",
+                                  "down_b", "router_w", "router_s", "router_b")]
+
+
+_L = None
+
+
+def lib() -> C.CDLL:
+    global _L
+    if _L is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = C.CDLL(LIB_PATH)
+        vp, i64, i32 = C.c_void_p, C.c_int64, C.c_int
+        L.orc_bf16_to_f32.restype = C.c_float
+        L.orc_bf16_to_f32.argtypes = [C.c_uint16]
+        L.orc_f32_to_bf16.restype = C.c_uint16
+        L.orc_f32_to_bf16.argtypes = [C.c_float]
+        L.orc_f16_to_f32.restype = C.c_float
+        L.orc_f16_to_f32.argtypes = [C.c_uint16]
+        L.orc_f32_to_f16.restype = C.c_uint16
+        L.orc_f32_to_f16.argtypes = [C.c_float]
+        L.orc_exp.restype = C.c_float
+        L.orc_exp.argtypes = [C.c_float]
+        L.orc_silu_mul.restype = C.c_float
+        L.orc_silu_mul.argtypes = [C.c_float, C.c_float]
+        L.orc_dequant.argtypes = [i32, vp, vp, vp, i32, vp, i64, i64, i32]
+        L.orc_qmatvec_shader.argtypes = [i32, vp, vp, vp, i32, vp, vp, i64, i64, i32]
+        L.orc_qmatvec_lanes.argtypes = [i32, vp, vp, vp, i32, vp, vp, i64, i64, i32, i32]
+        L.orc_qmatvec_f64.argtypes = [i32, vp, vp, vp, i32, vp, vp, vp, i64, i64, i32]
+        L.orc_route_topk.argtypes = [vp, i64, i32, i32, i32, i32, i32, vp, vp]
+        L.orc_router.argtypes = [C.POINTER(OrcLayer), vp, i64, i32, i32, vp, vp, vp]
+        L.orc_moe_decode.argtypes = [C.POINTER(OrcLayer), vp, i64, i32, i32, vp, vp, vp, vp, i32, vp]
+        L.orc_group_rows.argtypes = [vp, i64, i32, i32, vp, vp, vp, vp]
+        L.orc_moe_prefill.argtypes = [C.POINTER(OrcLayer), vp, i64, i32, vp, vp, i32, vp]
+        L.orc_moe_decode_baseline.argtypes = [C.POINTER(OrcLayer), vp, i32, i32, i32, vp, vp, vp]
+        L.orc_omp_max_threads.restype = C.c_int
+        _L = L
+    return _L
+
+
+def _p(a: Optional[np.ndarray]):
+    return None if a is None else a.ctypes.data
+
+
+def _c(a, dtype) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=dtype)
+
+
+def _rc(rc: int, what: str) -> None:
+    if rc != 0:
+        raise ValueError(f"{what}: oracle rejected the arguments (rc={rc})")
+
+
+# ---- scalars ---------------------------------------------------------------
+def bf16_to_f32(h: int) -> float:
+    return lib().orc_bf16_to_f32(h)
+
+
+def f32_to_bf16(f: float) -> int:
+    return lib().orc_f32_to_bf16(f)
+
+
+def f16_to_f32(h: int) -> float:
+    return lib().orc_f16_to_f32(h)
+
+
+def f32_to_f16(f: float) -> int:
+    return lib().orc_f32_to_f16(f)
+
+
+def exp(x: float) -> float:
+    return lib().orc_exp(x)
+
+
+def silu_mul(g: float, u: float) -> float:
+    return lib().orc_silu_mul(g, u)
+
+
+# ---- tensors ---------------------------------------------------------------
+def dequant(bits: int, w, s, b, rows: int, cols: int, group: int = 64, sb_type: int = SB_BF16) -> np.ndarray:
+    w, s, b = _c(w, np.uint32), _c(s, np.uint16), _c(b, np.uint16)
+    out = np.empty((rows, cols), np.float32)
+    _rc(lib().orc_dequant(bits, _p(w), _p(s), _p(b), sb_type, _p(out), rows, cols, group), "dequant")
+    return out
+
+
+def qmatvec(kind: str, bits: int, w, s, b, x_f32, in_f: int, out_f: int, group: int = 64, lanes: int = 64,
+            sb_type: int = SB_BF16):
+    """kind: 'shader' | 'lanes' -> fp32 y; 'f64' -> (y f64, absbound f64)."""
+    w, s, b, x = _c(w, np.uint32), _c(s, np.uint16), _c(b, np.uint16), _c(x_f32, np.float32)
+    L = lib()
+    if kind == "f64":
+        y = np.empty(out_f, np.float64)
+        ab = np.empty(out_f, np.float64)
+        _rc(L.orc_qmatvec_f64(bits, _p(w), _p(s), _p(b), sb_type, _p(x), _p(y), _p(ab), in_f, out_f, group), kind)
+        return y, ab
+    y = np.empty(out_f, np.float32)
+    if kind == "shader":
+        _rc(L.orc_qmatvec_shader(bits, _p(w), _p(s), _p(b), sb_type, _p(x), _p(y), in_f, out_f, group), kind)
+    elif kind == "lanes":
+        _rc(L.orc_qmatvec_lanes(bits, _p(w), _p(s), _p(b), sb_type, _p(x), _p(y), in_f, out_f, group, lanes), kind)
+    else:
+        raise ValueError(kind)
+    return y
+
+
+def route_topk(logits, k: int, norm_topk: bool = True, sum_order: int = SUM_WAVE,
+               emulate_f16: bool = False) -> Tuple[np.ndarray, np.ndarray]:
+    lg = _c(logits, np.float32)
+    if lg.ndim == 1:
+        lg = lg[None, :]
+    T, n = lg.shape
+    ids = np.empty((T, k), np.int32)
+    w = np.empty((T, k), np.float32)
+    _rc(lib().orc_route_topk(_p(lg), T, n, k, int(norm_topk), sum_order, int(emulate_f16), _p(ids), _p(w)),
+        "route_topk")
+    return ids, w
+
+
+class Layer:
+    """Keeps numpy arrays alive and exposes the orc_layer struct."""
+
+    def __init__(self, t: Dict[str, np.ndarray], n_exp: int, hidden: int, inter: int, group: int = 64):
+        self.arrs = {k: np.ascontiguousarray(v) for k, v in t.items()}
+        self.s = OrcLayer(n_exp, hidden, inter, group, *[self.arrs[k].ctypes.data for k in (
+            "gate_w", "gate_s", "gate_b", "up_w", "up_s", "up_b", "down_w", "down_s", "down_b",
+            "router_w", "router_s", "router_b")])
+        self.n_exp, self.hidden, self.inter, self.group = n_exp, hidden, inter, group
+
+
+def router(layer: Layer, x_bf16, k: int, norm_topk: bool = True):
+    x = _c(x_bf16, np.uint16).reshape(-1, layer.hidden)
+    T = x.shape[0]
+    lg = np.empty((T, layer.n_exp), np.float32)
+    ids = np.empty((T, k), np.int32)
+    w = np.empty((T, k), np.float32)
+    _rc(lib().orc_router(C.byref(layer.s), _p(x), T, k, int(norm_topk), _p(lg), _p(ids), _p(w)), "router")
+    return lg, ids, w
+
+
+def moe_decode(layer: Layer, x_bf16, k: int, norm_topk: bool = True, ids=None, w=None, mode: int = MODE_F64):
+    x = _c(x_bf16, np.uint16).reshape(-1, layer.hidden)
+    T = x.shape[0]
+    y = np.empty((T, layer.hidden), np.float64)
+    ids_o = np.empty((T, k), np.int32)
+    w_o = np.empty((T, k), np.float32)
+    ids_i = None if ids is None else _c(ids, np.int32).reshape(T, k)
+    w_i = None if w is None else _c(w, np.float32).reshape(T, k)
+    _rc(lib().orc_moe_decode(C.byref(layer.s), _p(x), T, k, int(norm_topk), _p(ids_i), _p(w_i), _p(ids_o),
+                             _p(w_o), mode, _p(y)), "moe_decode")
+    if ids is None:
+        return y, ids_o, w_o
+    return y, ids_i, w_i
+
+
+def group_rows(ids, n_exp: int):
+    ids = _c(ids, np.int32)
+    T, k = ids.shape
+    counts = np.empty(n_exp, np.int32)
+    offsets = np.empty(n_exp + 1, np.int32)
+    row_token = np.empty(T * k, np.int32)
+    slot_row = np.empty(T * k, np.int32)
+    _rc(lib().orc_group_rows(_p(ids), T, k, n_exp, _p(counts), _p(offsets), _p(row_token), _p(slot_row)),
+        "group_rows")
+    return counts, offsets, row_token, slot_row
+
+
+def moe_prefill(layer: Layer, X_bf16, ids, w, mode: int = MODE_F64) -> np.ndarray:
+    X = _c(X_bf16, np.uint16).reshape(-1, layer.hidden)
+    T = X.shape[0]
+    ids, w = _c(ids, np.int32), _c(w, np.float32)
+    k = ids.shape[1]
+    y = np.empty((T, layer.hidden), np.float64)
+    _rc(lib().orc_moe_prefill(C.byref(layer.s), _p(X), T, k, _p(ids), _p(w), mode, _p(y)), "moe_prefill")
+    return y
+
+
+def moe_decode_baseline(layer: Layer, x_bf16, k: int, norm_topk: bool = True, nthreads: int = 0):
+    x = _c(x_bf16, np.uint16).reshape(layer.hidden)
+    ids = np.empty(k, np.int32)
+    w = np.empty(k, np.float32)
+    y = np.empty(layer.hidden, np.float32)
+    _rc(lib().orc_moe_decode_baseline(C.byref(layer.s), _p(x), k, int(norm_topk), nthreads, _p(ids), _p(w), _p(y)),
+        "baseline")
+    return ids, w, y
+
+
+def omp_max_threads() -> int:
+    return lib().orc_omp_max_threads()
+
+
+# ---- independent NumPy restatement (validate_dequant.py:26-30) --------------
+def dequant_numpy(W: np.ndarray, S_f32: np.ndarray, B_f32: np.ndarray, group: int = 64) -> np.ndarray:
+    """nibble j of uint32 word = (word >> 4j) & 0xF; element i at word i//8,
+    nibble i%8; value = nibble*scale[g] + bias[g] (fp32)."""
+    Wn = np.asarray(W).astype(np.uint32)
+    out_f = Wn.shape[0]
+    in_f = Wn.shape[1] * 8
+    nib = np.stack([(Wn >> (4 * j)) & 0xF for j in range(8)], -1).reshape(out_f, in_f).astype(np.float32)
+    return nib * np.repeat(S_f32, group, axis=1) + np.repeat(B_f32, group, axis=1)

@@ -1,0 +1,162 @@
+// obs_context.hip — context, buffers, stream, timing: the HIP replacement of
+// ObsidianExecutor (src/executor.rs:39-70) and the Model buffer helpers
+// (src/forward.rs:264-286).
+#include <cstdlib>
+#include <cstring>
+
+#include "obs_internal.hpp"
+
+namespace {
+thread_local std::string g_create_error;
+}
+
+namespace obs {
+
+int set_error(obs_ctx* ctx, int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  if (ctx) ctx->err = buf;
+  return code;
+}
+
+int ensure_decode_ws(obs_ctx* ctx, size_t bytes, void** out) {
+  if (ctx->decode_ws_bytes < bytes) {
+    if (ctx->decode_ws) {
+      OBS_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+      OBS_HIP_TRY(ctx, hipFree(ctx->decode_ws));
+      ctx->decode_ws = nullptr;
+      ctx->decode_ws_bytes = 0;
+    }
+    size_t sz = (bytes + 4095) & ~size_t(4095);
+    OBS_HIP_TRY(ctx, hipMalloc(&ctx->decode_ws, sz));
+    OBS_HIP_TRY(ctx, hipMemset(ctx->decode_ws, 0, sz));
+    ctx->decode_ws_bytes = sz;
+  }
+  *out = ctx->decode_ws;
+  return OBS_OK;
+}
+
+}  // namespace obs
+
+extern "C" {
+
+const char* obs_create_error(void) { return g_create_error.c_str(); }
+
+int obs_create(int device, obs_ctx** out) {
+  g_create_error.clear();
+  if (!out) { g_create_error = "out is NULL"; return OBS_E_INVALID; }
+  *out = nullptr;
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess || n <= 0) {
+    g_create_error = std::string("no HIP device: ") + (e != hipSuccess ? hipGetErrorString(e) : "count 0");
+    return OBS_E_UNSUPPORTED;
+  }
+  if (device < 0 || device >= n) { g_create_error = "device index out of range"; return OBS_E_INVALID; }
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, device) != hipSuccess) { g_create_error = "hipGetDeviceProperties failed"; return OBS_E_HIP; }
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+    g_create_error = std::string("device is ") + prop.gcnArchName + ", this library is built for gfx950 only";
+    return OBS_E_UNSUPPORTED;
+  }
+  if (hipSetDevice(device) != hipSuccess) { g_create_error = "hipSetDevice failed"; return OBS_E_HIP; }
+  obs_ctx* ctx = new obs_ctx();
+  ctx->device = device;
+  ctx->num_cus = prop.multiProcessorCount;
+  if (hipStreamCreateWithFlags(&ctx->own_stream, hipStreamNonBlocking) != hipSuccess ||
+      hipEventCreate(&ctx->ev_start) != hipSuccess || hipEventCreate(&ctx->ev_stop) != hipSuccess) {
+    g_create_error = "stream/event creation failed";
+    delete ctx;
+    return OBS_E_HIP;
+  }
+  ctx->stream = ctx->own_stream;
+  *out = ctx;
+  return OBS_OK;
+}
+
+void obs_destroy(obs_ctx* ctx) {
+  if (!ctx) return;
+  (void)hipSetDevice(ctx->device);
+  if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+  if (ctx->decode_ws) (void)hipFree(ctx->decode_ws);
+  if (ctx->ev_start) (void)hipEventDestroy(ctx->ev_start);
+  if (ctx->ev_stop) (void)hipEventDestroy(ctx->ev_stop);
+  if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
+  delete ctx;
+}
+
+const char* obs_last_error(const obs_ctx* ctx) { return ctx ? ctx->err.c_str() : "null context"; }
+
+int obs_set_stream(obs_ctx* ctx, void* hip_stream) {
+  if (!ctx) return OBS_E_INVALID;
+  ctx->stream = hip_stream ? static_cast<hipStream_t>(hip_stream) : ctx->own_stream;
+  return OBS_OK;
+}
+
+void* obs_get_stream(const obs_ctx* ctx) { return ctx ? ctx->stream : nullptr; }
+
+int obs_alloc(obs_ctx* ctx, size_t bytes, void** dptr) {
+  if (!ctx || !dptr) return OBS_E_INVALID;
+  *dptr = nullptr;
+  if (bytes == 0) return obs::set_error(ctx, OBS_E_INVALID, "obs_alloc: zero bytes");
+  hipError_t e = hipMalloc(dptr, bytes);
+  if (e != hipSuccess) return obs::set_error(ctx, OBS_E_NOMEM, "hipMalloc(%zu) failed: %s", bytes, hipGetErrorString(e));
+  return OBS_OK;
+}
+
+int obs_free(obs_ctx* ctx, void* dptr) {
+  if (!ctx) return OBS_E_INVALID;
+  if (!dptr) return OBS_OK;
+  OBS_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+  OBS_HIP_TRY(ctx, hipFree(dptr));
+  return OBS_OK;
+}
+
+int obs_upload(obs_ctx* ctx, void* dst, const void* src, size_t bytes) {
+  if (!ctx || (!dst && bytes) || (!src && bytes)) return OBS_E_INVALID;
+  if (!bytes) return OBS_OK;
+  OBS_HIP_TRY(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream));
+  // pageable host memory: make the call safe to reuse the host buffer at once
+  OBS_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+  return OBS_OK;
+}
+
+int obs_download(obs_ctx* ctx, void* dst, const void* src, size_t bytes) {
+  if (!ctx || (!dst && bytes) || (!src && bytes)) return OBS_E_INVALID;
+  if (!bytes) return OBS_OK;
+  OBS_HIP_TRY(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream));
+  OBS_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+  return OBS_OK;
+}
+
+int obs_memset(obs_ctx* ctx, void* dst, int value, size_t bytes) {
+  if (!ctx || (!dst && bytes)) return OBS_E_INVALID;
+  if (!bytes) return OBS_OK;
+  OBS_HIP_TRY(ctx, hipMemsetAsync(dst, value, bytes, ctx->stream));
+  return OBS_OK;
+}
+
+int obs_sync(obs_ctx* ctx) {
+  if (!ctx) return OBS_E_INVALID;
+  OBS_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+  return OBS_OK;
+}
+
+int obs_timer_start(obs_ctx* ctx) {
+  if (!ctx) return OBS_E_INVALID;
+  OBS_HIP_TRY(ctx, hipEventRecord(ctx->ev_start, ctx->stream));
+  return OBS_OK;
+}
+
+int obs_timer_stop(obs_ctx* ctx, float* ms) {
+  if (!ctx || !ms) return OBS_E_INVALID;
+  OBS_HIP_TRY(ctx, hipEventRecord(ctx->ev_stop, ctx->stream));
+  OBS_HIP_TRY(ctx, hipEventSynchronize(ctx->ev_stop));
+  OBS_HIP_TRY(ctx, hipEventElapsedTime(ms, ctx->ev_start, ctx->ev_stop));
+  return OBS_OK;
+}
+
+}  // extern "C"

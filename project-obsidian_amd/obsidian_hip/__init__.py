@@ -1,0 +1,371 @@
+"""obsidian_hip — Python host over the libobsidian_hip C ABI (include/obsidian_hip.h).
+
+The names mirror the reference host so code reads like the Rust engine:
+
+* ``ObsidianExecutor``  — src/executor.rs:39-70 (device + queue; here a HIP
+  context and stream).
+* ``MoeRouter``         — src/router.rs:16-94 (``route``, ``route_dispatch``,
+  ``read_route``).
+* ``Model``-style ops   — src/forward.rs: ``dequant`` (:303), ``matmul_raw``
+  (:313), ``swiglu`` (:370), ``scaled_add`` (:376), ``gate_gpu`` (:386), and the
+  MoE halves of ``forward_layer`` (:421-441) / ``prefill_batched`` (:164-247).
+
+Every call goes through the native library; there is no CPU fallback. If the
+library is missing or no gfx950 device is present, the call raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from dataclasses import dataclass, field
+from typing import Dict, List, Optional, Sequence, Tuple
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(os.path.dirname(_HERE), "libobsidian_hip.so")
+
+OBS_OK = 0
+OBS_E_INVALID = -1
+OBS_E_SHAPE = -2
+OBS_E_ALIGN = -3
+OBS_E_HIP = -4
+OBS_E_NOMEM = -5
+OBS_E_UNSUPPORTED = -6
+
+_ERRNAMES = {
+    OBS_E_INVALID: "OBS_E_INVALID",
+    OBS_E_SHAPE: "OBS_E_SHAPE",
+    OBS_E_ALIGN: "OBS_E_ALIGN",
+    OBS_E_HIP: "OBS_E_HIP",
+    OBS_E_NOMEM: "OBS_E_NOMEM",
+    OBS_E_UNSUPPORTED: "OBS_E_UNSUPPORTED",
+}
+
+# Every symbol the C ABI exports (include/obsidian_hip.h).
+EXPORTS = (
+    "obs_create", "obs_destroy", "obs_last_error", "obs_create_error", "obs_set_stream",
+    "obs_get_stream", "obs_alloc", "obs_free", "obs_upload", "obs_download", "obs_memset",
+    "obs_sync", "obs_timer_start", "obs_timer_stop", "obs_dequant", "obs_q4_matvec",
+    "obs_q4_matmul", "obs_q8_gate_logits", "obs_route_topk", "obs_swiglu", "obs_scaled_add",
+    "obs_moe_decode", "obs_moe_prefill_workspace", "obs_moe_prefill",
+)
+
+
+class ObsError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"{_ERRNAMES.get(code, code)}: {msg}")
+        self.code = code
+
+
+class ObsMoeConfig(C.Structure):
+    _fields_ = [("n_exp", C.c_uint32), ("top_k", C.c_uint32), ("hidden", C.c_uint32),
+                ("inter", C.c_uint32), ("group", C.c_uint32), ("norm_topk", C.c_int32)]
+
+
+class ObsMoeLayer(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in (
+        "gate_w", "gate_s", "gate_b", "up_w", "up_s", "up_b", "down_w", "down_s", "down_b",
+        "router_w", "router_s", "router_b")]
+
+
+_lib_handle = None
+
+
+def lib() -> C.CDLL:
+    """Load libobsidian_hip.so (built in-tree); raise if it is absent."""
+    global _lib_handle
+    if _lib_handle is not None:
+        return _lib_handle
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"{LIB_PATH} is not built; run __graft_entry__.build() (or make in project-obsidian_amd/)")
+    L = C.CDLL(LIB_PATH)
+    vp, u32, i32, f32, sz = C.c_void_p, C.c_uint32, C.c_int32, C.c_float, C.c_size_t
+    sig = {
+        "obs_create": (i32, [C.c_int, C.POINTER(vp)]),
+        "obs_destroy": (None, [vp]),
+        "obs_last_error": (C.c_char_p, [vp]),
+        "obs_create_error": (C.c_char_p, []),
+        "obs_set_stream": (i32, [vp, vp]),
+        "obs_get_stream": (vp, [vp]),
+        "obs_alloc": (i32, [vp, sz, C.POINTER(vp)]),
+        "obs_free": (i32, [vp, vp]),
+        "obs_upload": (i32, [vp, vp, vp, sz]),
+        "obs_download": (i32, [vp, vp, vp, sz]),
+        "obs_memset": (i32, [vp, vp, C.c_int, sz]),
+        "obs_sync": (i32, [vp]),
+        "obs_timer_start": (i32, [vp]),
+        "obs_timer_stop": (i32, [vp, C.POINTER(f32)]),
+        "obs_dequant": (i32, [vp, C.c_int, vp, vp, vp, vp, vp, u32, u32, u32]),
+        "obs_q4_matvec": (i32, [vp, vp, vp, vp, vp, vp, vp, u32, u32, u32]),
+        "obs_q4_matmul": (i32, [vp, vp, vp, vp, vp, vp, u32, u32, u32, u32]),
+        "obs_q8_gate_logits": (i32, [vp, vp, vp, vp, vp, vp, u32, u32, u32, u32]),
+        "obs_route_topk": (i32, [vp, vp, vp, vp, u32, u32, u32, C.c_int]),
+        "obs_swiglu": (i32, [vp, vp, vp, vp, u32]),
+        "obs_scaled_add": (i32, [vp, vp, vp, f32, u32]),
+        "obs_moe_decode": (i32, [vp, C.POINTER(ObsMoeConfig), C.POINTER(ObsMoeLayer), vp, vp, vp, vp, vp]),
+        "obs_moe_prefill_workspace": (sz, [C.POINTER(ObsMoeConfig), u32]),
+        "obs_moe_prefill": (i32, [vp, C.POINTER(ObsMoeConfig), C.POINTER(ObsMoeLayer), vp, vp, vp, u32,
+                                  vp, vp, vp, sz]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib_handle = L
+    return L
+
+
+def _ptr(x) -> Optional[int]:
+    if x is None:
+        return None
+    if isinstance(x, DeviceBuffer):
+        return x.ptr
+    if isinstance(x, int):
+        return x
+    raise TypeError(f"expected DeviceBuffer / int device pointer, got {type(x)}")
+
+
+@dataclass
+class DeviceBuffer:
+    """A device allocation (the reference's Metal `Buffer`, forward.rs:264)."""
+    exec: "ObsidianExecutor"
+    ptr: int
+    nbytes: int
+    dtype: np.dtype
+    shape: Tuple[int, ...]
+    owned: bool = True
+
+    def download(self) -> np.ndarray:
+        out = np.empty(self.shape, dtype=self.dtype)
+        self.exec._check(lib().obs_download(self.exec.ctx, out.ctypes.data, self.ptr, out.nbytes))
+        return out
+
+    def upload(self, arr: np.ndarray) -> None:
+        a = np.ascontiguousarray(arr, dtype=self.dtype)
+        if a.nbytes != self.nbytes:
+            raise ValueError(f"size mismatch: {a.nbytes} != {self.nbytes}")
+        self.exec._check(lib().obs_upload(self.exec.ctx, self.ptr, a.ctypes.data, a.nbytes))
+
+    def free(self) -> None:
+        if self.owned and self.ptr:
+            lib().obs_free(self.exec.ctx, self.ptr)
+            self.ptr = 0
+
+
+class ObsidianExecutor:
+    """HIP context + stream. executor.rs:39-58 `ObsidianExecutor::new`."""
+
+    def __init__(self, device: int = 0):
+        L = lib()
+        ctx = C.c_void_p()
+        rc = L.obs_create(device, C.byref(ctx))
+        if rc != OBS_OK:
+            raise ObsError(rc, L.obs_create_error().decode())
+        self.ctx = ctx.value
+        self._bufs: List[DeviceBuffer] = []
+
+    # -- errors ----------------------------------------------------------
+    def _check(self, rc: int) -> None:
+        if rc != OBS_OK:
+            raise ObsError(rc, lib().obs_last_error(self.ctx).decode())
+
+    def last_error(self) -> str:
+        return lib().obs_last_error(self.ctx).decode()
+
+    # -- buffers (device.new_buffer / contents / drain) ------------------
+    def alloc(self, shape, dtype) -> DeviceBuffer:
+        shape = tuple(int(s) for s in (shape if isinstance(shape, (tuple, list)) else (shape,)))
+        dtype = np.dtype(dtype)
+        nbytes = max(int(np.prod(shape)) * dtype.itemsize, 1)
+        p = C.c_void_p()
+        self._check(lib().obs_alloc(self.ctx, nbytes, C.byref(p)))
+        buf = DeviceBuffer(self, p.value, nbytes, dtype, shape)
+        self._bufs.append(buf)
+        return buf
+
+    def upload(self, arr: np.ndarray) -> DeviceBuffer:
+        a = np.ascontiguousarray(arr)
+        buf = self.alloc(a.shape, a.dtype)
+        if a.nbytes:
+            self._check(lib().obs_upload(self.ctx, buf.ptr, a.ctypes.data, a.nbytes))
+        return buf
+
+    def zeros(self, shape, dtype) -> DeviceBuffer:
+        buf = self.alloc(shape, dtype)
+        self._check(lib().obs_memset(self.ctx, buf.ptr, 0, buf.nbytes))
+        return buf
+
+    def sync(self) -> None:
+        """Model::drain (forward.rs:282-286)."""
+        self._check(lib().obs_sync(self.ctx))
+
+    drain = sync
+
+    def timer_start(self) -> None:
+        self._check(lib().obs_timer_start(self.ctx))
+
+    def timer_stop(self) -> float:
+        ms = C.c_float()
+        self._check(lib().obs_timer_stop(self.ctx, C.byref(ms)))
+        return ms.value
+
+    def set_stream(self, stream: Optional[int]) -> None:
+        self._check(lib().obs_set_stream(self.ctx, stream))
+
+    def close(self) -> None:
+        if getattr(self, "ctx", None):
+            for b in self._bufs:
+                b.free()
+            self._bufs.clear()
+            lib().obs_destroy(self.ctx)
+            self.ctx = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    # -- kernels ---------------------------------------------------------
+    def dequant_tensor(self, bits: int, w, s, b, rows: int, cols: int, group: int = 64,
+                       out_f32=None, out_bf16=None) -> None:
+        """mx.dequantize (validate_dequant.py:21): fp32 and/or bf16 output."""
+        self._check(lib().obs_dequant(self.ctx, bits, _ptr(w), _ptr(s), _ptr(b), _ptr(out_f32),
+                                      _ptr(out_bf16), rows, cols, group))
+
+    def q4_matvec(self, w, s, b, x, in_f: int, out_f: int, group: int = 64, y_f32=None, y_bf16=None) -> None:
+        self._check(lib().obs_q4_matvec(self.ctx, _ptr(w), _ptr(s), _ptr(b), _ptr(x), _ptr(y_f32),
+                                        _ptr(y_bf16), in_f, out_f, group))
+
+    def q4_matmul(self, w, s, b, X, Y, T: int, in_f: int, out_f: int, group: int = 64) -> None:
+        self._check(lib().obs_q4_matmul(self.ctx, _ptr(w), _ptr(s), _ptr(b), _ptr(X), _ptr(Y), T, in_f,
+                                        out_f, group))
+
+    def q8_gate_logits(self, w, s, b, x, logits, T: int, in_f: int, n_exp: int, group: int = 64) -> None:
+        self._check(lib().obs_q8_gate_logits(self.ctx, _ptr(w), _ptr(s), _ptr(b), _ptr(x), _ptr(logits), T,
+                                             in_f, n_exp, group))
+
+    def route_topk(self, logits, ids, weights, T: int, n_exp: int, k: int, norm_topk: bool) -> None:
+        self._check(lib().obs_route_topk(self.ctx, _ptr(logits), _ptr(ids), _ptr(weights), T, n_exp, k,
+                                         int(bool(norm_topk))))
+
+    def swiglu_raw(self, g, u, h, n: int) -> None:
+        self._check(lib().obs_swiglu(self.ctx, _ptr(g), _ptr(u), _ptr(h), n))
+
+    def scaled_add_raw(self, acc, y, scale: float, n: int) -> None:
+        self._check(lib().obs_scaled_add(self.ctx, _ptr(acc), _ptr(y), float(scale), n))
+
+    def moe_decode(self, cfg: "MoeConfig", layer: "MoeLayer", x, y, residual=None, ids_out=None,
+                   w_out=None) -> None:
+        c, l = cfg.to_c(), layer.to_c()
+        self._check(lib().obs_moe_decode(self.ctx, C.byref(c), C.byref(l), _ptr(x), _ptr(residual), _ptr(y),
+                                         _ptr(ids_out), _ptr(w_out)))
+
+    def moe_prefill_workspace(self, cfg: "MoeConfig", T: int) -> int:
+        c = cfg.to_c()
+        return int(lib().obs_moe_prefill_workspace(C.byref(c), T))
+
+    def moe_prefill(self, cfg: "MoeConfig", layer: "MoeLayer", X, Y, T: int, ids=None, weights=None,
+                    residual=None, ws=None, ws_bytes: Optional[int] = None) -> None:
+        c, l = cfg.to_c(), layer.to_c()
+        if ws_bytes is None:
+            ws_bytes = ws.nbytes if isinstance(ws, DeviceBuffer) else 0
+        self._check(lib().obs_moe_prefill(self.ctx, C.byref(c), C.byref(l), _ptr(X), _ptr(residual), _ptr(Y), T,
+                                          _ptr(ids), _ptr(weights), _ptr(ws), ws_bytes))
+
+
+@dataclass
+class MoeConfig:
+    """Shape constants from Qwen3MoeConfig (src/model.rs:7-23)."""
+    n_exp: int = 128
+    top_k: int = 8
+    hidden: int = 2048
+    inter: int = 768
+    group: int = 64
+    norm_topk: bool = True
+
+    def to_c(self) -> ObsMoeConfig:
+        return ObsMoeConfig(self.n_exp, self.top_k, self.hidden, self.inter, self.group, int(bool(self.norm_topk)))
+
+
+PROJ_KEYS = ("gate_w", "gate_s", "gate_b", "up_w", "up_s", "up_b", "down_w", "down_s", "down_b",
+             "router_w", "router_s", "router_b")
+
+
+@dataclass
+class MoeLayer:
+    """One layer of the HBM-resident expert table: device pointers of the
+    stacked switch_mlp tensors plus the 8-bit router gate (replaces the SSD
+    ExpertIndex + expert_pool, disk_io.rs:36-102, forward.rs:79-89)."""
+    ptrs: Dict[str, int] = field(default_factory=dict)
+
+    @classmethod
+    def upload(cls, exe: ObsidianExecutor, tensors: Dict[str, np.ndarray]) -> "MoeLayer":
+        return cls({k: exe.upload(tensors[k]).ptr for k in PROJ_KEYS})
+
+    def to_c(self) -> ObsMoeLayer:
+        return ObsMoeLayer(*[self.ptrs[k] for k in PROJ_KEYS])
+
+
+class MoeRouter:
+    """router.rs:16-94. `route` = dispatch + drain + read; `route_dispatch`
+    returns device buffers; `read_route` reads them after a drain."""
+
+    def __init__(self, n_experts: int, top_k: int, norm_topk: bool):
+        self.n_experts, self.top_k, self.norm_topk = n_experts, top_k, norm_topk
+
+    def route_dispatch(self, exe: ObsidianExecutor, gate_logits: DeviceBuffer, T: int = 1):
+        idx = exe.alloc((T, self.top_k), np.int32)
+        w = exe.alloc((T, self.top_k), np.float32)
+        exe.route_topk(gate_logits, idx, w, T, self.n_experts, self.top_k, self.norm_topk)
+        return idx, w
+
+    def read_route(self, idx_buf: DeviceBuffer, w_buf: DeviceBuffer):
+        ids = idx_buf.download()
+        w = w_buf.download()
+        if ids.shape[0] == 1:
+            return [int(i) for i in ids[0]], [float(v) for v in w[0]]
+        return ids, w
+
+    def route(self, exe: ObsidianExecutor, gate_logits: DeviceBuffer):
+        idx, w = self.route_dispatch(exe, gate_logits, 1)
+        exe.drain()
+        out = self.read_route(idx, w)
+        idx.free()
+        w.free()
+        return out
+
+
+def gate_gpu(exe: ObsidianExecutor, layer: MoeLayer, cfg: MoeConfig, x: DeviceBuffer, T: int = 1) -> DeviceBuffer:
+    """forward.rs:386-397: router logits for T tokens (fp32 here)."""
+    out = exe.alloc((T, cfg.n_exp), np.float32)
+    exe.q8_gate_logits(layer.ptrs["router_w"], layer.ptrs["router_s"], layer.ptrs["router_b"], x, out, T,
+                       cfg.hidden, cfg.n_exp, cfg.group)
+    return out
+
+
+def dequant(exe: ObsidianExecutor, w, s, b, x: DeviceBuffer, in_f: int, out_f: int) -> DeviceBuffer:
+    """forward.rs:303-310: y = dequant(W) . x (one token), bf16 out."""
+    y = exe.alloc((out_f,), np.uint16)
+    exe.q4_matvec(w, s, b, x, in_f, out_f, 64, y_bf16=y)
+    return y
+
+
+def matmul_raw(exe: ObsidianExecutor, w, s, b, xc: DeviceBuffer, t: int, in_f: int, out_f: int) -> DeviceBuffer:
+    """forward.rs:313-321: Y[t, out] = Xc[t, in] . dequant(W)^T (bf16)."""
+    y = exe.alloc((t, out_f), np.uint16)
+    exe.q4_matmul(w, s, b, xc, y, t, in_f, out_f, 64)
+    return y
+
+
+def swiglu(exe: ObsidianExecutor, g: DeviceBuffer, u: DeviceBuffer, n: int) -> DeviceBuffer:
+    """forward.rs:370-375."""
+    h = exe.alloc((n,), np.uint16)
+    exe.swiglu_raw(g, u, h, n)
+    return h
+
+
+def scaled_add(exe: ObsidianExecutor, acc: DeviceBuffer, y: DeviceBuffer, scale: float, n: int) -> None:
+    """forward.rs:376-380: acc += scale * y (in place)."""
+    exe.scaled_add_raw(acc, y, scale, n)

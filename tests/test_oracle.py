@@ -1,0 +1,365 @@
+"""Pins the CPU oracle (oracle/oracle.c) against closed forms, exhaustive
+checks, brute force and invariants — never against a retyped copy of itself.
+
+Reference semantics pinned here: validate_dequant.py:26-30 (unpack),
+fused_dequant_matvec_4bit.metal:29-52 (serial mat-vec), dequant_matvec_8bit.metal
+(8-bit router gate), moe_routing_topk.metal:31-56 (softmax/top-k/renorm),
+ops.metal:18-29 (SwiGLU, scaled add), forward.rs:200-232 / :421-441 (compositions).
+"""
+import math
+from fractions import Fraction
+
+import numpy as np
+import pytest
+
+import oracle as O
+from obsidian_hip import synth
+
+U = 2.0 ** -24  # fp32 unit roundoff
+
+
+# ---------------------------------------------------------------- 16-bit floats
+def test_bf16_roundtrip_exhaustive():
+    L = O.lib()
+    for h in range(0, 65536, 1):
+        f = L.orc_bf16_to_f32(h)
+        exp_bits = (h >> 7) & 0xFF
+        man = h & 0x7F
+        if exp_bits == 0xFF and man:  # NaN: stays NaN, quiet bit set
+            assert math.isnan(f)
+            assert L.orc_f32_to_bf16(f) & 0x7FC0 == 0x7FC0
+            continue
+        assert L.orc_f32_to_bf16(f) == h
+
+
+def test_f32_to_bf16_rne_against_numpy_restatement():
+    rng = np.random.default_rng(1)
+    bits = rng.integers(0, 2**32, size=20000, dtype=np.uint64).astype(np.uint32)
+    # force exact ties (low half == 0x8000) for a quarter of them
+    bits[::4] = (bits[::4] & 0xFFFF0000) | 0x8000
+    vals = bits.view(np.float32)
+    ref = synth.f32_to_bf16_bits(vals)
+    got = np.array([O.f32_to_bf16(float(v)) for v in vals], dtype=np.uint16)
+    finite = ~np.isnan(vals)
+    assert np.array_equal(got[finite], ref[finite])
+    # ties go to even
+    assert O.f32_to_bf16(float(np.uint32(0x3F808000).view(np.float32))) == 0x3F80
+    assert O.f32_to_bf16(float(np.uint32(0x3F818000).view(np.float32))) == 0x3F82
+
+
+def test_f16_conversions_against_numpy():
+    hs = np.arange(65536, dtype=np.uint16)
+    ref = hs.view(np.float16).astype(np.float32)
+    got = np.array([O.f16_to_f32(int(h)) for h in hs], dtype=np.float32)
+    nan = np.isnan(ref)
+    assert np.array_equal(got[~nan], ref[~nan]) and np.all(np.isnan(got[nan]))
+    rng = np.random.default_rng(2)
+    vals = np.concatenate([
+        rng.standard_normal(5000).astype(np.float32) * np.float32(1e-5),  # f16 subnormal range
+        rng.standard_normal(5000).astype(np.float32) * np.float32(1e3),
+        np.array([65504.0, 65519.99, 65520.0, 1e9, -1e9, 2.0**-25, 2.0**-24, 3 * 2.0**-26], np.float32),
+    ])
+    ref = vals.astype(np.float16).view(np.uint16)
+    got = np.array([O.f32_to_f16(float(v)) for v in vals], dtype=np.uint16)
+    assert np.array_equal(got, ref)
+
+
+# ---------------------------------------------------------------- dequant
+def _pack4(q: np.ndarray) -> np.ndarray:
+    """q [rows, cols] ints 0..15 -> uint32 words, element c at nibble c%8 of word c/8."""
+    rows, cols = q.shape
+    q = q.reshape(rows, cols // 8, 8).astype(np.uint32)
+    return np.bitwise_or.reduce(q << (4 * np.arange(8, dtype=np.uint32)), axis=2)
+
+
+def test_dequant_known_answers():
+    s = synth.f32_to_bf16_bits(np.array([[0.5, 2.0]], np.float32))
+    b = synth.f32_to_bf16_bits(np.array([[-1.0, 0.25]], np.float32))
+    # word 0x76543210 holds q = 0..7 in column order; 0xFEDCBA98 holds 8..15
+    w = np.array([[0x76543210, 0xFEDCBA98] + [0] * 6 + [0xFFFFFFFF] * 8], np.uint32)
+    out = O.dequant(4, w, s, b, 1, 128, 64)
+    assert list(out[0, :16]) == [0.5 * q - 1.0 for q in range(16)]
+    assert np.all(out[0, 16:64] == -1.0)                 # q = 0 -> bias
+    assert np.all(out[0, 64:] == np.float32(15 * 2.0 + 0.25))  # q = 15, second group
+    # group boundary: column 63 uses group 0, column 64 group 1
+    assert out[0, 63] == -1.0 and out[0, 64] == np.float32(30.25)
+
+
+def test_dequant_8bit_known_answers():
+    s = synth.f32_to_bf16_bits(np.array([[0.125]], np.float32))
+    b = synth.f32_to_bf16_bits(np.array([[1.0]], np.float32))
+    w = np.array([[0x03020100] + [0xFF80017F] * 15], np.uint32)
+    out = O.dequant(8, w, s, b, 1, 64, 64)
+    assert list(out[0, :4]) == [1.0, 1.125, 1.25, 1.375]
+    assert list(out[0, 4:8]) == [np.float32(0x7F * 0.125 + 1), np.float32(0x01 * 0.125 + 1),
+                                 np.float32(0x80 * 0.125 + 1), np.float32(0xFF * 0.125 + 1)]
+
+
+def test_dequant_matches_numpy_replica_of_validate_dequant():
+    rng = np.random.default_rng(3)
+    w, s, b = synth.quant_tensor(rng, 96, 512, 4, 64)
+    got = O.dequant(4, w, s, b, 96, 512, 64)
+    ref = O.dequant_numpy(w, synth.bf16_bits_to_f32(s), synth.bf16_bits_to_f32(b), 64)
+    assert np.array_equal(got, ref)  # bit-exact: one rounding (q*s is exact)
+
+
+def test_dequant_f16_scales_path():
+    rng = np.random.default_rng(4)
+    w = rng.integers(0, 2**32, size=(4, 16), dtype=np.uint64).astype(np.uint32)
+    sf = (np.abs(rng.standard_normal((4, 2))) * 0.02).astype(np.float16)
+    bf = (rng.standard_normal((4, 2)) * 0.01).astype(np.float16)
+    got = O.dequant(4, w, sf.view(np.uint16), bf.view(np.uint16), 4, 128, 64, sb_type=O.SB_F16)
+    ref = O.dequant_numpy(w, sf.astype(np.float32), bf.astype(np.float32), 64)
+    assert np.array_equal(got, ref)
+
+
+def test_dequant_rejects_bad_shapes():
+    w = np.zeros((1, 12), np.uint32)
+    s = np.zeros((1, 2), np.uint16)
+    with pytest.raises(ValueError):
+        O.dequant(4, w, s, s, 1, 96, 64)  # 96 % 64 != 0 (the reference silently drops the tail)
+
+
+# ---------------------------------------------------------------- mat-vec
+def _round_f32(fr: Fraction) -> float:
+    """Exact round-to-nearest-even of a rational to fp32."""
+    c = np.float32(float(fr))
+    best = None
+    for cand in (np.nextafter(c, np.float32(-np.inf)), c, np.nextafter(c, np.float32(np.inf))):
+        d = abs(Fraction(float(cand)) - fr)
+        if best is None or d < best[0] or (d == best[0] and (np.float32(cand).view(np.uint32) & 1) == 0):
+            best = (d, cand)
+    return float(best[1])
+
+
+def test_qmatvec_one_hot_selects_column():
+    rng = np.random.default_rng(5)
+    w, s, b = synth.quant_tensor(rng, 32, 256, 4, 64)
+    W = O.dequant(4, w, s, b, 32, 256)
+    for j in (0, 63, 64, 200, 255):
+        x = np.zeros(256, np.float32)
+        x[j] = 1.0
+        for kind in ("shader", "lanes"):
+            y = O.qmatvec(kind, 4, w, s, b, x, 256, 32, lanes=64)
+            assert np.array_equal(y, W[:, j])
+
+
+def test_qmatvec_lanes1_equals_exact_serial_fma():
+    rng = np.random.default_rng(6)
+    w, s, b = synth.quant_tensor(rng, 3, 64, 4, 64)
+    x = synth.bf16_bits_to_f32(synth.bf16_normal(rng, 64))
+    W = O.dequant(4, w, s, b, 3, 64)
+    y = O.qmatvec("lanes", 4, w, s, b, x, 64, 3, lanes=1)
+    for r in range(3):
+        acc = 0.0
+        for c in range(64):
+            acc = _round_f32(Fraction(float(W[r, c])) * Fraction(float(x[c])) + Fraction(acc))
+        assert y[r] == np.float32(acc)
+
+
+def test_qmatvec_shader_is_serial_rounded_products():
+    rng = np.random.default_rng(7)
+    w, s, b = synth.quant_tensor(rng, 3, 64, 4, 64)
+    x = synth.bf16_bits_to_f32(synth.bf16_normal(rng, 64))
+    W = O.dequant(4, w, s, b, 3, 64)
+    y = O.qmatvec("shader", 4, w, s, b, x, 64, 3)
+    for r in range(3):
+        acc = np.float32(0.0)
+        for c in range(64):
+            acc = np.float32(acc + np.float32(W[r, c] * x[c]))
+        assert y[r] == acc
+
+
+@pytest.mark.parametrize("bits,in_f,out_f", [(4, 768, 64), (4, 2048, 32), (8, 2048, 16)])
+def test_qmatvec_error_bound_vs_fp64(bits, in_f, out_f):
+    rng = np.random.default_rng(8)
+    w, s, b = synth.quant_tensor(rng, out_f, in_f, bits, 64)
+    x = synth.bf16_bits_to_f32(synth.bf16_normal(rng, in_f))
+    W = O.dequant(bits, w, s, b, out_f, in_f).astype(np.float64)
+    y64, ab = O.qmatvec("f64", bits, w, s, b, x, in_f, out_f)
+    assert np.allclose(y64, W @ x.astype(np.float64), rtol=1e-12, atol=1e-12)
+    assert np.allclose(ab, np.abs(W) @ np.abs(x.astype(np.float64)), rtol=1e-12)
+    gamma = in_f * U / (1 - in_f * U)
+    for kind in ("shader", "lanes"):
+        y = O.qmatvec(kind, bits, w, s, b, x, in_f, out_f).astype(np.float64)
+        assert np.all(np.abs(y - y64) <= gamma * ab + 1e-30)
+
+
+# ---------------------------------------------------------------- exp / silu
+def test_exp_against_libm():
+    xs = np.concatenate([np.linspace(-86.0, 88.5, 200001, dtype=np.float32),
+                         np.float32([0.0, -0.0, 1e-30, -1e-30, 0.5, -0.5])])
+    got = np.array([O.exp(float(v)) for v in xs[::7]], np.float32)
+    ref = np.exp(xs[::7].astype(np.float64)).astype(np.float32)
+    ulp = np.abs(got.view(np.int32).astype(np.int64) - ref.view(np.int32).astype(np.int64))
+    assert ulp.max() <= 2
+    assert O.exp(0.0) == 1.0
+    assert O.exp(-86.5) == 0.0 and O.exp(-1e30) == 0.0 and O.exp(float("-inf")) == 0.0
+    assert math.isinf(O.exp(88.6)) and math.isnan(O.exp(float("nan")))
+    srt = got[np.argsort(xs[::7], kind="stable")]
+    assert np.all(np.diff(srt.astype(np.float64)) >= 0)  # monotone on the grid
+
+
+def test_silu_mul_closed_form():
+    for g, u in [(0.0, 3.0), (1.0, 1.0), (-2.5, 4.0), (20.0, 0.5), (-100.0, 7.0)]:
+        ref = g / (1.0 + math.exp(-g)) * u
+        assert abs(O.silu_mul(g, u) - ref) <= 4e-7 * max(1.0, abs(ref))
+    assert O.silu_mul(-100.0, 7.0) == pytest.approx(0.0, abs=1e-30)
+
+
+# ---------------------------------------------------------------- routing
+@pytest.mark.parametrize("order", [O.SUM_SERIAL, O.SUM_WAVE])
+def test_route_topk_matches_sorted_logits(order):
+    rng = np.random.default_rng(9)
+    lg = rng.standard_normal((64, 128)).astype(np.float32) * 3
+    ids, w = O.route_topk(lg, 8, True, order)
+    ref = np.argsort(-lg.astype(np.float64), axis=1, kind="stable")[:, :8]
+    assert np.array_equal(ids, ref)
+    # closed form of the renormalised weight: e_i / sum_sel e_j (full-softmax S cancels)
+    sel = np.take_along_axis(lg.astype(np.float64), ref, axis=1)
+    e = np.exp(sel - lg.max(axis=1, keepdims=True))
+    assert np.allclose(w, e / e.sum(axis=1, keepdims=True), rtol=2e-6, atol=1e-9)
+    assert np.allclose(w.sum(axis=1), 1.0, atol=4e-7)
+
+
+def test_route_topk_ties_lower_id_wins():
+    lg = np.zeros((1, 16), np.float32)
+    lg[0, [3, 7, 11]] = 2.0
+    ids, w = O.route_topk(lg, 5, True)
+    assert list(ids[0]) == [3, 7, 11, 0, 1]
+    lg2 = np.full((1, 128), -1.0, np.float32)
+    lg2[0, 100] = 5.0
+    lg2[0, [5, 50, 120]] = 4.0
+    ids, _ = O.route_topk(lg2, 8)
+    assert list(ids[0]) == [100, 5, 50, 120, 0, 1, 2, 3]
+
+
+def test_route_topk_permutation_equivariance():
+    rng = np.random.default_rng(10)
+    lg = rng.standard_normal(128).astype(np.float32)
+    perm = rng.permutation(128)
+    ids, w = O.route_topk(lg, 8)
+    ids_p, w_p = O.route_topk(lg[perm], 8)
+    assert np.array_equal(perm[ids_p[0]], ids[0])
+
+
+def test_route_topk_no_norm_and_f16_emulation():
+    rng = np.random.default_rng(11)
+    lg = rng.standard_normal((4, 128)).astype(np.float32)
+    ids, w = O.route_topk(lg, 8, norm_topk=False)
+    p = np.exp(lg.astype(np.float64) - lg.max(axis=1, keepdims=True))
+    p /= p.sum(axis=1, keepdims=True)
+    assert np.allclose(w, np.take_along_axis(p, ids, axis=1), rtol=2e-6)
+    _, wf = O.route_topk(lg, 8, True, emulate_f16=True)
+    assert np.array_equal(wf.astype(np.float16).astype(np.float32), wf)
+
+
+def test_route_topk_nan_and_k_equals_n():
+    lg = np.full((1, 8), np.nan, np.float32)
+    ids, w = O.route_topk(lg, 3)
+    assert list(ids[0]) == [-1, -1, -1] and list(w[0]) == [0.0, 0.0, 0.0]
+    rng = np.random.default_rng(12)
+    lg = rng.standard_normal((3, 16)).astype(np.float32)
+    ids, w = O.route_topk(lg, 16)
+    assert all(sorted(r) == list(range(16)) for r in ids)
+    assert np.allclose(w.sum(axis=1), 1.0, atol=1e-6)
+
+
+def test_route_sum_orders_agree_on_random_data():
+    rng = np.random.default_rng(13)
+    lg = (rng.standard_normal((512, 128)) * 4).astype(np.float32)
+    a, wa = O.route_topk(lg, 8, True, O.SUM_SERIAL)
+    b, wb = O.route_topk(lg, 8, True, O.SUM_WAVE)
+    assert np.array_equal(a, b)
+    assert np.allclose(wa, wb, rtol=1e-6)
+
+
+# ---------------------------------------------------------------- compositions
+@pytest.fixture(scope="module")
+def small_layer():
+    E, H, I = 16, 512, 256
+    t = synth.moe_layer(20, E, H, I, 64)
+    return O.Layer(t, E, H, I, 64), t
+
+
+def _expert_numpy(t, e, x64, H, I):
+    """Independent fp64 expert FFN from the numpy dequant replica."""
+    def W(p, r, c):
+        return O.dequant_numpy(t[f"{p}_w"][e], synth.bf16_bits_to_f32(t[f"{p}_s"][e]),
+                               synth.bf16_bits_to_f32(t[f"{p}_b"][e])).astype(np.float64)
+    g = W("gate", I, H) @ x64
+    u = W("up", I, H) @ x64
+    h = g / (1 + np.exp(-g)) * u
+    return W("down", H, I) @ h
+
+
+def test_moe_decode_one_hot_weight_is_one_expert(small_layer):
+    L, t = small_layer
+    rng = np.random.default_rng(21)
+    x = synth.bf16_normal(rng, 512)
+    x64 = synth.bf16_bits_to_f32(x).astype(np.float64)
+    ids = np.array([[5, 2, 9, 1]], np.int32)
+    w = np.array([[1.0, 0.0, 0.0, 0.0]], np.float32)
+    y, _, _ = O.moe_decode(L, x, 4, ids=ids, w=w)
+    ref = _expert_numpy(t, 5, x64, 512, 256)
+    assert np.allclose(y[0], ref, rtol=1e-10, atol=1e-9 * np.abs(ref).max())
+
+
+def test_moe_decode_linear_in_routing_weights(small_layer):
+    L, _ = small_layer
+    rng = np.random.default_rng(22)
+    x = synth.bf16_normal(rng, 512)
+    ids = np.array([[3, 7]], np.int32)
+    y1, _, _ = O.moe_decode(L, x, 2, ids=ids, w=np.array([[1.0, 0.0]], np.float32))
+    y2, _, _ = O.moe_decode(L, x, 2, ids=ids, w=np.array([[0.0, 1.0]], np.float32))
+    y3, _, _ = O.moe_decode(L, x, 2, ids=ids, w=np.array([[0.25, 0.75]], np.float32))
+    assert np.allclose(y3, 0.25 * y1 + 0.75 * y2, rtol=1e-12, atol=1e-12 * np.abs(y3).max())
+
+
+def test_moe_decode_router_consistent_with_route_topk(small_layer):
+    L, _ = small_layer
+    rng = np.random.default_rng(23)
+    x = synth.bf16_normal(rng, (3, 512))
+    lg, ids, w = O.router(L, x, 4)
+    xf = synth.bf16_bits_to_f32(x)
+    for t in range(3):
+        ref = O.qmatvec("lanes", 8, L.arrs["router_w"], L.arrs["router_s"], L.arrs["router_b"], xf[t], 512, 16)
+        assert np.array_equal(lg[t], ref)
+    ids2, w2 = O.route_topk(lg, 4, True, O.SUM_WAVE)
+    assert np.array_equal(ids, ids2) and np.array_equal(w, w2)
+
+
+def test_moe_shader_f16_mode_close_to_f64(small_layer):
+    L, _ = small_layer
+    rng = np.random.default_rng(24)
+    x = synth.bf16_normal(rng, 512)
+    y64, ids, w = O.moe_decode(L, x, 4)
+    y16, _, _ = O.moe_decode(L, x, 4, ids=ids, w=w, mode=O.MODE_SHADER_F16)
+    assert np.linalg.norm(y16 - y64) / np.linalg.norm(y64) < 2e-2
+
+
+def test_group_rows_invariants():
+    ids, _ = synth.zipf_routing(300, 32, 6, seed=3)
+    counts, offsets, row_token, slot_row = O.group_rows(ids, 32)
+    assert counts.sum() == 300 * 6 and offsets[-1] == 300 * 6
+    for e in range(32):
+        toks = row_token[offsets[e]:offsets[e + 1]]
+        assert np.all(np.diff(toks) > 0)  # ascending token order (forward.rs:203-204)
+        assert set(toks) == set(np.nonzero((ids == e).any(axis=1))[0])
+    for t in range(300):
+        for r in range(6):
+            assert row_token[slot_row[t * 6 + r]] == t
+
+
+def test_prefill_t1_equals_decode_and_bf16_mode_close(small_layer):
+    L, _ = small_layer
+    rng = np.random.default_rng(25)
+    X = synth.bf16_normal(rng, (5, 512))
+    ids, w = synth.zipf_routing(5, 16, 4, seed=4)
+    yp = O.moe_prefill(L, X, ids, w, O.MODE_F64)
+    for t in range(5):
+        yd, _, _ = O.moe_decode(L, X[t], 4, ids=ids[t:t + 1], w=w[t:t + 1])
+        assert np.allclose(yp[t], yd[0], rtol=1e-12, atol=1e-10 * np.abs(yd).max())
+    yb = O.moe_prefill(L, X, ids, w, O.MODE_MFMA_BF16)
+    rel = np.linalg.norm(yb - yp) / np.linalg.norm(yp)
+    assert 0 < rel < 1e-2
