@@ -84,6 +84,36 @@ int obs_timer_start(obs_ctx* ctx);
 int obs_timer_stop(obs_ctx* ctx, float* ms);
 
 /* ------------------------------------------------------------------ */
+/* Graph capture (no reference counterpart: the Metal engine commits one  */
+/* command buffer per dispatch, forward.rs:289-301). Calls issued between */
+/* begin and end are recorded, not run, and replay as one HIP graph.      */
+/* Nothing that allocates may be captured: run each entry point once      */
+/* before capturing it so its workspace exists.                           */
+/* ------------------------------------------------------------------ */
+typedef struct obs_graph obs_graph;
+int obs_capture_begin(obs_ctx* ctx);
+int obs_capture_end(obs_ctx* ctx, obs_graph** out);
+int obs_graph_launch(obs_ctx* ctx, obs_graph* graph);
+void obs_graph_destroy(obs_graph* graph);
+
+/* ------------------------------------------------------------------ */
+/* In-stream kernel timing (no reference counterpart). While enabled,     */
+/* every kernel the library launches on the context's stream is bracketed */
+/* by a pair of HIP events (also inside a capture). obs_profile_accumulate */
+/* waits for the stream and adds each pair's elapsed time to a per-kernel */
+/* total; a captured graph can be replayed and accumulated repeatedly.    */
+/* ------------------------------------------------------------------ */
+/* Enqueue a kernel that keeps the stream busy for `us` microseconds (capped
+ * at 1 s, measured on the GPU's constant-rate clock) so the host can queue
+ * the launches to be timed ahead of their execution. */
+int obs_stream_hold(obs_ctx* ctx, uint32_t us);
+int obs_profile_enable(obs_ctx* ctx, int on);
+int obs_profile_accumulate(obs_ctx* ctx);
+int obs_profile_count(const obs_ctx* ctx);
+int obs_profile_stat(const obs_ctx* ctx, int i, const char** name, double* total_ms, int64_t* launches);
+int obs_profile_clear(obs_ctx* ctx);
+
+/* ------------------------------------------------------------------ */
 /* Quantized tensor kernels                                            */
 /* ------------------------------------------------------------------ */
 

@@ -8,7 +8,14 @@
 
 namespace {
 thread_local std::string g_create_error;
+
+// Busy-waits `ticks` of the 100 MHz constant clock on one lane; always ends.
+__global__ void hold_kernel(uint64_t ticks) {
+  if (threadIdx.x != 0) return;
+  const uint64_t t0 = wall_clock64();
+  while (wall_clock64() - t0 < ticks) __builtin_amdgcn_s_sleep(64);
 }
+}  // namespace
 
 namespace obs {
 
@@ -20,6 +27,22 @@ int set_error(obs_ctx* ctx, int code, const char* fmt, ...) {
   va_end(ap);
   if (ctx) ctx->err = buf;
   return code;
+}
+
+int prof_begin(obs_ctx* ctx, const char* name) {
+  if (!ctx->prof_on) return OBS_OK;
+  obs_prof_pair p{name, nullptr, nullptr};
+  OBS_HIP_TRY(ctx, hipEventCreate(&p.e0));
+  OBS_HIP_TRY(ctx, hipEventCreate(&p.e1));
+  OBS_HIP_TRY(ctx, hipEventRecord(p.e0, ctx->stream));
+  ctx->prof_pairs.push_back(p);
+  return OBS_OK;
+}
+
+int prof_end(obs_ctx* ctx) {
+  if (!ctx->prof_on || ctx->prof_pairs.empty()) return OBS_OK;
+  OBS_HIP_TRY(ctx, hipEventRecord(ctx->prof_pairs.back().e1, ctx->stream));
+  return OBS_OK;
 }
 
 int ensure_decode_ws(obs_ctx* ctx, size_t bytes, void** out) {
@@ -81,6 +104,7 @@ void obs_destroy(obs_ctx* ctx) {
   if (!ctx) return;
   (void)hipSetDevice(ctx->device);
   if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+  (void)obs_profile_clear(ctx);
   if (ctx->decode_ws) (void)hipFree(ctx->decode_ws);
   if (ctx->ev_start) (void)hipEventDestroy(ctx->ev_start);
   if (ctx->ev_stop) (void)hipEventDestroy(ctx->ev_stop);
@@ -156,6 +180,103 @@ int obs_timer_stop(obs_ctx* ctx, float* ms) {
   OBS_HIP_TRY(ctx, hipEventRecord(ctx->ev_stop, ctx->stream));
   OBS_HIP_TRY(ctx, hipEventSynchronize(ctx->ev_stop));
   OBS_HIP_TRY(ctx, hipEventElapsedTime(ms, ctx->ev_start, ctx->ev_stop));
+  return OBS_OK;
+}
+
+int obs_capture_begin(obs_ctx* ctx) {
+  if (!ctx) return OBS_E_INVALID;
+  OBS_HIP_TRY(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+  return OBS_OK;
+}
+
+int obs_capture_end(obs_ctx* ctx, obs_graph** out) {
+  if (!ctx || !out) return OBS_E_INVALID;
+  *out = nullptr;
+  obs_graph* g = new obs_graph();
+  hipError_t e = hipStreamEndCapture(ctx->stream, &g->graph);
+  if (e != hipSuccess) {
+    delete g;
+    return obs::set_error(ctx, OBS_E_HIP, "hipStreamEndCapture failed: %s", hipGetErrorString(e));
+  }
+  e = hipGraphInstantiate(&g->exec, g->graph, nullptr, nullptr, 0);
+  if (e != hipSuccess) {
+    (void)hipGraphDestroy(g->graph);
+    delete g;
+    return obs::set_error(ctx, OBS_E_HIP, "hipGraphInstantiate failed: %s", hipGetErrorString(e));
+  }
+  *out = g;
+  return OBS_OK;
+}
+
+int obs_graph_launch(obs_ctx* ctx, obs_graph* g) {
+  if (!ctx || !g || !g->exec) return OBS_E_INVALID;
+  OBS_HIP_TRY(ctx, hipGraphLaunch(g->exec, ctx->stream));
+  return OBS_OK;
+}
+
+void obs_graph_destroy(obs_graph* g) {
+  if (!g) return;
+  if (g->exec) (void)hipGraphExecDestroy(g->exec);
+  if (g->graph) (void)hipGraphDestroy(g->graph);
+  delete g;
+}
+
+int obs_stream_hold(obs_ctx* ctx, uint32_t us) {
+  if (!ctx) return OBS_E_INVALID;
+  if (us > 1000000u) us = 1000000u;
+  int rate_khz = 0;
+  OBS_HIP_TRY(ctx, hipDeviceGetAttribute(&rate_khz, hipDeviceAttributeWallClockRate, ctx->device));
+  if (rate_khz <= 0) rate_khz = 100000;
+  const uint64_t ticks = static_cast<uint64_t>(us) * static_cast<uint64_t>(rate_khz) / 1000u;
+  hold_kernel<<<1, 64, 0, ctx->stream>>>(ticks);
+  OBS_LAUNCH_CHECK(ctx);
+  return OBS_OK;
+}
+
+int obs_profile_enable(obs_ctx* ctx, int on) {
+  if (!ctx) return OBS_E_INVALID;
+  ctx->prof_on = on != 0;
+  return OBS_OK;
+}
+
+int obs_profile_accumulate(obs_ctx* ctx) {
+  if (!ctx) return OBS_E_INVALID;
+  OBS_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+  for (const obs_prof_pair& p : ctx->prof_pairs) {
+    float ms = 0.0f;
+    OBS_HIP_TRY(ctx, hipEventElapsedTime(&ms, p.e0, p.e1));
+    obs_prof_stat* st = nullptr;
+    for (obs_prof_stat& s : ctx->prof_stats)
+      if (std::strcmp(s.name, p.name) == 0) st = &s;
+    if (!st) {
+      ctx->prof_stats.push_back({p.name, 0.0, 0});
+      st = &ctx->prof_stats.back();
+    }
+    st->total_ms += ms;
+    st->launches += 1;
+  }
+  return OBS_OK;
+}
+
+int obs_profile_count(const obs_ctx* ctx) { return ctx ? static_cast<int>(ctx->prof_stats.size()) : 0; }
+
+int obs_profile_stat(const obs_ctx* ctx, int i, const char** name, double* total_ms, int64_t* launches) {
+  if (!ctx || i < 0 || i >= static_cast<int>(ctx->prof_stats.size())) return OBS_E_INVALID;
+  const obs_prof_stat& s = ctx->prof_stats[static_cast<size_t>(i)];
+  if (name) *name = s.name;
+  if (total_ms) *total_ms = s.total_ms;
+  if (launches) *launches = s.launches;
+  return OBS_OK;
+}
+
+int obs_profile_clear(obs_ctx* ctx) {
+  if (!ctx) return OBS_E_INVALID;
+  for (obs_prof_pair& p : ctx->prof_pairs) {
+    (void)hipEventDestroy(p.e0);
+    (void)hipEventDestroy(p.e1);
+  }
+  ctx->prof_pairs.clear();
+  ctx->prof_stats.clear();
   return OBS_OK;
 }
 

@@ -229,21 +229,22 @@ int launch_decode_experts(obs_ctx* ctx, const obs_moe_config* cfg, const obs_moe
   const uint32_t gu_blocks = (rows + GU_WAVES * GU_ROWS_PER_WAVE - 1) / (GU_WAVES * GU_ROWS_PER_WAVE);
   switch (H) {
     case 1024:
-      decode_gateup_kernel<2><<<gu_blocks, GU_WAVES * 64, 0, ctx->stream>>>(L->gate_w, L->gate_s, L->gate_b, L->up_w, L->up_s, L->up_b, x, ids, h, E, k, H, I, G);
+      OBS_LAUNCH(ctx, "decode_gateup", decode_gateup_kernel<2><<<gu_blocks, GU_WAVES * 64, 0, ctx->stream>>>(L->gate_w, L->gate_s, L->gate_b, L->up_w, L->up_s, L->up_b, x, ids, h, E, k, H, I, G));
       break;
     case 2048:
-      decode_gateup_kernel<4><<<gu_blocks, GU_WAVES * 64, 0, ctx->stream>>>(L->gate_w, L->gate_s, L->gate_b, L->up_w, L->up_s, L->up_b, x, ids, h, E, k, H, I, G);
+      OBS_LAUNCH(ctx, "decode_gateup", decode_gateup_kernel<4><<<gu_blocks, GU_WAVES * 64, 0, ctx->stream>>>(L->gate_w, L->gate_s, L->gate_b, L->up_w, L->up_s, L->up_b, x, ids, h, E, k, H, I, G));
       break;
     default:
-      decode_gateup_kernel<8><<<gu_blocks, GU_WAVES * 64, 0, ctx->stream>>>(L->gate_w, L->gate_s, L->gate_b, L->up_w, L->up_s, L->up_b, x, ids, h, E, k, H, I, G);
+      OBS_LAUNCH(ctx, "decode_gateup", decode_gateup_kernel<8><<<gu_blocks, GU_WAVES * 64, 0, ctx->stream>>>(L->gate_w, L->gate_s, L->gate_b, L->up_w, L->up_s, L->up_b, x, ids, h, E, k, H, I, G));
       break;
   }
-  OBS_LAUNCH_CHECK(ctx);
   const uint32_t dn_blocks = (H + DN_WAVES * DN_ROWS_PER_WAVE - 1) / (DN_WAVES * DN_ROWS_PER_WAVE);
   const size_t lds = sizeof(float) * k * I;
-#define OBS_DOWN(CPL)                                                                                   \
-  decode_down_kernel<CPL><<<dn_blocks, DN_WAVES * 64, lds, ctx->stream>>>(L->down_w, L->down_s, L->down_b, h, \
-                                                                          ids, w, residual, y, E, k, H, I, G)
+#define OBS_DOWN(CPL)                                                                                       \
+  OBS_LAUNCH(ctx, "decode_down",                                                                            \
+             decode_down_kernel<CPL><<<dn_blocks, DN_WAVES * 64, lds, ctx->stream>>>(L->down_w, L->down_s,  \
+                                                                                     L->down_b, h, ids, w,  \
+                                                                                     residual, y, E, k, H, I, G))
   switch (I / 8) {
     case 32: OBS_DOWN(32); break;
     case 64: OBS_DOWN(64); break;
@@ -255,7 +256,6 @@ int launch_decode_experts(obs_ctx* ctx, const obs_moe_config* cfg, const obs_moe
     default: OBS_DOWN(256); break;
   }
 #undef OBS_DOWN
-  OBS_LAUNCH_CHECK(ctx);
   return OBS_OK;
 }
 

@@ -26,8 +26,7 @@ int obs_swiglu(obs_ctx* ctx, const uint16_t* g, const uint16_t* u, uint16_t* h, 
   if (!ctx) return OBS_E_INVALID;
   if (!g || !u || !h) return obs::set_error(ctx, OBS_E_INVALID, "obs_swiglu: null pointer");
   if (n == 0) return OBS_OK;
-  swiglu_kernel<<<(n + 255) / 256, 256, 0, ctx->stream>>>(g, u, h, n);
-  OBS_LAUNCH_CHECK(ctx);
+  OBS_LAUNCH(ctx, "swiglu", swiglu_kernel<<<(n + 255) / 256, 256, 0, ctx->stream>>>(g, u, h, n));
   return OBS_OK;
 }
 
@@ -35,8 +34,7 @@ int obs_scaled_add(obs_ctx* ctx, uint16_t* acc, const uint16_t* y, float scale, 
   if (!ctx) return OBS_E_INVALID;
   if (!acc || !y) return obs::set_error(ctx, OBS_E_INVALID, "obs_scaled_add: null pointer");
   if (n == 0) return OBS_OK;
-  scaled_add_kernel<<<(n + 255) / 256, 256, 0, ctx->stream>>>(acc, y, scale, n);
-  OBS_LAUNCH_CHECK(ctx);
+  OBS_LAUNCH(ctx, "scaled_add", scaled_add_kernel<<<(n + 255) / 256, 256, 0, ctx->stream>>>(acc, y, scale, n));
   return OBS_OK;
 }
 

@@ -7,12 +7,23 @@
 #include <cstdint>
 #include <cstdio>
 #include <string>
+#include <vector>
 
 #include "../../include/obsidian_hip.h"
 
 // ---------------------------------------------------------------------------
 // Context
 // ---------------------------------------------------------------------------
+struct obs_prof_pair {
+  const char* name;
+  hipEvent_t e0, e1;
+};
+struct obs_prof_stat {
+  const char* name;
+  double total_ms;
+  int64_t launches;
+};
+
 struct obs_ctx {
   int device = 0;
   int num_cus = 0;
@@ -23,11 +34,25 @@ struct obs_ctx {
   // decode workspace (logits, ids, weights, h, sync counters), grown on demand
   void* decode_ws = nullptr;
   size_t decode_ws_bytes = 0;
+  // in-stream kernel timing
+  bool prof_on = false;
+  std::vector<obs_prof_pair> prof_pairs;
+  std::vector<obs_prof_stat> prof_stats;
+};
+
+struct obs_graph {
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
 };
 
 namespace obs {
 
 int set_error(obs_ctx* ctx, int code, const char* fmt, ...);
+
+// Kernel bracketing for obs_profile_*: call prof_begin before a launch and
+// prof_end after it; both are no-ops unless profiling is enabled.
+int prof_begin(obs_ctx* ctx, const char* name);
+int prof_end(obs_ctx* ctx);
 
 #define OBS_HIP_TRY(ctx, call)                                                   \
   do {                                                                           \
@@ -39,6 +64,17 @@ int set_error(obs_ctx* ctx, int code, const char* fmt, ...);
 
 // Checks the launch just issued (invalid configuration and the like).
 #define OBS_LAUNCH_CHECK(ctx) OBS_HIP_TRY(ctx, hipGetLastError())
+
+// Launch statement bracketed for in-stream timing, then checked.
+#define OBS_LAUNCH(ctx, name, ...)                         \
+  do {                                                     \
+    int rc_ = ::obs::prof_begin((ctx), (name));            \
+    if (rc_) return rc_;                                   \
+    __VA_ARGS__;                                           \
+    OBS_LAUNCH_CHECK(ctx);                                 \
+    rc_ = ::obs::prof_end(ctx);                            \
+    if (rc_) return rc_;                                   \
+  } while (0)
 
 inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 

@@ -106,10 +106,9 @@ int obs_dequant(obs_ctx* ctx, int bits, const uint32_t* w, const uint16_t* scale
   const uint64_t n = static_cast<uint64_t>(rows) * (cols / per);
   const uint32_t blocks = static_cast<uint32_t>((n + 255) / 256);
   if (bits == 4)
-    dequant_kernel<4><<<blocks, 256, 0, ctx->stream>>>(w, scales, biases, out_f32, out_bf16, rows, cols, group);
+    OBS_LAUNCH(ctx, "dequant4", dequant_kernel<4><<<blocks, 256, 0, ctx->stream>>>(w, scales, biases, out_f32, out_bf16, rows, cols, group));
   else
-    dequant_kernel<8><<<blocks, 256, 0, ctx->stream>>>(w, scales, biases, out_f32, out_bf16, rows, cols, group);
-  OBS_LAUNCH_CHECK(ctx);
+    OBS_LAUNCH(ctx, "dequant8", dequant_kernel<8><<<blocks, 256, 0, ctx->stream>>>(w, scales, biases, out_f32, out_bf16, rows, cols, group));
   return OBS_OK;
 }
 
@@ -126,8 +125,7 @@ int obs_q4_matvec(obs_ctx* ctx, const uint32_t* w, const uint16_t* scales, const
     return obs::set_error(ctx, OBS_E_SHAPE, "obs_q4_matvec: in (%u) must be a non-zero multiple of group (%u), group a multiple of 8", in, group);
   if (!obs::aligned(x, 16)) return obs::set_error(ctx, OBS_E_ALIGN, "obs_q4_matvec: x must be 16-byte aligned");
   const uint32_t blocks = (out + 3) / 4;
-  q4_matvec_kernel<<<blocks, 256, 0, ctx->stream>>>(w, scales, biases, x, y_f32, y_bf16, in, out, group);
-  OBS_LAUNCH_CHECK(ctx);
+  OBS_LAUNCH(ctx, "q4_matvec", q4_matvec_kernel<<<blocks, 256, 0, ctx->stream>>>(w, scales, biases, x, y_f32, y_bf16, in, out, group));
   return OBS_OK;
 }
 

@@ -186,19 +186,17 @@ int launch_gate_logits(obs_ctx* ctx, const uint32_t* w8, const uint16_t* s, cons
                        uint32_t group) {
   dim3 grid((n_exp + 3) / 4, (T + ROUTER_TOKENS_PER_WAVE - 1) / ROUTER_TOKENS_PER_WAVE);
   switch (in) {
-    case 512: q8_gate_logits_kernel<2><<<grid, 256, 0, ctx->stream>>>(w8, s, b, x, logits, T, in, n_exp, group); break;
-    case 1024: q8_gate_logits_kernel<4><<<grid, 256, 0, ctx->stream>>>(w8, s, b, x, logits, T, in, n_exp, group); break;
-    case 2048: q8_gate_logits_kernel<8><<<grid, 256, 0, ctx->stream>>>(w8, s, b, x, logits, T, in, n_exp, group); break;
-    default: q8_gate_logits_kernel<16><<<grid, 256, 0, ctx->stream>>>(w8, s, b, x, logits, T, in, n_exp, group); break;
+    case 512: OBS_LAUNCH(ctx, "q8_gate_logits", q8_gate_logits_kernel<2><<<grid, 256, 0, ctx->stream>>>(w8, s, b, x, logits, T, in, n_exp, group)); break;
+    case 1024: OBS_LAUNCH(ctx, "q8_gate_logits", q8_gate_logits_kernel<4><<<grid, 256, 0, ctx->stream>>>(w8, s, b, x, logits, T, in, n_exp, group)); break;
+    case 2048: OBS_LAUNCH(ctx, "q8_gate_logits", q8_gate_logits_kernel<8><<<grid, 256, 0, ctx->stream>>>(w8, s, b, x, logits, T, in, n_exp, group)); break;
+    default: OBS_LAUNCH(ctx, "q8_gate_logits", q8_gate_logits_kernel<16><<<grid, 256, 0, ctx->stream>>>(w8, s, b, x, logits, T, in, n_exp, group)); break;
   }
-  OBS_LAUNCH_CHECK(ctx);
   return OBS_OK;
 }
 
 int launch_route_topk(obs_ctx* ctx, const float* logits, int32_t* ids, float* w, uint32_t T,
                       uint32_t n_exp, uint32_t k, int norm_topk) {
-  route_topk_kernel<<<(T + 3) / 4, 256, 0, ctx->stream>>>(logits, ids, w, T, n_exp, k, norm_topk);
-  OBS_LAUNCH_CHECK(ctx);
+  OBS_LAUNCH(ctx, "route_topk", route_topk_kernel<<<(T + 3) / 4, 256, 0, ctx->stream>>>(logits, ids, w, T, n_exp, k, norm_topk));
   return OBS_OK;
 }
 

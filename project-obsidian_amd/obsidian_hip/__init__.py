@@ -48,7 +48,9 @@ EXPORTS = (
     "obs_get_stream", "obs_alloc", "obs_free", "obs_upload", "obs_download", "obs_memset",
     "obs_sync", "obs_timer_start", "obs_timer_stop", "obs_dequant", "obs_q4_matvec",
     "obs_q4_matmul", "obs_q8_gate_logits", "obs_route_topk", "obs_swiglu", "obs_scaled_add",
-    "obs_moe_decode", "obs_moe_prefill_workspace", "obs_moe_prefill",
+    "obs_moe_decode", "obs_moe_prefill_workspace", "obs_moe_prefill", "obs_capture_begin",
+    "obs_capture_end", "obs_graph_launch", "obs_graph_destroy", "obs_stream_hold", "obs_profile_enable",
+    "obs_profile_accumulate", "obs_profile_count", "obs_profile_stat", "obs_profile_clear",
 )
 
 
@@ -107,6 +109,17 @@ def lib() -> C.CDLL:
         "obs_moe_prefill_workspace": (sz, [C.POINTER(ObsMoeConfig), u32]),
         "obs_moe_prefill": (i32, [vp, C.POINTER(ObsMoeConfig), C.POINTER(ObsMoeLayer), vp, vp, vp, u32,
                                   vp, vp, vp, sz]),
+        "obs_capture_begin": (i32, [vp]),
+        "obs_capture_end": (i32, [vp, C.POINTER(vp)]),
+        "obs_graph_launch": (i32, [vp, vp]),
+        "obs_graph_destroy": (None, [vp]),
+        "obs_stream_hold": (i32, [vp, u32]),
+        "obs_profile_enable": (i32, [vp, C.c_int]),
+        "obs_profile_accumulate": (i32, [vp]),
+        "obs_profile_count": (C.c_int, [vp]),
+        "obs_profile_stat": (i32, [vp, C.c_int, C.POINTER(C.c_char_p), C.POINTER(C.c_double),
+                                   C.POINTER(C.c_int64)]),
+        "obs_profile_clear": (i32, [vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -212,6 +225,45 @@ class ObsidianExecutor:
 
     def set_stream(self, stream: Optional[int]) -> None:
         self._check(lib().obs_set_stream(self.ctx, stream))
+
+    # -- graph capture / replay ------------------------------------------
+    def capture_begin(self) -> None:
+        self._check(lib().obs_capture_begin(self.ctx))
+
+    def capture_end(self) -> int:
+        g = C.c_void_p()
+        self._check(lib().obs_capture_end(self.ctx, C.byref(g)))
+        return g.value
+
+    def graph_launch(self, graph: int) -> None:
+        self._check(lib().obs_graph_launch(self.ctx, graph))
+
+    @staticmethod
+    def graph_destroy(graph: int) -> None:
+        lib().obs_graph_destroy(graph)
+
+    # -- in-stream kernel timing -------------------------------------------
+    def stream_hold(self, us: int) -> None:
+        self._check(lib().obs_stream_hold(self.ctx, int(us)))
+
+    def profile_enable(self, on: bool) -> None:
+        self._check(lib().obs_profile_enable(self.ctx, int(bool(on))))
+
+    def profile_accumulate(self) -> None:
+        self._check(lib().obs_profile_accumulate(self.ctx))
+
+    def profile_stats(self) -> Dict[str, Tuple[float, int]]:
+        """{kernel name: (total ms, launches)}"""
+        L = lib()
+        out = {}
+        for i in range(L.obs_profile_count(self.ctx)):
+            name, ms, n = C.c_char_p(), C.c_double(), C.c_int64()
+            self._check(L.obs_profile_stat(self.ctx, i, C.byref(name), C.byref(ms), C.byref(n)))
+            out[name.value.decode()] = (ms.value, n.value)
+        return out
+
+    def profile_clear(self) -> None:
+        self._check(lib().obs_profile_clear(self.ctx))
 
     def close(self) -> None:
         if getattr(self, "ctx", None):
