@@ -117,13 +117,16 @@ def bench_decode(torch, oh, exe, args):
     for g in graphs:
         exe.graph_destroy(g)
     kernels = {n: {"avg_us": 1000.0 * t / c, "launches": c} for n, (t, c) in stats.items()}
-    gu = kernels.get("decode_gateup")
+    # the fused layer kernel moves all of a layer's algorithmic bytes; the
+    # 4-launch path's largest kernel is gate/up
+    name, nbytes = ("decode_fused", LAYER_BYTES) if "decode_fused" in kernels else ("decode_gateup", GATEUP_BYTES)
     roof = None
-    if gu:
-        ach = GATEUP_BYTES / (gu["avg_us"] * 1e-6) / 1e9
-        roof = {"kernel": "decode_gateup", "bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
+    if name in kernels:
+        us = kernels[name]["avg_us"]
+        ach = nbytes / (us * 1e-6) / 1e9
+        roof = {"kernel": name, "bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
-                "bytes_per_launch": GATEUP_BYTES, "avg_launch_us": round(gu["avg_us"], 3)}
+                "bytes_per_launch": nbytes, "avg_launch_us": round(us, 3)}
     del table, xs, ys
     torch.cuda.empty_cache()
     return {"ms_step": ms_step, "us_layer": us_layer, "gbs": gbs, "kernels": kernels, "roofline": roof}

@@ -198,10 +198,26 @@ typedef struct obs_moe_layer {
  * weighted sum in rank order. x, y bf16 [hidden]. If residual is non-NULL,
  * y = residual + sum (forward.rs:440 accumulates into the residual stream x1).
  * ids_out [top_k] / w_out [top_k] (may be NULL) receive the routing.
- * Workspace comes from the context (allocated once, on first use). */
+ * Workspace comes from the context (allocated once, on first use: make the
+ * first call outside a graph capture).
+ * For hidden 2048 / inter 768 / top_k 8 / group 64 (Qwen3-30B-A3B) the layer
+ * runs as ONE launch of 256 workgroups that exchange data through bounded
+ * device-side waits; it needs the GPU's CUs free for that launch (no other
+ * kernel holding them). A wait that times out is reported by
+ * obs_device_status(). Other shapes run as 4 launches. */
 int obs_moe_decode(obs_ctx* ctx, const obs_moe_config* cfg, const obs_moe_layer* layer,
                    const uint16_t* x, const uint16_t* residual, uint16_t* y,
                    int32_t* ids_out, float* w_out);
+
+/* Decode path selection (no reference counterpart; like the reference's
+ * OBSIDIAN_NO_GEMM switch, forward.rs:125-126, it exists to compare paths). */
+enum { OBS_DECODE_AUTO = 0, OBS_DECODE_MULTI = 1, OBS_DECODE_FUSED = 2 };
+int obs_set_decode_path(obs_ctx* ctx, int path);
+
+/* Waits for the stream, then reports (OBS_E_HIP + message) and clears a
+ * device-side failure of the fused decode path (a bounded wait that timed
+ * out); OBS_OK otherwise. The reference never checks GPU status. */
+int obs_device_status(obs_ctx* ctx);
 
 /* Workspace bytes obs_moe_prefill needs for T tokens. */
 size_t obs_moe_prefill_workspace(const obs_moe_config* cfg, uint32_t T);

@@ -162,7 +162,7 @@ int orc_qmatvec_shader(int bits, const uint32_t* w, const uint16_t* s, const uin
 }
 
 /* The documented lane order: lane l owns columns [l*in/L, (l+1)*in/L), serial
- * fmaf accumulation; lanes combined by an xor butterfly with offsets L/2..1
+ * fmaf accumulation; lanes combined by an xor butterfly with offsets 1, 2, ..., L/2
  * (every lane ends with the same value; lane 0's is returned). */
 static float row_dot_lanes(int bits, const uint32_t* wr, const uint16_t* sr, const uint16_t* br,
                            int sb_type, const float* x, int64_t in, int group, int lanes) {
@@ -177,7 +177,7 @@ static float row_dot_lanes(int bits, const uint32_t* wr, const uint16_t* sr, con
     }
     part[l] = acc;
   }
-  for (int off = lanes / 2; off >= 1; off >>= 1) {
+  for (int off = 1; off < lanes; off <<= 1) {
     float nxt[256];
     for (int l = 0; l < lanes; ++l) nxt[l] = part[l] + part[l ^ off];
     memcpy(part, nxt, sizeof(float) * (size_t)lanes);
@@ -269,7 +269,7 @@ static void route_one(const float* l, int n, int k, int norm_topk, int sum_order
       for (int j = ln; j < n; j += 64) a = a + p[j];
       part[ln] = a;
     }
-    for (int off = 32; off >= 1; off >>= 1) {
+    for (int off = 1; off < 64; off <<= 1) {
       float nxt[64];
       for (int ln = 0; ln < 64; ++ln) nxt[ln] = part[ln] + part[ln ^ off];
       memcpy(part, nxt, sizeof part);

@@ -53,7 +53,7 @@ int orc_dequant(int bits, const uint32_t* w, const uint16_t* s, const uint16_t* 
  * _lanes : the documented fixed order of the HIP router kernel: `lanes` lanes
  *          each own in/lanes contiguous columns, accumulate serially with a
  *          fused multiply-add, then combine by an xor butterfly
- *          (offsets lanes/2, ..., 1).
+ *          (offsets 1, 2, 4, ..., lanes/2, ascending).
  * _f64   : fp64 accumulation of the same fp32 weights (truth), plus
  *          absbound[o] = sum |w*x| for error bounds (may be NULL). */
 int orc_qmatvec_shader(int bits, const uint32_t* w, const uint16_t* s, const uint16_t* b, int sb_type,
@@ -75,7 +75,7 @@ enum { ORC_SUM_SERIAL = 0, ORC_SUM_WAVE = 1 };
  * with wsum the serial fp32 sum of the selected p in selection order.
  * sum_order picks the order of S: serial (the reference kernel) or the wave
  * order of the HIP kernel (lane l sums experts l, l+64, l+128, l+192 in that
- * order, then an xor butterfly over 64 lanes). emulate_f16 = 1 additionally
+ * order, then an xor butterfly over 64 lanes with offsets 1, 2, ..., 32). emulate_f16 = 1 additionally
  * rounds the weights to f16 as moe_routing_topk.metal:49,55 does.
  * A slot with no selectable expert (NaN probabilities) gets id -1, weight 0. */
 int orc_route_topk(const float* logits, int64_t T, int n_exp, int k, int norm_topk,

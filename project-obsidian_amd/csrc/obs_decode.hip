@@ -32,21 +32,6 @@ constexpr int GU_WAVES = 4;
 constexpr int DN_ROWS_PER_WAVE = 2;
 constexpr int DN_WAVES = 4;
 
-// 8 nibbles of `w` times 8 consecutive x values, fp32, fixed order 0..7.
-__device__ __forceinline__ float dot8_q4(uint32_t w, const float* x, float acc) {
-  const uint32_t lo = w & 0x0f0f0f0fu;         // nibbles 0,2,4,6 in bytes 0..3
-  const uint32_t hi = (w >> 4) & 0x0f0f0f0fu;  // nibbles 1,3,5,7
-  acc = __builtin_fmaf(static_cast<float>(lo & 0xffu), x[0], acc);
-  acc = __builtin_fmaf(static_cast<float>(hi & 0xffu), x[1], acc);
-  acc = __builtin_fmaf(static_cast<float>((lo >> 8) & 0xffu), x[2], acc);
-  acc = __builtin_fmaf(static_cast<float>((hi >> 8) & 0xffu), x[3], acc);
-  acc = __builtin_fmaf(static_cast<float>((lo >> 16) & 0xffu), x[4], acc);
-  acc = __builtin_fmaf(static_cast<float>((hi >> 16) & 0xffu), x[5], acc);
-  acc = __builtin_fmaf(static_cast<float>(lo >> 24), x[6], acc);
-  acc = __builtin_fmaf(static_cast<float>(hi >> 24), x[7], acc);
-  return acc;
-}
-
 // h[r, o] = silu(gate_e[o] . x) * (up_e[o] . x) for e = ids[r].
 // One wave per (r, o) row pair; lane l owns the 8*WPL contiguous columns
 // [l*8*WPL, (l+1)*8*WPL), which lie inside one quantization group.
@@ -115,8 +100,8 @@ __global__ void __launch_bounds__(GU_WAVES * 64) decode_gateup_kernel(
       }
       float pg = __builtin_fmaf(sg, ag, bgv * xs);
       float pu = __builtin_fmaf(su, au, bu * xs);
-      pg = wave_sum_xor(pg);
-      pu = wave_sum_xor(pu);
+      pg = wave_sum_asc(pg);
+      pu = wave_sum_asc(pu);
       hv = silu_mul(pg, pu);
     }
     if (lane == 0) h[row] = hv;
@@ -133,7 +118,25 @@ __global__ void __launch_bounds__(DN_WAVES * 64) decode_down_kernel(
     uint32_t H, uint32_t I, uint32_t group) {
   constexpr int BLK = CPL / 32;  // 32-column blocks per lane (each inside one group)
   extern __shared__ float sh_h[];  // [k][I]
-  for (uint32_t i = threadIdx.x; i < k * I; i += blockDim.x) sh_h[i] = h[i];
+  {
+    // stage h in batches of 8 independent 16-byte loads per thread (k*I % 4 == 0)
+    const uint32_t n4 = (k * I) / 4;
+    const float4* h4 = reinterpret_cast<const float4*>(h);
+    float4* s4 = reinterpret_cast<float4*>(sh_h);
+    for (uint32_t base = threadIdx.x; base < n4; base += 8 * blockDim.x) {
+      float4 v[8];
+#pragma unroll
+      for (uint32_t u = 0; u < 8; ++u) {
+        const uint32_t i = base + u * blockDim.x;
+        if (i < n4) v[u] = h4[i];
+      }
+#pragma unroll
+      for (uint32_t u = 0; u < 8; ++u) {
+        const uint32_t i = base + u * blockDim.x;
+        if (i < n4) s4[i] = v[u];
+      }
+    }
+  }
   __syncthreads();
   const uint32_t lane = threadIdx.x & 63;
   const uint32_t r = lane >> 3, m = lane & 7;
@@ -272,6 +275,11 @@ int obs_moe_decode(obs_ctx* ctx, const obs_moe_config* cfg, const obs_moe_layer*
   if (rc) return rc;
   if (!x || !y) return obs::set_error(ctx, OBS_E_INVALID, "obs_moe_decode: null x or y");
   if (!obs::aligned(x, 16)) return obs::set_error(ctx, OBS_E_ALIGN, "obs_moe_decode: x must be 16-byte aligned");
+  const bool fused_ok = obs::fused_decode_supported(cfg);
+  if (ctx->decode_path == OBS_DECODE_FUSED && !fused_ok)
+    return obs::set_error(ctx, OBS_E_SHAPE, "obs_moe_decode: the fused path needs hidden 2048, inter 768, top_k 8, group 64, n_exp <= 256");
+  if (fused_ok && ctx->decode_path != OBS_DECODE_MULTI)
+    return obs::launch_fused_decode(ctx, cfg, layer, x, residual, y, ids_out, w_out);
   const uint32_t E = cfg->n_exp, k = cfg->top_k, H = cfg->hidden, I = cfg->inter;
   // workspace: logits [E] | ids [k] | w [k] | h [k, I]
   const size_t off_ids = align256(sizeof(float) * E);
@@ -291,6 +299,19 @@ int obs_moe_decode(obs_ctx* ctx, const obs_moe_config* cfg, const obs_moe_layer*
   rc = obs::launch_route_topk(ctx, logits, ids, w, 1, E, k, cfg->norm_topk);
   if (rc) return rc;
   return obs::launch_decode_experts(ctx, cfg, layer, x, residual, y, ids, w, h);
+}
+
+int obs_set_decode_path(obs_ctx* ctx, int path) {
+  if (!ctx) return OBS_E_INVALID;
+  if (path != OBS_DECODE_AUTO && path != OBS_DECODE_MULTI && path != OBS_DECODE_FUSED)
+    return obs::set_error(ctx, OBS_E_INVALID, "obs_set_decode_path: unknown path %d", path);
+  ctx->decode_path = path;
+  return OBS_OK;
+}
+
+int obs_device_status(obs_ctx* ctx) {
+  if (!ctx) return OBS_E_INVALID;
+  return obs::fused_decode_status(ctx);
 }
 
 }  // extern "C"

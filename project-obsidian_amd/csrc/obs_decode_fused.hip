@@ -1,0 +1,386 @@
+// obs_decode_fused.hip — the decode MoE half of one layer (src/forward.rs:421-441)
+// in ONE launch, for the Qwen3-30B-A3B expert shape (hidden 2048, moe_inter 768,
+// top-8, group 64, up to 256 experts).
+//
+// Why one launch: at T=1 the layer moves ~21.5 MB, 2.7 us at the 8 TB/s HBM
+// peak, while every kernel boundary costs ~1.6 us even inside a HIP graph and
+// an agent-scope release or acquire fence costs 2-5 us. The layer therefore
+// runs as 256 workgroups (one per CU) that exchange the few values that cross
+// workgroups — router logits, the SwiGLU activations h, the per-expert down
+// outputs — through epoch-tagged 64-bit slots written and polled with relaxed
+// device-coherent atomics. A reader spins until every slot it needs carries the
+// current launch's epoch, so the value arrives with the flag: no counters, no
+// fences, no second round trip.
+//
+// Work split. Workgroup b belongs to group g = b % 8 (the hardware dispatches
+// consecutive workgroups round-robin over the 8 XCDs, so a group shares one L2)
+// and has index j = b / 8 within it.
+//   1. Router: each group computes all E logits (one 2 KB row per wave) in the
+//      router's documented reduction order, so every group sees bit-identical
+//      logits; then every wave runs softmax + top-8 itself (no broadcast).
+//   2. Group g serves routing rank g: expert e_g = ids[g]. Its 128 waves stream
+//      the 768 gate and up rows (6 each) and, at the same time, the down rows the
+//      workgroup will need (64 rows x 384 B per workgroup), so the down weights
+//      arrive during the gate/up phase.
+//   3. h = silu(gate.x) * (up.x) goes to the group's h slots; each workgroup
+//      polls all 768 into LDS and finishes its 64 down rows from registers.
+//   4. Group 0 combines: workgroup j polls the 8 ranks' outputs for its 64 rows
+//      and accumulates residual + sum_r w_r * y_r in rank order (forward.rs:440).
+// The last workgroup to exit advances the launch counter that defines the next
+// launch's epoch, so graph replays need no host involvement.
+//
+// Every wait is bounded (100 ms on the GPU's constant clock); a timeout sets a
+// device error flag, later launches then exit at once, and obs_device_status()
+// reports it and resets the workspace.
+#include "obs_internal.hpp"
+
+namespace {
+
+using namespace obsd;
+
+constexpr uint32_t FH = 2048, FI = 768, FK = 8, FG = 64;
+constexpr uint32_t NGROUP = 8, WG_PER_GROUP = 32, NWG = NGROUP * WG_PER_GROUP;
+constexpr uint32_t MAX_E = 256;
+constexpr uint32_t GU_ROWS = FI / (WG_PER_GROUP * 4);  // gate/up rows per wave: 6
+constexpr uint32_t DN_ROWS_WG = FH / WG_PER_GROUP;     // down rows per workgroup: 64
+
+constexpr size_t WS_LAUNCH = 0, WS_EXIT = 128, WS_ERR = 256;
+constexpr size_t WS_LOGITS = 1024;                              // [8][MAX_E] slots
+constexpr size_t WS_H = WS_LOGITS + size_t(NGROUP) * MAX_E * 8;  // [8][FI] slots
+constexpr size_t WS_Y = WS_H + size_t(NGROUP) * FI * 8;          // [8][FH] slots
+constexpr size_t WS_BYTES = WS_Y + size_t(NGROUP) * FH * 8;
+constexpr uint64_t WAIT_TICKS = 10000000ull;  // 100 ms at 100 MHz
+
+struct FusedArgs {
+  const uint32_t* gate_w; const uint16_t* gate_s; const uint16_t* gate_b;
+  const uint32_t* up_w; const uint16_t* up_s; const uint16_t* up_b;
+  const uint32_t* down_w; const uint16_t* down_s; const uint16_t* down_b;
+  const uint32_t* router_w; const uint16_t* router_s; const uint16_t* router_b;
+  const uint16_t* x; const uint16_t* residual; uint16_t* y;
+  int32_t* ids_out; float* w_out;
+  unsigned char* ws;
+  uint32_t n_exp;
+  int norm_topk;
+};
+
+__device__ __forceinline__ void slot_store(uint64_t* p, uint32_t epoch, float v) {
+  __hip_atomic_store(p, (static_cast<uint64_t>(epoch) << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t slot_load(const uint64_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ bool slot_ready(uint64_t v, uint32_t epoch) {
+  return static_cast<uint32_t>(v >> 32) == epoch;
+}
+__device__ __forceinline__ float slot_val(uint64_t v) { return __uint_as_float(static_cast<uint32_t>(v)); }
+
+__device__ __forceinline__ void raise_error(unsigned char* ws) {
+  __hip_atomic_store(reinterpret_cast<uint32_t*>(ws + WS_ERR), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ void unpack_bf16x8(const uint4& v, float* f) {
+  f[0] = bf16lo(v.x); f[1] = bf16hi(v.x); f[2] = bf16lo(v.y); f[3] = bf16hi(v.y);
+  f[4] = bf16lo(v.z); f[5] = bf16hi(v.z); f[6] = bf16lo(v.w); f[7] = bf16hi(v.w);
+}
+
+__global__ void __launch_bounds__(256, 1) decode_fused_kernel(FusedArgs a) {
+  __shared__ uint32_t s_epoch;
+  __shared__ int s_abort;
+  __shared__ float s_h[FI];
+  __shared__ float s_y[FK][64];
+
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  const uint32_t g = blockIdx.x % NGROUP, j = blockIdx.x / NGROUP;
+  uint32_t* ctl_launch = reinterpret_cast<uint32_t*>(a.ws + WS_LAUNCH);
+  uint32_t* ctl_exit = reinterpret_cast<uint32_t*>(a.ws + WS_EXIT);
+  const uint32_t* ctl_err = reinterpret_cast<const uint32_t*>(a.ws + WS_ERR);
+  uint64_t* logit_slots = reinterpret_cast<uint64_t*>(a.ws + WS_LOGITS) + size_t(g) * MAX_E;
+  uint64_t* h_slots = reinterpret_cast<uint64_t*>(a.ws + WS_H) + size_t(g) * FI;
+  uint64_t* y_slots = reinterpret_cast<uint64_t*>(a.ws + WS_Y);
+  const uint32_t n_exp = a.n_exp;
+
+  if (tid == 0) {
+    s_epoch = __hip_atomic_load(ctl_launch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+    s_abort = __hip_atomic_load(ctl_err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u;
+  }
+  // this lane's 32 input columns [32*lane, 32*lane + 32)
+  uint4 xq[4];
+  {
+    const uint4* xp = reinterpret_cast<const uint4*>(a.x + 32u * lane);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) xq[i] = xp[i];
+  }
+  // router rows of this wave: e = 4j + wave (+128)
+  const uint32_t e0 = 4u * j + wave;
+  uint4 rq[2][2];
+  uint16_t rs[2], rb[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const uint32_t e = e0 + 128u * t;
+    if (e < n_exp) {
+      const uint4* rp = reinterpret_cast<const uint4*>(a.router_w + size_t(e) * (FH / 4) + 8u * lane);
+      rq[t][0] = rp[0];
+      rq[t][1] = rp[1];
+      rs[t] = a.router_s[size_t(e) * (FH / FG) + lane / 2u];
+      rb[t] = a.router_b[size_t(e) * (FH / FG) + lane / 2u];
+    }
+  }
+  __syncthreads();
+  const uint32_t epoch = s_epoch;
+  if (s_abort) return;  // a previous launch failed: the host must reset first
+
+  float xf[32];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) unpack_bf16x8(xq[i], xf + 8 * i);
+  float xs = 0.0f;
+#pragma unroll
+  for (int c = 0; c < 32; ++c) xs = xs + xf[c];
+
+  // ---- 1. router logits (order of obs_q8_gate_logits: serial fma, then wave_sum_asc)
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const uint32_t e = e0 + 128u * t;
+    if (e < n_exp) {  // wave-uniform
+      const float sc = bf16_to_f32(rs[t]), bi = bf16_to_f32(rb[t]);
+      const uint32_t wd[8] = {rq[t][0].x, rq[t][0].y, rq[t][0].z, rq[t][0].w,
+                              rq[t][1].x, rq[t][1].y, rq[t][1].z, rq[t][1].w};
+      float acc = 0.0f;
+#pragma unroll
+      for (int c = 0; c < 32; ++c) {
+        const float wv = __builtin_fmaf(static_cast<float>((wd[c >> 2] >> (8 * (c & 3))) & 0xffu), sc, bi);
+        acc = __builtin_fmaf(wv, xf[c], acc);
+      }
+      acc = wave_sum_asc(acc);
+      if (lane == 0) slot_store(logit_slots + e, epoch, acc);
+    }
+  }
+
+  // ---- 2. every wave polls its group's logits and routes the token
+  bool ok = true;
+  float lg[4];
+  {
+    const uint64_t t0 = wall_clock64();
+    while (true) {
+      bool ready = true;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t idx = lane + 64u * q;
+        lg[q] = 0.0f;
+        if (idx < n_exp) {
+          const uint64_t v = slot_load(logit_slots + idx);
+          lg[q] = slot_val(v);
+          ready = ready && slot_ready(v, epoch);
+        }
+      }
+      if (__all(ready)) break;
+      if (wall_clock64() - t0 > WAIT_TICKS) { ok = false; break; }
+    }
+  }
+  if (!ok && lane == 0) raise_error(a.ws);
+  int32_t sel_id;
+  float sel_w;
+  route_wave(lg, n_exp, FK, a.norm_topk, lane, &sel_id, &sel_w);
+  if (blockIdx.x == 0 && wave == 0 && lane < FK) {
+    if (a.ids_out) a.ids_out[lane] = sel_id;
+    if (a.w_out) a.w_out[lane] = sel_w;
+  }
+  const int32_t eg = __builtin_amdgcn_readlane(sel_id, static_cast<int>(g));
+  const bool have = ok && eg >= 0 && static_cast<uint32_t>(eg) < n_exp;
+
+  // ---- 3. issue every weight load this wave needs: 6 gate + 6 up rows, 2x3 down blocks
+  uint4 gq[GU_ROWS], uq[GU_ROWS];
+  uint16_t gsv[GU_ROWS], gbv[GU_ROWS], usv[GU_ROWS], ubv[GU_ROWS];
+  uint4 dq[2][3];
+  uint16_t dsv[2][3], dbv[2][3];
+  const uint32_t m = lane & 7u;         // down column slice [96m, 96m + 96)
+  const uint32_t r8 = lane >> 3;        // down row within an 8-row pass
+  if (have) {
+    const size_t eoff_gu = size_t(eg) * FI;
+#pragma unroll
+    for (uint32_t t = 0; t < GU_ROWS; ++t) {
+      const size_t row = eoff_gu + e0 + 128u * t;
+      gq[t] = reinterpret_cast<const uint4*>(a.gate_w + row * (FH / 8))[lane];
+      uq[t] = reinterpret_cast<const uint4*>(a.up_w + row * (FH / 8))[lane];
+      gsv[t] = a.gate_s[row * (FH / FG) + lane / 2u];
+      gbv[t] = a.gate_b[row * (FH / FG) + lane / 2u];
+      usv[t] = a.up_s[row * (FH / FG) + lane / 2u];
+      ubv[t] = a.up_b[row * (FH / FG) + lane / 2u];
+    }
+#pragma unroll
+    for (uint32_t p = 0; p < 2; ++p) {
+      const size_t row = size_t(eg) * FH + DN_ROWS_WG * j + 16u * wave + 8u * p + r8;
+      const uint4* dp = reinterpret_cast<const uint4*>(a.down_w + row * (FI / 8) + 12u * m);
+#pragma unroll
+      for (uint32_t b = 0; b < 3; ++b) {
+        dq[p][b] = dp[b];
+        const uint32_t gi = (96u * m + 32u * b) / FG;
+        dsv[p][b] = a.down_s[row * (FI / FG) + gi];
+        dbv[p][b] = a.down_b[row * (FI / FG) + gi];
+      }
+    }
+  }
+
+  // ---- 4. gate/up rows -> h slots (factored per group: s*sum(q x) + b*sum(x))
+#pragma unroll
+  for (uint32_t t = 0; t < GU_ROWS; ++t) {
+    float pg = 0.0f, pu = 0.0f;
+    if (have) {
+      float ag = 0.0f, au = 0.0f;
+      ag = dot8_q4(gq[t].x, xf + 0, ag);
+      ag = dot8_q4(gq[t].y, xf + 8, ag);
+      ag = dot8_q4(gq[t].z, xf + 16, ag);
+      ag = dot8_q4(gq[t].w, xf + 24, ag);
+      au = dot8_q4(uq[t].x, xf + 0, au);
+      au = dot8_q4(uq[t].y, xf + 8, au);
+      au = dot8_q4(uq[t].z, xf + 16, au);
+      au = dot8_q4(uq[t].w, xf + 24, au);
+      pg = __builtin_fmaf(bf16_to_f32(gsv[t]), ag, bf16_to_f32(gbv[t]) * xs);
+      pu = __builtin_fmaf(bf16_to_f32(usv[t]), au, bf16_to_f32(ubv[t]) * xs);
+    }
+    pg = wave_sum_asc(pg);
+    pu = wave_sum_asc(pu);
+    const float hv = have ? silu_mul(pg, pu) : 0.0f;
+    if (lane == 0) slot_store(h_slots + e0 + 128u * t, epoch, hv);
+  }
+
+  // ---- 5. poll the group's 768 h values into LDS
+  {
+    bool wave_ok = ok;
+    const uint64_t t0 = wall_clock64();
+    while (wave_ok) {
+      bool ready = true;
+#pragma unroll
+      for (uint32_t u = 0; u < FI / 256; ++u) {
+        const uint32_t idx = tid + 256u * u;
+        const uint64_t v = slot_load(h_slots + idx);
+        s_h[idx] = slot_val(v);
+        ready = ready && slot_ready(v, epoch);
+      }
+      if (__all(ready)) break;
+      if (wall_clock64() - t0 > WAIT_TICKS) {
+        wave_ok = false;
+        if (lane == 0) raise_error(a.ws);
+      }
+    }
+    ok = ok && wave_ok;
+  }
+  __syncthreads();
+
+  // ---- 6. this workgroup's 64 down rows of expert e_g (unscaled by w_g)
+  {
+    float hsum[3];
+    float hreg[96];
+#pragma unroll
+    for (uint32_t c = 0; c < 96; c += 4) {
+      const float4 v = *reinterpret_cast<const float4*>(s_h + 96u * m + c);
+      hreg[c] = v.x; hreg[c + 1] = v.y; hreg[c + 2] = v.z; hreg[c + 3] = v.w;
+    }
+#pragma unroll
+    for (uint32_t b = 0; b < 3; ++b) {
+      float s = 0.0f;
+#pragma unroll
+      for (uint32_t c = 0; c < 32; ++c) s = s + hreg[32u * b + c];
+      hsum[b] = s;
+    }
+#pragma unroll
+    for (uint32_t p = 0; p < 2; ++p) {
+      float part = 0.0f;
+      if (have) {
+#pragma unroll
+        for (uint32_t b = 0; b < 3; ++b) {
+          float acc = 0.0f;
+          acc = dot8_q4(dq[p][b].x, hreg + 32u * b + 0, acc);
+          acc = dot8_q4(dq[p][b].y, hreg + 32u * b + 8, acc);
+          acc = dot8_q4(dq[p][b].z, hreg + 32u * b + 16, acc);
+          acc = dot8_q4(dq[p][b].w, hreg + 32u * b + 24, acc);
+          part = part + __builtin_fmaf(bf16_to_f32(dsv[p][b]), acc, bf16_to_f32(dbv[p][b]) * hsum[b]);
+        }
+      }
+      part = group8_sum(part);
+      const uint32_t row = DN_ROWS_WG * j + 16u * wave + 8u * p + r8;
+      if (m == 0) slot_store(y_slots + size_t(g) * FH + row, epoch, part);
+    }
+  }
+
+  // ---- 7. group 0: combine the 8 ranks for rows [64j, 64j + 64) in rank order
+  if (g == 0) {
+    bool wave_ok = ok;
+    const uint64_t t0 = wall_clock64();
+    while (wave_ok) {
+      bool ready = true;
+#pragma unroll
+      for (uint32_t u = 0; u < 2; ++u) {
+        const uint32_t s = tid + 256u * u;  // rank s/64, row s%64
+        const uint64_t v = slot_load(y_slots + size_t(s >> 6) * FH + DN_ROWS_WG * j + (s & 63u));
+        s_y[s >> 6][s & 63u] = slot_val(v);
+        ready = ready && slot_ready(v, epoch);
+      }
+      if (__all(ready)) break;
+      if (wall_clock64() - t0 > WAIT_TICKS) {
+        wave_ok = false;
+        if (lane == 0) raise_error(a.ws);
+      }
+    }
+    __syncthreads();
+    if (wave == 0) {
+      const uint32_t o = DN_ROWS_WG * j + lane;
+      float acc = a.residual ? bf16_to_f32(a.residual[o]) : 0.0f;
+#pragma unroll
+      for (uint32_t r = 0; r < FK; ++r) acc = __builtin_fmaf(readlane_f32(sel_w, static_cast<int>(r)), s_y[r][lane], acc);
+      a.y[o] = f32_to_bf16(acc);
+    }
+  }
+
+  // ---- 8. exit: the last workgroup advances the launch counter (next epoch)
+  __syncthreads();
+  if (tid == 0) {
+    const uint32_t old = __hip_atomic_fetch_add(ctl_exit, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if ((old + 1u) % NWG == 0u) __hip_atomic_store(ctl_launch, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+}  // namespace
+
+namespace obs {
+
+bool fused_decode_supported(const obs_moe_config* cfg) {
+  return cfg->hidden == FH && cfg->inter == FI && cfg->top_k == FK && cfg->group == FG && cfg->n_exp <= MAX_E;
+}
+
+size_t fused_decode_ws_bytes() { return WS_BYTES; }
+
+int launch_fused_decode(obs_ctx* ctx, const obs_moe_config* cfg, const obs_moe_layer* L, const uint16_t* x,
+                        const uint16_t* residual, uint16_t* y, int32_t* ids_out, float* w_out) {
+  if (!ctx->fused_ws) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    OBS_HIP_TRY(ctx, hipStreamIsCapturing(ctx->stream, &cs));
+    if (cs != hipStreamCaptureStatusNone)
+      return set_error(ctx, OBS_E_INVALID, "obs_moe_decode: run once before capturing (workspace allocation)");
+    OBS_HIP_TRY(ctx, hipMalloc(&ctx->fused_ws, WS_BYTES));
+    OBS_HIP_TRY(ctx, hipMemset(ctx->fused_ws, 0, WS_BYTES));
+    OBS_HIP_TRY(ctx, hipDeviceSynchronize());
+  }
+  FusedArgs a{L->gate_w, L->gate_s, L->gate_b, L->up_w, L->up_s, L->up_b, L->down_w, L->down_s, L->down_b,
+              L->router_w, L->router_s, L->router_b, x, residual, y, ids_out, w_out,
+              static_cast<unsigned char*>(ctx->fused_ws), cfg->n_exp, cfg->norm_topk};
+  OBS_LAUNCH(ctx, "decode_fused", decode_fused_kernel<<<NWG, 256, 0, ctx->stream>>>(a));
+  return OBS_OK;
+}
+
+int fused_decode_status(obs_ctx* ctx) {
+  if (!ctx->fused_ws) return OBS_OK;
+  OBS_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+  uint32_t err = 0;
+  OBS_HIP_TRY(ctx, hipMemcpy(&err, static_cast<unsigned char*>(ctx->fused_ws) + WS_ERR, 4, hipMemcpyDeviceToHost));
+  if (err) {
+    OBS_HIP_TRY(ctx, hipMemset(ctx->fused_ws, 0, WS_BYTES));
+    OBS_HIP_TRY(ctx, hipDeviceSynchronize());
+    return set_error(ctx, OBS_E_HIP,
+                     "fused decode: a cross-workgroup wait timed out (were all CUs available?); "
+                     "outputs since then are invalid; workspace reset");
+  }
+  return OBS_OK;
+}
+
+}  // namespace obs

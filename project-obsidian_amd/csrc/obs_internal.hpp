@@ -31,9 +31,12 @@ struct obs_ctx {
   hipStream_t stream = nullptr;  // own_stream or a caller stream
   hipEvent_t ev_start = nullptr, ev_stop = nullptr;
   std::string err;
-  // decode workspace (logits, ids, weights, h, sync counters), grown on demand
+  // decode workspace (logits, ids, weights, h), grown on demand
   void* decode_ws = nullptr;
   size_t decode_ws_bytes = 0;
+  // fused decode workspace (epoch-tagged exchange slots + counters), zeroed once
+  void* fused_ws = nullptr;
+  int decode_path = 0;  // OBS_DECODE_AUTO / _MULTI / _FUSED
   // in-stream kernel timing
   bool prof_on = false;
   std::vector<obs_prof_pair> prof_pairs;
@@ -80,6 +83,14 @@ inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_
 
 // Workspace for decode: returns device pointer of at least `bytes`.
 int ensure_decode_ws(obs_ctx* ctx, size_t bytes, void** out);
+
+// Fused single-launch decode (obs_decode_fused.hip).
+bool fused_decode_supported(const obs_moe_config* cfg);
+size_t fused_decode_ws_bytes();
+int launch_fused_decode(obs_ctx* ctx, const obs_moe_config* cfg, const obs_moe_layer* L, const uint16_t* x,
+                        const uint16_t* residual, uint16_t* y, int32_t* ids_out, float* w_out);
+// Reads and clears the fused path's device error flag (synchronizes).
+int fused_decode_status(obs_ctx* ctx);
 
 }  // namespace obs
 
@@ -137,11 +148,153 @@ __device__ __forceinline__ float exp_det(float x) {
 // silu(g) * u with the deterministic exp (ops.metal:21 form).
 __device__ __forceinline__ float silu_mul(float g, float u) { return (g / (1.0f + exp_det(-g))) * u; }
 
-// Wave-wide xor butterfly sum (64 lanes); identical result on every lane.
-__device__ __forceinline__ float wave_sum_xor(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v = v + __shfl_xor(v, off, 64);
+// Sum over the 8 nibbles of `w` of q_j * x[j] (nibble j = (w >> 4j) & 15),
+// fp32 fma chain in nibble order. The nibbles are split into the bytes of two
+// words so each converts with one byte-to-float instruction.
+__device__ __forceinline__ float dot8_q4(uint32_t w, const float* x, float acc) {
+  const uint32_t lo = w & 0x0f0f0f0fu;         // nibbles 0,2,4,6 in bytes 0..3
+  const uint32_t hi = (w >> 4) & 0x0f0f0f0fu;  // nibbles 1,3,5,7
+  acc = __builtin_fmaf(static_cast<float>(lo & 0xffu), x[0], acc);
+  acc = __builtin_fmaf(static_cast<float>(hi & 0xffu), x[1], acc);
+  acc = __builtin_fmaf(static_cast<float>((lo >> 8) & 0xffu), x[2], acc);
+  acc = __builtin_fmaf(static_cast<float>((hi >> 8) & 0xffu), x[3], acc);
+  acc = __builtin_fmaf(static_cast<float>((lo >> 16) & 0xffu), x[4], acc);
+  acc = __builtin_fmaf(static_cast<float>((hi >> 16) & 0xffu), x[5], acc);
+  acc = __builtin_fmaf(static_cast<float>(lo >> 24), x[6], acc);
+  acc = __builtin_fmaf(static_cast<float>(hi >> 24), x[7], acc);
+  return acc;
+}
+
+// ---- DPP cross-lane primitives (gfx9 DPP controls) -------------------------
+constexpr int DPP_XOR1 = 0xB1;         // quad_perm [1,0,3,2]
+constexpr int DPP_XOR2 = 0x4E;         // quad_perm [2,3,0,1]
+constexpr int DPP_HALF_MIRROR = 0x141; // lane i <- lane 7-i within each 8-lane half row
+constexpr int DPP_MIRROR = 0x140;      // lane i <- lane 15-i within each 16-lane row
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+template <int CTRL>
+__device__ __forceinline__ int dpp_i32(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, true);
+}
+__device__ __forceinline__ float readlane_f32(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+// Xor-butterfly sum over 64 lanes with ascending offsets 1, 2, 4, 8, 16, 32;
+// the result is returned on every lane. Offsets 1 and 2 are quad
+// permutations; on quad-uniform (then half-row-uniform) data the half-row and
+// row mirrors pair exactly the lanes an xor by 4 (then 8) would; the last two
+// steps combine the four row sums as (r0 + r1) + (r2 + r3). fp32 addition is
+// commutative, so this is value-for-value the textbook butterfly.
+__device__ __forceinline__ float wave_sum_asc(float v) {
+  v = v + dpp_f32<DPP_XOR1>(v);
+  v = v + dpp_f32<DPP_XOR2>(v);
+  v = v + dpp_f32<DPP_HALF_MIRROR>(v);
+  v = v + dpp_f32<DPP_MIRROR>(v);
+  const float r0 = readlane_f32(v, 0), r1 = readlane_f32(v, 16);
+  const float r2 = readlane_f32(v, 32), r3 = readlane_f32(v, 48);
+  return (r0 + r1) + (r2 + r3);
+}
+
+// Sum over each aligned group of 8 lanes (xor offsets 1, 2, 4); uniform in the group.
+__device__ __forceinline__ float group8_sum(float v) {
+  v = v + dpp_f32<DPP_XOR1>(v);
+  v = v + dpp_f32<DPP_XOR2>(v);
+  v = v + dpp_f32<DPP_HALF_MIRROR>(v);
   return v;
+}
+
+__device__ __forceinline__ float wave_max_f32(float v) {
+  v = __builtin_fmaxf(v, dpp_f32<DPP_XOR1>(v));
+  v = __builtin_fmaxf(v, dpp_f32<DPP_XOR2>(v));
+  v = __builtin_fmaxf(v, dpp_f32<DPP_HALF_MIRROR>(v));
+  v = __builtin_fmaxf(v, dpp_f32<DPP_MIRROR>(v));
+  return __builtin_fmaxf(__builtin_fmaxf(readlane_f32(v, 0), readlane_f32(v, 16)),
+                         __builtin_fmaxf(readlane_f32(v, 32), readlane_f32(v, 48)));
+}
+
+__device__ __forceinline__ int wave_max_i32(int v) {
+  v = max(v, dpp_i32<DPP_XOR1>(v));
+  v = max(v, dpp_i32<DPP_XOR2>(v));
+  v = max(v, dpp_i32<DPP_HALF_MIRROR>(v));
+  v = max(v, dpp_i32<DPP_MIRROR>(v));
+  return max(max(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+             max(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+}
+
+// Softmax + top-k of one token on one wave (moe_routing_topk.metal:31-56).
+// lane l holds the logits of experts l, l+64, l+128, l+192 (absent ones are
+// ignored). m = max logit; e = exp_det(l - m); S = sum of e in the wave order
+// (lane-serial over its experts from 0, then wave_sum_asc); p = e / S; k rounds
+// select the largest p (lowest expert id on ties); wsum is the serial sum of
+// the selected p; weights are p / wsum when norm_topk and wsum > 0.
+// Lane kk < k receives slot kk (id -1, weight 0 if nothing is selectable).
+// Must be called with all 64 lanes active.
+__device__ __forceinline__ void route_wave(const float (&lg)[4], uint32_t n_exp, uint32_t k, int norm_topk,
+                                           uint32_t lane, int32_t* my_id, float* my_w) {
+  float m = -__builtin_huge_valf();
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    if (lane + 64u * j < n_exp) m = __builtin_fmaxf(m, lg[j]);
+  m = wave_max_f32(m);
+  float e[4];
+  float a = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    e[j] = 0.0f;
+    if (lane + 64u * j < n_exp) {
+      e[j] = exp_det(lg[j] - m);
+      a = a + e[j];
+    }
+  }
+  const float S = wave_sum_asc(a);
+  int key[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    if (lane + 64u * j < n_exp) {
+      const float p = e[j] / S;
+      key[j] = (p != p) ? -2 : __float_as_int(p);
+    } else {
+      key[j] = -1;
+    }
+  }
+  float wsum = 0.0f;
+  int32_t sel_id = -1;
+  float sel_p = 0.0f;
+  for (uint32_t kk = 0; kk < k; ++kk) {
+    const int lm = max(max(key[0], key[1]), max(key[2], key[3]));
+    const int bk = wave_max_i32(lm);
+    if (bk < 0) break;  // keys only decrease: no later slot is selectable either
+    uint32_t bidx;
+    const unsigned long long m0 = __ballot(key[0] == bk);
+    if (m0) {
+      bidx = static_cast<uint32_t>(__builtin_ctzll(m0));
+    } else {
+      const unsigned long long m1 = __ballot(key[1] == bk);
+      if (m1) {
+        bidx = 64u + static_cast<uint32_t>(__builtin_ctzll(m1));
+      } else {
+        const unsigned long long m2 = __ballot(key[2] == bk);
+        bidx = m2 ? 128u + static_cast<uint32_t>(__builtin_ctzll(m2))
+                  : 192u + static_cast<uint32_t>(__builtin_ctzll(__ballot(key[3] == bk)));
+      }
+    }
+    const float p = __int_as_float(bk);
+    if (lane == kk) { sel_id = static_cast<int32_t>(bidx); sel_p = p; }
+    wsum = wsum + p;
+    if ((bidx & 63u) == lane) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (static_cast<uint32_t>(j) == (bidx >> 6)) key[j] = -1;
+    }
+  }
+  float w = sel_p;
+  if (norm_topk && wsum > 0.0f && sel_id >= 0) w = sel_p / wsum;
+  *my_id = sel_id;
+  *my_w = sel_id >= 0 ? w : 0.0f;
 }
 
 }  // namespace obsd

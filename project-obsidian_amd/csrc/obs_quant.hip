@@ -79,7 +79,7 @@ __global__ void __launch_bounds__(256) q4_matvec_kernel(const uint32_t* __restri
       acc = __builtin_fmaf(__builtin_fmaf(q, sc, bi), xf, acc);
     }
   }
-  acc = wave_sum_xor(acc);
+  acc = wave_sum_asc(acc);
   if (lane == 0) {
     if (y_f32) y_f32[row] = acc;
     if (y_bf16) y_bf16[row] = f32_to_bf16(acc);

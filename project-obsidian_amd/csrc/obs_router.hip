@@ -69,96 +69,25 @@ __global__ void __launch_bounds__(256) q8_gate_logits_kernel(const uint32_t* __r
       acc = __builtin_fmaf(wv[c + 6], bf16lo(xv.w), acc);
       acc = __builtin_fmaf(wv[c + 7], bf16hi(xv.w), acc);
     }
-    acc = wave_sum_xor(acc);
+    acc = wave_sum_asc(acc);
     if (lane == 0) logits[static_cast<uint64_t>(t) * n_exp + e] = acc;
   }
 }
 
-__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    const unsigned long long o = __shfl_xor(v, off, 64);
-    v = o > v ? o : v;
-  }
-  return v;
-}
-
-__device__ __forceinline__ float wave_max_f32(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v = __builtin_fmaxf(v, __shfl_xor(v, off, 64));
-  return v;
-}
-
-// One wave per token; n_exp <= 256, k <= 64. Result written by lanes 0..k-1.
-__device__ __forceinline__ void route_one_wave(const float* __restrict__ lg, uint32_t n_exp, uint32_t k,
-                                               int norm_topk, uint32_t lane, int32_t* my_id, float* my_w) {
-  float l[4], e[4];
-  int key[4];
-  float m = -__builtin_huge_valf();
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const uint32_t i = lane + 64u * j;
-    l[j] = i < n_exp ? lg[i] : 0.0f;
-    if (i < n_exp) m = __builtin_fmaxf(m, l[j]);
-  }
-  m = wave_max_f32(m);
-  float a = 0.0f;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const uint32_t i = lane + 64u * j;
-    e[j] = 0.0f;
-    if (i < n_exp) {
-      e[j] = exp_det(l[j] - m);
-      a = a + e[j];
-    }
-  }
-  const float S = wave_sum_xor(a);
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const uint32_t i = lane + 64u * j;
-    if (i < n_exp) {
-      const float p = e[j] / S;
-      key[j] = (p != p) ? -2 : __float_as_int(p);
-    } else {
-      key[j] = -1;
-    }
-  }
-  float wsum = 0.0f;
-  int32_t sel_id = -1;
-  float sel_p = 0.0f;
-  for (uint32_t kk = 0; kk < k; ++kk) {
-    // lane-local best: first maximum over j (ids increase with j)
-    int bk = key[0];
-    uint32_t bi = lane;
-#pragma unroll
-    for (int j = 1; j < 4; ++j)
-      if (key[j] > bk) { bk = key[j]; bi = lane + 64u * j; }
-    const unsigned long long packed =
-        (static_cast<unsigned long long>(static_cast<uint32_t>(bk + 2)) << 32) | static_cast<uint32_t>(~bi);
-    const unsigned long long best = wave_max_u64(packed);
-    const int bkey = static_cast<int>(static_cast<uint32_t>(best >> 32)) - 2;
-    const uint32_t bidx = ~static_cast<uint32_t>(best & 0xffffffffull);
-    if (bkey < 0) continue;  // nothing selectable: slot keeps id -1, weight 0
-    const float p = __int_as_float(bkey);
-    if (lane == kk) { sel_id = static_cast<int32_t>(bidx); sel_p = p; }
-    wsum = wsum + p;
-    if ((bidx & 63u) == lane) key[bidx >> 6] = -1;
-  }
-  float wout = sel_p;
-  if (norm_topk && wsum > 0.0f && sel_id >= 0) wout = sel_p / wsum;
-  *my_id = sel_id;
-  *my_w = sel_id >= 0 ? wout : 0.0f;
-}
-
+// One wave per token (route_wave); n_exp <= 256, k <= 64.
 __global__ void __launch_bounds__(256) route_topk_kernel(const float* __restrict__ logits, int32_t* __restrict__ ids,
                                                          float* __restrict__ weights, uint32_t T, uint32_t n_exp,
                                                          uint32_t k, int norm_topk) {
   const uint32_t lane = threadIdx.x & 63;
   const uint32_t t = blockIdx.x * 4 + threadIdx.x / 64;
-  if (t >= T) return;
+  if (t >= T) return;  // wave-uniform: every lane of a wave shares t
+  const float* lg = logits + static_cast<uint64_t>(t) * n_exp;
+  float l[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) l[j] = (lane + 64u * j < n_exp) ? lg[lane + 64u * j] : 0.0f;
   int32_t id;
   float w;
-  route_one_wave(logits + static_cast<uint64_t>(t) * n_exp, n_exp, k, norm_topk, lane, &id, &w);
+  route_wave(l, n_exp, k, norm_topk, lane, &id, &w);
   if (lane < k) {
     ids[static_cast<uint64_t>(t) * k + lane] = id;
     weights[static_cast<uint64_t>(t) * k + lane] = w;

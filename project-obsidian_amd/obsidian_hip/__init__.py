@@ -33,6 +33,8 @@ OBS_E_HIP = -4
 OBS_E_NOMEM = -5
 OBS_E_UNSUPPORTED = -6
 
+OBS_DECODE_AUTO, OBS_DECODE_MULTI, OBS_DECODE_FUSED = 0, 1, 2
+
 _ERRNAMES = {
     OBS_E_INVALID: "OBS_E_INVALID",
     OBS_E_SHAPE: "OBS_E_SHAPE",
@@ -49,7 +51,8 @@ EXPORTS = (
     "obs_sync", "obs_timer_start", "obs_timer_stop", "obs_dequant", "obs_q4_matvec",
     "obs_q4_matmul", "obs_q8_gate_logits", "obs_route_topk", "obs_swiglu", "obs_scaled_add",
     "obs_moe_decode", "obs_moe_prefill_workspace", "obs_moe_prefill", "obs_capture_begin",
-    "obs_capture_end", "obs_graph_launch", "obs_graph_destroy", "obs_stream_hold", "obs_profile_enable",
+    "obs_capture_end", "obs_graph_launch", "obs_graph_destroy", "obs_set_decode_path",
+    "obs_device_status", "obs_stream_hold", "obs_profile_enable",
     "obs_profile_accumulate", "obs_profile_count", "obs_profile_stat", "obs_profile_clear",
 )
 
@@ -113,6 +116,8 @@ def lib() -> C.CDLL:
         "obs_capture_end": (i32, [vp, C.POINTER(vp)]),
         "obs_graph_launch": (i32, [vp, vp]),
         "obs_graph_destroy": (None, [vp]),
+        "obs_set_decode_path": (i32, [vp, C.c_int]),
+        "obs_device_status": (i32, [vp]),
         "obs_stream_hold": (i32, [vp, u32]),
         "obs_profile_enable": (i32, [vp, C.c_int]),
         "obs_profile_accumulate": (i32, [vp]),
@@ -225,6 +230,13 @@ class ObsidianExecutor:
 
     def set_stream(self, stream: Optional[int]) -> None:
         self._check(lib().obs_set_stream(self.ctx, stream))
+
+    def set_decode_path(self, path: int) -> None:
+        self._check(lib().obs_set_decode_path(self.ctx, int(path)))
+
+    def device_status(self) -> None:
+        """Raise if the fused decode path recorded a device-side failure."""
+        self._check(lib().obs_device_status(self.ctx))
 
     # -- graph capture / replay ------------------------------------------
     def capture_begin(self) -> None:

@@ -29,8 +29,16 @@ def _check_close(y_gpu_bits, y64):
     return rel
 
 
+@pytest.fixture(params=[oh.OBS_DECODE_FUSED, oh.OBS_DECODE_MULTI], ids=["fused", "multi"])
+def path(exe, request):
+    exe.set_decode_path(request.param)
+    yield request.param
+    exe.set_decode_path(oh.OBS_DECODE_AUTO)
+    exe.device_status()
+
+
 @pytest.mark.parametrize("seed", [0, 1, 2])
-def test_moe_decode_config2(exe, qwen_layer, seed):
+def test_moe_decode_config2(exe, qwen_layer, path, seed):
     t, layer, L = qwen_layer
     cfg = oh.MoeConfig(128, 8, 2048, 768, 64, True)
     rng = np.random.default_rng(1000 + seed)
@@ -40,6 +48,7 @@ def test_moe_decode_config2(exe, qwen_layer, seed):
     ids = exe.alloc(8, np.int32)
     w = exe.alloc(8, np.float32)
     exe.moe_decode(cfg, layer, dx, y, ids_out=ids, w_out=w)
+    exe.device_status()
     gi, gw = ids.download(), w.download()
     _, ri, rw = O.router(L, x, 8, True)
     assert np.array_equal(gi, ri[0])
@@ -49,7 +58,65 @@ def test_moe_decode_config2(exe, qwen_layer, seed):
     print(f"seed {seed}: ids {list(gi)} rel err {rel:.2e}")
 
 
-def test_moe_decode_residual_and_one_hot(exe, qwen_layer):
+def test_moe_decode_fused_matches_multi_and_repeats(exe, qwen_layer):
+    """Many back-to-back fused launches (device-side epoch advances every
+    launch) agree with the 4-launch path to bf16 rounding."""
+    t, layer, L = qwen_layer
+    cfg = oh.MoeConfig(128, 8, 2048, 768, 64, True)
+    rng = np.random.default_rng(1050)
+    xs = [synth.bf16_normal(rng, 2048) for _ in range(12)]
+    dxs = [exe.upload(x) for x in xs]
+    outs = {}
+    for p in (oh.OBS_DECODE_FUSED, oh.OBS_DECODE_MULTI):
+        exe.set_decode_path(p)
+        ys = [exe.alloc(2048, np.uint16) for _ in xs]
+        idb = [exe.alloc(8, np.int32) for _ in xs]
+        for dx, y, i in zip(dxs, ys, idb):
+            exe.moe_decode(cfg, layer, dx, y, ids_out=i)
+        exe.device_status()
+        outs[p] = ([synth.bf16_bits_to_f32(y.download()) for y in ys], [i.download() for i in idb])
+    exe.set_decode_path(oh.OBS_DECODE_AUTO)
+    for n in range(len(xs)):
+        assert np.array_equal(outs[1][1][n], outs[2][1][n])
+        a, b = outs[1][0][n].astype(np.float64), outs[2][0][n].astype(np.float64)
+        assert np.linalg.norm(a - b) / np.linalg.norm(b) < 4e-3
+
+
+def test_moe_decode_fused_graph_replay(exe, qwen_layer):
+    """Captured once, replayed many times with new inputs written in between:
+    every replay must see its own epoch and produce the right layer output."""
+    t, layer, L = qwen_layer
+    cfg = oh.MoeConfig(128, 8, 2048, 768, 64, True)
+    exe.set_decode_path(oh.OBS_DECODE_FUSED)
+    rng = np.random.default_rng(1060)
+    dx = exe.alloc(2048, np.uint16)
+    y = exe.alloc(2048, np.uint16)
+    ids = exe.alloc(8, np.int32)
+    w = exe.alloc(8, np.float32)
+    dx.upload(synth.bf16_normal(rng, 2048))
+    exe.moe_decode(cfg, layer, dx, y, ids_out=ids, w_out=w)  # workspace exists before capture
+    exe.sync()
+    exe.capture_begin()
+    exe.moe_decode(cfg, layer, dx, y, ids_out=ids, w_out=w)
+    g = exe.capture_end()
+    try:
+        for rep in range(6):
+            x = synth.bf16_normal(rng, 2048)
+            dx.upload(x)
+            for _ in range(rep % 3 + 1):
+                exe.graph_launch(g)
+            exe.device_status()
+            gi, gw = ids.download(), w.download()
+            _, ri, rw = O.router(L, x, 8, True)
+            assert np.array_equal(gi, ri[0])
+            y64, _, _ = O.moe_decode(L, x, 8, True, ids=gi[None], w=gw[None])
+            _check_close(y.download(), y64[0])
+    finally:
+        exe.graph_destroy(g)
+        exe.set_decode_path(oh.OBS_DECODE_AUTO)
+
+
+def test_moe_decode_residual_and_one_hot(exe, qwen_layer, path):
     t, layer, L = qwen_layer
     cfg = oh.MoeConfig(128, 8, 2048, 768, 64, True)
     rng = np.random.default_rng(1100)
@@ -110,3 +177,11 @@ def test_moe_decode_rejects_bad_config(exe, qwen_layer):
         with pytest.raises(oh.ObsError) as ei:
             exe.moe_decode(cfg, layer, x, y)
         assert ei.value.code == oh.OBS_E_SHAPE
+    # the fused path refuses shapes it is not built for
+    exe.set_decode_path(oh.OBS_DECODE_FUSED)
+    try:
+        with pytest.raises(oh.ObsError) as ei:
+            exe.moe_decode(oh.MoeConfig(128, 4, 2048, 768, 64), layer, x, y)
+        assert ei.value.code == oh.OBS_E_SHAPE
+    finally:
+        exe.set_decode_path(oh.OBS_DECODE_AUTO)
