@@ -34,6 +34,11 @@
 // reports it and resets the workspace.
 #include "obs_internal.hpp"
 
+// Phase markers for timing harnesses; no code is generated unless one defines it.
+#ifndef OBS_FUSED_MARK
+#define OBS_FUSED_MARK(phase)
+#endif
+
 namespace {
 
 using namespace obsd;
@@ -63,9 +68,12 @@ struct FusedArgs {
   int norm_topk;
 };
 
+// Slot stores are system-scope (written through to memory): measured on MI355X,
+// an agent-scope store polled by an agent-scope load from a CU of the SAME XCD
+// takes ~2.7 us to become visible, a write-through store ~0.55 us.
 __device__ __forceinline__ void slot_store(uint64_t* p, uint32_t epoch, float v) {
   __hip_atomic_store(p, (static_cast<uint64_t>(epoch) << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
-                     __HIP_MEMORY_SCOPE_AGENT);
+                     __HIP_MEMORY_SCOPE_SYSTEM);
 }
 __device__ __forceinline__ uint64_t slot_load(const uint64_t* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -76,7 +84,7 @@ __device__ __forceinline__ bool slot_ready(uint64_t v, uint32_t epoch) {
 __device__ __forceinline__ float slot_val(uint64_t v) { return __uint_as_float(static_cast<uint32_t>(v)); }
 
 __device__ __forceinline__ void raise_error(unsigned char* ws) {
-  __hip_atomic_store(reinterpret_cast<uint32_t*>(ws + WS_ERR), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(reinterpret_cast<uint32_t*>(ws + WS_ERR), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
 __device__ __forceinline__ void unpack_bf16x8(const uint4& v, float* f) {
@@ -84,9 +92,15 @@ __device__ __forceinline__ void unpack_bf16x8(const uint4& v, float* f) {
   f[4] = bf16lo(v.z); f[5] = bf16hi(v.z); f[6] = bf16lo(v.w); f[7] = bf16hi(v.w);
 }
 
+// NQ = router logit slots per lane: 2 for up to 128 experts, 4 for up to 256.
+template <int NQ>
 __global__ void __launch_bounds__(256, 1) decode_fused_kernel(FusedArgs a) {
+  constexpr int RT = NQ / 2;  // router rows per wave
   __shared__ uint32_t s_epoch;
   __shared__ int s_abort;
+  __shared__ int32_t s_ids[FK];
+  __shared__ float s_w[FK];
+  __shared__ bool s_ok;
   __shared__ float s_h[FI];
   __shared__ float s_y[FK][64];
 
@@ -100,6 +114,7 @@ __global__ void __launch_bounds__(256, 1) decode_fused_kernel(FusedArgs a) {
   uint64_t* y_slots = reinterpret_cast<uint64_t*>(a.ws + WS_Y);
   const uint32_t n_exp = a.n_exp;
 
+  OBS_FUSED_MARK(0);
   if (tid == 0) {
     s_epoch = __hip_atomic_load(ctl_launch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
     s_abort = __hip_atomic_load(ctl_err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u;
@@ -113,10 +128,10 @@ __global__ void __launch_bounds__(256, 1) decode_fused_kernel(FusedArgs a) {
   }
   // router rows of this wave: e = 4j + wave (+128)
   const uint32_t e0 = 4u * j + wave;
-  uint4 rq[2][2];
-  uint16_t rs[2], rb[2];
+  uint4 rq[RT][2];
+  uint16_t rs[RT], rb[RT];
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
+  for (int t = 0; t < RT; ++t) {
     const uint32_t e = e0 + 128u * t;
     if (e < n_exp) {
       const uint4* rp = reinterpret_cast<const uint4*>(a.router_w + size_t(e) * (FH / 4) + 8u * lane);
@@ -129,6 +144,7 @@ __global__ void __launch_bounds__(256, 1) decode_fused_kernel(FusedArgs a) {
   __syncthreads();
   const uint32_t epoch = s_epoch;
   if (s_abort) return;  // a previous launch failed: the host must reset first
+  OBS_FUSED_MARK(1);
 
   float xf[32];
 #pragma unroll
@@ -139,7 +155,7 @@ __global__ void __launch_bounds__(256, 1) decode_fused_kernel(FusedArgs a) {
 
   // ---- 1. router logits (order of obs_q8_gate_logits: serial fma, then wave_sum_asc)
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
+  for (int t = 0; t < RT; ++t) {
     const uint32_t e = e0 + 128u * t;
     if (e < n_exp) {  // wave-uniform
       const float sc = bf16_to_f32(rs[t]), bi = bf16_to_f32(rb[t]);
@@ -156,37 +172,51 @@ __global__ void __launch_bounds__(256, 1) decode_fused_kernel(FusedArgs a) {
     }
   }
 
+  OBS_FUSED_MARK(2);
   // ---- 2. every wave polls its group's logits and routes the token
   bool ok = true;
-  float lg[4];
-  {
+  float lg[NQ];
+  if (wave == 0) {
     const uint64_t t0 = wall_clock64();
     while (true) {
+      // all slot loads in flight together (clamped index, no per-load branch)
+      uint64_t v[NQ];
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) v[q] = slot_load(logit_slots + min(lane + 64u * q, n_exp - 1u));
       bool ready = true;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const uint32_t idx = lane + 64u * q;
-        lg[q] = 0.0f;
-        if (idx < n_exp) {
-          const uint64_t v = slot_load(logit_slots + idx);
-          lg[q] = slot_val(v);
-          ready = ready && slot_ready(v, epoch);
-        }
+      for (int q = 0; q < NQ; ++q) {
+        lg[q] = slot_val(v[q]);
+        ready = ready && slot_ready(v[q], epoch);
       }
       if (__all(ready)) break;
       if (wall_clock64() - t0 > WAIT_TICKS) { ok = false; break; }
     }
   }
+  OBS_FUSED_MARK(9);
   if (!ok && lane == 0) raise_error(a.ws);
-  int32_t sel_id;
-  float sel_w;
-  route_wave(lg, n_exp, FK, a.norm_topk, lane, &sel_id, &sel_w);
-  if (blockIdx.x == 0 && wave == 0 && lane < FK) {
-    if (a.ids_out) a.ids_out[lane] = sel_id;
-    if (a.w_out) a.w_out[lane] = sel_w;
+  // one wave per workgroup routes (the CU has one scalar unit; four identical
+  // routings would contend for it), then broadcasts through LDS
+  if (wave == 0) {
+    int32_t id;
+    float w;
+    route_wave<NQ>(lg, n_exp, FK, a.norm_topk, lane, &id, &w);
+    if (lane < FK) {
+      s_ids[lane] = id;
+      s_w[lane] = w;
+      s_ok = ok;
+      if (blockIdx.x == 0) {
+        if (a.ids_out) a.ids_out[lane] = id;
+        if (a.w_out) a.w_out[lane] = w;
+      }
+    }
   }
-  const int32_t eg = __builtin_amdgcn_readlane(sel_id, static_cast<int>(g));
+  __syncthreads();
+  ok = ok && s_ok;
+  const float sel_w = lane < FK ? s_w[lane] : 0.0f;  // rank weights in lanes 0..7 (combine)
+  const int32_t eg = s_ids[g];
   const bool have = ok && eg >= 0 && static_cast<uint32_t>(eg) < n_exp;
+  OBS_FUSED_MARK(3);
 
   // ---- 3. issue every weight load this wave needs: 6 gate + 6 up rows, 2x3 down blocks
   uint4 gq[GU_ROWS], uq[GU_ROWS];
@@ -221,6 +251,7 @@ __global__ void __launch_bounds__(256, 1) decode_fused_kernel(FusedArgs a) {
     }
   }
 
+  OBS_FUSED_MARK(4);
   // ---- 4. gate/up rows -> h slots (factored per group: s*sum(q x) + b*sum(x))
 #pragma unroll
   for (uint32_t t = 0; t < GU_ROWS; ++t) {
@@ -244,6 +275,7 @@ __global__ void __launch_bounds__(256, 1) decode_fused_kernel(FusedArgs a) {
     if (lane == 0) slot_store(h_slots + e0 + 128u * t, epoch, hv);
   }
 
+  OBS_FUSED_MARK(5);
   // ---- 5. poll the group's 768 h values into LDS
   {
     bool wave_ok = ok;
@@ -267,6 +299,7 @@ __global__ void __launch_bounds__(256, 1) decode_fused_kernel(FusedArgs a) {
   }
   __syncthreads();
 
+  OBS_FUSED_MARK(6);
   // ---- 6. this workgroup's 64 down rows of expert e_g (unscaled by w_g)
   {
     float hsum[3];
@@ -303,6 +336,7 @@ __global__ void __launch_bounds__(256, 1) decode_fused_kernel(FusedArgs a) {
     }
   }
 
+  OBS_FUSED_MARK(7);
   // ---- 7. group 0: combine the 8 ranks for rows [64j, 64j + 64) in rank order
   if (g == 0) {
     bool wave_ok = ok;
@@ -332,6 +366,7 @@ __global__ void __launch_bounds__(256, 1) decode_fused_kernel(FusedArgs a) {
     }
   }
 
+  OBS_FUSED_MARK(8);
   // ---- 8. exit: the last workgroup advances the launch counter (next epoch)
   __syncthreads();
   if (tid == 0) {
@@ -364,7 +399,10 @@ int launch_fused_decode(obs_ctx* ctx, const obs_moe_config* cfg, const obs_moe_l
   FusedArgs a{L->gate_w, L->gate_s, L->gate_b, L->up_w, L->up_s, L->up_b, L->down_w, L->down_s, L->down_b,
               L->router_w, L->router_s, L->router_b, x, residual, y, ids_out, w_out,
               static_cast<unsigned char*>(ctx->fused_ws), cfg->n_exp, cfg->norm_topk};
-  OBS_LAUNCH(ctx, "decode_fused", decode_fused_kernel<<<NWG, 256, 0, ctx->stream>>>(a));
+  if (cfg->n_exp <= 128)
+    OBS_LAUNCH(ctx, "decode_fused", decode_fused_kernel<2><<<NWG, 256, 0, ctx->stream>>>(a));
+  else
+    OBS_LAUNCH(ctx, "decode_fused", decode_fused_kernel<4><<<NWG, 256, 0, ctx->stream>>>(a));
   return OBS_OK;
 }
 

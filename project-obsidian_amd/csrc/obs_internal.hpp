@@ -232,64 +232,166 @@ __device__ __forceinline__ int wave_max_i32(int v) {
 // select the largest p (lowest expert id on ties); wsum is the serial sum of
 // the selected p; weights are p / wsum when norm_topk and wsum > 0.
 // Lane kk < k receives slot kk (id -1, weight 0 if nothing is selectable).
-// Must be called with all 64 lanes active.
-__device__ __forceinline__ void route_wave(const float (&lg)[4], uint32_t n_exp, uint32_t k, int norm_topk,
+// Must be called with all 64 lanes active. NQ = logit slots per lane
+// (ceil(n_exp / 64), at most 4); selection is branch-free per round.
+template <int NQ>
+__device__ __forceinline__ void route_wave(const float (&lg)[NQ], uint32_t n_exp, uint32_t k, int norm_topk,
                                            uint32_t lane, int32_t* my_id, float* my_w) {
+  bool present[NQ];
   float m = -__builtin_huge_valf();
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
-    if (lane + 64u * j < n_exp) m = __builtin_fmaxf(m, lg[j]);
+  for (int j = 0; j < NQ; ++j) {
+    present[j] = lane + 64u * j < n_exp;
+    m = present[j] ? __builtin_fmaxf(m, lg[j]) : m;
+  }
   m = wave_max_f32(m);
-  float e[4];
+  float e[NQ];
   float a = 0.0f;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    e[j] = 0.0f;
-    if (lane + 64u * j < n_exp) {
-      e[j] = exp_det(lg[j] - m);
-      a = a + e[j];
-    }
+  for (int j = 0; j < NQ; ++j) {
+    e[j] = exp_det(present[j] ? lg[j] - m : -100.0f);  // absent -> 0, not added below
+    a = present[j] ? a + e[j] : a;
   }
   const float S = wave_sum_asc(a);
-  int key[4];
+  int key[NQ];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    if (lane + 64u * j < n_exp) {
-      const float p = e[j] / S;
-      key[j] = (p != p) ? -2 : __float_as_int(p);
-    } else {
-      key[j] = -1;
-    }
+  for (int j = 0; j < NQ; ++j) {
+    const float p = e[j] / S;
+    key[j] = present[j] ? ((p != p) ? -2 : __float_as_int(p)) : -1;
   }
   float wsum = 0.0f;
   int32_t sel_id = -1;
   float sel_p = 0.0f;
   for (uint32_t kk = 0; kk < k; ++kk) {
-    const int lm = max(max(key[0], key[1]), max(key[2], key[3]));
+    int lm = key[0];
+#pragma unroll
+    for (int j = 1; j < NQ; ++j) lm = max(lm, key[j]);
     const int bk = wave_max_i32(lm);
     if (bk < 0) break;  // keys only decrease: no later slot is selectable either
-    uint32_t bidx;
-    const unsigned long long m0 = __ballot(key[0] == bk);
-    if (m0) {
-      bidx = static_cast<uint32_t>(__builtin_ctzll(m0));
-    } else {
-      const unsigned long long m1 = __ballot(key[1] == bk);
-      if (m1) {
-        bidx = 64u + static_cast<uint32_t>(__builtin_ctzll(m1));
-      } else {
-        const unsigned long long m2 = __ballot(key[2] == bk);
-        bidx = m2 ? 128u + static_cast<uint32_t>(__builtin_ctzll(m2))
-                  : 192u + static_cast<uint32_t>(__builtin_ctzll(__ballot(key[3] == bk)));
-      }
+    // lowest expert id holding bk: slot-major (ids 64j + lane), lowest lane first
+    uint32_t bidx = 0xffffffffu;
+#pragma unroll
+    for (int j = NQ - 1; j >= 0; --j) {
+      const unsigned long long mj = __ballot(key[j] == bk);
+      bidx = mj ? 64u * j + static_cast<uint32_t>(__builtin_ctzll(mj)) : bidx;
     }
     const float p = __int_as_float(bk);
-    if (lane == kk) { sel_id = static_cast<int32_t>(bidx); sel_p = p; }
+    sel_id = (lane == kk) ? static_cast<int32_t>(bidx) : sel_id;
+    sel_p = (lane == kk) ? p : sel_p;
     wsum = wsum + p;
-    if ((bidx & 63u) == lane) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        if (static_cast<uint32_t>(j) == (bidx >> 6)) key[j] = -1;
+    for (int j = 0; j < NQ; ++j) key[j] = (64u * j + lane == bidx) ? -1 : key[j];
+  }
+  float w = sel_p;
+  if (norm_topk && wsum > 0.0f && sel_id >= 0) w = sel_p / wsum;
+  *my_id = sel_id;
+  *my_w = sel_id >= 0 ? w : 0.0f;
+}
+
+// Same contract and bit-identical result as route_wave for k = 8, without
+// eight dependent argmax rounds: (1) a binary search over the 31-bit keys
+// (ballot population counts) finds T, the 8th largest key; (2) the selected set
+// is every key > T plus the lowest-id keys == T up to 8; (3) the (key, id)
+// pairs are gathered into scalar registers in id order and sorted by
+// (key desc, id asc) with a 19-comparator network; lane s takes slot s.
+// Because (key desc, id asc) is a strict total order, this equals k rounds of
+// "largest p, lowest id on ties".
+template <int NQ>
+__device__ __forceinline__ void route_wave_top8(const float (&lg)[NQ], uint32_t n_exp, int norm_topk,
+                                                uint32_t lane, int32_t* my_id, float* my_w) {
+  constexpr int K = 8;
+  bool present[NQ];
+  float m = -__builtin_huge_valf();
+#pragma unroll
+  for (int j = 0; j < NQ; ++j) {
+    present[j] = lane + 64u * j < n_exp;
+    m = present[j] ? __builtin_fmaxf(m, lg[j]) : m;
+  }
+  m = wave_max_f32(m);
+  float e[NQ];
+  float a = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NQ; ++j) {
+    e[j] = exp_det(present[j] ? lg[j] - m : -100.0f);
+    a = present[j] ? a + e[j] : a;
+  }
+  const float S = wave_sum_asc(a);
+  int key[NQ];
+#pragma unroll
+  for (int j = 0; j < NQ; ++j) {
+    const float p = e[j] / S;
+    key[j] = present[j] ? ((p != p) ? -2 : __float_as_int(p)) : -1;
+  }
+  // (1) T = largest value with count(key >= T) >= K (0 if fewer than K selectable)
+  int T = 0;
+#pragma unroll
+  for (int bit = 30; bit >= 0; --bit) {
+    const int cand = T | (1 << bit);
+    uint32_t c = 0;
+#pragma unroll
+    for (int j = 0; j < NQ; ++j) c += static_cast<uint32_t>(__popcll(__ballot(key[j] >= cand)));
+    T = (c >= static_cast<uint32_t>(K)) ? cand : T;
+  }
+  // (2) membership
+  uint32_t n_gt = 0;
+#pragma unroll
+  for (int j = 0; j < NQ; ++j) n_gt += static_cast<uint32_t>(__popcll(__ballot(key[j] > T)));
+  const unsigned long long lt_mask = (1ull << lane) - 1ull;
+  uint32_t eq_before = 0;
+  unsigned long long msel[NQ];
+#pragma unroll
+  for (int j = 0; j < NQ; ++j) {
+    const unsigned long long meq = __ballot(key[j] == T);
+    const uint32_t r = eq_before + static_cast<uint32_t>(__popcll(meq & lt_mask));
+    msel[j] = __ballot(key[j] > T || (key[j] == T && n_gt + r < static_cast<uint32_t>(K)));
+    eq_before += static_cast<uint32_t>(__popcll(meq));
+  }
+  // (3) gather in ascending id order (uniform values)
+  int sk[K], si[K];
+#pragma unroll
+  for (int s = 0; s < K; ++s) {
+    sk[s] = -1;
+    si[s] = -1;
+    bool found = false;
+#pragma unroll
+    for (int j = 0; j < NQ; ++j) {
+      if (!found && msel[j] != 0ull) {
+        const int l = __builtin_ctzll(msel[j]);
+        msel[j] &= msel[j] - 1ull;
+        sk[s] = __builtin_amdgcn_readlane(key[j], l);
+        si[s] = 64 * j + l;
+        found = true;
+      }
     }
+  }
+  // (4) sort: element a precedes b iff key_a > key_b or (key_a == key_b and id_a < id_b);
+  // empty entries (key -1) sort last
+#define OBS_CSWAP(A, B)                                                                  \
+  do {                                                                                   \
+    const bool sw = (sk[B] > sk[A]) || (sk[B] == sk[A] && si[B] < si[A]);                \
+    const int tk = sw ? sk[B] : sk[A], ti = sw ? si[B] : si[A];                          \
+    sk[B] = sw ? sk[A] : sk[B];                                                          \
+    si[B] = sw ? si[A] : si[B];                                                          \
+    sk[A] = tk;                                                                          \
+    si[A] = ti;                                                                          \
+  } while (0)
+  OBS_CSWAP(0, 2); OBS_CSWAP(1, 3); OBS_CSWAP(4, 6); OBS_CSWAP(5, 7);
+  OBS_CSWAP(0, 4); OBS_CSWAP(1, 5); OBS_CSWAP(2, 6); OBS_CSWAP(3, 7);
+  OBS_CSWAP(0, 1); OBS_CSWAP(2, 3); OBS_CSWAP(4, 5); OBS_CSWAP(6, 7);
+  OBS_CSWAP(2, 4); OBS_CSWAP(3, 5);
+  OBS_CSWAP(1, 4); OBS_CSWAP(3, 6);
+  OBS_CSWAP(1, 2); OBS_CSWAP(3, 4); OBS_CSWAP(5, 6);
+#undef OBS_CSWAP
+  // (5) weights: wsum is the serial sum of the selected p in rank order
+  float wsum = 0.0f;
+  int32_t sel_id = -1;
+  float sel_p = 0.0f;
+#pragma unroll
+  for (int s = 0; s < K; ++s) {
+    const float ps = __int_as_float(sk[s]);
+    wsum = si[s] >= 0 ? wsum + ps : wsum;
+    sel_id = (lane == static_cast<uint32_t>(s)) ? si[s] : sel_id;
+    sel_p = (lane == static_cast<uint32_t>(s)) ? ps : sel_p;
   }
   float w = sel_p;
   if (norm_topk && wsum > 0.0f && sel_id >= 0) w = sel_p / wsum;

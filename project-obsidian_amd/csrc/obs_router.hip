@@ -74,7 +74,8 @@ __global__ void __launch_bounds__(256) q8_gate_logits_kernel(const uint32_t* __r
   }
 }
 
-// One wave per token (route_wave); n_exp <= 256, k <= 64.
+// One wave per token (route_wave); n_exp <= 64 * NQ, k <= 64.
+template <int NQ>
 __global__ void __launch_bounds__(256) route_topk_kernel(const float* __restrict__ logits, int32_t* __restrict__ ids,
                                                          float* __restrict__ weights, uint32_t T, uint32_t n_exp,
                                                          uint32_t k, int norm_topk) {
@@ -82,12 +83,15 @@ __global__ void __launch_bounds__(256) route_topk_kernel(const float* __restrict
   const uint32_t t = blockIdx.x * 4 + threadIdx.x / 64;
   if (t >= T) return;  // wave-uniform: every lane of a wave shares t
   const float* lg = logits + static_cast<uint64_t>(t) * n_exp;
-  float l[4];
+  float l[NQ];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) l[j] = (lane + 64u * j < n_exp) ? lg[lane + 64u * j] : 0.0f;
+  for (int j = 0; j < NQ; ++j) l[j] = lg[min(lane + 64u * j, n_exp - 1u)];
   int32_t id;
   float w;
-  route_wave(l, n_exp, k, norm_topk, lane, &id, &w);
+  if (k == 8)
+    route_wave_top8<NQ>(l, n_exp, norm_topk, lane, &id, &w);
+  else
+    route_wave<NQ>(l, n_exp, k, norm_topk, lane, &id, &w);
   if (lane < k) {
     ids[static_cast<uint64_t>(t) * k + lane] = id;
     weights[static_cast<uint64_t>(t) * k + lane] = w;
@@ -125,7 +129,12 @@ int launch_gate_logits(obs_ctx* ctx, const uint32_t* w8, const uint16_t* s, cons
 
 int launch_route_topk(obs_ctx* ctx, const float* logits, int32_t* ids, float* w, uint32_t T,
                       uint32_t n_exp, uint32_t k, int norm_topk) {
-  OBS_LAUNCH(ctx, "route_topk", route_topk_kernel<<<(T + 3) / 4, 256, 0, ctx->stream>>>(logits, ids, w, T, n_exp, k, norm_topk));
+  if (n_exp <= 64)
+    OBS_LAUNCH(ctx, "route_topk", route_topk_kernel<1><<<(T + 3) / 4, 256, 0, ctx->stream>>>(logits, ids, w, T, n_exp, k, norm_topk));
+  else if (n_exp <= 128)
+    OBS_LAUNCH(ctx, "route_topk", route_topk_kernel<2><<<(T + 3) / 4, 256, 0, ctx->stream>>>(logits, ids, w, T, n_exp, k, norm_topk));
+  else
+    OBS_LAUNCH(ctx, "route_topk", route_topk_kernel<4><<<(T + 3) / 4, 256, 0, ctx->stream>>>(logits, ids, w, T, n_exp, k, norm_topk));
   return OBS_OK;
 }
 
