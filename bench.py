@@ -180,6 +180,9 @@ def bench_prefill(torch, oh, exe, args):
     exe.profile_clear()
     kernels = {n: {"avg_us": 1000.0 * tt / c, "launches": c} for n, (tt, c) in stats.items()}
     gemm_us = sum(v["avg_us"] for n, v in kernels.items() if n.startswith("grouped_gemm"))
+    ys = Y.float().cpu()
+    if not bool(torch.isfinite(ys).all()):
+        raise RuntimeError("prefill produced non-finite outputs")
     out = {"T": PREFILL_T, "ms": ms, "tflops": PREFILL_FLOP / (ms * 1e-3) / 1e12,
            "gemm_us": gemm_us, "gemm_tflops": PREFILL_FLOP / (gemm_us * 1e-6) / 1e12 if gemm_us else None,
            "kernels": kernels}

@@ -473,56 +473,53 @@ int orc_moe_prefill(const orc_layer* L, const uint16_t* x_bf16, int64_t T, int k
   /* per-row expert outputs [R, H] */
   double* Y = (double*)malloc(sizeof(double) * (size_t)R * H);
   const int bf = (mode == ORC_MODE_MFMA_BF16);
+  /* one expert at a time per thread: dequantize its three matrices once
+   * (bf16-rounded in MFMA mode), then run all of its rows */
 #pragma omp parallel
   {
+    float* Wg = (float*)malloc(sizeof(float) * (size_t)I * H);
+    float* Wu = (float*)malloc(sizeof(float) * (size_t)I * H);
+    float* Wd = (float*)malloc(sizeof(float) * (size_t)H * I);
     float* x = (float*)malloc(sizeof(float) * H);
-    double* g = (double*)malloc(sizeof(double) * I);
-    double* u = (double*)malloc(sizeof(double) * I);
     double* h = (double*)malloc(sizeof(double) * I);
-    float* wrow = (float*)malloc(sizeof(float) * (H > I ? H : I));
-#pragma omp for schedule(dynamic, 4)
-    for (int64_t row = 0; row < R; ++row) {
-      int e = 0;
-      while (offsets[e + 1] <= row) ++e;
-      const int64_t t = row_token[row];
-      orc_bf16_to_f32_n(x_bf16 + t * H, x, H);
-      for (int pj = 0; pj < 2; ++pj) {
-        const uint32_t* W = (pj ? L->up_w : L->gate_w) + e * gw;
-        const uint16_t* S = (pj ? L->up_s : L->gate_s) + e * gs;
-        const uint16_t* B = (pj ? L->up_b : L->gate_b) + e * gs;
-        double* dst = pj ? u : g;
-        for (int o = 0; o < I; ++o) {
-          orc_dequant(4, W + (size_t)o * (H / 8), S + (size_t)o * (H / G), B + (size_t)o * (H / G), ORC_SB_BF16, wrow, 1, H, G);
-          double acc = 0.0;
+#pragma omp for schedule(dynamic, 1)
+    for (int e = 0; e < E; ++e) {
+      if (counts[e] == 0) continue;
+      orc_dequant(4, L->gate_w + e * gw, L->gate_s + e * gs, L->gate_b + e * gs, ORC_SB_BF16, Wg, I, H, G);
+      orc_dequant(4, L->up_w + e * gw, L->up_s + e * gs, L->up_b + e * gs, ORC_SB_BF16, Wu, I, H, G);
+      orc_dequant(4, L->down_w + e * dw, L->down_s + e * ds, L->down_b + e * ds, ORC_SB_BF16, Wd, H, I, G);
+      if (bf) {
+        for (size_t i = 0; i < (size_t)I * H; ++i) {
+          Wg[i] = orc_bf16_to_f32(orc_f32_to_bf16(Wg[i]));
+          Wu[i] = orc_bf16_to_f32(orc_f32_to_bf16(Wu[i]));
+          Wd[i] = orc_bf16_to_f32(orc_f32_to_bf16(Wd[i]));
+        }
+      }
+      for (int64_t row = offsets[e]; row < offsets[e + 1]; ++row) {
+        const int64_t t = row_token[row];
+        orc_bf16_to_f32_n(x_bf16 + t * H, x, H);
+        for (int i = 0; i < I; ++i) {
+          double g = 0.0, u = 0.0;
+          const float* wg = Wg + (size_t)i * H;
+          const float* wu = Wu + (size_t)i * H;
           for (int c = 0; c < H; ++c) {
-            const float wv = bf ? orc_bf16_to_f32(orc_f32_to_bf16(wrow[c])) : wrow[c];
-            acc += (double)wv * (double)x[c];
+            g += (double)wg[c] * (double)x[c];
+            u += (double)wu[c] * (double)x[c];
           }
-          dst[o] = acc;
+          if (bf)
+            h[i] = (double)orc_bf16_to_f32(orc_f32_to_bf16(orc_silu_mul((float)g, (float)u)));
+          else
+            h[i] = silu_mul_d(g, u);
         }
-      }
-      for (int i = 0; i < I; ++i) {
-        if (bf) {
-          const float hv = orc_silu_mul((float)g[i], (float)u[i]);
-          h[i] = (double)orc_bf16_to_f32(orc_f32_to_bf16(hv));
-        } else {
-          h[i] = silu_mul_d(g[i], u[i]);
+        for (int o = 0; o < H; ++o) {
+          const float* wd = Wd + (size_t)o * I;
+          double acc = 0.0;
+          for (int c = 0; c < I; ++c) acc += (double)wd[c] * h[c];
+          Y[row * H + o] = bf ? (double)orc_bf16_to_f32(orc_f32_to_bf16((float)acc)) : acc;
         }
-      }
-      const uint32_t* W = L->down_w + e * dw;
-      const uint16_t* S = L->down_s + e * ds;
-      const uint16_t* B = L->down_b + e * ds;
-      for (int o = 0; o < H; ++o) {
-        orc_dequant(4, W + (size_t)o * (I / 8), S + (size_t)o * (I / G), B + (size_t)o * (I / G), ORC_SB_BF16, wrow, 1, I, G);
-        double acc = 0.0;
-        for (int c = 0; c < I; ++c) {
-          const float wv = bf ? orc_bf16_to_f32(orc_f32_to_bf16(wrow[c])) : wrow[c];
-          acc += (double)wv * h[c];
-        }
-        Y[row * H + o] = bf ? (double)orc_bf16_to_f32(orc_f32_to_bf16((float)acc)) : acc;
       }
     }
-    free(x); free(g); free(u); free(h); free(wrow);
+    free(Wg); free(Wu); free(Wd); free(x); free(h);
   }
   /* un-permute and combine in rank order (forward.rs:225-232) */
   for (int64_t t = 0; t < T; ++t) {

@@ -1,20 +1,483 @@
-// obs_prefill.hip — grouped prefill MoE (placeholder until the grouped GEMM lands).
+// obs_prefill.hip — grouped prefill MoE (src/forward.rs:164-247) and the
+// per-expert batched dequant matmul (Model::matmul_raw, forward.rs:313-321).
+//
+// Pipeline for T tokens (all on the GPU, no host round trip):
+//   1. routing: computed (gate logits + top-k kernels) or injected;
+//   2. grouping: rows of expert e are the tokens routed to e in ascending
+//      token order (forward.rs:203-204); one workgroup counts per 64-token
+//      chunk, scans, and ranks tokens inside a chunk with LDS lane bitmasks;
+//      it also emits the tile list (expert, first row, rows <= 128);
+//   3. gate/up grouped GEMM with a SwiGLU epilogue -> H [T*k, I] bf16;
+//   4. down grouped GEMM -> Yp, written at the token-major slot t*k + r;
+//   5. combine: y[t] = residual[t] + sum_r w[t,r] * Yp[t*k+r], fp32, rank order
+//      (forward.rs:225-232), rounded once to bf16.
+//
+// The GEMM. A workgroup (4 waves) owns a tile of up to 128 permuted rows x 128
+// output columns; wave w owns columns [32w, 32w+32) (and the same columns of
+// the up matrix for gate/up). Per 64-column quantization group:
+//   - A (activations, gathered by row through a_rows) is staged in LDS,
+//     double-buffered, row stride padded to 72 bf16;
+//   - B is read straight from HBM into registers: lane l takes 16 bytes
+//     (32 nibbles) of weight row n = n0 + 32w + l%32, columns
+//     [k0 + 32(l/32), +32), and dequantizes them to bf16 = RNE(q*s + b);
+//   - v_mfma_f32_32x32x16_bf16 accumulates in fp32. The MFMA's 16 k-slots of
+//     K-step s map to columns k0 + 32h + 8s + j (h = lane half, j = 0..7), for
+//     A and B alike, so each lane's 16-byte load feeds all four K-steps.
 #include "obs_internal.hpp"
+
+namespace obs {
+int check_moe_config(obs_ctx* ctx, const char* who, const obs_moe_config* cfg);
+int check_moe_layer(obs_ctx* ctx, const char* who, const obs_moe_layer* L);
+int launch_gate_logits(obs_ctx* ctx, const uint32_t* w8, const uint16_t* s, const uint16_t* b,
+                       const uint16_t* x, float* logits, uint32_t T, uint32_t in, uint32_t n_exp, uint32_t group);
+int launch_route_topk(obs_ctx* ctx, const float* logits, int32_t* ids, float* w, uint32_t T,
+                      uint32_t n_exp, uint32_t k, int norm_topk);
+}  // namespace obs
+
+namespace {
+
+using namespace obsd;
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16_t;
+
+constexpr uint32_t TM = 128;          // tile rows
+constexpr uint32_t TN = 128;          // tile output columns (4 waves x 32)
+constexpr uint32_t GK = 64;           // quantization group = K step of the main loop
+constexpr uint32_t LDS_STRIDE = 72;   // bf16 per staged A row (64 + 8 padding)
+constexpr uint32_t GROUP_TOKENS = 64; // tokens per grouping chunk (one wave)
+
+struct GemmArgs {
+  const uint16_t* A;        // bf16 [a_rows_total, K]
+  const int32_t* a_rows;    // permuted row -> A row (nullptr: identity)
+  uint32_t a_rows_total;    // bound for a_rows values
+  const uint32_t* w0; const uint16_t* s0; const uint16_t* b0;  // [E, N, K/8], [E, N, K/64]
+  const uint32_t* w1; const uint16_t* s1; const uint16_t* b1;  // up matrix (SwiGLU only)
+  uint16_t* out;            // bf16 rows of N
+  const int32_t* out_rows;  // permuted row -> output row (nullptr: identity)
+  const int4* tiles;        // {expert, row0, rows, 0}; nullptr: dense rows of expert 0
+  const int32_t* n_tiles;   // device tile count (grouped mode)
+  uint32_t dense_rows;      // row count in dense mode
+  uint32_t K, N;
+};
+
+// 16 bytes = 32 nibbles of one weight row -> 4 bf16x8 MFMA fragments (K-steps 0..3).
+__device__ __forceinline__ void dequant_frags(const uint4& q, float s, float b, bf16x8_t (&f)[4]) {
+  const uint32_t wd[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+  for (int st = 0; st < 4; ++st) {
+    const uint32_t w = wd[st];
+    const uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
+    float v[8];
+    v[0] = __builtin_fmaf(static_cast<float>(lo & 0xffu), s, b);
+    v[1] = __builtin_fmaf(static_cast<float>(hi & 0xffu), s, b);
+    v[2] = __builtin_fmaf(static_cast<float>((lo >> 8) & 0xffu), s, b);
+    v[3] = __builtin_fmaf(static_cast<float>((hi >> 8) & 0xffu), s, b);
+    v[4] = __builtin_fmaf(static_cast<float>((lo >> 16) & 0xffu), s, b);
+    v[5] = __builtin_fmaf(static_cast<float>((hi >> 16) & 0xffu), s, b);
+    v[6] = __builtin_fmaf(static_cast<float>(lo >> 24), s, b);
+    v[7] = __builtin_fmaf(static_cast<float>(hi >> 24), s, b);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) f[st][j] = static_cast<__bf16>(v[j]);  // RNE
+  }
+}
+
+template <bool SWIGLU>
+__global__ void __launch_bounds__(256, 1) grouped_gemm_kernel(GemmArgs a) {
+  __shared__ uint16_t sA[2][TM * LDS_STRIDE];
+  __shared__ int32_t s_arow[TM];
+  int4 tile;
+  if (a.tiles) {
+    if (blockIdx.x >= static_cast<uint32_t>(*a.n_tiles)) return;  // uniform per workgroup
+    tile = a.tiles[blockIdx.x];
+  } else {
+    const uint32_t r0 = blockIdx.x * TM;
+    tile = make_int4(0, static_cast<int32_t>(r0), static_cast<int32_t>(min(TM, a.dense_rows - r0)), 0);
+  }
+  const uint32_t e = static_cast<uint32_t>(tile.x), row0 = static_cast<uint32_t>(tile.y);
+  const uint32_t nrows = static_cast<uint32_t>(tile.z);
+  const uint32_t nblk = (nrows + 31u) / 32u;  // active 32-row blocks
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  const uint32_t n = blockIdx.y * TN + 32u * wave + (lane & 31u);  // this lane's weight row
+  const uint32_t h = lane >> 5;                                    // k half within a group
+  const uint32_t K = a.K, groups = K / GK;
+
+  if (tid < TM) {
+    int32_t r = -1;
+    if (tid < nrows) {
+      const uint32_t p = row0 + tid;
+      r = a.a_rows ? a.a_rows[p] : static_cast<int32_t>(p);
+      if (r < 0 || static_cast<uint32_t>(r) >= a.a_rows_total) r = -1;
+    }
+    s_arow[tid] = r;
+  }
+  __syncthreads();
+
+  // A staging: thread t -> tile row t/2, 32 bf16 at column 32*(t%2) of the group
+  const uint32_t ar = tid >> 1, ac = 32u * (tid & 1u);
+  const int32_t arow = s_arow[ar];
+  const uint16_t* aptr = arow >= 0 ? a.A + static_cast<size_t>(arow) * K + ac : nullptr;
+  auto load_a = [&](uint32_t g, uint4 (&r)[4]) {
+    if (aptr) {
+      const uint4* p = reinterpret_cast<const uint4*>(aptr + g * GK);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) r[i] = p[i];
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) r[i] = make_uint4(0u, 0u, 0u, 0u);
+    }
+  };
+  auto store_a = [&](uint32_t buf, const uint4 (&r)[4]) {
+    uint4* d = reinterpret_cast<uint4*>(&sA[buf][ar * LDS_STRIDE + ac]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) d[i] = r[i];
+  };
+
+  // B pointers of this lane's weight row(s)
+  const size_t wrow = static_cast<size_t>(e) * a.N + n;
+  const uint4* w0p = reinterpret_cast<const uint4*>(a.w0 + wrow * (K / 8)) + h;  // + 2*g per group
+  const uint16_t* s0p = a.s0 + wrow * groups;
+  const uint16_t* b0p = a.b0 + wrow * groups;
+  const uint4* w1p = SWIGLU ? reinterpret_cast<const uint4*>(a.w1 + wrow * (K / 8)) + h : nullptr;
+  const uint16_t* s1p = SWIGLU ? a.s1 + wrow * groups : nullptr;
+  const uint16_t* b1p = SWIGLU ? a.b1 + wrow * groups : nullptr;
+
+  f32x16_t acc0[4], acc1[4];
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) { acc0[mb][v] = 0.0f; acc1[mb][v] = 0.0f; }
+  }
+
+  uint4 ra[4];
+  load_a(0, ra);
+  uint4 q0 = w0p[0], q1 = SWIGLU ? w1p[0] : make_uint4(0u, 0u, 0u, 0u);
+  uint16_t sv0 = s0p[0], bv0 = b0p[0], sv1 = SWIGLU ? s1p[0] : 0, bv1 = SWIGLU ? b1p[0] : 0;
+  store_a(0, ra);
+
+  for (uint32_t g = 0; g < groups; ++g) {
+    const uint32_t buf = g & 1u;
+    // prefetch group g+1 (A into registers, B words and scales)
+    uint4 nq0 = q0, nq1 = q1;
+    uint16_t nsv0 = sv0, nbv0 = bv0, nsv1 = sv1, nbv1 = bv1;
+    const bool more = g + 1 < groups;
+    if (more) {
+      load_a(g + 1, ra);
+      nq0 = w0p[2u * (g + 1)];
+      nsv0 = s0p[g + 1];
+      nbv0 = b0p[g + 1];
+      if (SWIGLU) {
+        nq1 = w1p[2u * (g + 1)];
+        nsv1 = s1p[g + 1];
+        nbv1 = b1p[g + 1];
+      }
+    }
+    bf16x8_t f0[4], f1[4];
+    dequant_frags(q0, bf16_to_f32(sv0), bf16_to_f32(bv0), f0);
+    if (SWIGLU) dequant_frags(q1, bf16_to_f32(sv1), bf16_to_f32(bv1), f1);
+    __syncthreads();  // A tile of group g visible in sA[buf]
+#pragma unroll
+    for (uint32_t st = 0; st < 4; ++st) {
+#pragma unroll
+      for (uint32_t mb = 0; mb < 4; ++mb) {
+        if (mb < nblk) {
+          const bf16x8_t af = *reinterpret_cast<const bf16x8_t*>(
+              &sA[buf][(32u * mb + (lane & 31u)) * LDS_STRIDE + 32u * h + 8u * st]);
+          acc0[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, f0[st], acc0[mb], 0, 0, 0);
+          if (SWIGLU) acc1[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, f1[st], acc1[mb], 0, 0, 0);
+        }
+      }
+    }
+    if (more) store_a(buf ^ 1u, ra);  // the other buffer was last read in group g-1
+    q0 = nq0; q1 = nq1;
+    sv0 = nsv0; bv0 = nbv0; sv1 = nsv1; bv1 = nbv1;
+  }
+
+  // epilogue: lane holds C[i][n] for i = 32mb + 8(v/4) + 4h + v%4
+#pragma unroll
+  for (uint32_t mb = 0; mb < 4; ++mb) {
+    if (mb >= nblk) continue;
+#pragma unroll
+    for (uint32_t v = 0; v < 16; ++v) {
+      const uint32_t i = 32u * mb + 8u * (v / 4u) + 4u * h + (v % 4u);
+      if (i < nrows) {
+        const float val = SWIGLU ? silu_mul(acc0[mb][v], acc1[mb][v]) : acc0[mb][v];
+        const uint32_t p = row0 + i;
+        const size_t orow = a.out_rows ? static_cast<size_t>(a.out_rows[p]) : p;
+        a.out[orow * a.N + n] = f32_to_bf16(val);
+      }
+    }
+  }
+}
+
+// int32 slots before the 8-byte-aligned bitmask area of the grouping kernel's LDS
+__host__ __device__ constexpr size_t group_lds_ints(uint32_t nchunks, uint32_t E) {
+  return (static_cast<size_t>(nchunks) * E + 3u * E + 2u + 1u) & ~size_t(1);
+}
+
+// Grouping (one workgroup of 1024 threads). LDS: cnt[nchunks][E] ints, bits[16 waves][E] u64.
+__global__ void __launch_bounds__(1024) group_kernel(const int32_t* __restrict__ ids, uint32_t T, uint32_t k,
+                                                     uint32_t E, int32_t* counts, int32_t* offsets,
+                                                     int32_t* row_token, int32_t* row_slot, int4* tiles,
+                                                     int32_t* n_tiles) {
+  extern __shared__ int32_t sm[];
+  const uint32_t nchunks = (T + GROUP_TOKENS - 1) / GROUP_TOKENS;
+  int32_t* cnt = sm;                                        // [nchunks][E]
+  int32_t* tot = cnt + nchunks * E;                         // [E]
+  int32_t* off = tot + E;                                   // [E + 1]
+  int32_t* toff = off + E + 1;                              // [E + 1] tile offsets
+  unsigned long long* bits = reinterpret_cast<unsigned long long*>(sm + group_lds_ints(nchunks, E));  // [16][E]
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6, nwaves = blockDim.x / 64u;
+
+  for (uint32_t i = tid; i < nchunks * E; i += blockDim.x) cnt[i] = 0;
+  __syncthreads();
+  // a token's valid experts: in range and not repeated among its k ids
+  auto valid = [&](uint32_t t, uint32_t r, int32_t e) -> bool {
+    if (e < 0 || static_cast<uint32_t>(e) >= E) return false;
+    for (uint32_t q = 0; q < r; ++q)
+      if (ids[static_cast<size_t>(t) * k + q] == e) return false;
+    return true;
+  };
+  for (uint32_t c = wave; c < nchunks; c += nwaves) {
+    const uint32_t t = c * GROUP_TOKENS + lane;
+    if (t < T)
+      for (uint32_t r = 0; r < k; ++r) {
+        const int32_t e = ids[static_cast<size_t>(t) * k + r];
+        if (valid(t, r, e)) atomicAdd(&cnt[c * E + static_cast<uint32_t>(e)], 1);
+      }
+  }
+  __syncthreads();
+  for (uint32_t e = tid; e < E; e += blockDim.x) {
+    int32_t run = 0;
+    for (uint32_t c = 0; c < nchunks; ++c) {
+      const int32_t v = cnt[c * E + e];
+      cnt[c * E + e] = run;
+      run += v;
+    }
+    tot[e] = run;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int32_t o = 0, to = 0;
+    for (uint32_t e = 0; e < E; ++e) {
+      off[e] = o;
+      toff[e] = to;
+      o += tot[e];
+      to += (tot[e] + static_cast<int32_t>(TM) - 1) / static_cast<int32_t>(TM);
+    }
+    off[E] = o;
+    toff[E] = to;
+    *n_tiles = to;
+  }
+  __syncthreads();
+  for (uint32_t e = tid; e <= E; e += blockDim.x) {
+    offsets[e] = off[e];
+    if (e < E) counts[e] = tot[e];
+  }
+  for (uint32_t e = tid; e < E; e += blockDim.x) {
+    const int32_t nt = toff[e + 1] - toff[e];
+    for (int32_t q = 0; q < nt; ++q) {
+      const int32_t r0 = q * static_cast<int32_t>(TM);
+      tiles[toff[e] + q] = make_int4(static_cast<int32_t>(e), off[e] + r0, min(static_cast<int32_t>(TM), tot[e] - r0), 0);
+    }
+  }
+  // rank inside a chunk: lanes (tokens) below me routed to the same expert
+  unsigned long long* wb = bits + static_cast<size_t>(wave) * E;
+  const unsigned long long lt = (1ull << lane) - 1ull;
+  for (uint32_t c = wave; c < nchunks; c += nwaves) {
+    for (uint32_t e = lane; e < E; e += 64u) wb[e] = 0ull;
+    __builtin_amdgcn_wave_barrier();
+    const uint32_t t = c * GROUP_TOKENS + lane;
+    if (t < T)
+      for (uint32_t r = 0; r < k; ++r) {
+        const int32_t e = ids[static_cast<size_t>(t) * k + r];
+        if (valid(t, r, e)) atomicOr(&wb[e], 1ull << lane);
+      }
+    __builtin_amdgcn_wave_barrier();
+    if (t < T)
+      for (uint32_t r = 0; r < k; ++r) {
+        const int32_t e = ids[static_cast<size_t>(t) * k + r];
+        if (!valid(t, r, e)) continue;
+        const int32_t row = off[e] + cnt[c * E + static_cast<uint32_t>(e)] + __popcll(wb[e] & lt);
+        row_token[row] = static_cast<int32_t>(t);
+        row_slot[row] = static_cast<int32_t>(t * k + r);
+      }
+    __builtin_amdgcn_wave_barrier();
+  }
+}
+
+// y[t, :] = residual + sum_r w[t, r] * Yp[t*k + r, :] (fp32, rank order), 8 columns per thread.
+__global__ void __launch_bounds__(256) combine_kernel(const uint16_t* __restrict__ Yp, const int32_t* __restrict__ ids,
+                                                      const float* __restrict__ w, const uint16_t* __restrict__ residual,
+                                                      uint16_t* __restrict__ y, uint32_t T, uint32_t k, uint32_t H,
+                                                      uint32_t E) {
+  const uint32_t per_tok = H / 8u;
+  const uint64_t idx = static_cast<uint64_t>(blockIdx.x) * 256u + threadIdx.x;
+  if (idx >= static_cast<uint64_t>(T) * per_tok) return;
+  const uint32_t t = static_cast<uint32_t>(idx / per_tok), c = 8u * static_cast<uint32_t>(idx % per_tok);
+  float acc[8];
+  if (residual) {
+    const uint4 rv = *reinterpret_cast<const uint4*>(residual + static_cast<size_t>(t) * H + c);
+    acc[0] = bf16lo(rv.x); acc[1] = bf16hi(rv.x); acc[2] = bf16lo(rv.y); acc[3] = bf16hi(rv.y);
+    acc[4] = bf16lo(rv.z); acc[5] = bf16hi(rv.z); acc[6] = bf16lo(rv.w); acc[7] = bf16hi(rv.w);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
+  }
+  for (uint32_t r = 0; r < k; ++r) {
+    const int32_t e = ids[static_cast<size_t>(t) * k + r];
+    bool dup = false;
+    for (uint32_t q = 0; q < r; ++q) dup = dup || ids[static_cast<size_t>(t) * k + q] == e;
+    if (e < 0 || static_cast<uint32_t>(e) >= E || dup) continue;  // rows the grouping skipped
+    const float wr = w[static_cast<size_t>(t) * k + r];
+    const uint4 v = *reinterpret_cast<const uint4*>(Yp + (static_cast<size_t>(t) * k + r) * H + c);
+    acc[0] = __builtin_fmaf(wr, bf16lo(v.x), acc[0]); acc[1] = __builtin_fmaf(wr, bf16hi(v.x), acc[1]);
+    acc[2] = __builtin_fmaf(wr, bf16lo(v.y), acc[2]); acc[3] = __builtin_fmaf(wr, bf16hi(v.y), acc[3]);
+    acc[4] = __builtin_fmaf(wr, bf16lo(v.z), acc[4]); acc[5] = __builtin_fmaf(wr, bf16hi(v.z), acc[5]);
+    acc[6] = __builtin_fmaf(wr, bf16lo(v.w), acc[6]); acc[7] = __builtin_fmaf(wr, bf16hi(v.w), acc[7]);
+  }
+  *reinterpret_cast<uint4*>(y + static_cast<size_t>(t) * H + c) =
+      make_uint4(pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3]), pack_bf16x2(acc[4], acc[5]),
+                 pack_bf16x2(acc[6], acc[7]));
+}
+
+constexpr size_t al256(size_t v) { return (v + 255) & ~size_t(255); }
+
+struct PrefillWs {
+  size_t logits, ids, w, counts, offsets, ntiles, row_token, row_slot, tiles, H, Yp, total;
+  uint32_t max_tiles;
+};
+
+PrefillWs prefill_layout(const obs_moe_config* cfg, uint32_t T) {
+  PrefillWs L{};
+  const size_t R = static_cast<size_t>(T) * cfg->top_k;
+  L.max_tiles = static_cast<uint32_t>((R + TM - 1) / TM + cfg->n_exp);
+  size_t o = 0;
+  L.logits = o; o += al256(sizeof(float) * T * cfg->n_exp);
+  L.ids = o; o += al256(sizeof(int32_t) * R);
+  L.w = o; o += al256(sizeof(float) * R);
+  L.counts = o; o += al256(sizeof(int32_t) * cfg->n_exp);
+  L.offsets = o; o += al256(sizeof(int32_t) * (cfg->n_exp + 1));
+  L.ntiles = o; o += 256;
+  L.row_token = o; o += al256(sizeof(int32_t) * R);
+  L.row_slot = o; o += al256(sizeof(int32_t) * R);
+  L.tiles = o; o += al256(sizeof(int4) * L.max_tiles);
+  L.H = o; o += al256(sizeof(uint16_t) * R * cfg->inter);
+  L.Yp = o; o += al256(sizeof(uint16_t) * R * cfg->hidden);
+  L.total = o;
+  return L;
+}
+
+size_t group_lds_bytes(uint32_t T, uint32_t E) {
+  const uint32_t nchunks = (T + GROUP_TOKENS - 1) / GROUP_TOKENS;
+  return sizeof(int32_t) * group_lds_ints(nchunks, E) + sizeof(uint64_t) * 16 * E;
+}
+
+int launch_gemm(obs_ctx* ctx, bool swiglu, const GemmArgs& a, uint32_t grid_tiles) {
+  dim3 grid(grid_tiles, a.N / TN);
+  if (swiglu)
+    OBS_LAUNCH(ctx, "grouped_gemm_gateup", grouped_gemm_kernel<true><<<grid, 256, 0, ctx->stream>>>(a));
+  else
+    OBS_LAUNCH(ctx, "grouped_gemm_down", grouped_gemm_kernel<false><<<grid, 256, 0, ctx->stream>>>(a));
+  return OBS_OK;
+}
+
+}  // namespace
 
 extern "C" {
 
-size_t obs_moe_prefill_workspace(const obs_moe_config* cfg, uint32_t T) { (void)cfg; (void)T; return 0; }
-
-int obs_moe_prefill(obs_ctx* ctx, const obs_moe_config*, const obs_moe_layer*, const uint16_t*, const uint16_t*,
-                    uint16_t*, uint32_t, const int32_t*, const float*, void*, size_t) {
-  if (!ctx) return OBS_E_INVALID;
-  return obs::set_error(ctx, OBS_E_UNSUPPORTED, "obs_moe_prefill: not built yet");
+size_t obs_moe_prefill_workspace(const obs_moe_config* cfg, uint32_t T) {
+  if (!cfg || T == 0) return 0;
+  return prefill_layout(cfg, T).total;
 }
 
-int obs_q4_matmul(obs_ctx* ctx, const uint32_t*, const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*,
-                  uint32_t, uint32_t, uint32_t, uint32_t) {
+int obs_moe_prefill(obs_ctx* ctx, const obs_moe_config* cfg, const obs_moe_layer* layer, const uint16_t* X,
+                    const uint16_t* residual, uint16_t* Y, uint32_t T, const int32_t* ids, const float* weights,
+                    void* ws, size_t ws_bytes) {
   if (!ctx) return OBS_E_INVALID;
-  return obs::set_error(ctx, OBS_E_UNSUPPORTED, "obs_q4_matmul: not built yet");
+  int rc = obs::check_moe_config(ctx, "obs_moe_prefill", cfg);
+  if (rc) return rc;
+  rc = obs::check_moe_layer(ctx, "obs_moe_prefill", layer);
+  if (rc) return rc;
+  if (!X || !Y || !ws) return obs::set_error(ctx, OBS_E_INVALID, "obs_moe_prefill: null X, Y or workspace");
+  if ((ids == nullptr) != (weights == nullptr))
+    return obs::set_error(ctx, OBS_E_INVALID, "obs_moe_prefill: pass both ids and weights, or neither");
+  if (T == 0) return OBS_OK;
+  const uint32_t E = cfg->n_exp, k = cfg->top_k, H = cfg->hidden, I = cfg->inter;
+  if (H % TN != 0 || I % TN != 0)
+    return obs::set_error(ctx, OBS_E_SHAPE, "obs_moe_prefill: hidden and inter must be multiples of %u", TN);
+  const PrefillWs L = prefill_layout(cfg, T);
+  if (ws_bytes < L.total)
+    return obs::set_error(ctx, OBS_E_NOMEM, "obs_moe_prefill: workspace %zu bytes < %zu needed", ws_bytes, L.total);
+  const size_t lds = group_lds_bytes(T, E);
+  if (lds > 64 * 1024)
+    return obs::set_error(ctx, OBS_E_SHAPE, "obs_moe_prefill: T=%u with %u experts exceeds one grouping pass", T, E);
+  if (!obs::aligned(X, 16) || !obs::aligned(Y, 16) || (residual && !obs::aligned(residual, 16)) || !obs::aligned(ws, 256))
+    return obs::set_error(ctx, OBS_E_ALIGN, "obs_moe_prefill: X/Y/residual need 16-byte, ws 256-byte alignment");
+  char* base = static_cast<char*>(ws);
+  int32_t* d_ids = reinterpret_cast<int32_t*>(base + L.ids);
+  float* d_w = reinterpret_cast<float*>(base + L.w);
+  if (!ids) {
+    rc = obs::launch_gate_logits(ctx, layer->router_w, layer->router_s, layer->router_b, X,
+                                 reinterpret_cast<float*>(base + L.logits), T, H, E, cfg->group);
+    if (rc) return rc;
+    rc = obs::launch_route_topk(ctx, reinterpret_cast<float*>(base + L.logits), d_ids, d_w, T, E, k, cfg->norm_topk);
+    if (rc) return rc;
+    ids = d_ids;
+    weights = d_w;
+  }
+  int32_t* counts = reinterpret_cast<int32_t*>(base + L.counts);
+  int32_t* offsets = reinterpret_cast<int32_t*>(base + L.offsets);
+  int32_t* ntiles = reinterpret_cast<int32_t*>(base + L.ntiles);
+  int32_t* row_token = reinterpret_cast<int32_t*>(base + L.row_token);
+  int32_t* row_slot = reinterpret_cast<int32_t*>(base + L.row_slot);
+  int4* tiles = reinterpret_cast<int4*>(base + L.tiles);
+  uint16_t* Hbuf = reinterpret_cast<uint16_t*>(base + L.H);
+  uint16_t* Yp = reinterpret_cast<uint16_t*>(base + L.Yp);
+  OBS_LAUNCH(ctx, "moe_group", group_kernel<<<1, 1024, lds, ctx->stream>>>(ids, T, k, E, counts, offsets, row_token,
+                                                                               row_slot, tiles, ntiles));
+  GemmArgs g{};
+  g.A = X; g.a_rows = row_token; g.a_rows_total = T;
+  g.w0 = layer->gate_w; g.s0 = layer->gate_s; g.b0 = layer->gate_b;
+  g.w1 = layer->up_w; g.s1 = layer->up_s; g.b1 = layer->up_b;
+  g.out = Hbuf; g.out_rows = nullptr;
+  g.tiles = tiles; g.n_tiles = ntiles;
+  g.K = H; g.N = I;
+  rc = launch_gemm(ctx, true, g, L.max_tiles);
+  if (rc) return rc;
+  GemmArgs d{};
+  d.A = Hbuf; d.a_rows = nullptr; d.a_rows_total = T * k;
+  d.w0 = layer->down_w; d.s0 = layer->down_s; d.b0 = layer->down_b;
+  d.out = Yp; d.out_rows = row_slot;
+  d.tiles = tiles; d.n_tiles = ntiles;
+  d.K = I; d.N = H;
+  rc = launch_gemm(ctx, false, d, L.max_tiles);
+  if (rc) return rc;
+  const uint64_t nthreads = static_cast<uint64_t>(T) * (H / 8u);
+  OBS_LAUNCH(ctx, "moe_combine", combine_kernel<<<static_cast<uint32_t>((nthreads + 255) / 256), 256, 0, ctx->stream>>>(
+                                     Yp, ids, weights, residual, Y, T, k, H, E));
+  return OBS_OK;
+}
+
+int obs_q4_matmul(obs_ctx* ctx, const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
+                  const uint16_t* X, uint16_t* Y, uint32_t T, uint32_t in, uint32_t out, uint32_t group) {
+  if (!ctx) return OBS_E_INVALID;
+  if (!w || !scales || !biases || !X || !Y) return obs::set_error(ctx, OBS_E_INVALID, "obs_q4_matmul: null pointer");
+  if (group != GK) return obs::set_error(ctx, OBS_E_SHAPE, "obs_q4_matmul: group must be %u (got %u)", GK, group);
+  if (in == 0 || in % GK != 0 || out == 0 || out % TN != 0)
+    return obs::set_error(ctx, OBS_E_SHAPE, "obs_q4_matmul: in must be a multiple of %u and out of %u (got %u, %u)",
+                          GK, TN, in, out);
+  if (!obs::aligned(X, 16) || !obs::aligned(w, 16))
+    return obs::set_error(ctx, OBS_E_ALIGN, "obs_q4_matmul: X and w must be 16-byte aligned");
+  if (T == 0) return OBS_OK;
+  const uint32_t tiles = (T + TM - 1) / TM;
+  GemmArgs g{};
+  g.A = X; g.a_rows = nullptr; g.a_rows_total = T;
+  g.w0 = w; g.s0 = scales; g.b0 = biases;
+  g.out = Y; g.out_rows = nullptr;
+  g.tiles = nullptr; g.n_tiles = nullptr; g.dense_rows = T;
+  g.K = in; g.N = out;
+  return launch_gemm(ctx, false, g, tiles);
 }
 
 }  // extern "C"
