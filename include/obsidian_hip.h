@@ -136,7 +136,8 @@ int obs_q4_matvec(obs_ctx* ctx, const uint32_t* w, const uint16_t* scales,
 
 /* Y[T, out] = X[T, in] . dequant(W)^T, bf16 in/out, fp32 accumulate — Model::matmul_raw
  * (forward.rs:313-321) / matmul_dequant_4bit.metal. Runs the grouped
- * dequant-to-LDS bf16 MFMA GEMM with a single group. */
+ * dequant-to-register bf16 MFMA GEMM with a single expert. Requires group == 64,
+ * in % 256 == 0 and out % 128 == 0 (OBS_E_SHAPE otherwise). */
 int obs_q4_matmul(obs_ctx* ctx, const uint32_t* w, const uint16_t* scales,
                   const uint16_t* biases, const uint16_t* X, uint16_t* Y,
                   uint32_t T, uint32_t in, uint32_t out, uint32_t group);

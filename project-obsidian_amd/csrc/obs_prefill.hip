@@ -40,6 +40,7 @@ using namespace obsd;
 
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
 typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16_t;
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));  // register-friendly 16-byte word
 
 constexpr uint32_t TM = 128;          // tile rows
 constexpr uint32_t TN = 128;          // tile output columns (4 waves x 32)
@@ -62,12 +63,15 @@ struct GemmArgs {
 };
 
 // 16 bytes = 32 nibbles of one weight row -> 4 bf16x8 MFMA fragments (K-steps 0..3).
-__device__ __forceinline__ void dequant_frags(const uint4& q, float s, float b, bf16x8_t (&f)[4]) {
+__device__ __forceinline__ void dequant_frags(const u32x4_t& q, float s, float b, bf16x8_t (&f)[4]) {
   const uint32_t wd[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
   for (int st = 0; st < 4; ++st) {
     const uint32_t w = wd[st];
-    const uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
+    uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
+    // opaque to the optimizer, so each byte below converts with one v_cvt_f32_ubyteN
+    // instead of being re-derived from w with a shift and a mask
+    asm("" : "+v"(lo), "+v"(hi));
     float v[8];
     v[0] = __builtin_fmaf(static_cast<float>(lo & 0xffu), s, b);
     v[1] = __builtin_fmaf(static_cast<float>(hi & 0xffu), s, b);
@@ -79,6 +83,148 @@ __device__ __forceinline__ void dequant_frags(const uint4& q, float s, float b, 
     v[7] = __builtin_fmaf(static_cast<float>(hi >> 24), s, b);
 #pragma unroll
     for (int j = 0; j < 8; ++j) f[st][j] = static_cast<__bf16>(v[j]);  // RNE
+  }
+}
+
+// One tile's main loop and epilogue, NB = active 32-row blocks (1..4), so the
+// MFMA sequence is straight-line code.
+template <bool SWIGLU, uint32_t NB>
+__device__ __forceinline__ void gemm_tile(const GemmArgs& a, uint16_t (&sA)[2][TM * LDS_STRIDE],
+                                          const int32_t* s_arow, uint32_t e, uint32_t row0, uint32_t nrows) {
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  const uint32_t n = blockIdx.y * TN + 32u * wave + (lane & 31u);  // this lane's weight row
+  const uint32_t h = lane >> 5;                                    // k half within a group
+  const uint32_t K = a.K, groups = K / GK;
+
+  // A staging: thread t -> tile row t/2, 32 bf16 at column 32*(t%2) of the group
+  const uint32_t ar = tid >> 1, ac = 32u * (tid & 1u);
+  const int32_t arow = s_arow[ar];
+  // Padding rows (no A row) load row 0 (their values are never stored) and keep
+  // the zeros written here in both LDS buffers.
+  const bool a_ok = arow >= 0;
+  const uint16_t* aptr = a.A + static_cast<size_t>(a_ok ? arow : 0) * K + ac;
+  auto load_a = [&](uint32_t g, u32x4_t (&r)[4]) __attribute__((always_inline)) {
+    const u32x4_t* p = reinterpret_cast<const u32x4_t*>(aptr + g * GK);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r[i] = p[i];
+  };
+  auto store_a = [&](uint32_t buf, const u32x4_t (&r)[4]) __attribute__((always_inline)) {
+    if (a_ok) {
+      u32x4_t* d = reinterpret_cast<u32x4_t*>(&sA[buf][ar * LDS_STRIDE + ac]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) d[i] = r[i];
+    }
+  };
+  if (!a_ok) {
+#pragma unroll
+    for (uint32_t buf = 0; buf < 2; ++buf) {
+      u32x4_t* d = reinterpret_cast<u32x4_t*>(&sA[buf][ar * LDS_STRIDE + ac]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) d[i] = u32x4_t{0u, 0u, 0u, 0u};
+    }
+  }
+
+  // B pointers of this lane's weight row(s)
+  const size_t wrow = static_cast<size_t>(e) * a.N + n;
+  const u32x4_t* w0p = reinterpret_cast<const u32x4_t*>(a.w0 + wrow * (K / 8)) + h;  // + 2*g per group
+  const uint16_t* s0p = a.s0 + wrow * groups;
+  const uint16_t* b0p = a.b0 + wrow * groups;
+  const u32x4_t* w1p = SWIGLU ? reinterpret_cast<const u32x4_t*>(a.w1 + wrow * (K / 8)) + h : nullptr;
+  const uint16_t* s1p = SWIGLU ? a.s1 + wrow * groups : nullptr;
+  const uint16_t* b1p = SWIGLU ? a.b1 + wrow * groups : nullptr;
+
+  struct BRaw {
+    u32x4_t q0, q1;
+    uint16_t s0, b0, s1, b1;
+  };
+  auto load_b = [&](uint32_t g) __attribute__((always_inline)) {
+    BRaw r;
+    const uint32_t gg = g < groups ? g : groups - 1u;  // clamped: the tail loads are never used
+    r.q0 = w0p[2u * gg];
+    r.s0 = s0p[gg];
+    r.b0 = b0p[gg];
+    if (SWIGLU) {
+      r.q1 = w1p[2u * gg];
+      r.s1 = s1p[gg];
+      r.b1 = b1p[gg];
+    }
+    return r;
+  };
+
+  f32x16_t acc0[NB], acc1[NB];
+#pragma unroll
+  for (int mb = 0; mb < NB; ++mb) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) { acc0[mb][v] = 0.0f; acc1[mb][v] = 0.0f; }
+  }
+
+  // Pipeline: B is loaded four groups ahead into one of four register slots,
+  // A two groups ahead into one of two (then to the LDS buffer of its group);
+  // per group the A fragments are read from LDS first, the next group's B is
+  // dequantized while they arrive, then the MFMAs run back to back. The loop
+  // is unrolled by four so every slot is a fixed set of registers: rotating
+  // values between slots would make each group wait for its own prefetches.
+  BRaw bs0, bs1 = load_b(1), bs2 = load_b(2), bs3 = load_b(3);
+  u32x4_t ras0[4], ras1[4];
+  load_a(0, ras0);
+  load_a(1, ras1);
+  store_a(0, ras0);
+  bf16x8_t fa0[4], fa1[4], fb0[4], fb1[4];
+  {
+    const BRaw b0r = load_b(0);
+    dequant_frags(b0r.q0, bf16_to_f32(b0r.s0), bf16_to_f32(b0r.b0), fa0);
+    if (SWIGLU) dequant_frags(b0r.q1, bf16_to_f32(b0r.s1), bf16_to_f32(b0r.b1), fa1);
+  }
+
+  // group g: B of g+4 -> bld, A of g+2 -> rld, A of g+1 (rst) -> LDS, B of g+1
+  // (bdq) -> fragments fn, MFMAs with fragments fc
+  auto step = [&](uint32_t g, BRaw& bld, const BRaw& bdq, u32x4_t (&rld)[4], const u32x4_t (&rst)[4],
+                  const bf16x8_t (&fc0)[4], const bf16x8_t (&fc1)[4], bf16x8_t (&fn0)[4],
+                  bf16x8_t (&fn1)[4]) __attribute__((always_inline)) {
+    const uint32_t buf = g & 1u;
+    bld = load_b(g + 4);
+    load_a(g + 2 < groups ? g + 2 : g, rld);  // the tail reload is never stored
+    __syncthreads();  // A of group g visible in sA[buf]; sA[buf^1] no longer read
+    bf16x8_t af[4][NB];
+#pragma unroll
+    for (uint32_t st = 0; st < 4; ++st) {
+#pragma unroll
+      for (uint32_t mb = 0; mb < NB; ++mb)
+        af[st][mb] = *reinterpret_cast<const bf16x8_t*>(
+            &sA[buf][(32u * mb + (lane & 31u)) * LDS_STRIDE + 32u * h + 8u * st]);
+    }
+    if (g + 1 < groups) store_a(buf ^ 1u, rst);
+    dequant_frags(bdq.q0, bf16_to_f32(bdq.s0), bf16_to_f32(bdq.b0), fn0);
+    if (SWIGLU) dequant_frags(bdq.q1, bf16_to_f32(bdq.s1), bf16_to_f32(bdq.b1), fn1);
+#pragma unroll
+    for (uint32_t st = 0; st < 4; ++st) {
+#pragma unroll
+      for (uint32_t mb = 0; mb < NB; ++mb) {
+        acc0[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[st][mb], fc0[st], acc0[mb], 0, 0, 0);
+        if (SWIGLU) acc1[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[st][mb], fc1[st], acc1[mb], 0, 0, 0);
+      }
+    }
+  };
+  for (uint32_t g = 0; g < groups; g += 4) {  // groups % 4 == 0 (K % 256 == 0, checked by the host)
+    step(g, bs0, bs1, ras0, ras1, fa0, fa1, fb0, fb1);
+    step(g + 1, bs1, bs2, ras1, ras0, fb0, fb1, fa0, fa1);
+    step(g + 2, bs2, bs3, ras0, ras1, fa0, fa1, fb0, fb1);
+    step(g + 3, bs3, bs0, ras1, ras0, fb0, fb1, fa0, fa1);
+  }
+
+  // epilogue: lane holds C[i][n] for i = 32mb + 8(v/4) + 4h + v%4
+#pragma unroll
+  for (uint32_t mb = 0; mb < NB; ++mb) {
+#pragma unroll
+    for (uint32_t v = 0; v < 16; ++v) {
+      const uint32_t i = 32u * mb + 8u * (v / 4u) + 4u * h + (v % 4u);
+      if (i < nrows) {
+        const float val = SWIGLU ? silu_mul(acc0[mb][v], acc1[mb][v]) : acc0[mb][v];
+        const uint32_t p = row0 + i;
+        const size_t orow = a.out_rows ? static_cast<size_t>(a.out_rows[p]) : p;
+        a.out[orow * a.N + n] = f32_to_bf16(val);
+      }
+    }
   }
 }
 
@@ -96,12 +242,7 @@ __global__ void __launch_bounds__(256, 1) grouped_gemm_kernel(GemmArgs a) {
   }
   const uint32_t e = static_cast<uint32_t>(tile.x), row0 = static_cast<uint32_t>(tile.y);
   const uint32_t nrows = static_cast<uint32_t>(tile.z);
-  const uint32_t nblk = (nrows + 31u) / 32u;  // active 32-row blocks
-  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-  const uint32_t n = blockIdx.y * TN + 32u * wave + (lane & 31u);  // this lane's weight row
-  const uint32_t h = lane >> 5;                                    // k half within a group
-  const uint32_t K = a.K, groups = K / GK;
-
+  const uint32_t tid = threadIdx.x;
   if (tid < TM) {
     int32_t r = -1;
     if (tid < nrows) {
@@ -112,101 +253,11 @@ __global__ void __launch_bounds__(256, 1) grouped_gemm_kernel(GemmArgs a) {
     s_arow[tid] = r;
   }
   __syncthreads();
-
-  // A staging: thread t -> tile row t/2, 32 bf16 at column 32*(t%2) of the group
-  const uint32_t ar = tid >> 1, ac = 32u * (tid & 1u);
-  const int32_t arow = s_arow[ar];
-  const uint16_t* aptr = arow >= 0 ? a.A + static_cast<size_t>(arow) * K + ac : nullptr;
-  auto load_a = [&](uint32_t g, uint4 (&r)[4]) {
-    if (aptr) {
-      const uint4* p = reinterpret_cast<const uint4*>(aptr + g * GK);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) r[i] = p[i];
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) r[i] = make_uint4(0u, 0u, 0u, 0u);
-    }
-  };
-  auto store_a = [&](uint32_t buf, const uint4 (&r)[4]) {
-    uint4* d = reinterpret_cast<uint4*>(&sA[buf][ar * LDS_STRIDE + ac]);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) d[i] = r[i];
-  };
-
-  // B pointers of this lane's weight row(s)
-  const size_t wrow = static_cast<size_t>(e) * a.N + n;
-  const uint4* w0p = reinterpret_cast<const uint4*>(a.w0 + wrow * (K / 8)) + h;  // + 2*g per group
-  const uint16_t* s0p = a.s0 + wrow * groups;
-  const uint16_t* b0p = a.b0 + wrow * groups;
-  const uint4* w1p = SWIGLU ? reinterpret_cast<const uint4*>(a.w1 + wrow * (K / 8)) + h : nullptr;
-  const uint16_t* s1p = SWIGLU ? a.s1 + wrow * groups : nullptr;
-  const uint16_t* b1p = SWIGLU ? a.b1 + wrow * groups : nullptr;
-
-  f32x16_t acc0[4], acc1[4];
-#pragma unroll
-  for (int mb = 0; mb < 4; ++mb) {
-#pragma unroll
-    for (int v = 0; v < 16; ++v) { acc0[mb][v] = 0.0f; acc1[mb][v] = 0.0f; }
-  }
-
-  uint4 ra[4];
-  load_a(0, ra);
-  uint4 q0 = w0p[0], q1 = SWIGLU ? w1p[0] : make_uint4(0u, 0u, 0u, 0u);
-  uint16_t sv0 = s0p[0], bv0 = b0p[0], sv1 = SWIGLU ? s1p[0] : 0, bv1 = SWIGLU ? b1p[0] : 0;
-  store_a(0, ra);
-
-  for (uint32_t g = 0; g < groups; ++g) {
-    const uint32_t buf = g & 1u;
-    // prefetch group g+1 (A into registers, B words and scales)
-    uint4 nq0 = q0, nq1 = q1;
-    uint16_t nsv0 = sv0, nbv0 = bv0, nsv1 = sv1, nbv1 = bv1;
-    const bool more = g + 1 < groups;
-    if (more) {
-      load_a(g + 1, ra);
-      nq0 = w0p[2u * (g + 1)];
-      nsv0 = s0p[g + 1];
-      nbv0 = b0p[g + 1];
-      if (SWIGLU) {
-        nq1 = w1p[2u * (g + 1)];
-        nsv1 = s1p[g + 1];
-        nbv1 = b1p[g + 1];
-      }
-    }
-    bf16x8_t f0[4], f1[4];
-    dequant_frags(q0, bf16_to_f32(sv0), bf16_to_f32(bv0), f0);
-    if (SWIGLU) dequant_frags(q1, bf16_to_f32(sv1), bf16_to_f32(bv1), f1);
-    __syncthreads();  // A tile of group g visible in sA[buf]
-#pragma unroll
-    for (uint32_t st = 0; st < 4; ++st) {
-#pragma unroll
-      for (uint32_t mb = 0; mb < 4; ++mb) {
-        if (mb < nblk) {
-          const bf16x8_t af = *reinterpret_cast<const bf16x8_t*>(
-              &sA[buf][(32u * mb + (lane & 31u)) * LDS_STRIDE + 32u * h + 8u * st]);
-          acc0[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, f0[st], acc0[mb], 0, 0, 0);
-          if (SWIGLU) acc1[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, f1[st], acc1[mb], 0, 0, 0);
-        }
-      }
-    }
-    if (more) store_a(buf ^ 1u, ra);  // the other buffer was last read in group g-1
-    q0 = nq0; q1 = nq1;
-    sv0 = nsv0; bv0 = nbv0; sv1 = nsv1; bv1 = nbv1;
-  }
-
-  // epilogue: lane holds C[i][n] for i = 32mb + 8(v/4) + 4h + v%4
-#pragma unroll
-  for (uint32_t mb = 0; mb < 4; ++mb) {
-    if (mb >= nblk) continue;
-#pragma unroll
-    for (uint32_t v = 0; v < 16; ++v) {
-      const uint32_t i = 32u * mb + 8u * (v / 4u) + 4u * h + (v % 4u);
-      if (i < nrows) {
-        const float val = SWIGLU ? silu_mul(acc0[mb][v], acc1[mb][v]) : acc0[mb][v];
-        const uint32_t p = row0 + i;
-        const size_t orow = a.out_rows ? static_cast<size_t>(a.out_rows[p]) : p;
-        a.out[orow * a.N + n] = f32_to_bf16(val);
-      }
-    }
+  switch ((nrows + 31u) / 32u) {  // uniform per workgroup
+    case 1: gemm_tile<SWIGLU, 1>(a, sA, s_arow, e, row0, nrows); break;
+    case 2: gemm_tile<SWIGLU, 2>(a, sA, s_arow, e, row0, nrows); break;
+    case 3: gemm_tile<SWIGLU, 3>(a, sA, s_arow, e, row0, nrows); break;
+    default: gemm_tile<SWIGLU, 4>(a, sA, s_arow, e, row0, nrows); break;
   }
 }
 
@@ -231,20 +282,25 @@ __global__ void __launch_bounds__(1024) group_kernel(const int32_t* __restrict__
 
   for (uint32_t i = tid; i < nchunks * E; i += blockDim.x) cnt[i] = 0;
   __syncthreads();
-  // a token's valid experts: in range and not repeated among its k ids
-  auto valid = [&](uint32_t t, uint32_t r, int32_t e) -> bool {
-    if (e < 0 || static_cast<uint32_t>(e) >= E) return false;
-    for (uint32_t q = 0; q < r; ++q)
-      if (ids[static_cast<size_t>(t) * k + q] == e) return false;
-    return true;
+  // A token's k (<= 8) ids in registers, -1 where invalid: out of range or a
+  // repeat of an earlier rank of the same token.
+  auto load_ids = [&](uint32_t t, int32_t (&ev)[8]) {
+#pragma unroll
+    for (uint32_t r = 0; r < 8; ++r) ev[r] = (t < T && r < k) ? ids[static_cast<size_t>(t) * k + r] : -1;
+#pragma unroll
+    for (uint32_t r = 0; r < 8; ++r) {
+      bool ok = ev[r] >= 0 && static_cast<uint32_t>(ev[r]) < E;
+#pragma unroll
+      for (uint32_t q = 0; q < r; ++q) ok = ok && ev[q] != ev[r];
+      ev[r] = ok ? ev[r] : -1;
+    }
   };
   for (uint32_t c = wave; c < nchunks; c += nwaves) {
-    const uint32_t t = c * GROUP_TOKENS + lane;
-    if (t < T)
-      for (uint32_t r = 0; r < k; ++r) {
-        const int32_t e = ids[static_cast<size_t>(t) * k + r];
-        if (valid(t, r, e)) atomicAdd(&cnt[c * E + static_cast<uint32_t>(e)], 1);
-      }
+    int32_t ev[8];
+    load_ids(c * GROUP_TOKENS + lane, ev);
+#pragma unroll
+    for (uint32_t r = 0; r < 8; ++r)
+      if (ev[r] >= 0) atomicAdd(&cnt[c * E + static_cast<uint32_t>(ev[r])], 1);
   }
   __syncthreads();
   for (uint32_t e = tid; e < E; e += blockDim.x) {
@@ -285,23 +341,23 @@ __global__ void __launch_bounds__(1024) group_kernel(const int32_t* __restrict__
   unsigned long long* wb = bits + static_cast<size_t>(wave) * E;
   const unsigned long long lt = (1ull << lane) - 1ull;
   for (uint32_t c = wave; c < nchunks; c += nwaves) {
+    const uint32_t t = c * GROUP_TOKENS + lane;
+    int32_t ev[8];
+    load_ids(t, ev);
     for (uint32_t e = lane; e < E; e += 64u) wb[e] = 0ull;
     __builtin_amdgcn_wave_barrier();
-    const uint32_t t = c * GROUP_TOKENS + lane;
-    if (t < T)
-      for (uint32_t r = 0; r < k; ++r) {
-        const int32_t e = ids[static_cast<size_t>(t) * k + r];
-        if (valid(t, r, e)) atomicOr(&wb[e], 1ull << lane);
-      }
+#pragma unroll
+    for (uint32_t r = 0; r < 8; ++r)
+      if (ev[r] >= 0) atomicOr(&wb[ev[r]], 1ull << lane);
     __builtin_amdgcn_wave_barrier();
-    if (t < T)
-      for (uint32_t r = 0; r < k; ++r) {
-        const int32_t e = ids[static_cast<size_t>(t) * k + r];
-        if (!valid(t, r, e)) continue;
-        const int32_t row = off[e] + cnt[c * E + static_cast<uint32_t>(e)] + __popcll(wb[e] & lt);
-        row_token[row] = static_cast<int32_t>(t);
-        row_slot[row] = static_cast<int32_t>(t * k + r);
-      }
+#pragma unroll
+    for (uint32_t r = 0; r < 8; ++r) {
+      if (ev[r] < 0) continue;
+      const uint32_t e = static_cast<uint32_t>(ev[r]);
+      const int32_t row = off[e] + cnt[c * E + e] + __popcll(wb[e] & lt);
+      row_token[row] = static_cast<int32_t>(t);
+      row_slot[row] = static_cast<int32_t>(t * k + r);
+    }
     __builtin_amdgcn_wave_barrier();
   }
 }
@@ -464,9 +520,9 @@ int obs_q4_matmul(obs_ctx* ctx, const uint32_t* w, const uint16_t* scales, const
   if (!ctx) return OBS_E_INVALID;
   if (!w || !scales || !biases || !X || !Y) return obs::set_error(ctx, OBS_E_INVALID, "obs_q4_matmul: null pointer");
   if (group != GK) return obs::set_error(ctx, OBS_E_SHAPE, "obs_q4_matmul: group must be %u (got %u)", GK, group);
-  if (in == 0 || in % GK != 0 || out == 0 || out % TN != 0)
+  if (in == 0 || in % (4u * GK) != 0 || out == 0 || out % TN != 0)
     return obs::set_error(ctx, OBS_E_SHAPE, "obs_q4_matmul: in must be a multiple of %u and out of %u (got %u, %u)",
-                          GK, TN, in, out);
+                          4u * GK, TN, in, out);
   if (!obs::aligned(X, 16) || !obs::aligned(w, 16))
     return obs::set_error(ctx, OBS_E_ALIGN, "obs_q4_matmul: X and w must be 16-byte aligned");
   if (T == 0) return OBS_OK;
