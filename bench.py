@@ -117,19 +117,54 @@ def bench_decode(torch, oh, exe, args):
     for g in graphs:
         exe.graph_destroy(g)
     kernels = {n: {"avg_us": 1000.0 * t / c, "launches": c} for n, (t, c) in stats.items()}
-    # the fused layer kernel moves all of a layer's algorithmic bytes; the
-    # 4-launch path's largest kernel is gate/up
-    name, nbytes = ("decode_fused", LAYER_BYTES) if "decode_fused" in kernels else ("decode_gateup", GATEUP_BYTES)
+    # The fused path is one launch per layer, so its average launch duration
+    # is the timed region (HIP events on the context's stream around the graph
+    # replays) divided by the launches in it; the per-launch event pairs above
+    # add the event records' own overhead and are reported beside it. The
+    # 4-launch path's largest kernel is gate/up, timed by its event pairs.
     roof = None
-    if name in kernels:
-        us = kernels[name]["avg_us"]
+    if "decode_fused" in kernels:
+        name, nbytes, us = "decode_fused", LAYER_BYTES, us_layer
+    elif "decode_gateup" in kernels:
+        name, nbytes, us = "decode_gateup", GATEUP_BYTES, kernels["decode_gateup"]["avg_us"]
+    else:
+        name = None
+    if name is not None:
         ach = nbytes / (us * 1e-6) / 1e9
         roof = {"kernel": name, "bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
-                "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
-                "bytes_per_launch": nbytes, "avg_launch_us": round(us, 3)}
+                "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": measured_traffic(name),
+                "bytes_per_launch": nbytes, "avg_launch_us": round(us, 3),
+                "event_pair_us": round(kernels[name]["avg_us"], 3)}
     del table, xs, ys
     torch.cuda.empty_cache()
     return {"ms_step": ms_step, "us_layer": us_layer, "gbs": gbs, "kernels": kernels, "roofline": roof}
+
+
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed counter summary
+    (rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE passes, each scaled by the same
+    counter over a plain device copy of known size); None when not measured."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+    try:
+        with open(path) as f:
+            rec = json.load(f).get(kernel)
+    except (OSError, ValueError):
+        return None
+    return None if rec is None else rec.get("traffic_bytes_per_launch")
+
+
+def calibrate_copy(torch, mib):
+    """A plain device-to-device copy of `mib` MiB, three times: the known-size
+    kernel that scales the FETCH_SIZE / WRITE_SIZE counters to bytes."""
+    n = mib << 20
+    src = torch.empty(n, dtype=torch.uint8, device="cuda").random_(0, 256)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    ok = bool(torch.equal(dst[:4096], src[:4096]))
+    print(json.dumps({"calibration": "device copy", "bytes_read": n, "bytes_written": n, "copies": 3, "ok": ok}))
 
 
 def bench_prefill(torch, oh, exe, args):
@@ -230,6 +265,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="only run a plain MIB-MiB device copy (counter calibration) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
@@ -237,6 +274,9 @@ def main():
         sys.exit(2)
 
     import torch
+    if args.calibrate_copy:
+        calibrate_copy(torch, args.calibrate_copy)
+        return
     import obsidian_hip as oh
 
     exe = oh.ObsidianExecutor(0)

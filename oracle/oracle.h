@@ -17,6 +17,14 @@
  * Every function is pinned by a check in tests/ (known-answer vectors,
  * closed forms, brute force on small inputs or invariants); the header of
  * oracle.c lists which.
+ *
+ * Parity unpinned (relative to the reference itself, not to this file):
+ *   - the bf16 rounding of MLX mx.dequantize's output (validate_dequant.py:21):
+ *     MLX is absent, so the bf16 value is defined here as one RNE of the exact
+ *     fp32 q*s+b;
+ *   - Metal fast-math exp and contraction inside the reference shaders: the
+ *     reference's f16 logits and routing weights are restated semantically
+ *     (orc_route_topk's emulate_f16 mode), not bit for bit.
  */
 #ifndef OBSIDIAN_ORACLE_H
 #define OBSIDIAN_ORACLE_H
