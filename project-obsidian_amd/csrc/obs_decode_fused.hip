@@ -17,7 +17,8 @@
 // and has index j = b / 8 within it.
 //   1. Router: each group computes all E logits (one 2 KB row per wave) in the
 //      router's documented reduction order, so every group sees bit-identical
-//      logits; then every wave runs softmax + top-8 itself (no broadcast).
+//      logits; wave 0 of every workgroup runs softmax + top-8 on them and
+//      shares the result through LDS.
 //   2. Group g serves routing rank g: expert e_g = ids[g]. Its 128 waves stream
 //      the 768 gate and up rows (6 each) and, at the same time, the down rows the
 //      workgroup will need (64 rows x 384 B per workgroup), so the down weights
@@ -101,7 +102,8 @@ __global__ void __launch_bounds__(256, 1) decode_fused_kernel(FusedArgs a) {
   __shared__ int32_t s_ids[FK];
   __shared__ float s_w[FK];
   __shared__ bool s_ok;
-  __shared__ float s_h[FI];
+  __shared__ __attribute__((aligned(16))) f16x2_t s_hp[FI / 2];  // h as f16 pairs, dot8_q4_off order
+  __shared__ float s_hsum[FI / 32], s_hoff[FI / 32];              // per 32 columns: sum h, sum off*h
   __shared__ float s_y[FK][64];
 
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
@@ -152,6 +154,14 @@ __global__ void __launch_bounds__(256, 1) decode_fused_kernel(FusedArgs a) {
   float xs = 0.0f;
 #pragma unroll
   for (int c = 0; c < 32; ++c) xs = xs + xf[c];
+  // the lane's 32 activations as f16 pairs for the expert rows, and the offset
+  // part of dot8_q4_off over them (shared by every row)
+  f16x2_t xh[16];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) f16_pairs8(xf + 8 * i, xh + 4 * i);
+  float xoff = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) xoff = dot8_off_only(xh + 4 * i, xoff);
 
   // ---- 1. router logits (order of obs_q8_gate_logits: serial fma, then wave_sum_asc)
 #pragma unroll
@@ -195,8 +205,8 @@ __global__ void __launch_bounds__(256, 1) decode_fused_kernel(FusedArgs a) {
   }
   OBS_FUSED_MARK(9);
   if (!ok && lane == 0) raise_error(a.ws);
-  // one wave per workgroup routes (the CU has one scalar unit; four identical
-  // routings would contend for it), then broadcasts through LDS
+  // one wave per workgroup routes (moe_routing_topk.metal:31-56), then
+  // broadcasts through LDS
   if (wave == 0) {
     int32_t id;
     float w;
@@ -258,16 +268,16 @@ __global__ void __launch_bounds__(256, 1) decode_fused_kernel(FusedArgs a) {
     float pg = 0.0f, pu = 0.0f;
     if (have) {
       float ag = 0.0f, au = 0.0f;
-      ag = dot8_q4(gq[t].x, xf + 0, ag);
-      ag = dot8_q4(gq[t].y, xf + 8, ag);
-      ag = dot8_q4(gq[t].z, xf + 16, ag);
-      ag = dot8_q4(gq[t].w, xf + 24, ag);
-      au = dot8_q4(uq[t].x, xf + 0, au);
-      au = dot8_q4(uq[t].y, xf + 8, au);
-      au = dot8_q4(uq[t].z, xf + 16, au);
-      au = dot8_q4(uq[t].w, xf + 24, au);
-      pg = __builtin_fmaf(bf16_to_f32(gsv[t]), ag, bf16_to_f32(gbv[t]) * xs);
-      pu = __builtin_fmaf(bf16_to_f32(usv[t]), au, bf16_to_f32(ubv[t]) * xs);
+      ag = dot8_q4_off(gq[t].x, xh + 0, ag);
+      ag = dot8_q4_off(gq[t].y, xh + 4, ag);
+      ag = dot8_q4_off(gq[t].z, xh + 8, ag);
+      ag = dot8_q4_off(gq[t].w, xh + 12, ag);
+      au = dot8_q4_off(uq[t].x, xh + 0, au);
+      au = dot8_q4_off(uq[t].y, xh + 4, au);
+      au = dot8_q4_off(uq[t].z, xh + 8, au);
+      au = dot8_q4_off(uq[t].w, xh + 12, au);
+      pg = __builtin_fmaf(bf16_to_f32(gsv[t]), ag - xoff, bf16_to_f32(gbv[t]) * xs);
+      pu = __builtin_fmaf(bf16_to_f32(usv[t]), au - xoff, bf16_to_f32(ubv[t]) * xs);
     }
     pg = wave_sum_asc(pg);
     pu = wave_sum_asc(pu);
@@ -276,17 +286,19 @@ __global__ void __launch_bounds__(256, 1) decode_fused_kernel(FusedArgs a) {
   }
 
   OBS_FUSED_MARK(5);
-  // ---- 5. poll the group's 768 h values into LDS
+  // ---- 5. poll the group's 768 h values; store them to LDS as f16 in the pair
+  // order of dot8_q4_off, with the sum and the offset sum of every 32 columns
+  // (32 consecutive columns sit in one half-wave)
   {
     bool wave_ok = ok;
+    float hv[FI / 256];
     const uint64_t t0 = wall_clock64();
     while (wave_ok) {
       bool ready = true;
 #pragma unroll
       for (uint32_t u = 0; u < FI / 256; ++u) {
-        const uint32_t idx = tid + 256u * u;
-        const uint64_t v = slot_load(h_slots + idx);
-        s_h[idx] = slot_val(v);
+        const uint64_t v = slot_load(h_slots + tid + 256u * u);
+        hv[u] = slot_val(v);
         ready = ready && slot_ready(v, epoch);
       }
       if (__all(ready)) break;
@@ -296,25 +308,39 @@ __global__ void __launch_bounds__(256, 1) decode_fused_kernel(FusedArgs a) {
       }
     }
     ok = ok && wave_ok;
+    _Float16* hp16 = reinterpret_cast<_Float16*>(s_hp);
+#pragma unroll
+    for (uint32_t u = 0; u < FI / 256; ++u) {
+      const uint32_t idx = tid + 256u * u, jn = idx & 7u;  // column idx = 8 * word + jn
+      hp16[(idx & ~7u) + 2u * (jn & 3u) + (jn >> 2)] = static_cast<_Float16>(hv[u]);
+      // offsets of dot8_q4_off: 1024 at even nibble positions, 64 at odd ones;
+      // the sums use the f16-rounded values the dot products see
+      const float hr = static_cast<float>(static_cast<_Float16>(hv[u]));
+      const float sum = half_wave_sum(hr);
+      const float off = half_wave_sum(hr * ((jn & 1u) ? 64.0f : 1024.0f));
+      if ((idx & 31u) == 0u) {
+        s_hsum[idx >> 5] = sum;
+        s_hoff[idx >> 5] = off;
+      }
+    }
   }
   __syncthreads();
 
   OBS_FUSED_MARK(6);
   // ---- 6. this workgroup's 64 down rows of expert e_g (unscaled by w_g)
   {
-    float hsum[3];
-    float hreg[96];
+    // the lane's 96 columns [96m, 96m + 96) = three 32-column blocks
+    f16x2_t hp[48];
+    float hsum[3], hoff[3];
 #pragma unroll
-    for (uint32_t c = 0; c < 96; c += 4) {
-      const float4 v = *reinterpret_cast<const float4*>(s_h + 96u * m + c);
-      hreg[c] = v.x; hreg[c + 1] = v.y; hreg[c + 2] = v.z; hreg[c + 3] = v.w;
+    for (uint32_t c = 0; c < 48; c += 4) {
+      const uint4 v = *reinterpret_cast<const uint4*>(s_hp + 48u * m + c);
+      hp[c] = as_f16x2(v.x); hp[c + 1] = as_f16x2(v.y); hp[c + 2] = as_f16x2(v.z); hp[c + 3] = as_f16x2(v.w);
     }
 #pragma unroll
     for (uint32_t b = 0; b < 3; ++b) {
-      float s = 0.0f;
-#pragma unroll
-      for (uint32_t c = 0; c < 32; ++c) s = s + hreg[32u * b + c];
-      hsum[b] = s;
+      hsum[b] = s_hsum[3u * m + b];
+      hoff[b] = s_hoff[3u * m + b];
     }
 #pragma unroll
     for (uint32_t p = 0; p < 2; ++p) {
@@ -323,11 +349,11 @@ __global__ void __launch_bounds__(256, 1) decode_fused_kernel(FusedArgs a) {
 #pragma unroll
         for (uint32_t b = 0; b < 3; ++b) {
           float acc = 0.0f;
-          acc = dot8_q4(dq[p][b].x, hreg + 32u * b + 0, acc);
-          acc = dot8_q4(dq[p][b].y, hreg + 32u * b + 8, acc);
-          acc = dot8_q4(dq[p][b].z, hreg + 32u * b + 16, acc);
-          acc = dot8_q4(dq[p][b].w, hreg + 32u * b + 24, acc);
-          part = part + __builtin_fmaf(bf16_to_f32(dsv[p][b]), acc, bf16_to_f32(dbv[p][b]) * hsum[b]);
+          acc = dot8_q4_off(dq[p][b].x, hp + 16u * b + 0, acc);
+          acc = dot8_q4_off(dq[p][b].y, hp + 16u * b + 4, acc);
+          acc = dot8_q4_off(dq[p][b].z, hp + 16u * b + 8, acc);
+          acc = dot8_q4_off(dq[p][b].w, hp + 16u * b + 12, acc);
+          part = part + __builtin_fmaf(bf16_to_f32(dsv[p][b]), acc - hoff[b], bf16_to_f32(dbv[p][b]) * hsum[b]);
         }
       }
       part = group8_sum(part);

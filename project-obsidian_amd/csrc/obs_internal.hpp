@@ -207,6 +207,77 @@ __device__ __forceinline__ float group8_sum(float v) {
   return v;
 }
 
+// Sum over each 32-lane half of the wave (every lane of the half gets it).
+__device__ __forceinline__ float half_wave_sum(float v) {
+  v = v + dpp_f32<DPP_XOR1>(v);
+  v = v + dpp_f32<DPP_XOR2>(v);
+  v = v + dpp_f32<DPP_HALF_MIRROR>(v);
+  v = v + dpp_f32<DPP_MIRROR>(v);
+  // lanes i and i^16 within each 32-lane group: ds_swizzle bit mode, xor mask 16
+  return v + __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F));
+}
+
+// ---- 4-bit dot products through f16 pairs (v_dot2_f32_f16) -------------------
+// A nibble q becomes an exact f16 by OR-ing it into the mantissa of a constant:
+// at bits 3:0 of 0x6400 (1024.0) it reads 1024 + q, at bits 7:4 of 0x5400 (64.0)
+// it reads 64 + q (one mantissa unit there is 1/16 of 16 = 1). So for a word w
+// holding nibbles q0..q7 of columns c..c+7,
+//   (w & 0x000F000F) | 0x64006400        = (1024 + q0, 1024 + q4)
+//   (w & 0x00F000F0) | 0x54005400        = (  64 + q1,   64 + q5)
+//   ((w>>8) & 0x000F000F) | 0x64006400   = (1024 + q2, 1024 + q6)
+//   ((w>>8) & 0x00F000F0) | 0x54005400   = (  64 + q3,   64 + q7)
+// and four dot2 against the f16 activation pairs (x0,x4), (x1,x5), (x2,x6),
+// (x3,x7) accumulate sum_j (off_j + q_j) x_j in fp32 (each product is exact).
+// The offset part sum_j off_j x_j depends on x only, so it is computed once
+// (dot8_q4_off with w = 0) and subtracted per row: 9 instructions per 8
+// nibbles instead of a convert and an fma per nibble.
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ f16x2_t as_f16x2(uint32_t v) { return __builtin_bit_cast(f16x2_t, v); }
+
+__device__ __forceinline__ f16x2_t f16x2_of(float a, float b) {  // round to nearest even
+  f16x2_t r;
+  r.x = static_cast<_Float16>(a);
+  r.y = static_cast<_Float16>(b);
+  return r;
+}
+
+// (w & mask) | magic in one v_and_or_b32: the compiler splits it into an AND and
+// an OR because VOP3 here takes no literal, so the mask rides in a VGPR and the
+// magic in an SGPR (one constant-bus read).
+__device__ __forceinline__ uint32_t and_or(uint32_t w, uint32_t mask, uint32_t magic) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(w), "v"(mask), "s"(magic));
+  return r;
+}
+
+// xp[0..3] = (x0,x4), (x1,x5), (x2,x6), (x3,x7) of the word's eight columns
+__device__ __forceinline__ float dot8_q4_off(uint32_t w, const f16x2_t* xp, float acc) {
+  const uint32_t w8 = w >> 8;
+  acc = __builtin_amdgcn_fdot2(as_f16x2(and_or(w, 0x000F000Fu, 0x64006400u)), xp[0], acc, false);
+  acc = __builtin_amdgcn_fdot2(as_f16x2(and_or(w, 0x00F000F0u, 0x54005400u)), xp[1], acc, false);
+  acc = __builtin_amdgcn_fdot2(as_f16x2(and_or(w8, 0x000F000Fu, 0x64006400u)), xp[2], acc, false);
+  acc = __builtin_amdgcn_fdot2(as_f16x2(and_or(w8, 0x00F000F0u, 0x54005400u)), xp[3], acc, false);
+  return acc;
+}
+
+// The offset part sum_j off_j x_j of dot8_q4_off (its value for w = 0).
+__device__ __forceinline__ float dot8_off_only(const f16x2_t* xp, float acc) {
+  acc = __builtin_amdgcn_fdot2(as_f16x2(0x64006400u), xp[0], acc, false);
+  acc = __builtin_amdgcn_fdot2(as_f16x2(0x54005400u), xp[1], acc, false);
+  acc = __builtin_amdgcn_fdot2(as_f16x2(0x64006400u), xp[2], acc, false);
+  acc = __builtin_amdgcn_fdot2(as_f16x2(0x54005400u), xp[3], acc, false);
+  return acc;
+}
+
+// f16 pairs of eight consecutive fp32 values in the order dot8_q4_off expects
+__device__ __forceinline__ void f16_pairs8(const float* x, f16x2_t* xp) {
+  xp[0] = f16x2_of(x[0], x[4]);
+  xp[1] = f16x2_of(x[1], x[5]);
+  xp[2] = f16x2_of(x[2], x[6]);
+  xp[3] = f16x2_of(x[3], x[7]);
+}
+
 __device__ __forceinline__ float wave_max_f32(float v) {
   v = __builtin_fmaxf(v, dpp_f32<DPP_XOR1>(v));
   v = __builtin_fmaxf(v, dpp_f32<DPP_XOR2>(v));
@@ -234,9 +305,11 @@ __device__ __forceinline__ int wave_max_i32(int v) {
 // Lane kk < k receives slot kk (id -1, weight 0 if nothing is selectable).
 // Must be called with all 64 lanes active. NQ = logit slots per lane
 // (ceil(n_exp / 64), at most 4); selection is branch-free per round.
+// Softmax of one token's logits (expert 64j + lane in lg[j]) as selection keys:
+// key = bit pattern of p = e / S (non-negative, so integer order = p order),
+// -1 for an absent expert, -2 for NaN.
 template <int NQ>
-__device__ __forceinline__ void route_wave(const float (&lg)[NQ], uint32_t n_exp, uint32_t k, int norm_topk,
-                                           uint32_t lane, int32_t* my_id, float* my_w) {
+__device__ __forceinline__ void route_keys(const float (&lg)[NQ], uint32_t n_exp, uint32_t lane, int (&key)[NQ]) {
   bool present[NQ];
   float m = -__builtin_huge_valf();
 #pragma unroll
@@ -253,12 +326,18 @@ __device__ __forceinline__ void route_wave(const float (&lg)[NQ], uint32_t n_exp
     a = present[j] ? a + e[j] : a;
   }
   const float S = wave_sum_asc(a);
-  int key[NQ];
 #pragma unroll
   for (int j = 0; j < NQ; ++j) {
     const float p = e[j] / S;
     key[j] = present[j] ? ((p != p) ? -2 : __float_as_int(p)) : -1;
   }
+}
+
+template <int NQ>
+__device__ __forceinline__ void route_wave(const float (&lg)[NQ], uint32_t n_exp, uint32_t k, int norm_topk,
+                                           uint32_t lane, int32_t* my_id, float* my_w) {
+  int key[NQ];
+  route_keys<NQ>(lg, n_exp, lane, key);
   float wsum = 0.0f;
   int32_t sel_id = -1;
   float sel_p = 0.0f;
@@ -300,28 +379,8 @@ template <int NQ>
 __device__ __forceinline__ void route_wave_top8(const float (&lg)[NQ], uint32_t n_exp, int norm_topk,
                                                 uint32_t lane, int32_t* my_id, float* my_w) {
   constexpr int K = 8;
-  bool present[NQ];
-  float m = -__builtin_huge_valf();
-#pragma unroll
-  for (int j = 0; j < NQ; ++j) {
-    present[j] = lane + 64u * j < n_exp;
-    m = present[j] ? __builtin_fmaxf(m, lg[j]) : m;
-  }
-  m = wave_max_f32(m);
-  float e[NQ];
-  float a = 0.0f;
-#pragma unroll
-  for (int j = 0; j < NQ; ++j) {
-    e[j] = exp_det(present[j] ? lg[j] - m : -100.0f);
-    a = present[j] ? a + e[j] : a;
-  }
-  const float S = wave_sum_asc(a);
   int key[NQ];
-#pragma unroll
-  for (int j = 0; j < NQ; ++j) {
-    const float p = e[j] / S;
-    key[j] = present[j] ? ((p != p) ? -2 : __float_as_int(p)) : -1;
-  }
+  route_keys<NQ>(lg, n_exp, lane, key);
   // (1) T = largest value with count(key >= T) >= K (0 if fewer than K selectable)
   int T = 0;
 #pragma unroll
