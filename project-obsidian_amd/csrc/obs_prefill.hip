@@ -47,6 +47,8 @@ constexpr uint32_t TN = 128;          // tile output columns (4 waves x 32)
 constexpr uint32_t GK = 64;           // quantization group = K step of the main loop
 constexpr uint32_t LDS_STRIDE = 72;   // bf16 per staged A row (64 + 8 padding)
 constexpr uint32_t GROUP_TOKENS = 64; // tokens per grouping chunk (one wave)
+constexpr uint32_t SB_STRIDE = TN + 1;  // words per (matrix, group) row of staged scale|bias
+constexpr uint32_t SB_LDS_MAX = 96u * 1024u;  // bytes of staged scale|bias per workgroup
 
 struct GemmArgs {
   const uint16_t* A;        // bf16 [a_rows_total, K]
@@ -90,9 +92,11 @@ __device__ __forceinline__ void dequant_frags(const u32x4_t& q, float s, float b
 // MFMA sequence is straight-line code.
 template <bool SWIGLU, uint32_t NB>
 __device__ __forceinline__ void gemm_tile(const GemmArgs& a, uint16_t (&sA)[2][TM * LDS_STRIDE],
-                                          const int32_t* s_arow, uint32_t e, uint32_t row0, uint32_t nrows) {
+                                          const int32_t* s_arow, const uint32_t* s_sb, uint32_t e, uint32_t row0,
+                                          uint32_t nrows, uint32_t n0) {
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-  const uint32_t n = blockIdx.y * TN + 32u * wave + (lane & 31u);  // this lane's weight row
+  const uint32_t nl = 32u * wave + (lane & 31u);                   // this lane's column in the tile
+  const uint32_t n = n0 + nl;                                      // this lane's weight row
   const uint32_t h = lane >> 5;                                    // k half within a group
   const uint32_t K = a.K, groups = K / GK;
 
@@ -127,27 +131,19 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, uint16_t (&sA)[2][T
   // B pointers of this lane's weight row(s)
   const size_t wrow = static_cast<size_t>(e) * a.N + n;
   const u32x4_t* w0p = reinterpret_cast<const u32x4_t*>(a.w0 + wrow * (K / 8)) + h;  // + 2*g per group
-  const uint16_t* s0p = a.s0 + wrow * groups;
-  const uint16_t* b0p = a.b0 + wrow * groups;
   const u32x4_t* w1p = SWIGLU ? reinterpret_cast<const u32x4_t*>(a.w1 + wrow * (K / 8)) + h : nullptr;
-  const uint16_t* s1p = SWIGLU ? a.s1 + wrow * groups : nullptr;
-  const uint16_t* b1p = SWIGLU ? a.b1 + wrow * groups : nullptr;
+  // staged scale|bias of this lane's column: [matrix][group] at stride SB_STRIDE words
+  const uint32_t* sb0 = s_sb + nl;
+  const uint32_t* sb1 = s_sb + static_cast<size_t>(groups) * SB_STRIDE + nl;
 
   struct BRaw {
     u32x4_t q0, q1;
-    uint16_t s0, b0, s1, b1;
   };
   auto load_b = [&](uint32_t g) __attribute__((always_inline)) {
     BRaw r;
     const uint32_t gg = g < groups ? g : groups - 1u;  // clamped: the tail loads are never used
     r.q0 = w0p[2u * gg];
-    r.s0 = s0p[gg];
-    r.b0 = b0p[gg];
-    if (SWIGLU) {
-      r.q1 = w1p[2u * gg];
-      r.s1 = s1p[gg];
-      r.b1 = b1p[gg];
-    }
+    if (SWIGLU) r.q1 = w1p[2u * gg];
     return r;
   };
 
@@ -172,8 +168,12 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, uint16_t (&sA)[2][T
   bf16x8_t fa0[4], fa1[4], fb0[4], fb1[4];
   {
     const BRaw b0r = load_b(0);
-    dequant_frags(b0r.q0, bf16_to_f32(b0r.s0), bf16_to_f32(b0r.b0), fa0);
-    if (SWIGLU) dequant_frags(b0r.q1, bf16_to_f32(b0r.s1), bf16_to_f32(b0r.b1), fa1);
+    const uint32_t sv0 = sb0[0];
+    dequant_frags(b0r.q0, bf16lo(sv0), bf16hi(sv0), fa0);
+    if (SWIGLU) {
+      const uint32_t sv1 = sb1[0];
+      dequant_frags(b0r.q1, bf16lo(sv1), bf16hi(sv1), fa1);
+    }
   }
 
   // group g: B of g+4 -> bld, A of g+2 -> rld, A of g+1 (rst) -> LDS, B of g+1
@@ -194,8 +194,13 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, uint16_t (&sA)[2][T
             &sA[buf][(32u * mb + (lane & 31u)) * LDS_STRIDE + 32u * h + 8u * st]);
     }
     if (g + 1 < groups) store_a(buf ^ 1u, rst);
-    dequant_frags(bdq.q0, bf16_to_f32(bdq.s0), bf16_to_f32(bdq.b0), fn0);
-    if (SWIGLU) dequant_frags(bdq.q1, bf16_to_f32(bdq.s1), bf16_to_f32(bdq.b1), fn1);
+    const uint32_t gn = g + 1 < groups ? g + 1 : g;  // the tail dequant is never used
+    const uint32_t sv0 = sb0[gn * SB_STRIDE];
+    dequant_frags(bdq.q0, bf16lo(sv0), bf16hi(sv0), fn0);
+    if (SWIGLU) {
+      const uint32_t sv1 = sb1[gn * SB_STRIDE];
+      dequant_frags(bdq.q1, bf16lo(sv1), bf16hi(sv1), fn1);
+    }
 #pragma unroll
     for (uint32_t st = 0; st < 4; ++st) {
 #pragma unroll
@@ -228,16 +233,27 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, uint16_t (&sA)[2][T
   }
 }
 
+// Work items are (tile, 128-column block) pairs in tile order, and tiles are in
+// expert order. The dispatcher deals consecutive workgroups round-robin over
+// the 8 XCDs, so workgroup l takes item (l % 8) * chunk + l / 8: each XCD runs
+// a contiguous run of items, and the tiles of one expert share its weights (and
+// the column blocks of one tile share its activation rows) in that XCD's L2.
 template <bool SWIGLU>
 __global__ void __launch_bounds__(256, 1) grouped_gemm_kernel(GemmArgs a) {
   __shared__ uint16_t sA[2][TM * LDS_STRIDE];
   __shared__ int32_t s_arow[TM];
+  extern __shared__ uint32_t s_sb[];  // [matrix][group][SB_STRIDE]: scale | bias << 16
+  const uint32_t ncb = a.N / TN;
+  const uint32_t n_tiles = a.tiles ? static_cast<uint32_t>(*a.n_tiles) : (a.dense_rows + TM - 1) / TM;
+  const uint32_t n_items = n_tiles * ncb, chunk = (n_items + 7u) / 8u;
+  const uint32_t item = (blockIdx.x % 8u) * chunk + blockIdx.x / 8u;
+  if (blockIdx.x / 8u >= chunk || item >= n_items) return;  // uniform per workgroup
+  const uint32_t t_idx = item / ncb, n0 = (item % ncb) * TN;
   int4 tile;
   if (a.tiles) {
-    if (blockIdx.x >= static_cast<uint32_t>(*a.n_tiles)) return;  // uniform per workgroup
-    tile = a.tiles[blockIdx.x];
+    tile = a.tiles[t_idx];
   } else {
-    const uint32_t r0 = blockIdx.x * TM;
+    const uint32_t r0 = t_idx * TM;
     tile = make_int4(0, static_cast<int32_t>(r0), static_cast<int32_t>(min(TM, a.dense_rows - r0)), 0);
   }
   const uint32_t e = static_cast<uint32_t>(tile.x), row0 = static_cast<uint32_t>(tile.y);
@@ -252,12 +268,33 @@ __global__ void __launch_bounds__(256, 1) grouped_gemm_kernel(GemmArgs a) {
     }
     s_arow[tid] = r;
   }
+  // Stage the scales and biases of the tile's 128 weight rows. Rows n0.. of
+  // expert e are contiguous ([E, N, groups] bf16), so 8-byte chunks (4 groups
+  // of one row; groups % 4 == 0) load coalesced; each becomes 4 packed words.
+  {
+    const uint32_t groups = a.K / GK, cpr = groups / 4u;  // chunks per row
+    const size_t base = (static_cast<size_t>(e) * a.N + n0) * groups;
+#pragma unroll
+    for (uint32_t mat = 0; mat < (SWIGLU ? 2u : 1u); ++mat) {
+      const uint2* sp = reinterpret_cast<const uint2*>((mat ? a.s1 : a.s0) + base);
+      const uint2* bp = reinterpret_cast<const uint2*>((mat ? a.b1 : a.b0) + base);
+      for (uint32_t c = tid; c < TN * cpr; c += 256u) {
+        const uint2 sv = sp[c], bv = bp[c];
+        const uint32_t row = c / cpr, g0 = 4u * (c % cpr);
+        uint32_t* d = s_sb + (static_cast<size_t>(mat) * groups + g0) * SB_STRIDE + row;
+        d[0] = (sv.x & 0xffffu) | (bv.x << 16);
+        d[SB_STRIDE] = (sv.x >> 16) | (bv.x & 0xffff0000u);
+        d[2u * SB_STRIDE] = (sv.y & 0xffffu) | (bv.y << 16);
+        d[3u * SB_STRIDE] = (sv.y >> 16) | (bv.y & 0xffff0000u);
+      }
+    }
+  }
   __syncthreads();
   switch ((nrows + 31u) / 32u) {  // uniform per workgroup
-    case 1: gemm_tile<SWIGLU, 1>(a, sA, s_arow, e, row0, nrows); break;
-    case 2: gemm_tile<SWIGLU, 2>(a, sA, s_arow, e, row0, nrows); break;
-    case 3: gemm_tile<SWIGLU, 3>(a, sA, s_arow, e, row0, nrows); break;
-    default: gemm_tile<SWIGLU, 4>(a, sA, s_arow, e, row0, nrows); break;
+    case 1: gemm_tile<SWIGLU, 1>(a, sA, s_arow, s_sb, e, row0, nrows, n0); break;
+    case 2: gemm_tile<SWIGLU, 2>(a, sA, s_arow, s_sb, e, row0, nrows, n0); break;
+    case 3: gemm_tile<SWIGLU, 3>(a, sA, s_arow, s_sb, e, row0, nrows, n0); break;
+    default: gemm_tile<SWIGLU, 4>(a, sA, s_arow, s_sb, e, row0, nrows, n0); break;
   }
 }
 
@@ -429,12 +466,29 @@ size_t group_lds_bytes(uint32_t T, uint32_t E) {
   return sizeof(int32_t) * group_lds_ints(nchunks, E) + sizeof(uint64_t) * 16 * E;
 }
 
+// Staged scale|bias bytes per workgroup.
+size_t gemm_sb_bytes(bool swiglu, uint32_t K) {
+  return sizeof(uint32_t) * (swiglu ? 2u : 1u) * (K / GK) * SB_STRIDE;
+}
+
+// grid_tiles: an upper bound of the tile count (the device holds the exact one)
 int launch_gemm(obs_ctx* ctx, bool swiglu, const GemmArgs& a, uint32_t grid_tiles) {
-  dim3 grid(grid_tiles, a.N / TN);
+  const uint32_t items = grid_tiles * (a.N / TN);
+  const uint32_t grid = (items + 7u) / 8u * 8u;  // every XCD gets the same number of slots
+  const size_t lds = gemm_sb_bytes(swiglu, a.K);
+  // the staged scales can take the block past 64 KB of LDS (gfx950 has 160 KB)
+  static bool lds_raised = false;
+  if (!lds_raised) {
+    OBS_HIP_TRY(ctx, hipFuncSetAttribute(reinterpret_cast<const void*>(&grouped_gemm_kernel<true>),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, SB_LDS_MAX));
+    OBS_HIP_TRY(ctx, hipFuncSetAttribute(reinterpret_cast<const void*>(&grouped_gemm_kernel<false>),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, SB_LDS_MAX));
+    lds_raised = true;
+  }
   if (swiglu)
-    OBS_LAUNCH(ctx, "grouped_gemm_gateup", grouped_gemm_kernel<true><<<grid, 256, 0, ctx->stream>>>(a));
+    OBS_LAUNCH(ctx, "grouped_gemm_gateup", grouped_gemm_kernel<true><<<grid, 256, lds, ctx->stream>>>(a));
   else
-    OBS_LAUNCH(ctx, "grouped_gemm_down", grouped_gemm_kernel<false><<<grid, 256, 0, ctx->stream>>>(a));
+    OBS_LAUNCH(ctx, "grouped_gemm_down", grouped_gemm_kernel<false><<<grid, 256, lds, ctx->stream>>>(a));
   return OBS_OK;
 }
 
@@ -523,6 +577,9 @@ int obs_q4_matmul(obs_ctx* ctx, const uint32_t* w, const uint16_t* scales, const
   if (in == 0 || in % (4u * GK) != 0 || out == 0 || out % TN != 0)
     return obs::set_error(ctx, OBS_E_SHAPE, "obs_q4_matmul: in must be a multiple of %u and out of %u (got %u, %u)",
                           4u * GK, TN, in, out);
+  if (gemm_sb_bytes(false, in) > SB_LDS_MAX)
+    return obs::set_error(ctx, OBS_E_SHAPE, "obs_q4_matmul: in must be at most %u (got %u)",
+                          static_cast<uint32_t>(SB_LDS_MAX / (sizeof(uint32_t) * SB_STRIDE)) * GK, in);
   if (!obs::aligned(X, 16) || !obs::aligned(w, 16))
     return obs::set_error(ctx, OBS_E_ALIGN, "obs_q4_matmul: X and w must be 16-byte aligned");
   if (T == 0) return OBS_OK;
