@@ -64,28 +64,26 @@ struct GemmArgs {
   uint32_t K, N;
 };
 
-// 16 bytes = 32 nibbles of one weight row -> 4 bf16x8 MFMA fragments (K-steps 0..3).
-__device__ __forceinline__ void dequant_frags(const u32x4_t& q, float s, float b, bf16x8_t (&f)[4]) {
-  const uint32_t wd[4] = {q.x, q.y, q.z, q.w};
+// One 32-bit word = 8 nibbles of a weight row -> one bf16x8 MFMA fragment,
+// bf16 = RNE(fp32(q*s + b)) (q*s is exact in fp32, so one rounding).
+__device__ __forceinline__ bf16x8_t dequant_word(uint32_t w, float s, float b) {
+  uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
+  // opaque to the optimizer, so each byte converts with one v_cvt_f32_ubyteN
+  // instead of being re-derived from w with a shift and a mask
+  asm("" : "+v"(lo), "+v"(hi));
+  float v[8];
+  v[0] = __builtin_fmaf(static_cast<float>(lo & 0xffu), s, b);
+  v[1] = __builtin_fmaf(static_cast<float>(hi & 0xffu), s, b);
+  v[2] = __builtin_fmaf(static_cast<float>((lo >> 8) & 0xffu), s, b);
+  v[3] = __builtin_fmaf(static_cast<float>((hi >> 8) & 0xffu), s, b);
+  v[4] = __builtin_fmaf(static_cast<float>((lo >> 16) & 0xffu), s, b);
+  v[5] = __builtin_fmaf(static_cast<float>((hi >> 16) & 0xffu), s, b);
+  v[6] = __builtin_fmaf(static_cast<float>(lo >> 24), s, b);
+  v[7] = __builtin_fmaf(static_cast<float>(hi >> 24), s, b);
+  bf16x8_t f;
 #pragma unroll
-  for (int st = 0; st < 4; ++st) {
-    const uint32_t w = wd[st];
-    uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
-    // opaque to the optimizer, so each byte below converts with one v_cvt_f32_ubyteN
-    // instead of being re-derived from w with a shift and a mask
-    asm("" : "+v"(lo), "+v"(hi));
-    float v[8];
-    v[0] = __builtin_fmaf(static_cast<float>(lo & 0xffu), s, b);
-    v[1] = __builtin_fmaf(static_cast<float>(hi & 0xffu), s, b);
-    v[2] = __builtin_fmaf(static_cast<float>((lo >> 8) & 0xffu), s, b);
-    v[3] = __builtin_fmaf(static_cast<float>((hi >> 8) & 0xffu), s, b);
-    v[4] = __builtin_fmaf(static_cast<float>((lo >> 16) & 0xffu), s, b);
-    v[5] = __builtin_fmaf(static_cast<float>((hi >> 16) & 0xffu), s, b);
-    v[6] = __builtin_fmaf(static_cast<float>(lo >> 24), s, b);
-    v[7] = __builtin_fmaf(static_cast<float>(hi >> 24), s, b);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) f[st][j] = static_cast<__bf16>(v[j]);  // RNE
-  }
+  for (int j = 0; j < 8; ++j) f[j] = static_cast<__bf16>(v[j]);  // RNE
+  return f;
 }
 
 // One tile's main loop and epilogue, NB = active 32-row blocks (1..4), so the
@@ -103,30 +101,19 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, uint16_t (&sA)[2][T
   // A staging: thread t -> tile row t/2, 32 bf16 at column 32*(t%2) of the group
   const uint32_t ar = tid >> 1, ac = 32u * (tid & 1u);
   const int32_t arow = s_arow[ar];
-  // Padding rows (no A row) load row 0 (their values are never stored) and keep
-  // the zeros written here in both LDS buffers.
-  const bool a_ok = arow >= 0;
-  const uint16_t* aptr = a.A + static_cast<size_t>(a_ok ? arow : 0) * K + ac;
+  // Padding rows (no A row) stage row 0: row i of an MFMA product depends on
+  // row i of A only, and the epilogue discards padding rows.
+  const uint16_t* aptr = a.A + static_cast<size_t>(arow >= 0 ? arow : 0) * K + ac;
   auto load_a = [&](uint32_t g, u32x4_t (&r)[4]) __attribute__((always_inline)) {
     const u32x4_t* p = reinterpret_cast<const u32x4_t*>(aptr + g * GK);
 #pragma unroll
     for (int i = 0; i < 4; ++i) r[i] = p[i];
   };
   auto store_a = [&](uint32_t buf, const u32x4_t (&r)[4]) __attribute__((always_inline)) {
-    if (a_ok) {
-      u32x4_t* d = reinterpret_cast<u32x4_t*>(&sA[buf][ar * LDS_STRIDE + ac]);
+    u32x4_t* d = reinterpret_cast<u32x4_t*>(&sA[buf][ar * LDS_STRIDE + ac]);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) d[i] = r[i];
-    }
+    for (int i = 0; i < 4; ++i) d[i] = r[i];
   };
-  if (!a_ok) {
-#pragma unroll
-    for (uint32_t buf = 0; buf < 2; ++buf) {
-      u32x4_t* d = reinterpret_cast<u32x4_t*>(&sA[buf][ar * LDS_STRIDE + ac]);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) d[i] = u32x4_t{0u, 0u, 0u, 0u};
-    }
-  }
 
   // B pointers of this lane's weight row(s)
   const size_t wrow = static_cast<size_t>(e) * a.N + n;
@@ -154,67 +141,47 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, uint16_t (&sA)[2][T
     for (int v = 0; v < 16; ++v) { acc0[mb][v] = 0.0f; acc1[mb][v] = 0.0f; }
   }
 
-  // Pipeline: B is loaded four groups ahead into one of four register slots,
-  // A two groups ahead into one of two (then to the LDS buffer of its group);
-  // per group the A fragments are read from LDS first, the next group's B is
-  // dequantized while they arrive, then the MFMAs run back to back. The loop
-  // is unrolled by four so every slot is a fixed set of registers: rotating
-  // values between slots would make each group wait for its own prefetches.
-  BRaw bs0, bs1 = load_b(1), bs2 = load_b(2), bs3 = load_b(3);
-  u32x4_t ras0[4], ras1[4];
-  load_a(0, ras0);
-  load_a(1, ras1);
-  store_a(0, ras0);
-  bf16x8_t fa0[4], fa1[4], fb0[4], fb1[4];
-  {
-    const BRaw b0r = load_b(0);
-    const uint32_t sv0 = sb0[0];
-    dequant_frags(b0r.q0, bf16lo(sv0), bf16hi(sv0), fa0);
-    if (SWIGLU) {
-      const uint32_t sv1 = sb1[0];
-      dequant_frags(b0r.q1, bf16lo(sv1), bf16hi(sv1), fa1);
-    }
-  }
+  // Pipeline, sized for two resident waves per SIMD: B two groups ahead (two
+  // register slots), A one group ahead (registers, then the other LDS buffer).
+  // Per K-step the A fragments are read and the B fragment dequantized just
+  // before its MFMAs, so few values are live; the co-resident workgroup hides
+  // the LDS and memory latencies. Unrolled by two so each slot is a fixed set
+  // of registers.
+  BRaw bs0 = load_b(0), bs1 = load_b(1);
+  u32x4_t ras[4];
+  load_a(0, ras);
+  store_a(0, ras);
 
-  // group g: B of g+4 -> bld, A of g+2 -> rld, A of g+1 (rst) -> LDS, B of g+1
-  // (bdq) -> fragments fn, MFMAs with fragments fc
-  auto step = [&](uint32_t g, BRaw& bld, const BRaw& bdq, u32x4_t (&rld)[4], const u32x4_t (&rst)[4],
-                  const bf16x8_t (&fc0)[4], const bf16x8_t (&fc1)[4], bf16x8_t (&fn0)[4],
-                  bf16x8_t (&fn1)[4]) __attribute__((always_inline)) {
+  auto step = [&](uint32_t g, BRaw& bcur) __attribute__((always_inline)) {
     const uint32_t buf = g & 1u;
-    bld = load_b(g + 4);
-    load_a(g + 2 < groups ? g + 2 : g, rld);  // the tail reload is never stored
     __syncthreads();  // A of group g visible in sA[buf]; sA[buf^1] no longer read
-    bf16x8_t af[4][NB];
+    load_a(g + 1 < groups ? g + 1 : g, ras);  // the tail reload is stored but never read
+    const uint32_t sv0 = sb0[g * SB_STRIDE];
+    const uint32_t sv1 = SWIGLU ? sb1[g * SB_STRIDE] : 0u;
+    const uint32_t q0w[4] = {bcur.q0.x, bcur.q0.y, bcur.q0.z, bcur.q0.w};
+    const uint32_t q1w[4] = {bcur.q1.x, bcur.q1.y, bcur.q1.z, bcur.q1.w};
 #pragma unroll
     for (uint32_t st = 0; st < 4; ++st) {
+      bf16x8_t af[NB];
 #pragma unroll
       for (uint32_t mb = 0; mb < NB; ++mb)
-        af[st][mb] = *reinterpret_cast<const bf16x8_t*>(
+        af[mb] = *reinterpret_cast<const bf16x8_t*>(
             &sA[buf][(32u * mb + (lane & 31u)) * LDS_STRIDE + 32u * h + 8u * st]);
-    }
-    if (g + 1 < groups) store_a(buf ^ 1u, rst);
-    const uint32_t gn = g + 1 < groups ? g + 1 : g;  // the tail dequant is never used
-    const uint32_t sv0 = sb0[gn * SB_STRIDE];
-    dequant_frags(bdq.q0, bf16lo(sv0), bf16hi(sv0), fn0);
-    if (SWIGLU) {
-      const uint32_t sv1 = sb1[gn * SB_STRIDE];
-      dequant_frags(bdq.q1, bf16lo(sv1), bf16hi(sv1), fn1);
-    }
-#pragma unroll
-    for (uint32_t st = 0; st < 4; ++st) {
+      const bf16x8_t f0 = dequant_word(q0w[st], bf16lo(sv0), bf16hi(sv0));
+      bf16x8_t f1;
+      if (SWIGLU) f1 = dequant_word(q1w[st], bf16lo(sv1), bf16hi(sv1));
 #pragma unroll
       for (uint32_t mb = 0; mb < NB; ++mb) {
-        acc0[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[st][mb], fc0[st], acc0[mb], 0, 0, 0);
-        if (SWIGLU) acc1[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[st][mb], fc1[st], acc1[mb], 0, 0, 0);
+        acc0[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mb], f0, acc0[mb], 0, 0, 0);
+        if (SWIGLU) acc1[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mb], f1, acc1[mb], 0, 0, 0);
       }
     }
+    bcur = load_b(g + 2);    // clamped past the end; never used there
+    store_a(buf ^ 1u, ras);  // read after the next barrier
   };
-  for (uint32_t g = 0; g < groups; g += 4) {  // groups % 4 == 0 (K % 256 == 0, checked by the host)
-    step(g, bs0, bs1, ras0, ras1, fa0, fa1, fb0, fb1);
-    step(g + 1, bs1, bs2, ras1, ras0, fb0, fb1, fa0, fa1);
-    step(g + 2, bs2, bs3, ras0, ras1, fa0, fa1, fb0, fb1);
-    step(g + 3, bs3, bs0, ras1, ras0, fb0, fb1, fa0, fa1);
+  for (uint32_t g = 0; g < groups; g += 2) {  // groups % 4 == 0 (K % 256 == 0, checked by the host)
+    step(g, bs0);
+    step(g + 1, bs1);
   }
 
   // epilogue: lane holds C[i][n] for i = 32mb + 8(v/4) + 4h + v%4
@@ -238,8 +205,10 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, uint16_t (&sA)[2][T
 // the 8 XCDs, so workgroup l takes item (l % 8) * chunk + l / 8: each XCD runs
 // a contiguous run of items, and the tiles of one expert share its weights (and
 // the column blocks of one tile share its activation rows) in that XCD's L2.
+// Two workgroups per CU (at most 256 registers per lane): the co-resident
+// workgroup hides each one's load, LDS and barrier latency.
 template <bool SWIGLU>
-__global__ void __launch_bounds__(256, 1) grouped_gemm_kernel(GemmArgs a) {
+__global__ void __launch_bounds__(256, 2) grouped_gemm_kernel(GemmArgs a) {
   __shared__ uint16_t sA[2][TM * LDS_STRIDE];
   __shared__ int32_t s_arow[TM];
   extern __shared__ uint32_t s_sb[];  // [matrix][group][SB_STRIDE]: scale | bias << 16
