@@ -4,9 +4,10 @@
 // Pipeline for T tokens (all on the GPU, no host round trip):
 //   1. routing: computed (gate logits + top-k kernels) or injected;
 //   2. grouping: rows of expert e are the tokens routed to e in ascending
-//      token order (forward.rs:203-204); one workgroup counts per 64-token
-//      chunk, scans, and ranks tokens inside a chunk with LDS lane bitmasks;
-//      it also emits the tile list (expert, first row, rows <= 128);
+//      token order (forward.rs:203-204); one wave per 64-token chunk counts,
+//      one workgroup scans the counts into row bases and emits the tile list
+//      (expert, first row, rows <= 128), then one wave per chunk ranks its
+//      tokens with LDS lane bitmasks and scatters the row maps;
 //   3. gate/up grouped GEMM with a SwiGLU epilogue -> H [T*k, I] bf16;
 //   4. down grouped GEMM -> Yp, written at the token-major slot t*k + r;
 //   5. combine: y[t] = residual[t] + sum_r w[t,r] * Yp[t*k+r], fp32, rank order
@@ -19,7 +20,8 @@
 //     double-buffered, row stride padded to 72 bf16;
 //   - B is read straight from HBM into registers: lane l takes 16 bytes
 //     (32 nibbles) of weight row n = n0 + 32w + l%32, columns
-//     [k0 + 32(l/32), +32), and dequantizes them to bf16 = RNE(q*s + b);
+//     [k0 + 32(l/32), +32), and dequantizes them to bf16 = RNE(q*s + b) with
+//     the tile's scales and biases, staged once per tile in LDS;
 //   - v_mfma_f32_32x32x16_bf16 accumulates in fp32. The MFMA's 16 k-slots of
 //     K-step s map to columns k0 + 32h + 8s + j (h = lane half, j = 0..7), for
 //     A and B alike, so each lane's 16-byte load feeds all four K-steps.
@@ -267,104 +269,130 @@ __global__ void __launch_bounds__(256, 2) grouped_gemm_kernel(GemmArgs a) {
   }
 }
 
-// int32 slots before the 8-byte-aligned bitmask area of the grouping kernel's LDS
-__host__ __device__ constexpr size_t group_lds_ints(uint32_t nchunks, uint32_t E) {
-  return (static_cast<size_t>(nchunks) * E + 3u * E + 2u + 1u) & ~size_t(1);
+// ---- grouping: rows of expert e are its routed (token, rank) pairs in
+// ascending token order (forward.rs:203-204). Three launches: per 64-token
+// chunk counts, one scan, per chunk ranks + scatter.
+
+// A token's k (<= 8) ids in registers, -1 where invalid: out of range or a
+// repeat of an earlier rank of the same token.
+__device__ __forceinline__ void load_token_ids(const int32_t* __restrict__ ids, uint32_t t, uint32_t T, uint32_t k,
+                                               uint32_t E, int32_t (&ev)[8]) {
+#pragma unroll
+  for (uint32_t r = 0; r < 8; ++r) ev[r] = (t < T && r < k) ? ids[static_cast<size_t>(t) * k + r] : -1;
+#pragma unroll
+  for (uint32_t r = 0; r < 8; ++r) {
+    bool ok = ev[r] >= 0 && static_cast<uint32_t>(ev[r]) < E;
+#pragma unroll
+    for (uint32_t q = 0; q < r; ++q) ok = ok && ev[q] != ev[r];
+    ev[r] = ok ? ev[r] : -1;
+  }
 }
 
-// Grouping (one workgroup of 1024 threads). LDS: cnt[nchunks][E] ints, bits[16 waves][E] u64.
-__global__ void __launch_bounds__(1024) group_kernel(const int32_t* __restrict__ ids, uint32_t T, uint32_t k,
-                                                     uint32_t E, int32_t* counts, int32_t* offsets,
-                                                     int32_t* row_token, int32_t* row_slot, int4* tiles,
-                                                     int32_t* n_tiles) {
-  extern __shared__ int32_t sm[];
-  const uint32_t nchunks = (T + GROUP_TOKENS - 1) / GROUP_TOKENS;
-  int32_t* cnt = sm;                                        // [nchunks][E]
-  int32_t* tot = cnt + nchunks * E;                         // [E]
-  int32_t* off = tot + E;                                   // [E + 1]
-  int32_t* toff = off + E + 1;                              // [E + 1] tile offsets
-  unsigned long long* bits = reinterpret_cast<unsigned long long*>(sm + group_lds_ints(nchunks, E));  // [16][E]
-  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6, nwaves = blockDim.x / 64u;
+// 1. one wave per chunk: chunk_cnt[c][e] = rows of expert e among the chunk's tokens
+__global__ void __launch_bounds__(64) group_count_kernel(const int32_t* __restrict__ ids, uint32_t T, uint32_t k,
+                                                         uint32_t E, int32_t* __restrict__ chunk_cnt) {
+  __shared__ int32_t hist[256];
+  const uint32_t lane = threadIdx.x, c = blockIdx.x;
+  for (uint32_t e = lane; e < E; e += 64u) hist[e] = 0;
+  __syncthreads();
+  int32_t ev[8];
+  load_token_ids(ids, c * GROUP_TOKENS + lane, T, k, E, ev);
+#pragma unroll
+  for (uint32_t r = 0; r < 8; ++r)
+    if (ev[r] >= 0) atomicAdd(&hist[ev[r]], 1);
+  __syncthreads();
+  for (uint32_t e = lane; e < E; e += 64u) chunk_cnt[static_cast<size_t>(c) * E + e] = hist[e];
+}
 
-  for (uint32_t i = tid; i < nchunks * E; i += blockDim.x) cnt[i] = 0;
+// Exclusive prefix sum over one workgroup of 256 threads (v per thread).
+__device__ __forceinline__ int32_t block_exclusive_scan256(int32_t v, int32_t* s_wave, int32_t* total) {
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  int32_t x = v;
+#pragma unroll
+  for (uint32_t d = 1; d < 64; d <<= 1) {
+    const int32_t y = __shfl_up(x, d, 64);
+    if (lane >= d) x += y;
+  }
+  if (lane == 63u) s_wave[wave] = x;
   __syncthreads();
-  // A token's k (<= 8) ids in registers, -1 where invalid: out of range or a
-  // repeat of an earlier rank of the same token.
-  auto load_ids = [&](uint32_t t, int32_t (&ev)[8]) {
+  int32_t before = 0;
+  for (uint32_t w = 0; w < wave; ++w) before += s_wave[w];
+  *total = s_wave[0] + s_wave[1] + s_wave[2] + s_wave[3];
+  __syncthreads();
+  return before + x - v;
+}
+
+// 2. one workgroup (thread e = expert e, E <= 256): chunk counts -> absolute row
+// bases per (chunk, expert), expert offsets and counts, the tile list.
+__global__ void __launch_bounds__(256) group_scan_kernel(uint32_t nchunks, uint32_t E, int32_t* __restrict__ chunk_cnt,
+                                                         int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
+                                                         int4* __restrict__ tiles, int32_t* __restrict__ n_tiles) {
+  __shared__ int32_t s_wave[4];
+  const uint32_t e = threadIdx.x;
+  const bool have = e < E;
+  int32_t tot = 0;
+  if (have) {  // chunk-exclusive prefix per expert, in place
+    for (uint32_t c0 = 0; c0 < nchunks; c0 += 16u) {
+      int32_t v[16];
 #pragma unroll
-    for (uint32_t r = 0; r < 8; ++r) ev[r] = (t < T && r < k) ? ids[static_cast<size_t>(t) * k + r] : -1;
+      for (uint32_t i = 0; i < 16; ++i) v[i] = c0 + i < nchunks ? chunk_cnt[static_cast<size_t>(c0 + i) * E + e] : 0;
 #pragma unroll
-    for (uint32_t r = 0; r < 8; ++r) {
-      bool ok = ev[r] >= 0 && static_cast<uint32_t>(ev[r]) < E;
-#pragma unroll
-      for (uint32_t q = 0; q < r; ++q) ok = ok && ev[q] != ev[r];
-      ev[r] = ok ? ev[r] : -1;
+      for (uint32_t i = 0; i < 16; ++i) {
+        if (c0 + i < nchunks) chunk_cnt[static_cast<size_t>(c0 + i) * E + e] = tot;
+        tot += v[i];
+      }
     }
-  };
-  for (uint32_t c = wave; c < nchunks; c += nwaves) {
-    int32_t ev[8];
-    load_ids(c * GROUP_TOKENS + lane, ev);
-#pragma unroll
-    for (uint32_t r = 0; r < 8; ++r)
-      if (ev[r] >= 0) atomicAdd(&cnt[c * E + static_cast<uint32_t>(ev[r])], 1);
   }
-  __syncthreads();
-  for (uint32_t e = tid; e < E; e += blockDim.x) {
-    int32_t run = 0;
-    for (uint32_t c = 0; c < nchunks; ++c) {
-      const int32_t v = cnt[c * E + e];
-      cnt[c * E + e] = run;
-      run += v;
-    }
-    tot[e] = run;
-  }
-  __syncthreads();
-  if (tid == 0) {
-    int32_t o = 0, to = 0;
-    for (uint32_t e = 0; e < E; ++e) {
-      off[e] = o;
-      toff[e] = to;
-      o += tot[e];
-      to += (tot[e] + static_cast<int32_t>(TM) - 1) / static_cast<int32_t>(TM);
-    }
-    off[E] = o;
-    toff[E] = to;
-    *n_tiles = to;
-  }
-  __syncthreads();
-  for (uint32_t e = tid; e <= E; e += blockDim.x) {
-    offsets[e] = off[e];
-    if (e < E) counts[e] = tot[e];
-  }
-  for (uint32_t e = tid; e < E; e += blockDim.x) {
-    const int32_t nt = toff[e + 1] - toff[e];
+  int32_t all_rows, all_tiles;
+  const int32_t nt = (tot + static_cast<int32_t>(TM) - 1) / static_cast<int32_t>(TM);
+  const int32_t off = block_exclusive_scan256(tot, s_wave, &all_rows);
+  const int32_t toff = block_exclusive_scan256(nt, s_wave, &all_tiles);
+  if (have) {
+    counts[e] = tot;
+    offsets[e] = off;
     for (int32_t q = 0; q < nt; ++q) {
       const int32_t r0 = q * static_cast<int32_t>(TM);
-      tiles[toff[e] + q] = make_int4(static_cast<int32_t>(e), off[e] + r0, min(static_cast<int32_t>(TM), tot[e] - r0), 0);
+      tiles[toff + q] = make_int4(static_cast<int32_t>(e), off + r0, min(static_cast<int32_t>(TM), tot - r0), 0);
+    }
+    for (uint32_t c0 = 0; c0 < nchunks; c0 += 16u) {  // batched: all loads in flight together
+      int32_t v[16];
+#pragma unroll
+      for (uint32_t i = 0; i < 16; ++i) v[i] = c0 + i < nchunks ? chunk_cnt[static_cast<size_t>(c0 + i) * E + e] : 0;
+#pragma unroll
+      for (uint32_t i = 0; i < 16; ++i)
+        if (c0 + i < nchunks) chunk_cnt[static_cast<size_t>(c0 + i) * E + e] = v[i] + off;
     }
   }
-  // rank inside a chunk: lanes (tokens) below me routed to the same expert
-  unsigned long long* wb = bits + static_cast<size_t>(wave) * E;
+  if (e == 0) {
+    offsets[E] = all_rows;
+    *n_tiles = all_tiles;
+  }
+}
+
+// 3. one wave per chunk: a token's row in expert e = chunk base + the number of
+// lower lanes (earlier tokens) of the chunk routed to e (LDS lane bitmasks).
+__global__ void __launch_bounds__(64) group_rank_kernel(const int32_t* __restrict__ ids, uint32_t T, uint32_t k,
+                                                        uint32_t E, const int32_t* __restrict__ chunk_base,
+                                                        int32_t* __restrict__ row_token, int32_t* __restrict__ row_slot) {
+  __shared__ unsigned long long wb[256];
+  const uint32_t lane = threadIdx.x, c = blockIdx.x, t = c * GROUP_TOKENS + lane;
+  for (uint32_t e = lane; e < E; e += 64u) wb[e] = 0ull;
+  __syncthreads();
+  int32_t ev[8];
+  load_token_ids(ids, t, T, k, E, ev);
+#pragma unroll
+  for (uint32_t r = 0; r < 8; ++r)
+    if (ev[r] >= 0) atomicOr(&wb[ev[r]], 1ull << lane);
+  __syncthreads();
   const unsigned long long lt = (1ull << lane) - 1ull;
-  for (uint32_t c = wave; c < nchunks; c += nwaves) {
-    const uint32_t t = c * GROUP_TOKENS + lane;
-    int32_t ev[8];
-    load_ids(t, ev);
-    for (uint32_t e = lane; e < E; e += 64u) wb[e] = 0ull;
-    __builtin_amdgcn_wave_barrier();
+  const int32_t* base = chunk_base + static_cast<size_t>(c) * E;
 #pragma unroll
-    for (uint32_t r = 0; r < 8; ++r)
-      if (ev[r] >= 0) atomicOr(&wb[ev[r]], 1ull << lane);
-    __builtin_amdgcn_wave_barrier();
-#pragma unroll
-    for (uint32_t r = 0; r < 8; ++r) {
-      if (ev[r] < 0) continue;
-      const uint32_t e = static_cast<uint32_t>(ev[r]);
-      const int32_t row = off[e] + cnt[c * E + e] + __popcll(wb[e] & lt);
-      row_token[row] = static_cast<int32_t>(t);
-      row_slot[row] = static_cast<int32_t>(t * k + r);
-    }
-    __builtin_amdgcn_wave_barrier();
+  for (uint32_t r = 0; r < 8; ++r) {
+    if (ev[r] < 0) continue;
+    const uint32_t e = static_cast<uint32_t>(ev[r]);
+    const int32_t row = base[e] + __popcll(wb[e] & lt);
+    row_token[row] = static_cast<int32_t>(t);
+    row_slot[row] = static_cast<int32_t>(t * k + r);
   }
 }
 
@@ -406,8 +434,8 @@ __global__ void __launch_bounds__(256) combine_kernel(const uint16_t* __restrict
 constexpr size_t al256(size_t v) { return (v + 255) & ~size_t(255); }
 
 struct PrefillWs {
-  size_t logits, ids, w, counts, offsets, ntiles, row_token, row_slot, tiles, H, Yp, total;
-  uint32_t max_tiles;
+  size_t logits, ids, w, counts, offsets, ntiles, chunk_cnt, row_token, row_slot, tiles, H, Yp, total;
+  uint32_t max_tiles, nchunks;
 };
 
 PrefillWs prefill_layout(const obs_moe_config* cfg, uint32_t T) {
@@ -421,6 +449,8 @@ PrefillWs prefill_layout(const obs_moe_config* cfg, uint32_t T) {
   L.counts = o; o += al256(sizeof(int32_t) * cfg->n_exp);
   L.offsets = o; o += al256(sizeof(int32_t) * (cfg->n_exp + 1));
   L.ntiles = o; o += 256;
+  L.nchunks = (T + GROUP_TOKENS - 1) / GROUP_TOKENS;
+  L.chunk_cnt = o; o += al256(sizeof(int32_t) * L.nchunks * cfg->n_exp);
   L.row_token = o; o += al256(sizeof(int32_t) * R);
   L.row_slot = o; o += al256(sizeof(int32_t) * R);
   L.tiles = o; o += al256(sizeof(int4) * L.max_tiles);
@@ -428,11 +458,6 @@ PrefillWs prefill_layout(const obs_moe_config* cfg, uint32_t T) {
   L.Yp = o; o += al256(sizeof(uint16_t) * R * cfg->hidden);
   L.total = o;
   return L;
-}
-
-size_t group_lds_bytes(uint32_t T, uint32_t E) {
-  const uint32_t nchunks = (T + GROUP_TOKENS - 1) / GROUP_TOKENS;
-  return sizeof(int32_t) * group_lds_ints(nchunks, E) + sizeof(uint64_t) * 16 * E;
 }
 
 // Staged scale|bias bytes per workgroup.
@@ -488,9 +513,6 @@ int obs_moe_prefill(obs_ctx* ctx, const obs_moe_config* cfg, const obs_moe_layer
   const PrefillWs L = prefill_layout(cfg, T);
   if (ws_bytes < L.total)
     return obs::set_error(ctx, OBS_E_NOMEM, "obs_moe_prefill: workspace %zu bytes < %zu needed", ws_bytes, L.total);
-  const size_t lds = group_lds_bytes(T, E);
-  if (lds > 64 * 1024)
-    return obs::set_error(ctx, OBS_E_SHAPE, "obs_moe_prefill: T=%u with %u experts exceeds one grouping pass", T, E);
   if (!obs::aligned(X, 16) || !obs::aligned(Y, 16) || (residual && !obs::aligned(residual, 16)) || !obs::aligned(ws, 256))
     return obs::set_error(ctx, OBS_E_ALIGN, "obs_moe_prefill: X/Y/residual need 16-byte, ws 256-byte alignment");
   char* base = static_cast<char*>(ws);
@@ -513,8 +535,12 @@ int obs_moe_prefill(obs_ctx* ctx, const obs_moe_config* cfg, const obs_moe_layer
   int4* tiles = reinterpret_cast<int4*>(base + L.tiles);
   uint16_t* Hbuf = reinterpret_cast<uint16_t*>(base + L.H);
   uint16_t* Yp = reinterpret_cast<uint16_t*>(base + L.Yp);
-  OBS_LAUNCH(ctx, "moe_group", group_kernel<<<1, 1024, lds, ctx->stream>>>(ids, T, k, E, counts, offsets, row_token,
-                                                                               row_slot, tiles, ntiles));
+  int32_t* chunk_cnt = reinterpret_cast<int32_t*>(base + L.chunk_cnt);
+  OBS_LAUNCH(ctx, "moe_group_count", group_count_kernel<<<L.nchunks, 64, 0, ctx->stream>>>(ids, T, k, E, chunk_cnt));
+  OBS_LAUNCH(ctx, "moe_group_scan", group_scan_kernel<<<1, 256, 0, ctx->stream>>>(L.nchunks, E, chunk_cnt, counts,
+                                                                                   offsets, tiles, ntiles));
+  OBS_LAUNCH(ctx, "moe_group_rank", group_rank_kernel<<<L.nchunks, 64, 0, ctx->stream>>>(ids, T, k, E, chunk_cnt,
+                                                                                          row_token, row_slot));
   GemmArgs g{};
   g.A = X; g.a_rows = row_token; g.a_rows_total = T;
   g.w0 = layer->gate_w; g.s0 = layer->gate_s; g.b0 = layer->gate_b;
