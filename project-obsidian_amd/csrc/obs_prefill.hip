@@ -92,7 +92,8 @@ __device__ __forceinline__ bf16x8_t dequant_word(uint32_t w, float s, float b) {
 // MFMA sequence is straight-line code.
 template <bool SWIGLU, uint32_t NB>
 __device__ __forceinline__ void gemm_tile(const GemmArgs& a, uint16_t (&sA)[2][TM * LDS_STRIDE],
-                                          const int32_t* s_arow, const uint32_t* s_sb, uint32_t e, uint32_t row0,
+                                          const int32_t* s_arow, const int32_t* s_orow, const uint32_t* s_sb,
+                                          uint32_t e, uint32_t row0,
                                           uint32_t nrows, uint32_t n0) {
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   const uint32_t nl = 32u * wave + (lane & 31u);                   // this lane's column in the tile
@@ -186,18 +187,29 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, uint16_t (&sA)[2][T
     step(g + 1, bs1);
   }
 
-  // epilogue: lane holds C[i][n] for i = 32mb + 8(v/4) + 4h + v%4
+  // Epilogue: lane holds C[i][nl] for i = 32mb + 8(v/4) + 4h + v%4. The tile
+  // goes through LDS (the A buffers are free now) so each output row leaves as
+  // sixteen coalesced 16-byte stores instead of 128 scattered 2-byte ones.
+  constexpr uint32_t C_STRIDE = TN + 8;  // bf16 per staged row (bank spread)
+  static_assert(TM * C_STRIDE <= 2 * TM * LDS_STRIDE, "C tile must fit the A buffers");
+  uint16_t* sC = reinterpret_cast<uint16_t*>(sA);
+  __syncthreads();  // every wave is done reading sA
 #pragma unroll
   for (uint32_t mb = 0; mb < NB; ++mb) {
 #pragma unroll
     for (uint32_t v = 0; v < 16; ++v) {
       const uint32_t i = 32u * mb + 8u * (v / 4u) + 4u * h + (v % 4u);
-      if (i < nrows) {
-        const float val = SWIGLU ? silu_mul(acc0[mb][v], acc1[mb][v]) : acc0[mb][v];
-        const uint32_t p = row0 + i;
-        const size_t orow = a.out_rows ? static_cast<size_t>(a.out_rows[p]) : p;
-        a.out[orow * a.N + n] = f32_to_bf16(val);
-      }
+      const float val = SWIGLU ? silu_mul(acc0[mb][v], acc1[mb][v]) : acc0[mb][v];
+      sC[i * C_STRIDE + nl] = f32_to_bf16(val);
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (uint32_t q = 0; q < TM * TN / 8u / 256u; ++q) {
+    const uint32_t chunk = tid + 256u * q, i = chunk / (TN / 8u), c8 = 8u * (chunk % (TN / 8u));
+    if (i < nrows) {
+      const uint4 v = *reinterpret_cast<const uint4*>(&sC[i * C_STRIDE + c8]);
+      *reinterpret_cast<uint4*>(a.out + static_cast<size_t>(s_orow[i]) * a.N + n0 + c8) = v;
     }
   }
 }
@@ -212,7 +224,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, uint16_t (&sA)[2][T
 template <bool SWIGLU>
 __global__ void __launch_bounds__(256, 2) grouped_gemm_kernel(GemmArgs a) {
   __shared__ uint16_t sA[2][TM * LDS_STRIDE];
-  __shared__ int32_t s_arow[TM];
+  __shared__ int32_t s_arow[TM], s_orow[TM];
   extern __shared__ uint32_t s_sb[];  // [matrix][group][SB_STRIDE]: scale | bias << 16
   const uint32_t ncb = a.N / TN;
   const uint32_t n_tiles = a.tiles ? static_cast<uint32_t>(*a.n_tiles) : (a.dense_rows + TM - 1) / TM;
@@ -238,6 +250,10 @@ __global__ void __launch_bounds__(256, 2) grouped_gemm_kernel(GemmArgs a) {
       if (r < 0 || static_cast<uint32_t>(r) >= a.a_rows_total) r = -1;
     }
     s_arow[tid] = r;
+    if (tid < nrows) {
+      const uint32_t p = row0 + tid;
+      s_orow[tid] = a.out_rows ? a.out_rows[p] : static_cast<int32_t>(p);
+    }
   }
   // Stage the scales and biases of the tile's 128 weight rows. Rows n0.. of
   // expert e are contiguous ([E, N, groups] bf16), so 8-byte chunks (4 groups
@@ -262,10 +278,10 @@ __global__ void __launch_bounds__(256, 2) grouped_gemm_kernel(GemmArgs a) {
   }
   __syncthreads();
   switch ((nrows + 31u) / 32u) {  // uniform per workgroup
-    case 1: gemm_tile<SWIGLU, 1>(a, sA, s_arow, s_sb, e, row0, nrows, n0); break;
-    case 2: gemm_tile<SWIGLU, 2>(a, sA, s_arow, s_sb, e, row0, nrows, n0); break;
-    case 3: gemm_tile<SWIGLU, 3>(a, sA, s_arow, s_sb, e, row0, nrows, n0); break;
-    default: gemm_tile<SWIGLU, 4>(a, sA, s_arow, s_sb, e, row0, nrows, n0); break;
+    case 1: gemm_tile<SWIGLU, 1>(a, sA, s_arow, s_orow, s_sb, e, row0, nrows, n0); break;
+    case 2: gemm_tile<SWIGLU, 2>(a, sA, s_arow, s_orow, s_sb, e, row0, nrows, n0); break;
+    case 3: gemm_tile<SWIGLU, 3>(a, sA, s_arow, s_orow, s_sb, e, row0, nrows, n0); break;
+    default: gemm_tile<SWIGLU, 4>(a, sA, s_arow, s_orow, s_sb, e, row0, nrows, n0); break;
   }
 }
 
@@ -575,8 +591,8 @@ int obs_q4_matmul(obs_ctx* ctx, const uint32_t* w, const uint16_t* scales, const
   if (gemm_sb_bytes(false, in) > SB_LDS_MAX)
     return obs::set_error(ctx, OBS_E_SHAPE, "obs_q4_matmul: in must be at most %u (got %u)",
                           static_cast<uint32_t>(SB_LDS_MAX / (sizeof(uint32_t) * SB_STRIDE)) * GK, in);
-  if (!obs::aligned(X, 16) || !obs::aligned(w, 16))
-    return obs::set_error(ctx, OBS_E_ALIGN, "obs_q4_matmul: X and w must be 16-byte aligned");
+  if (!obs::aligned(X, 16) || !obs::aligned(w, 16) || !obs::aligned(Y, 16))
+    return obs::set_error(ctx, OBS_E_ALIGN, "obs_q4_matmul: X, w and Y must be 16-byte aligned");
   if (T == 0) return OBS_OK;
   const uint32_t tiles = (T + TM - 1) / TM;
   GemmArgs g{};
