@@ -107,15 +107,23 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, uint16_t (&sA)[2][T
   // Padding rows (no A row) stage row 0: row i of an MFMA product depends on
   // row i of A only, and the epilogue discards padding rows.
   const uint16_t* aptr = a.A + static_cast<size_t>(arow >= 0 ? arow : 0) * K + ac;
+  // Rows at or past 32 * NB are never read by the MFMAs: in the down kernel the
+  // waves that would stage them (wave >= NB, uniform) skip it. (Measured: the
+  // gate/up kernel is faster staging every row, its loop stays one block.)
+  const bool a_stage = SWIGLU || NB == 4 || ar < 32u * NB;
   auto load_a = [&](uint32_t g, u32x4_t (&r)[4]) __attribute__((always_inline)) {
-    const u32x4_t* p = reinterpret_cast<const u32x4_t*>(aptr + g * GK);
+    if (a_stage) {
+      const u32x4_t* p = reinterpret_cast<const u32x4_t*>(aptr + g * GK);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) r[i] = p[i];
+      for (int i = 0; i < 4; ++i) r[i] = p[i];
+    }
   };
   auto store_a = [&](uint32_t buf, const u32x4_t (&r)[4]) __attribute__((always_inline)) {
-    u32x4_t* d = reinterpret_cast<u32x4_t*>(&sA[buf][ar * LDS_STRIDE + ac]);
+    if (a_stage) {
+      u32x4_t* d = reinterpret_cast<u32x4_t*>(&sA[buf][ar * LDS_STRIDE + ac]);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) d[i] = r[i];
+      for (int i = 0; i < 4; ++i) d[i] = r[i];
+    }
   };
 
   // B pointers of this lane's weight row(s)
