@@ -420,15 +420,13 @@ __global__ void __launch_bounds__(64) group_rank_kernel(const int32_t* __restric
   }
 }
 
-// y[t, :] = residual + sum_r w[t, r] * Yp[t*k + r, :] (fp32, rank order), 8 columns per thread.
-__global__ void __launch_bounds__(256) combine_kernel(const uint16_t* __restrict__ Yp, const int32_t* __restrict__ ids,
+// y[t, :] = residual + sum_r w[t, r] * Yp[t*k + r, :] (fp32, rank order). One
+// workgroup per token (H / 8 threads, 8 columns each): the token's ids and
+// weights are uniform, so they load once into scalar registers.
+__global__ void __launch_bounds__(512) combine_kernel(const uint16_t* __restrict__ Yp, const int32_t* __restrict__ ids,
                                                       const float* __restrict__ w, const uint16_t* __restrict__ residual,
-                                                      uint16_t* __restrict__ y, uint32_t T, uint32_t k, uint32_t H,
-                                                      uint32_t E) {
-  const uint32_t per_tok = H / 8u;
-  const uint64_t idx = static_cast<uint64_t>(blockIdx.x) * 256u + threadIdx.x;
-  if (idx >= static_cast<uint64_t>(T) * per_tok) return;
-  const uint32_t t = static_cast<uint32_t>(idx / per_tok), c = 8u * static_cast<uint32_t>(idx % per_tok);
+                                                      uint16_t* __restrict__ y, uint32_t k, uint32_t H, uint32_t E) {
+  const uint32_t t = blockIdx.x, c = 8u * threadIdx.x;
   float acc[8];
   if (residual) {
     const uint4 rv = *reinterpret_cast<const uint4*>(residual + static_cast<size_t>(t) * H + c);
@@ -438,11 +436,12 @@ __global__ void __launch_bounds__(256) combine_kernel(const uint16_t* __restrict
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
   }
+  const int32_t* tid_ids = ids + static_cast<size_t>(t) * k;
   for (uint32_t r = 0; r < k; ++r) {
-    const int32_t e = ids[static_cast<size_t>(t) * k + r];
-    bool dup = false;
-    for (uint32_t q = 0; q < r; ++q) dup = dup || ids[static_cast<size_t>(t) * k + q] == e;
-    if (e < 0 || static_cast<uint32_t>(e) >= E || dup) continue;  // rows the grouping skipped
+    const int32_t e = tid_ids[r];
+    bool skip = e < 0 || static_cast<uint32_t>(e) >= E;  // rows the grouping skipped
+    for (uint32_t q = 0; q < r; ++q) skip = skip || tid_ids[q] == e;
+    if (skip) continue;
     const float wr = w[static_cast<size_t>(t) * k + r];
     const uint4 v = *reinterpret_cast<const uint4*>(Yp + (static_cast<size_t>(t) * k + r) * H + c);
     acc[0] = __builtin_fmaf(wr, bf16lo(v.x), acc[0]); acc[1] = __builtin_fmaf(wr, bf16hi(v.x), acc[1]);
@@ -582,9 +581,7 @@ int obs_moe_prefill(obs_ctx* ctx, const obs_moe_config* cfg, const obs_moe_layer
   d.K = I; d.N = H;
   rc = launch_gemm(ctx, false, d, L.max_tiles);
   if (rc) return rc;
-  const uint64_t nthreads = static_cast<uint64_t>(T) * (H / 8u);
-  OBS_LAUNCH(ctx, "moe_combine", combine_kernel<<<static_cast<uint32_t>((nthreads + 255) / 256), 256, 0, ctx->stream>>>(
-                                     Yp, ids, weights, residual, Y, T, k, H, E));
+  OBS_LAUNCH(ctx, "moe_combine", combine_kernel<<<T, H / 8u, 0, ctx->stream>>>(Yp, ids, weights, residual, Y, k, H, E));
   return OBS_OK;
 }
 
