@@ -66,8 +66,66 @@ struct GemmArgs {
   uint32_t K, N;
 };
 
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// Two fp32 values -> one packed bf16 pair (RNE, v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t pack_bf16_rne(float lo, float hi) {
+  const f32x2_t f = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2_t));
+}
+
+// fp32 fma(h, s, b) where h is the low (HI = 0) or high (HI = 1) f16 half of v
+// (v_fma_mix_f32: the f16 operand converts exactly to fp32 inside the fma).
+template <int HI>
+__device__ __forceinline__ float fma_mix_f16(uint32_t v, float s, float b) {
+  float r;
+  if (HI)
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(v), "v"(s), "v"(b));
+  else
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(v), "v"(s), "v"(b));
+  return r;
+}
+
+// Scale operands of dequant_word_mix for one (row, group): s * 2^24, s * 2^20.
+struct MixScale {
+  float s24, s20, b;
+};
+__device__ __forceinline__ MixScale mix_scale(uint32_t packed_sb) {
+  const float s = bf16lo(packed_sb);
+  return MixScale{s * 0x1p24f, s * 0x1p20f, bf16hi(packed_sb)};
+}
+
 // One 32-bit word = 8 nibbles of a weight row -> one bf16x8 MFMA fragment,
-// bf16 = RNE(fp32(q*s + b)) (q*s is exact in fp32, so one rounding).
+// bf16 = RNE(fp32(q*s + b)), with 17 VALU instructions. A nibble masked in
+// place at bits 3:0 (or 7:4) of a 16-bit half is the f16 subnormal q * 2^-24
+// (or q * 2^-20), exactly; fma_mix multiplies it by s * 2^24 (or s * 2^20),
+// which is exact (a power-of-two scaling of the bf16 s, then a 4 x 8-bit
+// significand product), and adds b with the single fp32 rounding of
+// fmaf(q, s, b). Valid for |s| <= 2^100 (so s * 2^24 cannot overflow); tiles
+// holding larger scales use dequant_word. Checked bit for bit against
+// fmaf(q, s, b) for every finite bf16 s in that range, on the target GPU.
+__device__ __forceinline__ bf16x8_t dequant_word_mix(uint32_t w, const MixScale& m) {
+  const uint32_t w8 = w >> 8;
+  const uint32_t p04 = w & 0x000F000Fu;   // (q0, q4) * 2^-24
+  const uint32_t p15 = w & 0x00F000F0u;   // (q1, q5) * 2^-20
+  const uint32_t p26 = w8 & 0x000F000Fu;  // (q2, q6) * 2^-24
+  const uint32_t p37 = w8 & 0x00F000F0u;  // (q3, q7) * 2^-20
+  u32x4_t r;
+  r.x = pack_bf16_rne(fma_mix_f16<0>(p04, m.s24, m.b), fma_mix_f16<0>(p15, m.s20, m.b));
+  r.y = pack_bf16_rne(fma_mix_f16<0>(p26, m.s24, m.b), fma_mix_f16<0>(p37, m.s20, m.b));
+  r.z = pack_bf16_rne(fma_mix_f16<1>(p04, m.s24, m.b), fma_mix_f16<1>(p15, m.s20, m.b));
+  r.w = pack_bf16_rne(fma_mix_f16<1>(p26, m.s24, m.b), fma_mix_f16<1>(p37, m.s20, m.b));
+  return __builtin_bit_cast(bf16x8_t, r);
+}
+
+// A staged scale|bias word whose scale is beyond dequant_word_mix's range
+// (|s| > 2^100, inf, NaN): bf16 exponent field above 127 + 100.
+__device__ __forceinline__ bool scale_out_of_mix_range(uint32_t packed_sb) {
+  return (packed_sb & 0x7f80u) > (227u << 7);
+}
+
+// Reference-form dequant of one word (convert, fma, round), for any scale.
 __device__ __forceinline__ bf16x8_t dequant_word(uint32_t w, float s, float b) {
   uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
   // opaque to the optimizer, so each byte converts with one v_cvt_f32_ubyteN
@@ -82,15 +140,18 @@ __device__ __forceinline__ bf16x8_t dequant_word(uint32_t w, float s, float b) {
   v[5] = __builtin_fmaf(static_cast<float>((hi >> 16) & 0xffu), s, b);
   v[6] = __builtin_fmaf(static_cast<float>(lo >> 24), s, b);
   v[7] = __builtin_fmaf(static_cast<float>(hi >> 24), s, b);
-  bf16x8_t f;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) f[j] = static_cast<__bf16>(v[j]);  // RNE
-  return f;
+  u32x4_t r;
+  r.x = pack_bf16_rne(v[0], v[1]);
+  r.y = pack_bf16_rne(v[2], v[3]);
+  r.z = pack_bf16_rne(v[4], v[5]);
+  r.w = pack_bf16_rne(v[6], v[7]);
+  return __builtin_bit_cast(bf16x8_t, r);
 }
 
 // One tile's main loop and epilogue, NB = active 32-row blocks (1..4), so the
-// MFMA sequence is straight-line code.
-template <bool SWIGLU, uint32_t NB>
+// MFMA sequence is straight-line code. MIX: every staged scale is within
+// dequant_word_mix's range (decided per tile).
+template <bool SWIGLU, uint32_t NB, bool MIX>
 __device__ __forceinline__ void gemm_tile(const GemmArgs& a, uint16_t (&sA)[2][TM * LDS_STRIDE],
                                           const int32_t* s_arow, const int32_t* s_orow, const uint32_t* s_sb,
                                           uint32_t e, uint32_t row0,
@@ -101,29 +162,27 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, uint16_t (&sA)[2][T
   const uint32_t h = lane >> 5;                                    // k half within a group
   const uint32_t K = a.K, groups = K / GK;
 
-  // A staging: thread t -> tile row t/2, 32 bf16 at column 32*(t%2) of the group
-  const uint32_t ar = tid >> 1, ac = 32u * (tid & 1u);
-  const int32_t arow = s_arow[ar];
-  // Padding rows (no A row) stage row 0: row i of an MFMA product depends on
-  // row i of A only, and the epilogue discards padding rows.
-  const uint16_t* aptr = a.A + static_cast<size_t>(arow >= 0 ? arow : 0) * K + ac;
-  // Rows at or past 32 * NB are never read by the MFMAs: in the down kernel the
-  // waves that would stage them (wave >= NB, uniform) skip it. (Measured: the
-  // gate/up kernel is faster staging every row, its loop stays one block.)
-  const bool a_stage = SWIGLU || NB == 4 || ar < 32u * NB;
-  auto load_a = [&](uint32_t g, u32x4_t (&r)[4]) __attribute__((always_inline)) {
-    if (a_stage) {
-      const u32x4_t* p = reinterpret_cast<const u32x4_t*>(aptr + g * GK);
+  // A staging: thread t -> 16 bytes (8 bf16, chunk t % 8 of the group) of tile
+  // rows t/8 + 32i, i = 0..3, so each wave instruction reads 8 whole 128-byte
+  // row segments. Rows of blocks >= NB are never read by the MFMAs and are not
+  // staged (i is unrolled, so this costs no branch).
+  const uint32_t ac = 8u * (tid & 7u);
+  const uint16_t* aptr[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) r[i] = p[i];
-    }
+  for (uint32_t i = 0; i < 4; ++i) {
+    const int32_t arow = s_arow[tid / 8u + 32u * i];
+    // Padding rows (no A row) stage row 0: row i of an MFMA product depends on
+    // row i of A only, and the epilogue discards padding rows.
+    aptr[i] = a.A + static_cast<size_t>(arow >= 0 ? arow : 0) * K + ac;
+  }
+  auto load_a = [&](uint32_t g, u32x4_t (&r)[4]) __attribute__((always_inline)) {
+#pragma unroll
+    for (uint32_t i = 0; i < NB; ++i) r[i] = *reinterpret_cast<const u32x4_t*>(aptr[i] + g * GK);
   };
   auto store_a = [&](uint32_t buf, const u32x4_t (&r)[4]) __attribute__((always_inline)) {
-    if (a_stage) {
-      u32x4_t* d = reinterpret_cast<u32x4_t*>(&sA[buf][ar * LDS_STRIDE + ac]);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) d[i] = r[i];
-    }
+    for (uint32_t i = 0; i < NB; ++i)
+      *reinterpret_cast<u32x4_t*>(&sA[buf][(tid / 8u + 32u * i) * LDS_STRIDE + ac]) = r[i];
   };
 
   // B pointers of this lane's weight row(s)
@@ -167,10 +226,14 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, uint16_t (&sA)[2][T
     const uint32_t buf = g & 1u;
     __syncthreads();  // A of group g visible in sA[buf]; sA[buf^1] no longer read
     load_a(g + 1 < groups ? g + 1 : g, ras);  // the tail reload is stored but never read
+    // keep the A loads here, a whole group ahead of their LDS store: left to
+    // itself the scheduler sinks them next to the store and exposes their latency
+    __builtin_amdgcn_sched_barrier(0);
     const uint32_t sv0 = sb0[g * SB_STRIDE];
     const uint32_t sv1 = SWIGLU ? sb1[g * SB_STRIDE] : 0u;
     const uint32_t q0w[4] = {bcur.q0.x, bcur.q0.y, bcur.q0.z, bcur.q0.w};
     const uint32_t q1w[4] = {bcur.q1.x, bcur.q1.y, bcur.q1.z, bcur.q1.w};
+    const MixScale m0 = mix_scale(sv0), m1 = mix_scale(sv1);
 #pragma unroll
     for (uint32_t st = 0; st < 4; ++st) {
       bf16x8_t af[NB];
@@ -178,15 +241,16 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, uint16_t (&sA)[2][T
       for (uint32_t mb = 0; mb < NB; ++mb)
         af[mb] = *reinterpret_cast<const bf16x8_t*>(
             &sA[buf][(32u * mb + (lane & 31u)) * LDS_STRIDE + 32u * h + 8u * st]);
-      const bf16x8_t f0 = dequant_word(q0w[st], bf16lo(sv0), bf16hi(sv0));
+      const bf16x8_t f0 = MIX ? dequant_word_mix(q0w[st], m0) : dequant_word(q0w[st], bf16lo(sv0), bf16hi(sv0));
       bf16x8_t f1;
-      if (SWIGLU) f1 = dequant_word(q1w[st], bf16lo(sv1), bf16hi(sv1));
+      if (SWIGLU) f1 = MIX ? dequant_word_mix(q1w[st], m1) : dequant_word(q1w[st], bf16lo(sv1), bf16hi(sv1));
 #pragma unroll
       for (uint32_t mb = 0; mb < NB; ++mb) {
         acc0[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mb], f0, acc0[mb], 0, 0, 0);
         if (SWIGLU) acc1[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mb], f1, acc1[mb], 0, 0, 0);
       }
     }
+    __builtin_amdgcn_sched_barrier(0);  // the A store waits for its loads: keep it last
     bcur = load_b(g + 2);    // clamped past the end; never used there
     store_a(buf ^ 1u, ras);  // read after the next barrier
   };
@@ -266,6 +330,7 @@ __global__ void __launch_bounds__(256, 2) grouped_gemm_kernel(GemmArgs a) {
   // Stage the scales and biases of the tile's 128 weight rows. Rows n0.. of
   // expert e are contiguous ([E, N, groups] bf16), so 8-byte chunks (4 groups
   // of one row; groups % 4 == 0) load coalesced; each becomes 4 packed words.
+  bool wide_scale = false;  // some staged |s| is beyond dequant_word_mix's range
   {
     const uint32_t groups = a.K / GK, cpr = groups / 4u;  // chunks per row
     const size_t base = (static_cast<size_t>(e) * a.N + n0) * groups;
@@ -281,15 +346,22 @@ __global__ void __launch_bounds__(256, 2) grouped_gemm_kernel(GemmArgs a) {
         d[SB_STRIDE] = (sv.x >> 16) | (bv.x & 0xffff0000u);
         d[2u * SB_STRIDE] = (sv.y & 0xffffu) | (bv.y << 16);
         d[3u * SB_STRIDE] = (sv.y >> 16) | (bv.y & 0xffff0000u);
+        wide_scale = wide_scale || scale_out_of_mix_range(sv.x) || scale_out_of_mix_range(sv.x >> 16) ||
+                     scale_out_of_mix_range(sv.y) || scale_out_of_mix_range(sv.y >> 16);
       }
     }
   }
-  __syncthreads();
-  switch ((nrows + 31u) / 32u) {  // uniform per workgroup
-    case 1: gemm_tile<SWIGLU, 1>(a, sA, s_arow, s_orow, s_sb, e, row0, nrows, n0); break;
-    case 2: gemm_tile<SWIGLU, 2>(a, sA, s_arow, s_orow, s_sb, e, row0, nrows, n0); break;
-    case 3: gemm_tile<SWIGLU, 3>(a, sA, s_arow, s_orow, s_sb, e, row0, nrows, n0); break;
-    default: gemm_tile<SWIGLU, 4>(a, sA, s_arow, s_orow, s_sb, e, row0, nrows, n0); break;
+  const bool mix = !__syncthreads_or(wide_scale);  // uniform per workgroup
+  const uint32_t nb = (nrows + 31u) / 32u;
+  if (mix) {
+    switch (nb) {
+      case 1: gemm_tile<SWIGLU, 1, true>(a, sA, s_arow, s_orow, s_sb, e, row0, nrows, n0); break;
+      case 2: gemm_tile<SWIGLU, 2, true>(a, sA, s_arow, s_orow, s_sb, e, row0, nrows, n0); break;
+      case 3: gemm_tile<SWIGLU, 3, true>(a, sA, s_arow, s_orow, s_sb, e, row0, nrows, n0); break;
+      default: gemm_tile<SWIGLU, 4, true>(a, sA, s_arow, s_orow, s_sb, e, row0, nrows, n0); break;
+    }
+  } else {  // scales beyond 2^100 (never in real checkpoints): reference-form dequant
+    gemm_tile<SWIGLU, 4, false>(a, sA, s_arow, s_orow, s_sb, e, row0, nrows, n0);
   }
 }
 

@@ -78,6 +78,42 @@ def test_q4_matmul_dense(exe, T, in_f, out_f):
     _close(_f32(Y.download()), _f32(X) @ W.astype(np.float64).T, 1e-2)
 
 
+def _extreme_scales(rng, rows, groups, huge):
+    """bf16 scales over the whole exponent range (subnormal to 2^100, both
+    signs), optionally one of 2^110; biases nonzero so every weight stays a
+    normal number."""
+    # smallest subnormal (both signs), largest subnormal, smallest normal, +-1,
+    # 2^-105, +-2^100 (the fast path's limit), ~0.01, +-0
+    pats = np.array([0x0001, 0x8001, 0x007F, 0x0080, 0x3F80, 0xBF80, 0x0B00, 0x7180, 0xF180, 0x3C23, 0x0000, 0x8000],
+                    np.uint16)
+    s = synth.bf16_normal(rng, (rows, groups), 0.02, absval=True)
+    pick = rng.random((rows, groups)) < 0.5
+    s[pick] = rng.choice(pats, size=int(pick.sum()))
+    if huge:
+        s[rows // 2, groups - 1] = 0x76D0  # 1.6e33 (> 2^100): tile falls back to the reference-form dequant
+    b = synth.bf16_normal(rng, (rows, groups), 0.01)
+    b[np.abs(synth.bf16_bits_to_f32(b)) < 1e-3] = 0x3C23
+    return s, b
+
+
+@pytest.mark.parametrize("huge", [False, True])
+def test_q4_matmul_weight_operand_bit_exact(exe, huge):
+    """One-hot activation rows make the GEMM output equal its bf16 weight
+    operand: Y[t, o] = RNE_bf16(fl32(q*s + b)) of column t, bit for bit, for
+    scales across the bf16 range (and a tile beyond the fast path's 2^100)."""
+    rng = np.random.default_rng(4242 + huge)
+    out_f, in_f = 256, 256
+    w = rng.integers(0, 2**32, size=(out_f, in_f // 8), dtype=np.uint64).astype(np.uint32)
+    s, b = _extreme_scales(rng, out_f, in_f // 64, huge)
+    X = np.zeros((in_f, in_f), np.uint16)
+    X[np.arange(in_f), np.arange(in_f)] = 0x3F80  # bf16 1.0
+    Y = exe.alloc((in_f, out_f), np.uint16)
+    exe.q4_matmul(exe.upload(w), exe.upload(s), exe.upload(b), exe.upload(X), Y, in_f, in_f, out_f, 64)
+    ref = synth.f32_to_bf16_bits(O.dequant(4, w, s, b, out_f, in_f)).T  # [in, out]
+    got = Y.download()
+    assert np.array_equal(got, ref), int(np.sum(got != ref))
+
+
 @pytest.mark.parametrize("T,seed", [(64, 0), (37, 1), (1, 2)])
 def test_moe_prefill_zipf_vs_oracle(exe, qwen, T, seed):
     t, layer, L = qwen
