@@ -119,6 +119,13 @@ __device__ __forceinline__ bf16x8_t dequant_word_mix(uint32_t w, const MixScale&
   return __builtin_bit_cast(bf16x8_t, r);
 }
 
+// silu(g) * u for the GEMM epilogue with the hardware exp2 and reciprocal
+// (about 2 ulp in fp32; the result is rounded to bf16 right after).
+__device__ __forceinline__ float silu_mul_fast(float g, float u) {
+  const float e = __builtin_amdgcn_exp2f(-g * 1.44269504088896341f);
+  return (g * __builtin_amdgcn_rcpf(1.0f + e)) * u;
+}
+
 // A staged scale|bias word whose scale is beyond dequant_word_mix's range
 // (|s| > 2^100, inf, NaN): bf16 exponent field above 127 + 100.
 __device__ __forceinline__ bool scale_out_of_mix_range(uint32_t packed_sb) {
@@ -262,17 +269,29 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, uint16_t (&sA)[2][T
   // Epilogue: lane holds C[i][nl] for i = 32mb + 8(v/4) + 4h + v%4. The tile
   // goes through LDS (the A buffers are free now) so each output row leaves as
   // sixteen coalesced 16-byte stores instead of 128 scattered 2-byte ones.
+  // Lanes nl and nl^1 (columns c, c+1) swap halves of their packed row pairs,
+  // so each LDS write is a 4-byte (row, c..c+1) pair: the even lane writes rows
+  // i0 and i0+2, the odd lane rows i0+1 and i0+3.
   constexpr uint32_t C_STRIDE = TN + 8;  // bf16 per staged row (bank spread)
   static_assert(TM * C_STRIDE <= 2 * TM * LDS_STRIDE, "C tile must fit the A buffers");
   uint16_t* sC = reinterpret_cast<uint16_t*>(sA);
+  const uint32_t odd = nl & 1u, c_even = nl & ~1u;
+  const uint32_t sel = odd ? 0x03020706u : 0x05040100u;  // v_perm: (partner.hi, own.hi) : (own.lo, partner.lo)
   __syncthreads();  // every wave is done reading sA
 #pragma unroll
   for (uint32_t mb = 0; mb < NB; ++mb) {
 #pragma unroll
-    for (uint32_t v = 0; v < 16; ++v) {
-      const uint32_t i = 32u * mb + 8u * (v / 4u) + 4u * h + (v % 4u);
-      const float val = SWIGLU ? silu_mul(acc0[mb][v], acc1[mb][v]) : acc0[mb][v];
-      sC[i * C_STRIDE + nl] = f32_to_bf16(val);
+    for (uint32_t qd = 0; qd < 4; ++qd) {
+      float v[4];
+#pragma unroll
+      for (uint32_t j = 0; j < 4; ++j)
+        v[j] = SWIGLU ? silu_mul_fast(acc0[mb][4 * qd + j], acc1[mb][4 * qd + j]) : acc0[mb][4 * qd + j];
+      const uint32_t p01 = pack_bf16_rne(v[0], v[1]), p23 = pack_bf16_rne(v[2], v[3]);
+      const uint32_t s01 = static_cast<uint32_t>(dpp_i32<DPP_XOR1>(static_cast<int>(p01)));
+      const uint32_t s23 = static_cast<uint32_t>(dpp_i32<DPP_XOR1>(static_cast<int>(p23)));
+      const uint32_t i0 = 32u * mb + 8u * qd + 4u * h + odd;
+      *reinterpret_cast<uint32_t*>(&sC[i0 * C_STRIDE + c_even]) = __builtin_amdgcn_perm(s01, p01, sel);
+      *reinterpret_cast<uint32_t*>(&sC[(i0 + 2u) * C_STRIDE + c_even]) = __builtin_amdgcn_perm(s23, p23, sel);
     }
   }
   __syncthreads();
@@ -330,24 +349,46 @@ __global__ void __launch_bounds__(256, 2) grouped_gemm_kernel(GemmArgs a) {
   // Stage the scales and biases of the tile's 128 weight rows. Rows n0.. of
   // expert e are contiguous ([E, N, groups] bf16), so 8-byte chunks (4 groups
   // of one row; groups % 4 == 0) load coalesced; each becomes 4 packed words.
+  // All of a batch's loads (up to 4 chunks per thread and matrix) are issued
+  // before any is stored, so the staging pays one memory latency per batch
+  // (one batch for K <= 2048) instead of one per chunk.
   bool wide_scale = false;  // some staged |s| is beyond dequant_word_mix's range
   {
-    const uint32_t groups = a.K / GK, cpr = groups / 4u;  // chunks per row
+    constexpr uint32_t NMAT = SWIGLU ? 2u : 1u, PER = 4u;
+    const uint32_t groups = a.K / GK, cpr = groups / 4u, nchunk = TN * cpr;  // chunks per row, per matrix
     const size_t base = (static_cast<size_t>(e) * a.N + n0) * groups;
+    for (uint32_t c0 = 0; c0 < nchunk; c0 += PER * 256u) {
+      uint2 sv[NMAT][PER], bv[NMAT][PER];
 #pragma unroll
-    for (uint32_t mat = 0; mat < (SWIGLU ? 2u : 1u); ++mat) {
-      const uint2* sp = reinterpret_cast<const uint2*>((mat ? a.s1 : a.s0) + base);
-      const uint2* bp = reinterpret_cast<const uint2*>((mat ? a.b1 : a.b0) + base);
-      for (uint32_t c = tid; c < TN * cpr; c += 256u) {
-        const uint2 sv = sp[c], bv = bp[c];
-        const uint32_t row = c / cpr, g0 = 4u * (c % cpr);
-        uint32_t* d = s_sb + (static_cast<size_t>(mat) * groups + g0) * SB_STRIDE + row;
-        d[0] = (sv.x & 0xffffu) | (bv.x << 16);
-        d[SB_STRIDE] = (sv.x >> 16) | (bv.x & 0xffff0000u);
-        d[2u * SB_STRIDE] = (sv.y & 0xffffu) | (bv.y << 16);
-        d[3u * SB_STRIDE] = (sv.y >> 16) | (bv.y & 0xffff0000u);
-        wide_scale = wide_scale || scale_out_of_mix_range(sv.x) || scale_out_of_mix_range(sv.x >> 16) ||
-                     scale_out_of_mix_range(sv.y) || scale_out_of_mix_range(sv.y >> 16);
+      for (uint32_t mat = 0; mat < NMAT; ++mat) {
+        const uint2* sp = reinterpret_cast<const uint2*>((mat ? a.s1 : a.s0) + base);
+        const uint2* bp = reinterpret_cast<const uint2*>((mat ? a.b1 : a.b0) + base);
+#pragma unroll
+        for (uint32_t j = 0; j < PER; ++j) {
+          const uint32_t c = c0 + tid + 256u * j;
+          if (c < nchunk) {
+            sv[mat][j] = sp[c];
+            bv[mat][j] = bp[c];
+          }
+        }
+      }
+#pragma unroll
+      for (uint32_t mat = 0; mat < NMAT; ++mat) {
+#pragma unroll
+        for (uint32_t j = 0; j < PER; ++j) {
+          const uint32_t c = c0 + tid + 256u * j;
+          if (c < nchunk) {
+            const uint2 s2 = sv[mat][j], b2 = bv[mat][j];
+            const uint32_t row = c / cpr, g0 = 4u * (c % cpr);
+            uint32_t* d = s_sb + (static_cast<size_t>(mat) * groups + g0) * SB_STRIDE + row;
+            d[0] = (s2.x & 0xffffu) | (b2.x << 16);
+            d[SB_STRIDE] = (s2.x >> 16) | (b2.x & 0xffff0000u);
+            d[2u * SB_STRIDE] = (s2.y & 0xffffu) | (b2.y << 16);
+            d[3u * SB_STRIDE] = (s2.y >> 16) | (b2.y & 0xffff0000u);
+            wide_scale = wide_scale || scale_out_of_mix_range(s2.x) || scale_out_of_mix_range(s2.x >> 16) ||
+                         scale_out_of_mix_range(s2.y) || scale_out_of_mix_range(s2.y >> 16);
+          }
+        }
       }
     }
   }
