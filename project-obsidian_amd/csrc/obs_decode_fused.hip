@@ -27,8 +27,8 @@
 //      polls all 768 into LDS and finishes its 64 down rows from registers.
 //   4. Group 0 combines: workgroup j polls the 8 ranks' outputs for its 64 rows
 //      and accumulates residual + sum_r w_r * y_r in rank order (forward.rs:440).
-// The last workgroup to exit advances the launch counter that defines the next
-// launch's epoch, so graph replays need no host involvement.
+// The epoch is derived from a device-side count of exited workgroups (see the
+// kernel's first lines), so graph replays need no host involvement.
 //
 // Every wait is bounded (100 ms on the GPU's constant clock); a timeout sets a
 // device error flag, later launches then exit at once, and obs_device_status()
@@ -44,13 +44,15 @@ namespace {
 
 using namespace obsd;
 
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
 constexpr uint32_t FH = 2048, FI = 768, FK = 8, FG = 64;
 constexpr uint32_t NGROUP = 8, WG_PER_GROUP = 32, NWG = NGROUP * WG_PER_GROUP;
 constexpr uint32_t MAX_E = 256;
 constexpr uint32_t GU_ROWS = FI / (WG_PER_GROUP * 4);  // gate/up rows per wave: 6
 constexpr uint32_t DN_ROWS_WG = FH / WG_PER_GROUP;     // down rows per workgroup: 64
 
-constexpr size_t WS_LAUNCH = 0, WS_EXIT = 128, WS_ERR = 256;
+constexpr size_t WS_COUNT = 0, WS_ERR = 256;  // WS_COUNT: 64-bit workgroup count
 constexpr size_t WS_LOGITS = 1024;                              // [8][MAX_E] slots
 constexpr size_t WS_H = WS_LOGITS + size_t(NGROUP) * MAX_E * 8;  // [8][FI] slots
 constexpr size_t WS_Y = WS_H + size_t(NGROUP) * FI * 8;          // [8][FH] slots
@@ -94,8 +96,10 @@ __device__ __forceinline__ void unpack_bf16x8(const uint4& v, float* f) {
 }
 
 // NQ = router logit slots per lane: 2 for up to 128 experts, 4 for up to 256.
+// One workgroup per CU, so one wave per SIMD: the compiler is told so and need
+// not trade waits for registers.
 template <int NQ>
-__global__ void __launch_bounds__(256, 1) decode_fused_kernel(FusedArgs a) {
+__global__ void __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) decode_fused_kernel(FusedArgs a) {
   constexpr int RT = NQ / 2;  // router rows per wave
   __shared__ uint32_t s_epoch;
   __shared__ int s_abort;
@@ -105,11 +109,11 @@ __global__ void __launch_bounds__(256, 1) decode_fused_kernel(FusedArgs a) {
   __shared__ __attribute__((aligned(16))) f16x2_t s_hp[FI / 2];  // h as f16 pairs, dot8_q4_off order
   __shared__ float s_hsum[FI / 32], s_hoff[FI / 32];              // per 32 columns: sum h, sum off*h
   __shared__ float s_y[FK][64];
+  __shared__ __attribute__((aligned(16))) uint16_t s_sc[4][1536];  // per wave: staged scales (see phase 3)
 
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   const uint32_t g = blockIdx.x % NGROUP, j = blockIdx.x / NGROUP;
-  uint32_t* ctl_launch = reinterpret_cast<uint32_t*>(a.ws + WS_LAUNCH);
-  uint32_t* ctl_exit = reinterpret_cast<uint32_t*>(a.ws + WS_EXIT);
+  uint64_t* ctl_count = reinterpret_cast<uint64_t*>(a.ws + WS_COUNT);
   const uint32_t* ctl_err = reinterpret_cast<const uint32_t*>(a.ws + WS_ERR);
   uint64_t* logit_slots = reinterpret_cast<uint64_t*>(a.ws + WS_LOGITS) + size_t(g) * MAX_E;
   uint64_t* h_slots = reinterpret_cast<uint64_t*>(a.ws + WS_H) + size_t(g) * FI;
@@ -118,7 +122,11 @@ __global__ void __launch_bounds__(256, 1) decode_fused_kernel(FusedArgs a) {
 
   OBS_FUSED_MARK(0);
   if (tid == 0) {
-    s_epoch = __hip_atomic_load(ctl_launch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+    // Every workgroup adds 1 to the count as it exits (after this read). All NWG
+    // workgroups of every earlier launch have added theirs (the kernel boundary
+    // completes them), and of this launch fewer than NWG can have (this one has
+    // not), so the quotient is the number of earlier launches.
+    s_epoch = static_cast<uint32_t>(__hip_atomic_load(ctl_count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) / NWG) + 1u;
     s_abort = __hip_atomic_load(ctl_err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u;
   }
   // this lane's 32 input columns [32*lane, 32*lane + 32)
@@ -145,7 +153,10 @@ __global__ void __launch_bounds__(256, 1) decode_fused_kernel(FusedArgs a) {
   }
   __syncthreads();
   const uint32_t epoch = s_epoch;
-  if (s_abort) return;  // a previous launch failed: the host must reset first
+  if (s_abort) {  // a previous launch failed: the host must reset first
+    if (tid == 0) __hip_atomic_fetch_add(ctl_count, uint64_t{1}, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
   OBS_FUSED_MARK(1);
 
   float xf[32];
@@ -228,41 +239,67 @@ __global__ void __launch_bounds__(256, 1) decode_fused_kernel(FusedArgs a) {
   const bool have = ok && eg >= 0 && static_cast<uint32_t>(eg) < n_exp;
   OBS_FUSED_MARK(3);
 
-  // ---- 3. issue every weight load this wave needs: 6 gate + 6 up rows, 2x3 down blocks
+  // ---- 3. issue every weight load this wave needs: 6 gate + 6 up rows, 2x3 down blocks.
+  // Wide loads only: each gate/up row is one coalesced 1 KB load; the down rows
+  // are read a 128-byte line per 8 lanes (lane (r8, m) takes bytes
+  // [128L + 16m, +16) of row r8, L = 0..2: columns [256L + 32m, +32)); the
+  // scales and biases the wave needs (24 gate/up segments of 64 bytes, 2 x 384
+  // contiguous down bytes) come in 3 16-byte loads per lane and are spread
+  // through the wave's own LDS area, not one 2-byte load per value.
   uint4 gq[GU_ROWS], uq[GU_ROWS];
-  uint16_t gsv[GU_ROWS], gbv[GU_ROWS], usv[GU_ROWS], ubv[GU_ROWS];
   uint4 dq[2][3];
-  uint16_t dsv[2][3], dbv[2][3];
-  const uint32_t m = lane & 7u;         // down column slice [96m, 96m + 96)
-  const uint32_t r8 = lane >> 3;        // down row within an 8-row pass
-  if (have) {
-    const size_t eoff_gu = size_t(eg) * FI;
+  const uint32_t m = lane & 7u;   // down: 16-byte chunk within each 128-byte line
+  const uint32_t r8 = lane >> 3;  // down: row within an 8-row pass
+  const uint32_t dn_row0 = DN_ROWS_WG * j + 16u * wave;  // the wave's 16 down rows
+  u32x4_t scq0, scq1, scq2;  // native vectors (a uint4 array stored through a pointer went to scratch)
+  {
+    // Unconditional (a valid expert when this group has none, results unused):
+    // loads under a branch make the compiler wait for all of them at the join.
+    const uint32_t el = have ? static_cast<uint32_t>(eg) : 0u;
+    const size_t eoff_gu = size_t(el) * FI;
+    // Loads in the order they are consumed (the memory counter is in order): the
+    // gate/up scales and rows, then the down scales and rows. Lanes past the
+    // last chunk reload a valid one, so no load is predicated.
+#pragma unroll
+    for (uint32_t i = 0; i < 2; ++i) {  // chunk c = 16 bytes of segment c/4 = (row t, array)
+      const uint32_t c = min(lane + 64u * i, GU_ROWS * 16u - 1u), sg = c / 4u, t = sg / 4u, arr = sg % 4u;
+      const uint16_t* base = arr == 0u ? a.gate_s : arr == 1u ? a.gate_b : arr == 2u ? a.up_s : a.up_b;
+      const u32x4_t v = *reinterpret_cast<const u32x4_t*>(base + (eoff_gu + e0 + 128u * t) * (FH / FG) + 8u * (c % 4u));
+      if (i == 0) scq0 = v; else scq1 = v;
+    }
+    __builtin_amdgcn_sched_barrier(0);  // keep the issue order (see above)
 #pragma unroll
     for (uint32_t t = 0; t < GU_ROWS; ++t) {
       const size_t row = eoff_gu + e0 + 128u * t;
       gq[t] = reinterpret_cast<const uint4*>(a.gate_w + row * (FH / 8))[lane];
       uq[t] = reinterpret_cast<const uint4*>(a.up_w + row * (FH / 8))[lane];
-      gsv[t] = a.gate_s[row * (FH / FG) + lane / 2u];
-      gbv[t] = a.gate_b[row * (FH / FG) + lane / 2u];
-      usv[t] = a.up_s[row * (FH / FG) + lane / 2u];
-      ubv[t] = a.up_b[row * (FH / FG) + lane / 2u];
     }
+    __builtin_amdgcn_sched_barrier(0);
+    {  // down scales (chunks 0..23) and biases (24..47) of the wave's 16 rows
+      const uint32_t c = min(lane, 47u);
+      scq2 = *reinterpret_cast<const u32x4_t*>((c < 24u ? a.down_s : a.down_b) +
+                                               (size_t(el) * FH + dn_row0) * (FI / FG) + 8u * (c % 24u));
+    }
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (uint32_t p = 0; p < 2; ++p) {
-      const size_t row = size_t(eg) * FH + DN_ROWS_WG * j + 16u * wave + 8u * p + r8;
-      const uint4* dp = reinterpret_cast<const uint4*>(a.down_w + row * (FI / 8) + 12u * m);
+      const size_t row = size_t(el) * FH + dn_row0 + 8u * p + r8;
+      const uint4* dp = reinterpret_cast<const uint4*>(a.down_w + row * (FI / 8)) + m;
 #pragma unroll
-      for (uint32_t b = 0; b < 3; ++b) {
-        dq[p][b] = dp[b];
-        const uint32_t gi = (96u * m + 32u * b) / FG;
-        dsv[p][b] = a.down_s[row * (FI / FG) + gi];
-        dbv[p][b] = a.down_b[row * (FI / FG) + gi];
-      }
+      for (uint32_t L = 0; L < 3; ++L) dq[p][L] = dp[8u * L];
     }
   }
+  // the wave's staged scales: gate/up segment sg = 4t + {gate_s, gate_b, up_s,
+  // up_b} at [32 sg], down scales at [1024 + 12 r], down biases at [1216 + 12 r]
+  const uint16_t* sc16 = s_sc[wave];
 
   OBS_FUSED_MARK(4);
   // ---- 4. gate/up rows -> h slots (factored per group: s*sum(q x) + b*sum(x))
+  {  // the wave's own LDS area: no barrier (its LDS accesses run in order)
+    u32x4_t* sc = reinterpret_cast<u32x4_t*>(s_sc[wave]);
+    sc[lane] = scq0;
+    sc[64u + lane] = scq1;  // chunks 96..127: padding
+  }
 #pragma unroll
   for (uint32_t t = 0; t < GU_ROWS; ++t) {
     float pg = 0.0f, pu = 0.0f;
@@ -276,8 +313,9 @@ __global__ void __launch_bounds__(256, 1) decode_fused_kernel(FusedArgs a) {
       au = dot8_q4_off(uq[t].y, xh + 4, au);
       au = dot8_q4_off(uq[t].z, xh + 8, au);
       au = dot8_q4_off(uq[t].w, xh + 12, au);
-      pg = __builtin_fmaf(bf16_to_f32(gsv[t]), ag - xoff, bf16_to_f32(gbv[t]) * xs);
-      pu = __builtin_fmaf(bf16_to_f32(usv[t]), au - xoff, bf16_to_f32(ubv[t]) * xs);
+      const uint16_t* sg = sc16 + 128u * t + lane / 2u;  // this lane's group of row t
+      pg = __builtin_fmaf(bf16_to_f32(sg[0]), ag - xoff, bf16_to_f32(sg[32]) * xs);
+      pu = __builtin_fmaf(bf16_to_f32(sg[64]), au - xoff, bf16_to_f32(sg[96]) * xs);
     }
     pg = wave_sum_asc(pg);
     pu = wave_sum_asc(pu);
@@ -328,36 +366,40 @@ __global__ void __launch_bounds__(256, 1) decode_fused_kernel(FusedArgs a) {
 
   OBS_FUSED_MARK(6);
   // ---- 6. this workgroup's 64 down rows of expert e_g (unscaled by w_g)
+  reinterpret_cast<u32x4_t*>(s_sc[wave])[128u + lane] = scq2;  // chunks 176..191: padding
   {
-    // the lane's 96 columns [96m, 96m + 96) = three 32-column blocks
+    // the lane's 96 columns: blocks [256L + 32m, +32), L = 0..2
     f16x2_t hp[48];
     float hsum[3], hoff[3];
 #pragma unroll
-    for (uint32_t c = 0; c < 48; c += 4) {
-      const uint4 v = *reinterpret_cast<const uint4*>(s_hp + 48u * m + c);
-      hp[c] = as_f16x2(v.x); hp[c + 1] = as_f16x2(v.y); hp[c + 2] = as_f16x2(v.z); hp[c + 3] = as_f16x2(v.w);
-    }
+    for (uint32_t L = 0; L < 3; ++L) {
 #pragma unroll
-    for (uint32_t b = 0; b < 3; ++b) {
-      hsum[b] = s_hsum[3u * m + b];
-      hoff[b] = s_hoff[3u * m + b];
+      for (uint32_t c = 0; c < 16; c += 4) {
+        const uint4 v = *reinterpret_cast<const uint4*>(s_hp + 128u * L + 16u * m + c);
+        hp[16 * L + c] = as_f16x2(v.x); hp[16 * L + c + 1] = as_f16x2(v.y);
+        hp[16 * L + c + 2] = as_f16x2(v.z); hp[16 * L + c + 3] = as_f16x2(v.w);
+      }
+      hsum[L] = s_hsum[8u * L + m];
+      hoff[L] = s_hoff[8u * L + m];
     }
 #pragma unroll
     for (uint32_t p = 0; p < 2; ++p) {
       float part = 0.0f;
       if (have) {
+        const uint16_t* dsb = sc16 + 1024u + 12u * (8u * p + r8);
 #pragma unroll
-        for (uint32_t b = 0; b < 3; ++b) {
+        for (uint32_t L = 0; L < 3; ++L) {
           float acc = 0.0f;
-          acc = dot8_q4_off(dq[p][b].x, hp + 16u * b + 0, acc);
-          acc = dot8_q4_off(dq[p][b].y, hp + 16u * b + 4, acc);
-          acc = dot8_q4_off(dq[p][b].z, hp + 16u * b + 8, acc);
-          acc = dot8_q4_off(dq[p][b].w, hp + 16u * b + 12, acc);
-          part = part + __builtin_fmaf(bf16_to_f32(dsv[p][b]), acc - hoff[b], bf16_to_f32(dbv[p][b]) * hsum[b]);
+          acc = dot8_q4_off(dq[p][L].x, hp + 16u * L + 0, acc);
+          acc = dot8_q4_off(dq[p][L].y, hp + 16u * L + 4, acc);
+          acc = dot8_q4_off(dq[p][L].z, hp + 16u * L + 8, acc);
+          acc = dot8_q4_off(dq[p][L].w, hp + 16u * L + 12, acc);
+          const uint32_t gi = 4u * L + m / 2u;  // quantization group of block L
+          part = part + __builtin_fmaf(bf16_to_f32(dsb[gi]), acc - hoff[L], bf16_to_f32(dsb[192u + gi]) * hsum[L]);
         }
       }
       part = group8_sum(part);
-      const uint32_t row = DN_ROWS_WG * j + 16u * wave + 8u * p + r8;
+      const uint32_t row = dn_row0 + 8u * p + r8;
       if (m == 0) slot_store(y_slots + size_t(g) * FH + row, epoch, part);
     }
   }
@@ -393,12 +435,8 @@ __global__ void __launch_bounds__(256, 1) decode_fused_kernel(FusedArgs a) {
   }
 
   OBS_FUSED_MARK(8);
-  // ---- 8. exit: the last workgroup advances the launch counter (next epoch)
-  __syncthreads();
-  if (tid == 0) {
-    const uint32_t old = __hip_atomic_fetch_add(ctl_exit, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if ((old + 1u) % NWG == 0u) __hip_atomic_store(ctl_launch, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
+  // ---- 8. exit: count this workgroup (a no-return add: nothing waits for it)
+  if (tid == 0) __hip_atomic_fetch_add(ctl_count, uint64_t{1}, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 }  // namespace
