@@ -171,6 +171,15 @@ int obs_swiglu(obs_ctx* ctx, const uint16_t* g, const uint16_t* u, uint16_t* h, 
 /* acc = acc + scale * y in place, bf16, fp32 math */
 int obs_scaled_add(obs_ctx* ctx, uint16_t* acc, const uint16_t* y, float scale, uint32_t n);
 
+/* RMSNorm of `rows` rows of `dim` bf16 values — shaders/rmsnorm.metal (the
+ * rmsnorm pipeline) / Model::rmsnorm (forward.rs:345-357):
+ * rms = sqrt(sum(x^2) / dim + eps), out = (x / rms) * weight, fp32 math,
+ * rounded once to bf16. sum(x^2) has a fixed order (64 lanes each own dim/64
+ * contiguous columns, serial fma, then an xor butterfly), so the result is
+ * reproducible bit for bit. dim % 64 == 0, dim <= 8192; x and out may alias. */
+int obs_rmsnorm(obs_ctx* ctx, const uint16_t* x, const uint16_t* weight, uint16_t* out,
+                uint32_t rows, uint32_t dim, float eps);
+
 /* ------------------------------------------------------------------ */
 /* HBM-resident expert table + fused MoE layer                         */
 /* (replaces ExpertIndex / read_experts_parallel / expert_pool,        */
@@ -184,6 +193,7 @@ typedef struct obs_moe_config {
   uint32_t inter;    /* moe_intermediate_size (model.rs:17) */
   uint32_t group;    /* quantization group size (64) */
   int32_t norm_topk; /* norm_topk_prob (model.rs:22) */
+  float rms_eps;     /* rms_norm_eps (model.rs:18); used when layer->norm_w is set */
 } obs_moe_config;
 
 /* One layer's MoE weights, all device pointers, stacked on the expert axis. */
@@ -192,12 +202,18 @@ typedef struct obs_moe_layer {
   const uint32_t* up_w;   const uint16_t* up_s;   const uint16_t* up_b;   /* [E, I, H/8], [E, I, H/G] */
   const uint32_t* down_w; const uint16_t* down_s; const uint16_t* down_b; /* [E, H, I/8], [E, H, I/G] */
   const uint32_t* router_w; const uint16_t* router_s; const uint16_t* router_b; /* 8-bit [E, H/4], [E, H/G] */
+  /* post_attention_layernorm.weight, bf16 [H], 16-byte aligned (forward.rs:419);
+   * NULL: the MoE input is used as given (already normalised). */
+  const uint16_t* norm_w;
 } obs_moe_layer;
 
 /* Decode MoE half of one layer for one token (forward.rs:421-441):
  * logits -> top-k -> per selected expert silu(gate x) * (up x) -> down ->
  * weighted sum in rank order. x, y bf16 [hidden]. If residual is non-NULL,
  * y = residual + sum (forward.rs:440 accumulates into the residual stream x1).
+ * If layer->norm_w is set, the router and the experts see rmsnorm(x) with that
+ * weight and cfg->rms_eps (forward.rs:419-421, as obs_rmsnorm computes it, in
+ * the same launch); pass x1 as both x and residual for x1 + MoE(rmsnorm(x1)).
  * ids_out [top_k] / w_out [top_k] (may be NULL) receive the routing.
  * Workspace comes from the context (allocated once, on first use: make the
  * first call outside a graph capture).
@@ -229,7 +245,8 @@ size_t obs_moe_prefill_workspace(const obs_moe_config* cfg, uint32_t T);
  * distinct per token). Tokens are permuted into per-expert groups on the GPU,
  * gate/up/down run as grouped dequant-to-LDS bf16 MFMA GEMMs with a SwiGLU
  * epilogue, and outputs are combined per token in rank order in fp32.
- * X, Y bf16 [T, hidden]; residual (nullable) as in obs_moe_decode.
+ * X, Y bf16 [T, hidden]; residual (nullable) and layer->norm_w as in
+ * obs_moe_decode (the norm runs as one more launch into the workspace).
  * ws: caller-owned device workspace of obs_moe_prefill_workspace() bytes. */
 int obs_moe_prefill(obs_ctx* ctx, const obs_moe_config* cfg, const obs_moe_layer* layer,
                     const uint16_t* X, const uint16_t* residual, uint16_t* Y, uint32_t T,

@@ -21,6 +21,11 @@
  *                                 forced ties -> lowest id, permutation of logits
  *                                 permutes ids, renormalised weights sum to 1,
  *                                 closed form w_i = e_i / sum_sel e_j.
+ *   orc_rmsnorm ................. closed form for a constant row (x = c, w = 1:
+ *                                 ss = dim c^2 exactly, out = bf16(c / sqrtf(c^2 + eps))),
+ *                                 exact invariance under x -> 2x when eps = 0, an fp64
+ *                                 numpy restatement within one bf16 step, and the
+ *                                 butterfly order equal to a serial sum where exact.
  *   orc_moe_decode / _prefill ... one-hot routing weight reproduces one expert;
  *                                 prefill with T=1 equals decode; linearity in the
  *                                 routing weights; grouping invariants.
@@ -312,6 +317,32 @@ int orc_route_topk(const float* logits, int64_t T, int n_exp, int k, int norm_to
 /* ------------------------------------------------------------------------- */
 
 /* ops.metal:21: silu(g)*u = (g / (1 + exp(-g))) * u */
+int orc_rmsnorm(const uint16_t* x, const uint16_t* w, float eps, int64_t rows, int64_t dim, uint16_t* out) {
+  if (dim <= 0 || dim % 64 != 0 || rows < 0) return -1;
+  const int64_t chunk = dim / 64;
+  for (int64_t r = 0; r < rows; ++r) {
+    const uint16_t* xr = x + r * dim;
+    float part[64];
+    for (int l = 0; l < 64; ++l) {
+      float acc = 0.0f;
+      for (int64_t c = l * chunk; c < (l + 1) * chunk; ++c) {
+        const float v = orc_bf16_to_f32(xr[c]);
+        acc = fmaf(v, v, acc);
+      }
+      part[l] = acc;
+    }
+    for (int off = 1; off < 64; off <<= 1) {
+      float nxt[64];
+      for (int l = 0; l < 64; ++l) nxt[l] = part[l] + part[l ^ off];
+      memcpy(part, nxt, sizeof(nxt));
+    }
+    const float rms = sqrtf(part[0] / (float)dim + eps);
+    for (int64_t c = 0; c < dim; ++c)
+      out[r * dim + c] = orc_f32_to_bf16((orc_bf16_to_f32(xr[c]) / rms) * orc_bf16_to_f32(w[c]));
+  }
+  return 0;
+}
+
 float orc_silu_mul(float g, float u) { return (g / (1.0f + orc_exp(-g))) * u; }
 
 void orc_swiglu(const float* g, const float* u, float* h, int64_t n) {

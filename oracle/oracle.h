@@ -11,6 +11,7 @@
  *   - 8-bit router gate mat-vec ............. shaders/dequant_matvec_8bit.metal:17-30
  *   - softmax + top-k + renormalise ......... shaders/moe_routing_topk.metal:24-56
  *   - SwiGLU / scaled add ................... shaders/ops.metal:18-29
+ *   - RMSNorm (post-attention, router input) . shaders/rmsnorm.metal:17-35, src/forward.rs:419
  *   - decode MoE composition ................ src/forward.rs:421-441
  *   - prefill grouping + rank-order combine . src/forward.rs:200-232
  *
@@ -88,6 +89,14 @@ enum { ORC_SUM_SERIAL = 0, ORC_SUM_WAVE = 1 };
  * A slot with no selectable expert (NaN probabilities) gets id -1, weight 0. */
 int orc_route_topk(const float* logits, int64_t T, int n_exp, int k, int norm_topk,
                    int sum_order, int emulate_f16, int32_t* ids, float* w);
+
+/* ---- RMSNorm (shaders/rmsnorm.metal:17-35, Model::rmsnorm forward.rs:345-357) ----
+ * rows x dim, bf16 in and out. ss = sum of x^2 in the documented lane order
+ * (64 lanes each own dim/64 contiguous columns and accumulate x*x serially with
+ * fmaf from 0; lanes combined by the xor butterfly with offsets 1, 2, ..., 32);
+ * rms = sqrtf(ss / dim + eps); out = RNE_bf16((x / rms) * w), IEEE division.
+ * dim % 64 == 0. Returns 0, or -1 on a bad shape. */
+int orc_rmsnorm(const uint16_t* x, const uint16_t* w, float eps, int64_t rows, int64_t dim, uint16_t* out);
 
 /* ---- elementwise (ops.metal:18-29) ---- */
 float orc_silu_mul(float g, float u);           /* g/(1+exp(-g))*u in fp32 */

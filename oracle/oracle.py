@@ -65,6 +65,7 @@ def lib() -> C.CDLL:
         L.orc_group_rows.argtypes = [vp, i64, i32, i32, vp, vp, vp, vp]
         L.orc_moe_prefill.argtypes = [C.POINTER(OrcLayer), vp, i64, i32, vp, vp, i32, vp]
         L.orc_moe_decode_baseline.argtypes = [C.POINTER(OrcLayer), vp, i32, i32, i32, vp, vp, vp]
+        L.orc_rmsnorm.argtypes = [vp, vp, C.c_float, i64, i64, vp]
         L.orc_omp_max_threads.restype = C.c_int
         _L = L
     return _L
@@ -109,6 +110,19 @@ def silu_mul(g: float, u: float) -> float:
 
 
 # ---- tensors ---------------------------------------------------------------
+def rmsnorm(x_bf16, w_bf16, eps: float) -> np.ndarray:
+    """RMSNorm of the rows of x (bf16 [..., dim]) -> bf16 bits, the documented
+    lane order (orc_rmsnorm; rmsnorm.metal:17-35)."""
+    x = _c(x_bf16, np.uint16)
+    w = _c(w_bf16, np.uint16)
+    dim = x.shape[-1]
+    rows = x.size // dim
+    out = np.empty(x.shape, np.uint16)
+    _rc(lib().orc_rmsnorm(_p(x), _p(w), eps, rows, dim, _p(out)), "rmsnorm")
+    return out
+
+
+
 def dequant(bits: int, w, s, b, rows: int, cols: int, group: int = 64, sb_type: int = SB_BF16) -> np.ndarray:
     w, s, b = _c(w, np.uint32), _c(s, np.uint16), _c(b, np.uint16)
     out = np.empty((rows, cols), np.float32)

@@ -222,6 +222,8 @@ int check_moe_layer(obs_ctx* ctx, const char* who, const obs_moe_layer* L) {
     return set_error(ctx, OBS_E_INVALID, "%s: null weight pointer in layer", who);
   if (!aligned(L->gate_w, 16) || !aligned(L->up_w, 16) || !aligned(L->down_w, 16) || !aligned(L->router_w, 16))
     return set_error(ctx, OBS_E_ALIGN, "%s: packed weights must be 16-byte aligned", who);
+  if (L->norm_w && !aligned(L->norm_w, 16))
+    return set_error(ctx, OBS_E_ALIGN, "%s: norm_w must be 16-byte aligned", who);
   return OBS_OK;
 }
 
@@ -281,11 +283,12 @@ int obs_moe_decode(obs_ctx* ctx, const obs_moe_config* cfg, const obs_moe_layer*
   if (fused_ok && ctx->decode_path != OBS_DECODE_MULTI)
     return obs::launch_fused_decode(ctx, cfg, layer, x, residual, y, ids_out, w_out);
   const uint32_t E = cfg->n_exp, k = cfg->top_k, H = cfg->hidden, I = cfg->inter;
-  // workspace: logits [E] | ids [k] | w [k] | h [k, I]
+  // workspace: logits [E] | ids [k] | w [k] | h [k, I] | normed x [H]
   const size_t off_ids = align256(sizeof(float) * E);
   const size_t off_w = off_ids + align256(sizeof(int32_t) * k);
   const size_t off_h = off_w + align256(sizeof(float) * k);
-  const size_t total = off_h + align256(sizeof(float) * k * I);
+  const size_t off_xn = off_h + align256(sizeof(float) * k * I);
+  const size_t total = off_xn + align256(sizeof(uint16_t) * H);
   void* ws = nullptr;
   rc = obs::ensure_decode_ws(ctx, total, &ws);
   if (rc) return rc;
@@ -294,6 +297,12 @@ int obs_moe_decode(obs_ctx* ctx, const obs_moe_config* cfg, const obs_moe_layer*
   int32_t* ids = ids_out ? ids_out : reinterpret_cast<int32_t*>(base + off_ids);
   float* w = w_out ? w_out : reinterpret_cast<float*>(base + off_w);
   float* h = reinterpret_cast<float*>(base + off_h);
+  if (layer->norm_w) {  // the router and experts see rmsnorm(x) (forward.rs:419-421)
+    uint16_t* xn = reinterpret_cast<uint16_t*>(base + off_xn);
+    rc = obs::launch_rmsnorm(ctx, x, layer->norm_w, xn, 1, H, cfg->rms_eps);
+    if (rc) return rc;
+    x = xn;
+  }
   rc = obs::launch_gate_logits(ctx, layer->router_w, layer->router_s, layer->router_b, x, logits, 1, H, E, cfg->group);
   if (rc) return rc;
   rc = obs::launch_route_topk(ctx, logits, ids, w, 1, E, k, cfg->norm_topk);

@@ -65,6 +65,8 @@ struct FusedArgs {
   const uint32_t* down_w; const uint16_t* down_s; const uint16_t* down_b;
   const uint32_t* router_w; const uint16_t* router_s; const uint16_t* router_b;
   const uint16_t* x; const uint16_t* residual; uint16_t* y;
+  const uint16_t* norm_w;  // nullable: rmsnorm the input first (forward.rs:419-421)
+  float rms_eps;
   int32_t* ids_out; float* w_out;
   unsigned char* ws;
   uint32_t n_exp;
@@ -121,35 +123,41 @@ __global__ void __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 
   const uint32_t n_exp = a.n_exp;
 
   OBS_FUSED_MARK(0);
-  if (tid == 0) {
-    // Every workgroup adds 1 to the count as it exits (after this read). All NWG
-    // workgroups of every earlier launch have added theirs (the kernel boundary
-    // completes them), and of this launch fewer than NWG can have (this one has
-    // not), so the quotient is the number of earlier launches.
-    s_epoch = static_cast<uint32_t>(__hip_atomic_load(ctl_count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) / NWG) + 1u;
-    s_abort = __hip_atomic_load(ctl_err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u;
-  }
   // this lane's 32 input columns [32*lane, 32*lane + 32)
-  uint4 xq[4];
+  uint4 xq[4], nq[4];
   {
     const uint4* xp = reinterpret_cast<const uint4*>(a.x + 32u * lane);
 #pragma unroll
     for (int i = 0; i < 4; ++i) xq[i] = xp[i];
+    // unconditional (x again when there is no norm, unused then): a load under
+    // a branch makes the compiler wait for every load in flight at the join
+    const uint4* np = reinterpret_cast<const uint4*>((a.norm_w ? a.norm_w : a.x) + 32u * lane);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) nq[i] = np[i];
   }
   // router rows of this wave: e = 4j + wave (+128)
   const uint32_t e0 = 4u * j + wave;
   uint4 rq[RT][2];
   uint16_t rs[RT], rb[RT];
 #pragma unroll
-  for (int t = 0; t < RT; ++t) {
-    const uint32_t e = e0 + 128u * t;
-    if (e < n_exp) {
-      const uint4* rp = reinterpret_cast<const uint4*>(a.router_w + size_t(e) * (FH / 4) + 8u * lane);
-      rq[t][0] = rp[0];
-      rq[t][1] = rp[1];
-      rs[t] = a.router_s[size_t(e) * (FH / FG) + lane / 2u];
-      rb[t] = a.router_b[size_t(e) * (FH / FG) + lane / 2u];
-    }
+  for (int t = 0; t < RT; ++t) {  // unconditional (a clamped row when e >= n_exp, unused then)
+    const uint32_t e = min(e0 + 128u * t, n_exp - 1u);
+    const uint4* rp = reinterpret_cast<const uint4*>(a.router_w + size_t(e) * (FH / 4) + 8u * lane);
+    rq[t][0] = rp[0];
+    rq[t][1] = rp[1];
+    rs[t] = a.router_s[size_t(e) * (FH / FG) + lane / 2u];
+    rb[t] = a.router_b[size_t(e) * (FH / FG) + lane / 2u];
+  }
+  // after the activation and router loads, so its two reads overlap them
+  if (tid == 0) {
+    // Every workgroup adds 1 to the count as it exits (after this read). All NWG
+    // workgroups of every earlier launch have added theirs (the kernel boundary
+    // completes them), and of this launch fewer than NWG can have (this one has
+    // not), so the quotient is the number of earlier launches.
+    const uint64_t counted = __hip_atomic_load(ctl_count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t err = __hip_atomic_load(ctl_err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // both in flight
+    s_epoch = static_cast<uint32_t>(counted / NWG) + 1u;
+    s_abort = err != 0u;
   }
   __syncthreads();
   const uint32_t epoch = s_epoch;
@@ -162,6 +170,20 @@ __global__ void __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 
   float xf[32];
 #pragma unroll
   for (int i = 0; i < 4; ++i) unpack_bf16x8(xq[i], xf + 8 * i);
+  if (a.norm_w) {
+    // RMSNorm in obs_rmsnorm's sequence (the lane owns 2048/64 contiguous
+    // columns): serial fma of x^2, wave butterfly, sqrt(ss/2048 + eps), then
+    // x/rms*w rounded to bf16 — bit-identical to the standalone kernel.
+    float ss = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 32; ++c) ss = __builtin_fmaf(xf[c], xf[c], ss);
+    const float rms = __builtin_sqrtf(wave_sum_asc(ss) / static_cast<float>(FH) + a.rms_eps);
+    float wf[32];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) unpack_bf16x8(nq[i], wf + 8 * i);
+#pragma unroll
+    for (int c = 0; c < 32; ++c) xf[c] = bf16_to_f32(f32_to_bf16((xf[c] / rms) * wf[c]));
+  }
   float xs = 0.0f;
 #pragma unroll
   for (int c = 0; c < 32; ++c) xs = xs + xf[c];
@@ -461,7 +483,7 @@ int launch_fused_decode(obs_ctx* ctx, const obs_moe_config* cfg, const obs_moe_l
     OBS_HIP_TRY(ctx, hipDeviceSynchronize());
   }
   FusedArgs a{L->gate_w, L->gate_s, L->gate_b, L->up_w, L->up_s, L->up_b, L->down_w, L->down_s, L->down_b,
-              L->router_w, L->router_s, L->router_b, x, residual, y, ids_out, w_out,
+              L->router_w, L->router_s, L->router_b, x, residual, y, L->norm_w, cfg->rms_eps, ids_out, w_out,
               static_cast<unsigned char*>(ctx->fused_ws), cfg->n_exp, cfg->norm_topk};
   if (cfg->n_exp <= 128)
     OBS_LAUNCH(ctx, "decode_fused", decode_fused_kernel<2><<<NWG, 256, 0, ctx->stream>>>(a));

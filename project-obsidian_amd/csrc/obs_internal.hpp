@@ -84,6 +84,10 @@ inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_
 // Workspace for decode: returns device pointer of at least `bytes`.
 int ensure_decode_ws(obs_ctx* ctx, size_t bytes, void** out);
 
+// RMSNorm of rows x dim bf16 (obs_elementwise.hip); dim % 64 == 0, <= 8192.
+int launch_rmsnorm(obs_ctx* ctx, const uint16_t* x, const uint16_t* w, uint16_t* out, uint32_t rows, uint32_t dim,
+                   float eps);
+
 // Fused single-launch decode (obs_decode_fused.hip).
 bool fused_decode_supported(const obs_moe_config* cfg);
 size_t fused_decode_ws_bytes();

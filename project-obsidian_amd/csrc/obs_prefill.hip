@@ -570,7 +570,7 @@ __global__ void __launch_bounds__(512) combine_kernel(const uint16_t* __restrict
 constexpr size_t al256(size_t v) { return (v + 255) & ~size_t(255); }
 
 struct PrefillWs {
-  size_t logits, ids, w, counts, offsets, ntiles, chunk_cnt, row_token, row_slot, tiles, H, Yp, total;
+  size_t logits, ids, w, counts, offsets, ntiles, chunk_cnt, row_token, row_slot, tiles, H, Yp, Xn, total;
   uint32_t max_tiles, nchunks;
 };
 
@@ -592,6 +592,7 @@ PrefillWs prefill_layout(const obs_moe_config* cfg, uint32_t T) {
   L.tiles = o; o += al256(sizeof(int4) * L.max_tiles);
   L.H = o; o += al256(sizeof(uint16_t) * R * cfg->inter);
   L.Yp = o; o += al256(sizeof(uint16_t) * R * cfg->hidden);
+  L.Xn = o; o += al256(sizeof(uint16_t) * static_cast<size_t>(T) * cfg->hidden);  // rmsnorm(X) when layer->norm_w
   L.total = o;
   return L;
 }
@@ -652,10 +653,17 @@ int obs_moe_prefill(obs_ctx* ctx, const obs_moe_config* cfg, const obs_moe_layer
   if (!obs::aligned(X, 16) || !obs::aligned(Y, 16) || (residual && !obs::aligned(residual, 16)) || !obs::aligned(ws, 256))
     return obs::set_error(ctx, OBS_E_ALIGN, "obs_moe_prefill: X/Y/residual need 16-byte, ws 256-byte alignment");
   char* base = static_cast<char*>(ws);
+  const uint16_t* Xin = X;  // the MoE input: X, or rmsnorm(X) (forward.rs:419-421); X stays the caller's
+  if (layer->norm_w) {
+    uint16_t* Xn = reinterpret_cast<uint16_t*>(base + L.Xn);
+    rc = obs::launch_rmsnorm(ctx, X, layer->norm_w, Xn, T, H, cfg->rms_eps);
+    if (rc) return rc;
+    Xin = Xn;
+  }
   int32_t* d_ids = reinterpret_cast<int32_t*>(base + L.ids);
   float* d_w = reinterpret_cast<float*>(base + L.w);
   if (!ids) {
-    rc = obs::launch_gate_logits(ctx, layer->router_w, layer->router_s, layer->router_b, X,
+    rc = obs::launch_gate_logits(ctx, layer->router_w, layer->router_s, layer->router_b, Xin,
                                  reinterpret_cast<float*>(base + L.logits), T, H, E, cfg->group);
     if (rc) return rc;
     rc = obs::launch_route_topk(ctx, reinterpret_cast<float*>(base + L.logits), d_ids, d_w, T, E, k, cfg->norm_topk);
@@ -678,7 +686,7 @@ int obs_moe_prefill(obs_ctx* ctx, const obs_moe_config* cfg, const obs_moe_layer
   OBS_LAUNCH(ctx, "moe_group_rank", group_rank_kernel<<<L.nchunks, 64, 0, ctx->stream>>>(ids, T, k, E, chunk_cnt,
                                                                                           row_token, row_slot));
   GemmArgs g{};
-  g.A = X; g.a_rows = row_token; g.a_rows_total = T;
+  g.A = Xin; g.a_rows = row_token; g.a_rows_total = T;
   g.w0 = layer->gate_w; g.s0 = layer->gate_s; g.b0 = layer->gate_b;
   g.w1 = layer->up_w; g.s1 = layer->up_s; g.b1 = layer->up_b;
   g.out = Hbuf; g.out_rows = nullptr;

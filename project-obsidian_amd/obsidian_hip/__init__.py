@@ -49,7 +49,7 @@ EXPORTS = (
     "obs_create", "obs_destroy", "obs_last_error", "obs_create_error", "obs_set_stream",
     "obs_get_stream", "obs_alloc", "obs_free", "obs_upload", "obs_download", "obs_memset",
     "obs_sync", "obs_timer_start", "obs_timer_stop", "obs_dequant", "obs_q4_matvec",
-    "obs_q4_matmul", "obs_q8_gate_logits", "obs_route_topk", "obs_swiglu", "obs_scaled_add",
+    "obs_q4_matmul", "obs_q8_gate_logits", "obs_route_topk", "obs_swiglu", "obs_scaled_add", "obs_rmsnorm",
     "obs_moe_decode", "obs_moe_prefill_workspace", "obs_moe_prefill", "obs_capture_begin",
     "obs_capture_end", "obs_graph_launch", "obs_graph_destroy", "obs_set_decode_path",
     "obs_device_status", "obs_stream_hold", "obs_profile_enable",
@@ -65,13 +65,14 @@ class ObsError(RuntimeError):
 
 class ObsMoeConfig(C.Structure):
     _fields_ = [("n_exp", C.c_uint32), ("top_k", C.c_uint32), ("hidden", C.c_uint32),
-                ("inter", C.c_uint32), ("group", C.c_uint32), ("norm_topk", C.c_int32)]
+                ("inter", C.c_uint32), ("group", C.c_uint32), ("norm_topk", C.c_int32),
+                ("rms_eps", C.c_float)]
 
 
 class ObsMoeLayer(C.Structure):
     _fields_ = [(n, C.c_void_p) for n in (
         "gate_w", "gate_s", "gate_b", "up_w", "up_s", "up_b", "down_w", "down_s", "down_b",
-        "router_w", "router_s", "router_b")]
+        "router_w", "router_s", "router_b", "norm_w")]
 
 
 _lib_handle = None
@@ -108,6 +109,7 @@ def lib() -> C.CDLL:
         "obs_route_topk": (i32, [vp, vp, vp, vp, u32, u32, u32, C.c_int]),
         "obs_swiglu": (i32, [vp, vp, vp, vp, u32]),
         "obs_scaled_add": (i32, [vp, vp, vp, f32, u32]),
+        "obs_rmsnorm": (i32, [vp, vp, vp, vp, u32, u32, f32]),
         "obs_moe_decode": (i32, [vp, C.POINTER(ObsMoeConfig), C.POINTER(ObsMoeLayer), vp, vp, vp, vp, vp]),
         "obs_moe_prefill_workspace": (sz, [C.POINTER(ObsMoeConfig), u32]),
         "obs_moe_prefill": (i32, [vp, C.POINTER(ObsMoeConfig), C.POINTER(ObsMoeLayer), vp, vp, vp, u32,
@@ -320,6 +322,9 @@ class ObsidianExecutor:
     def scaled_add_raw(self, acc, y, scale: float, n: int) -> None:
         self._check(lib().obs_scaled_add(self.ctx, _ptr(acc), _ptr(y), float(scale), n))
 
+    def rmsnorm_raw(self, x, w, out, rows: int, dim: int, eps: float) -> None:
+        self._check(lib().obs_rmsnorm(self.ctx, _ptr(x), _ptr(w), _ptr(out), rows, dim, float(eps)))
+
     def moe_decode(self, cfg: "MoeConfig", layer: "MoeLayer", x, y, residual=None, ids_out=None,
                    w_out=None) -> None:
         c, l = cfg.to_c(), layer.to_c()
@@ -348,9 +353,11 @@ class MoeConfig:
     inter: int = 768
     group: int = 64
     norm_topk: bool = True
+    rms_eps: float = 1e-6  # rms_norm_eps (model.rs:18); used when the layer has norm_w
 
     def to_c(self) -> ObsMoeConfig:
-        return ObsMoeConfig(self.n_exp, self.top_k, self.hidden, self.inter, self.group, int(bool(self.norm_topk)))
+        return ObsMoeConfig(self.n_exp, self.top_k, self.hidden, self.inter, self.group, int(bool(self.norm_topk)),
+                            float(self.rms_eps))
 
 
 PROJ_KEYS = ("gate_w", "gate_s", "gate_b", "up_w", "up_s", "up_b", "down_w", "down_s", "down_b",
@@ -366,10 +373,15 @@ class MoeLayer:
 
     @classmethod
     def upload(cls, exe: ObsidianExecutor, tensors: Dict[str, np.ndarray]) -> "MoeLayer":
-        return cls({k: exe.upload(tensors[k]).ptr for k in PROJ_KEYS})
+        """tensors: the PROJ_KEYS arrays, plus optionally "norm_w" (the layer's
+        post_attention_layernorm.weight, bf16 [hidden], forward.rs:419)."""
+        ptrs = {k: exe.upload(tensors[k]).ptr for k in PROJ_KEYS}
+        if tensors.get("norm_w") is not None:
+            ptrs["norm_w"] = exe.upload(tensors["norm_w"]).ptr
+        return cls(ptrs)
 
     def to_c(self) -> ObsMoeLayer:
-        return ObsMoeLayer(*[self.ptrs[k] for k in PROJ_KEYS])
+        return ObsMoeLayer(*[self.ptrs[k] for k in PROJ_KEYS], self.ptrs.get("norm_w"))
 
 
 class MoeRouter:
@@ -433,3 +445,12 @@ def swiglu(exe: ObsidianExecutor, g: DeviceBuffer, u: DeviceBuffer, n: int) -> D
 def scaled_add(exe: ObsidianExecutor, acc: DeviceBuffer, y: DeviceBuffer, scale: float, n: int) -> None:
     """forward.rs:376-380: acc += scale * y (in place)."""
     exe.scaled_add_raw(acc, y, scale, n)
+
+
+def rmsnorm(exe: ObsidianExecutor, x: DeviceBuffer, w: DeviceBuffer, dim: int, rows: int = 1,
+            eps: float = 1e-6) -> DeviceBuffer:
+    """forward.rs:345-357 (Model::rmsnorm, rmsnorm.metal): a new bf16 [rows, dim]
+    buffer holding rmsnorm(x) * w."""
+    out = exe.alloc((rows, dim), np.uint16)
+    exe.rmsnorm_raw(x, w, out, rows, dim, eps)
+    return out

@@ -58,6 +58,34 @@ def test_moe_decode_config2(exe, qwen_layer, path, seed):
     print(f"seed {seed}: ids {list(gi)} rel err {rel:.2e}")
 
 
+@pytest.mark.parametrize("seed", [0, 1])
+def test_moe_decode_with_post_attention_norm(exe, qwen_layer, path, seed):
+    """forward.rs:419-440: x1n = rmsnorm(x1) feeds the router and experts and
+    the combine accumulates into x1. With the layer's norm weight set, the
+    layer equals the oracle on O.rmsnorm(x1): ids and weights bit-exact (the
+    norm is bit-exact), output within 1e-2 of fp64 with x1 as residual."""
+    t, _, L = qwen_layer
+    rng = np.random.default_rng(2000 + seed)
+    norm_w = synth.bf16_normal(rng, 2048, 0.5)
+    layer = oh.MoeLayer.upload(exe, dict(t, norm_w=norm_w))
+    cfg = oh.MoeConfig(128, 8, 2048, 768, 64, True, rms_eps=1e-6)
+    x1 = synth.bf16_normal(rng, 2048, 3.0)
+    dx = exe.upload(x1)
+    y = exe.alloc(2048, np.uint16)
+    ids = exe.alloc(8, np.int32)
+    w = exe.alloc(8, np.float32)
+    exe.moe_decode(cfg, layer, dx, y, residual=dx, ids_out=ids, w_out=w)
+    exe.device_status()
+    x1n = O.rmsnorm(x1, norm_w, 1e-6)
+    _, ri, rw = O.router(L, x1n, 8, True)
+    gi, gw = ids.download(), w.download()
+    assert np.array_equal(gi, ri[0])
+    assert np.array_equal(gw.view(np.uint32), rw[0].view(np.uint32))
+    y64, _, _ = O.moe_decode(L, x1n, 8, True, ids=gi[None], w=gw[None])
+    rel = _check_close(y.download(), y64[0] + synth.bf16_bits_to_f32(x1).astype(np.float64))
+    print(f"norm seed {seed}: rel err {rel:.2e}")
+
+
 def test_moe_decode_fused_matches_multi_and_repeats(exe, qwen_layer):
     """Many back-to-back fused launches (device-side epoch advances every
     launch) agree with the 4-launch path to bf16 rounding."""

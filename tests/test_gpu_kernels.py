@@ -10,6 +10,7 @@ import numpy as np
 import pytest
 
 import oracle as O
+import obsidian_hip as oh
 from obsidian_hip import synth
 
 pytestmark = pytest.mark.gpu
@@ -161,6 +162,31 @@ def test_swiglu_and_scaled_add(exe):
     exe.scaled_add_raw(da, exe.upload(y), 0.37, n)
     exact = np.float32(0.37).astype(np.float64) * _f32(y).astype(np.float64) + _f32(acc).astype(np.float64)
     assert np.array_equal(da.download(), synth.f32_to_bf16_bits(exact.astype(np.float32)))
+
+
+@pytest.mark.parametrize("rows,dim", [(1, 2048), (7, 2048), (300, 2048), (5, 1024), (3, 4096), (4, 192)])
+def test_rmsnorm_bit_exact(exe, rows, dim):
+    """obs_rmsnorm (rmsnorm.metal / Model::rmsnorm) equals the oracle bit for
+    bit: same sum-of-squares order, IEEE sqrt and division, one bf16 rounding.
+    dim 192 takes the generic (unvectorized) kernel."""
+    rng = np.random.default_rng(rows * 7 + dim)
+    x = synth.bf16_normal(rng, (rows, dim), 2.0)
+    w = synth.bf16_normal(rng, dim, 1.0)
+    eps = 1e-6
+    out = exe.alloc((rows, dim), np.uint16)
+    dx, dw = exe.upload(x), exe.upload(w)
+    exe.rmsnorm_raw(dx, dw, out, rows, dim, eps)
+    want = O.rmsnorm(x, w, eps)
+    assert np.array_equal(out.download(), want)
+    exe.rmsnorm_raw(dx, dw, dx, rows, dim, eps)  # in place (x and out alias)
+    assert np.array_equal(dx.download(), want)
+
+
+def test_rmsnorm_rejects_bad_dim(exe):
+    buf = exe.alloc(256, np.uint16)
+    with pytest.raises(oh.ObsError) as e:
+        exe.rmsnorm_raw(buf, buf, buf, 1, 100, 1e-6)
+    assert e.value.code == oh.OBS_E_SHAPE
 
 
 def test_argument_validation_errors(exe):

@@ -142,6 +142,23 @@ def test_moe_prefill_computed_routing_and_residual(exe, qwen):
     _close(y, ref, 1e-2)
 
 
+def test_moe_prefill_with_post_attention_norm(exe, qwen):
+    """forward.rs:419-421 in prefill: with the layer's norm weight the routing
+    and the experts see rmsnorm(X); the residual stays X."""
+    t, _, L = qwen
+    rng = np.random.default_rng(901)
+    norm_w = synth.bf16_normal(rng, H, 0.5)
+    layer = oh.MoeLayer.upload(exe, dict(t, norm_w=norm_w))
+    cfg = oh.MoeConfig(E, K, H, I, 64, True, rms_eps=1e-6)
+    T = 40
+    X = synth.bf16_normal(rng, (T, H), 3.0)
+    y = _f32(_prefill(exe, cfg, layer, X, residual=X))
+    Xn = O.rmsnorm(X, norm_w, 1e-6)
+    _, ids, w = O.router(L, Xn, K, True)
+    ref = O.moe_prefill(L, Xn, ids, w, O.MODE_F64) + _f32(X)
+    _close(y, ref, 1e-2)
+
+
 def test_moe_prefill_t2048_matches_decode(exe, qwen):
     """Config 3 size: every token of a T=2048 prefill (routing computed on the
     GPU) equals the fused decode of that token, within tolerance."""

@@ -4,7 +4,8 @@ checks, brute force and invariants — never against a retyped copy of itself.
 Reference semantics pinned here: validate_dequant.py:26-30 (unpack),
 fused_dequant_matvec_4bit.metal:29-52 (serial mat-vec), dequant_matvec_8bit.metal
 (8-bit router gate), moe_routing_topk.metal:31-56 (softmax/top-k/renorm),
-ops.metal:18-29 (SwiGLU, scaled add), forward.rs:200-232 / :421-441 (compositions).
+ops.metal:18-29 (SwiGLU, scaled add), rmsnorm.metal:17-35 (RMSNorm),
+forward.rs:200-232 / :421-441 (compositions).
 """
 import math
 from fractions import Fraction
@@ -198,6 +199,62 @@ def test_exp_against_libm():
     assert math.isinf(O.exp(88.6)) and math.isnan(O.exp(float("nan")))
     srt = got[np.argsort(xs[::7], kind="stable")]
     assert np.all(np.diff(srt.astype(np.float64)) >= 0)  # monotone on the grid
+
+
+# ---------------------------------------------------------------- RMSNorm
+def test_rmsnorm_constant_row_closed_form():
+    """x = c everywhere, w = 1: every partial sum is exact (c^2 has 16
+    significant bits), so ss = dim * c^2 and out = bf16(c / sqrtf(c^2 + eps))."""
+    for c_bits, eps in ((0x3FC0, 0.0), (0x3FC0, 1e-6), (0xC0A0, 1e-5), (0x3C23, 1e-6)):
+        x = np.full((2, 2048), c_bits, np.uint16)
+        w = np.full(2048, 0x3F80, np.uint16)
+        c = np.float32(synth.bf16_bits_to_f32(np.array([c_bits], np.uint16))[0])
+        rms = np.sqrt(np.float32(c * c) + np.float32(eps), dtype=np.float32)
+        want = synth.f32_to_bf16_bits(np.array([c / rms], np.float32))[0]
+        assert np.all(O.rmsnorm(x, w, eps) == want)
+    # c = 1.5, eps = 0: rms = 1.5 exactly, out = 1.0 exactly
+    assert np.all(O.rmsnorm(np.full((1, 1024), 0x3FC0, np.uint16), np.full(1024, 0x3F80, np.uint16), 0.0) == 0x3F80)
+
+
+def test_rmsnorm_scale_invariance_without_eps():
+    """With eps = 0, doubling x scales ss by 4, rms by 2 (exactly, IEEE sqrt)
+    and leaves x / rms unchanged bit for bit."""
+    rng = np.random.default_rng(11)
+    x = synth.bf16_normal(rng, (5, 2048))
+    w = synth.bf16_normal(rng, 2048)
+    x2 = synth.f32_to_bf16_bits(synth.bf16_bits_to_f32(x) * np.float32(2.0))
+    assert np.array_equal(O.rmsnorm(x, w, 0.0), O.rmsnorm(x2, w, 0.0))
+
+
+def test_rmsnorm_against_fp64_restatement():
+    """An fp64 restatement of rmsnorm.metal:20-34: every output within one
+    bf16 rounding (plus fp32 noise) of the exact value."""
+    rng = np.random.default_rng(12)
+    for dim in (64, 1024, 2048, 4096):
+        x = synth.bf16_normal(rng, (9, dim), 3.0)
+        w = synth.bf16_normal(rng, dim)
+        got = synth.bf16_bits_to_f32(O.rmsnorm(x, w, 1e-6)).astype(np.float64)
+        xf = synth.bf16_bits_to_f32(x).astype(np.float64)
+        ref = xf / np.sqrt((xf ** 2).mean(axis=1, keepdims=True) + 1e-6) * synth.bf16_bits_to_f32(w)
+        assert np.all(np.abs(got - ref) <= np.abs(ref) * (2.0 ** -8 + 1e-5) + 1e-30)
+
+
+def test_rmsnorm_sum_order_is_exact_on_integers():
+    """Small integers keep every partial sum exact, so the lane butterfly
+    gives the true sum of squares: out = bf16((x / sqrt(mean x^2)) * w)."""
+    rng = np.random.default_rng(13)
+    xi = rng.integers(-8, 9, size=(4, 512)).astype(np.float32)
+    x = synth.f32_to_bf16_bits(xi)
+    w = np.full(512, 0x3F80, np.uint16)
+    rms = np.sqrt((xi.astype(np.float64) ** 2).sum(axis=1, keepdims=True).astype(np.float32) / np.float32(512),
+                  dtype=np.float32)
+    want = synth.f32_to_bf16_bits((xi / rms).astype(np.float32))
+    assert np.array_equal(O.rmsnorm(x, w, 0.0), want)
+
+
+def test_rmsnorm_rejects_bad_dim():
+    with pytest.raises(ValueError):
+        O.rmsnorm(np.zeros((1, 100), np.uint16), np.zeros(100, np.uint16), 1e-6)
 
 
 def test_silu_mul_closed_form():
