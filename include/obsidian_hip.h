@@ -173,8 +173,8 @@ int obs_scaled_add(obs_ctx* ctx, uint16_t* acc, const uint16_t* y, float scale, 
 
 /* RMSNorm of `rows` rows of `dim` bf16 values — shaders/rmsnorm.metal (the
  * rmsnorm pipeline) / Model::rmsnorm (forward.rs:345-357):
- * rms = sqrt(sum(x^2) / dim + eps), out = (x / rms) * weight, fp32 math,
- * rounded once to bf16. sum(x^2) has a fixed order (64 lanes each own dim/64
+ * inv = 1 / sqrt(sum(x^2) / dim + eps) once per row, out = (x * inv) * weight,
+ * fp32 math, rounded once to bf16. sum(x^2) has a fixed order (64 lanes each own dim/64
  * contiguous columns, serial fma, then an xor butterfly), so the result is
  * reproducible bit for bit. dim % 64 == 0, dim <= 8192; x and out may alias. */
 int obs_rmsnorm(obs_ctx* ctx, const uint16_t* x, const uint16_t* weight, uint16_t* out,

@@ -22,7 +22,7 @@
  *                                 permutes ids, renormalised weights sum to 1,
  *                                 closed form w_i = e_i / sum_sel e_j.
  *   orc_rmsnorm ................. closed form for a constant row (x = c, w = 1:
- *                                 ss = dim c^2 exactly, out = bf16(c / sqrtf(c^2 + eps))),
+ *                                 ss = dim c^2 exactly, out = bf16(c * (1 / sqrtf(c^2 + eps)))),
  *                                 exact invariance under x -> 2x when eps = 0, an fp64
  *                                 numpy restatement within one bf16 step, and the
  *                                 butterfly order equal to a serial sum where exact.
@@ -336,9 +336,9 @@ int orc_rmsnorm(const uint16_t* x, const uint16_t* w, float eps, int64_t rows, i
       for (int l = 0; l < 64; ++l) nxt[l] = part[l] + part[l ^ off];
       memcpy(part, nxt, sizeof(nxt));
     }
-    const float rms = sqrtf(part[0] / (float)dim + eps);
+    const float inv = 1.0f / sqrtf(part[0] / (float)dim + eps);
     for (int64_t c = 0; c < dim; ++c)
-      out[r * dim + c] = orc_f32_to_bf16((orc_bf16_to_f32(xr[c]) / rms) * orc_bf16_to_f32(w[c]));
+      out[r * dim + c] = orc_f32_to_bf16((orc_bf16_to_f32(xr[c]) * inv) * orc_bf16_to_f32(w[c]));
   }
   return 0;
 }

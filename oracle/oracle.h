@@ -94,7 +94,9 @@ int orc_route_topk(const float* logits, int64_t T, int n_exp, int k, int norm_to
  * rows x dim, bf16 in and out. ss = sum of x^2 in the documented lane order
  * (64 lanes each own dim/64 contiguous columns and accumulate x*x serially with
  * fmaf from 0; lanes combined by the xor butterfly with offsets 1, 2, ..., 32);
- * rms = sqrtf(ss / dim + eps); out = RNE_bf16((x / rms) * w), IEEE division.
+ * inv = 1 / sqrtf(ss / dim + eps) (IEEE sqrt and division, once per row);
+ * out = RNE_bf16((x * inv) * w). (rmsnorm.metal divides each x by rms under
+ * Metal fast math; one reciprocal per row is the restated form.)
  * dim % 64 == 0. Returns 0, or -1 on a bad shape. */
 int orc_rmsnorm(const uint16_t* x, const uint16_t* w, float eps, int64_t rows, int64_t dim, uint16_t* out);
 

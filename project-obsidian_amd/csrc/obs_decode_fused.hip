@@ -172,17 +172,17 @@ __global__ void __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 
   for (int i = 0; i < 4; ++i) unpack_bf16x8(xq[i], xf + 8 * i);
   if (a.norm_w) {
     // RMSNorm in obs_rmsnorm's sequence (the lane owns 2048/64 contiguous
-    // columns): serial fma of x^2, wave butterfly, sqrt(ss/2048 + eps), then
-    // x/rms*w rounded to bf16 — bit-identical to the standalone kernel.
+    // columns): serial fma of x^2, wave butterfly, 1/sqrt(ss/2048 + eps), then
+    // x*inv*w rounded to bf16 — bit-identical to the standalone kernel.
     float ss = 0.0f;
 #pragma unroll
     for (int c = 0; c < 32; ++c) ss = __builtin_fmaf(xf[c], xf[c], ss);
-    const float rms = __builtin_sqrtf(wave_sum_asc(ss) / static_cast<float>(FH) + a.rms_eps);
+    const float inv = 1.0f / __builtin_sqrtf(wave_sum_asc(ss) / static_cast<float>(FH) + a.rms_eps);
     float wf[32];
 #pragma unroll
     for (int i = 0; i < 4; ++i) unpack_bf16x8(nq[i], wf + 8 * i);
 #pragma unroll
-    for (int c = 0; c < 32; ++c) xf[c] = bf16_to_f32(f32_to_bf16((xf[c] / rms) * wf[c]));
+    for (int c = 0; c < 32; ++c) xf[c] = bf16_to_f32(f32_to_bf16((xf[c] * inv) * wf[c]));
   }
   float xs = 0.0f;
 #pragma unroll

@@ -22,7 +22,9 @@ __global__ void __launch_bounds__(256) scaled_add_kernel(uint16_t* __restrict__ 
 }
 // One wave per row; lane l owns the dim/64 contiguous columns [l*c, (l+1)*c).
 // sum(x^2): serial fma over the lane's columns, then wave_sum_asc (the xor
-// butterfly 1..32) — the fused decode kernel computes the same sequence.
+// butterfly 1..32); inv = 1/sqrt(sum/dim + eps) with IEEE sqrt and division
+// once per row; out = (x * inv) * w — the fused decode kernel computes the
+// same sequence.
 // C = dim/64 when it is a multiple of 8 (16-byte loads), else 0 (any dim).
 template <uint32_t C>
 __global__ void __launch_bounds__(256) rmsnorm_kernel(const uint16_t* x, const uint16_t* __restrict__ w,
@@ -47,7 +49,7 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(const uint16_t* x, const u
         acc = __builtin_fmaf(b, b, acc);
       }
     }
-    const float rms = __builtin_sqrtf(wave_sum_asc(acc) / static_cast<float>(dim) + eps);
+    const float inv = 1.0f / __builtin_sqrtf(wave_sum_asc(acc) / static_cast<float>(dim) + eps);
 #pragma unroll
     for (uint32_t i = 0; i < C / 8; ++i) {
       const uint4 wv = reinterpret_cast<const uint4*>(w + c0)[i];
@@ -55,7 +57,7 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(const uint16_t* x, const u
       uint32_t o[4];
 #pragma unroll
       for (uint32_t j = 0; j < 4; ++j)
-        o[j] = pack_bf16x2((bf16lo(xd[j]) / rms) * bf16lo(wdd[j]), (bf16hi(xd[j]) / rms) * bf16hi(wdd[j]));
+        o[j] = pack_bf16x2((bf16lo(xd[j]) * inv) * bf16lo(wdd[j]), (bf16hi(xd[j]) * inv) * bf16hi(wdd[j]));
       reinterpret_cast<uint4*>(orow)[i] = make_uint4(o[0], o[1], o[2], o[3]);
     }
   } else {
@@ -64,9 +66,9 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(const uint16_t* x, const u
       const float v = bf16_to_f32(xr[c]);
       acc = __builtin_fmaf(v, v, acc);
     }
-    const float rms = __builtin_sqrtf(wave_sum_asc(acc) / static_cast<float>(dim) + eps);
+    const float inv = 1.0f / __builtin_sqrtf(wave_sum_asc(acc) / static_cast<float>(dim) + eps);
     float nv[128];  // chunk <= 128 (dim <= 8192): read all before writing (x and out may alias)
-    for (uint32_t c = 0; c < chunk; ++c) nv[c] = (bf16_to_f32(xr[c]) / rms) * bf16_to_f32(w[c0 + c]);
+    for (uint32_t c = 0; c < chunk; ++c) nv[c] = (bf16_to_f32(xr[c]) * inv) * bf16_to_f32(w[c0 + c]);
     for (uint32_t c = 0; c < chunk; ++c) orow[c] = f32_to_bf16(nv[c]);
   }
 }

@@ -204,21 +204,22 @@ def test_exp_against_libm():
 # ---------------------------------------------------------------- RMSNorm
 def test_rmsnorm_constant_row_closed_form():
     """x = c everywhere, w = 1: every partial sum is exact (c^2 has 16
-    significant bits), so ss = dim * c^2 and out = bf16(c / sqrtf(c^2 + eps))."""
+    significant bits), so ss = dim * c^2 and out = bf16(c * (1 / sqrtf(c^2 + eps)))."""
     for c_bits, eps in ((0x3FC0, 0.0), (0x3FC0, 1e-6), (0xC0A0, 1e-5), (0x3C23, 1e-6)):
         x = np.full((2, 2048), c_bits, np.uint16)
         w = np.full(2048, 0x3F80, np.uint16)
         c = np.float32(synth.bf16_bits_to_f32(np.array([c_bits], np.uint16))[0])
         rms = np.sqrt(np.float32(c * c) + np.float32(eps), dtype=np.float32)
-        want = synth.f32_to_bf16_bits(np.array([c / rms], np.float32))[0]
+        want = synth.f32_to_bf16_bits(np.array([c * (np.float32(1.0) / rms)], np.float32))[0]
         assert np.all(O.rmsnorm(x, w, eps) == want)
     # c = 1.5, eps = 0: rms = 1.5 exactly, out = 1.0 exactly
     assert np.all(O.rmsnorm(np.full((1, 1024), 0x3FC0, np.uint16), np.full(1024, 0x3F80, np.uint16), 0.0) == 0x3F80)
 
 
 def test_rmsnorm_scale_invariance_without_eps():
-    """With eps = 0, doubling x scales ss by 4, rms by 2 (exactly, IEEE sqrt)
-    and leaves x / rms unchanged bit for bit."""
+    """With eps = 0, doubling x scales ss by 4, rms by 2 and 1/rms by 1/2
+    (exactly: IEEE sqrt and division of powers of two) and leaves x * (1/rms)
+    unchanged bit for bit."""
     rng = np.random.default_rng(11)
     x = synth.bf16_normal(rng, (5, 2048))
     w = synth.bf16_normal(rng, 2048)
@@ -241,14 +242,14 @@ def test_rmsnorm_against_fp64_restatement():
 
 def test_rmsnorm_sum_order_is_exact_on_integers():
     """Small integers keep every partial sum exact, so the lane butterfly
-    gives the true sum of squares: out = bf16((x / sqrt(mean x^2)) * w)."""
+    gives the true sum of squares: out = bf16(x * (1 / sqrt(mean x^2)) * w)."""
     rng = np.random.default_rng(13)
     xi = rng.integers(-8, 9, size=(4, 512)).astype(np.float32)
     x = synth.f32_to_bf16_bits(xi)
     w = np.full(512, 0x3F80, np.uint16)
     rms = np.sqrt((xi.astype(np.float64) ** 2).sum(axis=1, keepdims=True).astype(np.float32) / np.float32(512),
                   dtype=np.float32)
-    want = synth.f32_to_bf16_bits((xi / rms).astype(np.float32))
+    want = synth.f32_to_bf16_bits((xi * (np.float32(1.0) / rms)).astype(np.float32))
     assert np.array_equal(O.rmsnorm(x, w, 0.0), want)
 
 
