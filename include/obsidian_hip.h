@@ -252,6 +252,74 @@ int obs_moe_prefill(obs_ctx* ctx, const obs_moe_config* cfg, const obs_moe_layer
                     const uint16_t* X, const uint16_t* residual, uint16_t* Y, uint32_t T,
                     const int32_t* ids, const float* weights, void* ws, size_t ws_bytes);
 
+/* ------------------------------------------------------------------ */
+/* Checkpoint loading: safetensors -> HBM-resident expert table        */
+/* (replaces Qwen3MoeConfig::from_file model.rs:26-30,                 */
+/*  Weights::load_non_expert weight_loader.rs:19-71, ExpertIndex::open */
+/*  disk_io.rs:36-63 and read_experts_parallel disk_io.rs:79-102)      */
+/* ------------------------------------------------------------------ */
+
+/* safetensors dtypes (the crate's Dtype names, safetensors 0.4.5). */
+enum {
+  OBS_DT_BOOL = 0, OBS_DT_U8 = 1, OBS_DT_I8 = 2, OBS_DT_F8_E5M2 = 3, OBS_DT_F8_E4M3 = 4,
+  OBS_DT_I16 = 5, OBS_DT_U16 = 6, OBS_DT_F16 = 7, OBS_DT_BF16 = 8, OBS_DT_I32 = 9,
+  OBS_DT_U32 = 10, OBS_DT_F32 = 11, OBS_DT_F64 = 12, OBS_DT_I64 = 13, OBS_DT_U64 = 14,
+};
+
+typedef struct obs_tensor_info {
+  int32_t dtype;      /* OBS_DT_* of the bytes on disk */
+  uint32_t ndim;
+  uint64_t shape[8];
+  uint64_t nbytes;    /* bytes on disk (prod(shape) * dtype size) */
+  uint32_t n_pieces;  /* 1 for a stored tensor; num_experts when gathered from split files */
+} obs_tensor_info;
+
+typedef struct obs_ckpt obs_ckpt;
+
+/* Opens a model directory (host only, no device work): config.json
+ * (model.rs:26-30), model.safetensors.index.json's weight_map
+ * (weight_loader.rs:20-30) or a single model.safetensors, and the split
+ * expert files <expert_dir>/layer_{l}_experts.safetensors
+ * (tools/split_experts.py:9-19); expert_dir NULL probes
+ * <model_dir>/splitted_moe (main.rs:70-73). Files are opened and their
+ * headers validated on first use. On failure *out is NULL and
+ * obs_ckpt_error(NULL) holds the message (per thread). */
+int obs_ckpt_open(const char* model_dir, const char* expert_dir, obs_ckpt** out);
+void obs_ckpt_close(obs_ckpt* ck);
+/* Message of the last failed call on ck; ck NULL: of this thread's last failed open. */
+const char* obs_ckpt_error(const obs_ckpt* ck);
+
+/* MoE shape from config.json (Qwen3MoeConfig, model.rs:7-23): the reference's
+ * required fields must be present; group from quantization.group_size
+ * (default 64, as forward.rs:306 fixes it); n_layers may be NULL. */
+int obs_ckpt_config(obs_ckpt* ck, obs_moe_config* cfg, uint32_t* n_layers);
+
+/* Describes a tensor. Stacked names model.layers.{l}.mlp.switch_mlp.{proj}.{kind}
+ * resolve to the stored stacked tensor, else to the split files' e{N}.{proj}.{kind}
+ * gathered in expert order (disk_io.rs:47-55 parses the same names). */
+int obs_ckpt_tensor_info(obs_ckpt* ck, const char* name, obs_tensor_info* info);
+/* Reads a tensor's on-disk bytes into host memory (bytes >= info.nbytes). */
+int obs_ckpt_read(obs_ckpt* ck, const char* name, void* dst_host, size_t bytes);
+
+/* Device bytes of one layer's table as obs_ckpt_load_moe_layer lays it out
+ * (13 tensors, each 256-byte aligned); 0 for an unsupported config. */
+size_t obs_moe_layer_bytes(const obs_moe_config* cfg);
+
+/* Loads layer `layer`'s expert table into dst_dev (device, 256-byte aligned,
+ * >= obs_moe_layer_bytes) and fills *out with pointers into it: the 4-bit
+ * switch_mlp tensors [E, ...], the 8-bit router gate mlp.gate [E, H/4] and
+ * post_attention_layernorm.weight (out->norm_w NULL if the checkpoint has
+ * none). Shapes and dtypes are checked against cfg (U32 weights; BF16 or F16
+ * scales, biases and norm; F16 is converted to bf16 on the device, round to
+ * nearest even). Reads run on host threads into a pinned ring and are copied
+ * to HBM on their own streams; the call returns when the table is resident.
+ * Replaces the per-token SSD paging of disk_io.rs:79-102 with a one-time load. */
+int obs_ckpt_load_moe_layer(obs_ctx* ctx, obs_ckpt* ck, uint32_t layer, const obs_moe_config* cfg,
+                            void* dst_dev, size_t bytes, obs_moe_layer* out);
+/* Loads one tensor's on-disk bytes (no conversion) to device memory
+ * (weight_loader.rs:61-66 copies each tensor into its own buffer). */
+int obs_ckpt_load_tensor(obs_ctx* ctx, obs_ckpt* ck, const char* name, void* dst_dev, size_t bytes);
+
 #ifdef __cplusplus
 }
 #endif

@@ -54,6 +54,8 @@ EXPORTS = (
     "obs_capture_end", "obs_graph_launch", "obs_graph_destroy", "obs_set_decode_path",
     "obs_device_status", "obs_stream_hold", "obs_profile_enable",
     "obs_profile_accumulate", "obs_profile_count", "obs_profile_stat", "obs_profile_clear",
+    "obs_ckpt_open", "obs_ckpt_close", "obs_ckpt_error", "obs_ckpt_config", "obs_ckpt_tensor_info",
+    "obs_ckpt_read", "obs_moe_layer_bytes", "obs_ckpt_load_moe_layer", "obs_ckpt_load_tensor",
 )
 
 
@@ -74,6 +76,21 @@ class ObsMoeLayer(C.Structure):
         "gate_w", "gate_s", "gate_b", "up_w", "up_s", "up_b", "down_w", "down_s", "down_b",
         "router_w", "router_s", "router_b", "norm_w")]
 
+
+class ObsTensorInfo(C.Structure):
+    _fields_ = [("dtype", C.c_int32), ("ndim", C.c_uint32), ("shape", C.c_uint64 * 8), ("nbytes", C.c_uint64),
+                ("n_pieces", C.c_uint32)]
+
+
+# OBS_DT_* codes -> (safetensors name, numpy dtype of the raw bytes; bf16 and fp8 as bit patterns)
+DTYPES = {
+    0: ("BOOL", np.bool_), 1: ("U8", np.uint8), 2: ("I8", np.int8), 3: ("F8_E5M2", np.uint8),
+    4: ("F8_E4M3", np.uint8), 5: ("I16", np.int16), 6: ("U16", np.uint16), 7: ("F16", np.float16),
+    8: ("BF16", np.uint16), 9: ("I32", np.int32), 10: ("U32", np.uint32), 11: ("F32", np.float32),
+    12: ("F64", np.float64), 13: ("I64", np.int64), 14: ("U64", np.uint64),
+}
+
+_DT_CODE = {v[0]: k for k, v in DTYPES.items()}
 
 _lib_handle = None
 
@@ -127,6 +144,15 @@ def lib() -> C.CDLL:
         "obs_profile_stat": (i32, [vp, C.c_int, C.POINTER(C.c_char_p), C.POINTER(C.c_double),
                                    C.POINTER(C.c_int64)]),
         "obs_profile_clear": (i32, [vp]),
+        "obs_ckpt_open": (i32, [C.c_char_p, C.c_char_p, C.POINTER(vp)]),
+        "obs_ckpt_close": (None, [vp]),
+        "obs_ckpt_error": (C.c_char_p, [vp]),
+        "obs_ckpt_config": (i32, [vp, C.POINTER(ObsMoeConfig), C.POINTER(u32)]),
+        "obs_ckpt_tensor_info": (i32, [vp, C.c_char_p, C.POINTER(ObsTensorInfo)]),
+        "obs_ckpt_read": (i32, [vp, C.c_char_p, vp, sz]),
+        "obs_moe_layer_bytes": (sz, [C.POINTER(ObsMoeConfig)]),
+        "obs_ckpt_load_moe_layer": (i32, [vp, vp, u32, C.POINTER(ObsMoeConfig), vp, sz, C.POINTER(ObsMoeLayer)]),
+        "obs_ckpt_load_tensor": (i32, [vp, vp, C.c_char_p, vp, sz]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -370,6 +396,7 @@ class MoeLayer:
     stacked switch_mlp tensors plus the 8-bit router gate (replaces the SSD
     ExpertIndex + expert_pool, disk_io.rs:36-102, forward.rs:79-89)."""
     ptrs: Dict[str, int] = field(default_factory=dict)
+    block: Optional[DeviceBuffer] = None  # the device block a checkpoint load filled
 
     @classmethod
     def upload(cls, exe: ObsidianExecutor, tensors: Dict[str, np.ndarray]) -> "MoeLayer":
@@ -454,3 +481,93 @@ def rmsnorm(exe: ObsidianExecutor, x: DeviceBuffer, w: DeviceBuffer, dim: int, r
     out = exe.alloc((rows, dim), np.uint16)
     exe.rmsnorm_raw(x, w, out, rows, dim, eps)
     return out
+
+
+@dataclass
+class TensorInfo:
+    dtype: str
+    shape: Tuple[int, ...]
+    nbytes: int
+    n_pieces: int
+
+
+class Checkpoint:
+    """A model directory on disk: config.json (Qwen3MoeConfig::from_file,
+    model.rs:26-30), the safetensors shards of model.safetensors.index.json
+    (Weights::load_non_expert, weight_loader.rs:19-71) and the split expert
+    files of tools/split_experts.py (ExpertIndex::open, disk_io.rs:36-63).
+
+    ``load_moe_layer`` makes one layer's stacked expert table resident in HBM
+    (replacing the per-token paging of read_experts_parallel, disk_io.rs:79-102).
+    Parsing and host reads need no GPU; loads go through the native library."""
+
+    def __init__(self, model_dir: str, expert_dir: Optional[str] = None):
+        L = lib()
+        h = C.c_void_p()
+        rc = L.obs_ckpt_open(os.fsencode(model_dir), os.fsencode(expert_dir) if expert_dir else None, C.byref(h))
+        if rc != OBS_OK:
+            raise ObsError(rc, L.obs_ckpt_error(None).decode())
+        self.h = h.value
+
+    def _check(self, rc: int) -> None:
+        if rc != OBS_OK:
+            raise ObsError(rc, lib().obs_ckpt_error(self.h).decode())
+
+    def config(self) -> Tuple[MoeConfig, int]:
+        """(MoeConfig, num_hidden_layers) from config.json."""
+        c, n = ObsMoeConfig(), C.c_uint32()
+        self._check(lib().obs_ckpt_config(self.h, C.byref(c), C.byref(n)))
+        return MoeConfig(c.n_exp, c.top_k, c.hidden, c.inter, c.group, bool(c.norm_topk), c.rms_eps), n.value
+
+    def tensor_info(self, name: str) -> TensorInfo:
+        i = ObsTensorInfo()
+        self._check(lib().obs_ckpt_tensor_info(self.h, name.encode(), C.byref(i)))
+        return TensorInfo(DTYPES[i.dtype][0], tuple(int(i.shape[k]) for k in range(i.ndim)), int(i.nbytes),
+                          int(i.n_pieces))
+
+    def read(self, name: str) -> np.ndarray:
+        """The tensor's on-disk bytes as a host array (bf16 as uint16 bit patterns)."""
+        info = self.tensor_info(name)
+        out = np.empty(info.shape, dtype=DTYPES[_DT_CODE[info.dtype]][1])
+        self._check(lib().obs_ckpt_read(self.h, name.encode(), out.ctypes.data, out.nbytes))
+        return out
+
+    def load_tensor(self, exe: ObsidianExecutor, name: str) -> DeviceBuffer:
+        info = self.tensor_info(name)
+        buf = exe.alloc(info.shape, DTYPES[_DT_CODE[info.dtype]][1])
+        exe._check(lib().obs_ckpt_load_tensor(exe.ctx, self.h, name.encode(), buf.ptr, buf.nbytes))
+        return buf
+
+    def load_moe_layer(self, exe: ObsidianExecutor, layer: int, cfg: Optional[MoeConfig] = None) -> MoeLayer:
+        """Layer `layer`'s expert table, router gate and post-attention norm in
+        one device block (bf16 scales; f16 ones converted on the device)."""
+        cfg = cfg or self.config()[0]
+        c = cfg.to_c()
+        nbytes = lib().obs_moe_layer_bytes(C.byref(c))
+        if nbytes == 0:
+            raise ObsError(OBS_E_SHAPE, f"unsupported layer config {cfg}")
+        block = exe.alloc((nbytes,), np.uint8)
+        out = ObsMoeLayer()
+        exe._check(lib().obs_ckpt_load_moe_layer(exe.ctx, self.h, layer, C.byref(c), block.ptr, nbytes,
+                                                   C.byref(out)))
+        ptrs = {k: getattr(out, k) for k in PROJ_KEYS}
+        if out.norm_w:
+            ptrs["norm_w"] = out.norm_w
+        return MoeLayer(ptrs, block)
+
+    def close(self) -> None:
+        if self.h:
+            lib().obs_ckpt_close(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -82,3 +82,94 @@ def bytes_per_expert(hidden: int = 2048, inter: int = 768, group: int = 64) -> i
 
 def router_bytes(n_exp: int = 128, hidden: int = 2048, group: int = 64) -> int:
     return n_exp * hidden + 2 * 2 * (n_exp * hidden // group)
+
+
+# Checkpoint tensor names of one layer's MoE block (MLX Qwen3-MoE checkpoints;
+# the split files of tools/split_experts.py:9-19 use e{N}.{proj}.{kind}).
+CKPT_NAMES = {
+    "gate_w": "mlp.switch_mlp.gate_proj.weight", "gate_s": "mlp.switch_mlp.gate_proj.scales",
+    "gate_b": "mlp.switch_mlp.gate_proj.biases", "up_w": "mlp.switch_mlp.up_proj.weight",
+    "up_s": "mlp.switch_mlp.up_proj.scales", "up_b": "mlp.switch_mlp.up_proj.biases",
+    "down_w": "mlp.switch_mlp.down_proj.weight", "down_s": "mlp.switch_mlp.down_proj.scales",
+    "down_b": "mlp.switch_mlp.down_proj.biases", "router_w": "mlp.gate.weight",
+    "router_s": "mlp.gate.scales", "router_b": "mlp.gate.biases",
+    "norm_w": "post_attention_layernorm.weight",
+}
+BF16_KEYS = ("gate_s", "gate_b", "up_s", "up_b", "down_s", "down_b", "router_s", "router_b", "norm_w")
+
+
+def hf_config(n_layers: int, n_exp: int = 128, top_k: int = 8, hidden: int = 2048, inter: int = 768,
+              group: int = 64, norm_topk: bool = True, rms_eps: float = 1e-6) -> dict:
+    """A Qwen3-MoE config.json (the fields of Qwen3MoeConfig, src/model.rs:9-22,
+    plus MLX's quantization block)."""
+    return {
+        "architectures": ["Qwen3MoeForCausalLM"], "model_type": "qwen3_moe",
+        "num_hidden_layers": n_layers, "hidden_size": hidden, "num_attention_heads": 32,
+        "num_key_value_heads": 4, "head_dim": 128, "num_experts": n_exp, "num_experts_per_tok": top_k,
+        "moe_intermediate_size": inter, "rms_norm_eps": rms_eps, "rope_theta": 10000000.0,
+        "vocab_size": 151936, "norm_topk_prob": norm_topk,
+        "quantization": {"group_size": group, "bits": 4},
+    }
+
+
+def write_checkpoint(model_dir: str, layers: Dict[int, Dict[str, np.ndarray]], config: dict,
+                     layout: str = "sharded", shards: int = 2) -> None:
+    """Writes `layers` ({layer: MoeLayer-keyed arrays}) as a safetensors model
+    directory with the `safetensors` package (an independent writer).
+
+    layout "single": one model.safetensors; "sharded": `shards` files listed in
+    model.safetensors.index.json, a layer's tensors spread over all of them;
+    "split": expert tensors in splitted_moe/layer_{l}_experts.safetensors as
+    e{N}.{proj}.{kind} with scales and biases cast to float16 (as
+    tools/split_experts.py:72-75 does), the rest in model.safetensors."""
+    import json
+    import os
+
+    import torch
+    from safetensors.torch import save_file
+
+    def tt(key: str, a: np.ndarray):
+        t = torch.from_numpy(np.array(a, copy=True))  # the writer refuses tensors sharing memory
+        return t.view(torch.bfloat16) if key in BF16_KEYS and a.dtype == np.uint16 else t
+
+    os.makedirs(model_dir, exist_ok=True)
+    with open(os.path.join(model_dir, "config.json"), "w") as f:
+        json.dump(config, f, indent=2)
+    named = {}
+    split = {}
+    for il, t in sorted(layers.items()):
+        for key, a in t.items():
+            if a is None:
+                continue
+            name = f"model.layers.{il}.{CKPT_NAMES[key]}"
+            if layout == "split" and key[:-2] in ("gate", "up", "down"):
+                proj, kind = CKPT_NAMES[key].split(".")[-2:]
+                for e in range(a.shape[0]):
+                    x = a[e]
+                    if key in BF16_KEYS and x.dtype == np.uint16:  # bf16 bits; float16 arrays go as given
+                        x = bf16_bits_to_f32(x).astype(np.float16)
+                    split.setdefault(il, {})[f"e{e}.{proj}.{kind}"] = torch.from_numpy(np.ascontiguousarray(x))
+            else:
+                named[name] = tt(key, a)
+    meta = {"format": "mlx"}
+    if layout in ("single", "split"):
+        save_file(named, os.path.join(model_dir, "model.safetensors"), metadata=meta)
+    elif layout == "sharded":
+        files = [f"model-{i + 1:05d}-of-{shards:05d}.safetensors" for i in range(shards)]
+        parts = [{} for _ in range(shards)]
+        weight_map = {}
+        for i, (name, t) in enumerate(sorted(named.items())):
+            parts[i % shards][name] = t
+            weight_map[name] = files[i % shards]
+        for fn, p in zip(files, parts):
+            save_file(p, os.path.join(model_dir, fn), metadata=meta)
+        with open(os.path.join(model_dir, "model.safetensors.index.json"), "w") as f:
+            json.dump({"metadata": {"total_size": sum(t.numel() * t.element_size() for t in named.values())},
+                       "weight_map": weight_map}, f, indent=2)
+    else:
+        raise ValueError(f"unknown layout {layout!r}")
+    if layout == "split":
+        d = os.path.join(model_dir, "splitted_moe")
+        os.makedirs(d, exist_ok=True)
+        for il, t in split.items():
+            save_file(t, os.path.join(d, f"layer_{il}_experts.safetensors"))

@@ -57,12 +57,13 @@ def test_python_binding_covers_exactly_the_header():
 def test_null_context_is_rejected_before_any_device_work():
     L = oh.lib()
     host_only = {"obs_create", "obs_create_error", "obs_destroy", "obs_last_error", "obs_get_stream",
-                 "obs_graph_destroy", "obs_moe_prefill_workspace", "obs_profile_count"}
+                 "obs_graph_destroy", "obs_moe_prefill_workspace", "obs_profile_count",
+                 "obs_ckpt_close", "obs_ckpt_error", "obs_moe_layer_bytes"}
     for name in declared_functions():
         if name in host_only:
             continue
         fn = getattr(L, name)
-        args = [None if a in (C.c_void_p,) or (isinstance(a, type) and issubclass(a, C._Pointer)) else 0
+        args = [None if a in (C.c_void_p, C.c_char_p) or (isinstance(a, type) and issubclass(a, C._Pointer)) else 0
                 for a in fn.argtypes]
         assert fn(*args) == oh.OBS_E_INVALID, name
     assert L.obs_last_error(None) == b"null context"
@@ -71,6 +72,11 @@ def test_null_context_is_rejected_before_any_device_work():
     L.obs_destroy(None)
     L.obs_graph_destroy(None)
     assert L.obs_create(0, None) == oh.OBS_E_INVALID
+    # checkpoint handles: the null checks above ran obs_ckpt_open(NULL, ...), whose
+    # message is kept per thread; closing NULL is a no-op
+    assert L.obs_ckpt_error(None) == b"obs_ckpt_open: null argument"
+    L.obs_ckpt_close(None)
+    assert L.obs_moe_layer_bytes(None) == 0
 
 
 def test_prefill_workspace_is_host_arithmetic():
