@@ -14,8 +14,10 @@
 //      (forward.rs:225-232), rounded once to bf16.
 //
 // The GEMM. A workgroup (4 waves) owns a tile of up to 128 permuted rows x 128
-// output columns; wave w owns columns [32w, 32w+32) (and the same columns of
-// the up matrix for gate/up). Per 64-column quantization group:
+// output columns; wave w owns columns [32w, 32w+32) and, in two of the three
+// modes, a second set of 32 B columns: the same columns of the up matrix
+// (gate/up, SwiGLU epilogue) or columns [128 + 32w, +32) of the same matrix
+// (wide mode, a 256-column tile: down). Per 64-column quantization group:
 //   - A (activations, gathered by row through a_rows) is staged in LDS,
 //     double-buffered, row stride padded to 72 bf16;
 //   - B is read straight from HBM into registers: lane l takes 16 bytes
@@ -45,23 +47,32 @@ typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16_t;
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));  // register-friendly 16-byte word
 
 constexpr uint32_t TM = 128;          // tile rows
-constexpr uint32_t TN = 128;          // tile output columns (4 waves x 32)
+constexpr uint32_t TN = 128;          // tile output columns per B column set (4 waves x 32)
 constexpr uint32_t GK = 64;           // quantization group = K step of the main loop
 constexpr uint32_t LDS_STRIDE = 72;   // bf16 per staged A row (64 + 8 padding)
 constexpr uint32_t GROUP_TOKENS = 64; // tokens per grouping chunk (one wave)
 constexpr uint32_t SB_STRIDE = TN + 1;  // words per (matrix, group) row of staged scale|bias
 constexpr uint32_t SB_LDS_MAX = 96u * 1024u;  // bytes of staged scale|bias per workgroup
 
+// Kernel modes: one B matrix, 128 columns; gate and up with a SwiGLU epilogue;
+// one B matrix, 256 columns (the second column set is the first one + 128 rows).
+enum GemmMode : uint32_t { MODE_NARROW = 0, MODE_SWIGLU = 1, MODE_WIDE = 2 };
+// Which row maps and work source a launch has (template flags, so that no load
+// sits under a branch: a load on one side of a branch makes the compiler wait
+// for every load at the join).
+enum GemmFlags : uint32_t { F_WORK = 1, F_AROWS = 2, F_OROWS = 4 };
+__host__ __device__ constexpr uint32_t mode_cols(uint32_t mode) { return mode == MODE_WIDE ? 2u * TN : TN; }
+
 struct GemmArgs {
   const uint16_t* A;        // bf16 [a_rows_total, K]
-  const int32_t* a_rows;    // permuted row -> A row (nullptr: identity)
+  const int32_t* a_rows;    // permuted row -> A row (with F_AROWS; else identity)
   uint32_t a_rows_total;    // bound for a_rows values
   const uint32_t* w0; const uint16_t* s0; const uint16_t* b0;  // [E, N, K/8], [E, N, K/64]
-  const uint32_t* w1; const uint16_t* s1; const uint16_t* b1;  // up matrix (SwiGLU only)
+  const uint32_t* w1; const uint16_t* s1; const uint16_t* b1;  // second B column set: up (SwiGLU), +128 rows (wide)
   uint16_t* out;            // bf16 rows of N
-  const int32_t* out_rows;  // permuted row -> output row (nullptr: identity)
-  const int4* tiles;        // {expert, row0, rows, 0}; nullptr: dense rows of expert 0
-  const int32_t* n_tiles;   // device tile count (grouped mode)
+  const int32_t* out_rows;  // permuted row -> output row (with F_OROWS; else identity)
+  const int4* work;         // per workgroup {expert, row0, rows, n0} with F_WORK; else dense rows of expert 0
+  const int32_t* work_count;  // items per XCD: workgroup l has one iff l / 8 < work_count[l % 8]
   uint32_t dense_rows;      // row count in dense mode
   uint32_t K, N;
 };
@@ -155,17 +166,39 @@ __device__ __forceinline__ bf16x8_t dequant_word(uint32_t w, float s, float b) {
   return __builtin_bit_cast(bf16x8_t, r);
 }
 
+// B operand of one 64-column group for one lane: 16 bytes (32 nibbles) of its
+// weight row in each B column set.
+struct BRaw {
+  u32x4_t q0, q1;
+};
+
+// Per-thread operand pointers of a tile, set up by the kernel's prologue.
+struct TileIn {
+  const uint16_t* aptr[4];  // A row of staging row t/8 + 32i, at this thread's 16-byte chunk
+  const u32x4_t* w0p;       // this lane's weight row (k half h), first column set; + 2g per group
+  const u32x4_t* w1p;       // second column set (up matrix, or 128 rows further)
+};
+
+template <bool TWO>
+__device__ __forceinline__ BRaw load_b(const TileIn& in, uint32_t g, uint32_t groups) {
+  BRaw r;
+  const uint32_t gg = g < groups ? g : groups - 1u;  // clamped: the tail loads are never used
+  r.q0 = in.w0p[2u * gg];
+  if (TWO) r.q1 = in.w1p[2u * gg];
+  return r;
+}
+
 // One tile's main loop and epilogue, NB = active 32-row blocks (1..4), so the
 // MFMA sequence is straight-line code. MIX: every staged scale is within
-// dequant_word_mix's range (decided per tile).
-template <bool SWIGLU, uint32_t NB, bool MIX>
+// dequant_word_mix's range (decided per tile). The prologue has loaded B
+// groups 0 and 1 (bs0, bs1) and A group 0 (ras).
+template <uint32_t MODE, uint32_t NB, bool MIX>
 __device__ __forceinline__ void gemm_tile(const GemmArgs& a, uint16_t (&sA)[2][TM * LDS_STRIDE],
-                                          const int32_t* s_arow, const int32_t* s_orow, const uint32_t* s_sb,
-                                          uint32_t e, uint32_t row0,
-                                          uint32_t nrows, uint32_t n0) {
+                                          const int32_t* s_orow, const uint32_t* s_sb, const TileIn& in,
+                                          uint32_t nrows, uint32_t n0, BRaw bs0, BRaw bs1, u32x4_t (&ras)[4]) {
+  constexpr bool SWIGLU = MODE == MODE_SWIGLU, TWO = MODE != MODE_NARROW;
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   const uint32_t nl = 32u * wave + (lane & 31u);                   // this lane's column in the tile
-  const uint32_t n = n0 + nl;                                      // this lane's weight row
   const uint32_t h = lane >> 5;                                    // k half within a group
   const uint32_t K = a.K, groups = K / GK;
 
@@ -174,42 +207,18 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, uint16_t (&sA)[2][T
   // row segments. Rows of blocks >= NB are never read by the MFMAs and are not
   // staged (i is unrolled, so this costs no branch).
   const uint32_t ac = 8u * (tid & 7u);
-  const uint16_t* aptr[4];
-#pragma unroll
-  for (uint32_t i = 0; i < 4; ++i) {
-    const int32_t arow = s_arow[tid / 8u + 32u * i];
-    // Padding rows (no A row) stage row 0: row i of an MFMA product depends on
-    // row i of A only, and the epilogue discards padding rows.
-    aptr[i] = a.A + static_cast<size_t>(arow >= 0 ? arow : 0) * K + ac;
-  }
   auto load_a = [&](uint32_t g, u32x4_t (&r)[4]) __attribute__((always_inline)) {
 #pragma unroll
-    for (uint32_t i = 0; i < NB; ++i) r[i] = *reinterpret_cast<const u32x4_t*>(aptr[i] + g * GK);
+    for (uint32_t i = 0; i < NB; ++i) r[i] = *reinterpret_cast<const u32x4_t*>(in.aptr[i] + g * GK);
   };
   auto store_a = [&](uint32_t buf, const u32x4_t (&r)[4]) __attribute__((always_inline)) {
 #pragma unroll
     for (uint32_t i = 0; i < NB; ++i)
       *reinterpret_cast<u32x4_t*>(&sA[buf][(tid / 8u + 32u * i) * LDS_STRIDE + ac]) = r[i];
   };
-
-  // B pointers of this lane's weight row(s)
-  const size_t wrow = static_cast<size_t>(e) * a.N + n;
-  const u32x4_t* w0p = reinterpret_cast<const u32x4_t*>(a.w0 + wrow * (K / 8)) + h;  // + 2*g per group
-  const u32x4_t* w1p = SWIGLU ? reinterpret_cast<const u32x4_t*>(a.w1 + wrow * (K / 8)) + h : nullptr;
   // staged scale|bias of this lane's column: [matrix][group] at stride SB_STRIDE words
   const uint32_t* sb0 = s_sb + nl;
   const uint32_t* sb1 = s_sb + static_cast<size_t>(groups) * SB_STRIDE + nl;
-
-  struct BRaw {
-    u32x4_t q0, q1;
-  };
-  auto load_b = [&](uint32_t g) __attribute__((always_inline)) {
-    BRaw r;
-    const uint32_t gg = g < groups ? g : groups - 1u;  // clamped: the tail loads are never used
-    r.q0 = w0p[2u * gg];
-    if (SWIGLU) r.q1 = w1p[2u * gg];
-    return r;
-  };
 
   f32x16_t acc0[NB], acc1[NB];
 #pragma unroll
@@ -224,20 +233,21 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, uint16_t (&sA)[2][T
   // before its MFMAs, so few values are live; the co-resident workgroup hides
   // the LDS and memory latencies. Unrolled by two so each slot is a fixed set
   // of registers.
-  BRaw bs0 = load_b(0), bs1 = load_b(1);
-  u32x4_t ras[4];
-  load_a(0, ras);
   store_a(0, ras);
 
   auto step = [&](uint32_t g, BRaw& bcur) __attribute__((always_inline)) {
     const uint32_t buf = g & 1u;
     __syncthreads();  // A of group g visible in sA[buf]; sA[buf^1] no longer read
     load_a(g + 1 < groups ? g + 1 : g, ras);  // the tail reload is stored but never read
-    // keep the A loads here, a whole group ahead of their LDS store: left to
-    // itself the scheduler sinks them next to the store and exposes their latency
+    // B two groups ahead, issued right after A: loads complete in issue order,
+    // so the A store at the end of this group waits only for loads issued a
+    // group or more earlier, and B has two groups to arrive
+    const BRaw bnext = load_b<TWO>(in, g + 2, groups);  // clamped past the end; never used there
+    // keep the loads here, a whole group ahead of their use: left to itself the
+    // scheduler sinks them next to the store and exposes their latency
     __builtin_amdgcn_sched_barrier(0);
     const uint32_t sv0 = sb0[g * SB_STRIDE];
-    const uint32_t sv1 = SWIGLU ? sb1[g * SB_STRIDE] : 0u;
+    const uint32_t sv1 = TWO ? sb1[g * SB_STRIDE] : 0u;
     const uint32_t q0w[4] = {bcur.q0.x, bcur.q0.y, bcur.q0.z, bcur.q0.w};
     const uint32_t q1w[4] = {bcur.q1.x, bcur.q1.y, bcur.q1.z, bcur.q1.w};
     const MixScale m0 = mix_scale(sv0), m1 = mix_scale(sv1);
@@ -250,15 +260,15 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, uint16_t (&sA)[2][T
             &sA[buf][(32u * mb + (lane & 31u)) * LDS_STRIDE + 32u * h + 8u * st]);
       const bf16x8_t f0 = MIX ? dequant_word_mix(q0w[st], m0) : dequant_word(q0w[st], bf16lo(sv0), bf16hi(sv0));
       bf16x8_t f1;
-      if (SWIGLU) f1 = MIX ? dequant_word_mix(q1w[st], m1) : dequant_word(q1w[st], bf16lo(sv1), bf16hi(sv1));
+      if (TWO) f1 = MIX ? dequant_word_mix(q1w[st], m1) : dequant_word(q1w[st], bf16lo(sv1), bf16hi(sv1));
 #pragma unroll
       for (uint32_t mb = 0; mb < NB; ++mb) {
         acc0[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mb], f0, acc0[mb], 0, 0, 0);
-        if (SWIGLU) acc1[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mb], f1, acc1[mb], 0, 0, 0);
+        if (TWO) acc1[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mb], f1, acc1[mb], 0, 0, 0);
       }
     }
     __builtin_amdgcn_sched_barrier(0);  // the A store waits for its loads: keep it last
-    bcur = load_b(g + 2);    // clamped past the end; never used there
+    bcur = bnext;
     store_a(buf ^ 1u, ras);  // read after the next barrier
   };
   for (uint32_t g = 0; g < groups; g += 2) {  // groups % 4 == 0 (K % 256 == 0, checked by the host)
@@ -271,138 +281,190 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, uint16_t (&sA)[2][T
   // sixteen coalesced 16-byte stores instead of 128 scattered 2-byte ones.
   // Lanes nl and nl^1 (columns c, c+1) swap halves of their packed row pairs,
   // so each LDS write is a 4-byte (row, c..c+1) pair: the even lane writes rows
-  // i0 and i0+2, the odd lane rows i0+1 and i0+3.
+  // i0 and i0+2, the odd lane rows i0+1 and i0+3. The wide mode writes its two
+  // 128-column halves one after the other through the same buffer.
   constexpr uint32_t C_STRIDE = TN + 8;  // bf16 per staged row (bank spread)
   static_assert(TM * C_STRIDE <= 2 * TM * LDS_STRIDE, "C tile must fit the A buffers");
   uint16_t* sC = reinterpret_cast<uint16_t*>(sA);
   const uint32_t odd = nl & 1u, c_even = nl & ~1u;
   const uint32_t sel = odd ? 0x03020706u : 0x05040100u;  // v_perm: (partner.hi, own.hi) : (own.lo, partner.lo)
-  __syncthreads();  // every wave is done reading sA
+  auto emit = [&](uint32_t half) __attribute__((always_inline)) {
+    __syncthreads();  // every wave is done reading sA (or the previous half)
 #pragma unroll
-  for (uint32_t mb = 0; mb < NB; ++mb) {
+    for (uint32_t mb = 0; mb < NB; ++mb) {
 #pragma unroll
-    for (uint32_t qd = 0; qd < 4; ++qd) {
-      float v[4];
+      for (uint32_t qd = 0; qd < 4; ++qd) {
+        float v[4];
 #pragma unroll
-      for (uint32_t j = 0; j < 4; ++j)
-        v[j] = SWIGLU ? silu_mul_fast(acc0[mb][4 * qd + j], acc1[mb][4 * qd + j]) : acc0[mb][4 * qd + j];
-      const uint32_t p01 = pack_bf16_rne(v[0], v[1]), p23 = pack_bf16_rne(v[2], v[3]);
-      const uint32_t s01 = static_cast<uint32_t>(dpp_i32<DPP_XOR1>(static_cast<int>(p01)));
-      const uint32_t s23 = static_cast<uint32_t>(dpp_i32<DPP_XOR1>(static_cast<int>(p23)));
-      const uint32_t i0 = 32u * mb + 8u * qd + 4u * h + odd;
-      *reinterpret_cast<uint32_t*>(&sC[i0 * C_STRIDE + c_even]) = __builtin_amdgcn_perm(s01, p01, sel);
-      *reinterpret_cast<uint32_t*>(&sC[(i0 + 2u) * C_STRIDE + c_even]) = __builtin_amdgcn_perm(s23, p23, sel);
+        for (uint32_t j = 0; j < 4; ++j) {
+          const float c0 = acc0[mb][4 * qd + j], c1 = acc1[mb][4 * qd + j];
+          v[j] = SWIGLU ? silu_mul_fast(c0, c1) : (half ? c1 : c0);
+        }
+        const uint32_t p01 = pack_bf16_rne(v[0], v[1]), p23 = pack_bf16_rne(v[2], v[3]);
+        const uint32_t s01 = static_cast<uint32_t>(dpp_i32<DPP_XOR1>(static_cast<int>(p01)));
+        const uint32_t s23 = static_cast<uint32_t>(dpp_i32<DPP_XOR1>(static_cast<int>(p23)));
+        const uint32_t i0 = 32u * mb + 8u * qd + 4u * h + odd;
+        *reinterpret_cast<uint32_t*>(&sC[i0 * C_STRIDE + c_even]) = __builtin_amdgcn_perm(s01, p01, sel);
+        *reinterpret_cast<uint32_t*>(&sC[(i0 + 2u) * C_STRIDE + c_even]) = __builtin_amdgcn_perm(s23, p23, sel);
+      }
     }
-  }
-  __syncthreads();
+    __syncthreads();
 #pragma unroll
-  for (uint32_t q = 0; q < TM * TN / 8u / 256u; ++q) {
-    const uint32_t chunk = tid + 256u * q, i = chunk / (TN / 8u), c8 = 8u * (chunk % (TN / 8u));
-    if (i < nrows) {
-      const uint4 v = *reinterpret_cast<const uint4*>(&sC[i * C_STRIDE + c8]);
-      *reinterpret_cast<uint4*>(a.out + static_cast<size_t>(s_orow[i]) * a.N + n0 + c8) = v;
+    for (uint32_t q = 0; q < TM * TN / 8u / 256u; ++q) {
+      const uint32_t chunk = tid + 256u * q, i = chunk / (TN / 8u), c8 = 8u * (chunk % (TN / 8u));
+      if (i < nrows) {
+        const uint4 v = *reinterpret_cast<const uint4*>(&sC[i * C_STRIDE + c8]);
+        *reinterpret_cast<uint4*>(a.out + static_cast<size_t>(s_orow[i]) * a.N + n0 + TN * half + c8) = v;
+      }
     }
-  }
+  };
+  emit(0);
+  if (MODE == MODE_WIDE) emit(1);
 }
 
-// Work items are (tile, 128-column block) pairs in tile order, and tiles are in
+// Work items are (tile, column block) pairs in tile order, and tiles are in
 // expert order. The dispatcher deals consecutive workgroups round-robin over
-// the 8 XCDs, so workgroup l takes item (l % 8) * chunk + l / 8: each XCD runs
-// a contiguous run of items, and the tiles of one expert share its weights (and
-// the column blocks of one tile share its activation rows) in that XCD's L2.
+// the 8 XCDs, so workgroup l takes item (l % 8) * chunk + l / 8 (the grouping
+// writes that table, work_table_fill): each XCD runs a contiguous run of
+// items, and the tiles of one expert share its weights (and the column blocks
+// of one tile share its activation rows) in that XCD's L2.
 // Two workgroups per CU (at most 256 registers per lane): the co-resident
 // workgroup hides each one's load, LDS and barrier latency.
-template <bool SWIGLU>
+template <uint32_t MODE, uint32_t FLAGS>
 __global__ void __launch_bounds__(256, 2) grouped_gemm_kernel(GemmArgs a) {
+  constexpr bool TWO = MODE != MODE_NARROW;
   __shared__ uint16_t sA[2][TM * LDS_STRIDE];
-  __shared__ int32_t s_arow[TM], s_orow[TM];
+  __shared__ int32_t s_orow[TM];
   extern __shared__ uint32_t s_sb[];  // [matrix][group][SB_STRIDE]: scale | bias << 16
-  const uint32_t ncb = a.N / TN;
-  const uint32_t n_tiles = a.tiles ? static_cast<uint32_t>(*a.n_tiles) : (a.dense_rows + TM - 1) / TM;
-  const uint32_t n_items = n_tiles * ncb, chunk = (n_items + 7u) / 8u;
-  const uint32_t item = (blockIdx.x % 8u) * chunk + blockIdx.x / 8u;
-  if (blockIdx.x / 8u >= chunk || item >= n_items) return;  // uniform per workgroup
-  const uint32_t t_idx = item / ncb, n0 = (item % ncb) * TN;
-  int4 tile;
-  if (a.tiles) {
-    tile = a.tiles[t_idx];
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  const uint32_t K = a.K, groups = K / GK;
+  // The work item: one load from the grouping's per-workgroup table, or, for
+  // dense rows, arithmetic on the launch index.
+  uint32_t e, row0, nrows, n0;
+  if (FLAGS & F_WORK) {
+    // both loads at once: the entry is inside the table even where it is unused
+    const int32_t count = a.work_count[blockIdx.x % 8u];
+    const int4 w = a.work[blockIdx.x];
+    if (static_cast<int32_t>(blockIdx.x / 8u) >= count) return;  // uniform per workgroup
+    e = static_cast<uint32_t>(w.x);
+    row0 = static_cast<uint32_t>(w.y);
+    nrows = static_cast<uint32_t>(w.z);
+    n0 = static_cast<uint32_t>(w.w);
   } else {
-    const uint32_t r0 = t_idx * TM;
-    tile = make_int4(0, static_cast<int32_t>(r0), static_cast<int32_t>(min(TM, a.dense_rows - r0)), 0);
+    const uint32_t ncb = a.N / mode_cols(MODE);
+    const uint32_t n_items = (a.dense_rows + TM - 1u) / TM * ncb, chunk = (n_items + 7u) / 8u;
+    const uint32_t item = (blockIdx.x % 8u) * chunk + blockIdx.x / 8u;
+    if (blockIdx.x / 8u >= chunk || item >= n_items) return;
+    e = 0;
+    row0 = item / ncb * TM;
+    nrows = min(TM, a.dense_rows - row0);
+    n0 = item % ncb * mode_cols(MODE);
   }
-  const uint32_t e = static_cast<uint32_t>(tile.x), row0 = static_cast<uint32_t>(tile.y);
-  const uint32_t nrows = static_cast<uint32_t>(tile.z);
-  const uint32_t tid = threadIdx.x;
-  if (tid < TM) {
-    int32_t r = -1;
-    if (tid < nrows) {
-      const uint32_t p = row0 + tid;
-      r = a.a_rows ? a.a_rows[p] : static_cast<int32_t>(p);
-      if (r < 0 || static_cast<uint32_t>(r) >= a.a_rows_total) r = -1;
-    }
-    s_arow[tid] = r;
-    if (tid < nrows) {
-      const uint32_t p = row0 + tid;
-      s_orow[tid] = a.out_rows ? a.out_rows[p] : static_cast<int32_t>(p);
-    }
+
+  // Every load that depends on the work item alone is issued before any is
+  // waited for: this thread's A row ids, the output row map, the tile's scales
+  // and biases, B groups 0 and 1. A group 0 follows as soon as its row ids are
+  // in. All of them are unconditional (indices clamped into the tile, results
+  // selected afterwards), so the waits count exactly the loads they need.
+  int32_t arow[4];
+#pragma unroll
+  for (uint32_t i = 0; i < 4; ++i) {
+    const uint32_t r = tid / 8u + 32u * i;
+    arow[i] = (FLAGS & F_AROWS) ? a.a_rows[row0 + min(r, nrows - 1u)] : static_cast<int32_t>(row0 + r);
+    if (r >= nrows) arow[i] = -1;
   }
-  // Stage the scales and biases of the tile's 128 weight rows. Rows n0.. of
-  // expert e are contiguous ([E, N, groups] bf16), so 8-byte chunks (4 groups
-  // of one row; groups % 4 == 0) load coalesced; each becomes 4 packed words.
-  // All of a batch's loads (up to 4 chunks per thread and matrix) are issued
-  // before any is stored, so the staging pays one memory latency per batch
-  // (one batch for K <= 2048) instead of one per chunk.
+  // threads t and t + 128 load and store the same entry (an unconditional store
+  // keeps the load from sinking under a branch)
+  const uint32_t orow_i = min(tid & (TM - 1u), nrows - 1u);
+  const int32_t orow = (FLAGS & F_OROWS) ? a.out_rows[row0 + orow_i] : static_cast<int32_t>(row0 + orow_i);
+
+  // Scales and biases of the tile's weight rows: rows n0.. of expert e are
+  // contiguous ([E, N, groups] bf16), so 8-byte chunks (4 groups of one row;
+  // groups % 4 == 0) load coalesced; each becomes 4 packed words in LDS. A
+  // batch (4 chunks per thread and matrix; past the end they reload the last
+  // chunk) covers K <= 2048; all its loads are issued before any is stored.
+  constexpr uint32_t NMAT = TWO ? 2u : 1u, PER = 4u;
+  const uint32_t cpr = groups / 4u, nchunk = TN * cpr;  // chunks per row, per matrix
+  const size_t sbase = (static_cast<size_t>(e) * a.N + n0) * groups;
   bool wide_scale = false;  // some staged |s| is beyond dequant_word_mix's range
-  {
-    constexpr uint32_t NMAT = SWIGLU ? 2u : 1u, PER = 4u;
-    const uint32_t groups = a.K / GK, cpr = groups / 4u, nchunk = TN * cpr;  // chunks per row, per matrix
-    const size_t base = (static_cast<size_t>(e) * a.N + n0) * groups;
-    for (uint32_t c0 = 0; c0 < nchunk; c0 += PER * 256u) {
-      uint2 sv[NMAT][PER], bv[NMAT][PER];
+  uint2 sv[NMAT][PER], bv[NMAT][PER];
+  auto issue_scales = [&](uint32_t c0) __attribute__((always_inline)) {
 #pragma unroll
-      for (uint32_t mat = 0; mat < NMAT; ++mat) {
-        const uint2* sp = reinterpret_cast<const uint2*>((mat ? a.s1 : a.s0) + base);
-        const uint2* bp = reinterpret_cast<const uint2*>((mat ? a.b1 : a.b0) + base);
+    for (uint32_t mat = 0; mat < NMAT; ++mat) {
+      const uint2* sp = reinterpret_cast<const uint2*>((mat ? a.s1 : a.s0) + sbase);
+      const uint2* bp = reinterpret_cast<const uint2*>((mat ? a.b1 : a.b0) + sbase);
 #pragma unroll
-        for (uint32_t j = 0; j < PER; ++j) {
-          const uint32_t c = c0 + tid + 256u * j;
-          if (c < nchunk) {
-            sv[mat][j] = sp[c];
-            bv[mat][j] = bp[c];
-          }
-        }
-      }
-#pragma unroll
-      for (uint32_t mat = 0; mat < NMAT; ++mat) {
-#pragma unroll
-        for (uint32_t j = 0; j < PER; ++j) {
-          const uint32_t c = c0 + tid + 256u * j;
-          if (c < nchunk) {
-            const uint2 s2 = sv[mat][j], b2 = bv[mat][j];
-            const uint32_t row = c / cpr, g0 = 4u * (c % cpr);
-            uint32_t* d = s_sb + (static_cast<size_t>(mat) * groups + g0) * SB_STRIDE + row;
-            d[0] = (s2.x & 0xffffu) | (b2.x << 16);
-            d[SB_STRIDE] = (s2.x >> 16) | (b2.x & 0xffff0000u);
-            d[2u * SB_STRIDE] = (s2.y & 0xffffu) | (b2.y << 16);
-            d[3u * SB_STRIDE] = (s2.y >> 16) | (b2.y & 0xffff0000u);
-            wide_scale = wide_scale || scale_out_of_mix_range(s2.x) || scale_out_of_mix_range(s2.x >> 16) ||
-                         scale_out_of_mix_range(s2.y) || scale_out_of_mix_range(s2.y >> 16);
-          }
-        }
+      for (uint32_t j = 0; j < PER; ++j) {
+        const uint32_t c = min(c0 + tid + 256u * j, nchunk - 1u);
+        sv[mat][j] = sp[c];
+        bv[mat][j] = bp[c];
       }
     }
+  };
+  auto store_scales = [&](uint32_t c0) __attribute__((always_inline)) {
+#pragma unroll
+    for (uint32_t mat = 0; mat < NMAT; ++mat) {
+#pragma unroll
+      for (uint32_t j = 0; j < PER; ++j) {
+        // clamped like the load: past the end, the last chunk is written again with
+        // the same values (no branch, so the loads cannot sink next to the stores)
+        const uint32_t c = min(c0 + tid + 256u * j, nchunk - 1u);
+        uint2 s2 = sv[mat][j], b2 = bv[mat][j];
+        // an opaque use here, after the issue phase: without it the range checks
+        // below are hoisted above the scheduling barrier, and their wait with them
+        asm volatile("" : "+v"(s2.x), "+v"(s2.y), "+v"(b2.x), "+v"(b2.y));
+        const uint32_t row = c / cpr, g0 = 4u * (c % cpr);
+        uint32_t* d = s_sb + (static_cast<size_t>(mat) * groups + g0) * SB_STRIDE + row;
+        d[0] = (s2.x & 0xffffu) | (b2.x << 16);
+        d[SB_STRIDE] = (s2.x >> 16) | (b2.x & 0xffff0000u);
+        d[2u * SB_STRIDE] = (s2.y & 0xffffu) | (b2.y << 16);
+        d[3u * SB_STRIDE] = (s2.y >> 16) | (b2.y & 0xffff0000u);
+        wide_scale = wide_scale || scale_out_of_mix_range(s2.x) || scale_out_of_mix_range(s2.x >> 16) ||
+                     scale_out_of_mix_range(s2.y) || scale_out_of_mix_range(s2.y >> 16);
+      }
+    }
+  };
+  issue_scales(0);
+
+  TileIn in;
+  {
+    const uint32_t n = n0 + 32u * wave + (lane & 31u), h = lane >> 5;  // this lane's weight row, k half
+    const size_t wrow = static_cast<size_t>(e) * a.N + n;
+    in.w0p = reinterpret_cast<const u32x4_t*>(a.w0 + wrow * (K / 8)) + h;
+    in.w1p = TWO ? reinterpret_cast<const u32x4_t*>(a.w1 + wrow * (K / 8)) + h : nullptr;
+  }
+  const BRaw bs0 = load_b<TWO>(in, 0, groups), bs1 = load_b<TWO>(in, 1, groups);
+
+  const uint32_t nb = (nrows + 31u) / 32u, ac = 8u * (tid & 7u);
+  u32x4_t ras[4];
+#pragma unroll
+  for (uint32_t i = 0; i < 4; ++i) {
+    // Padding rows (no A row) stage row 0: row i of an MFMA product depends on
+    // row i of A only, and the epilogue discards padding rows.
+    const int32_t r = arow[i] >= 0 && static_cast<uint32_t>(arow[i]) < a.a_rows_total ? arow[i] : 0;
+    in.aptr[i] = a.A + static_cast<size_t>(r) * K + ac;
+    ras[i] = *reinterpret_cast<const u32x4_t*>(in.aptr[i]);  // A group 0 (rows of unused blocks: row 0)
+  }
+  // every load above is issued before the first wait below: left alone, the
+  // scheduler moves the scale stores (and their waits) ahead of the B and A loads
+  __builtin_amdgcn_sched_barrier(0);
+
+  s_orow[tid & (TM - 1u)] = orow;
+  store_scales(0);
+  for (uint32_t c0 = PER * 256u; c0 < nchunk; c0 += PER * 256u) {  // K > 2048 only
+    issue_scales(c0);
+    store_scales(c0);
   }
   const bool mix = !__syncthreads_or(wide_scale);  // uniform per workgroup
-  const uint32_t nb = (nrows + 31u) / 32u;
   if (mix) {
     switch (nb) {
-      case 1: gemm_tile<SWIGLU, 1, true>(a, sA, s_arow, s_orow, s_sb, e, row0, nrows, n0); break;
-      case 2: gemm_tile<SWIGLU, 2, true>(a, sA, s_arow, s_orow, s_sb, e, row0, nrows, n0); break;
-      case 3: gemm_tile<SWIGLU, 3, true>(a, sA, s_arow, s_orow, s_sb, e, row0, nrows, n0); break;
-      default: gemm_tile<SWIGLU, 4, true>(a, sA, s_arow, s_orow, s_sb, e, row0, nrows, n0); break;
+      case 1: gemm_tile<MODE, 1, true>(a, sA, s_orow, s_sb, in, nrows, n0, bs0, bs1, ras); break;
+      case 2: gemm_tile<MODE, 2, true>(a, sA, s_orow, s_sb, in, nrows, n0, bs0, bs1, ras); break;
+      case 3: gemm_tile<MODE, 3, true>(a, sA, s_orow, s_sb, in, nrows, n0, bs0, bs1, ras); break;
+      default: gemm_tile<MODE, 4, true>(a, sA, s_orow, s_sb, in, nrows, n0, bs0, bs1, ras); break;
     }
   } else {  // scales beyond 2^100 (never in real checkpoints): reference-form dequant
-    gemm_tile<SWIGLU, 4, false>(a, sA, s_arow, s_orow, s_sb, e, row0, nrows, n0);
+    gemm_tile<MODE, 4, false>(a, sA, s_orow, s_sb, in, nrows, n0, bs0, bs1, ras);
   }
 }
 
@@ -459,11 +521,205 @@ __device__ __forceinline__ int32_t block_exclusive_scan256(int32_t v, int32_t* s
   return before + x - v;
 }
 
+// Measured cost of one (tile, column block) item by its active 32-row blocks
+// (1..4), in thousands of core cycles (per-wave timestamps at T = 2048 on
+// MI355X, two workgroups per CU): gate/up 74, 81, 91, 108; down (256 columns)
+// 36, 41, 45, 50. Only their ratios matter: they balance the XCDs.
+// Four 16-bit costs in one word: the device extracts one with a shift (a
+// four-entry array, or a select chain the compiler turns into one, would be
+// read from scratch memory).
+struct ItemCost {
+  unsigned long long packed;
+  __host__ __device__ constexpr uint32_t of(uint32_t nb) const {
+    return static_cast<uint32_t>((packed >> (16u * (nb - 1u))) & 0xffffu);
+  }
+};
+constexpr ItemCost item_cost(uint32_t c1, uint32_t c2, uint32_t c3, uint32_t c4) {
+  return ItemCost{c1 | (static_cast<unsigned long long>(c2) << 16) | (static_cast<unsigned long long>(c3) << 32) |
+                  (static_cast<unsigned long long>(c4) << 48)};
+}
+constexpr ItemCost COST_GATEUP = item_cost(74, 81, 91, 108);
+constexpr ItemCost COST_DOWN = item_cost(36, 41, 45, 50);
+constexpr uint32_t SCHED_MAX_TILES = 2048;  // tiles the cost-balanced schedule handles (else even split)
+
+// Workgroups a grouped GEMM launch needs for at most max_tiles tiles: an XCD's
+// cost share (total / 8) holds at most max_tiles * cmax / (8 * cmin) + 1 tiles.
+uint32_t sched_grid(uint32_t max_tiles, uint32_t ncb, const ItemCost& cost) {
+  const uint64_t cmin = cost.of(1), cmax = cost.of(4);
+  const uint64_t per_xcd = (static_cast<uint64_t>(max_tiles) * cmax + 8u * cmin - 1u) / (8u * cmin) + 1u;
+  const uint64_t even = (static_cast<uint64_t>(max_tiles) + 7u) / 8u;
+  return static_cast<uint32_t>(8u * (per_xcd > even ? per_xcd : even) * ncb);
+}
+
+// One GEMM's work table: where it goes and what its items cost. count[x] is the
+// number of items XCD x runs; entries at or beyond it are not written.
+struct WorkTable {
+  int4* work;
+  int32_t* count;
+  uint32_t grid, ncb, cols;
+  ItemCost cost;
+};
+
+// Exclusive prefix sum over the wave (64 lanes) and the wave total.
+template <typename T>
+__device__ __forceinline__ T wave_exclusive_scan(T v, T* total) {
+  const uint32_t lane = threadIdx.x & 63u;
+  T x = v;
+#pragma unroll
+  for (uint32_t d = 1; d < 64; d <<= 1) {
+    const T y = __shfl_up(x, d, 64);
+    if (lane >= d) x += y;
+  }
+  *total = __shfl(x, 63, 64);
+  return x - v;
+}
+
+struct SchedLds {
+  uint8_t te[SCHED_MAX_TILES];   // tile -> expert (E <= 256)
+  uint8_t tnb[SCHED_MAX_TILES];  // tile -> active 32-row blocks (1..4)
+  int32_t toff[257], roff[256], cnt[256];  // expert's first tile (toff[E] = all tiles), first row, rows
+  uint32_t first[9];             // XCD x's tiles are [first[x], first[x + 1])
+  unsigned long long pfirst[9];  // tiles with 1..4 blocks before first[x], 16-bit fields
+  uint32_t over;                 // some XCD's share exceeds the launch's workgroups
+};
+
+// One GEMM's per-workgroup work table (read by grouped_gemm_kernel), built by
+// one wave. The dispatcher deals consecutive workgroups round-robin over the
+// 8 XCDs and, within an XCD, to the first free slot, so workgroup l = 8p + x is
+// the p-th item XCD x runs. Tiles (expert order) are split into 8 contiguous
+// ranges of equal measured cost, one per XCD, so an expert's tiles share its
+// weights in one L2; within an XCD the items run in decreasing cost (longest
+// first). W.count[x] = the number of items XCD x runs. When the schedule does
+// not fit (more than SCHED_MAX_TILES tiles, or an XCD share beyond the
+// launch), the items are split evenly by count instead, in item order.
+__device__ void work_table_fill(const WorkTable W, uint32_t E, SchedLds& L) {  // by value: no scratch copy
+  const uint32_t lane = threadIdx.x & 63u, T_all = static_cast<uint32_t>(L.toff[E]), slots = W.grid / 8u;
+  const uint32_t ncb = W.ncb;
+  auto cost = [&](uint32_t nb) __attribute__((always_inline)) { return W.cost.of(nb) * ncb; };
+  auto item_of = [&](uint32_t e, uint32_t q, uint32_t cb) __attribute__((always_inline)) {
+    const int32_t r0 = static_cast<int32_t>(q * TM);
+    return make_int4(static_cast<int32_t>(e), L.roff[e] + r0, min(static_cast<int32_t>(TM), L.cnt[e] - r0),
+                     static_cast<int32_t>(cb * W.cols));
+  };
+  if (T_all <= SCHED_MAX_TILES) {
+    // Tallies of tiles by block count are packed 16 bits per count (T_all <=
+    // 2048 fits), so they add and scan as one integer: an array indexed by the
+    // block count would live in scratch memory.
+    auto unit = [](uint32_t nb) { return 1ull << (16u * (nb - 1u)); };
+    auto field = [](unsigned long long p, uint32_t nb) { return static_cast<uint32_t>((p >> (16u * (nb - 1u))) & 0xffffu); };
+    // this lane's contiguous block of tiles: cost and tallies
+    const uint32_t P = (T_all + 63u) / 64u, ta = min(lane * P, T_all), tb = min(ta + P, T_all);
+    uint32_t csum = 0;
+    unsigned long long vsum = 0;
+    for (uint32_t t = ta; t < tb; ++t) {
+      csum += cost(L.tnb[t]);
+      vsum += unit(L.tnb[t]);
+    }
+    uint32_t total;
+    unsigned long long vtot;
+    const uint32_t cpre = wave_exclusive_scan(csum, &total);
+    const unsigned long long vpre = wave_exclusive_scan(vsum, &vtot);
+    if (lane < 9) {
+      L.first[lane] = T_all;
+      L.pfirst[lane] = vtot;
+    }
+    if (lane == 0) L.over = 0;
+    __syncthreads();
+    // XCD of a tile: where its cost starts (32-bit: total <= 2048 tiles x 8 x 108)
+    auto xcd_at = [&](uint32_t c) __attribute__((always_inline)) {
+      return total ? min(7u, c * 8u / total) : 0u;
+    };
+    {
+      uint32_t c = cpre;
+      unsigned long long v = vpre;
+      int32_t xprev = ta == 0 ? -1 : static_cast<int32_t>(xcd_at(cpre - cost(L.tnb[ta - 1u])));
+      for (uint32_t t = ta; t < tb; ++t) {
+        const int32_t x = static_cast<int32_t>(xcd_at(c));
+        for (int32_t y = xprev + 1; y <= x; ++y) {
+          L.first[y] = t;
+          L.pfirst[y] = v;
+        }
+        xprev = x;
+        c += cost(L.tnb[t]);
+        v += unit(L.tnb[t]);
+      }
+    }
+    __syncthreads();
+    if (lane < 8 && (L.first[lane + 1] - L.first[lane]) * ncb > slots) L.over = 1;
+    __syncthreads();
+    if (L.over == 0) {
+      uint32_t c = cpre;
+      unsigned long long v = vpre;
+      for (uint32_t t = ta; t < tb; ++t) {
+        const uint32_t x = xcd_at(c), nb = L.tnb[t], e = L.te[t], q = t - static_cast<uint32_t>(L.toff[e]);
+        const unsigned long long lo = L.pfirst[x], hi = L.pfirst[x + 1];
+        uint32_t pos = field(v, nb) - field(lo, nb);  // same block count, earlier in this XCD
+        for (uint32_t w = nb + 1u; w <= 4u; ++w) pos += field(hi, w) - field(lo, w);
+        for (uint32_t cb = 0; cb < ncb; ++cb) W.work[8u * (pos * ncb + cb) + x] = item_of(e, q, cb);
+        c += cost(nb);
+        v += unit(nb);
+      }
+      if (lane < 8) W.count[lane] = static_cast<int32_t>((L.first[lane + 1] - L.first[lane]) * ncb);
+      return;
+    }
+  }
+  // even split by count: XCD x runs items [x * chunk, (x + 1) * chunk) in item order
+  const uint32_t n_items = T_all * ncb, chunk = (n_items + 7u) / 8u;
+  for (uint32_t i = lane; i < n_items; i += 64u) {
+    const int32_t t = static_cast<int32_t>(i / ncb);
+    uint32_t lo = 0, hi = E;  // the last expert whose first tile is <= t: toff[lo] <= t < toff[hi]
+    while (hi - lo > 1u) {
+      const uint32_t mid = (lo + hi) / 2u;
+      if (L.toff[mid] <= t) lo = mid; else hi = mid;
+    }
+    W.work[8u * (i % chunk) + i / chunk] = item_of(lo, static_cast<uint32_t>(t - L.toff[lo]), i % ncb);
+  }
+  if (lane < 8) W.count[lane] = static_cast<int32_t>(min(chunk, n_items - min(n_items, lane * chunk)));
+}
+
+// A scheduling wave: per-expert tiles from the row counts, then one GEMM's
+// work table. The rank launch runs one per GEMM beside the ranking waves
+// (nothing they write is read before the GEMMs).
+__device__ void build_work_table(const int32_t* __restrict__ counts, const int32_t* __restrict__ offsets, uint32_t E,
+                                 const WorkTable W) {
+  __shared__ SchedLds L;
+  const uint32_t lane = threadIdx.x & 63u;
+  // lane owns experts 4 * lane + j (E <= 256), kept in registers (static indices)
+  uint32_t rows[4], nts = 0;
+#pragma unroll
+  for (uint32_t j = 0; j < 4; ++j) {
+    const uint32_t e = 4u * lane + j, ec = min(e, E - 1u);  // clamped loads: no branch to wait at
+    const int32_t c = counts[ec], o = offsets[ec];
+    rows[j] = e < E ? static_cast<uint32_t>(c) : 0u;
+    if (e < E) {
+      L.cnt[e] = c;
+      L.roff[e] = o;
+    }
+    nts += (rows[j] + TM - 1u) / TM;
+  }
+  uint32_t T_all;
+  uint32_t t = wave_exclusive_scan(nts, &T_all);
+#pragma unroll
+  for (uint32_t j = 0; j < 4; ++j) {
+    const uint32_t e = 4u * lane + j, nt = (rows[j] + TM - 1u) / TM;
+    if (e < E) L.toff[e] = static_cast<int32_t>(t);
+    if (T_all <= SCHED_MAX_TILES) {
+      for (uint32_t q = 0; q < nt; ++q) {
+        L.te[t + q] = static_cast<uint8_t>(e);
+        L.tnb[t + q] = static_cast<uint8_t>((min(TM, rows[j] - q * TM) + 31u) / 32u);
+      }
+    }
+    t += nt;
+  }
+  if (lane == 0) L.toff[E] = static_cast<int32_t>(T_all);
+  __syncthreads();
+  work_table_fill(W, E, L);
+}
+
 // 2. one workgroup (thread e = expert e, E <= 256): chunk counts -> absolute row
-// bases per (chunk, expert), expert offsets and counts, the tile list.
+// bases per (chunk, expert), expert offsets and counts.
 __global__ void __launch_bounds__(256) group_scan_kernel(uint32_t nchunks, uint32_t E, int32_t* __restrict__ chunk_cnt,
-                                                         int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
-                                                         int4* __restrict__ tiles, int32_t* __restrict__ n_tiles) {
+                                                         int32_t* __restrict__ counts, int32_t* __restrict__ offsets) {
   __shared__ int32_t s_wave[4];
   const uint32_t e = threadIdx.x;
   const bool have = e < E;
@@ -480,17 +736,11 @@ __global__ void __launch_bounds__(256) group_scan_kernel(uint32_t nchunks, uint3
       }
     }
   }
-  int32_t all_rows, all_tiles;
-  const int32_t nt = (tot + static_cast<int32_t>(TM) - 1) / static_cast<int32_t>(TM);
+  int32_t all_rows;
   const int32_t off = block_exclusive_scan256(tot, s_wave, &all_rows);
-  const int32_t toff = block_exclusive_scan256(nt, s_wave, &all_tiles);
   if (have) {
     counts[e] = tot;
     offsets[e] = off;
-    for (int32_t q = 0; q < nt; ++q) {
-      const int32_t r0 = q * static_cast<int32_t>(TM);
-      tiles[toff + q] = make_int4(static_cast<int32_t>(e), off + r0, min(static_cast<int32_t>(TM), tot - r0), 0);
-    }
     for (uint32_t c0 = 0; c0 < nchunks; c0 += 16u) {  // batched: all loads in flight together
       int32_t v[16];
 #pragma unroll
@@ -500,17 +750,22 @@ __global__ void __launch_bounds__(256) group_scan_kernel(uint32_t nchunks, uint3
         if (c0 + i < nchunks) chunk_cnt[static_cast<size_t>(c0 + i) * E + e] = v[i] + off;
     }
   }
-  if (e == 0) {
-    offsets[E] = all_rows;
-    *n_tiles = all_tiles;
-  }
+  if (e == 0) offsets[E] = all_rows;
 }
 
 // 3. one wave per chunk: a token's row in expert e = chunk base + the number of
 // lower lanes (earlier tokens) of the chunk routed to e (LDS lane bitmasks).
+// Two more waves (the last two workgroups) build the GEMMs' work tables meanwhile.
 __global__ void __launch_bounds__(64) group_rank_kernel(const int32_t* __restrict__ ids, uint32_t T, uint32_t k,
                                                         uint32_t E, const int32_t* __restrict__ chunk_base,
-                                                        int32_t* __restrict__ row_token, int32_t* __restrict__ row_slot) {
+                                                        int32_t* __restrict__ row_token, int32_t* __restrict__ row_slot,
+                                                        const int32_t* __restrict__ counts,
+                                                        const int32_t* __restrict__ offsets, WorkTable gu,
+                                                        WorkTable dn) {
+  if (blockIdx.x + 2u >= gridDim.x) {  // uniform per workgroup
+    build_work_table(counts, offsets, E, blockIdx.x + 2u == gridDim.x ? gu : dn);
+    return;
+  }
   __shared__ unsigned long long wb[256];
   const uint32_t lane = threadIdx.x, c = blockIdx.x, t = c * GROUP_TOKENS + lane;
   for (uint32_t e = lane; e < E; e += 64u) wb[e] = 0ull;
@@ -569,9 +824,20 @@ __global__ void __launch_bounds__(512) combine_kernel(const uint16_t* __restrict
 
 constexpr size_t al256(size_t v) { return (v + 255) & ~size_t(255); }
 
+// The kernel mode of a GEMM: one-matrix GEMMs run wide when N allows it.
+uint32_t gemm_mode(bool swiglu, uint32_t N) {
+  return swiglu ? MODE_SWIGLU : (N % (2u * TN) == 0 ? MODE_WIDE : MODE_NARROW);
+}
+// Workgroups of a GEMM launch over at most `tiles` tiles: every XCD gets the same number.
+uint32_t gemm_grid(uint32_t tiles, uint32_t N, uint32_t mode) {
+  const uint32_t items = tiles * (N / mode_cols(mode));
+  return (items + 7u) / 8u * 8u;
+}
+
 struct PrefillWs {
-  size_t logits, ids, w, counts, offsets, ntiles, chunk_cnt, row_token, row_slot, tiles, H, Yp, Xn, total;
-  uint32_t max_tiles, nchunks;
+  size_t logits, ids, w, counts, offsets, chunk_cnt, row_token, row_slot, work_gu, work_dn, work_cnt, H, Yp, Xn,
+      total;
+  uint32_t max_tiles, nchunks, grid_gu, grid_dn;
 };
 
 PrefillWs prefill_layout(const obs_moe_config* cfg, uint32_t T) {
@@ -584,12 +850,15 @@ PrefillWs prefill_layout(const obs_moe_config* cfg, uint32_t T) {
   L.w = o; o += al256(sizeof(float) * R);
   L.counts = o; o += al256(sizeof(int32_t) * cfg->n_exp);
   L.offsets = o; o += al256(sizeof(int32_t) * (cfg->n_exp + 1));
-  L.ntiles = o; o += 256;
   L.nchunks = (T + GROUP_TOKENS - 1) / GROUP_TOKENS;
   L.chunk_cnt = o; o += al256(sizeof(int32_t) * L.nchunks * cfg->n_exp);
   L.row_token = o; o += al256(sizeof(int32_t) * R);
   L.row_slot = o; o += al256(sizeof(int32_t) * R);
-  L.tiles = o; o += al256(sizeof(int4) * L.max_tiles);
+  L.grid_gu = sched_grid(L.max_tiles, cfg->inter / mode_cols(gemm_mode(true, cfg->inter)), COST_GATEUP);
+  L.grid_dn = sched_grid(L.max_tiles, cfg->hidden / mode_cols(gemm_mode(false, cfg->hidden)), COST_DOWN);
+  L.work_gu = o; o += al256(sizeof(int4) * L.grid_gu);
+  L.work_dn = o; o += al256(sizeof(int4) * L.grid_dn);
+  L.work_cnt = o; o += 256;  // items per XCD, gate/up then down
   L.H = o; o += al256(sizeof(uint16_t) * R * cfg->inter);
   L.Yp = o; o += al256(sizeof(uint16_t) * R * cfg->hidden);
   L.Xn = o; o += al256(sizeof(uint16_t) * static_cast<size_t>(T) * cfg->hidden);  // rmsnorm(X) when layer->norm_w
@@ -598,28 +867,52 @@ PrefillWs prefill_layout(const obs_moe_config* cfg, uint32_t T) {
 }
 
 // Staged scale|bias bytes per workgroup.
-size_t gemm_sb_bytes(bool swiglu, uint32_t K) {
-  return sizeof(uint32_t) * (swiglu ? 2u : 1u) * (K / GK) * SB_STRIDE;
+size_t gemm_sb_bytes(uint32_t mode, uint32_t K) {
+  return sizeof(uint32_t) * (mode == MODE_NARROW ? 1u : 2u) * (K / GK) * SB_STRIDE;
 }
 
-// grid_tiles: an upper bound of the tile count (the device holds the exact one)
-int launch_gemm(obs_ctx* ctx, bool swiglu, const GemmArgs& a, uint32_t grid_tiles) {
-  const uint32_t items = grid_tiles * (a.N / TN);
-  const uint32_t grid = (items + 7u) / 8u * 8u;  // every XCD gets the same number of slots
-  const size_t lds = gemm_sb_bytes(swiglu, a.K);
-  // the staged scales can take the block past 64 KB of LDS (gfx950 has 160 KB)
-  static bool lds_raised = false;
-  if (!lds_raised) {
-    OBS_HIP_TRY(ctx, hipFuncSetAttribute(reinterpret_cast<const void*>(&grouped_gemm_kernel<true>),
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, SB_LDS_MAX));
-    OBS_HIP_TRY(ctx, hipFuncSetAttribute(reinterpret_cast<const void*>(&grouped_gemm_kernel<false>),
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, SB_LDS_MAX));
-    lds_raised = true;
+// grid: gemm_grid() of the launch; a.work (when set) has that many entries.
+// A one-matrix GEMM whose N is a multiple of 256 runs in the wide mode: its
+// second B column set is the first one 128 rows further on.
+int launch_gemm(obs_ctx* ctx, bool swiglu, GemmArgs a, uint32_t grid) {
+  const uint32_t mode = gemm_mode(swiglu, a.N);
+  if (mode == MODE_WIDE) {
+    a.w1 = a.w0 + static_cast<size_t>(TN) * (a.K / 8u);
+    a.s1 = a.s0 + static_cast<size_t>(TN) * (a.K / GK);
+    a.b1 = a.b0 + static_cast<size_t>(TN) * (a.K / GK);
   }
-  if (swiglu)
-    OBS_LAUNCH(ctx, "grouped_gemm_gateup", grouped_gemm_kernel<true><<<grid, 256, lds, ctx->stream>>>(a));
-  else
-    OBS_LAUNCH(ctx, "grouped_gemm_down", grouped_gemm_kernel<false><<<grid, 256, lds, ctx->stream>>>(a));
+  const size_t lds = gemm_sb_bytes(mode, a.K);
+  const uint32_t flags = (a.work ? F_WORK : 0u) | (a.a_rows ? F_AROWS : 0u) | (a.out_rows ? F_OROWS : 0u);
+  // The launches this library makes: gate/up (work, A row map), down (work,
+  // output row map) and dense matmuls (neither).
+  struct Variant {
+    uint32_t mode, flags;
+    const void* fn;
+    const char* name;
+  };
+  static const Variant variants[] = {
+      {MODE_SWIGLU, F_WORK | F_AROWS, reinterpret_cast<const void*>(&grouped_gemm_kernel<MODE_SWIGLU, F_WORK | F_AROWS>),
+       "grouped_gemm_gateup"},
+      {MODE_WIDE, F_WORK | F_OROWS, reinterpret_cast<const void*>(&grouped_gemm_kernel<MODE_WIDE, F_WORK | F_OROWS>),
+       "grouped_gemm_down"},
+      {MODE_NARROW, F_WORK | F_OROWS,
+       reinterpret_cast<const void*>(&grouped_gemm_kernel<MODE_NARROW, F_WORK | F_OROWS>), "grouped_gemm_down"},
+      {MODE_WIDE, 0, reinterpret_cast<const void*>(&grouped_gemm_kernel<MODE_WIDE, 0>), "q4_matmul"},
+      {MODE_NARROW, 0, reinterpret_cast<const void*>(&grouped_gemm_kernel<MODE_NARROW, 0>), "q4_matmul"},
+  };
+  static bool lds_raised[sizeof(variants) / sizeof(variants[0])] = {};
+  int v = -1;
+  for (int i = 0; i < static_cast<int>(sizeof(variants) / sizeof(variants[0])); ++i)
+    if (variants[i].mode == mode && variants[i].flags == flags) v = i;
+  if (v < 0) return obs::set_error(ctx, OBS_E_INVALID, "grouped GEMM: unsupported launch (mode %u, flags %u)", mode, flags);
+  const void* fn = variants[v].fn;
+  const char* name = variants[v].name;
+  if (!lds_raised[v]) {  // the staged scales can take the block past 64 KB of LDS (gfx950 has 160 KB)
+    OBS_HIP_TRY(ctx, hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, SB_LDS_MAX));
+    lds_raised[v] = true;
+  }
+  void* args[] = {&a};
+  OBS_LAUNCH(ctx, name, OBS_HIP_TRY(ctx, hipLaunchKernel(fn, dim3(grid), dim3(256), args, lds, ctx->stream)));
   return OBS_OK;
 }
 
@@ -673,34 +966,39 @@ int obs_moe_prefill(obs_ctx* ctx, const obs_moe_config* cfg, const obs_moe_layer
   }
   int32_t* counts = reinterpret_cast<int32_t*>(base + L.counts);
   int32_t* offsets = reinterpret_cast<int32_t*>(base + L.offsets);
-  int32_t* ntiles = reinterpret_cast<int32_t*>(base + L.ntiles);
   int32_t* row_token = reinterpret_cast<int32_t*>(base + L.row_token);
   int32_t* row_slot = reinterpret_cast<int32_t*>(base + L.row_slot);
-  int4* tiles = reinterpret_cast<int4*>(base + L.tiles);
+  int4* work_gu = reinterpret_cast<int4*>(base + L.work_gu);
+  int4* work_dn = reinterpret_cast<int4*>(base + L.work_dn);
   uint16_t* Hbuf = reinterpret_cast<uint16_t*>(base + L.H);
   uint16_t* Yp = reinterpret_cast<uint16_t*>(base + L.Yp);
   int32_t* chunk_cnt = reinterpret_cast<int32_t*>(base + L.chunk_cnt);
   OBS_LAUNCH(ctx, "moe_group_count", group_count_kernel<<<L.nchunks, 64, 0, ctx->stream>>>(ids, T, k, E, chunk_cnt));
-  OBS_LAUNCH(ctx, "moe_group_scan", group_scan_kernel<<<1, 256, 0, ctx->stream>>>(L.nchunks, E, chunk_cnt, counts,
-                                                                                   offsets, tiles, ntiles));
-  OBS_LAUNCH(ctx, "moe_group_rank", group_rank_kernel<<<L.nchunks, 64, 0, ctx->stream>>>(ids, T, k, E, chunk_cnt,
-                                                                                          row_token, row_slot));
+  OBS_LAUNCH(ctx, "moe_group_scan",
+             group_scan_kernel<<<1, 256, 0, ctx->stream>>>(L.nchunks, E, chunk_cnt, counts, offsets));
+  const uint32_t cols_dn = mode_cols(gemm_mode(false, H));
+  int32_t* work_cnt = reinterpret_cast<int32_t*>(base + L.work_cnt);
+  const WorkTable wt_gu{work_gu, work_cnt, L.grid_gu, I / TN, TN, COST_GATEUP};
+  const WorkTable wt_dn{work_dn, work_cnt + 8, L.grid_dn, H / cols_dn, cols_dn, COST_DOWN};
+  OBS_LAUNCH(ctx, "moe_group_rank",
+             group_rank_kernel<<<L.nchunks + 2u, 64, 0, ctx->stream>>>(ids, T, k, E, chunk_cnt, row_token, row_slot,
+                                                                       counts, offsets, wt_gu, wt_dn));
   GemmArgs g{};
   g.A = Xin; g.a_rows = row_token; g.a_rows_total = T;
   g.w0 = layer->gate_w; g.s0 = layer->gate_s; g.b0 = layer->gate_b;
   g.w1 = layer->up_w; g.s1 = layer->up_s; g.b1 = layer->up_b;
   g.out = Hbuf; g.out_rows = nullptr;
-  g.tiles = tiles; g.n_tiles = ntiles;
+  g.work = work_gu; g.work_count = work_cnt;
   g.K = H; g.N = I;
-  rc = launch_gemm(ctx, true, g, L.max_tiles);
+  rc = launch_gemm(ctx, true, g, L.grid_gu);
   if (rc) return rc;
   GemmArgs d{};
   d.A = Hbuf; d.a_rows = nullptr; d.a_rows_total = T * k;
   d.w0 = layer->down_w; d.s0 = layer->down_s; d.b0 = layer->down_b;
   d.out = Yp; d.out_rows = row_slot;
-  d.tiles = tiles; d.n_tiles = ntiles;
+  d.work = work_dn; d.work_count = work_cnt + 8;
   d.K = I; d.N = H;
-  rc = launch_gemm(ctx, false, d, L.max_tiles);
+  rc = launch_gemm(ctx, false, d, L.grid_dn);
   if (rc) return rc;
   OBS_LAUNCH(ctx, "moe_combine", combine_kernel<<<T, H / 8u, 0, ctx->stream>>>(Yp, ids, weights, residual, Y, k, H, E));
   return OBS_OK;
@@ -714,20 +1012,22 @@ int obs_q4_matmul(obs_ctx* ctx, const uint32_t* w, const uint16_t* scales, const
   if (in == 0 || in % (4u * GK) != 0 || out == 0 || out % TN != 0)
     return obs::set_error(ctx, OBS_E_SHAPE, "obs_q4_matmul: in must be a multiple of %u and out of %u (got %u, %u)",
                           4u * GK, TN, in, out);
-  if (gemm_sb_bytes(false, in) > SB_LDS_MAX)
-    return obs::set_error(ctx, OBS_E_SHAPE, "obs_q4_matmul: in must be at most %u (got %u)",
-                          static_cast<uint32_t>(SB_LDS_MAX / (sizeof(uint32_t) * SB_STRIDE)) * GK, in);
+  if (gemm_sb_bytes(gemm_mode(false, out), in) > SB_LDS_MAX)
+    return obs::set_error(ctx, OBS_E_SHAPE, "obs_q4_matmul: in must be at most %u for out = %u (got %u)",
+                          static_cast<uint32_t>(SB_LDS_MAX / (sizeof(uint32_t) * SB_STRIDE) /
+                                                (out % (2u * TN) == 0 ? 2u : 1u)) * GK, out, in);
   if (!obs::aligned(X, 16) || !obs::aligned(w, 16) || !obs::aligned(Y, 16))
     return obs::set_error(ctx, OBS_E_ALIGN, "obs_q4_matmul: X, w and Y must be 16-byte aligned");
   if (T == 0) return OBS_OK;
   const uint32_t tiles = (T + TM - 1) / TM;
+  const uint32_t grid = gemm_grid(tiles, out, gemm_mode(false, out));
   GemmArgs g{};
   g.A = X; g.a_rows = nullptr; g.a_rows_total = T;
   g.w0 = w; g.s0 = scales; g.b0 = biases;
   g.out = Y; g.out_rows = nullptr;
-  g.tiles = nullptr; g.n_tiles = nullptr; g.dense_rows = T;
+  g.work = nullptr; g.work_count = nullptr; g.dense_rows = T;
   g.K = in; g.N = out;
-  return launch_gemm(ctx, false, g, tiles);
+  return launch_gemm(ctx, false, g, grid);
 }
 
 }  // extern "C"

@@ -129,6 +129,27 @@ def test_moe_prefill_zipf_vs_oracle(exe, qwen, T, seed):
     print(f"T={T}: rel vs bf16-operand oracle {rel_bf:.2e}, vs fp64 oracle {rel64:.2e}")
 
 
+def test_moe_prefill_many_tiles_even_split(exe):
+    """More than 2048 row tiles (40,000 tokens x 8 ranks over 16 experts):
+    the GEMM work tables fall back from the cost-balanced longest-first
+    schedule to an even split by count. Each token's output depends on that
+    token alone, so a sample of tokens is checked against the oracle run on
+    just those tokens."""
+    e, k, h, i, T = 16, 8, 1024, 256, 40000
+    t = synth.moe_layer(31, e, h, i, 64)
+    layer, L = oh.MoeLayer.upload(exe, t), O.Layer(t, e, h, i, 64)
+    cfg = oh.MoeConfig(e, k, h, i, 64, True)
+    rng = np.random.default_rng(990)
+    X = synth.bf16_normal(rng, (T, h))
+    ids, w = synth.zipf_routing(T, e, k, 1.1, seed=9)
+    assert sum(-(-int(np.sum(ids == x)) // 128) for x in range(e)) > 2048
+    y = _f32(_prefill(exe, cfg, layer, X, ids, w))
+    sel = np.sort(rng.choice(T, 384, replace=False))
+    ref_bf = O.moe_prefill(L, X[sel], ids[sel], w[sel], O.MODE_MFMA_BF16)
+    _close(y[sel], ref_bf, BF_NORM, BF_ELEM)
+    assert np.all(np.isfinite(y))
+
+
 def test_moe_prefill_computed_routing_and_residual(exe, qwen):
     t, layer, L = qwen
     cfg = oh.MoeConfig(E, K, H, I, 64, True)
