@@ -29,6 +29,16 @@
  *   orc_moe_decode / _prefill ... one-hot routing weight reproduces one expert;
  *                                 prefill with T=1 equals decode; linearity in the
  *                                 routing weights; grouping invariants.
+ *   orc_rope_neox ............... pos 0 is the identity bit for bit; the complex
+ *                                 rotation (x0 + i x1) e^{i pos f_i} in numpy fp64
+ *                                 within one bf16 step; pair norms preserved; pair
+ *                                 i = 0 turns by exactly pos radians.
+ *   orc_sdpa_decode ............. one position returns v; equal keys return the
+ *                                 mean of v; a dominant score returns its v; the
+ *                                 GQA head map (kv head h / (n_heads / n_kv)) seen
+ *                                 through distinct kv heads; a numpy restatement.
+ *   orc_argmax .................. ties -> first index, NaN skipped, all -inf -> 0,
+ *                                 numpy argmax where no NaN.
  */
 #include "oracle.h"
 
@@ -608,4 +618,70 @@ int orc_omp_max_threads(void) {
 #else
   return 1;
 #endif
+}
+
+/* ------------------------------------------------------------------------- */
+/* Attention half of a decoder layer                                          */
+/* ------------------------------------------------------------------------- */
+
+int orc_rope_neox(uint16_t* x, int64_t n_heads, int64_t head_dim, int64_t pos, float theta) {
+  if (n_heads < 0 || head_dim <= 0 || head_dim % 2 != 0 || pos < 0) return -1;
+  const int64_t half = head_dim / 2;
+  for (int64_t i = 0; i < half; ++i) {
+    const float f = (float)pow((double)theta, -2.0 * (double)i / (double)head_dim);
+    const float angle = (float)pos * f;
+    const float c = (float)cos((double)angle), sn = (float)sin((double)angle);
+    for (int64_t h = 0; h < n_heads; ++h) {
+      uint16_t* r = x + h * head_dim;
+      const float x0 = orc_bf16_to_f32(r[i]), x1 = orc_bf16_to_f32(r[i + half]);
+      const float a = x0 * c, b = x1 * sn, cc = x1 * c, d = x0 * sn;
+      r[i] = orc_f32_to_bf16(a - b);
+      r[i + half] = orc_f32_to_bf16(cc + d);
+    }
+  }
+  return 0;
+}
+
+int orc_sdpa_decode(const uint16_t* q, const uint16_t* k, const uint16_t* v, int64_t n_heads, int64_t n_kv,
+                    int64_t head_dim, int64_t max_len, int64_t seq_len, double scale, double* out) {
+  if (n_heads <= 0 || n_kv <= 0 || n_heads % n_kv != 0 || head_dim <= 0 || seq_len <= 0 || seq_len > max_len)
+    return -1;
+  const int64_t grp = n_heads / n_kv;
+  double* p = (double*)malloc(sizeof(double) * (size_t)seq_len);
+  if (!p) return -1;
+  for (int64_t h = 0; h < n_heads; ++h) {
+    const int64_t kv = h / grp;
+    const uint16_t* qh = q + h * head_dim;
+    double mx = -INFINITY;
+    for (int64_t t = 0; t < seq_len; ++t) {
+      const uint16_t* kt = k + (kv * max_len + t) * head_dim;
+      double dot = 0.0;
+      for (int64_t d = 0; d < head_dim; ++d) dot += (double)orc_bf16_to_f32(qh[d]) * (double)orc_bf16_to_f32(kt[d]);
+      p[t] = dot * scale;
+      if (p[t] > mx) mx = p[t];
+    }
+    double sum = 0.0;
+    for (int64_t t = 0; t < seq_len; ++t) {
+      p[t] = exp(p[t] - mx);
+      sum += p[t];
+    }
+    for (int64_t d = 0; d < head_dim; ++d) {
+      double acc = 0.0;
+      for (int64_t t = 0; t < seq_len; ++t) acc += p[t] * (double)orc_bf16_to_f32(v[(kv * max_len + t) * head_dim + d]);
+      out[h * head_dim + d] = acc / sum;
+    }
+  }
+  free(p);
+  return 0;
+}
+
+int64_t orc_argmax(const float* x, int64_t n) {
+  int64_t best = 0;
+  float bv = -INFINITY;
+  for (int64_t i = 0; i < n; ++i)
+    if (x[i] > bv) {
+      bv = x[i];
+      best = i;
+    }
+  return best;
 }

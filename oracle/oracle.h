@@ -14,6 +14,9 @@
  *   - RMSNorm (post-attention, router input) . shaders/rmsnorm.metal:17-35, src/forward.rs:419
  *   - decode MoE composition ................ src/forward.rs:421-441
  *   - prefill grouping + rank-order combine . src/forward.rs:200-232
+ *   - NeoX RoPE, GQA decode SDPA, argmax .... shaders/rope.metal:12-26,
+ *                                             shaders/sdpa_decode.metal:22-47,
+ *                                             src/forward.rs:563-566
  *
  * Every function is pinned by a check in tests/ (known-answer vectors,
  * closed forms, brute force on small inputs or invariants); the header of
@@ -143,6 +146,30 @@ int orc_group_rows(const int32_t* ids, int64_t T, int k, int n_exp,
  * rank order (the operand roundings of the HIP grouped GEMM). y_out [T, H] fp64. */
 int orc_moe_prefill(const orc_layer* L, const uint16_t* x_bf16, int64_t T, int k,
                     const int32_t* ids, const float* w, int mode, double* y_out);
+
+/* ---- attention half of a decoder layer (forward.rs:403-419) ---- */
+
+/* NeoX (half-split) rotary embedding at one position, in place on bf16
+ * [n_heads, head_dim] (rope.metal:12-26): for i < head_dim/2 the pair
+ * (x[i], x[i + head_dim/2]) rotates by angle = fl32(pos * f_i) with
+ * f_i = fl32(theta^(-2i/head_dim)) (pow in double, rounded once), c and s =
+ * cos and sin of that fp32 angle evaluated in double and rounded once;
+ * r0 = x0*c - x1*s, r1 = x1*c + x0*s with each product rounded (no fma), then
+ * RNE to bf16. head_dim even. Returns 0, or -1 on a bad shape. */
+int orc_rope_neox(uint16_t* x, int64_t n_heads, int64_t head_dim, int64_t pos, float theta);
+
+/* Single-query GQA attention over a cache (sdpa_decode.metal:22-47), fp64
+ * truth: query head h reads kv head h / (n_heads / n_kv); scores
+ * s_t = scale * q.k_t for t < seq_len, softmax over t, out = sum_t p_t v_t.
+ * q bf16 [n_heads, head_dim]; k, v bf16 [n_kv, max_len, head_dim];
+ * out fp64 [n_heads, head_dim]. Returns 0, or -1 on a bad shape. */
+int orc_sdpa_decode(const uint16_t* q, const uint16_t* k, const uint16_t* v, int64_t n_heads, int64_t n_kv,
+                    int64_t head_dim, int64_t max_len, int64_t seq_len, double scale, double* out);
+
+/* Greedy token (forward.rs:563-566): the first index whose value is strictly
+ * greater than every earlier one, starting from -inf at index 0; NaN never
+ * wins. n == 0 or no value above -inf: 0. */
+int64_t orc_argmax(const float* x, int64_t n);
 
 /* CPU baseline: the decode MoE half of one token in the reference's shader
  * semantics, OpenMP over output rows (nthreads <= 0: all). Returns 0. */

@@ -66,6 +66,11 @@ def lib() -> C.CDLL:
         L.orc_moe_prefill.argtypes = [C.POINTER(OrcLayer), vp, i64, i32, vp, vp, i32, vp]
         L.orc_moe_decode_baseline.argtypes = [C.POINTER(OrcLayer), vp, i32, i32, i32, vp, vp, vp]
         L.orc_rmsnorm.argtypes = [vp, vp, C.c_float, i64, i64, vp]
+        L.orc_rope_neox.argtypes = [vp, i64, i64, i64, C.c_float]
+        L.orc_sdpa_decode.argtypes = [vp, vp, vp, i64, i64, i64, i64, i64, C.c_double, vp]
+        L.orc_argmax.restype = i64
+        L.orc_argmax.argtypes = [vp, i64]
+        L.orc_f32_to_bf16_n.argtypes = [vp, vp, i64]
         L.orc_omp_max_threads.restype = C.c_int
         _L = L
     return _L
@@ -233,6 +238,91 @@ def moe_decode_baseline(layer: Layer, x_bf16, k: int, norm_topk: bool = True, nt
 
 def omp_max_threads() -> int:
     return lib().orc_omp_max_threads()
+
+
+# ---- attention half and the whole decoder (forward.rs:398-443, :552-567) ----
+def rope_neox(x_bf16, pos: int, theta: float) -> np.ndarray:
+    """NeoX RoPE of bf16 [n_heads, head_dim] at `pos` -> new bf16 array (orc_rope_neox)."""
+    x = np.array(_c(x_bf16, np.uint16), copy=True)
+    _rc(lib().orc_rope_neox(_p(x), x.shape[0], x.shape[1], pos, theta), "rope")
+    return x
+
+
+def sdpa_decode(q_bf16, k_cache, v_cache, seq_len: int, scale: float) -> np.ndarray:
+    """GQA single-query attention, fp64 [n_heads, head_dim]; caches bf16 [n_kv, max_len, head_dim]."""
+    q, k, v = _c(q_bf16, np.uint16), _c(k_cache, np.uint16), _c(v_cache, np.uint16)
+    nh, hd = q.shape
+    nkv, ml, _ = k.shape
+    out = np.empty((nh, hd), np.float64)
+    _rc(lib().orc_sdpa_decode(_p(q), _p(k), _p(v), nh, nkv, hd, ml, seq_len, scale, _p(out)), "sdpa")
+    return out
+
+
+def argmax(x_f32) -> int:
+    x = _c(x_f32, np.float32)
+    return int(lib().orc_argmax(_p(x), x.size))
+
+
+def _bf16(a) -> np.ndarray:
+    """fp32 (or fp64 rounded to fp32 first) -> bf16 bits, RNE (orc_f32_to_bf16_n)."""
+    f = np.ascontiguousarray(a, dtype=np.float32)
+    out = np.empty(f.shape, np.uint16)
+    lib().orc_f32_to_bf16_n(_p(f), _p(out), f.size)
+    return out
+
+
+def _proj(P: Dict[str, np.ndarray], name: str, x_bf16, in_f: int, out_f: int) -> np.ndarray:
+    """4-bit projection in fp64 on the exact weights, rounded to bf16 (the stored activation)."""
+    xf = (_c(x_bf16, np.uint16).astype(np.uint32) << 16).view(np.float32)
+    y, _ = qmatvec("f64", 4, P[name + "_w"], P[name + "_s"], P[name + "_b"], xf, in_f, out_f)
+    return _bf16(y)
+
+
+def decoder_layer(P: Dict[str, np.ndarray], moe: "Layer", x_bf16, k_cache, v_cache, pos: int, cfg: Dict):
+    """One decoder layer for one token at position `pos` (forward.rs:398-443):
+    attention half with bf16 activations (projections in fp64 on the exact
+    weights, rounded to bf16; per-head q/k RMSNorm; NeoX RoPE; the caches get k
+    and v at `pos`; attention in fp64 rounded to bf16; x1 = bf16(x + o)), then
+    the MoE half x1 + sum_r w_r expert_r(rmsnorm(x1)) in fp64, rounded to bf16.
+    k_cache, v_cache (bf16 [n_kv, max_len, head_dim]) are updated in place."""
+    H, nh, nkv, hd = cfg["hidden"], cfg["n_heads"], cfg["n_kv"], cfg["head_dim"]
+    eps, theta = cfg["eps"], cfg["theta"]
+    x = _c(x_bf16, np.uint16)
+    xn = rmsnorm(x, P["in_norm"], eps)
+    q = _proj(P, "q", xn, H, nh * hd).reshape(nh, hd)
+    k = _proj(P, "k", xn, H, nkv * hd).reshape(nkv, hd)
+    v = _proj(P, "v", xn, H, nkv * hd).reshape(nkv, hd)
+    q = rope_neox(rmsnorm(q, P["q_norm"], eps), pos, theta)
+    k = rope_neox(rmsnorm(k, P["k_norm"], eps), pos, theta)
+    k_cache[:, pos, :] = k
+    v_cache[:, pos, :] = v
+    attn = _bf16(sdpa_decode(q, k_cache, v_cache, pos + 1, hd ** -0.5)).reshape(-1)
+    o = _proj(P, "o", attn, nh * hd, H)
+    x1 = _bf16(_f32(x) + _f32(o))
+    x1n = rmsnorm(x1, P["post_norm"], eps)
+    _, ids, w = router(moe, x1n, cfg["top_k"], cfg["norm_topk"])
+    y, _, _ = moe_decode(moe, x1n, cfg["top_k"], cfg["norm_topk"], ids=ids, w=w)
+    return _bf16(y[0] + _f32(x1))
+
+
+def _f32(b) -> np.ndarray:
+    return (_c(b, np.uint16).astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+
+
+def token_logits(G: Dict[str, np.ndarray], layers, tok: int, caches, pos: int, cfg: Dict) -> np.ndarray:
+    """One greedy decode step (run_one_token, forward.rs:552-567): the q4
+    embedding row of `tok` (bf16), every layer at `pos`, the final RMSNorm and
+    the 4-bit lm_head in fp64. layers: [(P, moe Layer)]; caches: [(k, v)].
+    Returns fp64 logits [vocab]."""
+    H, V = cfg["hidden"], cfg["vocab"]
+    x = _bf16(dequant(4, G["embed_w"][tok:tok + 1], G["embed_s"][tok:tok + 1], G["embed_b"][tok:tok + 1],
+                      1, H).reshape(-1))
+    for (P, moe), (kc, vc) in zip(layers, caches):
+        x = decoder_layer(P, moe, x, kc, vc, pos, cfg)
+    xn = rmsnorm(x, G["final_norm"], cfg["eps"])
+    xf = (xn.astype(np.uint32) << 16).view(np.float32)
+    y, _ = qmatvec("f64", 4, G["lm_w"], G["lm_s"], G["lm_b"], xf, H, V)
+    return y
 
 
 # ---- independent NumPy restatement (validate_dequant.py:26-30) --------------

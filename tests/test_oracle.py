@@ -421,3 +421,106 @@ def test_prefill_t1_equals_decode_and_bf16_mode_close(small_layer):
     yb = O.moe_prefill(L, X, ids, w, O.MODE_MFMA_BF16)
     rel = np.linalg.norm(yb - yp) / np.linalg.norm(yp)
     assert 0 < rel < 1e-2
+
+
+# ---- attention half: RoPE, GQA decode SDPA, argmax ---------------------------
+
+def _b2f(b):
+    return synth.bf16_bits_to_f32(b).astype(np.float64)
+
+
+def test_rope_pos0_is_identity_and_pair0_turns_by_pos():
+    rng = np.random.default_rng(40)
+    x = synth.bf16_normal(rng, (6, 128))
+    assert np.array_equal(O.rope_neox(x, 0, 1e7), x)  # cos 0 = 1, sin 0 = 0 exactly
+    # pair i = 0 has frequency theta^0 = 1: it turns by exactly pos radians
+    y = O.rope_neox(x, 3, 1e7)
+    c, s = math.cos(3.0), math.sin(3.0)
+    x0, x1 = _b2f(x[:, 0]), _b2f(x[:, 64])
+    assert np.allclose(_b2f(y[:, 0]), x0 * c - x1 * s, rtol=2 ** -7, atol=1e-6)
+    assert np.allclose(_b2f(y[:, 64]), x1 * c + x0 * s, rtol=2 ** -7, atol=1e-6)
+
+
+@pytest.mark.parametrize("pos,theta", [(1, 1e7), (517, 1e7), (4095, 1e7), (77, 1e4)])
+def test_rope_matches_complex_rotation(pos, theta):
+    """Independent restatement: (x0 + i x1) * exp(i * pos * theta^(-2i/d)) in
+    fp64 (complex multiply), within one bf16 step of the oracle; pair norms
+    are preserved within the same bound."""
+    rng = np.random.default_rng(41 + pos)
+    hd = 128
+    x = synth.bf16_normal(rng, (4, hd))
+    y = _b2f(O.rope_neox(x, pos, theta))
+    i = np.arange(hd // 2)
+    f = np.float32(theta) ** (-2.0 * i / hd)                      # fp64 pow of the fp32 theta
+    ang = np.float32(pos) * f.astype(np.float32)                   # the fp32 angle
+    z = (_b2f(x[:, :hd // 2]) + 1j * _b2f(x[:, hd // 2:])) * np.exp(1j * ang.astype(np.float64))
+    tol = 2 ** -7 * np.abs(z) + 1e-30
+    assert np.all(np.abs(y[:, :hd // 2] - z.real) <= tol)
+    assert np.all(np.abs(y[:, hd // 2:] - z.imag) <= tol)
+    n_in = np.hypot(_b2f(x[:, :hd // 2]), _b2f(x[:, hd // 2:]))
+    n_out = np.hypot(y[:, :hd // 2], y[:, hd // 2:])
+    assert np.all(np.abs(n_out - n_in) <= 2 ** -7 * n_in + 1e-30)
+
+
+def test_rope_rejects_odd_head_dim():
+    with pytest.raises(ValueError):
+        O.rope_neox(np.zeros((2, 3), np.uint16), 1, 1e7)
+
+
+def _cache(rng, nkv, ml, hd):
+    return synth.bf16_normal(rng, (nkv, ml, hd)), synth.bf16_normal(rng, (nkv, ml, hd))
+
+
+def test_sdpa_one_position_returns_v_and_equal_keys_average():
+    rng = np.random.default_rng(42)
+    nh, nkv, hd, ml = 8, 2, 64, 16
+    q = synth.bf16_normal(rng, (nh, hd))
+    k, v = _cache(rng, nkv, ml, hd)
+    out = O.sdpa_decode(q, k, v, 1, hd ** -0.5)
+    for h in range(nh):
+        assert np.array_equal(out[h], _b2f(v[h // (nh // nkv), 0]))  # softmax of one score is 1
+    k_eq = np.repeat(k[:, :1, :], ml, axis=1)  # every key equal: uniform weights
+    out = O.sdpa_decode(q, k_eq, v, 5, hd ** -0.5)
+    for h in range(nh):
+        assert np.allclose(out[h], _b2f(v[h // (nh // nkv), :5]).mean(axis=0), rtol=1e-12, atol=1e-12)
+
+
+def test_sdpa_dominant_score_and_gqa_map():
+    rng = np.random.default_rng(43)
+    nh, nkv, hd, ml = 8, 4, 64, 8
+    q = np.full((nh, hd), 0x3F80, np.uint16)   # all ones
+    k = np.zeros((nkv, ml, hd), np.uint16)
+    v = synth.bf16_normal(rng, (nkv, ml, hd))
+    for kv in range(nkv):
+        k[kv, kv + 1, :] = 0x4120  # 10.0: position kv + 1 dominates kv head kv (score 640 * scale)
+    out = O.sdpa_decode(q, k, v, 6, 1.0)
+    for h in range(nh):
+        kv = h // (nh // nkv)                   # query heads 2kv, 2kv+1 read kv head kv
+        assert np.allclose(out[h], _b2f(v[kv, kv + 1]), rtol=0, atol=1e-200)
+
+
+def test_sdpa_matches_numpy_restatement():
+    rng = np.random.default_rng(44)
+    nh, nkv, hd, ml, L = 16, 4, 128, 40, 33
+    q = synth.bf16_normal(rng, (nh, hd))
+    k, v = _cache(rng, nkv, ml, hd)
+    out = O.sdpa_decode(q, k, v, L, hd ** -0.5)
+    qf, kf, vf = _b2f(q), _b2f(k), _b2f(v)
+    for h in range(nh):
+        kv = h * nkv // nh
+        s = kf[kv, :L] @ qf[h] * hd ** -0.5
+        p = np.exp(s - s.max())
+        assert np.allclose(out[h], p @ vf[kv, :L] / p.sum(), rtol=1e-12, atol=1e-12)
+
+
+def test_argmax_semantics():
+    assert O.argmax(np.array([1, 5, 5, 2], np.float32)) == 1           # first of a tie
+    assert O.argmax(np.array([np.nan, 3, np.nan, 7], np.float32)) == 3  # NaN never wins
+    assert O.argmax(np.array([np.nan, np.nan], np.float32)) == 0
+    assert O.argmax(np.full(5, -np.inf, np.float32)) == 0               # nothing above -inf
+    assert O.argmax(np.array([-np.inf, -1e30], np.float32)) == 1
+    rng = np.random.default_rng(45)
+    for _ in range(20):
+        x = rng.standard_normal(1000).astype(np.float32)
+        x[rng.integers(0, 1000, 5)] = x.max()
+        assert O.argmax(x) == int(np.argmax(x))
