@@ -253,6 +253,61 @@ int obs_moe_prefill(obs_ctx* ctx, const obs_moe_config* cfg, const obs_moe_layer
                     const int32_t* ids, const float* weights, void* ws, size_t ws_bytes);
 
 /* ------------------------------------------------------------------ */
+/* The rest of a decode step around the MoE block                      */
+/* (the attention half of Model::forward_layer, forward.rs:398-419;    */
+/*  Model::embed :445-462; run_one_token :552-567)                     */
+/* ------------------------------------------------------------------ */
+/* Decode steps read their position and token from a device array
+ * state = {pos, tok} (int32); obs_argmax writes the next token and advances
+ * pos, so one captured graph of a whole step replays for every token.
+ * Caches are bf16: keys [n_kv, max_len, head_dim] (kv_cache.rs:3), values
+ * transposed [n_kv, head_dim, max_len]. */
+
+/* One 4-bit MLX-affine matrix of a fused mat-vec: rows x in, y = W x in fp32,
+ * written as fp32 (y_f32) and/or bf16 (y_bf16 = RNE(residual + W x) when
+ * residual is set). Replaces Model::dequant_named (forward.rs:339-343). */
+typedef struct obs_gemv_part {
+  const uint32_t* w; const uint16_t* scales; const uint16_t* biases; /* [rows, in/8], [rows, in/64] */
+  float* y_f32; uint16_t* y_bf16; const uint16_t* residual;
+  uint32_t rows;
+} obs_gemv_part;
+/* y_i = W_i x for 1-3 matrices sharing x (bf16 [in]) in one launch (q, k, v
+ * projections; lm_head; o_proj with the residual add of forward.rs:418).
+ * in 2048 or 4096, group 64. */
+int obs_q4_gemv(obs_ctx* ctx, const uint16_t* x, uint32_t in, uint32_t group, const obs_gemv_part* parts,
+                uint32_t n_parts);
+
+/* Per-head q/k RMSNorm (q_norm/k_norm weights [head_dim], eps), NeoX RoPE at
+ * state[0] with rope_theta, q rotated in place, k and v appended to the caches
+ * at state[0] (forward.rs:407-416, rope.metal, ops.metal:31-36). q bf16
+ * [n_heads, head_dim], k, v bf16 [n_kv, head_dim]. head_dim 128, n_heads a
+ * multiple of n_kv (at most 16 per kv head), max_len a multiple of 32; a
+ * position outside [0, max_len) appends nothing. */
+int obs_attn_prep(obs_ctx* ctx, uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* q_norm,
+                  const uint16_t* k_norm, uint16_t* k_cache, uint16_t* v_cache_t, uint32_t n_heads, uint32_t n_kv,
+                  uint32_t head_dim, uint32_t max_len, float eps, float theta, const int32_t* state);
+
+/* Workspace bytes of obs_sdpa_decode (0 for an unsupported shape). */
+size_t obs_sdpa_workspace(uint32_t n_heads, uint32_t n_kv, uint32_t head_dim, uint32_t max_len);
+/* Single-query GQA attention over positions [0, state[0]] (Attention::sdpa,
+ * attention.rs:23-41; sdpa_decode.metal): scale 1/sqrt(head_dim), query head h
+ * reads kv head h / (n_heads / n_kv). out bf16 [n_heads, head_dim]. */
+int obs_sdpa_decode(obs_ctx* ctx, const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache_t, uint16_t* out,
+                    uint32_t n_heads, uint32_t n_kv, uint32_t head_dim, uint32_t max_len, const int32_t* state,
+                    void* ws, size_t ws_bytes);
+
+/* out = bf16 row state[1] of a 4-bit embedding table [vocab, hidden] (Model::embed,
+ * forward.rs:445-462; the token is clamped into [0, vocab)). */
+int obs_embed_q4(obs_ctx* ctx, const uint32_t* w, const uint16_t* scales, const uint16_t* biases, uint32_t hidden,
+                 uint32_t group, uint32_t vocab, const int32_t* state, uint16_t* out);
+
+/* Greedy token of fp32 logits [n] (forward.rs:563-566: first index of the
+ * maximum, NaN never wins, 0 when nothing exceeds -inf) into state[1], then
+ * state[0] += 1. ws: obs_argmax_workspace() bytes, 8-byte aligned. */
+size_t obs_argmax_workspace(void);
+int obs_argmax(obs_ctx* ctx, const float* x, uint32_t n, int32_t* state, void* ws, size_t ws_bytes);
+
+/* ------------------------------------------------------------------ */
 /* Checkpoint loading: safetensors -> HBM-resident expert table        */
 /* (replaces Qwen3MoeConfig::from_file model.rs:26-30,                 */
 /*  Weights::load_non_expert weight_loader.rs:19-71, ExpertIndex::open */

@@ -1,0 +1,558 @@
+// obs_attention.hip — the rest of a decode step around the MoE block: the
+// attention half of a decoder layer and the token step's ends
+// (src/forward.rs:398-419, :445-462, :552-567; shaders/rope.metal,
+// shaders/sdpa_decode.metal, shaders/ops.metal:31-36, src/attention.rs,
+// src/kv_cache.rs).
+//
+// Device state. A decode step reads its position and token from a device
+// array state = {pos, tok} and the argmax at its end writes the next token and
+// advances pos, so one captured graph of a whole step replays for every
+// token with no host work in between.
+//
+// Caches (bf16): keys [n_kv, max_len, head_dim] as the reference lays them
+// out (kv_cache.rs:3), values transposed [n_kv, head_dim, max_len] so that the
+// attention's value operand reads consecutive positions of one dimension.
+#include "obs_internal.hpp"
+
+namespace {
+
+using namespace obsd;
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+constexpr uint32_t HD = 128;  // head_dim the attention kernels are written for
+
+// ---------------------------------------------------------------------------
+// 4-bit mat-vec for the decoder's projections and lm_head
+// ---------------------------------------------------------------------------
+// One wave per output row, four rows in flight per wave. Lane l covers
+// columns [2048 s + 32 l, +32) of every 2048-column segment s: one coalesced
+// 16-byte load per row and segment (a 1 KB row segment per wave load). The
+// 32 nibbles are dotted with the lane's activations as f16 pairs through the
+// magic-offset unpack (dot8_q4_off, 9 instructions per 8 nibbles), then
+// y_lane = s (sum q x) + b (sum x) with the lane's group scale and bias, and
+// the wave sums in the butterfly order (wave_sum_asc).
+struct GemvPart {
+  const uint32_t* w;
+  const uint16_t* s;
+  const uint16_t* b;
+  float* y_f32;
+  uint16_t* y_bf16;
+  const uint16_t* residual;  // y = residual + W x (bf16 output only)
+  uint32_t rows;
+};
+struct GemvArgs {
+  GemvPart p[3];
+  uint32_t n_parts, total_rows, in;
+};
+
+template <uint32_t SEG>
+__global__ void __launch_bounds__(256) q4_gemv_kernel(const uint16_t* __restrict__ x, GemvArgs a) {
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t wave_g = blockIdx.x * 4u + (threadIdx.x >> 6), n_waves = gridDim.x * 4u;
+  constexpr uint32_t IN = 2048u * SEG, GROUPS = IN / 64u;
+  // the lane's activations (f16 pairs), their sum and the offset part, per segment
+  f16x2_t xh[SEG][16];
+  float xs[SEG], xoff[SEG];
+#pragma unroll
+  for (uint32_t sg = 0; sg < SEG; ++sg) {
+    const uint4* xp = reinterpret_cast<const uint4*>(x + 2048u * sg + 32u * lane);
+    float xf[32];
+#pragma unroll
+    for (uint32_t i = 0; i < 4; ++i) {
+      const uint4 v = xp[i];
+      const uint32_t wd[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (uint32_t j = 0; j < 4; ++j) {
+        xf[8 * i + 2 * j] = bf16lo(wd[j]);
+        xf[8 * i + 2 * j + 1] = bf16hi(wd[j]);
+      }
+    }
+    float sum = 0.0f;
+#pragma unroll
+    for (uint32_t c = 0; c < 32; ++c) sum = sum + xf[c];
+    xs[sg] = sum;
+#pragma unroll
+    for (uint32_t i = 0; i < 4; ++i) f16_pairs8(xf + 8 * i, xh[sg] + 4 * i);
+    float off = 0.0f;
+#pragma unroll
+    for (uint32_t i = 0; i < 4; ++i) off = dot8_off_only(xh[sg] + 4 * i, off);
+    xoff[sg] = off;
+  }
+  // a part's fields by index, as selects (indexing the argument struct would copy it to scratch)
+  auto part_of = [&](uint32_t pi) __attribute__((always_inline)) {
+    return pi == 0u ? a.p[0] : (pi == 1u ? a.p[1] : a.p[2]);
+  };
+  for (uint32_t r0 = 4u * wave_g; r0 < a.total_rows; r0 += 4u * n_waves) {
+    uint4 q[4][SEG];
+    uint16_t sc[4][SEG], bi[4][SEG];
+    uint32_t pidx[4], prow[4];
+    // every load of the four rows first (rows past the end reload the last one)
+#pragma unroll
+    for (uint32_t k = 0; k < 4; ++k) {
+      uint32_t r = min(r0 + k, a.total_rows - 1u), pi = 0;
+      if (a.n_parts > 1u && r >= a.p[0].rows) {
+        r -= a.p[0].rows;
+        pi = 1;
+        if (a.n_parts > 2u && r >= a.p[1].rows) {
+          r -= a.p[1].rows;
+          pi = 2;
+        }
+      }
+      pidx[k] = pi;
+      prow[k] = r;
+      const GemvPart P = part_of(pi);
+#pragma unroll
+      for (uint32_t sg = 0; sg < SEG; ++sg) {
+        q[k][sg] = reinterpret_cast<const uint4*>(P.w + static_cast<size_t>(r) * (IN / 8u) + 256u * sg)[lane];
+        const size_t gi = static_cast<size_t>(r) * GROUPS + 32u * sg + lane / 2u;
+        sc[k][sg] = P.s[gi];
+        bi[k][sg] = P.b[gi];
+      }
+    }
+#pragma unroll
+    for (uint32_t k = 0; k < 4; ++k) {
+      float part = 0.0f;
+#pragma unroll
+      for (uint32_t sg = 0; sg < SEG; ++sg) {
+        float acc = 0.0f;
+        acc = dot8_q4_off(q[k][sg].x, xh[sg] + 0, acc);
+        acc = dot8_q4_off(q[k][sg].y, xh[sg] + 4, acc);
+        acc = dot8_q4_off(q[k][sg].z, xh[sg] + 8, acc);
+        acc = dot8_q4_off(q[k][sg].w, xh[sg] + 12, acc);
+        part = part + __builtin_fmaf(bf16_to_f32(sc[k][sg]), acc - xoff[sg], bf16_to_f32(bi[k][sg]) * xs[sg]);
+      }
+      part = wave_sum_asc(part);
+      if (lane == 0 && r0 + k < a.total_rows) {
+        const GemvPart P = part_of(pidx[k]);
+        const uint32_t r = prow[k];
+        if (P.y_f32) P.y_f32[r] = part;
+        if (P.y_bf16) P.y_bf16[r] = f32_to_bf16(P.residual ? bf16_to_f32(P.residual[r]) + part : part);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// q/k RMSNorm + NeoX RoPE + cache append, one launch
+// ---------------------------------------------------------------------------
+// One wave per head; lane l owns columns 2l, 2l+1 (the RMSNorm lane order of
+// obs_rmsnorm at dim 128). Heads [0, nh): query heads, normed and rotated in
+// place; [nh, nh+nkv): key heads, normed, rotated, written to the key cache at
+// pos; [nh+nkv, nh+2nkv): value heads, written to the transposed value cache.
+// RoPE pairs column i with i + 64, held by lane l ^ 32. Frequencies, cosines
+// and sines follow the oracle's restatement: f = fl32(theta^(-2i/128)) and
+// cos, sin of the fp32 angle fl32(pos * f), each evaluated in double and
+// rounded once; r0 = x0 c - x1 s, r1 = x1 c + x0 s with rounded products.
+__global__ void __launch_bounds__(256) attn_prep_kernel(uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+                                                        const uint16_t* __restrict__ v,
+                                                        const uint16_t* __restrict__ q_norm,
+                                                        const uint16_t* __restrict__ k_norm,
+                                                        uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache_t,
+                                                        uint32_t nh, uint32_t nkv, uint32_t max_len, float eps,
+                                                        float theta, const int32_t* __restrict__ state) {
+  const uint32_t lane = threadIdx.x & 63u, head = blockIdx.x * 4u + (threadIdx.x >> 6);
+  if (head >= nh + 2u * nkv) return;  // wave-uniform
+  const int32_t pos_i = state[0];
+  const uint32_t pos = static_cast<uint32_t>(pos_i);
+  const bool pos_ok = pos_i >= 0 && pos < max_len;
+  const uint32_t c0 = 2u * lane;
+  if (head >= nh + nkv) {  // value head: transposed cache column pos
+    const uint32_t kv = head - nh - nkv;
+    const uint32_t vv = *reinterpret_cast<const uint32_t*>(v + kv * HD + c0);
+    if (pos_ok) {
+      uint16_t* dst = v_cache_t + (static_cast<size_t>(kv) * HD + c0) * max_len + pos;
+      dst[0] = static_cast<uint16_t>(vv & 0xffffu);
+      dst[max_len] = static_cast<uint16_t>(vv >> 16);
+    }
+    return;
+  }
+  const bool is_q = head < nh;
+  const uint32_t hk = is_q ? head : head - nh;
+  const uint16_t* src = is_q ? q + hk * HD : k + hk * HD;
+  const uint16_t* wn = is_q ? q_norm : k_norm;
+  const uint32_t xv = *reinterpret_cast<const uint32_t*>(src + c0);
+  const uint32_t wv = *reinterpret_cast<const uint32_t*>(wn + c0);
+  const float x0 = bf16lo(xv), x1 = bf16hi(xv);
+  float ss = __builtin_fmaf(x0, x0, 0.0f);
+  ss = __builtin_fmaf(x1, x1, ss);
+  const float inv = 1.0f / __builtin_sqrtf(wave_sum_asc(ss) / static_cast<float>(HD) + eps);
+  // the normed values, rounded to bf16 as the stored q/k would be
+  const float n0 = bf16_to_f32(f32_to_bf16((x0 * inv) * bf16lo(wv)));
+  const float n1 = bf16_to_f32(f32_to_bf16((x1 * inv) * bf16hi(wv)));
+  const float p0 = __shfl_xor(n0, 32, 64), p1 = __shfl_xor(n1, 32, 64);  // columns c0 +- 64
+  const bool first = lane < 32u;
+  float r[2];
+#pragma unroll
+  for (uint32_t j = 0; j < 2; ++j) {
+    const uint32_t i = (c0 + j) & 63u;  // pair index
+    const float f = static_cast<float>(pow(static_cast<double>(theta), -2.0 * static_cast<double>(i) / 128.0));
+    const float angle = static_cast<float>(pos) * f;
+    const float c = static_cast<float>(cos(static_cast<double>(angle)));
+    const float s = static_cast<float>(sin(static_cast<double>(angle)));
+    const float own = j ? n1 : n0, other = j ? p1 : p0;
+    if (first) {  // own = x0 (column i), other = x1 (column i + 64)
+      const float a = own * c, b = other * s;
+      r[j] = a - b;
+    } else {      // own = x1, other = x0
+      const float a = own * c, b = other * s;
+      r[j] = a + b;
+    }
+  }
+  const uint32_t out = pack_bf16x2(r[0], r[1]);
+  if (is_q) {
+    *reinterpret_cast<uint32_t*>(q + hk * HD + c0) = out;
+  } else if (pos_ok) {
+    *reinterpret_cast<uint32_t*>(k_cache + (static_cast<size_t>(hk) * max_len + pos) * HD + c0) = out;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// GQA decode attention: split over positions, MFMA for both products
+// ---------------------------------------------------------------------------
+// Workgroup (one wave) = (kv head, split). The G <= 16 query heads of the kv
+// head are the N columns of v_mfma_f32_16x16x32_bf16 (padding heads are zero).
+// Per 32-position block:
+//   S^T [16 positions x 16 heads] = K_block . Q^T, twice (two 16-position
+//   tiles, 4 MFMAs each over 128 dims): A = key rows (one 16-byte load per
+//   lane and step), B = the query slices held in registers. The 16x16 output
+//   layout puts S[h][t] for h = l % 16, t = 4 (l / 16) + i in lane l.
+//   Online softmax per head in base 2: running max m, running sum l, P = 2^(s - m).
+//   O [16 heads x 128] += P . V_block: lane l's eight P values (positions
+//   4 g + i of tile 0 and 16 + 4 g + i of tile 1, g = l / 16) are already the
+//   A operand of one K = 32 MFMA; the B operand pairs them with the same
+//   positions of the transposed value cache (two 8-byte loads per dim tile).
+// The split's (m, l, O) go to the workspace; sdpa_combine_kernel merges them.
+__device__ __forceinline__ float shfl_xor_f(float v, int m) { return __shfl_xor(v, m, 64); }
+
+__global__ void __launch_bounds__(64) sdpa_split_kernel(const uint16_t* __restrict__ q,
+                                                        const uint16_t* __restrict__ k_cache,
+                                                        const uint16_t* __restrict__ v_cache_t,
+                                                        float* __restrict__ ws, uint32_t nh, uint32_t nkv,
+                                                        uint32_t max_len, uint32_t splits, float scale_log2,
+                                                        const int32_t* __restrict__ state) {
+  const uint32_t lane = threadIdx.x, kv = blockIdx.x / splits, sp = blockIdx.x % splits;
+  const uint32_t G = nh / nkv, col = lane & 15u, g = lane >> 4;
+  const int32_t pos = state[0];
+  const uint32_t seq = static_cast<uint32_t>(min(max(pos + 1, 1), static_cast<int32_t>(max_len)));
+  // positions of this split, in 32-position blocks
+  const uint32_t nblk = (seq + 31u) / 32u, per = (nblk + splits - 1u) / splits;
+  const uint32_t b0 = sp * per, b1 = min(nblk, b0 + per);
+  // query slices: B operand of the score MFMA, head col, dims 32 ks + 8 g + j
+  bf16x8_t qb[4];
+  {
+    const uint32_t h = kv * G + col;
+#pragma unroll
+    for (uint32_t ks = 0; ks < 4; ++ks) {
+      u32x4_t v = *reinterpret_cast<const u32x4_t*>(q + static_cast<size_t>(min(h, nh - 1u)) * HD + 32u * ks + 8u * g);
+      if (col >= G) v = u32x4_t{0u, 0u, 0u, 0u};
+      qb[ks] = __builtin_bit_cast(bf16x8_t, v);
+    }
+  }
+  float m_run = -__builtin_huge_valf(), l_run = 0.0f;  // per head col (replicated over g)
+  f32x4_t o[8];
+#pragma unroll
+  for (uint32_t nt = 0; nt < 8; ++nt) o[nt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  const uint16_t* kb = k_cache + static_cast<size_t>(kv) * max_len * HD;
+  const uint16_t* vb = v_cache_t + static_cast<size_t>(kv) * HD * max_len;
+  for (uint32_t blk = b0; blk < b1; ++blk) {
+    const uint32_t t0 = 32u * blk;
+    // scores of the two 16-position tiles
+    f32x4_t s[2];
+#pragma unroll
+    for (uint32_t tt = 0; tt < 2; ++tt) {
+      const uint16_t* kr = kb + static_cast<size_t>(t0 + 16u * tt + col) * HD + 8u * g;
+      f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (uint32_t ks = 0; ks < 4; ++ks) {
+        const bf16x8_t a = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4_t*>(kr + 32u * ks));
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qb[ks], acc, 0, 0, 0);
+      }
+      s[tt] = acc;
+    }
+    // lane holds S[h = col][t0 + 16 tt + 4 g + i]; mask positions >= seq
+    float sv[8];
+#pragma unroll
+    for (uint32_t tt = 0; tt < 2; ++tt)
+#pragma unroll
+      for (uint32_t i = 0; i < 4; ++i) {
+        const uint32_t t = t0 + 16u * tt + 4u * g + i;
+        sv[4 * tt + i] = t < seq ? s[tt][i] * scale_log2 : -__builtin_huge_valf();
+      }
+    float bm = sv[0];
+#pragma unroll
+    for (uint32_t i = 1; i < 8; ++i) bm = fmaxf(bm, sv[i]);
+    bm = fmaxf(bm, shfl_xor_f(bm, 16));
+    bm = fmaxf(bm, shfl_xor_f(bm, 32));
+    const float m_new = fmaxf(m_run, bm);  // finite: every block holds a position < seq
+    const float corr = __builtin_amdgcn_exp2f(m_run - m_new);
+    float p[8], psum = 0.0f;
+#pragma unroll
+    for (uint32_t i = 0; i < 8; ++i) {
+      // P is rounded to bf16 for the MFMA; the running sum adds the rounded values
+      p[i] = bf16_to_f32(f32_to_bf16(__builtin_amdgcn_exp2f(sv[i] - m_new)));
+      psum += p[i];
+    }
+    l_run = l_run * corr + psum;  // per lane; the four g lanes of a head are summed at the end
+    m_run = m_new;
+    // O rows are heads 4 g + i: their corrections live in lanes with col == 4 g + i
+    float oc[4];
+#pragma unroll
+    for (uint32_t i = 0; i < 4; ++i) oc[i] = __shfl(corr, static_cast<int>(4u * g + i), 64);
+    const bf16x8_t pa = __builtin_bit_cast(
+        bf16x8_t, u32x4_t{pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]), pack_bf16x2(p[4], p[5]),
+                          pack_bf16x2(p[6], p[7])});
+    // values of the same positions: dim 16 nt + col, positions t0 + 4 g + i and t0 + 16 + 4 g + i
+    const bool tail = t0 + 32u > seq;  // uniform; masked positions read zero values
+#pragma unroll
+    for (uint32_t nt = 0; nt < 8; ++nt) {
+      const uint16_t* vr = vb + static_cast<size_t>(16u * nt + col) * max_len + t0 + 4u * g;
+      u32x2_t v0 = *reinterpret_cast<const u32x2_t*>(vr);
+      u32x2_t v1 = *reinterpret_cast<const u32x2_t*>(vr + 16);
+      if (tail) {  // a word holds positions t (low half) and t + 1 (high half)
+        auto keep = [&](uint32_t w, uint32_t t) { return t >= seq ? 0u : (t + 1u >= seq ? (w & 0xffffu) : w); };
+        const uint32_t ta = t0 + 4u * g, tb = ta + 16u;
+        v0.x = keep(v0.x, ta);
+        v0.y = keep(v0.y, ta + 2u);
+        v1.x = keep(v1.x, tb);
+        v1.y = keep(v1.y, tb + 2u);
+      }
+      const bf16x8_t vbf = __builtin_bit_cast(bf16x8_t, u32x4_t{v0.x, v0.y, v1.x, v1.y});
+#pragma unroll
+      for (uint32_t i = 0; i < 4; ++i) o[nt][i] *= oc[i];
+      o[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, vbf, o[nt], 0, 0, 0);
+    }
+  }
+  // head col's total: the four g lanes
+  l_run += shfl_xor_f(l_run, 16);
+  l_run += shfl_xor_f(l_run, 32);
+  // workspace [kv][split][head in group][HD + 2]: O (unnormalised), m, l
+  float* base = ws + (static_cast<size_t>(kv) * splits + sp) * 16u * (HD + 2u);
+  if (lane < 16u && col < G) {
+    base[col * (HD + 2u) + HD] = m_run;
+    base[col * (HD + 2u) + HD + 1u] = l_run;
+  }
+#pragma unroll
+  for (uint32_t nt = 0; nt < 8; ++nt)
+#pragma unroll
+    for (uint32_t i = 0; i < 4; ++i) {
+      const uint32_t h = 4u * g + i;
+      if (h < G) base[h * (HD + 2u) + 16u * nt + col] = o[nt][i];
+    }
+}
+
+// out[h] = sum_s O_s 2^(m_s - M) / sum_s l_s 2^(m_s - M), M = max_s m_s; bf16.
+__global__ void __launch_bounds__(128) sdpa_combine_kernel(const float* __restrict__ ws, uint16_t* __restrict__ out,
+                                                           uint32_t nh, uint32_t nkv, uint32_t splits) {
+  const uint32_t h = blockIdx.x, d = threadIdx.x, G = nh / nkv, kv = h / G, hh = h % G;
+  const float* base = ws + static_cast<size_t>(kv) * splits * 16u * (HD + 2u) + hh * (HD + 2u);
+  float M = -__builtin_huge_valf();
+  for (uint32_t s = 0; s < splits; ++s) M = fmaxf(M, base[static_cast<size_t>(s) * 16u * (HD + 2u) + HD]);
+  float num = 0.0f, den = 0.0f;
+  for (uint32_t s = 0; s < splits; ++s) {
+    const float* p = base + static_cast<size_t>(s) * 16u * (HD + 2u);
+    const float ms = p[HD];
+    const float f = ms == -__builtin_huge_valf() ? 0.0f : __builtin_amdgcn_exp2f(ms - M);  // empty split: no weight
+    num = __builtin_fmaf(p[d], f, num);
+    den = __builtin_fmaf(p[HD + 1u], f, den);
+  }
+  out[static_cast<size_t>(h) * HD + d] = f32_to_bf16(num / den);
+}
+
+// ---------------------------------------------------------------------------
+// token step ends: embedding row of the state's token, greedy argmax
+// ---------------------------------------------------------------------------
+// out = bf16(q * s + b) of row state[1] (forward.rs:445-462), one word per thread.
+__global__ void __launch_bounds__(256) embed_q4_kernel(const uint32_t* __restrict__ w, const uint16_t* __restrict__ s,
+                                                       const uint16_t* __restrict__ b, uint32_t hidden, uint32_t group,
+                                                       uint32_t vocab, const int32_t* __restrict__ state,
+                                                       uint16_t* __restrict__ out) {
+  const uint32_t wi = blockIdx.x * 256u + threadIdx.x;
+  if (wi >= hidden / 8u) return;
+  const uint32_t tok = min(static_cast<uint32_t>(max(state[1], 0)), vocab - 1u);
+  const uint32_t word = w[static_cast<size_t>(tok) * (hidden / 8u) + wi];
+  const size_t gi = static_cast<size_t>(tok) * (hidden / group) + (8u * wi) / group;
+  const float sc = bf16_to_f32(s[gi]), bi = bf16_to_f32(b[gi]);
+  uint32_t o[4];
+#pragma unroll
+  for (uint32_t j = 0; j < 4; ++j)
+    o[j] = pack_bf16x2(__builtin_fmaf(static_cast<float>((word >> (8 * j)) & 0xfu), sc, bi),
+                       __builtin_fmaf(static_cast<float>((word >> (8 * j + 4)) & 0xfu), sc, bi));
+  *reinterpret_cast<uint4*>(out + 8u * wi) = make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+// Greedy argmax (forward.rs:563-566): the first index of the maximum, NaN never
+// wins, 0 when nothing exceeds -inf. Keys order (value, -index): a 64-bit key
+// (orderable value bits << 32 | ~index) whose maximum is the answer.
+__device__ __forceinline__ unsigned long long argmax_key(float v, uint32_t i) {
+  const uint32_t u = __float_as_uint(v);
+  const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);  // monotone in v
+  const bool valid = !(v != v) && v > -__builtin_huge_valf();
+  return valid ? (static_cast<unsigned long long>(ord) << 32) | static_cast<uint32_t>(~i) : 0ull;
+}
+__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long k) {
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) {
+    const unsigned long long o = __shfl_xor(k, m, 64);
+    k = o > k ? o : k;
+  }
+  return k;
+}
+__global__ void __launch_bounds__(256) argmax_partial_kernel(const float* __restrict__ x, uint32_t n,
+                                                             unsigned long long* __restrict__ part) {
+  __shared__ unsigned long long s_w[4];
+  const uint32_t per = (n + gridDim.x - 1u) / gridDim.x, a0 = blockIdx.x * per, a1 = min(n, a0 + per);
+  unsigned long long best = 0ull;
+  for (uint32_t i = a0 + threadIdx.x; i < a1; i += 256u) {
+    const unsigned long long k = argmax_key(x[i], i);
+    best = k > best ? k : best;
+  }
+  best = wave_max_u64(best);
+  if ((threadIdx.x & 63u) == 0) s_w[threadIdx.x >> 6] = best;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned long long r = s_w[0];
+    for (int w = 1; w < 4; ++w) r = s_w[w] > r ? s_w[w] : r;
+    part[blockIdx.x] = r;
+  }
+}
+__global__ void __launch_bounds__(256) argmax_final_kernel(const unsigned long long* __restrict__ part, uint32_t nparts,
+                                                           int32_t* __restrict__ state) {
+  __shared__ unsigned long long s_w[4];
+  unsigned long long best = 0ull;
+  for (uint32_t i = threadIdx.x; i < nparts; i += 256u) best = part[i] > best ? part[i] : best;
+  best = wave_max_u64(best);
+  if ((threadIdx.x & 63u) == 0) s_w[threadIdx.x >> 6] = best;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned long long r = s_w[0];
+    for (int w = 1; w < 4; ++w) r = s_w[w] > r ? s_w[w] : r;
+    state[1] = r ? static_cast<int32_t>(~static_cast<uint32_t>(r & 0xffffffffu)) : 0;
+    state[0] = state[0] + 1;
+  }
+}
+
+constexpr uint32_t ARGMAX_PARTS = 256;
+
+uint32_t sdpa_splits(uint32_t max_len) {
+  const uint32_t blocks = max_len / 32u;
+  return blocks < 64u ? blocks : 64u;
+}
+
+}  // namespace
+
+extern "C" {
+
+int obs_q4_gemv(obs_ctx* ctx, const uint16_t* x, uint32_t in, uint32_t group, const obs_gemv_part* parts,
+                uint32_t n_parts) {
+  if (!ctx) return OBS_E_INVALID;
+  if (!x || !parts || n_parts == 0 || n_parts > 3) return obs::set_error(ctx, OBS_E_INVALID, "obs_q4_gemv: null x/parts or n_parts not in 1..3");
+  if (group != 64 || (in != 2048 && in != 4096))
+    return obs::set_error(ctx, OBS_E_SHAPE, "obs_q4_gemv: in must be 2048 or 4096 and group 64 (got %u, %u)", in, group);
+  if (!obs::aligned(x, 16)) return obs::set_error(ctx, OBS_E_ALIGN, "obs_q4_gemv: x must be 16-byte aligned");
+  GemvArgs a{};
+  a.n_parts = n_parts;
+  a.in = in;
+  uint64_t total = 0;
+  for (uint32_t i = 0; i < n_parts; ++i) {
+    const obs_gemv_part& p = parts[i];
+    if (!p.w || !p.scales || !p.biases || (!p.y_f32 && !p.y_bf16))
+      return obs::set_error(ctx, OBS_E_INVALID, "obs_q4_gemv: part %u has a null pointer", i);
+    if (p.residual && !p.y_bf16)
+      return obs::set_error(ctx, OBS_E_INVALID, "obs_q4_gemv: part %u: a residual needs the bf16 output", i);
+    if (!obs::aligned(p.w, 16)) return obs::set_error(ctx, OBS_E_ALIGN, "obs_q4_gemv: part %u weights must be 16-byte aligned", i);
+    a.p[i] = GemvPart{p.w, p.scales, p.biases, p.y_f32, p.y_bf16, p.residual, p.rows};
+    total += p.rows;
+  }
+  if (total == 0) return OBS_OK;
+  if (total > 0x7fffffffull) return obs::set_error(ctx, OBS_E_SHAPE, "obs_q4_gemv: too many rows");
+  a.total_rows = static_cast<uint32_t>(total);
+  // four rows per wave in flight; enough workgroups to cover the rows once, at most 4 per CU
+  const uint32_t waves = (a.total_rows + 3u) / 4u;
+  const uint32_t grid = min((waves + 3u) / 4u, static_cast<uint32_t>(ctx->num_cus) * 4u);
+  if (in == 2048)
+    OBS_LAUNCH(ctx, "q4_gemv", q4_gemv_kernel<1><<<grid, 256, 0, ctx->stream>>>(x, a));
+  else
+    OBS_LAUNCH(ctx, "q4_gemv", q4_gemv_kernel<2><<<grid, 256, 0, ctx->stream>>>(x, a));
+  return OBS_OK;
+}
+
+int obs_attn_prep(obs_ctx* ctx, uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* q_norm,
+                  const uint16_t* k_norm, uint16_t* k_cache, uint16_t* v_cache_t, uint32_t n_heads, uint32_t n_kv,
+                  uint32_t head_dim, uint32_t max_len, float eps, float theta, const int32_t* state) {
+  if (!ctx) return OBS_E_INVALID;
+  if (!q || !k || !v || !q_norm || !k_norm || !k_cache || !v_cache_t || !state)
+    return obs::set_error(ctx, OBS_E_INVALID, "obs_attn_prep: null pointer");
+  if (head_dim != HD || n_heads == 0 || n_kv == 0 || n_heads % n_kv != 0 || n_heads / n_kv > 16 || max_len == 0 ||
+      max_len % 32u != 0)
+    return obs::set_error(ctx, OBS_E_SHAPE,
+                          "obs_attn_prep: head_dim must be 128, n_heads a multiple of n_kv with at most 16 per kv "
+                          "head, max_len a multiple of 32 (got %u, %u, %u, %u)", head_dim, n_heads, n_kv, max_len);
+  if (!obs::aligned(q, 4) || !obs::aligned(k, 4) || !obs::aligned(v, 4) || !obs::aligned(k_cache, 4))
+    return obs::set_error(ctx, OBS_E_ALIGN, "obs_attn_prep: q, k, v and the key cache must be 4-byte aligned");
+  const uint32_t heads = n_heads + 2u * n_kv;
+  OBS_LAUNCH(ctx, "attn_prep", attn_prep_kernel<<<(heads + 3u) / 4u, 256, 0, ctx->stream>>>(
+                                   q, k, v, q_norm, k_norm, k_cache, v_cache_t, n_heads, n_kv, max_len, eps, theta, state));
+  return OBS_OK;
+}
+
+size_t obs_sdpa_workspace(uint32_t n_heads, uint32_t n_kv, uint32_t head_dim, uint32_t max_len) {
+  if (head_dim != HD || n_kv == 0 || n_heads % n_kv != 0 || max_len < 32u) return 0;
+  return sizeof(float) * static_cast<size_t>(n_kv) * sdpa_splits(max_len) * 16u * (HD + 2u);
+}
+
+int obs_sdpa_decode(obs_ctx* ctx, const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache_t, uint16_t* out,
+                    uint32_t n_heads, uint32_t n_kv, uint32_t head_dim, uint32_t max_len, const int32_t* state,
+                    void* ws, size_t ws_bytes) {
+  if (!ctx) return OBS_E_INVALID;
+  if (!q || !k_cache || !v_cache_t || !out || !state || !ws)
+    return obs::set_error(ctx, OBS_E_INVALID, "obs_sdpa_decode: null pointer");
+  if (head_dim != HD || n_heads == 0 || n_kv == 0 || n_heads % n_kv != 0 || n_heads / n_kv > 16 || max_len == 0 ||
+      max_len % 32u != 0)
+    return obs::set_error(ctx, OBS_E_SHAPE,
+                          "obs_sdpa_decode: head_dim must be 128, n_heads a multiple of n_kv with at most 16 per kv "
+                          "head, max_len a multiple of 32 (got %u, %u, %u, %u)", head_dim, n_heads, n_kv, max_len);
+  const size_t need = obs_sdpa_workspace(n_heads, n_kv, head_dim, max_len);
+  if (ws_bytes < need)
+    return obs::set_error(ctx, OBS_E_NOMEM, "obs_sdpa_decode: workspace %zu bytes < %zu needed", ws_bytes, need);
+  if (!obs::aligned(q, 16) || !obs::aligned(k_cache, 16) || !obs::aligned(v_cache_t, 16) || !obs::aligned(ws, 16))
+    return obs::set_error(ctx, OBS_E_ALIGN, "obs_sdpa_decode: q, caches and workspace must be 16-byte aligned");
+  const uint32_t splits = sdpa_splits(max_len);
+  const float scale_log2 = 1.4426950408889634f / __builtin_sqrtf(static_cast<float>(HD));
+  float* w = static_cast<float*>(ws);
+  OBS_LAUNCH(ctx, "sdpa_split", sdpa_split_kernel<<<n_kv * splits, 64, 0, ctx->stream>>>(
+                                    q, k_cache, v_cache_t, w, n_heads, n_kv, max_len, splits, scale_log2, state));
+  OBS_LAUNCH(ctx, "sdpa_combine", sdpa_combine_kernel<<<n_heads, HD, 0, ctx->stream>>>(w, out, n_heads, n_kv, splits));
+  return OBS_OK;
+}
+
+int obs_embed_q4(obs_ctx* ctx, const uint32_t* w, const uint16_t* scales, const uint16_t* biases, uint32_t hidden,
+                 uint32_t group, uint32_t vocab, const int32_t* state, uint16_t* out) {
+  if (!ctx) return OBS_E_INVALID;
+  if (!w || !scales || !biases || !state || !out) return obs::set_error(ctx, OBS_E_INVALID, "obs_embed_q4: null pointer");
+  if (hidden == 0 || vocab == 0 || group == 0 || group % 8u != 0 || hidden % group != 0)
+    return obs::set_error(ctx, OBS_E_SHAPE, "obs_embed_q4: hidden must be a multiple of group, group of 8");
+  if (!obs::aligned(out, 16)) return obs::set_error(ctx, OBS_E_ALIGN, "obs_embed_q4: out must be 16-byte aligned");
+  OBS_LAUNCH(ctx, "embed_q4", embed_q4_kernel<<<(hidden / 8u + 255u) / 256u, 256, 0, ctx->stream>>>(
+                                  w, scales, biases, hidden, group, vocab, state, out));
+  return OBS_OK;
+}
+
+size_t obs_argmax_workspace(void) { return sizeof(unsigned long long) * ARGMAX_PARTS; }
+
+int obs_argmax(obs_ctx* ctx, const float* x, uint32_t n, int32_t* state, void* ws, size_t ws_bytes) {
+  if (!ctx) return OBS_E_INVALID;
+  if (!x || !state || !ws) return obs::set_error(ctx, OBS_E_INVALID, "obs_argmax: null pointer");
+  if (ws_bytes < obs_argmax_workspace())
+    return obs::set_error(ctx, OBS_E_NOMEM, "obs_argmax: workspace %zu bytes < %zu needed", ws_bytes, obs_argmax_workspace());
+  if (!obs::aligned(ws, 8)) return obs::set_error(ctx, OBS_E_ALIGN, "obs_argmax: workspace must be 8-byte aligned");
+  auto* part = static_cast<unsigned long long*>(ws);
+  OBS_LAUNCH(ctx, "argmax_partial", argmax_partial_kernel<<<ARGMAX_PARTS, 256, 0, ctx->stream>>>(x, n, part));
+  OBS_LAUNCH(ctx, "argmax_final", argmax_final_kernel<<<1, 256, 0, ctx->stream>>>(part, ARGMAX_PARTS, state));
+  return OBS_OK;
+}
+
+}  // extern "C"

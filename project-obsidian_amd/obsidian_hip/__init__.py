@@ -56,6 +56,8 @@ EXPORTS = (
     "obs_profile_accumulate", "obs_profile_count", "obs_profile_stat", "obs_profile_clear",
     "obs_ckpt_open", "obs_ckpt_close", "obs_ckpt_error", "obs_ckpt_config", "obs_ckpt_tensor_info",
     "obs_ckpt_read", "obs_moe_layer_bytes", "obs_ckpt_load_moe_layer", "obs_ckpt_load_tensor",
+    "obs_q4_gemv", "obs_attn_prep", "obs_sdpa_workspace", "obs_sdpa_decode", "obs_embed_q4",
+    "obs_argmax_workspace", "obs_argmax",
 )
 
 
@@ -75,6 +77,11 @@ class ObsMoeLayer(C.Structure):
     _fields_ = [(n, C.c_void_p) for n in (
         "gate_w", "gate_s", "gate_b", "up_w", "up_s", "up_b", "down_w", "down_s", "down_b",
         "router_w", "router_s", "router_b", "norm_w")]
+
+
+class ObsGemvPart(C.Structure):
+    _fields_ = [("w", C.c_void_p), ("scales", C.c_void_p), ("biases", C.c_void_p), ("y_f32", C.c_void_p),
+                ("y_bf16", C.c_void_p), ("residual", C.c_void_p), ("rows", C.c_uint32)]
 
 
 class ObsTensorInfo(C.Structure):
@@ -153,6 +160,13 @@ def lib() -> C.CDLL:
         "obs_moe_layer_bytes": (sz, [C.POINTER(ObsMoeConfig)]),
         "obs_ckpt_load_moe_layer": (i32, [vp, vp, u32, C.POINTER(ObsMoeConfig), vp, sz, C.POINTER(ObsMoeLayer)]),
         "obs_ckpt_load_tensor": (i32, [vp, vp, C.c_char_p, vp, sz]),
+        "obs_q4_gemv": (i32, [vp, vp, u32, u32, C.POINTER(ObsGemvPart), u32]),
+        "obs_attn_prep": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, u32, u32, u32, u32, f32, f32, vp]),
+        "obs_sdpa_workspace": (sz, [u32, u32, u32, u32]),
+        "obs_sdpa_decode": (i32, [vp, vp, vp, vp, vp, u32, u32, u32, u32, vp, vp, sz]),
+        "obs_embed_q4": (i32, [vp, vp, vp, vp, u32, u32, u32, vp, vp]),
+        "obs_argmax_workspace": (sz, []),
+        "obs_argmax": (i32, [vp, vp, u32, vp, vp, sz]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -356,6 +370,38 @@ class ObsidianExecutor:
         c, l = cfg.to_c(), layer.to_c()
         self._check(lib().obs_moe_decode(self.ctx, C.byref(c), C.byref(l), _ptr(x), _ptr(residual), _ptr(y),
                                          _ptr(ids_out), _ptr(w_out)))
+
+    # -- the rest of a decode step (forward.rs:398-419, :445-462, :552-567) --
+    def q4_gemv(self, x, in_f: int, parts: Sequence[Tuple], group: int = 64) -> None:
+        """parts: (w, s, b, rows, y_f32, y_bf16, residual) tuples, 1 to 3."""
+        arr = (ObsGemvPart * len(parts))()
+        for i, (w, s_, b, rows, yf, yb, res) in enumerate(parts):
+            arr[i] = ObsGemvPart(_ptr(w), _ptr(s_), _ptr(b), _ptr(yf), _ptr(yb), _ptr(res), rows)
+        self._check(lib().obs_q4_gemv(self.ctx, _ptr(x), in_f, group, arr, len(parts)))
+
+    def attn_prep(self, q, k, v, q_norm, k_norm, k_cache, v_cache_t, n_heads: int, n_kv: int, head_dim: int,
+                  max_len: int, eps: float, theta: float, state) -> None:
+        self._check(lib().obs_attn_prep(self.ctx, _ptr(q), _ptr(k), _ptr(v), _ptr(q_norm), _ptr(k_norm),
+                                        _ptr(k_cache), _ptr(v_cache_t), n_heads, n_kv, head_dim, max_len, eps,
+                                        theta, _ptr(state)))
+
+    @staticmethod
+    def sdpa_workspace(n_heads: int, n_kv: int, head_dim: int, max_len: int) -> int:
+        return lib().obs_sdpa_workspace(n_heads, n_kv, head_dim, max_len)
+
+    def sdpa_decode(self, q, k_cache, v_cache_t, out, n_heads: int, n_kv: int, head_dim: int, max_len: int, state,
+                    ws, ws_bytes: Optional[int] = None) -> None:
+        ws_bytes = ws.nbytes if ws_bytes is None else ws_bytes
+        self._check(lib().obs_sdpa_decode(self.ctx, _ptr(q), _ptr(k_cache), _ptr(v_cache_t), _ptr(out), n_heads,
+                                          n_kv, head_dim, max_len, _ptr(state), _ptr(ws), ws_bytes))
+
+    def embed_q4(self, w, s, b, hidden: int, vocab: int, state, out, group: int = 64) -> None:
+        self._check(lib().obs_embed_q4(self.ctx, _ptr(w), _ptr(s), _ptr(b), hidden, group, vocab, _ptr(state),
+                                       _ptr(out)))
+
+    def argmax(self, x, n: int, state, ws, ws_bytes: Optional[int] = None) -> None:
+        ws_bytes = ws.nbytes if ws_bytes is None else ws_bytes
+        self._check(lib().obs_argmax(self.ctx, _ptr(x), n, _ptr(state), _ptr(ws), ws_bytes))
 
     def moe_prefill_workspace(self, cfg: "MoeConfig", T: int) -> int:
         c = cfg.to_c()

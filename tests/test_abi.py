@@ -58,7 +58,8 @@ def test_null_context_is_rejected_before_any_device_work():
     L = oh.lib()
     host_only = {"obs_create", "obs_create_error", "obs_destroy", "obs_last_error", "obs_get_stream",
                  "obs_graph_destroy", "obs_moe_prefill_workspace", "obs_profile_count",
-                 "obs_ckpt_close", "obs_ckpt_error", "obs_moe_layer_bytes"}
+                 "obs_ckpt_close", "obs_ckpt_error", "obs_moe_layer_bytes", "obs_sdpa_workspace",
+                 "obs_argmax_workspace"}
     for name in declared_functions():
         if name in host_only:
             continue
@@ -77,6 +78,9 @@ def test_null_context_is_rejected_before_any_device_work():
     assert L.obs_ckpt_error(None) == b"obs_ckpt_open: null argument"
     L.obs_ckpt_close(None)
     assert L.obs_moe_layer_bytes(None) == 0
+    assert L.obs_argmax_workspace() == 256 * 8
+    assert L.obs_sdpa_workspace(32, 4, 128, 4096) == 4 * 64 * 16 * 130 * 4  # fp32 (m, l, O) per split and head slot
+    assert L.obs_sdpa_workspace(32, 4, 64, 4096) == 0 and L.obs_sdpa_workspace(32, 3, 128, 4096) == 0
 
 
 def test_prefill_workspace_is_host_arithmetic():
