@@ -278,13 +278,12 @@ def _proj(P: Dict[str, np.ndarray], name: str, x_bf16, in_f: int, out_f: int) ->
     return _bf16(y)
 
 
-def decoder_layer(P: Dict[str, np.ndarray], moe: "Layer", x_bf16, k_cache, v_cache, pos: int, cfg: Dict):
-    """One decoder layer for one token at position `pos` (forward.rs:398-443):
-    attention half with bf16 activations (projections in fp64 on the exact
-    weights, rounded to bf16; per-head q/k RMSNorm; NeoX RoPE; the caches get k
-    and v at `pos`; attention in fp64 rounded to bf16; x1 = bf16(x + o)), then
-    the MoE half x1 + sum_r w_r expert_r(rmsnorm(x1)) in fp64, rounded to bf16.
-    k_cache, v_cache (bf16 [n_kv, max_len, head_dim]) are updated in place."""
+def attention_half(P: Dict[str, np.ndarray], x_bf16, k_cache, v_cache, pos: int, cfg: Dict) -> np.ndarray:
+    """x1 = bf16(x + o) of one decoder layer for one token at `pos`
+    (forward.rs:403-418): projections in fp64 on the exact weights rounded to
+    bf16, per-head q/k RMSNorm, NeoX RoPE, k and v into the caches (bf16
+    [n_kv, max_len, head_dim], updated in place), attention in fp64 rounded to
+    bf16, o projection in fp64 rounded to bf16."""
     H, nh, nkv, hd = cfg["hidden"], cfg["n_heads"], cfg["n_kv"], cfg["head_dim"]
     eps, theta = cfg["eps"], cfg["theta"]
     x = _c(x_bf16, np.uint16)
@@ -298,11 +297,26 @@ def decoder_layer(P: Dict[str, np.ndarray], moe: "Layer", x_bf16, k_cache, v_cac
     v_cache[:, pos, :] = v
     attn = _bf16(sdpa_decode(q, k_cache, v_cache, pos + 1, hd ** -0.5)).reshape(-1)
     o = _proj(P, "o", attn, nh * hd, H)
-    x1 = _bf16(_f32(x) + _f32(o))
-    x1n = rmsnorm(x1, P["post_norm"], eps)
-    _, ids, w = router(moe, x1n, cfg["top_k"], cfg["norm_topk"])
+    return _bf16(_f32(x) + _f32(o))
+
+
+def moe_half(P: Dict[str, np.ndarray], moe: "Layer", x1_bf16, cfg: Dict, ids=None, w=None):
+    """x1 + sum_r w_r expert_r(rmsnorm(x1)) in fp64, rounded to bf16
+    (forward.rs:419-441); routing from the oracle router unless given.
+    Returns (x_out bf16, ids, w)."""
+    x1 = _c(x1_bf16, np.uint16)
+    x1n = rmsnorm(x1, P["post_norm"], cfg["eps"])
+    if ids is None:
+        _, ids, w = router(moe, x1n, cfg["top_k"], cfg["norm_topk"])
     y, _, _ = moe_decode(moe, x1n, cfg["top_k"], cfg["norm_topk"], ids=ids, w=w)
-    return _bf16(y[0] + _f32(x1))
+    return _bf16(y[0] + _f32(x1)), ids, w
+
+
+def decoder_layer(P: Dict[str, np.ndarray], moe: "Layer", x_bf16, k_cache, v_cache, pos: int, cfg: Dict):
+    """One decoder layer for one token at `pos` (forward.rs:398-443): the
+    attention half, then the MoE half. The caches are updated in place."""
+    x1 = attention_half(P, x_bf16, k_cache, v_cache, pos, cfg)
+    return moe_half(P, moe, x1, cfg)[0]
 
 
 def _f32(b) -> np.ndarray:

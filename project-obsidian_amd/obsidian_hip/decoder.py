@@ -1,0 +1,189 @@
+"""The decoder around the MoE block: the host mirror of the reference's Model
+(src/forward.rs:30-53, :398-443, :445-462, :552-567) over the C ABI.
+
+A decode step is embed -> for each layer (input RMSNorm, q/k/v projections in
+one mat-vec launch, q/k norm + RoPE + cache append, GQA attention, o
+projection with the residual add, then the fused MoE block with its
+post-attention norm and residual) -> final RMSNorm -> lm_head -> argmax. The
+position and token live in a device array, so the whole step is captured once
+as a HIP graph and replayed for every token (the reference commits one Metal
+command buffer per dispatch instead, forward.rs:289-301).
+
+Every kernel runs through libobsidian_hip; there is no CPU path.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Dict, List, Optional
+
+import numpy as np
+
+from . import DeviceBuffer, MoeConfig, MoeLayer, ObsidianExecutor, lib
+
+
+@dataclass
+class DecoderConfig:
+    """Qwen3MoeConfig (src/model.rs:7-23) plus the cache length."""
+    n_layers: int = 48
+    hidden: int = 2048
+    n_heads: int = 32
+    n_kv: int = 4
+    head_dim: int = 128
+    n_exp: int = 128
+    top_k: int = 8
+    inter: int = 768
+    vocab: int = 151936
+    rms_eps: float = 1e-6
+    rope_theta: float = 1e7
+    norm_topk: bool = True
+    group: int = 64
+    max_len: int = 4096  # KV cache positions (forward.rs:60-63 defaults to 16384)
+
+    def moe(self) -> MoeConfig:
+        return MoeConfig(self.n_exp, self.top_k, self.hidden, self.inter, self.group, self.norm_topk, self.rms_eps)
+
+
+# Per-layer tensors (names of the checkpoint's model.layers.{l}.* entries):
+#   in_norm (input_layernorm.weight), q_w/q_s/q_b, k_*, v_*, o_* (self_attn.*_proj),
+#   q_norm, k_norm (self_attn.{q,k}_norm.weight), post_norm (post_attention_layernorm.weight)
+#   and the MoE tables (PROJ_KEYS of MoeLayer).
+# Global tensors: embed_w/s/b (model.embed_tokens), final_norm (model.norm), lm_w/s/b (lm_head).
+ATTN_KEYS = ("in_norm", "q_w", "q_s", "q_b", "k_w", "k_s", "k_b", "v_w", "v_s", "v_b", "o_w", "o_s", "o_b",
+             "q_norm", "k_norm", "post_norm")
+GLOBAL_KEYS = ("embed_w", "embed_s", "embed_b", "final_norm", "lm_w", "lm_s", "lm_b")
+
+
+class Model:
+    """forward.rs:30-53. `layers` holds per-layer dicts of device pointers (or
+    DeviceBuffers) with ATTN_KEYS plus a MoeLayer under "moe"; `glob` holds
+    GLOBAL_KEYS. The KV caches, activations and workspaces are allocated here
+    once (forward.rs:56-104 allocates the pools once too)."""
+
+    def __init__(self, exe: ObsidianExecutor, cfg: DecoderConfig, layers: List[Dict], glob: Dict):
+        self.exe, self.cfg, self.layers, self.glob = exe, cfg, layers, glob
+        c = cfg
+        if c.n_heads * c.head_dim not in (2048, 4096) or c.hidden not in (2048, 4096):
+            raise ValueError("the fused mat-vec needs hidden and n_heads * head_dim in {2048, 4096}")
+        self.caches = [(exe.zeros((c.n_kv, c.max_len, c.head_dim), np.uint16),
+                        exe.zeros((c.n_kv, c.head_dim, c.max_len), np.uint16)) for _ in range(c.n_layers)]
+        self.state = exe.zeros(2, np.int32)              # {pos, tok}
+        self.x = exe.alloc(c.hidden, np.uint16)          # residual stream (layer input and output)
+        self.x1 = exe.alloc(c.hidden, np.uint16)         # after attention
+        self.xn = exe.alloc(c.hidden, np.uint16)
+        self.q = exe.alloc(c.n_heads * c.head_dim, np.uint16)
+        self.k = exe.alloc(c.n_kv * c.head_dim, np.uint16)
+        self.v = exe.alloc(c.n_kv * c.head_dim, np.uint16)
+        self.attn = exe.alloc(c.n_heads * c.head_dim, np.uint16)
+        self.logits = exe.alloc(c.vocab, np.float32)
+        self.sdpa_ws = exe.alloc(exe.sdpa_workspace(c.n_heads, c.n_kv, c.head_dim, c.max_len), np.uint8)
+        self.argmax_ws = exe.alloc(lib().obs_argmax_workspace(), np.uint8)
+        self.moe_cfg = c.moe()
+        self.graph: Optional[int] = None
+
+    # -- the pieces of forward_layer (forward.rs:398-443) ------------------
+    def forward_layer(self, il: int, ids_out=None, w_out=None) -> None:
+        """self.x <- layer il of self.x at the state's position (ids_out, w_out:
+        optional device buffers for the layer's routing)."""
+        c, e, L = self.cfg, self.exe, self.layers[il]
+        kc, vc = self.caches[il]
+        e.rmsnorm_raw(self.x, L["in_norm"], self.xn, 1, c.hidden, c.rms_eps)
+        qd, kvd = c.n_heads * c.head_dim, c.n_kv * c.head_dim
+        e.q4_gemv(self.xn, c.hidden, [(L["q_w"], L["q_s"], L["q_b"], qd, None, self.q, None),
+                                      (L["k_w"], L["k_s"], L["k_b"], kvd, None, self.k, None),
+                                      (L["v_w"], L["v_s"], L["v_b"], kvd, None, self.v, None)])
+        e.attn_prep(self.q, self.k, self.v, L["q_norm"], L["k_norm"], kc, vc, c.n_heads, c.n_kv, c.head_dim,
+                    c.max_len, c.rms_eps, c.rope_theta, self.state)
+        e.sdpa_decode(self.q, kc, vc, self.attn, c.n_heads, c.n_kv, c.head_dim, c.max_len, self.state, self.sdpa_ws)
+        e.q4_gemv(self.attn, qd, [(L["o_w"], L["o_s"], L["o_b"], c.hidden, None, self.x1, self.x)])
+        e.moe_decode(self.moe_cfg, L["moe"], self.x1, self.x, residual=self.x1, ids_out=ids_out, w_out=w_out)
+
+    def embed(self) -> None:
+        """forward.rs:445-462: self.x <- bf16 row state[1] of the 4-bit embedding table."""
+        g, c = self.glob, self.cfg
+        self.exe.embed_q4(g["embed_w"], g["embed_s"], g["embed_b"], c.hidden, c.vocab, self.state, self.x, c.group)
+
+    def head(self) -> None:
+        """forward.rs:559-566: final norm, lm_head logits (fp32), greedy token into
+        the state, position advanced."""
+        g, c, e = self.glob, self.cfg, self.exe
+        e.rmsnorm_raw(self.x, g["final_norm"], self.xn, 1, c.hidden, c.rms_eps)
+        e.q4_gemv(self.xn, c.hidden, [(g["lm_w"], g["lm_s"], g["lm_b"], c.vocab, self.logits, None, None)])
+        e.argmax(self.logits, c.vocab, self.state, self.argmax_ws)
+
+    def step(self) -> None:
+        """run_one_token (forward.rs:552-567) without the host read: enqueue one
+        whole decode step."""
+        self.embed()
+        for il in range(self.cfg.n_layers):
+            self.forward_layer(il)
+        self.head()
+
+    # -- state and graph ---------------------------------------------------
+    def set_state(self, pos: int, tok: int) -> None:
+        if not 0 <= pos < self.cfg.max_len:
+            raise ValueError(f"position {pos} outside the cache (max_len {self.cfg.max_len})")
+        self.state.upload(np.array([pos, tok], np.int32))
+
+    def read_state(self):
+        pos, tok = self.state.download()
+        return int(pos), int(tok)
+
+    def capture(self) -> int:
+        """Record one step as a graph. One eager step runs first (and its state
+        is restored) so that every workspace exists before the capture; it
+        writes the cache entries at the current position, which the next step
+        at that position writes again with the same values."""
+        if self.graph is None:
+            saved = self.state.download()
+            self.step()
+            self.state.upload(saved)
+            self.exe.capture_begin()
+            try:
+                self.step()
+            finally:
+                self.graph = self.exe.capture_end()
+        return self.graph
+
+    def replay(self, n: int = 1) -> None:
+        g = self.capture()
+        for _ in range(n):
+            self.exe.graph_launch(g)
+
+    def run_one_token(self, tok: int, pos: int) -> int:
+        """forward.rs:552-567: next greedy token after `tok` at `pos`."""
+        self.set_state(pos, tok)
+        self.step()
+        return self.read_state()[1]
+
+    def generate(self, tok: int, pos: int, n: int, graph: bool = True) -> List[int]:
+        """n greedy tokens after `tok` at `pos` (one step per token)."""
+        if pos + n > self.cfg.max_len:
+            raise ValueError("generation runs past the cache")
+        self.set_state(pos, tok)
+        out = []
+        for _ in range(n):
+            if graph:
+                self.replay(1)
+            else:
+                self.step()
+            out.append(self.read_state()[1])
+        return out
+
+    def close(self) -> None:
+        if self.graph is not None:
+            ObsidianExecutor.graph_destroy(self.graph)
+            self.graph = None
+
+
+def upload_weights(exe: ObsidianExecutor, layers: List[Dict[str, np.ndarray]], glob: Dict[str, np.ndarray]):
+    """Host arrays -> device buffers in the layout Model expects (layers[i]
+    holds ATTN_KEYS and the MoE PROJ_KEYS)."""
+    dl = []
+    for t in layers:
+        d = {k: exe.upload(t[k]) for k in ATTN_KEYS}
+        moe = {k: t[k] for k in t if k not in ATTN_KEYS}
+        moe["norm_w"] = t["post_norm"]
+        d["moe"] = MoeLayer.upload(exe, moe)
+        dl.append(d)
+    dg = {k: exe.upload(glob[k]) for k in GLOBAL_KEYS}
+    return dl, dg

@@ -173,3 +173,43 @@ def write_checkpoint(model_dir: str, layers: Dict[int, Dict[str, np.ndarray]], c
         os.makedirs(d, exist_ok=True)
         for il, t in split.items():
             save_file(t, os.path.join(d, f"layer_{il}_experts.safetensors"))
+
+
+def centered_quant(rng: np.random.Generator, rows: int, cols: int, group: int = 64,
+                   scale_std: float = 0.02) -> Tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """4-bit matrix whose dequantized values are centred on zero, as MLX
+    quantisation of real weights makes them (bias ~ -7.5 * scale, the group
+    minimum): scales bf16(|N(0, scale_std)|), biases bf16(-7.5 s + N(0, s/8))."""
+    w = rng.integers(0, 2**32, size=(rows, cols // 8), dtype=np.uint64).astype(np.uint32)
+    s = bf16_normal(rng, (rows, cols // group), scale_std, absval=True)
+    sf = bf16_bits_to_f32(s)
+    b = f32_to_bf16_bits(-7.5 * sf + rng.standard_normal(sf.shape).astype(np.float32) * sf / 8)
+    return w, s, b
+
+
+def norm_weight(rng: np.random.Generator, n: int) -> np.ndarray:
+    """RMSNorm weight around 1: bf16(1 + N(0, 0.1))."""
+    return f32_to_bf16_bits(1.0 + 0.1 * rng.standard_normal(n).astype(np.float32))
+
+
+def decoder_weights(seed: int, n_layers: int, hidden: int, n_heads: int, n_kv: int, head_dim: int, n_exp: int,
+                    inter: int, vocab: int, group: int = 64):
+    """Seeded random weights of a Qwen3-MoE decoder (host arrays): per layer the
+    attention tensors (centred 4-bit q/k/v/o, norm weights) and the MoE tables
+    of moe_layer(); globally the embedding, final norm and lm_head."""
+    rng = np.random.default_rng(seed)
+    layers = []
+    qd, kvd = n_heads * head_dim, n_kv * head_dim
+    for il in range(n_layers):
+        t = moe_layer(seed * 1000 + il, n_exp, hidden, inter, group)
+        for name, (r, c) in (("q", (qd, hidden)), ("k", (kvd, hidden)), ("v", (kvd, hidden)), ("o", (hidden, qd))):
+            t[name + "_w"], t[name + "_s"], t[name + "_b"] = centered_quant(rng, r, c, group)
+        t["in_norm"] = norm_weight(rng, hidden)
+        t["post_norm"] = norm_weight(rng, hidden)
+        t["q_norm"] = norm_weight(rng, head_dim)
+        t["k_norm"] = norm_weight(rng, head_dim)
+        layers.append(t)
+    glob = {"final_norm": norm_weight(rng, hidden)}
+    glob["embed_w"], glob["embed_s"], glob["embed_b"] = centered_quant(rng, vocab, hidden, group, 0.05)
+    glob["lm_w"], glob["lm_s"], glob["lm_b"] = centered_quant(rng, vocab, hidden, group)
+    return layers, glob
