@@ -140,6 +140,109 @@ def bench_decode(torch, oh, exe, args):
     return {"ms_step": ms_step, "us_layer": us_layer, "gbs": gbs, "kernels": kernels, "roofline": roof}
 
 
+def gpu_decoder(torch, oh, D, exe, n_layers, max_len, seed):
+    """A Qwen3-30B-A3B-shaped decoder with seeded random
+    weights generated on the GPU: centred 4-bit attention matrices, norm
+    weights around 1, the MoE tables of gpu_table, a 4-bit embedding and
+    lm_head; KV caches filled with random bf16 (the positions before the timed
+    ones stand for an earlier context)."""
+    c = D.DecoderConfig(n_layers=n_layers, max_len=max_len)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed)
+
+    def quant(rows, cols, std=0.02):
+        w = torch.randint(-2**31, 2**31, (rows, cols // 8), dtype=torch.int32, device="cuda", generator=gen)
+        sf = (torch.randn((rows, cols // G), device="cuda", generator=gen) * std).abs()
+        s = sf.to(torch.bfloat16)
+        sf = s.float()
+        b = (-7.5 * sf + torch.randn(sf.shape, device="cuda", generator=gen) * sf / 8).to(torch.bfloat16)
+        return w, s, b
+
+    def norm(n):
+        return (1.0 + 0.1 * torch.randn(n, device="cuda", generator=gen)).to(torch.bfloat16)
+
+    moe = gpu_table(torch, n_layers, seed + 1)
+    keep, layers, caches = [], [], []
+    qd, kvd = c.n_heads * c.head_dim, c.n_kv * c.head_dim
+    for il in range(n_layers):
+        t = {}
+        for name, (r, cc) in (("q", (qd, c.hidden)), ("k", (kvd, c.hidden)), ("v", (kvd, c.hidden)),
+                              ("o", (c.hidden, qd))):
+            t[name + "_w"], t[name + "_s"], t[name + "_b"] = quant(r, cc)
+        t["in_norm"], t["post_norm"] = norm(c.hidden), norm(c.hidden)
+        t["q_norm"], t["k_norm"] = norm(c.head_dim), norm(c.head_dim)
+        ptrs = {k: v.data_ptr() for k, v in t.items()}
+        mp = {k: v.data_ptr() for k, v in moe[il].items()}
+        mp["norm_w"] = ptrs["post_norm"]
+        ptrs["moe"] = oh.MoeLayer(mp)
+        layers.append(ptrs)
+        kc = torch.randn((c.n_kv, max_len, c.head_dim), device="cuda", generator=gen).to(torch.bfloat16)
+        vc = torch.randn((c.n_kv, c.head_dim, max_len), device="cuda", generator=gen).to(torch.bfloat16)
+        caches.append((kc.data_ptr(), vc.data_ptr()))
+        keep += [t, kc, vc]
+    g = {}
+    g["embed_w"], g["embed_s"], g["embed_b"] = quant(c.vocab, c.hidden, 0.05)
+    g["lm_w"], g["lm_s"], g["lm_b"] = quant(c.vocab, c.hidden)
+    g["final_norm"] = norm(c.hidden)
+    keep += [g, moe]
+    torch.cuda.synchronize()
+    model = D.Model(exe, c, layers, {k: v.data_ptr() for k, v in g.items()}, caches=caches)
+    return model, keep
+
+
+def decoder_token_bytes(c, seq):
+    """HBM bytes one decode step reads at attended length seq: attention
+    weights and MoE bytes per layer, the lm_head, the KV cache and the
+    embedding row (the per-token analogue of the MoE layer figure)."""
+    qd, kvd = c.n_heads * c.head_dim, c.n_kv * c.head_dim
+    def q4(rows, cols):
+        return rows * cols // 2 + 2 * 2 * rows * (cols // G)
+    attn = q4(qd + 2 * kvd, c.hidden) + q4(c.hidden, qd)
+    kv = 2 * kvd * 2 * seq
+    return c.n_layers * (attn + LAYER_BYTES + kv) + q4(c.vocab, c.hidden) + q4(1, c.hidden)
+
+
+def bench_decoder(torch, oh, exe, args):
+    """greedy decode steps of the 48-layer decoder around
+    context 4096, one captured graph per step, replayed back to back."""
+    from obsidian_hip import decoder as D
+    ctx = 4096
+    n_pos = args.dec_warmup + args.dec_steps
+    max_len = (ctx + n_pos + 31) // 32 * 32
+    model, keep = gpu_decoder(torch, oh, D, exe, args.layers, max_len, 4321)
+    start = ctx - n_pos // 2
+    model.set_state(start, 1)
+    model.capture()  # one eager step, then the capture
+    model.set_state(start, 1)
+    model.replay(args.dec_warmup)
+    exe.sync()
+    pos0, _ = model.read_state()
+    exe.timer_start()
+    model.replay(args.dec_steps)
+    ms = exe.timer_stop()
+    pos1, tok = model.read_state()
+    ms_tok = ms / args.dec_steps
+    seq_mid = (pos0 + pos1) / 2.0 + 1.0  # mean attended length of the timed steps
+    nbytes = decoder_token_bytes(model.cfg, seq_mid)
+    # kernel breakdown of one eager step (event pairs; the hold kernel lets the host queue it)
+    exe.profile_clear()
+    model.set_state(start, 1)
+    exe.stream_hold(30000)
+    exe.profile_enable(True)
+    model.step()
+    exe.profile_enable(False)
+    exe.profile_accumulate()
+    stats = exe.profile_stats()
+    exe.profile_clear()
+    model.close()
+    del keep
+    torch.cuda.empty_cache()
+    kern = {n: round(1000.0 * t, 1) for n, (t, c) in sorted(stats.items(), key=lambda kv: -kv[1][0])}
+    return {"tokens_per_s": 1000.0 / ms_tok, "ms_per_token": ms_tok, "positions": [pos0, pos1 - 1],
+            "bytes_per_token": int(nbytes), "gbs": nbytes / (ms_tok * 1e-3) / 1e9, "last_token": tok,
+            "step_kernels_us": kern}
+
+
 def measured_traffic(kernel):
     """HBM bytes per launch of `kernel` from the committed counter summary
     (rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE passes, each scaled by the same
@@ -265,6 +368,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-decoder", action="store_true")
+    ap.add_argument("--dec-steps", type=int, default=32)
+    ap.add_argument("--dec-warmup", type=int, default=4)
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain MIB-MiB device copy (counter calibration) and exit")
     args = ap.parse_args()
@@ -282,6 +388,7 @@ def main():
     exe = oh.ObsidianExecutor(0)
     dec = bench_decode(torch, oh, exe, args)
     pre = None if args.no_prefill else bench_prefill(torch, oh, exe, args)
+    dcd = None if args.no_decoder else bench_decoder(torch, oh, exe, args)
     cpu = None
     if not args.no_cpu:
         threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(os.cpu_count() or 1, 16)
@@ -314,6 +421,13 @@ def main():
             "gemm_tflops": None if pre["gemm_tflops"] is None else round(pre["gemm_tflops"], 1),
             "frac_of_bf16_peak": None if pre["gemm_tflops"] is None else round(pre["gemm_tflops"] / BF16_PEAK_TFLOPS, 4),
             "kernels": {n: round(v["avg_us"], 2) for n, v in pre["kernels"].items()}},
+        "decoder": None if dcd is None else {
+            "workload": f"greedy decode, {args.layers}-layer Qwen3-30B-A3B shape, bf16 KV cache, "
+                        f"positions {dcd['positions'][0]}-{dcd['positions'][1]} (context ~4096)",
+            "tokens_per_s": round(dcd["tokens_per_s"], 1), "ms_per_token": round(dcd["ms_per_token"], 4),
+            "bytes_per_token": dcd["bytes_per_token"], "gbs": round(dcd["gbs"], 1),
+            "frac_of_hbm_peak": round(dcd["gbs"] / HBM_PEAK_GBS, 4),
+            "step_kernels_us": dcd["step_kernels_us"]},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))

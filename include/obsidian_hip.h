@@ -273,9 +273,11 @@ typedef struct obs_gemv_part {
 } obs_gemv_part;
 /* y_i = W_i x for 1-3 matrices sharing x (bf16 [in]) in one launch (q, k, v
  * projections; lm_head; o_proj with the residual add of forward.rs:418).
- * in 2048 or 4096, group 64. */
+ * With norm_w (bf16 [in], 16-byte aligned) x is first replaced by
+ * bf16(rmsnorm(x) * norm_w) with eps, as obs_rmsnorm computes it (the input
+ * and final norms of forward.rs:403, :560, fused). in 2048 or 4096, group 64. */
 int obs_q4_gemv(obs_ctx* ctx, const uint16_t* x, uint32_t in, uint32_t group, const obs_gemv_part* parts,
-                uint32_t n_parts);
+                uint32_t n_parts, const uint16_t* norm_w, float eps);
 
 /* Per-head q/k RMSNorm (q_norm/k_norm weights [head_dim], eps), NeoX RoPE at
  * state[0] with rope_theta, q rotated in place, k and v appended to the caches

@@ -47,6 +47,8 @@ struct GemvPart {
 struct GemvArgs {
   GemvPart p[3];
   uint32_t n_parts, total_rows, in;
+  const uint16_t* norm_w;  // x <- bf16(rmsnorm(x) * norm_w) first (nullptr: x as given)
+  float eps;
 };
 
 template <uint32_t SEG>
@@ -54,43 +56,17 @@ __global__ void __launch_bounds__(256) q4_gemv_kernel(const uint16_t* __restrict
   const uint32_t lane = threadIdx.x & 63u;
   const uint32_t wave_g = blockIdx.x * 4u + (threadIdx.x >> 6), n_waves = gridDim.x * 4u;
   constexpr uint32_t IN = 2048u * SEG, GROUPS = IN / 64u;
-  // the lane's activations (f16 pairs), their sum and the offset part, per segment
-  f16x2_t xh[SEG][16];
-  float xs[SEG], xoff[SEG];
-#pragma unroll
-  for (uint32_t sg = 0; sg < SEG; ++sg) {
-    const uint4* xp = reinterpret_cast<const uint4*>(x + 2048u * sg + 32u * lane);
-    float xf[32];
-#pragma unroll
-    for (uint32_t i = 0; i < 4; ++i) {
-      const uint4 v = xp[i];
-      const uint32_t wd[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-      for (uint32_t j = 0; j < 4; ++j) {
-        xf[8 * i + 2 * j] = bf16lo(wd[j]);
-        xf[8 * i + 2 * j + 1] = bf16hi(wd[j]);
-      }
-    }
-    float sum = 0.0f;
-#pragma unroll
-    for (uint32_t c = 0; c < 32; ++c) sum = sum + xf[c];
-    xs[sg] = sum;
-#pragma unroll
-    for (uint32_t i = 0; i < 4; ++i) f16_pairs8(xf + 8 * i, xh[sg] + 4 * i);
-    float off = 0.0f;
-#pragma unroll
-    for (uint32_t i = 0; i < 4; ++i) off = dot8_off_only(xh[sg] + 4 * i, off);
-    xoff[sg] = off;
-  }
   // a part's fields by index, as selects (indexing the argument struct would copy it to scratch)
   auto part_of = [&](uint32_t pi) __attribute__((always_inline)) {
     return pi == 0u ? a.p[0] : (pi == 1u ? a.p[1] : a.p[2]);
   };
-  for (uint32_t r0 = 4u * wave_g; r0 < a.total_rows; r0 += 4u * n_waves) {
+  struct Rows {
     uint4 q[4][SEG];
     uint16_t sc[4][SEG], bi[4][SEG];
     uint32_t pidx[4], prow[4];
-    // every load of the four rows first (rows past the end reload the last one)
+  };
+  // every load of four rows (rows past the end reload the last one)
+  auto load_rows = [&](uint32_t r0, Rows& R) __attribute__((always_inline)) {
 #pragma unroll
     for (uint32_t k = 0; k < 4; ++k) {
       uint32_t r = min(r0 + k, a.total_rows - 1u), pi = 0;
@@ -102,37 +78,105 @@ __global__ void __launch_bounds__(256) q4_gemv_kernel(const uint16_t* __restrict
           pi = 2;
         }
       }
-      pidx[k] = pi;
-      prow[k] = r;
+      R.pidx[k] = pi;
+      R.prow[k] = r;
       const GemvPart P = part_of(pi);
 #pragma unroll
       for (uint32_t sg = 0; sg < SEG; ++sg) {
-        q[k][sg] = reinterpret_cast<const uint4*>(P.w + static_cast<size_t>(r) * (IN / 8u) + 256u * sg)[lane];
+        R.q[k][sg] = reinterpret_cast<const uint4*>(P.w + static_cast<size_t>(r) * (IN / 8u) + 256u * sg)[lane];
         const size_t gi = static_cast<size_t>(r) * GROUPS + 32u * sg + lane / 2u;
-        sc[k][sg] = P.s[gi];
-        bi[k][sg] = P.b[gi];
+        R.sc[k][sg] = P.s[gi];
+        R.bi[k][sg] = P.b[gi];
       }
     }
+  };
+  // the lane's activations: loaded, then the first rows' weights are issued
+  // (they do not depend on x) before the activation work below
+  uint4 xv[SEG][4], nv[SEG][4];
+#pragma unroll
+  for (uint32_t sg = 0; sg < SEG; ++sg)
+#pragma unroll
+    for (uint32_t i = 0; i < 4; ++i) {
+      xv[sg][i] = reinterpret_cast<const uint4*>(x + 2048u * sg + 32u * lane)[i];
+      nv[sg][i] = a.norm_w ? reinterpret_cast<const uint4*>(a.norm_w + 2048u * sg + 32u * lane)[i] : xv[sg][i];
+    }
+  Rows cur;
+  uint32_t r0 = 4u * wave_g;
+  if (r0 < a.total_rows) load_rows(r0, cur);
+  float xf[SEG][32];
+#pragma unroll
+  for (uint32_t sg = 0; sg < SEG; ++sg)
+#pragma unroll
+    for (uint32_t i = 0; i < 4; ++i) {
+      const uint32_t wd[4] = {xv[sg][i].x, xv[sg][i].y, xv[sg][i].z, xv[sg][i].w};
+#pragma unroll
+      for (uint32_t j = 0; j < 4; ++j) {
+        xf[sg][8 * i + 2 * j] = bf16lo(wd[j]);
+        xf[sg][8 * i + 2 * j + 1] = bf16hi(wd[j]);
+      }
+    }
+  if (a.norm_w) {  // RMSNorm of x (obs_rmsnorm's sequence; its lane order when in == 2048)
+    float ss = 0.0f;
+#pragma unroll
+    for (uint32_t sg = 0; sg < SEG; ++sg)
+#pragma unroll
+      for (uint32_t c = 0; c < 32; ++c) ss = __builtin_fmaf(xf[sg][c], xf[sg][c], ss);
+    const float inv = 1.0f / __builtin_sqrtf(wave_sum_asc(ss) / static_cast<float>(IN) + a.eps);
+#pragma unroll
+    for (uint32_t sg = 0; sg < SEG; ++sg)
+#pragma unroll
+      for (uint32_t i = 0; i < 4; ++i) {
+        const uint32_t wd[4] = {nv[sg][i].x, nv[sg][i].y, nv[sg][i].z, nv[sg][i].w};
+#pragma unroll
+        for (uint32_t j = 0; j < 4; ++j) {
+          float& e0 = xf[sg][8 * i + 2 * j];
+          float& e1 = xf[sg][8 * i + 2 * j + 1];
+          e0 = bf16_to_f32(f32_to_bf16((e0 * inv) * bf16lo(wd[j])));
+          e1 = bf16_to_f32(f32_to_bf16((e1 * inv) * bf16hi(wd[j])));
+        }
+      }
+  }
+  // f16 pairs, their sum and the offset part, per segment
+  f16x2_t xh[SEG][16];
+  float xs[SEG], xoff[SEG];
+#pragma unroll
+  for (uint32_t sg = 0; sg < SEG; ++sg) {
+    float sum = 0.0f;
+#pragma unroll
+    for (uint32_t c = 0; c < 32; ++c) sum = sum + xf[sg][c];
+    xs[sg] = sum;
+#pragma unroll
+    for (uint32_t i = 0; i < 4; ++i) f16_pairs8(xf[sg] + 8 * i, xh[sg] + 4 * i);
+    float off = 0.0f;
+#pragma unroll
+    for (uint32_t i = 0; i < 4; ++i) off = dot8_off_only(xh[sg] + 4 * i, off);
+    xoff[sg] = off;
+  }
+  for (; r0 < a.total_rows; r0 += 4u * n_waves) {
+    Rows nxt;
+    const uint32_t r1 = r0 + 4u * n_waves;
+    if (r1 < a.total_rows) load_rows(r1, nxt);  // uniform; the next rows' loads overlap this compute
 #pragma unroll
     for (uint32_t k = 0; k < 4; ++k) {
       float part = 0.0f;
 #pragma unroll
       for (uint32_t sg = 0; sg < SEG; ++sg) {
         float acc = 0.0f;
-        acc = dot8_q4_off(q[k][sg].x, xh[sg] + 0, acc);
-        acc = dot8_q4_off(q[k][sg].y, xh[sg] + 4, acc);
-        acc = dot8_q4_off(q[k][sg].z, xh[sg] + 8, acc);
-        acc = dot8_q4_off(q[k][sg].w, xh[sg] + 12, acc);
-        part = part + __builtin_fmaf(bf16_to_f32(sc[k][sg]), acc - xoff[sg], bf16_to_f32(bi[k][sg]) * xs[sg]);
+        acc = dot8_q4_off(cur.q[k][sg].x, xh[sg] + 0, acc);
+        acc = dot8_q4_off(cur.q[k][sg].y, xh[sg] + 4, acc);
+        acc = dot8_q4_off(cur.q[k][sg].z, xh[sg] + 8, acc);
+        acc = dot8_q4_off(cur.q[k][sg].w, xh[sg] + 12, acc);
+        part = part + __builtin_fmaf(bf16_to_f32(cur.sc[k][sg]), acc - xoff[sg], bf16_to_f32(cur.bi[k][sg]) * xs[sg]);
       }
       part = wave_sum_asc(part);
       if (lane == 0 && r0 + k < a.total_rows) {
-        const GemvPart P = part_of(pidx[k]);
-        const uint32_t r = prow[k];
+        const GemvPart P = part_of(cur.pidx[k]);
+        const uint32_t r = cur.prow[k];
         if (P.y_f32) P.y_f32[r] = part;
         if (P.y_bf16) P.y_bf16[r] = f32_to_bf16(P.residual ? bf16_to_f32(P.residual[r]) + part : part);
       }
     }
+    if (r1 < a.total_rows) cur = nxt;
   }
 }
 
@@ -260,17 +304,30 @@ __global__ void __launch_bounds__(64) sdpa_split_kernel(const uint16_t* __restri
   const uint16_t* vb = v_cache_t + static_cast<size_t>(kv) * HD * max_len;
   for (uint32_t blk = b0; blk < b1; ++blk) {
     const uint32_t t0 = 32u * blk;
+    // every load of the block first: the key rows of both tiles and the value
+    // columns (they do not depend on the scores)
+    u32x4_t ka[2][4];
+#pragma unroll
+    for (uint32_t tt = 0; tt < 2; ++tt) {
+      const uint16_t* kr = kb + static_cast<size_t>(t0 + 16u * tt + col) * HD + 8u * g;
+#pragma unroll
+      for (uint32_t ks = 0; ks < 4; ++ks) ka[tt][ks] = *reinterpret_cast<const u32x4_t*>(kr + 32u * ks);
+    }
+    u32x2_t va[8][2];
+#pragma unroll
+    for (uint32_t nt = 0; nt < 8; ++nt) {
+      const uint16_t* vr = vb + static_cast<size_t>(16u * nt + col) * max_len + t0 + 4u * g;
+      va[nt][0] = *reinterpret_cast<const u32x2_t*>(vr);
+      va[nt][1] = *reinterpret_cast<const u32x2_t*>(vr + 16);
+    }
     // scores of the two 16-position tiles
     f32x4_t s[2];
 #pragma unroll
     for (uint32_t tt = 0; tt < 2; ++tt) {
-      const uint16_t* kr = kb + static_cast<size_t>(t0 + 16u * tt + col) * HD + 8u * g;
       f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (uint32_t ks = 0; ks < 4; ++ks) {
-        const bf16x8_t a = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4_t*>(kr + 32u * ks));
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qb[ks], acc, 0, 0, 0);
-      }
+      for (uint32_t ks = 0; ks < 4; ++ks)
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, ka[tt][ks]), qb[ks], acc, 0, 0, 0);
       s[tt] = acc;
     }
     // lane holds S[h = col][t0 + 16 tt + 4 g + i]; mask positions >= seq
@@ -309,9 +366,7 @@ __global__ void __launch_bounds__(64) sdpa_split_kernel(const uint16_t* __restri
     const bool tail = t0 + 32u > seq;  // uniform; masked positions read zero values
 #pragma unroll
     for (uint32_t nt = 0; nt < 8; ++nt) {
-      const uint16_t* vr = vb + static_cast<size_t>(16u * nt + col) * max_len + t0 + 4u * g;
-      u32x2_t v0 = *reinterpret_cast<const u32x2_t*>(vr);
-      u32x2_t v1 = *reinterpret_cast<const u32x2_t*>(vr + 16);
+      u32x2_t v0 = va[nt][0], v1 = va[nt][1];
       if (tail) {  // a word holds positions t (low half) and t + 1 (high half)
         auto keep = [&](uint32_t w, uint32_t t) { return t >= seq ? 0u : (t + 1u >= seq ? (w & 0xffffu) : w); };
         const uint32_t ta = t0 + 4u * g, tb = ta + 16u;
@@ -345,21 +400,41 @@ __global__ void __launch_bounds__(64) sdpa_split_kernel(const uint16_t* __restri
 }
 
 // out[h] = sum_s O_s 2^(m_s - M) / sum_s l_s 2^(m_s - M), M = max_s m_s; bf16.
-__global__ void __launch_bounds__(128) sdpa_combine_kernel(const float* __restrict__ ws, uint16_t* __restrict__ out,
+// Wave 0 reads every split's (m, l) at once and forms the weights; then each
+// thread sums one dimension over a quarter of the splits with its loads all in
+// flight, and the quarters meet in LDS.
+__global__ void __launch_bounds__(512) sdpa_combine_kernel(const float* __restrict__ ws, uint16_t* __restrict__ out,
                                                            uint32_t nh, uint32_t nkv, uint32_t splits) {
-  const uint32_t h = blockIdx.x, d = threadIdx.x, G = nh / nkv, kv = h / G, hh = h % G;
-  const float* base = ws + static_cast<size_t>(kv) * splits * 16u * (HD + 2u) + hh * (HD + 2u);
-  float M = -__builtin_huge_valf();
-  for (uint32_t s = 0; s < splits; ++s) M = fmaxf(M, base[static_cast<size_t>(s) * 16u * (HD + 2u) + HD]);
-  float num = 0.0f, den = 0.0f;
-  for (uint32_t s = 0; s < splits; ++s) {
-    const float* p = base + static_cast<size_t>(s) * 16u * (HD + 2u);
-    const float ms = p[HD];
-    const float f = ms == -__builtin_huge_valf() ? 0.0f : __builtin_amdgcn_exp2f(ms - M);  // empty split: no weight
-    num = __builtin_fmaf(p[d], f, num);
-    den = __builtin_fmaf(p[HD + 1u], f, den);
+  __shared__ float s_f[64];
+  __shared__ float s_part[4][HD];
+  __shared__ float s_den;
+  const uint32_t h = blockIdx.x, tid = threadIdx.x, G = nh / nkv, kv = h / G, hh = h % G;
+  constexpr uint32_t STRIDE = 16u * (HD + 2u);  // floats between splits
+  const float* base = ws + static_cast<size_t>(kv) * splits * STRIDE + hh * (HD + 2u);
+  if (tid < 64u) {  // splits <= 64
+    const bool have = tid < splits;
+    const float m = have ? base[tid * STRIDE + HD] : -__builtin_huge_valf();
+    const float l = have ? base[tid * STRIDE + HD + 1u] : 0.0f;
+    float M = m;
+#pragma unroll
+    for (int k = 1; k < 64; k <<= 1) M = fmaxf(M, __shfl_xor(M, k, 64));
+    const float f = m == -__builtin_huge_valf() ? 0.0f : __builtin_amdgcn_exp2f(m - M);  // empty split: no weight
+    float den = l * f;
+#pragma unroll
+    for (int k = 1; k < 64; k <<= 1) den += __shfl_xor(den, k, 64);
+    s_f[tid] = f;
+    if (tid == 0) s_den = den;
   }
-  out[static_cast<size_t>(h) * HD + d] = f32_to_bf16(num / den);
+  __syncthreads();
+  const uint32_t d = tid & (HD - 1u), q4 = tid >> 7;  // 4 quarters of the splits
+  float num = 0.0f;
+#pragma unroll 4
+  for (uint32_t sp = q4; sp < splits; sp += 4u) num = __builtin_fmaf(base[sp * STRIDE + d], s_f[sp], num);
+  s_part[q4][d] = num;
+  __syncthreads();
+  if (tid < HD)
+    out[static_cast<size_t>(h) * HD + tid] =
+        f32_to_bf16(((s_part[0][tid] + s_part[1][tid]) + (s_part[2][tid] + s_part[3][tid])) / s_den);
 }
 
 // ---------------------------------------------------------------------------
@@ -447,15 +522,18 @@ uint32_t sdpa_splits(uint32_t max_len) {
 extern "C" {
 
 int obs_q4_gemv(obs_ctx* ctx, const uint16_t* x, uint32_t in, uint32_t group, const obs_gemv_part* parts,
-                uint32_t n_parts) {
+                uint32_t n_parts, const uint16_t* norm_w, float eps) {
   if (!ctx) return OBS_E_INVALID;
   if (!x || !parts || n_parts == 0 || n_parts > 3) return obs::set_error(ctx, OBS_E_INVALID, "obs_q4_gemv: null x/parts or n_parts not in 1..3");
   if (group != 64 || (in != 2048 && in != 4096))
     return obs::set_error(ctx, OBS_E_SHAPE, "obs_q4_gemv: in must be 2048 or 4096 and group 64 (got %u, %u)", in, group);
   if (!obs::aligned(x, 16)) return obs::set_error(ctx, OBS_E_ALIGN, "obs_q4_gemv: x must be 16-byte aligned");
+  if (norm_w && !obs::aligned(norm_w, 16)) return obs::set_error(ctx, OBS_E_ALIGN, "obs_q4_gemv: norm_w must be 16-byte aligned");
   GemvArgs a{};
   a.n_parts = n_parts;
   a.in = in;
+  a.norm_w = norm_w;
+  a.eps = eps;
   uint64_t total = 0;
   for (uint32_t i = 0; i < n_parts; ++i) {
     const obs_gemv_part& p = parts[i];
@@ -525,7 +603,7 @@ int obs_sdpa_decode(obs_ctx* ctx, const uint16_t* q, const uint16_t* k_cache, co
   float* w = static_cast<float*>(ws);
   OBS_LAUNCH(ctx, "sdpa_split", sdpa_split_kernel<<<n_kv * splits, 64, 0, ctx->stream>>>(
                                     q, k_cache, v_cache_t, w, n_heads, n_kv, max_len, splits, scale_log2, state));
-  OBS_LAUNCH(ctx, "sdpa_combine", sdpa_combine_kernel<<<n_heads, HD, 0, ctx->stream>>>(w, out, n_heads, n_kv, splits));
+  OBS_LAUNCH(ctx, "sdpa_combine", sdpa_combine_kernel<<<n_heads, 512, 0, ctx->stream>>>(w, out, n_heads, n_kv, splits));
   return OBS_OK;
 }
 

@@ -160,7 +160,7 @@ def lib() -> C.CDLL:
         "obs_moe_layer_bytes": (sz, [C.POINTER(ObsMoeConfig)]),
         "obs_ckpt_load_moe_layer": (i32, [vp, vp, u32, C.POINTER(ObsMoeConfig), vp, sz, C.POINTER(ObsMoeLayer)]),
         "obs_ckpt_load_tensor": (i32, [vp, vp, C.c_char_p, vp, sz]),
-        "obs_q4_gemv": (i32, [vp, vp, u32, u32, C.POINTER(ObsGemvPart), u32]),
+        "obs_q4_gemv": (i32, [vp, vp, u32, u32, C.POINTER(ObsGemvPart), u32, vp, f32]),
         "obs_attn_prep": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, u32, u32, u32, u32, f32, f32, vp]),
         "obs_sdpa_workspace": (sz, [u32, u32, u32, u32]),
         "obs_sdpa_decode": (i32, [vp, vp, vp, vp, vp, u32, u32, u32, u32, vp, vp, sz]),
@@ -372,12 +372,13 @@ class ObsidianExecutor:
                                          _ptr(ids_out), _ptr(w_out)))
 
     # -- the rest of a decode step (forward.rs:398-419, :445-462, :552-567) --
-    def q4_gemv(self, x, in_f: int, parts: Sequence[Tuple], group: int = 64) -> None:
-        """parts: (w, s, b, rows, y_f32, y_bf16, residual) tuples, 1 to 3."""
+    def q4_gemv(self, x, in_f: int, parts: Sequence[Tuple], group: int = 64, norm_w=None, eps: float = 1e-6) -> None:
+        """parts: (w, s, b, rows, y_f32, y_bf16, residual) tuples, 1 to 3; norm_w:
+        RMSNorm x first (fused)."""
         arr = (ObsGemvPart * len(parts))()
         for i, (w, s_, b, rows, yf, yb, res) in enumerate(parts):
             arr[i] = ObsGemvPart(_ptr(w), _ptr(s_), _ptr(b), _ptr(yf), _ptr(yb), _ptr(res), rows)
-        self._check(lib().obs_q4_gemv(self.ctx, _ptr(x), in_f, group, arr, len(parts)))
+        self._check(lib().obs_q4_gemv(self.ctx, _ptr(x), in_f, group, arr, len(parts), _ptr(norm_w), float(eps)))
 
     def attn_prep(self, q, k, v, q_norm, k_norm, k_cache, v_cache_t, n_heads: int, n_kv: int, head_dim: int,
                   max_len: int, eps: float, theta: float, state) -> None:

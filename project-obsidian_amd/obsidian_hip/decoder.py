@@ -59,17 +59,23 @@ class Model:
     GLOBAL_KEYS. The KV caches, activations and workspaces are allocated here
     once (forward.rs:56-104 allocates the pools once too)."""
 
-    def __init__(self, exe: ObsidianExecutor, cfg: DecoderConfig, layers: List[Dict], glob: Dict):
+    def __init__(self, exe: ObsidianExecutor, cfg: DecoderConfig, layers: List[Dict], glob: Dict,
+                 caches: Optional[List] = None):
+        """caches: optional per-layer (keys, transposed values) device buffers or
+        pointers (bf16 [n_kv, max_len, head_dim] and [n_kv, head_dim, max_len]);
+        zeroed ones are allocated otherwise (KvCache::new, kv_cache.rs:15-24)."""
         self.exe, self.cfg, self.layers, self.glob = exe, cfg, layers, glob
         c = cfg
         if c.n_heads * c.head_dim not in (2048, 4096) or c.hidden not in (2048, 4096):
             raise ValueError("the fused mat-vec needs hidden and n_heads * head_dim in {2048, 4096}")
-        self.caches = [(exe.zeros((c.n_kv, c.max_len, c.head_dim), np.uint16),
-                        exe.zeros((c.n_kv, c.head_dim, c.max_len), np.uint16)) for _ in range(c.n_layers)]
+        if caches is not None and len(caches) != c.n_layers:
+            raise ValueError("one (keys, values) cache pair per layer")
+        self.caches = caches if caches is not None else [
+            (exe.zeros((c.n_kv, c.max_len, c.head_dim), np.uint16), exe.zeros((c.n_kv, c.head_dim, c.max_len), np.uint16))
+            for _ in range(c.n_layers)]
         self.state = exe.zeros(2, np.int32)              # {pos, tok}
         self.x = exe.alloc(c.hidden, np.uint16)          # residual stream (layer input and output)
         self.x1 = exe.alloc(c.hidden, np.uint16)         # after attention
-        self.xn = exe.alloc(c.hidden, np.uint16)
         self.q = exe.alloc(c.n_heads * c.head_dim, np.uint16)
         self.k = exe.alloc(c.n_kv * c.head_dim, np.uint16)
         self.v = exe.alloc(c.n_kv * c.head_dim, np.uint16)
@@ -86,11 +92,12 @@ class Model:
         optional device buffers for the layer's routing)."""
         c, e, L = self.cfg, self.exe, self.layers[il]
         kc, vc = self.caches[il]
-        e.rmsnorm_raw(self.x, L["in_norm"], self.xn, 1, c.hidden, c.rms_eps)
         qd, kvd = c.n_heads * c.head_dim, c.n_kv * c.head_dim
-        e.q4_gemv(self.xn, c.hidden, [(L["q_w"], L["q_s"], L["q_b"], qd, None, self.q, None),
-                                      (L["k_w"], L["k_s"], L["k_b"], kvd, None, self.k, None),
-                                      (L["v_w"], L["v_s"], L["v_b"], kvd, None, self.v, None)])
+        # input RMSNorm (forward.rs:403) fused into the q/k/v mat-vec
+        e.q4_gemv(self.x, c.hidden, [(L["q_w"], L["q_s"], L["q_b"], qd, None, self.q, None),
+                                     (L["k_w"], L["k_s"], L["k_b"], kvd, None, self.k, None),
+                                     (L["v_w"], L["v_s"], L["v_b"], kvd, None, self.v, None)],
+                  norm_w=L["in_norm"], eps=c.rms_eps)
         e.attn_prep(self.q, self.k, self.v, L["q_norm"], L["k_norm"], kc, vc, c.n_heads, c.n_kv, c.head_dim,
                     c.max_len, c.rms_eps, c.rope_theta, self.state)
         e.sdpa_decode(self.q, kc, vc, self.attn, c.n_heads, c.n_kv, c.head_dim, c.max_len, self.state, self.sdpa_ws)
@@ -106,8 +113,8 @@ class Model:
         """forward.rs:559-566: final norm, lm_head logits (fp32), greedy token into
         the state, position advanced."""
         g, c, e = self.glob, self.cfg, self.exe
-        e.rmsnorm_raw(self.x, g["final_norm"], self.xn, 1, c.hidden, c.rms_eps)
-        e.q4_gemv(self.xn, c.hidden, [(g["lm_w"], g["lm_s"], g["lm_b"], c.vocab, self.logits, None, None)])
+        e.q4_gemv(self.x, c.hidden, [(g["lm_w"], g["lm_s"], g["lm_b"], c.vocab, self.logits, None, None)],
+                  norm_w=g["final_norm"], eps=c.rms_eps)  # final RMSNorm (forward.rs:560) fused
         e.argmax(self.logits, c.vocab, self.state, self.argmax_ws)
 
     def step(self) -> None:

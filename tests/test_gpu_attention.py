@@ -54,6 +54,26 @@ def test_q4_gemv_parts_vs_oracle(exe, in_f):
         assert np.all(np.abs(got - y64) <= bound), (i, float(np.max(np.abs(got - y64) / (ab + 1e-30))))
 
 
+@pytest.mark.parametrize("in_f", [2048, 4096])
+def test_q4_gemv_fused_rmsnorm(exe, in_f):
+    """norm_w: x is replaced by bf16(rmsnorm(x) * w) first (the input / final
+    norms fused); against the oracle norm then the oracle mat-vec."""
+    rng = np.random.default_rng(520 + in_f)
+    rows = 384
+    w, s, b = synth.quant_tensor(rng, rows, in_f, 4, 64)
+    x = synth.bf16_normal(rng, in_f, 3.0)
+    nw = synth.norm_weight(rng, in_f)
+    y = exe.alloc(rows, np.float32)
+    exe.q4_gemv(exe.upload(x), in_f, [(exe.upload(w), exe.upload(s), exe.upload(b), rows, y, None, None)],
+                norm_w=exe.upload(nw), eps=EPS)
+    xn = O.rmsnorm(x, nw, EPS)
+    y64, ab = O.qmatvec("f64", 4, w, s, b, synth.bf16_bits_to_f32(xn), in_f, rows)
+    got = y.download().astype(np.float64)
+    # in = 2048: the norm is obs_rmsnorm's sequence exactly; 4096 sums in another order (one bf16 step)
+    bound = (1e-3 if in_f == 2048 else 5e-3) * ab
+    assert np.all(np.abs(got - y64) <= bound), float(np.max(np.abs(got - y64) / ab))
+
+
 def test_q4_gemv_rejects_bad_shapes(exe):
     x = exe.alloc(3072, np.uint16)
     y = exe.alloc(4, np.float32)
