@@ -28,13 +28,19 @@ constexpr uint32_t HD = 128;  // head_dim the attention kernels are written for
 // ---------------------------------------------------------------------------
 // 4-bit mat-vec for the decoder's projections and lm_head
 // ---------------------------------------------------------------------------
-// One wave per output row, four rows in flight per wave. Lane l covers
-// columns [2048 s + 32 l, +32) of every 2048-column segment s: one coalesced
-// 16-byte load per row and segment (a 1 KB row segment per wave load). The
-// 32 nibbles are dotted with the lane's activations as f16 pairs through the
+// One wave per output row group of RPW rows, one pass: every load of the
+// wave (its activations, the norm weights, the RPW rows with their scales and
+// biases) is issued first, pinned there by a scheduling barrier, then the
+// activation work runs while the rows arrive. Lane l covers columns
+// [2048 s + 32 l, +32) of every 2048-column segment s: one coalesced 16-byte
+// load per row and segment (a 1 KB row segment per wave load). The 32
+// nibbles are dotted with the lane's activations as f16 pairs through the
 // magic-offset unpack (dot8_q4_off, 9 instructions per 8 nibbles), then
 // y_lane = s (sum q x) + b (sum x) with the lane's group scale and bias, and
-// the wave sums in the butterfly order (wave_sum_asc).
+// the wave sums in the butterfly order (wave_sum_asc). The hardware refills
+// the CUs with new workgroups as waves finish, so a large matrix (lm_head)
+// needs no loop, whose register copies and stores forced waits for the
+// prefetched rows.
 struct GemvPart {
   const uint32_t* w;
   const uint16_t* s;
@@ -51,58 +57,54 @@ struct GemvArgs {
   float eps;
 };
 
-template <uint32_t SEG>
+template <uint32_t SEG, uint32_t RPW>
 __global__ void __launch_bounds__(256) q4_gemv_kernel(const uint16_t* __restrict__ x, GemvArgs a) {
   const uint32_t lane = threadIdx.x & 63u;
-  const uint32_t wave_g = blockIdx.x * 4u + (threadIdx.x >> 6), n_waves = gridDim.x * 4u;
+  // the wave index in a scalar register, so that every row index and part
+  // choice below is wave-uniform: part fields are picked by scalar selects
+  // (a divergent index made the compiler fetch the argument struct with
+  // vector loads and wait for them before every row)
+  const uint32_t wave_g = __builtin_amdgcn_readfirstlane(blockIdx.x * 4u + (threadIdx.x >> 6));
   constexpr uint32_t IN = 2048u * SEG, GROUPS = IN / 64u;
-  // a part's fields by index, as selects (indexing the argument struct would copy it to scratch)
-  auto part_of = [&](uint32_t pi) __attribute__((always_inline)) {
-    return pi == 0u ? a.p[0] : (pi == 1u ? a.p[1] : a.p[2]);
+  const uint32_t r0 = RPW * wave_g;
+  if (r0 >= a.total_rows) return;  // wave-uniform
+  // rows [0, end0) are part 0, [end0, end1) part 1, the rest part 2 (unused parts have 0 rows)
+  const uint32_t end0 = a.p[0].rows, end1 = a.p[0].rows + a.p[1].rows;
+  auto pick = [](uint32_t pi, auto v0, auto v1, auto v2) __attribute__((always_inline)) {
+    return pi == 0u ? v0 : (pi == 1u ? v1 : v2);
   };
-  struct Rows {
-    uint4 q[4][SEG];
-    uint16_t sc[4][SEG], bi[4][SEG];
-    uint32_t pidx[4], prow[4];
-  };
-  // every load of four rows (rows past the end reload the last one)
-  auto load_rows = [&](uint32_t r0, Rows& R) __attribute__((always_inline)) {
-#pragma unroll
-    for (uint32_t k = 0; k < 4; ++k) {
-      uint32_t r = min(r0 + k, a.total_rows - 1u), pi = 0;
-      if (a.n_parts > 1u && r >= a.p[0].rows) {
-        r -= a.p[0].rows;
-        pi = 1;
-        if (a.n_parts > 2u && r >= a.p[1].rows) {
-          r -= a.p[1].rows;
-          pi = 2;
-        }
-      }
-      R.pidx[k] = pi;
-      R.prow[k] = r;
-      const GemvPart P = part_of(pi);
-#pragma unroll
-      for (uint32_t sg = 0; sg < SEG; ++sg) {
-        R.q[k][sg] = reinterpret_cast<const uint4*>(P.w + static_cast<size_t>(r) * (IN / 8u) + 256u * sg)[lane];
-        const size_t gi = static_cast<size_t>(r) * GROUPS + 32u * sg + lane / 2u;
-        R.sc[k][sg] = P.s[gi];
-        R.bi[k][sg] = P.b[gi];
-      }
-    }
-  };
-  // the lane's activations: loaded, then the first rows' weights are issued
-  // (they do not depend on x) before the activation work below
+  // the lane's activations and norm weights (unconditional loads)
+  const uint16_t* const nsrc = a.norm_w ? a.norm_w : x;
   uint4 xv[SEG][4], nv[SEG][4];
 #pragma unroll
   for (uint32_t sg = 0; sg < SEG; ++sg)
 #pragma unroll
     for (uint32_t i = 0; i < 4; ++i) {
       xv[sg][i] = reinterpret_cast<const uint4*>(x + 2048u * sg + 32u * lane)[i];
-      nv[sg][i] = a.norm_w ? reinterpret_cast<const uint4*>(a.norm_w + 2048u * sg + 32u * lane)[i] : xv[sg][i];
+      nv[sg][i] = reinterpret_cast<const uint4*>(nsrc + 2048u * sg + 32u * lane)[i];
     }
-  Rows cur;
-  uint32_t r0 = 4u * wave_g;
-  if (r0 < a.total_rows) load_rows(r0, cur);
+  // the rows (past the end: the last row again, results unused)
+  uint4 q[RPW][SEG];
+  uint16_t sc[RPW][SEG], bi[RPW][SEG], res[RPW];
+#pragma unroll
+  for (uint32_t k = 0; k < RPW; ++k) {
+    const uint32_t r = min(r0 + k, a.total_rows - 1u);
+    const uint32_t pi = (r >= end0 ? 1u : 0u) + (r >= end1 ? 1u : 0u);
+    const uint32_t rr = r - (pi == 0u ? 0u : (pi == 1u ? end0 : end1));
+    const uint32_t* w = pick(pi, a.p[0].w, a.p[1].w, a.p[2].w);
+    const uint16_t* sp = pick(pi, a.p[0].s, a.p[1].s, a.p[2].s);
+    const uint16_t* bp = pick(pi, a.p[0].b, a.p[1].b, a.p[2].b);
+    const uint16_t* rp = pick(pi, a.p[0].residual, a.p[1].residual, a.p[2].residual);
+#pragma unroll
+    for (uint32_t sg = 0; sg < SEG; ++sg) {
+      q[k][sg] = reinterpret_cast<const uint4*>(w + static_cast<size_t>(rr) * (IN / 8u) + 256u * sg)[lane];
+      const size_t gi = static_cast<size_t>(rr) * GROUPS + 32u * sg + lane / 2u;
+      sc[k][sg] = sp[gi];
+      bi[k][sg] = bp[gi];
+    }
+    res[k] = *(rp ? rp + rr : sp);  // the row's residual (the scales when the part has none; unused then)
+  }
+  __builtin_amdgcn_sched_barrier(0);
   float xf[SEG][32];
 #pragma unroll
   for (uint32_t sg = 0; sg < SEG; ++sg)
@@ -115,7 +117,9 @@ __global__ void __launch_bounds__(256) q4_gemv_kernel(const uint16_t* __restrict
         xf[sg][8 * i + 2 * j + 1] = bf16hi(wd[j]);
       }
     }
-  if (a.norm_w) {  // RMSNorm of x (obs_rmsnorm's sequence; its lane order when in == 2048)
+  {  // RMSNorm of x (obs_rmsnorm's sequence; its lane order when in == 2048),
+     // computed every time and selected (no branch around the loads' use)
+    const bool use_norm = a.norm_w != nullptr;
     float ss = 0.0f;
 #pragma unroll
     for (uint32_t sg = 0; sg < SEG; ++sg)
@@ -131,8 +135,10 @@ __global__ void __launch_bounds__(256) q4_gemv_kernel(const uint16_t* __restrict
         for (uint32_t j = 0; j < 4; ++j) {
           float& e0 = xf[sg][8 * i + 2 * j];
           float& e1 = xf[sg][8 * i + 2 * j + 1];
-          e0 = bf16_to_f32(f32_to_bf16((e0 * inv) * bf16lo(wd[j])));
-          e1 = bf16_to_f32(f32_to_bf16((e1 * inv) * bf16hi(wd[j])));
+          const float n0 = bf16_to_f32(f32_to_bf16((e0 * inv) * bf16lo(wd[j])));
+          const float n1 = bf16_to_f32(f32_to_bf16((e1 * inv) * bf16hi(wd[j])));
+          e0 = use_norm ? n0 : e0;
+          e1 = use_norm ? n1 : e1;
         }
       }
   }
@@ -152,31 +158,35 @@ __global__ void __launch_bounds__(256) q4_gemv_kernel(const uint16_t* __restrict
     for (uint32_t i = 0; i < 4; ++i) off = dot8_off_only(xh[sg] + 4 * i, off);
     xoff[sg] = off;
   }
-  for (; r0 < a.total_rows; r0 += 4u * n_waves) {
-    Rows nxt;
-    const uint32_t r1 = r0 + 4u * n_waves;
-    if (r1 < a.total_rows) load_rows(r1, nxt);  // uniform; the next rows' loads overlap this compute
+  // the rows' sums; lane k keeps row k's result, so one store serves the wave
+  float mine = 0.0f;
 #pragma unroll
-    for (uint32_t k = 0; k < 4; ++k) {
-      float part = 0.0f;
+  for (uint32_t k = 0; k < RPW; ++k) {
+    float part = 0.0f;
 #pragma unroll
-      for (uint32_t sg = 0; sg < SEG; ++sg) {
-        float acc = 0.0f;
-        acc = dot8_q4_off(cur.q[k][sg].x, xh[sg] + 0, acc);
-        acc = dot8_q4_off(cur.q[k][sg].y, xh[sg] + 4, acc);
-        acc = dot8_q4_off(cur.q[k][sg].z, xh[sg] + 8, acc);
-        acc = dot8_q4_off(cur.q[k][sg].w, xh[sg] + 12, acc);
-        part = part + __builtin_fmaf(bf16_to_f32(cur.sc[k][sg]), acc - xoff[sg], bf16_to_f32(cur.bi[k][sg]) * xs[sg]);
-      }
-      part = wave_sum_asc(part);
-      if (lane == 0 && r0 + k < a.total_rows) {
-        const GemvPart P = part_of(cur.pidx[k]);
-        const uint32_t r = cur.prow[k];
-        if (P.y_f32) P.y_f32[r] = part;
-        if (P.y_bf16) P.y_bf16[r] = f32_to_bf16(P.residual ? bf16_to_f32(P.residual[r]) + part : part);
-      }
+    for (uint32_t sg = 0; sg < SEG; ++sg) {
+      float acc = 0.0f;
+      acc = dot8_q4_off(q[k][sg].x, xh[sg] + 0, acc);
+      acc = dot8_q4_off(q[k][sg].y, xh[sg] + 4, acc);
+      acc = dot8_q4_off(q[k][sg].z, xh[sg] + 8, acc);
+      acc = dot8_q4_off(q[k][sg].w, xh[sg] + 12, acc);
+      part = part + __builtin_fmaf(bf16_to_f32(sc[k][sg]), acc - xoff[sg], bf16_to_f32(bi[k][sg]) * xs[sg]);
     }
-    if (r1 < a.total_rows) cur = nxt;
+    part = wave_sum_asc(part);
+    const float y = bf16_to_f32(res[k]) + part;  // used only where the part has a residual
+    const uint32_t r = min(r0 + k, a.total_rows - 1u);
+    const uint32_t pi = (r >= end0 ? 1u : 0u) + (r >= end1 ? 1u : 0u);
+    const bool has_res = pick(pi, a.p[0].residual, a.p[1].residual, a.p[2].residual) != nullptr;
+    mine = lane == k ? (has_res ? y : part) : mine;
+  }
+  const uint32_t r = r0 + lane;
+  if (lane < RPW && r < a.total_rows) {
+    const uint32_t pi = (r >= end0 ? 1u : 0u) + (r >= end1 ? 1u : 0u);
+    const uint32_t rr = r - (pi == 0u ? 0u : (pi == 1u ? end0 : end1));
+    float* yf = pick(pi, a.p[0].y_f32, a.p[1].y_f32, a.p[2].y_f32);
+    uint16_t* yb = pick(pi, a.p[0].y_bf16, a.p[1].y_bf16, a.p[2].y_bf16);
+    if (yf) yf[rr] = mine;
+    if (yb) yb[rr] = f32_to_bf16(mine);
   }
 }
 
@@ -548,13 +558,22 @@ int obs_q4_gemv(obs_ctx* ctx, const uint16_t* x, uint32_t in, uint32_t group, co
   if (total == 0) return OBS_OK;
   if (total > 0x7fffffffull) return obs::set_error(ctx, OBS_E_SHAPE, "obs_q4_gemv: too many rows");
   a.total_rows = static_cast<uint32_t>(total);
-  // four rows per wave in flight; enough workgroups to cover the rows once, at most 4 per CU
-  const uint32_t waves = (a.total_rows + 3u) / 4u;
-  const uint32_t grid = min((waves + 3u) / 4u, static_cast<uint32_t>(ctx->num_cus) * 4u);
-  if (in == 2048)
-    OBS_LAUNCH(ctx, "q4_gemv", q4_gemv_kernel<1><<<grid, 256, 0, ctx->stream>>>(x, a));
-  else
-    OBS_LAUNCH(ctx, "q4_gemv", q4_gemv_kernel<2><<<grid, 256, 0, ctx->stream>>>(x, a));
+  // one pass: 4 rows per wave for the projections (more waves in flight),
+  // 16 for large matrices (the activation work amortised over more rows)
+  const bool big = a.total_rows > 16384u;
+  const uint32_t rpw = big ? 16u : 4u;
+  const uint32_t grid = (a.total_rows + 4u * rpw - 1u) / (4u * rpw);
+  if (in == 2048) {
+    if (big)
+      OBS_LAUNCH(ctx, "q4_gemv", q4_gemv_kernel<1, 16><<<grid, 256, 0, ctx->stream>>>(x, a));
+    else
+      OBS_LAUNCH(ctx, "q4_gemv", q4_gemv_kernel<1, 4><<<grid, 256, 0, ctx->stream>>>(x, a));
+  } else {
+    if (big)  // 8 rows per wave at this width (16 would need more than 256 registers)
+      OBS_LAUNCH(ctx, "q4_gemv", q4_gemv_kernel<2, 8><<<(a.total_rows + 31u) / 32u, 256, 0, ctx->stream>>>(x, a));
+    else
+      OBS_LAUNCH(ctx, "q4_gemv", q4_gemv_kernel<2, 4><<<grid, 256, 0, ctx->stream>>>(x, a));
+  }
   return OBS_OK;
 }
 

@@ -74,6 +74,34 @@ def test_q4_gemv_fused_rmsnorm(exe, in_f):
     assert np.all(np.abs(got - y64) <= bound), float(np.max(np.abs(got - y64) / ab))
 
 
+@pytest.mark.parametrize("in_f,rows", [(2048, 16421), (4096, 16389)])
+def test_q4_gemv_large_matrix(exe, in_f, rows):
+    """Above 16,384 rows each wave takes 16 (in 2048) or 8 (in 4096) rows; a
+    row count that leaves the last wave partly empty, one bf16 part with a
+    residual next to an fp32 part, and the fused norm."""
+    rng = np.random.default_rng(540 + in_f)
+    r1 = 7
+    w, s, b = synth.quant_tensor(rng, rows - r1, in_f, 4, 64)
+    w1, s1, b1 = synth.quant_tensor(rng, r1, in_f, 4, 64)
+    x = synth.bf16_normal(rng, in_f, 2.0)
+    nw = synth.norm_weight(rng, in_f)
+    res = synth.bf16_normal(rng, r1, 4.0)
+    y = exe.alloc(rows - r1, np.float32)
+    y1 = exe.alloc(r1, np.uint16)
+    exe.q4_gemv(exe.upload(x), in_f, [(exe.upload(w), exe.upload(s), exe.upload(b), rows - r1, y, None, None),
+                                      (exe.upload(w1), exe.upload(s1), exe.upload(b1), r1, None, y1, exe.upload(res))],
+                norm_w=exe.upload(nw), eps=EPS)
+    xn = synth.bf16_bits_to_f32(O.rmsnorm(x, nw, EPS))
+    tol = 1e-3 if in_f == 2048 else 5e-3
+    y64, ab = O.qmatvec("f64", 4, w, s, b, xn, in_f, rows - r1)
+    got = y.download().astype(np.float64)
+    assert np.all(np.abs(got - y64) <= tol * ab), float(np.max(np.abs(got - y64) / ab))
+    y64, ab = O.qmatvec("f64", 4, w1, s1, b1, xn, in_f, r1)
+    y64, ab = y64 + _f(res), ab + np.abs(_f(res))
+    got = _f(y1.download())
+    assert np.all(np.abs(got - y64) <= tol * ab + 2.0 ** -8 * np.abs(y64))
+
+
 def test_q4_gemv_rejects_bad_shapes(exe):
     x = exe.alloc(3072, np.uint16)
     y = exe.alloc(4, np.float32)
