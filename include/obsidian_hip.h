@@ -310,6 +310,35 @@ size_t obs_argmax_workspace(void);
 int obs_argmax(obs_ctx* ctx, const float* x, uint32_t n, int32_t* state, void* ws, size_t ws_bytes);
 
 /* ------------------------------------------------------------------ */
+/* Prefill of the layers around the MoE block for a batch of tokens     */
+/* (Model::prefill_batched, forward.rs:114-160, :240-261)               */
+/* ------------------------------------------------------------------ */
+/* out[t] = bf16 row tokens[t] of a 4-bit embedding table (Model::embed per
+ * prompt token, forward.rs:136); tokens: device int32 [n_tokens], clamped into
+ * [0, vocab); out bf16 [n_tokens, hidden], rows 16-byte aligned. */
+int obs_embed_q4_rows(obs_ctx* ctx, const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
+                      uint32_t hidden, uint32_t group, uint32_t vocab, const int32_t* tokens, uint32_t n_tokens,
+                      uint16_t* out);
+
+/* obs_attn_prep for tokens [0, n_tokens) at positions pos0 + t (the per-token
+ * q/k norm, RoPE and KV appends of forward.rs:147-153): q bf16 [n_tokens,
+ * n_heads, head_dim] rotated in place, k, v bf16 [n_tokens, n_kv, head_dim]
+ * appended; pos0 + n_tokens <= max_len. */
+int obs_attn_prep_rows(obs_ctx* ctx, uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* q_norm,
+                       const uint16_t* k_norm, uint16_t* k_cache, uint16_t* v_cache_t, uint32_t n_heads,
+                       uint32_t n_kv, uint32_t head_dim, uint32_t max_len, float eps, float theta, uint32_t pos0,
+                       uint32_t n_tokens);
+
+/* Causal GQA attention of a prefill batch (the per-token Attention::sdpa of
+ * forward.rs:155 for tokens at positions pos0 + t): token t attends to cache
+ * positions [0, pos0 + t]; the batch's keys and values must be in the caches
+ * (obs_attn_prep_rows first). q, out bf16 [n_tokens, n_heads, head_dim];
+ * head_dim 128, query heads per kv head a divisor of 16. */
+int obs_sdpa_prefill(obs_ctx* ctx, const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache_t,
+                     uint16_t* out, uint32_t n_heads, uint32_t n_kv, uint32_t head_dim, uint32_t max_len,
+                     uint32_t pos0, uint32_t n_tokens);
+
+/* ------------------------------------------------------------------ */
 /* Checkpoint loading: safetensors -> HBM-resident expert table        */
 /* (replaces Qwen3MoeConfig::from_file model.rs:26-30,                 */
 /*  Weights::load_non_expert weight_loader.rs:19-71, ExpertIndex::open */

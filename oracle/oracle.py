@@ -339,6 +339,25 @@ def token_logits(G: Dict[str, np.ndarray], layers, tok: int, caches, pos: int, c
     return y
 
 
+def prefill(G: Dict[str, np.ndarray], layers, tokens, caches, pos0: int, cfg: Dict):
+    """prefill_batched (forward.rs:114-261): the embedding rows of `tokens`,
+    then layer-major, for every token i in order at position pos0 + i, the
+    decoder layer (the reference runs each token's attention with the per-token
+    kernels, forward.rs:141-158, so a token attends to the cache entries the
+    earlier tokens of the batch wrote), then the final RMSNorm and lm_head of
+    the last token. Returns (last layer's rows bf16 [T, hidden], fp64 logits
+    [vocab]); the caches are updated in place."""
+    H, V = cfg["hidden"], cfg["vocab"]
+    xs = [_bf16(dequant(4, G["embed_w"][t:t + 1], G["embed_s"][t:t + 1], G["embed_b"][t:t + 1], 1, H).reshape(-1))
+          for t in tokens]
+    for (P, moe), (kc, vc) in zip(layers, caches):
+        xs = [decoder_layer(P, moe, x, kc, vc, pos0 + i, cfg) for i, x in enumerate(xs)]
+    xn = rmsnorm(xs[-1], G["final_norm"], cfg["eps"])
+    xf = (xn.astype(np.uint32) << 16).view(np.float32)
+    y, _ = qmatvec("f64", 4, G["lm_w"], G["lm_s"], G["lm_b"], xf, H, V)
+    return np.stack(xs), y
+
+
 # ---- independent NumPy restatement (validate_dequant.py:26-30) --------------
 def dequant_numpy(W: np.ndarray, S_f32: np.ndarray, B_f32: np.ndarray, group: int = 64) -> np.ndarray:
     """nibble j of uint32 word = (word >> 4j) & 0xF; element i at word i//8,

@@ -193,43 +193,62 @@ __global__ void __launch_bounds__(256) q4_gemv_kernel(const uint16_t* __restrict
 // ---------------------------------------------------------------------------
 // q/k RMSNorm + NeoX RoPE + cache append, one launch
 // ---------------------------------------------------------------------------
-// One wave per head; lane l owns columns 2l, 2l+1 (the RMSNorm lane order of
-// obs_rmsnorm at dim 128). Heads [0, nh): query heads, normed and rotated in
-// place; [nh, nh+nkv): key heads, normed, rotated, written to the key cache at
-// pos; [nh+nkv, nh+2nkv): value heads, written to the transposed value cache.
-// RoPE pairs column i with i + 64, held by lane l ^ 32. Frequencies, cosines
-// and sines follow the oracle's restatement: f = fl32(theta^(-2i/128)) and
-// cos, sin of the fp32 angle fl32(pos * f), each evaluated in double and
-// rounded once; r0 = x0 c - x1 s, r1 = x1 c + x0 s with rounded products.
+// One wave per (token, head); lane l owns columns 2l, 2l+1 (the RMSNorm lane
+// order of obs_rmsnorm at dim 128). Heads [0, nh): query heads, normed and
+// rotated in place; [nh, nh+nkv): key heads, normed, rotated, written to the
+// key cache at pos; [nh+nkv, nh+2nkv): value heads, written to the transposed
+// value cache. RoPE pairs column i with i + 64, held by lane l ^ 32.
+// Frequencies, cosines and sines follow the oracle's restatement:
+// f = fl32(theta^(-2i/128)) and cos, sin of the fp32 angle fl32(pos * f), each
+// evaluated in double and rounded once; r0 = x0 c - x1 s, r1 = x1 c + x0 s
+// with rounded products.
+// ROWS = false (decode): one token at pos = state[0], read with a vector load
+// issued after the head's loads (a scalar load would be waited for together
+// with the kernel arguments, before any other load). ROWS = true (prefill):
+// tokens [0, n_tok) of q [n_tok, nh, 128], k, v [n_tok, nkv, 128] at
+// positions pos0 + token.
+template <bool ROWS>
 __global__ void __launch_bounds__(256) attn_prep_kernel(uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
                                                         const uint16_t* __restrict__ v,
                                                         const uint16_t* __restrict__ q_norm,
                                                         const uint16_t* __restrict__ k_norm,
                                                         uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache_t,
                                                         uint32_t nh, uint32_t nkv, uint32_t max_len, float eps,
-                                                        float theta, const int32_t* __restrict__ state) {
-  const uint32_t lane = threadIdx.x & 63u, head = blockIdx.x * 4u + (threadIdx.x >> 6);
-  if (head >= nh + 2u * nkv) return;  // wave-uniform
-  const int32_t pos_i = state[0];
-  const uint32_t pos = static_cast<uint32_t>(pos_i);
-  const bool pos_ok = pos_i >= 0 && pos < max_len;
+                                                        float theta, const int32_t* __restrict__ state, uint32_t pos0,
+                                                        uint32_t n_tok) {
+  const uint32_t lane = threadIdx.x & 63u, wave_g = blockIdx.x * 4u + (threadIdx.x >> 6);
+  const uint32_t heads = nh + 2u * nkv;
+  const uint32_t tok = ROWS ? wave_g / heads : 0u, head = ROWS ? wave_g % heads : wave_g;
+  if (tok >= n_tok || head >= heads) return;  // wave-uniform
+  q += static_cast<size_t>(tok) * nh * HD;
+  k += static_cast<size_t>(tok) * nkv * HD;
+  v += static_cast<size_t>(tok) * nkv * HD;
   const uint32_t c0 = 2u * lane;
-  if (head >= nh + nkv) {  // value head: transposed cache column pos
-    const uint32_t kv = head - nh - nkv;
-    const uint32_t vv = *reinterpret_cast<const uint32_t*>(v + kv * HD + c0);
-    if (pos_ok) {
-      uint16_t* dst = v_cache_t + (static_cast<size_t>(kv) * HD + c0) * max_len + pos;
-      dst[0] = static_cast<uint16_t>(vv & 0xffffu);
-      dst[max_len] = static_cast<uint16_t>(vv >> 16);
-    }
-    return;
-  }
-  const bool is_q = head < nh;
-  const uint32_t hk = is_q ? head : head - nh;
-  const uint16_t* src = is_q ? q + hk * HD : k + hk * HD;
+  const bool is_v = head >= nh + nkv, is_q = head < nh;
+  const uint32_t hk = is_q ? head : (is_v ? head - nh - nkv : head - nh);
+  // the head's values and norm weights (a value head loads its row twice; unused)
+  const uint16_t* src = is_q ? q + hk * HD : (is_v ? v + hk * HD : k + hk * HD);
   const uint16_t* wn = is_q ? q_norm : k_norm;
   const uint32_t xv = *reinterpret_cast<const uint32_t*>(src + c0);
   const uint32_t wv = *reinterpret_cast<const uint32_t*>(wn + c0);
+  int32_t pos_i;
+  if (ROWS) {
+    pos_i = static_cast<int32_t>(pos0 + tok);
+  } else {
+    uint32_t zero;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(zero));  // a per-lane index: a vector load
+    pos_i = state[zero];
+  }
+  const uint32_t pos = static_cast<uint32_t>(pos_i);
+  const bool pos_ok = pos_i >= 0 && pos < max_len;
+  if (is_v) {  // value head: transposed cache column pos
+    if (pos_ok) {
+      uint16_t* dst = v_cache_t + (static_cast<size_t>(hk) * HD + c0) * max_len + pos;
+      dst[0] = static_cast<uint16_t>(xv & 0xffffu);
+      dst[max_len] = static_cast<uint16_t>(xv >> 16);
+    }
+    return;
+  }
   const float x0 = bf16lo(xv), x1 = bf16hi(xv);
   float ss = __builtin_fmaf(x0, x0, 0.0f);
   ss = __builtin_fmaf(x1, x1, ss);
@@ -281,6 +300,14 @@ __global__ void __launch_bounds__(256) attn_prep_kernel(uint16_t* __restrict__ q
 //   positions of the transposed value cache (two 8-byte loads per dim tile).
 // The split's (m, l, O) go to the workspace; sdpa_combine_kernel merges them.
 __device__ __forceinline__ float shfl_xor_f(float v, int m) { return __shfl_xor(v, m, 64); }
+
+// Masks of a lane's four value words (positions ta, ta + 1 | ta + 2, ta + 3 |
+// ta + 16, ta + 17 | ta + 18, ta + 19; low half = the first): positions at or
+// past seq become zero.
+__device__ __forceinline__ u32x4_t value_masks(uint32_t ta, uint32_t seq) {
+  auto m = [&](uint32_t t) { return t >= seq ? 0u : (t + 1u >= seq ? 0xffffu : 0xffffffffu); };
+  return u32x4_t{m(ta), m(ta + 2u), m(ta + 16u), m(ta + 18u)};
+}
 
 __global__ void __launch_bounds__(64) sdpa_split_kernel(const uint16_t* __restrict__ q,
                                                         const uint16_t* __restrict__ k_cache,
@@ -373,19 +400,12 @@ __global__ void __launch_bounds__(64) sdpa_split_kernel(const uint16_t* __restri
         bf16x8_t, u32x4_t{pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]), pack_bf16x2(p[4], p[5]),
                           pack_bf16x2(p[6], p[7])});
     // values of the same positions: dim 16 nt + col, positions t0 + 4 g + i and t0 + 16 + 4 g + i
-    const bool tail = t0 + 32u > seq;  // uniform; masked positions read zero values
+    // masked positions read zero values (by select: a branch waits for loads at its join)
+    const u32x4_t vm = value_masks(t0 + 4u * g, seq);
 #pragma unroll
     for (uint32_t nt = 0; nt < 8; ++nt) {
-      u32x2_t v0 = va[nt][0], v1 = va[nt][1];
-      if (tail) {  // a word holds positions t (low half) and t + 1 (high half)
-        auto keep = [&](uint32_t w, uint32_t t) { return t >= seq ? 0u : (t + 1u >= seq ? (w & 0xffffu) : w); };
-        const uint32_t ta = t0 + 4u * g, tb = ta + 16u;
-        v0.x = keep(v0.x, ta);
-        v0.y = keep(v0.y, ta + 2u);
-        v1.x = keep(v1.x, tb);
-        v1.y = keep(v1.y, tb + 2u);
-      }
-      const bf16x8_t vbf = __builtin_bit_cast(bf16x8_t, u32x4_t{v0.x, v0.y, v1.x, v1.y});
+      const u32x2_t v0 = va[nt][0], v1 = va[nt][1];
+      const bf16x8_t vbf = __builtin_bit_cast(bf16x8_t, u32x4_t{v0.x & vm.x, v0.y & vm.y, v1.x & vm.z, v1.y & vm.w});
 #pragma unroll
       for (uint32_t i = 0; i < 4; ++i) o[nt][i] *= oc[i];
       o[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, vbf, o[nt], 0, 0, 0);
@@ -448,16 +468,165 @@ __global__ void __launch_bounds__(512) sdpa_combine_kernel(const float* __restri
 }
 
 // ---------------------------------------------------------------------------
+// Causal GQA attention for a prefill batch
+// ---------------------------------------------------------------------------
+// Tokens [0, n_tok) of q [n_tok, nh, 128] sit at positions pos0 + token and
+// attend to cache positions [0, pos0 + token]; the batch's own keys and values
+// are in the caches already (attn_prep over the rows runs first). One wave per
+// (kv head, TPW = 16 / G consecutive tokens): the N columns of the MFMAs are
+// (token j, query head i) = column G j + i, so each key/value block loaded
+// serves every query of the wave, and a column's scores past its token's
+// position are masked. The block math is sdpa_split_kernel's, over the whole
+// sequence (no split, no combine), with the next block's loads in flight
+// while one is computed (two register buffers in turn). Waves of the latest
+// tokens, the longest sequences, are dispatched first.
+__global__ void __launch_bounds__(64) sdpa_prefill_kernel(const uint16_t* __restrict__ q,
+                                                          const uint16_t* __restrict__ k_cache,
+                                                          const uint16_t* __restrict__ v_cache_t,
+                                                          uint16_t* __restrict__ out, uint32_t nh, uint32_t nkv,
+                                                          uint32_t max_len, uint32_t pos0, uint32_t n_tok,
+                                                          float scale_log2) {
+  const uint32_t lane = threadIdx.x, G = nh / nkv, TPW = 16u / G;
+  const uint32_t n_tb = (n_tok + TPW - 1u) / TPW;
+  const uint32_t kv = blockIdx.x % nkv, tb = (n_tb - 1u - blockIdx.x / nkv) * TPW;  // the wave's first token
+  const uint32_t col = lane & 15u, g = lane >> 4;
+  const uint32_t cj = col / G, ci = col % G;  // column: token tb + cj, query head kv G + ci
+  const bool col_ok = tb + cj < n_tok;
+  const uint32_t lim = pos0 + tb + cj + 1u;             // the column's sequence length
+  const uint32_t seq = pos0 + min(tb + TPW, n_tok);      // the wave's longest
+  bf16x8_t qb[4];
+  {
+    const uint32_t t = min(tb + cj, n_tok - 1u);
+    const uint16_t* qr = q + (static_cast<size_t>(t) * nh + kv * G + ci) * HD + 8u * g;
+#pragma unroll
+    for (uint32_t ks = 0; ks < 4; ++ks) {
+      u32x4_t v = *reinterpret_cast<const u32x4_t*>(qr + 32u * ks);
+      if (!col_ok) v = u32x4_t{0u, 0u, 0u, 0u};
+      qb[ks] = __builtin_bit_cast(bf16x8_t, v);
+    }
+  }
+  float m_run = -__builtin_huge_valf(), l_run = 0.0f;
+  f32x4_t o[8];
+#pragma unroll
+  for (uint32_t nt = 0; nt < 8; ++nt) o[nt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  const uint16_t* kb = k_cache + static_cast<size_t>(kv) * max_len * HD;
+  const uint16_t* vb = v_cache_t + static_cast<size_t>(kv) * HD * max_len;
+  const uint32_t nblk = (seq + 31u) / 32u;
+  struct Blk {
+    u32x4_t ka[2][4];
+    u32x2_t va[8][2];
+  };
+  auto load_blk = [&](uint32_t blk, Blk& B) __attribute__((always_inline)) {
+    const uint32_t t0 = 32u * blk;
+#pragma unroll
+    for (uint32_t tt = 0; tt < 2; ++tt) {
+      const uint16_t* kr = kb + static_cast<size_t>(t0 + 16u * tt + col) * HD + 8u * g;
+#pragma unroll
+      for (uint32_t ks = 0; ks < 4; ++ks) B.ka[tt][ks] = *reinterpret_cast<const u32x4_t*>(kr + 32u * ks);
+    }
+#pragma unroll
+    for (uint32_t nt = 0; nt < 8; ++nt) {
+      const uint16_t* vr = vb + static_cast<size_t>(16u * nt + col) * max_len + t0 + 4u * g;
+      B.va[nt][0] = *reinterpret_cast<const u32x2_t*>(vr);
+      B.va[nt][1] = *reinterpret_cast<const u32x2_t*>(vr + 16);
+    }
+  };
+  auto run_blk = [&](const Blk& B, uint32_t blk) __attribute__((always_inline)) {
+    const uint32_t t0 = 32u * blk;
+    f32x4_t sc[2];
+#pragma unroll
+    for (uint32_t tt = 0; tt < 2; ++tt) {
+      f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (uint32_t ks = 0; ks < 4; ++ks)
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, B.ka[tt][ks]), qb[ks], acc, 0, 0, 0);
+      sc[tt] = acc;
+    }
+    float sv[8];
+#pragma unroll
+    for (uint32_t tt = 0; tt < 2; ++tt)
+#pragma unroll
+      for (uint32_t i = 0; i < 4; ++i) {
+        const uint32_t t = t0 + 16u * tt + 4u * g + i;
+        sv[4 * tt + i] = t < lim ? sc[tt][i] * scale_log2 : -__builtin_huge_valf();
+      }
+    float bm = sv[0];
+#pragma unroll
+    for (uint32_t i = 1; i < 8; ++i) bm = fmaxf(bm, sv[i]);
+    bm = fmaxf(bm, shfl_xor_f(bm, 16));
+    bm = fmaxf(bm, shfl_xor_f(bm, 32));
+    // finite: block 0 holds position 0 of every column, so m_run is finite after it
+    const float m_new = fmaxf(m_run, bm);
+    const float corr = __builtin_amdgcn_exp2f(m_run - m_new);
+    float p[8], psum = 0.0f;
+#pragma unroll
+    for (uint32_t i = 0; i < 8; ++i) {
+      p[i] = bf16_to_f32(f32_to_bf16(__builtin_amdgcn_exp2f(sv[i] - m_new)));
+      psum += p[i];
+    }
+    l_run = l_run * corr + psum;
+    m_run = m_new;
+    float oc[4];
+#pragma unroll
+    for (uint32_t i = 0; i < 4; ++i) oc[i] = __shfl(corr, static_cast<int>(4u * g + i), 64);
+    const bf16x8_t pa = __builtin_bit_cast(
+        bf16x8_t, u32x4_t{pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]), pack_bf16x2(p[4], p[5]),
+                          pack_bf16x2(p[6], p[7])});
+    // positions at or past the wave's longest sequence read zero values (the
+    // cache there may hold anything); below it every column's P is finite
+    // (masks by select, not a branch: a branch would wait for the prefetch at its join)
+    const u32x4_t vm = value_masks(t0 + 4u * g, seq);
+#pragma unroll
+    for (uint32_t nt = 0; nt < 8; ++nt) {
+      const u32x2_t v0 = B.va[nt][0], v1 = B.va[nt][1];
+      const bf16x8_t vbf = __builtin_bit_cast(bf16x8_t, u32x4_t{v0.x & vm.x, v0.y & vm.y, v1.x & vm.z, v1.y & vm.w});
+#pragma unroll
+      for (uint32_t i = 0; i < 4; ++i) o[nt][i] *= oc[i];
+      o[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, vbf, o[nt], 0, 0, 0);
+    }
+  };
+  Blk b0, b1;
+  load_blk(0u, b0);
+  for (uint32_t blk = 0;;) {
+    load_blk(min(blk + 1u, nblk - 1u), b1);  // past the end: the last block again (unused)
+    run_blk(b0, blk);
+    if (++blk >= nblk) break;
+    load_blk(min(blk + 1u, nblk - 1u), b0);
+    run_blk(b1, blk);
+    if (++blk >= nblk) break;
+  }
+  // normalise: lane holds O[column 4 g + i][dim 16 nt + col]
+  l_run += shfl_xor_f(l_run, 16);
+  l_run += shfl_xor_f(l_run, 32);
+  float inv[4];
+#pragma unroll
+  for (uint32_t i = 0; i < 4; ++i) inv[i] = 1.0f / __shfl(l_run, static_cast<int>(4u * g + i), 64);
+#pragma unroll
+  for (uint32_t i = 0; i < 4; ++i) {
+    const uint32_t c = 4u * g + i, j = c / G, hh = c % G;
+    if (tb + j < n_tok) {
+      uint16_t* orow = out + (static_cast<size_t>(tb + j) * nh + kv * G + hh) * HD;
+#pragma unroll
+      for (uint32_t nt = 0; nt < 8; ++nt) orow[16u * nt + col] = f32_to_bf16(o[nt][i] * inv[i]);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // token step ends: embedding row of the state's token, greedy argmax
 // ---------------------------------------------------------------------------
-// out = bf16(q * s + b) of row state[1] (forward.rs:445-462), one word per thread.
+// out = bf16(q * s + b) of row state[1] (forward.rs:445-462), one word per
+// thread; with ROWS, row tokens[blockIdx.y] into out row blockIdx.y.
+template <bool ROWS>
 __global__ void __launch_bounds__(256) embed_q4_kernel(const uint32_t* __restrict__ w, const uint16_t* __restrict__ s,
                                                        const uint16_t* __restrict__ b, uint32_t hidden, uint32_t group,
                                                        uint32_t vocab, const int32_t* __restrict__ state,
                                                        uint16_t* __restrict__ out) {
   const uint32_t wi = blockIdx.x * 256u + threadIdx.x;
   if (wi >= hidden / 8u) return;
-  const uint32_t tok = min(static_cast<uint32_t>(max(state[1], 0)), vocab - 1u);
+  const int32_t tk = ROWS ? state[blockIdx.y] : state[1];
+  const uint32_t tok = min(static_cast<uint32_t>(max(tk, 0)), vocab - 1u);
+  out += ROWS ? static_cast<size_t>(blockIdx.y) * hidden : 0u;
   const uint32_t word = w[static_cast<size_t>(tok) * (hidden / 8u) + wi];
   const size_t gi = static_cast<size_t>(tok) * (hidden / group) + (8u * wi) / group;
   const float sc = bf16_to_f32(s[gi]), bi = bf16_to_f32(b[gi]);
@@ -591,8 +760,9 @@ int obs_attn_prep(obs_ctx* ctx, uint16_t* q, const uint16_t* k, const uint16_t* 
   if (!obs::aligned(q, 4) || !obs::aligned(k, 4) || !obs::aligned(v, 4) || !obs::aligned(k_cache, 4))
     return obs::set_error(ctx, OBS_E_ALIGN, "obs_attn_prep: q, k, v and the key cache must be 4-byte aligned");
   const uint32_t heads = n_heads + 2u * n_kv;
-  OBS_LAUNCH(ctx, "attn_prep", attn_prep_kernel<<<(heads + 3u) / 4u, 256, 0, ctx->stream>>>(
-                                   q, k, v, q_norm, k_norm, k_cache, v_cache_t, n_heads, n_kv, max_len, eps, theta, state));
+  OBS_LAUNCH(ctx, "attn_prep", attn_prep_kernel<false><<<(heads + 3u) / 4u, 256, 0, ctx->stream>>>(
+                                   q, k, v, q_norm, k_norm, k_cache, v_cache_t, n_heads, n_kv, max_len, eps, theta, state,
+                                   0u, 1u));
   return OBS_OK;
 }
 
@@ -633,8 +803,79 @@ int obs_embed_q4(obs_ctx* ctx, const uint32_t* w, const uint16_t* scales, const 
   if (hidden == 0 || vocab == 0 || group == 0 || group % 8u != 0 || hidden % group != 0)
     return obs::set_error(ctx, OBS_E_SHAPE, "obs_embed_q4: hidden must be a multiple of group, group of 8");
   if (!obs::aligned(out, 16)) return obs::set_error(ctx, OBS_E_ALIGN, "obs_embed_q4: out must be 16-byte aligned");
-  OBS_LAUNCH(ctx, "embed_q4", embed_q4_kernel<<<(hidden / 8u + 255u) / 256u, 256, 0, ctx->stream>>>(
+  OBS_LAUNCH(ctx, "embed_q4", embed_q4_kernel<false><<<(hidden / 8u + 255u) / 256u, 256, 0, ctx->stream>>>(
                                   w, scales, biases, hidden, group, vocab, state, out));
+  return OBS_OK;
+}
+
+int obs_embed_q4_rows(obs_ctx* ctx, const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
+                      uint32_t hidden, uint32_t group, uint32_t vocab, const int32_t* tokens, uint32_t n_tokens,
+                      uint16_t* out) {
+  if (!ctx) return OBS_E_INVALID;
+  if (!w || !scales || !biases || !tokens || !out)
+    return obs::set_error(ctx, OBS_E_INVALID, "obs_embed_q4_rows: null pointer");
+  if (hidden == 0 || vocab == 0 || group == 0 || group % 8u != 0 || hidden % group != 0 || n_tokens > 65535u)
+    return obs::set_error(ctx, OBS_E_SHAPE,
+                          "obs_embed_q4_rows: hidden must be a multiple of group, group of 8, at most 65535 tokens");
+  if (!obs::aligned(out, 16) || hidden % 8u != 0)
+    return obs::set_error(ctx, OBS_E_ALIGN, "obs_embed_q4_rows: out rows must be 16-byte aligned");
+  if (n_tokens == 0) return OBS_OK;
+  OBS_LAUNCH(ctx, "embed_q4_rows", embed_q4_kernel<true><<<dim3((hidden / 8u + 255u) / 256u, n_tokens), 256, 0,
+                                                         ctx->stream>>>(w, scales, biases, hidden, group, vocab, tokens,
+                                                                        out));
+  return OBS_OK;
+}
+
+int obs_attn_prep_rows(obs_ctx* ctx, uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* q_norm,
+                       const uint16_t* k_norm, uint16_t* k_cache, uint16_t* v_cache_t, uint32_t n_heads,
+                       uint32_t n_kv, uint32_t head_dim, uint32_t max_len, float eps, float theta, uint32_t pos0,
+                       uint32_t n_tokens) {
+  if (!ctx) return OBS_E_INVALID;
+  if (!q || !k || !v || !q_norm || !k_norm || !k_cache || !v_cache_t)
+    return obs::set_error(ctx, OBS_E_INVALID, "obs_attn_prep_rows: null pointer");
+  if (head_dim != HD || n_heads == 0 || n_kv == 0 || n_heads % n_kv != 0 || n_heads / n_kv > 16 || max_len == 0 ||
+      max_len % 32u != 0)
+    return obs::set_error(ctx, OBS_E_SHAPE,
+                          "obs_attn_prep_rows: head_dim must be 128, n_heads a multiple of n_kv with at most 16 per "
+                          "kv head, max_len a multiple of 32 (got %u, %u, %u, %u)", head_dim, n_heads, n_kv, max_len);
+  if (static_cast<uint64_t>(pos0) + n_tokens > max_len)
+    return obs::set_error(ctx, OBS_E_SHAPE, "obs_attn_prep_rows: positions %u..%u run past the cache (max_len %u)",
+                          pos0, pos0 + n_tokens, max_len);
+  if (!obs::aligned(q, 4) || !obs::aligned(k, 4) || !obs::aligned(v, 4) || !obs::aligned(k_cache, 4))
+    return obs::set_error(ctx, OBS_E_ALIGN, "obs_attn_prep_rows: q, k, v and the key cache must be 4-byte aligned");
+  if (n_tokens == 0) return OBS_OK;
+  const uint64_t waves = static_cast<uint64_t>(n_tokens) * (n_heads + 2u * n_kv);
+  if (waves > 0x3fffffffull) return obs::set_error(ctx, OBS_E_SHAPE, "obs_attn_prep_rows: too many tokens");
+  OBS_LAUNCH(ctx, "attn_prep_rows", attn_prep_kernel<true><<<static_cast<uint32_t>((waves + 3u) / 4u), 256, 0,
+                                                              ctx->stream>>>(q, k, v, q_norm, k_norm, k_cache, v_cache_t,
+                                                                             n_heads, n_kv, max_len, eps, theta, nullptr,
+                                                                             pos0, n_tokens));
+  return OBS_OK;
+}
+
+int obs_sdpa_prefill(obs_ctx* ctx, const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache_t,
+                     uint16_t* out, uint32_t n_heads, uint32_t n_kv, uint32_t head_dim, uint32_t max_len,
+                     uint32_t pos0, uint32_t n_tokens) {
+  if (!ctx) return OBS_E_INVALID;
+  if (!q || !k_cache || !v_cache_t || !out) return obs::set_error(ctx, OBS_E_INVALID, "obs_sdpa_prefill: null pointer");
+  if (head_dim != HD || n_kv == 0 || n_heads % n_kv != 0 || max_len == 0 || max_len % 32u != 0 ||
+      16u % (n_heads / n_kv) != 0)
+    return obs::set_error(ctx, OBS_E_SHAPE,
+                          "obs_sdpa_prefill: head_dim must be 128, query heads per kv head a divisor of 16, "
+                          "max_len a multiple of 32 (got %u, %u, %u, %u)", head_dim, n_heads, n_kv, max_len);
+  if (static_cast<uint64_t>(pos0) + n_tokens > max_len)
+    return obs::set_error(ctx, OBS_E_SHAPE, "obs_sdpa_prefill: positions %u..%u run past the cache (max_len %u)",
+                          pos0, pos0 + n_tokens, max_len);
+  if (!obs::aligned(q, 16) || !obs::aligned(k_cache, 16) || !obs::aligned(v_cache_t, 8))
+    return obs::set_error(ctx, OBS_E_ALIGN, "obs_sdpa_prefill: q and the key cache must be 16-byte aligned, the "
+                                            "value cache 8-byte aligned");
+  if (n_tokens == 0) return OBS_OK;
+  const uint32_t tpw = 16u / (n_heads / n_kv);
+  const uint64_t waves = static_cast<uint64_t>(n_kv) * ((n_tokens + tpw - 1u) / tpw);
+  if (waves > 0x7fffffffull) return obs::set_error(ctx, OBS_E_SHAPE, "obs_sdpa_prefill: too many tokens");
+  const float scale_log2 = 1.4426950408889634f / __builtin_sqrtf(static_cast<float>(HD));
+  OBS_LAUNCH(ctx, "sdpa_prefill", sdpa_prefill_kernel<<<static_cast<uint32_t>(waves), 64, 0, ctx->stream>>>(
+                                      q, k_cache, v_cache_t, out, n_heads, n_kv, max_len, pos0, n_tokens, scale_log2));
   return OBS_OK;
 }
 

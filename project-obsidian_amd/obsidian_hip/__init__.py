@@ -57,7 +57,7 @@ EXPORTS = (
     "obs_ckpt_open", "obs_ckpt_close", "obs_ckpt_error", "obs_ckpt_config", "obs_ckpt_tensor_info",
     "obs_ckpt_read", "obs_moe_layer_bytes", "obs_ckpt_load_moe_layer", "obs_ckpt_load_tensor",
     "obs_q4_gemv", "obs_attn_prep", "obs_sdpa_workspace", "obs_sdpa_decode", "obs_embed_q4",
-    "obs_argmax_workspace", "obs_argmax",
+    "obs_argmax_workspace", "obs_argmax", "obs_embed_q4_rows", "obs_attn_prep_rows", "obs_sdpa_prefill",
 )
 
 
@@ -167,6 +167,9 @@ def lib() -> C.CDLL:
         "obs_embed_q4": (i32, [vp, vp, vp, vp, u32, u32, u32, vp, vp]),
         "obs_argmax_workspace": (sz, []),
         "obs_argmax": (i32, [vp, vp, u32, vp, vp, sz]),
+        "obs_embed_q4_rows": (i32, [vp, vp, vp, vp, u32, u32, u32, vp, u32, vp]),
+        "obs_attn_prep_rows": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, u32, u32, u32, u32, f32, f32, u32, u32]),
+        "obs_sdpa_prefill": (i32, [vp, vp, vp, vp, vp, u32, u32, u32, u32, u32, u32]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -403,6 +406,22 @@ class ObsidianExecutor:
     def argmax(self, x, n: int, state, ws, ws_bytes: Optional[int] = None) -> None:
         ws_bytes = ws.nbytes if ws_bytes is None else ws_bytes
         self._check(lib().obs_argmax(self.ctx, _ptr(x), n, _ptr(state), _ptr(ws), ws_bytes))
+
+    # -- prefill of the layers around the MoE block (forward.rs:114-160) --
+    def embed_q4_rows(self, w, s, b, hidden: int, vocab: int, tokens, n_tokens: int, out, group: int = 64) -> None:
+        self._check(lib().obs_embed_q4_rows(self.ctx, _ptr(w), _ptr(s), _ptr(b), hidden, group, vocab, _ptr(tokens),
+                                            n_tokens, _ptr(out)))
+
+    def attn_prep_rows(self, q, k, v, q_norm, k_norm, k_cache, v_cache_t, n_heads: int, n_kv: int, head_dim: int,
+                       max_len: int, eps: float, theta: float, pos0: int, n_tokens: int) -> None:
+        self._check(lib().obs_attn_prep_rows(self.ctx, _ptr(q), _ptr(k), _ptr(v), _ptr(q_norm), _ptr(k_norm),
+                                             _ptr(k_cache), _ptr(v_cache_t), n_heads, n_kv, head_dim, max_len, eps,
+                                             theta, pos0, n_tokens))
+
+    def sdpa_prefill(self, q, k_cache, v_cache_t, out, n_heads: int, n_kv: int, head_dim: int, max_len: int,
+                     pos0: int, n_tokens: int) -> None:
+        self._check(lib().obs_sdpa_prefill(self.ctx, _ptr(q), _ptr(k_cache), _ptr(v_cache_t), _ptr(out), n_heads,
+                                           n_kv, head_dim, max_len, pos0, n_tokens))
 
     def moe_prefill_workspace(self, cfg: "MoeConfig", T: int) -> int:
         c = cfg.to_c()

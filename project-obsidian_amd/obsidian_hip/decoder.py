@@ -85,6 +85,10 @@ class Model:
         self.argmax_ws = exe.alloc(lib().obs_argmax_workspace(), np.uint8)
         self.moe_cfg = c.moe()
         self.graph: Optional[int] = None
+        self._pf: Optional[Dict] = None      # prefill buffers, grown to the largest batch
+        self.last_seq: List[int] = []        # the tokens whose keys and values the caches hold (run_turn)
+        self.last_reused = 0
+        self.last_prefilled = 0
 
     # -- the pieces of forward_layer (forward.rs:398-443) ------------------
     def forward_layer(self, il: int, ids_out=None, w_out=None) -> None:
@@ -109,11 +113,12 @@ class Model:
         g, c = self.glob, self.cfg
         self.exe.embed_q4(g["embed_w"], g["embed_s"], g["embed_b"], c.hidden, c.vocab, self.state, self.x, c.group)
 
-    def head(self) -> None:
+    def head(self, x=None) -> None:
         """forward.rs:559-566: final norm, lm_head logits (fp32), greedy token into
-        the state, position advanced."""
+        the state, position advanced. x: the hidden row (default self.x)."""
         g, c, e = self.glob, self.cfg, self.exe
-        e.q4_gemv(self.x, c.hidden, [(g["lm_w"], g["lm_s"], g["lm_b"], c.vocab, self.logits, None, None)],
+        e.q4_gemv(self.x if x is None else x, c.hidden,
+                  [(g["lm_w"], g["lm_s"], g["lm_b"], c.vocab, self.logits, None, None)],
                   norm_w=g["final_norm"], eps=c.rms_eps)  # final RMSNorm (forward.rs:560) fused
         e.argmax(self.logits, c.vocab, self.state, self.argmax_ws)
 
@@ -175,6 +180,126 @@ class Model:
                 self.step()
             out.append(self.read_state()[1])
         return out
+
+    # -- prefill (forward.rs:114-261) ------------------------------------------
+    def _prefill_buffers(self, T: int) -> Dict:
+        c, e = self.cfg, self.exe
+        if self._pf is None or self._pf["T"] < T:
+            self._pf = None  # release the smaller set first
+            qd, kvd = c.n_heads * c.head_dim, c.n_kv * c.head_dim
+            self._pf = {
+                "T": T, "tokens": e.alloc(T, np.int32),
+                "x": e.alloc((T, c.hidden), np.uint16), "x2": e.alloc((T, c.hidden), np.uint16),
+                "xn": e.alloc((T, c.hidden), np.uint16), "q": e.alloc((T, qd), np.uint16),
+                "k": e.alloc((T, kvd), np.uint16), "v": e.alloc((T, kvd), np.uint16),
+                "attn": e.alloc((T, qd), np.uint16), "o": e.alloc((T, c.hidden), np.uint16),
+                "ws": e.alloc(e.moe_prefill_workspace(self.moe_cfg, T), np.uint8),
+            }
+        return self._pf
+
+    def prefill_layers(self, tokens, pos0: int, trace: Optional[list] = None):
+        """The layer loop of prefill_batched (forward.rs:134-238): embed the T
+        tokens, then per layer, for all of them at once, the input RMSNorm,
+        q/k/v as 4-bit GEMMs, q/k norm + RoPE + cache appends at pos0 + t,
+        causal attention, o as a GEMM plus the residual, and the MoE prefill
+        (post-attention norm, GPU routing and grouping, grouped GEMMs,
+        rank-order combine with the residual). Returns the buffer holding the
+        last layer's output rows [T, hidden]. trace: a list that receives, per
+        layer, host copies (input rows, rows after attention, output rows)."""
+        c, e, g = self.cfg, self.exe, self.glob
+        toks = np.ascontiguousarray(tokens, dtype=np.int32).reshape(-1)
+        T = int(toks.size)
+        if T == 0:
+            raise ValueError("empty prompt")
+        if pos0 < 0 or pos0 + T > c.max_len:
+            raise ValueError(f"context overflow: positions {pos0}..{pos0 + T} past max_len {c.max_len}")
+        B = self._prefill_buffers(T)
+        e._check(lib().obs_upload(e.ctx, B["tokens"].ptr, toks.ctypes.data, toks.nbytes))
+        qd, kvd, H = c.n_heads * c.head_dim, c.n_kv * c.head_dim, c.hidden
+        e.embed_q4_rows(g["embed_w"], g["embed_s"], g["embed_b"], H, c.vocab, B["tokens"], T, B["x"], c.group)
+        x, x2 = B["x"], B["x2"]
+        for il in range(c.n_layers):
+            L = self.layers[il]
+            kc, vc = self.caches[il]
+            if trace is not None:
+                stages = [x.download()[:T].copy()]
+            e.rmsnorm_raw(x, L["in_norm"], B["xn"], T, H, c.rms_eps)                           # :145
+            e.q4_matmul(L["q_w"], L["q_s"], L["q_b"], B["xn"], B["q"], T, H, qd, c.group)       # :146-148
+            e.q4_matmul(L["k_w"], L["k_s"], L["k_b"], B["xn"], B["k"], T, H, kvd, c.group)
+            e.q4_matmul(L["v_w"], L["v_s"], L["v_b"], B["xn"], B["v"], T, H, kvd, c.group)
+            e.attn_prep_rows(B["q"], B["k"], B["v"], L["q_norm"], L["k_norm"], kc, vc, c.n_heads, c.n_kv,
+                             c.head_dim, c.max_len, c.rms_eps, c.rope_theta, pos0, T)         # :149-153
+            e.sdpa_prefill(B["q"], kc, vc, B["attn"], c.n_heads, c.n_kv, c.head_dim, c.max_len, pos0, T)  # :155
+            e.q4_matmul(L["o_w"], L["o_s"], L["o_b"], B["attn"], B["o"], T, qd, H, c.group)    # :156
+            e.scaled_add_raw(x, B["o"], 1.0, T * H)                                             # x1 = x + o
+            if trace is not None:
+                stages.append(x.download()[:T].copy())
+            e.moe_prefill(self.moe_cfg, L["moe"], x, x2, T, residual=x, ws=B["ws"])             # :162-238
+            x, x2 = x2, x
+            if trace is not None:
+                trace.append(tuple(stages) + (x.download()[:T].copy(),))
+        return x
+
+    def prefill(self, tokens, pos0: int) -> int:
+        """prefill_batched (forward.rs:114-261): the tokens at positions
+        pos0.. through every layer, layer-major, then the final norm, lm_head
+        and greedy pick of the last one. Returns the next token; the state
+        becomes (pos0 + T, next token)."""
+        x = self.prefill_layers(tokens, pos0)
+        T = len(tokens)
+        self.set_state(pos0 + T - 1, 0)
+        self.head(x.ptr + (T - 1) * self.cfg.hidden * 2)                                         # :240-261
+        return self.read_state()[1]
+
+    def fill_kv(self, tok: int, pos: int) -> None:
+        """forward.rs:543-550: one token through every layer (its keys and values
+        into the caches) without the lm_head."""
+        self.set_state(pos, tok)
+        self.embed()
+        for il in range(self.cfg.n_layers):
+            self.forward_layer(il)
+
+    def run_turn(self, prompt, max_new: int, eos: int, batch_min: int = 24) -> List[int]:
+        """forward.rs:471-535: one turn with prefix reuse. The caches keep the
+        previous turn's tokens (last_seq); the longest common prefix with this
+        prompt is reused and only the rest is prefilled (batched from
+        batch_min tokens, token by token below), keeping at least the last
+        prompt token; then greedy decode until max_new tokens or eos."""
+        prompt = [int(t) for t in prompt]
+        if not prompt:
+            return []
+        cap = self.cfg.max_len
+        if len(prompt) + max_new > cap:  # keep the prompt's tail (forward.rs:477-482)
+            keep = min(max(cap - (max_new + 1), 0), len(prompt))
+            if keep == 0:
+                raise ValueError(f"max_new {max_new} leaves no room for the prompt in the cache ({cap})")
+            prompt = prompt[len(prompt) - keep:]
+        lcp = 0
+        while lcp < min(len(self.last_seq), len(prompt)) and self.last_seq[lcp] == prompt[lcp]:
+            lcp += 1
+        lcp = min(lcp, len(prompt) - 1)
+        suffix = prompt[lcp:]
+        if len(suffix) >= batch_min:
+            nxt = self.prefill(suffix, lcp)
+        else:
+            for i, tk in enumerate(suffix[:-1]):
+                self.fill_kv(tk, lcp + i)
+            nxt = self.run_one_token(suffix[-1], len(prompt) - 1)
+        gen = [nxt]
+        pos = len(prompt)
+        while len(gen) < max_new and nxt != eos and pos < cap:
+            self.set_state(pos, nxt)  # run_one_token as a replay of the captured step
+            self.replay(1)
+            nxt = self.read_state()[1]
+            gen.append(nxt)
+            pos += 1
+        # the tokens whose keys and values the caches hold: the last generated
+        # token was never fed (the reference records it too, forward.rs:521-523,
+        # so a next prompt that repeats it would reuse a cache slot never written)
+        self.last_seq = prompt + gen[:-1]
+        self.last_reused = lcp
+        self.last_prefilled = len(prompt) - lcp
+        return gen
 
     def close(self) -> None:
         if self.graph is not None:

@@ -524,3 +524,34 @@ def test_argmax_semantics():
         x = rng.standard_normal(1000).astype(np.float32)
         x[rng.integers(0, 1000, 5)] = x.max()
         assert O.argmax(x) == int(np.argmax(x))
+
+
+def test_prefill_layer_major_equals_token_by_token():
+    """prefill_batched's loop order (layers outside, tokens inside,
+    forward.rs:134-238) gives exactly what run_one_token per token gives
+    (tokens outside, layers inside): the same caches bit for bit and the same
+    last-token logits. A mistake in how a batch token sees the cache entries of
+    the earlier ones (position offset, a token attending past itself) breaks
+    it."""
+    H, nh, nkv, hd, E, K, I, V, ml = 256, 4, 2, 128, 4, 2, 128, 64, 16
+    cfg = {"hidden": H, "n_heads": nh, "n_kv": nkv, "head_dim": hd, "eps": 1e-6, "theta": 1e7, "top_k": K,
+           "norm_topk": True, "vocab": V}
+    lays, glob = synth.decoder_weights(11, 2, H, nh, nkv, hd, E, I, V)
+    layers = [(t, O.Layer(t, E, H, I)) for t in lays]
+    rng = np.random.default_rng(12)
+    base = [(synth.bf16_normal(rng, (nkv, ml, hd)), synth.bf16_normal(rng, (nkv, ml, hd))) for _ in lays]
+    pos0, toks = 3, [7, 1, 63, 7, 20]
+    c1 = [(k.copy(), v.copy()) for k, v in base]
+    rows, logits = O.prefill(glob, layers, toks, c1, pos0, cfg)
+    c2 = [(k.copy(), v.copy()) for k, v in base]
+    for i, t in enumerate(toks):
+        lg = O.token_logits(glob, layers, t, c2, pos0 + i, cfg)
+    assert np.array_equal(logits, lg)
+    for (k1, v1), (k2, v2), (k0, v0) in zip(c1, c2, base):
+        assert np.array_equal(k1, k2) and np.array_equal(v1, v2)
+        # only the batch's positions were written
+        keep = np.ones(ml, bool)
+        keep[pos0:pos0 + len(toks)] = False
+        assert np.array_equal(k1[:, keep], k0[:, keep]) and np.array_equal(v1[:, keep], v0[:, keep])
+        assert not np.array_equal(k1[:, pos0:pos0 + len(toks)], k0[:, pos0:pos0 + len(toks)])
+    assert rows.shape == (len(toks), H)
