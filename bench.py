@@ -234,13 +234,56 @@ def bench_decoder(torch, oh, exe, args):
     exe.profile_accumulate()
     stats = exe.profile_stats()
     exe.profile_clear()
+    kern = {n: round(1000.0 * t, 1) for n, (t, c) in sorted(stats.items(), key=lambda kv: -kv[1][0])}
+    out = {"tokens_per_s": 1000.0 / ms_tok, "ms_per_token": ms_tok, "positions": [pos0, pos1 - 1],
+           "bytes_per_token": int(nbytes), "gbs": nbytes / (ms_tok * 1e-3) / 1e9, "last_token": tok,
+           "step_kernels_us": kern}
+    if args.pf_tokens:
+        out["prefill"] = bench_decoder_prefill(exe, model, args)
     model.close()
     del keep
     torch.cuda.empty_cache()
+    return out
+
+
+def prefill_flops(c, T, pos0=0):
+    """Matrix flops of a T-token prefill of the whole decoder at positions
+    pos0..: the q/k/v/o projections, the router, the 8 experts' gate/up/down
+    per token, causal attention (QK and PV over each token's positions) and
+    the last token's lm_head."""
+    qd, kvd = c.n_heads * c.head_dim, c.n_kv * c.head_dim
+    proj = 2 * T * c.hidden * (qd + 2 * kvd) + 2 * T * qd * c.hidden
+    moe = 2 * T * c.n_exp * c.hidden + 2 * T * c.top_k * 3 * c.hidden * c.inter
+    attn = 2 * 2 * c.n_heads * c.head_dim * sum(pos0 + t + 1 for t in range(T))
+    return c.n_layers * (proj + moe + attn) + 2 * c.vocab * c.hidden
+
+
+def bench_decoder_prefill(exe, model, args):
+    """Model.prefill of a T-token prompt at position 0 through every layer
+    (prefill_batched, forward.rs:114-261): one untimed, then timed repetitions
+    between HIP events; then a per-kernel breakdown of one more from event
+    pairs."""
+    import numpy as np
+    T, reps = args.pf_tokens, args.pf_reps
+    rng = np.random.default_rng(77)
+    toks = rng.integers(0, model.cfg.vocab, T).astype(np.int32)
+    model.prefill(toks, 0)
+    exe.sync()
+    exe.timer_start()
+    for _ in range(reps):
+        model.prefill(toks, 0)
+    ms = exe.timer_stop() / reps
+    exe.profile_clear()
+    exe.profile_enable(True)
+    model.prefill(toks, 0)
+    exe.profile_enable(False)
+    exe.profile_accumulate()
+    stats = exe.profile_stats()
+    exe.profile_clear()
+    flops = prefill_flops(model.cfg, T)
     kern = {n: round(1000.0 * t, 1) for n, (t, c) in sorted(stats.items(), key=lambda kv: -kv[1][0])}
-    return {"tokens_per_s": 1000.0 / ms_tok, "ms_per_token": ms_tok, "positions": [pos0, pos1 - 1],
-            "bytes_per_token": int(nbytes), "gbs": nbytes / (ms_tok * 1e-3) / 1e9, "last_token": tok,
-            "step_kernels_us": kern}
+    return {"T": T, "ms": ms, "tokens_per_s": T / (ms * 1e-3), "tflops": flops / (ms * 1e-3) / 1e12,
+            "flops": flops, "kernels_us": kern}
 
 
 def measured_traffic(kernel):
@@ -371,6 +414,8 @@ def main():
     ap.add_argument("--no-decoder", action="store_true")
     ap.add_argument("--dec-steps", type=int, default=32)
     ap.add_argument("--dec-warmup", type=int, default=4)
+    ap.add_argument("--pf-tokens", type=int, default=2048, help="decoder prefill prompt length (0: skip)")
+    ap.add_argument("--pf-reps", type=int, default=3)
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain MIB-MiB device copy (counter calibration) and exit")
     args = ap.parse_args()
@@ -427,7 +472,14 @@ def main():
             "tokens_per_s": round(dcd["tokens_per_s"], 1), "ms_per_token": round(dcd["ms_per_token"], 4),
             "bytes_per_token": dcd["bytes_per_token"], "gbs": round(dcd["gbs"], 1),
             "frac_of_hbm_peak": round(dcd["gbs"] / HBM_PEAK_GBS, 4),
-            "step_kernels_us": dcd["step_kernels_us"]},
+            "step_kernels_us": dcd["step_kernels_us"],
+            "prefill": None if dcd.get("prefill") is None else {
+                "workload": f"prefill of a {dcd['prefill']['T']}-token prompt at position 0 through "
+                            f"{args.layers} layers, last-token lm_head + greedy pick",
+                "tokens_per_s": round(dcd["prefill"]["tokens_per_s"], 1), "ms": round(dcd["prefill"]["ms"], 3),
+                "tflops": round(dcd["prefill"]["tflops"], 1),
+                "frac_of_bf16_peak": round(dcd["prefill"]["tflops"] / BF16_PEAK_TFLOPS, 4),
+                "kernels_us": dcd["prefill"]["kernels_us"]}},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))

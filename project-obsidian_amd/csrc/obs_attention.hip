@@ -193,20 +193,22 @@ __global__ void __launch_bounds__(256) q4_gemv_kernel(const uint16_t* __restrict
 // ---------------------------------------------------------------------------
 // q/k RMSNorm + NeoX RoPE + cache append, one launch
 // ---------------------------------------------------------------------------
-// One wave per (token, head); lane l owns columns 2l, 2l+1 (the RMSNorm lane
-// order of obs_rmsnorm at dim 128). Heads [0, nh): query heads, normed and
-// rotated in place; [nh, nh+nkv): key heads, normed, rotated, written to the
-// key cache at pos; [nh+nkv, nh+2nkv): value heads, written to the transposed
-// value cache. RoPE pairs column i with i + 64, held by lane l ^ 32.
-// Frequencies, cosines and sines follow the oracle's restatement:
-// f = fl32(theta^(-2i/128)) and cos, sin of the fp32 angle fl32(pos * f), each
-// evaluated in double and rounded once; r0 = x0 c - x1 s, r1 = x1 c + x0 s
-// with rounded products.
-// ROWS = false (decode): one token at pos = state[0], read with a vector load
-// issued after the head's loads (a scalar load would be waited for together
-// with the kernel arguments, before any other load). ROWS = true (prefill):
-// tokens [0, n_tok) of q [n_tok, nh, 128], k, v [n_tok, nkv, 128] at
-// positions pos0 + token.
+// Lane l owns columns 2l, 2l+1 of a head (the RMSNorm lane order of
+// obs_rmsnorm at dim 128). Heads [0, nh): query heads, normed and rotated in
+// place; [nh, nh+nkv): key heads, normed, rotated, written to the key cache at
+// pos; [nh+nkv, nh+2nkv): value heads, written to the transposed value cache.
+// RoPE pairs column i with i + 64, held by lane l ^ 32. Frequencies, cosines
+// and sines follow the oracle's restatement: f = fl32(theta^(-2i/128)) and
+// cos, sin of the fp32 angle fl32(pos * f), each evaluated in double and
+// rounded once; r0 = x0 c - x1 s, r1 = x1 c + x0 s with rounded products. The
+// cosines and sines depend on the position and the lane only, so a wave
+// evaluates them once and applies them to every head it owns.
+// ROWS = false (decode): one token at pos = state[0], one wave per head; the
+// position is read with a vector load issued after the head's loads (a scalar
+// load would be waited for together with the kernel arguments, before any
+// other load). ROWS = true (prefill): one workgroup per token of q [n_tok, nh,
+// 128], k, v [n_tok, nkv, 128] at position pos0 + token; wave w owns heads
+// w, w + 4, ...
 template <bool ROWS>
 __global__ void __launch_bounds__(256) attn_prep_kernel(uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
                                                         const uint16_t* __restrict__ v,
@@ -216,21 +218,24 @@ __global__ void __launch_bounds__(256) attn_prep_kernel(uint16_t* __restrict__ q
                                                         uint32_t nh, uint32_t nkv, uint32_t max_len, float eps,
                                                         float theta, const int32_t* __restrict__ state, uint32_t pos0,
                                                         uint32_t n_tok) {
-  const uint32_t lane = threadIdx.x & 63u, wave_g = blockIdx.x * 4u + (threadIdx.x >> 6);
+  const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
   const uint32_t heads = nh + 2u * nkv;
-  const uint32_t tok = ROWS ? wave_g / heads : 0u, head = ROWS ? wave_g % heads : wave_g;
-  if (tok >= n_tok || head >= heads) return;  // wave-uniform
+  const uint32_t tok = ROWS ? blockIdx.x : 0u;
+  const uint32_t h_first = ROWS ? wave : blockIdx.x * 4u + wave, h_step = ROWS ? 4u : heads;
+  if (tok >= n_tok || h_first >= heads) return;  // wave-uniform
   q += static_cast<size_t>(tok) * nh * HD;
   k += static_cast<size_t>(tok) * nkv * HD;
   v += static_cast<size_t>(tok) * nkv * HD;
   const uint32_t c0 = 2u * lane;
-  const bool is_v = head >= nh + nkv, is_q = head < nh;
-  const uint32_t hk = is_q ? head : (is_v ? head - nh - nkv : head - nh);
-  // the head's values and norm weights (a value head loads its row twice; unused)
-  const uint16_t* src = is_q ? q + hk * HD : (is_v ? v + hk * HD : k + hk * HD);
-  const uint16_t* wn = is_q ? q_norm : k_norm;
-  const uint32_t xv = *reinterpret_cast<const uint32_t*>(src + c0);
-  const uint32_t wv = *reinterpret_cast<const uint32_t*>(wn + c0);
+  auto head_src = [&](uint32_t head) __attribute__((always_inline)) {
+    const bool is_v = head >= nh + nkv, is_q = head < nh;
+    const uint32_t hk = is_q ? head : (is_v ? head - nh - nkv : head - nh);
+    return is_q ? q + hk * HD : (is_v ? v + hk * HD : k + hk * HD);
+  };
+  // the first head's values and both norm weights, before the position
+  const uint32_t xv0 = *reinterpret_cast<const uint32_t*>(head_src(h_first) + c0);
+  const uint32_t wq = *reinterpret_cast<const uint32_t*>(q_norm + c0);
+  const uint32_t wk = *reinterpret_cast<const uint32_t*>(k_norm + c0);
   int32_t pos_i;
   if (ROWS) {
     pos_i = static_cast<int32_t>(pos0 + tok);
@@ -241,45 +246,50 @@ __global__ void __launch_bounds__(256) attn_prep_kernel(uint16_t* __restrict__ q
   }
   const uint32_t pos = static_cast<uint32_t>(pos_i);
   const bool pos_ok = pos_i >= 0 && pos < max_len;
-  if (is_v) {  // value head: transposed cache column pos
-    if (pos_ok) {
-      uint16_t* dst = v_cache_t + (static_cast<size_t>(hk) * HD + c0) * max_len + pos;
-      dst[0] = static_cast<uint16_t>(xv & 0xffffu);
-      dst[max_len] = static_cast<uint16_t>(xv >> 16);
-    }
-    return;
-  }
-  const float x0 = bf16lo(xv), x1 = bf16hi(xv);
-  float ss = __builtin_fmaf(x0, x0, 0.0f);
-  ss = __builtin_fmaf(x1, x1, ss);
-  const float inv = 1.0f / __builtin_sqrtf(wave_sum_asc(ss) / static_cast<float>(HD) + eps);
-  // the normed values, rounded to bf16 as the stored q/k would be
-  const float n0 = bf16_to_f32(f32_to_bf16((x0 * inv) * bf16lo(wv)));
-  const float n1 = bf16_to_f32(f32_to_bf16((x1 * inv) * bf16hi(wv)));
-  const float p0 = __shfl_xor(n0, 32, 64), p1 = __shfl_xor(n1, 32, 64);  // columns c0 +- 64
-  const bool first = lane < 32u;
-  float r[2];
+  float cs[2], sn[2];
 #pragma unroll
   for (uint32_t j = 0; j < 2; ++j) {
     const uint32_t i = (c0 + j) & 63u;  // pair index
     const float f = static_cast<float>(pow(static_cast<double>(theta), -2.0 * static_cast<double>(i) / 128.0));
     const float angle = static_cast<float>(pos) * f;
-    const float c = static_cast<float>(cos(static_cast<double>(angle)));
-    const float s = static_cast<float>(sin(static_cast<double>(angle)));
-    const float own = j ? n1 : n0, other = j ? p1 : p0;
-    if (first) {  // own = x0 (column i), other = x1 (column i + 64)
-      const float a = own * c, b = other * s;
-      r[j] = a - b;
-    } else {      // own = x1, other = x0
-      const float a = own * c, b = other * s;
-      r[j] = a + b;
-    }
+    cs[j] = static_cast<float>(cos(static_cast<double>(angle)));
+    sn[j] = static_cast<float>(sin(static_cast<double>(angle)));
   }
-  const uint32_t out = pack_bf16x2(r[0], r[1]);
-  if (is_q) {
-    *reinterpret_cast<uint32_t*>(q + hk * HD + c0) = out;
-  } else if (pos_ok) {
-    *reinterpret_cast<uint32_t*>(k_cache + (static_cast<size_t>(hk) * max_len + pos) * HD + c0) = out;
+  const bool first = lane < 32u;
+  for (uint32_t head = h_first; head < heads; head += h_step) {
+    const uint32_t xv = head == h_first ? xv0 : *reinterpret_cast<const uint32_t*>(head_src(head) + c0);
+    const bool is_v = head >= nh + nkv, is_q = head < nh;
+    const uint32_t hk = is_q ? head : (is_v ? head - nh - nkv : head - nh);
+    if (is_v) {  // value head: transposed cache column pos
+      if (pos_ok) {
+        uint16_t* dst = v_cache_t + (static_cast<size_t>(hk) * HD + c0) * max_len + pos;
+        dst[0] = static_cast<uint16_t>(xv & 0xffffu);
+        dst[max_len] = static_cast<uint16_t>(xv >> 16);
+      }
+      continue;
+    }
+    const uint32_t wv = is_q ? wq : wk;
+    const float x0 = bf16lo(xv), x1 = bf16hi(xv);
+    float ss = __builtin_fmaf(x0, x0, 0.0f);
+    ss = __builtin_fmaf(x1, x1, ss);
+    const float inv = 1.0f / __builtin_sqrtf(wave_sum_asc(ss) / static_cast<float>(HD) + eps);
+    // the normed values, rounded to bf16 as the stored q/k would be
+    const float n0 = bf16_to_f32(f32_to_bf16((x0 * inv) * bf16lo(wv)));
+    const float n1 = bf16_to_f32(f32_to_bf16((x1 * inv) * bf16hi(wv)));
+    const float p0 = __shfl_xor(n0, 32, 64), p1 = __shfl_xor(n1, 32, 64);  // columns c0 +- 64
+    float r[2];
+#pragma unroll
+    for (uint32_t j = 0; j < 2; ++j) {
+      const float own = j ? n1 : n0, other = j ? p1 : p0;
+      const float a = own * cs[j], b = other * sn[j];
+      r[j] = first ? a - b : a + b;  // first: own = x0 (column i), other = x1 (column i + 64)
+    }
+    const uint32_t out = pack_bf16x2(r[0], r[1]);
+    if (is_q) {
+      *reinterpret_cast<uint32_t*>(q + hk * HD + c0) = out;
+    } else if (pos_ok) {
+      *reinterpret_cast<uint32_t*>(k_cache + (static_cast<size_t>(hk) * max_len + pos) * HD + c0) = out;
+    }
   }
 }
 
@@ -400,12 +410,20 @@ __global__ void __launch_bounds__(64) sdpa_split_kernel(const uint16_t* __restri
         bf16x8_t, u32x4_t{pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]), pack_bf16x2(p[4], p[5]),
                           pack_bf16x2(p[6], p[7])});
     // values of the same positions: dim 16 nt + col, positions t0 + 4 g + i and t0 + 16 + 4 g + i
-    // masked positions read zero values (by select: a branch waits for loads at its join)
-    const u32x4_t vm = value_masks(t0 + 4u * g, seq);
+    // masked positions read zero values; only the last block needs the masks,
+    // so they are applied under a (uniform) branch: here every load of the
+    // block has been waited for already, and the branch-free form measured
+    // slower
+    const bool tail = t0 + 32u > seq;
 #pragma unroll
     for (uint32_t nt = 0; nt < 8; ++nt) {
-      const u32x2_t v0 = va[nt][0], v1 = va[nt][1];
-      const bf16x8_t vbf = __builtin_bit_cast(bf16x8_t, u32x4_t{v0.x & vm.x, v0.y & vm.y, v1.x & vm.z, v1.y & vm.w});
+      u32x2_t v0 = va[nt][0], v1 = va[nt][1];
+      if (tail) {
+        const u32x4_t vm = value_masks(t0 + 4u * g, seq);
+        v0 = u32x2_t{v0.x & vm.x, v0.y & vm.y};
+        v1 = u32x2_t{v1.x & vm.z, v1.y & vm.w};
+      }
+      const bf16x8_t vbf = __builtin_bit_cast(bf16x8_t, u32x4_t{v0.x, v0.y, v1.x, v1.y});
 #pragma unroll
       for (uint32_t i = 0; i < 4; ++i) o[nt][i] *= oc[i];
       o[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, vbf, o[nt], 0, 0, 0);
@@ -472,142 +490,171 @@ __global__ void __launch_bounds__(512) sdpa_combine_kernel(const float* __restri
 // ---------------------------------------------------------------------------
 // Tokens [0, n_tok) of q [n_tok, nh, 128] sit at positions pos0 + token and
 // attend to cache positions [0, pos0 + token]; the batch's own keys and values
-// are in the caches already (attn_prep over the rows runs first). One wave per
-// (kv head, TPW = 16 / G consecutive tokens): the N columns of the MFMAs are
-// (token j, query head i) = column G j + i, so each key/value block loaded
-// serves every query of the wave, and a column's scores past its token's
-// position are masked. The block math is sdpa_split_kernel's, over the whole
-// sequence (no split, no combine), with the next block's loads in flight
-// while one is computed (two register buffers in turn). Waves of the latest
-// tokens, the longest sequences, are dispatched first.
-__global__ void __launch_bounds__(64) sdpa_prefill_kernel(const uint16_t* __restrict__ q,
-                                                          const uint16_t* __restrict__ k_cache,
-                                                          const uint16_t* __restrict__ v_cache_t,
-                                                          uint16_t* __restrict__ out, uint32_t nh, uint32_t nkv,
-                                                          uint32_t max_len, uint32_t pos0, uint32_t n_tok,
-                                                          float scale_log2) {
-  const uint32_t lane = threadIdx.x, G = nh / nkv, TPW = 16u / G;
-  const uint32_t n_tb = (n_tok + TPW - 1u) / TPW;
-  const uint32_t kv = blockIdx.x % nkv, tb = (n_tb - 1u - blockIdx.x / nkv) * TPW;  // the wave's first token
+// are in the caches already (attn_prep over the rows runs first).
+// A workgroup (4 waves) serves one kv head and 8 column groups of 16 MFMA
+// columns, a column being (token, query head) = TPG = 16 / G tokens x the
+// G query heads of the kv head; wave w owns groups 2w and 2w + 1. Per
+// 32-position block the workgroup stages the keys [32][128] and the
+// transposed values [128][32] in LDS once (rows padded against bank
+// conflicts), and every wave runs sdpa_split_kernel's block math on both of
+// its groups from there, so each key/value byte leaves L2 once per 8 TPG
+// tokens instead of once per TPG. The next block's loads are in flight while
+// a block is computed (registers, then the other LDS buffer). A column's
+// scores past its token's position are masked; values at or past the
+// workgroup's longest sequence read as zero. Workgroups of the latest tokens,
+// the longest sequences, are dispatched first.
+constexpr uint32_t PF_KROW = HD + 8u;  // padded key row (bf16): 272 bytes
+constexpr uint32_t PF_VROW = 32u + 4u; // padded transposed value row (bf16): 72 bytes
+constexpr uint32_t PF_BUF = 32u * PF_KROW + HD * PF_VROW;  // bf16 elements per staged block
+
+__global__ void __launch_bounds__(256, 2) sdpa_prefill_kernel(const uint16_t* __restrict__ q,
+                                                             const uint16_t* __restrict__ k_cache,
+                                                             const uint16_t* __restrict__ v_cache_t,
+                                                             uint16_t* __restrict__ out, uint32_t nh, uint32_t nkv,
+                                                             uint32_t max_len, uint32_t pos0, uint32_t n_tok,
+                                                             float scale_log2) {
+  __shared__ __attribute__((aligned(16))) uint16_t s_blk[2][PF_BUF];
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  const uint32_t G = nh / nkv, TPG = 16u / G, TPWG = 8u * TPG;
+  const uint32_t n_wg_tok = (n_tok + TPWG - 1u) / TPWG;
+  const uint32_t kv = blockIdx.x % nkv, tb = (n_wg_tok - 1u - blockIdx.x / nkv) * TPWG;  // first token
   const uint32_t col = lane & 15u, g = lane >> 4;
-  const uint32_t cj = col / G, ci = col % G;  // column: token tb + cj, query head kv G + ci
-  const bool col_ok = tb + cj < n_tok;
-  const uint32_t lim = pos0 + tb + cj + 1u;             // the column's sequence length
-  const uint32_t seq = pos0 + min(tb + TPW, n_tok);      // the wave's longest
-  bf16x8_t qb[4];
-  {
-    const uint32_t t = min(tb + cj, n_tok - 1u);
-    const uint16_t* qr = q + (static_cast<size_t>(t) * nh + kv * G + ci) * HD + 8u * g;
+  const uint32_t cj = col / G, ci = col % G;
+  const uint32_t seq = pos0 + min(tb + TPWG, n_tok);  // the workgroup's longest sequence
+  const uint32_t nblk = (seq + 31u) / 32u;
+  // the wave's two column groups: query slices (B operand), limits, state
+  bf16x8_t qb[2][4];
+  uint32_t lim[2];
+#pragma unroll
+  for (uint32_t cg = 0; cg < 2; ++cg) {
+    const uint32_t t = tb + (2u * wave + cg) * TPG + cj;
+    lim[cg] = pos0 + t + 1u;
+    const uint16_t* qr = q + (static_cast<size_t>(min(t, n_tok - 1u)) * nh + kv * G + ci) * HD + 8u * g;
 #pragma unroll
     for (uint32_t ks = 0; ks < 4; ++ks) {
       u32x4_t v = *reinterpret_cast<const u32x4_t*>(qr + 32u * ks);
-      if (!col_ok) v = u32x4_t{0u, 0u, 0u, 0u};
-      qb[ks] = __builtin_bit_cast(bf16x8_t, v);
+      if (t >= n_tok) v = u32x4_t{0u, 0u, 0u, 0u};
+      qb[cg][ks] = __builtin_bit_cast(bf16x8_t, v);
     }
   }
-  float m_run = -__builtin_huge_valf(), l_run = 0.0f;
-  f32x4_t o[8];
+  float m_run[2] = {-__builtin_huge_valf(), -__builtin_huge_valf()}, l_run[2] = {0.0f, 0.0f};
+  f32x4_t o[2][8];
 #pragma unroll
-  for (uint32_t nt = 0; nt < 8; ++nt) o[nt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  for (uint32_t cg = 0; cg < 2; ++cg)
+#pragma unroll
+    for (uint32_t nt = 0; nt < 8; ++nt) o[cg][nt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
   const uint16_t* kb = k_cache + static_cast<size_t>(kv) * max_len * HD;
   const uint16_t* vb = v_cache_t + static_cast<size_t>(kv) * HD * max_len;
-  const uint32_t nblk = (seq + 31u) / 32u;
-  struct Blk {
-    u32x4_t ka[2][4];
-    u32x2_t va[8][2];
-  };
-  auto load_blk = [&](uint32_t blk, Blk& B) __attribute__((always_inline)) {
+  // staging: thread t moves 16-byte chunks t and t + 256 of the key block
+  // (row c / 16, column 8 (c % 16)) and of the transposed value block (row
+  // c / 4, column 8 (c % 4))
+  auto load_blk = [&](uint32_t blk, u32x4_t* r) __attribute__((always_inline)) {
     const uint32_t t0 = 32u * blk;
 #pragma unroll
-    for (uint32_t tt = 0; tt < 2; ++tt) {
-      const uint16_t* kr = kb + static_cast<size_t>(t0 + 16u * tt + col) * HD + 8u * g;
-#pragma unroll
-      for (uint32_t ks = 0; ks < 4; ++ks) B.ka[tt][ks] = *reinterpret_cast<const u32x4_t*>(kr + 32u * ks);
-    }
-#pragma unroll
-    for (uint32_t nt = 0; nt < 8; ++nt) {
-      const uint16_t* vr = vb + static_cast<size_t>(16u * nt + col) * max_len + t0 + 4u * g;
-      B.va[nt][0] = *reinterpret_cast<const u32x2_t*>(vr);
-      B.va[nt][1] = *reinterpret_cast<const u32x2_t*>(vr + 16);
+    for (uint32_t h = 0; h < 2; ++h) {
+      const uint32_t c = tid + 256u * h;
+      r[h] = *reinterpret_cast<const u32x4_t*>(kb + static_cast<size_t>(t0 + c / 16u) * HD + 8u * (c % 16u));
+      r[2 + h] = *reinterpret_cast<const u32x4_t*>(vb + static_cast<size_t>(c / 4u) * max_len + t0 + 8u * (c % 4u));
     }
   };
-  auto run_blk = [&](const Blk& B, uint32_t blk) __attribute__((always_inline)) {
+  auto store_blk = [&](uint32_t buf, const u32x4_t* r) __attribute__((always_inline)) {
+#pragma unroll
+    for (uint32_t h = 0; h < 2; ++h) {
+      const uint32_t c = tid + 256u * h;
+      *reinterpret_cast<u32x4_t*>(&s_blk[buf][(c / 16u) * PF_KROW + 8u * (c % 16u)]) = r[h];
+      // a transposed value row of 32 positions is 4 chunks; rows are 72 bytes, so
+      // each chunk is stored as two 8-byte halves (8-byte alignment)
+      uint16_t* vr = &s_blk[buf][32u * PF_KROW + (c / 4u) * PF_VROW + 8u * (c % 4u)];
+      *reinterpret_cast<u32x2_t*>(vr) = u32x2_t{r[2 + h].x, r[2 + h].y};
+      *reinterpret_cast<u32x2_t*>(vr + 4) = u32x2_t{r[2 + h].z, r[2 + h].w};
+    }
+  };
+  auto run_blk = [&](uint32_t buf, uint32_t blk) __attribute__((always_inline)) {
     const uint32_t t0 = 32u * blk;
-    f32x4_t sc[2];
-#pragma unroll
-    for (uint32_t tt = 0; tt < 2; ++tt) {
-      f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-      for (uint32_t ks = 0; ks < 4; ++ks)
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, B.ka[tt][ks]), qb[ks], acc, 0, 0, 0);
-      sc[tt] = acc;
-    }
-    float sv[8];
-#pragma unroll
-    for (uint32_t tt = 0; tt < 2; ++tt)
-#pragma unroll
-      for (uint32_t i = 0; i < 4; ++i) {
-        const uint32_t t = t0 + 16u * tt + 4u * g + i;
-        sv[4 * tt + i] = t < lim ? sc[tt][i] * scale_log2 : -__builtin_huge_valf();
-      }
-    float bm = sv[0];
-#pragma unroll
-    for (uint32_t i = 1; i < 8; ++i) bm = fmaxf(bm, sv[i]);
-    bm = fmaxf(bm, shfl_xor_f(bm, 16));
-    bm = fmaxf(bm, shfl_xor_f(bm, 32));
-    // finite: block 0 holds position 0 of every column, so m_run is finite after it
-    const float m_new = fmaxf(m_run, bm);
-    const float corr = __builtin_amdgcn_exp2f(m_run - m_new);
-    float p[8], psum = 0.0f;
-#pragma unroll
-    for (uint32_t i = 0; i < 8; ++i) {
-      p[i] = bf16_to_f32(f32_to_bf16(__builtin_amdgcn_exp2f(sv[i] - m_new)));
-      psum += p[i];
-    }
-    l_run = l_run * corr + psum;
-    m_run = m_new;
-    float oc[4];
-#pragma unroll
-    for (uint32_t i = 0; i < 4; ++i) oc[i] = __shfl(corr, static_cast<int>(4u * g + i), 64);
-    const bf16x8_t pa = __builtin_bit_cast(
-        bf16x8_t, u32x4_t{pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]), pack_bf16x2(p[4], p[5]),
-                          pack_bf16x2(p[6], p[7])});
-    // positions at or past the wave's longest sequence read zero values (the
-    // cache there may hold anything); below it every column's P is finite
-    // (masks by select, not a branch: a branch would wait for the prefetch at its join)
+    const uint16_t* sk = s_blk[buf];
+    const uint16_t* sv = s_blk[buf] + 32u * PF_KROW;
     const u32x4_t vm = value_masks(t0 + 4u * g, seq);
 #pragma unroll
-    for (uint32_t nt = 0; nt < 8; ++nt) {
-      const u32x2_t v0 = B.va[nt][0], v1 = B.va[nt][1];
-      const bf16x8_t vbf = __builtin_bit_cast(bf16x8_t, u32x4_t{v0.x & vm.x, v0.y & vm.y, v1.x & vm.z, v1.y & vm.w});
+    for (uint32_t cg = 0; cg < 2; ++cg) {
+      f32x4_t sc[2];
 #pragma unroll
-      for (uint32_t i = 0; i < 4; ++i) o[nt][i] *= oc[i];
-      o[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, vbf, o[nt], 0, 0, 0);
+      for (uint32_t tt = 0; tt < 2; ++tt) {
+        f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        const uint16_t* kr = sk + (16u * tt + col) * PF_KROW + 8u * g;
+#pragma unroll
+        for (uint32_t ks = 0; ks < 4; ++ks)
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4_t*>(kr + 32u * ks)), qb[cg][ks], acc, 0, 0, 0);
+        sc[tt] = acc;
+      }
+      float svl[8];
+#pragma unroll
+      for (uint32_t tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (uint32_t i = 0; i < 4; ++i) {
+          const uint32_t t = t0 + 16u * tt + 4u * g + i;
+          svl[4 * tt + i] = t < lim[cg] ? sc[tt][i] * scale_log2 : -__builtin_huge_valf();
+        }
+      float bm = svl[0];
+#pragma unroll
+      for (uint32_t i = 1; i < 8; ++i) bm = fmaxf(bm, svl[i]);
+      bm = fmaxf(bm, shfl_xor_f(bm, 16));
+      bm = fmaxf(bm, shfl_xor_f(bm, 32));
+      // finite: block 0 holds position 0 of every column, so m_run is finite after it
+      const float m_new = fmaxf(m_run[cg], bm);
+      const float corr = __builtin_amdgcn_exp2f(m_run[cg] - m_new);
+      float p[8], psum = 0.0f;
+#pragma unroll
+      for (uint32_t i = 0; i < 8; ++i) {
+        p[i] = bf16_to_f32(f32_to_bf16(__builtin_amdgcn_exp2f(svl[i] - m_new)));
+        psum += p[i];
+      }
+      l_run[cg] = l_run[cg] * corr + psum;
+      m_run[cg] = m_new;
+      float oc[4];
+#pragma unroll
+      for (uint32_t i = 0; i < 4; ++i) oc[i] = __shfl(corr, static_cast<int>(4u * g + i), 64);
+      const bf16x8_t pa = __builtin_bit_cast(
+          bf16x8_t, u32x4_t{pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]), pack_bf16x2(p[4], p[5]),
+                            pack_bf16x2(p[6], p[7])});
+#pragma unroll
+      for (uint32_t nt = 0; nt < 8; ++nt) {
+        const uint16_t* vr = sv + (16u * nt + col) * PF_VROW + 4u * g;
+        const u32x2_t v0 = *reinterpret_cast<const u32x2_t*>(vr);
+        const u32x2_t v1 = *reinterpret_cast<const u32x2_t*>(vr + 16);
+        const bf16x8_t vbf =
+            __builtin_bit_cast(bf16x8_t, u32x4_t{v0.x & vm.x, v0.y & vm.y, v1.x & vm.z, v1.y & vm.w});
+#pragma unroll
+        for (uint32_t i = 0; i < 4; ++i) o[cg][nt][i] *= oc[i];
+        o[cg][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, vbf, o[cg][nt], 0, 0, 0);
+      }
     }
   };
-  Blk b0, b1;
-  load_blk(0u, b0);
-  for (uint32_t blk = 0;;) {
-    load_blk(min(blk + 1u, nblk - 1u), b1);  // past the end: the last block again (unused)
-    run_blk(b0, blk);
-    if (++blk >= nblk) break;
-    load_blk(min(blk + 1u, nblk - 1u), b0);
-    run_blk(b1, blk);
-    if (++blk >= nblk) break;
+  u32x4_t stage[4];
+  load_blk(0u, stage);
+  store_blk(0u, stage);
+  __syncthreads();
+  for (uint32_t blk = 0; blk < nblk; ++blk) {
+    load_blk(min(blk + 1u, nblk - 1u), stage);  // past the end: the last block again (unused)
+    run_blk(blk & 1u, blk);
+    store_blk((blk + 1u) & 1u, stage);
+    __syncthreads();
   }
-  // normalise: lane holds O[column 4 g + i][dim 16 nt + col]
-  l_run += shfl_xor_f(l_run, 16);
-  l_run += shfl_xor_f(l_run, 32);
-  float inv[4];
+  // normalise: lane holds O[column 4 g + i][dim 16 nt + col] of each group
 #pragma unroll
-  for (uint32_t i = 0; i < 4; ++i) inv[i] = 1.0f / __shfl(l_run, static_cast<int>(4u * g + i), 64);
+  for (uint32_t cg = 0; cg < 2; ++cg) {
+    float l = l_run[cg];
+    l += shfl_xor_f(l, 16);
+    l += shfl_xor_f(l, 32);
 #pragma unroll
-  for (uint32_t i = 0; i < 4; ++i) {
-    const uint32_t c = 4u * g + i, j = c / G, hh = c % G;
-    if (tb + j < n_tok) {
-      uint16_t* orow = out + (static_cast<size_t>(tb + j) * nh + kv * G + hh) * HD;
+    for (uint32_t i = 0; i < 4; ++i) {
+      const float inv = 1.0f / __shfl(l, static_cast<int>(4u * g + i), 64);
+      const uint32_t c = 4u * g + i, t = tb + (2u * wave + cg) * TPG + c / G, hh = c % G;
+      if (t < n_tok) {
+        uint16_t* orow = out + (static_cast<size_t>(t) * nh + kv * G + hh) * HD;
 #pragma unroll
-      for (uint32_t nt = 0; nt < 8; ++nt) orow[16u * nt + col] = f32_to_bf16(o[nt][i] * inv[i]);
+        for (uint32_t nt = 0; nt < 8; ++nt) orow[16u * nt + col] = f32_to_bf16(o[cg][nt][i] * inv);
+      }
     }
   }
 }
@@ -844,9 +891,8 @@ int obs_attn_prep_rows(obs_ctx* ctx, uint16_t* q, const uint16_t* k, const uint1
   if (!obs::aligned(q, 4) || !obs::aligned(k, 4) || !obs::aligned(v, 4) || !obs::aligned(k_cache, 4))
     return obs::set_error(ctx, OBS_E_ALIGN, "obs_attn_prep_rows: q, k, v and the key cache must be 4-byte aligned");
   if (n_tokens == 0) return OBS_OK;
-  const uint64_t waves = static_cast<uint64_t>(n_tokens) * (n_heads + 2u * n_kv);
-  if (waves > 0x3fffffffull) return obs::set_error(ctx, OBS_E_SHAPE, "obs_attn_prep_rows: too many tokens");
-  OBS_LAUNCH(ctx, "attn_prep_rows", attn_prep_kernel<true><<<static_cast<uint32_t>((waves + 3u) / 4u), 256, 0,
+  if (n_tokens > 0x7fffffffu) return obs::set_error(ctx, OBS_E_SHAPE, "obs_attn_prep_rows: too many tokens");
+  OBS_LAUNCH(ctx, "attn_prep_rows", attn_prep_kernel<true><<<n_tokens, 256, 0,
                                                               ctx->stream>>>(q, k, v, q_norm, k_norm, k_cache, v_cache_t,
                                                                              n_heads, n_kv, max_len, eps, theta, nullptr,
                                                                              pos0, n_tokens));
@@ -866,15 +912,14 @@ int obs_sdpa_prefill(obs_ctx* ctx, const uint16_t* q, const uint16_t* k_cache, c
   if (static_cast<uint64_t>(pos0) + n_tokens > max_len)
     return obs::set_error(ctx, OBS_E_SHAPE, "obs_sdpa_prefill: positions %u..%u run past the cache (max_len %u)",
                           pos0, pos0 + n_tokens, max_len);
-  if (!obs::aligned(q, 16) || !obs::aligned(k_cache, 16) || !obs::aligned(v_cache_t, 8))
-    return obs::set_error(ctx, OBS_E_ALIGN, "obs_sdpa_prefill: q and the key cache must be 16-byte aligned, the "
-                                            "value cache 8-byte aligned");
+  if (!obs::aligned(q, 16) || !obs::aligned(k_cache, 16) || !obs::aligned(v_cache_t, 16))
+    return obs::set_error(ctx, OBS_E_ALIGN, "obs_sdpa_prefill: q and the caches must be 16-byte aligned");
   if (n_tokens == 0) return OBS_OK;
-  const uint32_t tpw = 16u / (n_heads / n_kv);
-  const uint64_t waves = static_cast<uint64_t>(n_kv) * ((n_tokens + tpw - 1u) / tpw);
-  if (waves > 0x7fffffffull) return obs::set_error(ctx, OBS_E_SHAPE, "obs_sdpa_prefill: too many tokens");
+  const uint32_t tpwg = 8u * (16u / (n_heads / n_kv));  // tokens per workgroup
+  const uint64_t wgs = static_cast<uint64_t>(n_kv) * ((n_tokens + tpwg - 1u) / tpwg);
+  if (wgs > 0x7fffffffull) return obs::set_error(ctx, OBS_E_SHAPE, "obs_sdpa_prefill: too many tokens");
   const float scale_log2 = 1.4426950408889634f / __builtin_sqrtf(static_cast<float>(HD));
-  OBS_LAUNCH(ctx, "sdpa_prefill", sdpa_prefill_kernel<<<static_cast<uint32_t>(waves), 64, 0, ctx->stream>>>(
+  OBS_LAUNCH(ctx, "sdpa_prefill", sdpa_prefill_kernel<<<static_cast<uint32_t>(wgs), 256, 0, ctx->stream>>>(
                                       q, k_cache, v_cache_t, out, n_heads, n_kv, max_len, pos0, n_tokens, scale_log2));
   return OBS_OK;
 }

@@ -245,9 +245,11 @@ class Model:
         pos0.. through every layer, layer-major, then the final norm, lm_head
         and greedy pick of the last one. Returns the next token; the state
         becomes (pos0 + T, next token)."""
-        x = self.prefill_layers(tokens, pos0)
         T = len(tokens)
-        self.set_state(pos0 + T - 1, 0)
+        if T == 0:
+            raise ValueError("empty prompt")
+        self.set_state(pos0 + T - 1, 0)  # the head's argmax advances it; the layers take pos0 directly
+        x = self.prefill_layers(tokens, pos0)
         self.head(x.ptr + (T - 1) * self.cfg.hidden * 2)                                         # :240-261
         return self.read_state()[1]
 
