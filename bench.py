@@ -166,9 +166,11 @@ def gpu_decoder(torch, oh, D, exe, n_layers, max_len, seed):
     qd, kvd = c.n_heads * c.head_dim, c.n_kv * c.head_dim
     for il in range(n_layers):
         t = {}
-        for name, (r, cc) in (("q", (qd, c.hidden)), ("k", (kvd, c.hidden)), ("v", (kvd, c.hidden)),
-                              ("o", (c.hidden, qd))):
-            t[name + "_w"], t[name + "_s"], t[name + "_b"] = quant(r, cc)
+        # q, k, v back to back: one matrix for the prefill GEMM, three parts for the decode mat-vec
+        qkv = quant(qd + 2 * kvd, c.hidden)
+        for name, r0, r1 in (("q", 0, qd), ("k", qd, qd + kvd), ("v", qd + kvd, qd + 2 * kvd)):
+            t[name + "_w"], t[name + "_s"], t[name + "_b"] = (a[r0:r1] for a in qkv)
+        t["o_w"], t["o_s"], t["o_b"] = quant(c.hidden, qd)
         t["in_norm"], t["post_norm"] = norm(c.hidden), norm(c.hidden)
         t["q_norm"], t["k_norm"] = norm(c.head_dim), norm(c.head_dim)
         ptrs = {k: v.data_ptr() for k, v in t.items()}

@@ -321,22 +321,25 @@ int obs_embed_q4_rows(obs_ctx* ctx, const uint32_t* w, const uint16_t* scales, c
                       uint16_t* out);
 
 /* obs_attn_prep for tokens [0, n_tokens) at positions pos0 + t (the per-token
- * q/k norm, RoPE and KV appends of forward.rs:147-153): q bf16 [n_tokens,
- * n_heads, head_dim] rotated in place, k, v bf16 [n_tokens, n_kv, head_dim]
- * appended; pos0 + n_tokens <= max_len. */
+ * q/k norm, RoPE and KV appends of forward.rs:147-153): q bf16 rows of q_ld
+ * elements holding [n_heads, head_dim], rotated in place; k, v bf16 rows of
+ * kv_ld holding [n_kv, head_dim], appended (q_ld, kv_ld even; 0 = dense rows,
+ * so q, k and v may be column ranges of one fused projection's output);
+ * pos0 + n_tokens <= max_len. */
 int obs_attn_prep_rows(obs_ctx* ctx, uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* q_norm,
                        const uint16_t* k_norm, uint16_t* k_cache, uint16_t* v_cache_t, uint32_t n_heads,
                        uint32_t n_kv, uint32_t head_dim, uint32_t max_len, float eps, float theta, uint32_t pos0,
-                       uint32_t n_tokens);
+                       uint32_t n_tokens, uint32_t q_ld, uint32_t kv_ld);
 
 /* Causal GQA attention of a prefill batch (the per-token Attention::sdpa of
  * forward.rs:155 for tokens at positions pos0 + t): token t attends to cache
  * positions [0, pos0 + t]; the batch's keys and values must be in the caches
- * (obs_attn_prep_rows first). q, out bf16 [n_tokens, n_heads, head_dim];
- * head_dim 128, query heads per kv head a divisor of 16. */
+ * (obs_attn_prep_rows first). q bf16 rows of q_ld elements (a multiple of 8;
+ * 0 = dense) holding [n_heads, head_dim]; out bf16 [n_tokens, n_heads,
+ * head_dim]; head_dim 128, query heads per kv head a divisor of 16. */
 int obs_sdpa_prefill(obs_ctx* ctx, const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache_t,
                      uint16_t* out, uint32_t n_heads, uint32_t n_kv, uint32_t head_dim, uint32_t max_len,
-                     uint32_t pos0, uint32_t n_tokens);
+                     uint32_t pos0, uint32_t n_tokens, uint32_t q_ld);
 
 /* ------------------------------------------------------------------ */
 /* Checkpoint loading: safetensors -> HBM-resident expert table        */

@@ -206,9 +206,9 @@ __global__ void __launch_bounds__(256) q4_gemv_kernel(const uint16_t* __restrict
 // ROWS = false (decode): one token at pos = state[0], one wave per head; the
 // position is read with a vector load issued after the head's loads (a scalar
 // load would be waited for together with the kernel arguments, before any
-// other load). ROWS = true (prefill): one workgroup per token of q [n_tok, nh,
-// 128], k, v [n_tok, nkv, 128] at position pos0 + token; wave w owns heads
-// w, w + 4, ...
+// other load). ROWS = true (prefill): one workgroup per token of q (rows of
+// q_ld elements holding nh x 128), k, v (rows of kv_ld holding nkv x 128) at
+// position pos0 + token; wave w owns heads w, w + 4, ...
 template <bool ROWS>
 __global__ void __launch_bounds__(256) attn_prep_kernel(uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
                                                         const uint16_t* __restrict__ v,
@@ -217,15 +217,15 @@ __global__ void __launch_bounds__(256) attn_prep_kernel(uint16_t* __restrict__ q
                                                         uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache_t,
                                                         uint32_t nh, uint32_t nkv, uint32_t max_len, float eps,
                                                         float theta, const int32_t* __restrict__ state, uint32_t pos0,
-                                                        uint32_t n_tok) {
+                                                        uint32_t n_tok, uint32_t q_ld, uint32_t kv_ld) {
   const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
   const uint32_t heads = nh + 2u * nkv;
   const uint32_t tok = ROWS ? blockIdx.x : 0u;
   const uint32_t h_first = ROWS ? wave : blockIdx.x * 4u + wave, h_step = ROWS ? 4u : heads;
   if (tok >= n_tok || h_first >= heads) return;  // wave-uniform
-  q += static_cast<size_t>(tok) * nh * HD;
-  k += static_cast<size_t>(tok) * nkv * HD;
-  v += static_cast<size_t>(tok) * nkv * HD;
+  q += static_cast<size_t>(tok) * q_ld;
+  k += static_cast<size_t>(tok) * kv_ld;
+  v += static_cast<size_t>(tok) * kv_ld;
   const uint32_t c0 = 2u * lane;
   auto head_src = [&](uint32_t head) __attribute__((always_inline)) {
     const bool is_v = head >= nh + nkv, is_q = head < nh;
@@ -367,6 +367,9 @@ __global__ void __launch_bounds__(64) sdpa_split_kernel(const uint16_t* __restri
       va[nt][0] = *reinterpret_cast<const u32x2_t*>(vr);
       va[nt][1] = *reinterpret_cast<const u32x2_t*>(vr + 16);
     }
+    // all 24 loads issued before the first wait (left alone, the scheduler
+    // interleaved waits between them and the kernel ran at half speed)
+    __builtin_amdgcn_sched_barrier(0);
     // scores of the two 16-position tiles
     f32x4_t s[2];
 #pragma unroll
@@ -488,10 +491,10 @@ __global__ void __launch_bounds__(512) sdpa_combine_kernel(const float* __restri
 // ---------------------------------------------------------------------------
 // Causal GQA attention for a prefill batch
 // ---------------------------------------------------------------------------
-// Tokens [0, n_tok) of q [n_tok, nh, 128] sit at positions pos0 + token and
-// attend to cache positions [0, pos0 + token]; the batch's own keys and values
-// are in the caches already (attn_prep over the rows runs first).
-// A workgroup (4 waves) serves one kv head and 8 column groups of 16 MFMA
+// Tokens [0, n_tok) of q (rows of q_ld elements holding nh x 128) sit at
+// positions pos0 + token and attend to cache positions [0, pos0 + token]; the
+// batch's own keys and values are in the caches already (attn_prep over the
+// rows runs first). A workgroup (4 waves) serves one kv head and 8 column groups of 16 MFMA
 // columns, a column being (token, query head) = TPG = 16 / G tokens x the
 // G query heads of the kv head; wave w owns groups 2w and 2w + 1. Per
 // 32-position block the workgroup stages the keys [32][128] and the
@@ -512,7 +515,7 @@ __global__ void __launch_bounds__(256, 2) sdpa_prefill_kernel(const uint16_t* __
                                                              const uint16_t* __restrict__ v_cache_t,
                                                              uint16_t* __restrict__ out, uint32_t nh, uint32_t nkv,
                                                              uint32_t max_len, uint32_t pos0, uint32_t n_tok,
-                                                             float scale_log2) {
+                                                             uint32_t q_ld, float scale_log2) {
   __shared__ __attribute__((aligned(16))) uint16_t s_blk[2][PF_BUF];
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   const uint32_t G = nh / nkv, TPG = 16u / G, TPWG = 8u * TPG;
@@ -529,7 +532,7 @@ __global__ void __launch_bounds__(256, 2) sdpa_prefill_kernel(const uint16_t* __
   for (uint32_t cg = 0; cg < 2; ++cg) {
     const uint32_t t = tb + (2u * wave + cg) * TPG + cj;
     lim[cg] = pos0 + t + 1u;
-    const uint16_t* qr = q + (static_cast<size_t>(min(t, n_tok - 1u)) * nh + kv * G + ci) * HD + 8u * g;
+    const uint16_t* qr = q + static_cast<size_t>(min(t, n_tok - 1u)) * q_ld + (kv * G + ci) * HD + 8u * g;
 #pragma unroll
     for (uint32_t ks = 0; ks < 4; ++ks) {
       u32x4_t v = *reinterpret_cast<const u32x4_t*>(qr + 32u * ks);
@@ -809,7 +812,7 @@ int obs_attn_prep(obs_ctx* ctx, uint16_t* q, const uint16_t* k, const uint16_t* 
   const uint32_t heads = n_heads + 2u * n_kv;
   OBS_LAUNCH(ctx, "attn_prep", attn_prep_kernel<false><<<(heads + 3u) / 4u, 256, 0, ctx->stream>>>(
                                    q, k, v, q_norm, k_norm, k_cache, v_cache_t, n_heads, n_kv, max_len, eps, theta, state,
-                                   0u, 1u));
+                                   0u, 1u, 0u, 0u));
   return OBS_OK;
 }
 
@@ -876,8 +879,10 @@ int obs_embed_q4_rows(obs_ctx* ctx, const uint32_t* w, const uint16_t* scales, c
 int obs_attn_prep_rows(obs_ctx* ctx, uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* q_norm,
                        const uint16_t* k_norm, uint16_t* k_cache, uint16_t* v_cache_t, uint32_t n_heads,
                        uint32_t n_kv, uint32_t head_dim, uint32_t max_len, float eps, float theta, uint32_t pos0,
-                       uint32_t n_tokens) {
+                       uint32_t n_tokens, uint32_t q_ld, uint32_t kv_ld) {
   if (!ctx) return OBS_E_INVALID;
+  q_ld = q_ld ? q_ld : n_heads * head_dim;
+  kv_ld = kv_ld ? kv_ld : n_kv * head_dim;
   if (!q || !k || !v || !q_norm || !k_norm || !k_cache || !v_cache_t)
     return obs::set_error(ctx, OBS_E_INVALID, "obs_attn_prep_rows: null pointer");
   if (head_dim != HD || n_heads == 0 || n_kv == 0 || n_heads % n_kv != 0 || n_heads / n_kv > 16 || max_len == 0 ||
@@ -888,6 +893,9 @@ int obs_attn_prep_rows(obs_ctx* ctx, uint16_t* q, const uint16_t* k, const uint1
   if (static_cast<uint64_t>(pos0) + n_tokens > max_len)
     return obs::set_error(ctx, OBS_E_SHAPE, "obs_attn_prep_rows: positions %u..%u run past the cache (max_len %u)",
                           pos0, pos0 + n_tokens, max_len);
+  if (q_ld < n_heads * head_dim || kv_ld < n_kv * head_dim || q_ld % 2u != 0 || kv_ld % 2u != 0)
+    return obs::set_error(ctx, OBS_E_SHAPE, "obs_attn_prep_rows: row strides %u, %u must be even and hold a row",
+                          q_ld, kv_ld);
   if (!obs::aligned(q, 4) || !obs::aligned(k, 4) || !obs::aligned(v, 4) || !obs::aligned(k_cache, 4))
     return obs::set_error(ctx, OBS_E_ALIGN, "obs_attn_prep_rows: q, k, v and the key cache must be 4-byte aligned");
   if (n_tokens == 0) return OBS_OK;
@@ -895,14 +903,15 @@ int obs_attn_prep_rows(obs_ctx* ctx, uint16_t* q, const uint16_t* k, const uint1
   OBS_LAUNCH(ctx, "attn_prep_rows", attn_prep_kernel<true><<<n_tokens, 256, 0,
                                                               ctx->stream>>>(q, k, v, q_norm, k_norm, k_cache, v_cache_t,
                                                                              n_heads, n_kv, max_len, eps, theta, nullptr,
-                                                                             pos0, n_tokens));
+                                                                             pos0, n_tokens, q_ld, kv_ld));
   return OBS_OK;
 }
 
 int obs_sdpa_prefill(obs_ctx* ctx, const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache_t,
                      uint16_t* out, uint32_t n_heads, uint32_t n_kv, uint32_t head_dim, uint32_t max_len,
-                     uint32_t pos0, uint32_t n_tokens) {
+                     uint32_t pos0, uint32_t n_tokens, uint32_t q_ld) {
   if (!ctx) return OBS_E_INVALID;
+  q_ld = q_ld ? q_ld : n_heads * head_dim;
   if (!q || !k_cache || !v_cache_t || !out) return obs::set_error(ctx, OBS_E_INVALID, "obs_sdpa_prefill: null pointer");
   if (head_dim != HD || n_kv == 0 || n_heads % n_kv != 0 || max_len == 0 || max_len % 32u != 0 ||
       16u % (n_heads / n_kv) != 0)
@@ -912,6 +921,9 @@ int obs_sdpa_prefill(obs_ctx* ctx, const uint16_t* q, const uint16_t* k_cache, c
   if (static_cast<uint64_t>(pos0) + n_tokens > max_len)
     return obs::set_error(ctx, OBS_E_SHAPE, "obs_sdpa_prefill: positions %u..%u run past the cache (max_len %u)",
                           pos0, pos0 + n_tokens, max_len);
+  if (q_ld < n_heads * head_dim || q_ld % 8u != 0)
+    return obs::set_error(ctx, OBS_E_SHAPE, "obs_sdpa_prefill: q row stride %u must be a multiple of 8 holding a row",
+                          q_ld);
   if (!obs::aligned(q, 16) || !obs::aligned(k_cache, 16) || !obs::aligned(v_cache_t, 16))
     return obs::set_error(ctx, OBS_E_ALIGN, "obs_sdpa_prefill: q and the caches must be 16-byte aligned");
   if (n_tokens == 0) return OBS_OK;
@@ -920,7 +932,8 @@ int obs_sdpa_prefill(obs_ctx* ctx, const uint16_t* q, const uint16_t* k_cache, c
   if (wgs > 0x7fffffffull) return obs::set_error(ctx, OBS_E_SHAPE, "obs_sdpa_prefill: too many tokens");
   const float scale_log2 = 1.4426950408889634f / __builtin_sqrtf(static_cast<float>(HD));
   OBS_LAUNCH(ctx, "sdpa_prefill", sdpa_prefill_kernel<<<static_cast<uint32_t>(wgs), 256, 0, ctx->stream>>>(
-                                      q, k_cache, v_cache_t, out, n_heads, n_kv, max_len, pos0, n_tokens, scale_log2));
+                                      q, k_cache, v_cache_t, out, n_heads, n_kv, max_len, pos0, n_tokens, q_ld,
+                                      scale_log2));
   return OBS_OK;
 }
 

@@ -874,8 +874,7 @@ size_t gemm_sb_bytes(uint32_t mode, uint32_t K) {
 // grid: gemm_grid() of the launch; a.work (when set) has that many entries.
 // A one-matrix GEMM whose N is a multiple of 256 runs in the wide mode: its
 // second B column set is the first one 128 rows further on.
-int launch_gemm(obs_ctx* ctx, bool swiglu, GemmArgs a, uint32_t grid) {
-  const uint32_t mode = gemm_mode(swiglu, a.N);
+int launch_gemm(obs_ctx* ctx, GemmArgs a, uint32_t grid, uint32_t mode) {
   if (mode == MODE_WIDE) {
     a.w1 = a.w0 + static_cast<size_t>(TN) * (a.K / 8u);
     a.s1 = a.s0 + static_cast<size_t>(TN) * (a.K / GK);
@@ -990,7 +989,7 @@ int obs_moe_prefill(obs_ctx* ctx, const obs_moe_config* cfg, const obs_moe_layer
   g.out = Hbuf; g.out_rows = nullptr;
   g.work = work_gu; g.work_count = work_cnt;
   g.K = H; g.N = I;
-  rc = launch_gemm(ctx, true, g, L.grid_gu);
+  rc = launch_gemm(ctx, g, L.grid_gu, MODE_SWIGLU);
   if (rc) return rc;
   GemmArgs d{};
   d.A = Hbuf; d.a_rows = nullptr; d.a_rows_total = T * k;
@@ -998,7 +997,7 @@ int obs_moe_prefill(obs_ctx* ctx, const obs_moe_config* cfg, const obs_moe_layer
   d.out = Yp; d.out_rows = row_slot;
   d.work = work_dn; d.work_count = work_cnt + 8;
   d.K = I; d.N = H;
-  rc = launch_gemm(ctx, false, d, L.grid_dn);
+  rc = launch_gemm(ctx, d, L.grid_dn, gemm_mode(false, H));
   if (rc) return rc;
   OBS_LAUNCH(ctx, "moe_combine", combine_kernel<<<T, H / 8u, 0, ctx->stream>>>(Yp, ids, weights, residual, Y, k, H, E));
   return OBS_OK;
@@ -1012,22 +1011,27 @@ int obs_q4_matmul(obs_ctx* ctx, const uint32_t* w, const uint16_t* scales, const
   if (in == 0 || in % (4u * GK) != 0 || out == 0 || out % TN != 0)
     return obs::set_error(ctx, OBS_E_SHAPE, "obs_q4_matmul: in must be a multiple of %u and out of %u (got %u, %u)",
                           4u * GK, TN, in, out);
-  if (gemm_sb_bytes(gemm_mode(false, out), in) > SB_LDS_MAX)
-    return obs::set_error(ctx, OBS_E_SHAPE, "obs_q4_matmul: in must be at most %u for out = %u (got %u)",
-                          static_cast<uint32_t>(SB_LDS_MAX / (sizeof(uint32_t) * SB_STRIDE) /
-                                                (out % (2u * TN) == 0 ? 2u : 1u)) * GK, out, in);
+  // the wide mode (256 columns per item) unless that leaves CUs idle and the
+  // 128-column mode would not
+  const uint32_t tiles = T == 0 ? 1u : (T + TM - 1) / TM;
+  uint32_t mode = gemm_mode(false, out);
+  if (mode == MODE_WIDE && (tiles * (out / (2u * TN)) < static_cast<uint32_t>(ctx->num_cus) ||
+                            gemm_sb_bytes(mode, in) > SB_LDS_MAX))
+    mode = MODE_NARROW;
+  if (gemm_sb_bytes(mode, in) > SB_LDS_MAX)
+    return obs::set_error(ctx, OBS_E_SHAPE, "obs_q4_matmul: in must be at most %u (got %u)",
+                          static_cast<uint32_t>(SB_LDS_MAX / (sizeof(uint32_t) * SB_STRIDE)) * GK, in);
   if (!obs::aligned(X, 16) || !obs::aligned(w, 16) || !obs::aligned(Y, 16))
     return obs::set_error(ctx, OBS_E_ALIGN, "obs_q4_matmul: X, w and Y must be 16-byte aligned");
   if (T == 0) return OBS_OK;
-  const uint32_t tiles = (T + TM - 1) / TM;
-  const uint32_t grid = gemm_grid(tiles, out, gemm_mode(false, out));
+  const uint32_t grid = gemm_grid(tiles, out, mode);
   GemmArgs g{};
   g.A = X; g.a_rows = nullptr; g.a_rows_total = T;
   g.w0 = w; g.s0 = scales; g.b0 = biases;
   g.out = Y; g.out_rows = nullptr;
   g.work = nullptr; g.work_count = nullptr; g.dense_rows = T;
   g.K = in; g.N = out;
-  return launch_gemm(ctx, false, g, grid);
+  return launch_gemm(ctx, g, grid, mode);
 }
 
 }  // extern "C"

@@ -24,10 +24,13 @@ using namespace obsd;
 
 constexpr int ROUTER_TOKENS_PER_WAVE = 8;
 
-// grid: x = ceil(n_exp / 4) (4 waves per block, one expert row each),
+// grid: x = ceil(n_exp / (4 EPW)) (4 waves per block, EPW expert rows each),
 //       y = ceil(T / ROUTER_TOKENS_PER_WAVE)
-// WPL = packed words per lane (in = 64 lanes * 4 cols * WPL).
-template <int WPL>
+// WPL = packed words per lane (in = 64 lanes * 4 cols * WPL). A wave keeps its
+// EPW rows dequantized in registers and streams its tokens' activations once
+// for all of them: with one row per wave every activation row was read from
+// L2 once per expert (1 GB at T = 2048), which bounded the launch.
+template <int WPL, int EPW>
 __global__ void __launch_bounds__(256) q8_gate_logits_kernel(const uint32_t* __restrict__ w8,
                                                              const uint16_t* __restrict__ s,
                                                              const uint16_t* __restrict__ b,
@@ -37,40 +40,47 @@ __global__ void __launch_bounds__(256) q8_gate_logits_kernel(const uint32_t* __r
                                                              uint32_t group) {
   constexpr int C = 4 * WPL;  // columns per lane
   const uint32_t lane = threadIdx.x & 63;
-  const uint32_t e = blockIdx.x * 4 + threadIdx.x / 64;
-  if (e >= n_exp) return;
+  const uint32_t e0 = (blockIdx.x * 4 + threadIdx.x / 64) * EPW;
+  if (e0 >= n_exp) return;
   const uint32_t words = in / 4, groups = in / group;
-  const uint32_t* wr = w8 + static_cast<uint64_t>(e) * words + lane * WPL;
-  const uint16_t* sr = s + static_cast<uint64_t>(e) * groups;
-  const uint16_t* br = b + static_cast<uint64_t>(e) * groups;
-  // dequantize this lane's C weights once (exact: byte*scale has <= 16 bits)
-  float wv[C];
+  // dequantize this lane's C weights of each row once (exact: byte*scale has <= 16 bits)
+  float wv[EPW][C];
 #pragma unroll
-  for (int j = 0; j < WPL; ++j) {
-    const uint32_t word = wr[j];
-    const uint32_t g = (lane * C + 4 * j) / group;
-    const float sc = bf16_to_f32(sr[g]), bi = bf16_to_f32(br[g]);
+  for (int r = 0; r < EPW; ++r) {
+    const uint32_t e = min(e0 + r, n_exp - 1u);  // rows past the last expert: computed, not stored
+    const uint32_t* wr = w8 + static_cast<uint64_t>(e) * words + lane * WPL;
+    const uint16_t* sr = s + static_cast<uint64_t>(e) * groups;
+    const uint16_t* br = b + static_cast<uint64_t>(e) * groups;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) wv[4 * j + q] = __builtin_fmaf(static_cast<float>((word >> (8 * q)) & 0xffu), sc, bi);
+    for (int j = 0; j < WPL; ++j) {
+      const uint32_t word = wr[j];
+      const uint32_t g = (lane * C + 4 * j) / group;
+      const float sc = bf16_to_f32(sr[g]), bi = bf16_to_f32(br[g]);
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        wv[r][4 * j + q] = __builtin_fmaf(static_cast<float>((word >> (8 * q)) & 0xffu), sc, bi);
+    }
   }
   const uint32_t t0 = blockIdx.y * ROUTER_TOKENS_PER_WAVE;
   for (uint32_t t = t0; t < t0 + ROUTER_TOKENS_PER_WAVE && t < T; ++t) {
     const uint16_t* xr = x + static_cast<uint64_t>(t) * in + lane * C;
-    float acc = 0.0f;
+    float xf[C];
 #pragma unroll
     for (int c = 0; c < C; c += 8) {
       const uint4 xv = *reinterpret_cast<const uint4*>(xr + c);
-      acc = __builtin_fmaf(wv[c + 0], bf16lo(xv.x), acc);
-      acc = __builtin_fmaf(wv[c + 1], bf16hi(xv.x), acc);
-      acc = __builtin_fmaf(wv[c + 2], bf16lo(xv.y), acc);
-      acc = __builtin_fmaf(wv[c + 3], bf16hi(xv.y), acc);
-      acc = __builtin_fmaf(wv[c + 4], bf16lo(xv.z), acc);
-      acc = __builtin_fmaf(wv[c + 5], bf16hi(xv.z), acc);
-      acc = __builtin_fmaf(wv[c + 6], bf16lo(xv.w), acc);
-      acc = __builtin_fmaf(wv[c + 7], bf16hi(xv.w), acc);
+      xf[c + 0] = bf16lo(xv.x); xf[c + 1] = bf16hi(xv.x); xf[c + 2] = bf16lo(xv.y); xf[c + 3] = bf16hi(xv.y);
+      xf[c + 4] = bf16lo(xv.z); xf[c + 5] = bf16hi(xv.z); xf[c + 6] = bf16lo(xv.w); xf[c + 7] = bf16hi(xv.w);
     }
-    acc = wave_sum_asc(acc);
-    if (lane == 0) logits[static_cast<uint64_t>(t) * n_exp + e] = acc;
+    float mine = 0.0f;  // lane r keeps row r's logit
+#pragma unroll
+    for (int r = 0; r < EPW; ++r) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int c = 0; c < C; ++c) acc = __builtin_fmaf(wv[r][c], xf[c], acc);
+      acc = wave_sum_asc(acc);
+      mine = lane == static_cast<uint32_t>(r) ? acc : mine;
+    }
+    if (lane < static_cast<uint32_t>(EPW) && e0 + lane < n_exp) logits[static_cast<uint64_t>(t) * n_exp + e0 + lane] = mine;
   }
 }
 
@@ -117,12 +127,14 @@ int check_router_shape(obs_ctx* ctx, const char* who, uint32_t in, uint32_t n_ex
 int launch_gate_logits(obs_ctx* ctx, const uint32_t* w8, const uint16_t* s, const uint16_t* b,
                        const uint16_t* x, float* logits, uint32_t T, uint32_t in, uint32_t n_exp,
                        uint32_t group) {
-  dim3 grid((n_exp + 3) / 4, (T + ROUTER_TOKENS_PER_WAVE - 1) / ROUTER_TOKENS_PER_WAVE);
+  // 4 rows per wave (2 at in = 4096, whose rows hold 64 columns per lane)
+  const uint32_t ty = (T + ROUTER_TOKENS_PER_WAVE - 1) / ROUTER_TOKENS_PER_WAVE;
+  const dim3 grid4((n_exp + 15) / 16, ty), grid2((n_exp + 7) / 8, ty);
   switch (in) {
-    case 512: OBS_LAUNCH(ctx, "q8_gate_logits", q8_gate_logits_kernel<2><<<grid, 256, 0, ctx->stream>>>(w8, s, b, x, logits, T, in, n_exp, group)); break;
-    case 1024: OBS_LAUNCH(ctx, "q8_gate_logits", q8_gate_logits_kernel<4><<<grid, 256, 0, ctx->stream>>>(w8, s, b, x, logits, T, in, n_exp, group)); break;
-    case 2048: OBS_LAUNCH(ctx, "q8_gate_logits", q8_gate_logits_kernel<8><<<grid, 256, 0, ctx->stream>>>(w8, s, b, x, logits, T, in, n_exp, group)); break;
-    default: OBS_LAUNCH(ctx, "q8_gate_logits", q8_gate_logits_kernel<16><<<grid, 256, 0, ctx->stream>>>(w8, s, b, x, logits, T, in, n_exp, group)); break;
+    case 512: OBS_LAUNCH(ctx, "q8_gate_logits", q8_gate_logits_kernel<2, 4><<<grid4, 256, 0, ctx->stream>>>(w8, s, b, x, logits, T, in, n_exp, group)); break;
+    case 1024: OBS_LAUNCH(ctx, "q8_gate_logits", q8_gate_logits_kernel<4, 4><<<grid4, 256, 0, ctx->stream>>>(w8, s, b, x, logits, T, in, n_exp, group)); break;
+    case 2048: OBS_LAUNCH(ctx, "q8_gate_logits", q8_gate_logits_kernel<8, 4><<<grid4, 256, 0, ctx->stream>>>(w8, s, b, x, logits, T, in, n_exp, group)); break;
+    default: OBS_LAUNCH(ctx, "q8_gate_logits", q8_gate_logits_kernel<16, 2><<<grid2, 256, 0, ctx->stream>>>(w8, s, b, x, logits, T, in, n_exp, group)); break;
   }
   return OBS_OK;
 }

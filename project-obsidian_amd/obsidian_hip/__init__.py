@@ -168,8 +168,9 @@ def lib() -> C.CDLL:
         "obs_argmax_workspace": (sz, []),
         "obs_argmax": (i32, [vp, vp, u32, vp, vp, sz]),
         "obs_embed_q4_rows": (i32, [vp, vp, vp, vp, u32, u32, u32, vp, u32, vp]),
-        "obs_attn_prep_rows": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, u32, u32, u32, u32, f32, f32, u32, u32]),
-        "obs_sdpa_prefill": (i32, [vp, vp, vp, vp, vp, u32, u32, u32, u32, u32, u32]),
+        "obs_attn_prep_rows": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, u32, u32, u32, u32, f32, f32, u32, u32, u32,
+                                     u32]),
+        "obs_sdpa_prefill": (i32, [vp, vp, vp, vp, vp, u32, u32, u32, u32, u32, u32, u32]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -413,15 +414,17 @@ class ObsidianExecutor:
                                             n_tokens, _ptr(out)))
 
     def attn_prep_rows(self, q, k, v, q_norm, k_norm, k_cache, v_cache_t, n_heads: int, n_kv: int, head_dim: int,
-                       max_len: int, eps: float, theta: float, pos0: int, n_tokens: int) -> None:
+                       max_len: int, eps: float, theta: float, pos0: int, n_tokens: int, q_ld: int = 0,
+                       kv_ld: int = 0) -> None:
+        """q_ld, kv_ld: row strides in elements (0: dense rows)."""
         self._check(lib().obs_attn_prep_rows(self.ctx, _ptr(q), _ptr(k), _ptr(v), _ptr(q_norm), _ptr(k_norm),
                                              _ptr(k_cache), _ptr(v_cache_t), n_heads, n_kv, head_dim, max_len, eps,
-                                             theta, pos0, n_tokens))
+                                             theta, pos0, n_tokens, q_ld, kv_ld))
 
     def sdpa_prefill(self, q, k_cache, v_cache_t, out, n_heads: int, n_kv: int, head_dim: int, max_len: int,
-                     pos0: int, n_tokens: int) -> None:
+                     pos0: int, n_tokens: int, q_ld: int = 0) -> None:
         self._check(lib().obs_sdpa_prefill(self.ctx, _ptr(q), _ptr(k_cache), _ptr(v_cache_t), _ptr(out), n_heads,
-                                           n_kv, head_dim, max_len, pos0, n_tokens))
+                                           n_kv, head_dim, max_len, pos0, n_tokens, q_ld))
 
     def moe_prefill_workspace(self, cfg: "MoeConfig", T: int) -> int:
         c = cfg.to_c()

@@ -18,7 +18,7 @@ from typing import Dict, List, Optional
 
 import numpy as np
 
-from . import DeviceBuffer, MoeConfig, MoeLayer, ObsidianExecutor, lib
+from . import DeviceBuffer, MoeConfig, MoeLayer, ObsidianExecutor, _ptr, lib
 
 
 @dataclass
@@ -193,9 +193,24 @@ class Model:
                 "xn": e.alloc((T, c.hidden), np.uint16), "q": e.alloc((T, qd), np.uint16),
                 "k": e.alloc((T, kvd), np.uint16), "v": e.alloc((T, kvd), np.uint16),
                 "attn": e.alloc((T, qd), np.uint16), "o": e.alloc((T, c.hidden), np.uint16),
+                "qkv": e.alloc((T, qd + 2 * kvd), np.uint16),
                 "ws": e.alloc(e.moe_prefill_workspace(self.moe_cfg, T), np.uint8),
             }
         return self._pf
+
+    def fused_qkv(self, il: int):
+        """(w, s, b) of layer il's q, k and v projections as one [q + k + v rows,
+        hidden] matrix when they are stored back to back (upload_weights and
+        the checkpoint layout here place them so), else None."""
+        c, L = self.cfg, self.layers[il]
+        qd, kvd, H = c.n_heads * c.head_dim, c.n_kv * c.head_dim, c.hidden
+        out = []
+        for kind, row_bytes in (("w", H // 2), ("s", H // c.group * 2), ("b", H // c.group * 2)):
+            q, k, v = (_ptr(L[f"{p}_{kind}"]) for p in "qkv")
+            if k != q + qd * row_bytes or v != k + kvd * row_bytes:
+                return None
+            out.append(q)
+        return tuple(out)
 
     def prefill_layers(self, tokens, pos0: int, trace: Optional[list] = None):
         """The layer loop of prefill_batched (forward.rs:134-238): embed the T
@@ -224,12 +239,20 @@ class Model:
             if trace is not None:
                 stages = [x.download()[:T].copy()]
             e.rmsnorm_raw(x, L["in_norm"], B["xn"], T, H, c.rms_eps)                           # :145
-            e.q4_matmul(L["q_w"], L["q_s"], L["q_b"], B["xn"], B["q"], T, H, qd, c.group)       # :146-148
-            e.q4_matmul(L["k_w"], L["k_s"], L["k_b"], B["xn"], B["k"], T, H, kvd, c.group)
-            e.q4_matmul(L["v_w"], L["v_s"], L["v_b"], B["xn"], B["v"], T, H, kvd, c.group)
-            e.attn_prep_rows(B["q"], B["k"], B["v"], L["q_norm"], L["k_norm"], kc, vc, c.n_heads, c.n_kv,
-                             c.head_dim, c.max_len, c.rms_eps, c.rope_theta, pos0, T)         # :149-153
-            e.sdpa_prefill(B["q"], kc, vc, B["attn"], c.n_heads, c.n_kv, c.head_dim, c.max_len, pos0, T)  # :155
+            fused = self.fused_qkv(il)
+            if fused is not None:  # q, k, v as one GEMM; their column ranges of each output row
+                ld = qd + 2 * kvd
+                e.q4_matmul(*fused, B["xn"], B["qkv"], T, H, ld, c.group)                     # :146-148
+                q, k, v = B["qkv"].ptr, B["qkv"].ptr + 2 * qd, B["qkv"].ptr + 2 * (qd + kvd)
+                ldq = ldkv = ld
+            else:
+                e.q4_matmul(L["q_w"], L["q_s"], L["q_b"], B["xn"], B["q"], T, H, qd, c.group)
+                e.q4_matmul(L["k_w"], L["k_s"], L["k_b"], B["xn"], B["k"], T, H, kvd, c.group)
+                e.q4_matmul(L["v_w"], L["v_s"], L["v_b"], B["xn"], B["v"], T, H, kvd, c.group)
+                q, k, v, ldq, ldkv = B["q"], B["k"], B["v"], 0, 0
+            e.attn_prep_rows(q, k, v, L["q_norm"], L["k_norm"], kc, vc, c.n_heads, c.n_kv, c.head_dim,
+                             c.max_len, c.rms_eps, c.rope_theta, pos0, T, ldq, ldkv)            # :149-153
+            e.sdpa_prefill(q, kc, vc, B["attn"], c.n_heads, c.n_kv, c.head_dim, c.max_len, pos0, T, ldq)  # :155
             e.q4_matmul(L["o_w"], L["o_s"], L["o_b"], B["attn"], B["o"], T, qd, H, c.group)    # :156
             e.scaled_add_raw(x, B["o"], 1.0, T * H)                                             # x1 = x + o
             if trace is not None:
@@ -314,7 +337,16 @@ def upload_weights(exe: ObsidianExecutor, layers: List[Dict[str, np.ndarray]], g
     holds ATTN_KEYS and the MoE PROJ_KEYS)."""
     dl = []
     for t in layers:
-        d = {k: exe.upload(t[k]) for k in ATTN_KEYS}
+        qkv_keys = {f"{p}_{kind}" for p in "qkv" for kind in "wsb"}
+        d = {k: exe.upload(t[k]) for k in ATTN_KEYS if k not in qkv_keys}
+        for kind in "wsb":  # q, k, v back to back (one matrix for the prefill GEMM)
+            buf = exe.upload(np.concatenate([t[f"{p}_{kind}"] for p in "qkv"]))
+            d[f"_qkv_{kind}"] = buf
+            rows = [t[f"{p}_{kind}"].shape[0] for p in "qkv"]
+            row_bytes = t[f"q_{kind}"].nbytes // rows[0]
+            d[f"q_{kind}"] = buf.ptr
+            d[f"k_{kind}"] = buf.ptr + rows[0] * row_bytes
+            d[f"v_{kind}"] = buf.ptr + (rows[0] + rows[1]) * row_bytes
         moe = {k: t[k] for k in t if k not in ATTN_KEYS}
         moe["norm_w"] = t["post_norm"]
         d["moe"] = MoeLayer.upload(exe, moe)
