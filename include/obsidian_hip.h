@@ -309,6 +309,26 @@ int obs_embed_q4(obs_ctx* ctx, const uint32_t* w, const uint16_t* scales, const 
 size_t obs_argmax_workspace(void);
 int obs_argmax(obs_ctx* ctx, const float* x, uint32_t n, int32_t* state, void* ws, size_t ws_bytes);
 
+/* The attention half of a decode layer in ONE launch, for the
+ * Qwen3-30B-A3B shape (hidden 2048, 32 query heads, 4 kv heads, head_dim 128):
+ * x1 = x + o_proj(attention) with q, k, v = projections of rmsnorm(x, in_norm),
+ * per-head q/k RMSNorm, NeoX RoPE at state[0], the key and value appended to
+ * the caches at state[0] (forward.rs:403-418) — what obs_q4_gemv (q/k/v,
+ * fused norm) + obs_attn_prep + obs_sdpa_decode + obs_q4_gemv (o, residual)
+ * compute, in one launch of 256 workgroups that exchange values through a
+ * context-owned area (allocated on the first call: run one before a graph
+ * capture). Needs all 256 CUs; other shapes use the separate calls. */
+typedef struct obs_attn_layer {
+  const uint32_t* q_w; const uint16_t* q_s; const uint16_t* q_b;  /* [4096, 2048/8], [4096, 32] */
+  const uint32_t* k_w; const uint16_t* k_s; const uint16_t* k_b;  /* [512, ...] */
+  const uint32_t* v_w; const uint16_t* v_s; const uint16_t* v_b;  /* [512, ...] */
+  const uint32_t* o_w; const uint16_t* o_s; const uint16_t* o_b;  /* [2048, 4096/8], [2048, 64] */
+  const uint16_t* in_norm; const uint16_t* q_norm; const uint16_t* k_norm;
+} obs_attn_layer;
+int obs_attn_decode(obs_ctx* ctx, const obs_attn_layer* layer, const uint16_t* x, uint16_t* k_cache,
+                    uint16_t* v_cache_t, uint32_t max_len, float eps, float theta, const int32_t* state,
+                    uint16_t* x1);
+
 /* ------------------------------------------------------------------ */
 /* Prefill of the layers around the MoE block for a batch of tokens     */
 /* (Model::prefill_batched, forward.rs:114-160, :240-261)               */

@@ -741,12 +741,50 @@ __global__ void __launch_bounds__(256) argmax_final_kernel(const unsigned long l
 
 constexpr uint32_t ARGMAX_PARTS = 256;
 
+// RoPE table entry (p, i) = (cos, sin) of fl32(p * fl32(theta^(-2i/128))), each
+// in double and rounded once: the values attn_prep_kernel computes.
+__global__ void __launch_bounds__(256) rope_table_kernel(float* __restrict__ table, uint32_t max_len, float theta) {
+  const uint32_t e = blockIdx.x * 256u + threadIdx.x;
+  if (e >= max_len * 64u) return;
+  const uint32_t p = e / 64u, i = e % 64u;
+  const float f = static_cast<float>(pow(static_cast<double>(theta), -2.0 * static_cast<double>(i) / 128.0));
+  const float angle = static_cast<float>(p) * f;
+  table[2u * e] = static_cast<float>(cos(static_cast<double>(angle)));
+  table[2u * e + 1u] = static_cast<float>(sin(static_cast<double>(angle)));
+}
+
 uint32_t sdpa_splits(uint32_t max_len) {
   const uint32_t blocks = max_len / 32u;
   return blocks < 64u ? blocks : 64u;
 }
 
 }  // namespace
+
+namespace obs {
+
+int ensure_rope_table(obs_ctx* ctx, float theta, uint32_t max_len, const float** out) {
+  if (!ctx->rope_table || ctx->rope_theta != theta || ctx->rope_len < max_len) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    OBS_HIP_TRY(ctx, hipStreamIsCapturing(ctx->stream, &cs));
+    if (cs != hipStreamCaptureStatusNone)
+      return set_error(ctx, OBS_E_INVALID, "RoPE table: run once before capturing (table for theta %g, %u positions)",
+                       static_cast<double>(theta), max_len);
+    OBS_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    if (ctx->rope_table) OBS_HIP_TRY(ctx, hipFree(ctx->rope_table));
+    ctx->rope_table = nullptr;
+    ctx->rope_len = 0;
+    OBS_HIP_TRY(ctx, hipMalloc(&ctx->rope_table, sizeof(float) * 128u * max_len));
+    rope_table_kernel<<<(max_len * 64u + 255u) / 256u, 256, 0, ctx->stream>>>(ctx->rope_table, max_len, theta);
+    OBS_HIP_TRY(ctx, hipGetLastError());
+    OBS_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    ctx->rope_len = max_len;
+    ctx->rope_theta = theta;
+  }
+  *out = ctx->rope_table;
+  return OBS_OK;
+}
+
+}  // namespace obs
 
 extern "C" {
 

@@ -1,0 +1,678 @@
+// obs_attention_fused.hip — the attention half of a decode layer in ONE launch
+// for the Qwen3-30B-A3B shape (hidden 2048, 32 query heads, 4 kv heads, head
+// dim 128): x1 = x + o_proj(attention(rope(norm(q)), rope(norm(k)), v)) with
+// q, k, v = projections of rmsnorm(x) (src/forward.rs:403-418).
+//
+// Why one launch: the separate launches (q/k/v mat-vec, norm + RoPE + cache
+// append, split attention, split combine, o mat-vec) each move a few MB or
+// less, and a launch boundary with its fences and first memory round trip
+// cost about as much as their work. Here 256 workgroups (one per CU) pass the
+// few values that cross workgroups through epoch-tagged slots (see
+// slot_store), as decode_fused_kernel does for the MoE half:
+//   1. every wave computes 5 of the 5,120 q/k/v rows (RMSNorm of x fused) and
+//      publishes them;
+//   2. workgroup b < 128 is (kv head b % 4, split b / 4 of 32): it polls
+//      the 8 query heads and the key/value head of its kv head, applies the
+//      per-head RMSNorm and NeoX RoPE, appends the key and value at pos to the
+//      caches (the workgroup whose split holds pos) and runs the split's
+//      attention with the decode kernel's MFMA block math (its own key/value
+//      at pos spliced in from registers); the 4 waves' partials are merged in
+//      LDS and published (32 splits, not 64: the same one block per wave at a
+//      4,096-token context, and half the partials to exchange);
+//   3. workgroup j combines the 32 splits of head j / 8 for 16 of its dims and
+//      publishes them as bf16 pairs;
+//   4. every workgroup polls the 4,096 attention outputs into LDS and each
+//      wave computes 2 rows of x1 = x + W_o attn.
+// All weight, activation and cache loads that do not depend on an exchange
+// are issued at the start, so the exchanges overlap the memory stream.
+// Every wait is bounded (100 ms of the constant clock); a time-out sets the
+// workspace's error flag, reported and cleared by obs_device_status.
+#include "obs_internal.hpp"
+
+// Phase markers for timing harnesses; no code is generated unless one defines it.
+#ifndef OBS_ATTN_MARK
+#define OBS_ATTN_MARK(phase)
+#endif
+
+namespace {
+
+using namespace obsd;
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+constexpr uint32_t AH = 2048, ANH = 32, ANKV = 4, AHD = 128, AG = ANH / ANKV;  // G = 8
+constexpr uint32_t AQD = ANH * AHD, AKVD = ANKV * AHD, AQKV = AQD + 2 * AKVD;  // 4096, 512, 5120
+constexpr uint32_t ANWG = 256, ANWAVE = ANWG * 4;
+constexpr uint32_t A_RPW = AQKV / ANWAVE;       // q/k/v rows per wave: 5
+constexpr uint32_t A_ORPW = AH / ANWAVE;        // o rows per wave: 2
+constexpr uint32_t A_NSPLIT = 32;               // splits per kv head (workgroups 0..127 attend)
+constexpr uint32_t A_NATT = A_NSPLIT * ANKV;    // attending workgroups: 128
+constexpr uint32_t A_CDIM = AQD / ANWG;         // combined outputs per workgroup: 16
+constexpr uint32_t A_NEED = AG * AHD + 2 * AHD; // slots a split polls: its 8 query heads, k, v
+constexpr uint32_t A_PART = AG * (AHD + 2);     // a split's partial: 8 heads x (O[128], m, l)
+static_assert(A_RPW * ANWAVE == AQKV && A_ORPW * ANWAVE == AH && A_CDIM * ANWG == AQD, "shape");
+
+constexpr size_t AW_COUNT = 0, AW_ERR = 256;
+constexpr size_t AW_QKV = 1024;                                // [5120] slots
+constexpr size_t AW_PART = AW_QKV + size_t(AQKV) * 8;           // [128][1040] slots
+constexpr size_t AW_ATTN = AW_PART + size_t(A_NATT) * A_PART * 8; // [2048] slots: bf16 pairs
+constexpr size_t AW_BYTES = AW_ATTN + size_t(AQD / 2) * 8;
+constexpr uint64_t A_WAIT_TICKS = 10000000ull;  // 100 ms at 100 MHz
+
+struct AttnArgs {
+  const uint32_t* q_w; const uint16_t* q_s; const uint16_t* q_b;
+  const uint32_t* k_w; const uint16_t* k_s; const uint16_t* k_b;
+  const uint32_t* v_w; const uint16_t* v_s; const uint16_t* v_b;
+  const uint32_t* o_w; const uint16_t* o_s; const uint16_t* o_b;
+  const uint16_t* in_norm; const uint16_t* q_norm; const uint16_t* k_norm;
+  const uint16_t* x; uint16_t* x1;
+  uint16_t* k_cache; uint16_t* v_cache_t;
+  const int32_t* state;
+  const float* rope;  // [max_len][64] (cos, sin) pairs, rope_table_kernel
+  unsigned char* ws;
+  uint32_t max_len;
+  float eps, scale_log2;
+};
+
+__device__ __forceinline__ float shfl_f(float v, int src) { return __shfl(v, src, 64); }
+__device__ __forceinline__ float shfl_xor_f(float v, int m) { return __shfl_xor(v, m, 64); }
+
+__global__ void __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 1)))
+attn_fused_kernel(AttnArgs a) {
+  __shared__ uint32_t s_epoch;
+  __shared__ int s_abort, s_fail;
+  __shared__ float s_qkv[A_NEED];                                    // the split's q (8 heads), k, v
+  __shared__ __attribute__((aligned(16))) uint16_t s_rot[AG + 2][AHD];  // rotated q heads, k, then v (bf16)
+  __shared__ float s_pm[4][16], s_pl[4][16];
+  __shared__ float s_po[4][AG][AHD];
+  __shared__ float s_cm[A_NSPLIT], s_cl[A_NSPLIT], s_co[A_NSPLIT][A_CDIM];
+  __shared__ float s_rl[16][A_CDIM], s_ra[16][A_CDIM];
+  __shared__ __attribute__((aligned(16))) f16x2_t s_ap[AQD / 2];    // attention output as f16 pairs
+  __shared__ float s_asum[AQD / 32], s_aoff[AQD / 32];
+
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  const uint32_t wave_g = __builtin_amdgcn_readfirstlane(blockIdx.x * 4u + wave);
+  uint64_t* ctl_count = reinterpret_cast<uint64_t*>(a.ws + AW_COUNT);
+  uint32_t* ctl_err = reinterpret_cast<uint32_t*>(a.ws + AW_ERR);
+  uint64_t* qkv_slots = reinterpret_cast<uint64_t*>(a.ws + AW_QKV);
+  uint64_t* part_slots = reinterpret_cast<uint64_t*>(a.ws + AW_PART);
+  uint64_t* attn_slots = reinterpret_cast<uint64_t*>(a.ws + AW_ATTN);
+
+  OBS_ATTN_MARK(0);
+  // ---- 0. loads that need no exchange, in the order they are used: the
+  // launch count first (its round trip gates the first publish), the
+  // position, the activations and every weight row, then what depends on the
+  // position (the first key/value block, the RoPE cosines and sines)
+  // every workgroup adds 1 to the count as it exits: the quotient counts the
+  // earlier launches (as in decode_fused_kernel). Every thread loads it (the
+  // same address): a load under a branch is waited for at the branch's join.
+  const uint64_t counted = __hip_atomic_load(ctl_count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint32_t err = __hip_atomic_load(ctl_err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // the position through the scalar cache (its own counter: the key/value
+  // loads that need it wait for it alone, not for the vector loads before them)
+  const int32_t pos_i = a.state[0];
+  __builtin_amdgcn_sched_barrier(0);
+  uint4 xq[4], nq[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    xq[i] = reinterpret_cast<const uint4*>(a.x + 32u * lane)[i];
+    nq[i] = reinterpret_cast<const uint4*>(a.in_norm + 32u * lane)[i];
+  }
+  uint4 rq[A_RPW];
+  uint16_t rsc[A_RPW], rbi[A_RPW];
+#pragma unroll
+  for (uint32_t k = 0; k < A_RPW; ++k) {
+    const uint32_t r = A_RPW * wave_g + k;  // wave-uniform
+    const bool is_q = r < AQD, is_k = !is_q && r < AQD + AKVD;
+    const uint32_t rr = is_q ? r : (is_k ? r - AQD : r - AQD - AKVD);
+    const uint32_t* w = is_q ? a.q_w : (is_k ? a.k_w : a.v_w);
+    const uint16_t* sp = is_q ? a.q_s : (is_k ? a.k_s : a.v_s);
+    const uint16_t* bp = is_q ? a.q_b : (is_k ? a.k_b : a.v_b);
+    rq[k] = reinterpret_cast<const uint4*>(w + static_cast<size_t>(rr) * (AH / 8u))[lane];
+    rsc[k] = sp[static_cast<size_t>(rr) * (AH / 64u) + lane / 2u];
+    rbi[k] = bp[static_cast<size_t>(rr) * (AH / 64u) + lane / 2u];
+  }
+  uint4 oq[A_ORPW][2];
+  uint16_t osc[A_ORPW][2], obi[A_ORPW][2], ores[A_ORPW];
+#pragma unroll
+  for (uint32_t k = 0; k < A_ORPW; ++k) {
+    const uint32_t r = A_ORPW * wave_g + k;
+#pragma unroll
+    for (uint32_t sg = 0; sg < 2; ++sg) {
+      oq[k][sg] = reinterpret_cast<const uint4*>(a.o_w + static_cast<size_t>(r) * (AQD / 8u) + 256u * sg)[lane];
+      const size_t gi = static_cast<size_t>(r) * (AQD / 64u) + 32u * sg + lane / 2u;
+      osc[k][sg] = a.o_s[gi];
+      obi[k][sg] = a.o_b[gi];
+    }
+    ores[k] = a.x[r];
+  }
+  const uint32_t wq = *reinterpret_cast<const uint32_t*>(a.q_norm + 2u * lane);
+  const uint32_t wk = *reinterpret_cast<const uint32_t*>(a.k_norm + 2u * lane);
+  // this workgroup's split of kv head kv, and the position's loads
+  const bool attends = blockIdx.x < A_NATT;  // uniform
+  const uint32_t kv = blockIdx.x % ANKV, sp = min(blockIdx.x / ANKV, A_NSPLIT - 1u);
+  const uint32_t max_len = a.max_len;
+  const uint32_t pos = static_cast<uint32_t>(pos_i);
+  const bool pos_ok = pos_i >= 0 && pos < max_len;
+  const uint32_t seq = static_cast<uint32_t>(min(max(pos_i + 1, 1), static_cast<int32_t>(max_len)));
+  const uint32_t nblk = (seq + 31u) / 32u, per = (nblk + A_NSPLIT - 1u) / A_NSPLIT;
+  const uint32_t b0 = sp * per, b1 = min(nblk, b0 + per);
+  const uint32_t col = lane & 15u, g = lane >> 4;
+  const uint16_t* kb = a.k_cache + static_cast<size_t>(kv) * max_len * AHD;
+  const uint16_t* vb = a.v_cache_t + static_cast<size_t>(kv) * AHD * max_len;
+  // wave w runs blocks b0 + w, b0 + w + 4, ...; its first block's loads go out
+  // now (clamped into the sequence when it has none; unused then)
+  u32x4_t ka[2][4];
+  u32x2_t va[8][2];
+  auto load_block = [&](uint32_t blk) __attribute__((always_inline)) {
+    const uint32_t t0 = 32u * blk;
+#pragma unroll
+    for (uint32_t tt = 0; tt < 2; ++tt) {
+      const uint16_t* kr = kb + static_cast<size_t>(t0 + 16u * tt + col) * AHD + 8u * g;
+#pragma unroll
+      for (uint32_t ks = 0; ks < 4; ++ks) ka[tt][ks] = *reinterpret_cast<const u32x4_t*>(kr + 32u * ks);
+    }
+#pragma unroll
+    for (uint32_t nt = 0; nt < 8; ++nt) {
+      const uint16_t* vr = vb + static_cast<size_t>(16u * nt + col) * max_len + t0 + 4u * g;
+      va[nt][0] = *reinterpret_cast<const u32x2_t*>(vr);
+      va[nt][1] = *reinterpret_cast<const u32x2_t*>(vr + 16);
+    }
+  };
+  // the position's loads: the wave's first key/value block (clamped into the
+  // sequence; unused by workgroups that do not attend or waves without a
+  // block) and the lane's RoPE cosines and sines, pairs (2 lane, 2 lane + 1)
+  // mod 64: (cos, sin, cos, sin)
+  load_block(min(b0 + wave, nblk - 1u));
+  const f32x4_t csn = *reinterpret_cast<const f32x4_t*>(a.rope + static_cast<size_t>(min(pos, max_len - 1u)) * 128u +
+                                                        4u * (lane & 31u));
+  __builtin_amdgcn_sched_barrier(0);
+  if (tid == 0) {
+    s_epoch = static_cast<uint32_t>(counted / ANWG) + 1u;
+    s_abort = err != 0u;
+    s_fail = 0;
+  }
+  __syncthreads();
+  const uint32_t epoch = s_epoch;
+  if (s_abort) {  // a previous launch failed: the host must reset first
+    if (tid == 0) __hip_atomic_fetch_add(ctl_count, uint64_t{1}, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
+
+  OBS_ATTN_MARK(1);
+  // ---- 1. q/k/v rows of rmsnorm(x) (obs_rmsnorm's sequence), rounded to bf16
+  {
+    float xf[32];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t wd[4] = {xq[i].x, xq[i].y, xq[i].z, xq[i].w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        xf[8 * i + 2 * j] = bf16lo(wd[j]);
+        xf[8 * i + 2 * j + 1] = bf16hi(wd[j]);
+      }
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 32; ++c) ss = __builtin_fmaf(xf[c], xf[c], ss);
+    const float inv = 1.0f / __builtin_sqrtf(wave_sum_asc(ss) / static_cast<float>(AH) + a.eps);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t wd[4] = {nq[i].x, nq[i].y, nq[i].z, nq[i].w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        xf[8 * i + 2 * j] = bf16_to_f32(f32_to_bf16((xf[8 * i + 2 * j] * inv) * bf16lo(wd[j])));
+        xf[8 * i + 2 * j + 1] = bf16_to_f32(f32_to_bf16((xf[8 * i + 2 * j + 1] * inv) * bf16hi(wd[j])));
+      }
+    }
+    float xs = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 32; ++c) xs = xs + xf[c];
+    f16x2_t xh[16];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) f16_pairs8(xf + 8 * i, xh + 4 * i);
+    float xoff = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) xoff = dot8_off_only(xh + 4 * i, xoff);
+    float mine = 0.0f;  // lane k keeps row k
+#pragma unroll
+    for (uint32_t k = 0; k < A_RPW; ++k) {
+      float acc = 0.0f;
+      acc = dot8_q4_off(rq[k].x, xh + 0, acc);
+      acc = dot8_q4_off(rq[k].y, xh + 4, acc);
+      acc = dot8_q4_off(rq[k].z, xh + 8, acc);
+      acc = dot8_q4_off(rq[k].w, xh + 12, acc);
+      float part = __builtin_fmaf(bf16_to_f32(rsc[k]), acc - xoff, bf16_to_f32(rbi[k]) * xs);
+      part = wave_sum_asc(part);
+      mine = lane == k ? bf16_to_f32(f32_to_bf16(part)) : mine;
+    }
+    if (lane < A_RPW) slot_store(qkv_slots + A_RPW * wave_g + lane, epoch, mine);
+  }
+  OBS_ATTN_MARK(2);
+  if (attends) {  // workgroup-uniform
+
+  // ---- 2. this workgroup's split of kv head kv: poll the split's q heads
+  // (rows 1024 kv ..), k (4096 + 128 kv ..) and v (4608 + 128 kv ..)
+  {
+    float vals[5];
+    const uint64_t t0 = wall_clock64();
+    bool ok = true;
+    while (true) {
+      bool ready = true;
+#pragma unroll
+      for (uint32_t u = 0; u < 5; ++u) {
+        const uint32_t i = tid + 256u * u;
+        const uint32_t row = i < AG * AHD ? kv * AG * AHD + i
+                                          : (i < AG * AHD + AHD ? AQD + kv * AHD + (i - AG * AHD)
+                                                                : AQD + AKVD + kv * AHD + (i - AG * AHD - AHD));
+        const uint64_t v = slot_load(qkv_slots + row);
+        vals[u] = slot_val(v);
+        ready = ready && slot_ready(v, epoch);
+      }
+      if (__all(ready)) break;
+      if (wall_clock64() - t0 > A_WAIT_TICKS) {
+        ok = false;
+        break;
+      }
+    }
+    if (!ok && lane == 0) s_fail = 1;
+#pragma unroll
+    for (uint32_t u = 0; u < 5; ++u) s_qkv[tid + 256u * u] = vals[u];
+  }
+  __syncthreads();
+  OBS_ATTN_MARK(3);
+  // per-head RMSNorm + NeoX RoPE (attn_prep_kernel's sequence): wave w owns
+  // heads w, w + 4 (query heads) and, for wave 0, head 8 = the key head
+  {
+    const float cs[2] = {csn[0], csn[2]}, sn[2] = {csn[1], csn[3]};
+    const bool first = lane < 32u;
+    for (uint32_t h = wave; h <= AG; h += 4u) {
+      const float x0 = s_qkv[h * AHD + 2u * lane], x1 = s_qkv[h * AHD + 2u * lane + 1u];
+      const uint32_t wv = h < AG ? wq : wk;
+      float ss = __builtin_fmaf(x0, x0, 0.0f);
+      ss = __builtin_fmaf(x1, x1, ss);
+      const float inv = 1.0f / __builtin_sqrtf(wave_sum_asc(ss) / static_cast<float>(AHD) + a.eps);
+      const float n0 = bf16_to_f32(f32_to_bf16((x0 * inv) * bf16lo(wv)));
+      const float n1 = bf16_to_f32(f32_to_bf16((x1 * inv) * bf16hi(wv)));
+      const float p0 = shfl_xor_f(n0, 32), p1 = shfl_xor_f(n1, 32);
+      float r[2];
+#pragma unroll
+      for (uint32_t j = 0; j < 2; ++j) {
+        const float own = j ? n1 : n0, other = j ? p1 : p0;
+        const float aa = own * cs[j], bb = other * sn[j];
+        r[j] = first ? aa - bb : aa + bb;
+      }
+      *reinterpret_cast<uint32_t*>(&s_rot[h][2u * lane]) = pack_bf16x2(r[0], r[1]);
+    }
+    if (wave == 1) {  // the value head, as bf16
+      *reinterpret_cast<uint32_t*>(&s_rot[AG + 1][2u * lane]) =
+          pack_bf16x2(s_qkv[(AG + 1) * AHD + 2u * lane], s_qkv[(AG + 1) * AHD + 2u * lane + 1u]);
+    }
+  }
+  __syncthreads();
+  OBS_ATTN_MARK(4);
+  const uint32_t pblk = pos / 32u;
+  const bool own_pos = pos_ok && pblk >= b0 && pblk < b1;  // this split holds pos: append it
+  if (own_pos && wave == 0) {
+    *reinterpret_cast<uint32_t*>(a.k_cache + (static_cast<size_t>(kv) * max_len + pos) * AHD + 2u * lane) =
+        *reinterpret_cast<const uint32_t*>(&s_rot[AG][2u * lane]);
+  } else if (own_pos && wave == 1) {
+    uint16_t* dst = a.v_cache_t + (static_cast<size_t>(kv) * AHD + 2u * lane) * max_len + pos;
+    dst[0] = s_rot[AG + 1][2u * lane];
+    dst[max_len] = s_rot[AG + 1][2u * lane + 1u];
+  }
+  // query slices: B operand, head col (zero for the padding columns 8..15)
+  bf16x8_t qb[4];
+#pragma unroll
+  for (uint32_t ks = 0; ks < 4; ++ks) {
+    u32x4_t v = *reinterpret_cast<const u32x4_t*>(&s_rot[min(col, AG - 1u)][32u * ks + 8u * g]);
+    if (col >= AG) v = u32x4_t{0u, 0u, 0u, 0u};
+    qb[ks] = __builtin_bit_cast(bf16x8_t, v);
+  }
+  float m_run = -__builtin_huge_valf(), l_run = 0.0f;
+  f32x4_t o[8];
+#pragma unroll
+  for (uint32_t nt = 0; nt < 8; ++nt) o[nt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  for (uint32_t blk = b0 + wave; blk < b1; blk += 4u) {
+    if (blk != b0 + wave) load_block(blk);
+    const uint32_t t0 = 32u * blk;
+    if (pblk == blk) {  // uniform: splice this token's key and value (the cache held the old ones)
+#pragma unroll
+      for (uint32_t tt = 0; tt < 2; ++tt)
+        if (t0 + 16u * tt + col == pos)
+#pragma unroll
+          for (uint32_t ks = 0; ks < 4; ++ks)
+            ka[tt][ks] = *reinterpret_cast<const u32x4_t*>(&s_rot[AG][32u * ks + 8u * g]);
+#pragma unroll
+      for (uint32_t nt = 0; nt < 8; ++nt) {
+        const uint32_t vv = s_rot[AG + 1][16u * nt + col];
+#pragma unroll
+        for (uint32_t hh = 0; hh < 2; ++hh) {
+          const uint32_t ta = t0 + 16u * hh + 4u * g;  // positions ta .. ta + 3 in two words
+          if (pos >= ta && pos < ta + 4u) {
+            const uint32_t e = pos - ta, sh = 16u * (e & 1u);
+            uint32_t wd = (e >> 1) ? va[nt][hh].y : va[nt][hh].x;
+            wd = (wd & ~(0xffffu << sh)) | (vv << sh);
+            if (e >> 1) va[nt][hh].y = wd; else va[nt][hh].x = wd;
+          }
+        }
+      }
+    }
+    f32x4_t s[2];
+#pragma unroll
+    for (uint32_t tt = 0; tt < 2; ++tt) {
+      f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (uint32_t ks = 0; ks < 4; ++ks)
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, ka[tt][ks]), qb[ks], acc, 0, 0, 0);
+      s[tt] = acc;
+    }
+    float sv[8];
+#pragma unroll
+    for (uint32_t tt = 0; tt < 2; ++tt)
+#pragma unroll
+      for (uint32_t i = 0; i < 4; ++i) {
+        const uint32_t t = t0 + 16u * tt + 4u * g + i;
+        sv[4 * tt + i] = t < seq ? s[tt][i] * a.scale_log2 : -__builtin_huge_valf();
+      }
+    float bm = sv[0];
+#pragma unroll
+    for (uint32_t i = 1; i < 8; ++i) bm = fmaxf(bm, sv[i]);
+    bm = fmaxf(bm, shfl_xor_f(bm, 16));
+    bm = fmaxf(bm, shfl_xor_f(bm, 32));
+    const float m_new = fmaxf(m_run, bm);  // finite: every block holds a position < seq
+    const float corr = __builtin_amdgcn_exp2f(m_run - m_new);
+    float p[8], psum = 0.0f;
+#pragma unroll
+    for (uint32_t i = 0; i < 8; ++i) {
+      p[i] = bf16_to_f32(f32_to_bf16(__builtin_amdgcn_exp2f(sv[i] - m_new)));
+      psum += p[i];
+    }
+    l_run = l_run * corr + psum;
+    m_run = m_new;
+    float oc[4];
+#pragma unroll
+    for (uint32_t i = 0; i < 4; ++i) oc[i] = shfl_f(corr, static_cast<int>(4u * g + i));
+    const bf16x8_t pa = __builtin_bit_cast(
+        bf16x8_t, u32x4_t{pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]), pack_bf16x2(p[4], p[5]),
+                          pack_bf16x2(p[6], p[7])});
+    const bool tail = t0 + 32u > seq;  // positions past seq read zero values
+#pragma unroll
+    for (uint32_t nt = 0; nt < 8; ++nt) {
+      u32x2_t v0 = va[nt][0], v1 = va[nt][1];
+      if (tail) {
+        auto keep = [&](uint32_t w, uint32_t t) { return t >= seq ? 0u : (t + 1u >= seq ? (w & 0xffffu) : w); };
+        const uint32_t ta = t0 + 4u * g, tb = ta + 16u;
+        v0.x = keep(v0.x, ta);
+        v0.y = keep(v0.y, ta + 2u);
+        v1.x = keep(v1.x, tb);
+        v1.y = keep(v1.y, tb + 2u);
+      }
+      const bf16x8_t vbf = __builtin_bit_cast(bf16x8_t, u32x4_t{v0.x, v0.y, v1.x, v1.y});
+#pragma unroll
+      for (uint32_t i = 0; i < 4; ++i) o[nt][i] *= oc[i];
+      o[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, vbf, o[nt], 0, 0, 0);
+    }
+  }
+  OBS_ATTN_MARK(5);
+  // the wave's partial: m, l per head column (l summed over the four g lanes), O rows 4 g + i
+  l_run += shfl_xor_f(l_run, 16);
+  l_run += shfl_xor_f(l_run, 32);
+  if (lane < 16u) {
+    s_pm[wave][lane] = m_run;
+    s_pl[wave][lane] = l_run;
+  }
+  if (g < 2u) {
+#pragma unroll
+    for (uint32_t nt = 0; nt < 8; ++nt)
+#pragma unroll
+      for (uint32_t i = 0; i < 4; ++i) s_po[wave][4u * g + i][16u * nt + col] = o[nt][i];
+  }
+  __syncthreads();
+  // merge the four waves (a wave without blocks has m = -inf, l = 0, O = 0) and publish
+  {
+    uint64_t* dst = part_slots + static_cast<size_t>(blockIdx.x) * A_PART;
+    const uint32_t h = tid / 32u, d0 = 4u * (tid % 32u);
+    float M = s_pm[0][h];
+#pragma unroll
+    for (uint32_t w = 1; w < 4; ++w) M = fmaxf(M, s_pm[w][h]);
+    float wt[4], L = 0.0f;
+#pragma unroll
+    for (uint32_t w = 0; w < 4; ++w) {
+      wt[w] = s_pm[w][h] == -__builtin_huge_valf() ? 0.0f : __builtin_amdgcn_exp2f(s_pm[w][h] - M);
+      L = __builtin_fmaf(s_pl[w][h], wt[w], L);
+    }
+#pragma unroll
+    for (uint32_t d = 0; d < 4; ++d) {
+      float acc = 0.0f;
+#pragma unroll
+      for (uint32_t w = 0; w < 4; ++w) acc = __builtin_fmaf(s_po[w][h][d0 + d], wt[w], acc);
+      slot_store(dst + h * (AHD + 2u) + d0 + d, epoch, acc);
+    }
+    if (tid % 32u == 0u) {
+      slot_store(dst + h * (AHD + 2u) + AHD, epoch, M);
+      slot_store(dst + h * (AHD + 2u) + AHD + 1u, epoch, L);
+    }
+  }
+
+  }  // attends
+  OBS_ATTN_MARK(6);
+  // ---- 3. combine head j / 8, dims 16 (j % 8) .. + 16 over the 32 splits
+  {
+    const uint32_t h = blockIdx.x / 8u, d0 = A_CDIM * (blockIdx.x % 8u);
+    const uint32_t ckv = h / AG, hh = h % AG;
+    const uint32_t s = tid / 8u, q8 = tid % 8u;  // split s, dims d0 + 2 q8, + 1
+    const uint64_t* src = part_slots + static_cast<size_t>(s * ANKV + ckv) * A_PART + hh * (AHD + 2u);
+    float v[4];
+    const uint64_t t0 = wall_clock64();
+    bool ok = s_fail == 0;
+    while (ok) {
+      const uint64_t x0 = slot_load(src + d0 + 2u * q8), x1 = slot_load(src + d0 + 2u * q8 + 1u);
+      const uint64_t xm = slot_load(src + AHD), xl = slot_load(src + AHD + 1u);
+      v[0] = slot_val(x0);
+      v[1] = slot_val(x1);
+      v[2] = slot_val(xm);
+      v[3] = slot_val(xl);
+      const bool ready = slot_ready(x0, epoch) && slot_ready(x1, epoch) && slot_ready(xm, epoch) &&
+                         slot_ready(xl, epoch);
+      if (__all(ready)) break;
+      if (wall_clock64() - t0 > A_WAIT_TICKS) {
+        ok = false;
+        if (lane == 0) s_fail = 1;
+      }
+    }
+    s_co[s][2u * q8] = v[0];
+    s_co[s][2u * q8 + 1u] = v[1];
+    if (q8 == 0u) {
+      s_cm[s] = v[2];
+      s_cl[s] = v[3];
+    }
+    __syncthreads();
+    OBS_ATTN_MARK(7);
+    {  // thread (group q, dim d): splits 2 q, 2 q + 1; then the 16 groups in order
+      const uint32_t d = tid % A_CDIM, q = tid / A_CDIM;
+      float M = -__builtin_huge_valf();
+      for (uint32_t k = 0; k < A_NSPLIT; ++k) M = fmaxf(M, s_cm[k]);
+      float L = 0.0f, acc = 0.0f;
+#pragma unroll
+      for (uint32_t k = 2u * q; k < 2u * q + 2u; ++k) {
+        const float wt = s_cm[k] == -__builtin_huge_valf() ? 0.0f : __builtin_amdgcn_exp2f(s_cm[k] - M);
+        L = __builtin_fmaf(s_cl[k], wt, L);
+        acc = __builtin_fmaf(s_co[k][d], wt, acc);
+      }
+      s_rl[q][d] = L;
+      s_ra[q][d] = acc;
+    }
+    __syncthreads();
+    if (wave == 0) {  // lanes 0..15: one dim each; even lanes publish (dim, dim + 1) as a bf16 pair
+      float L = 0.0f, acc = 0.0f;
+#pragma unroll
+      for (uint32_t q = 0; q < 16; ++q) {
+        L += s_rl[q][lane & 15u];
+        acc += s_ra[q][lane & 15u];
+      }
+      const uint32_t mine = f32_to_bf16(acc / L);
+      const uint32_t next = __shfl_xor(static_cast<int>(mine), 1, 64);
+      if (lane < A_CDIM && (lane & 1u) == 0u)
+        slot_store(attn_slots + (h * AHD + d0 + lane) / 2u, epoch, __uint_as_float(mine | (next << 16)));
+    }
+  }
+  OBS_ATTN_MARK(8);
+
+  // ---- 4. x1 = x + W_o attn: the attention output into LDS as f16 pairs in
+  // dot8_q4_off order, with the sum and the offset sum of every 32 columns
+  {
+    // the 2,048 bf16 pairs (the loop decisions are workgroup-uniform)
+    bool ok = s_fail == 0;
+    const uint64_t t0 = wall_clock64();
+    uint32_t pv[AQD / 512];
+    while (ok) {
+      bool ready = true;
+#pragma unroll
+      for (uint32_t u = 0; u < AQD / 512; ++u) {
+        const uint64_t x = slot_load(attn_slots + tid + 256u * u);
+        pv[u] = static_cast<uint32_t>(x);
+        ready = ready && slot_ready(x, epoch);
+      }
+      const int late = wall_clock64() - t0 > A_WAIT_TICKS;
+      if (__syncthreads_and(ready)) break;
+      if (__syncthreads_or(late)) ok = false;
+    }
+    if (!ok && tid == 0) s_fail = 1;
+    _Float16* ap16 = reinterpret_cast<_Float16*>(s_ap);
+#pragma unroll
+    for (uint32_t u = 0; u < AQD / 512; ++u) {
+      const uint32_t k = tid + 256u * u, i0 = 2u * k;  // columns i0 (low half), i0 + 1
+      const _Float16 h0 = static_cast<_Float16>(bf16lo(pv[u])), h1 = static_cast<_Float16>(bf16hi(pv[u]));
+      const uint32_t j0 = i0 & 7u, j1 = j0 + 1u;
+      ap16[(i0 & ~7u) + 2u * (j0 & 3u) + (j0 >> 2)] = h0;
+      ap16[(i0 & ~7u) + 2u * (j1 & 3u) + (j1 >> 2)] = h1;
+      // per 32 columns = 16 consecutive lanes: the sum and the offset sum of
+      // dot8_q4_off (1024 at even positions, 64 at odd ones) over the f16 values
+      float sum = static_cast<float>(h0) + static_cast<float>(h1);
+      float off = static_cast<float>(h0) * 1024.0f + static_cast<float>(h1) * 64.0f;
+      sum = sum + dpp_f32<DPP_XOR1>(sum);
+      sum = sum + dpp_f32<DPP_XOR2>(sum);
+      sum = sum + dpp_f32<DPP_HALF_MIRROR>(sum);
+      sum = sum + dpp_f32<DPP_MIRROR>(sum);
+      off = off + dpp_f32<DPP_XOR1>(off);
+      off = off + dpp_f32<DPP_XOR2>(off);
+      off = off + dpp_f32<DPP_HALF_MIRROR>(off);
+      off = off + dpp_f32<DPP_MIRROR>(off);
+      if ((k & 15u) == 0u) {
+        s_asum[k >> 4] = sum;
+        s_aoff[k >> 4] = off;
+      }
+    }
+  }
+  __syncthreads();
+  OBS_ATTN_MARK(9);
+  {
+    f16x2_t ah[2][16];
+    float asum[2], aoff[2];
+#pragma unroll
+    for (uint32_t sg = 0; sg < 2; ++sg) {
+      const uint32_t c0 = 2048u * sg + 32u * lane;
+#pragma unroll
+      for (uint32_t i = 0; i < 4; ++i) {
+        const uint4 w4 = *reinterpret_cast<const uint4*>(&s_ap[c0 / 2u + 4u * i]);
+        ah[sg][4 * i] = as_f16x2(w4.x); ah[sg][4 * i + 1] = as_f16x2(w4.y);
+        ah[sg][4 * i + 2] = as_f16x2(w4.z); ah[sg][4 * i + 3] = as_f16x2(w4.w);
+      }
+      asum[sg] = s_asum[c0 / 32u];
+      aoff[sg] = s_aoff[c0 / 32u];
+    }
+    float mine = 0.0f;  // lane k keeps row k
+#pragma unroll
+    for (uint32_t k = 0; k < A_ORPW; ++k) {
+      float part = 0.0f;
+#pragma unroll
+      for (uint32_t sg = 0; sg < 2; ++sg) {
+        float acc = 0.0f;
+        acc = dot8_q4_off(oq[k][sg].x, ah[sg] + 0, acc);
+        acc = dot8_q4_off(oq[k][sg].y, ah[sg] + 4, acc);
+        acc = dot8_q4_off(oq[k][sg].z, ah[sg] + 8, acc);
+        acc = dot8_q4_off(oq[k][sg].w, ah[sg] + 12, acc);
+        part = part + __builtin_fmaf(bf16_to_f32(osc[k][sg]), acc - aoff[sg], bf16_to_f32(obi[k][sg]) * asum[sg]);
+      }
+      part = wave_sum_asc(part);
+      mine = lane == k ? bf16_to_f32(ores[k]) + part : mine;
+    }
+    if (lane < A_ORPW) a.x1[A_ORPW * wave_g + lane] = f32_to_bf16(mine);
+  }
+  __syncthreads();
+  OBS_ATTN_MARK(10);
+  if (tid == 0) {
+    if (s_fail) __hip_atomic_store(ctl_err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    __hip_atomic_fetch_add(ctl_count, uint64_t{1}, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+}  // namespace
+
+namespace obs {
+
+int attn_fused_status(obs_ctx* ctx) {
+  if (!ctx->attn_ws) return OBS_OK;
+  OBS_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+  uint32_t err = 0;
+  OBS_HIP_TRY(ctx, hipMemcpy(&err, static_cast<unsigned char*>(ctx->attn_ws) + AW_ERR, 4, hipMemcpyDeviceToHost));
+  if (err) {
+    OBS_HIP_TRY(ctx, hipMemset(ctx->attn_ws, 0, AW_BYTES));
+    OBS_HIP_TRY(ctx, hipDeviceSynchronize());
+    return set_error(ctx, OBS_E_HIP,
+                     "fused attention: a cross-workgroup wait timed out (were all CUs available?); "
+                     "outputs since then are invalid; workspace reset");
+  }
+  return OBS_OK;
+}
+
+}  // namespace obs
+
+extern "C" {
+
+int obs_attn_decode(obs_ctx* ctx, const obs_attn_layer* L, const uint16_t* x, uint16_t* k_cache,
+                    uint16_t* v_cache_t, uint32_t max_len, float eps, float theta, const int32_t* state,
+                    uint16_t* x1) {
+  if (!ctx) return OBS_E_INVALID;
+  if (!L || !x || !k_cache || !v_cache_t || !state || !x1)
+    return obs::set_error(ctx, OBS_E_INVALID, "obs_attn_decode: null pointer");
+  const void* ptrs[] = {L->q_w, L->q_s, L->q_b, L->k_w, L->k_s, L->k_b, L->v_w, L->v_s, L->v_b,
+                        L->o_w, L->o_s, L->o_b, L->in_norm, L->q_norm, L->k_norm};
+  for (const void* p : ptrs)
+    if (!p) return obs::set_error(ctx, OBS_E_INVALID, "obs_attn_decode: a layer tensor is null");
+  if (max_len == 0 || max_len % 32u != 0)
+    return obs::set_error(ctx, OBS_E_SHAPE, "obs_attn_decode: max_len must be a positive multiple of 32 (got %u)",
+                          max_len);
+  if (!obs::aligned(x, 16) || !obs::aligned(L->in_norm, 16) || !obs::aligned(L->q_w, 16) ||
+      !obs::aligned(L->k_w, 16) || !obs::aligned(L->v_w, 16) || !obs::aligned(L->o_w, 16) ||
+      !obs::aligned(L->q_norm, 4) || !obs::aligned(L->k_norm, 4) || !obs::aligned(k_cache, 16) ||
+      !obs::aligned(v_cache_t, 8))
+    return obs::set_error(ctx, OBS_E_ALIGN, "obs_attn_decode: weights, x and the key cache must be 16-byte aligned");
+  if (ctx->num_cus < static_cast<int>(ANWG))
+    return obs::set_error(ctx, OBS_E_UNSUPPORTED, "obs_attn_decode: needs %u CUs (the device has %d)", ANWG,
+                          ctx->num_cus);
+  if (!ctx->attn_ws) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    OBS_HIP_TRY(ctx, hipStreamIsCapturing(ctx->stream, &cs));
+    if (cs != hipStreamCaptureStatusNone)
+      return obs::set_error(ctx, OBS_E_INVALID, "obs_attn_decode: run once before capturing (workspace allocation)");
+    OBS_HIP_TRY(ctx, hipMalloc(&ctx->attn_ws, AW_BYTES));
+    OBS_HIP_TRY(ctx, hipMemset(ctx->attn_ws, 0, AW_BYTES));
+    OBS_HIP_TRY(ctx, hipDeviceSynchronize());
+  }
+  const float* rope = nullptr;
+  int rc = obs::ensure_rope_table(ctx, theta, max_len, &rope);
+  if (rc != OBS_OK) return rc;
+  AttnArgs a{L->q_w, L->q_s, L->q_b, L->k_w, L->k_s, L->k_b, L->v_w, L->v_s, L->v_b, L->o_w, L->o_s, L->o_b,
+             L->in_norm, L->q_norm, L->k_norm, x, x1, k_cache, v_cache_t, state, rope,
+             static_cast<unsigned char*>(ctx->attn_ws), max_len, eps,
+             1.4426950408889634f / __builtin_sqrtf(static_cast<float>(AHD))};
+  OBS_LAUNCH(ctx, "attn_fused", attn_fused_kernel<<<ANWG, 256, 0, ctx->stream>>>(a));
+  return OBS_OK;
+}
+
+}  // extern "C"

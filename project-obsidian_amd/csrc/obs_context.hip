@@ -106,6 +106,9 @@ void obs_destroy(obs_ctx* ctx) {
   if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
   (void)obs_profile_clear(ctx);
   if (ctx->decode_ws) (void)hipFree(ctx->decode_ws);
+  if (ctx->fused_ws) (void)hipFree(ctx->fused_ws);
+  if (ctx->attn_ws) (void)hipFree(ctx->attn_ws);
+  if (ctx->rope_table) (void)hipFree(ctx->rope_table);
   if (ctx->ev_start) (void)hipEventDestroy(ctx->ev_start);
   if (ctx->ev_stop) (void)hipEventDestroy(ctx->ev_stop);
   if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);

@@ -320,7 +320,9 @@ int obs_set_decode_path(obs_ctx* ctx, int path) {
 
 int obs_device_status(obs_ctx* ctx) {
   if (!ctx) return OBS_E_INVALID;
-  return obs::fused_decode_status(ctx);
+  const int a = obs::fused_decode_status(ctx);
+  const int b = obs::attn_fused_status(ctx);
+  return a != OBS_OK ? a : b;
 }
 
 }  // extern "C"

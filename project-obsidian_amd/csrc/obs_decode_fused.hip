@@ -73,21 +73,6 @@ struct FusedArgs {
   int norm_topk;
 };
 
-// Slot stores are system-scope (written through to memory): measured on MI355X,
-// an agent-scope store polled by an agent-scope load from a CU of the SAME XCD
-// takes ~2.7 us to become visible, a write-through store ~0.55 us.
-__device__ __forceinline__ void slot_store(uint64_t* p, uint32_t epoch, float v) {
-  __hip_atomic_store(p, (static_cast<uint64_t>(epoch) << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
-                     __HIP_MEMORY_SCOPE_SYSTEM);
-}
-__device__ __forceinline__ uint64_t slot_load(const uint64_t* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ bool slot_ready(uint64_t v, uint32_t epoch) {
-  return static_cast<uint32_t>(v >> 32) == epoch;
-}
-__device__ __forceinline__ float slot_val(uint64_t v) { return __uint_as_float(static_cast<uint32_t>(v)); }
-
 __device__ __forceinline__ void raise_error(unsigned char* ws) {
   __hip_atomic_store(reinterpret_cast<uint32_t*>(ws + WS_ERR), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }

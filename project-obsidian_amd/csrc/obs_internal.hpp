@@ -36,6 +36,12 @@ struct obs_ctx {
   size_t decode_ws_bytes = 0;
   // fused decode workspace (epoch-tagged exchange slots + counters), zeroed once
   void* fused_ws = nullptr;
+  // fused attention-half workspace (exchange slots + counters), zeroed once
+  void* attn_ws = nullptr;
+  // RoPE (cos, sin) table [rope_len][64][2] fp32 for rope_theta
+  float* rope_table = nullptr;
+  uint32_t rope_len = 0;
+  float rope_theta = 0.0f;
   int decode_path = 0;  // OBS_DECODE_AUTO / _MULTI / _FUSED
   // in-stream kernel timing
   bool prof_on = false;
@@ -95,6 +101,16 @@ int launch_fused_decode(obs_ctx* ctx, const obs_moe_config* cfg, const obs_moe_l
                         const uint16_t* residual, uint16_t* y, int32_t* ids_out, float* w_out);
 // Reads and clears the fused path's device error flag (synchronizes).
 int fused_decode_status(obs_ctx* ctx);
+
+// Fused attention half of a decode layer (obs_attention_fused.hip): its
+// device error flag, read and cleared (synchronizes).
+int attn_fused_status(obs_ctx* ctx);
+
+// The context's RoPE table for (theta, max_len) (obs_attention.hip): entry
+// [p][i] = (cos, sin) of fl32(p * fl32(theta^(-2i/128))), each evaluated in
+// double and rounded once (attn_prep_kernel's values). Built on first use
+// (not under graph capture).
+int ensure_rope_table(obs_ctx* ctx, float theta, uint32_t max_len, const float** out);
 
 }  // namespace obs
 
@@ -213,6 +229,24 @@ __device__ __forceinline__ float group8_sum(float v) {
 }
 
 // Sum over each 32-lane half of the wave (every lane of the half gets it).
+// Epoch-tagged exchange slots between the workgroups of one launch:
+// (epoch << 32) | fp32 bits, so a reader knows a value is this launch's from
+// the value itself (no flag, no fence, no clearing between launches). Stores
+// are system-scope (written through to memory): measured on MI355X, an
+// agent-scope store polled by an agent-scope load from a CU of the same XCD
+// takes ~2.7 us to become visible, a write-through store ~0.55 us.
+__device__ __forceinline__ void slot_store(uint64_t* p, uint32_t epoch, float v) {
+  __hip_atomic_store(p, (static_cast<uint64_t>(epoch) << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ __forceinline__ uint64_t slot_load(const uint64_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ bool slot_ready(uint64_t v, uint32_t epoch) {
+  return static_cast<uint32_t>(v >> 32) == epoch;
+}
+__device__ __forceinline__ float slot_val(uint64_t v) { return __uint_as_float(static_cast<uint32_t>(v)); }
+
 __device__ __forceinline__ float half_wave_sum(float v) {
   v = v + dpp_f32<DPP_XOR1>(v);
   v = v + dpp_f32<DPP_XOR2>(v);

@@ -58,6 +58,7 @@ EXPORTS = (
     "obs_ckpt_read", "obs_moe_layer_bytes", "obs_ckpt_load_moe_layer", "obs_ckpt_load_tensor",
     "obs_q4_gemv", "obs_attn_prep", "obs_sdpa_workspace", "obs_sdpa_decode", "obs_embed_q4",
     "obs_argmax_workspace", "obs_argmax", "obs_embed_q4_rows", "obs_attn_prep_rows", "obs_sdpa_prefill",
+    "obs_attn_decode",
 )
 
 
@@ -82,6 +83,12 @@ class ObsMoeLayer(C.Structure):
 class ObsGemvPart(C.Structure):
     _fields_ = [("w", C.c_void_p), ("scales", C.c_void_p), ("biases", C.c_void_p), ("y_f32", C.c_void_p),
                 ("y_bf16", C.c_void_p), ("residual", C.c_void_p), ("rows", C.c_uint32)]
+
+
+class ObsAttnLayer(C.Structure):
+    KEYS = ("q_w", "q_s", "q_b", "k_w", "k_s", "k_b", "v_w", "v_s", "v_b", "o_w", "o_s", "o_b",
+            "in_norm", "q_norm", "k_norm")
+    _fields_ = [(k, C.c_void_p) for k in KEYS]
 
 
 class ObsTensorInfo(C.Structure):
@@ -171,6 +178,7 @@ def lib() -> C.CDLL:
         "obs_attn_prep_rows": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, u32, u32, u32, u32, f32, f32, u32, u32, u32,
                                      u32]),
         "obs_sdpa_prefill": (i32, [vp, vp, vp, vp, vp, u32, u32, u32, u32, u32, u32, u32]),
+        "obs_attn_decode": (i32, [vp, C.POINTER(ObsAttnLayer), vp, vp, vp, u32, f32, f32, vp, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -407,6 +415,15 @@ class ObsidianExecutor:
     def argmax(self, x, n: int, state, ws, ws_bytes: Optional[int] = None) -> None:
         ws_bytes = ws.nbytes if ws_bytes is None else ws_bytes
         self._check(lib().obs_argmax(self.ctx, _ptr(x), n, _ptr(state), _ptr(ws), ws_bytes))
+
+    def attn_decode(self, layer: Dict, x, k_cache, v_cache_t, max_len: int, eps: float, theta: float, state,
+                    x1) -> None:
+        """The attention half of a decode layer in one launch (Qwen3-30B-A3B
+        shape): layer holds ATTN_KEYS-style device pointers (q_w .. o_b,
+        in_norm, q_norm, k_norm)."""
+        L = ObsAttnLayer(*(_ptr(layer[k]) for k in ObsAttnLayer.KEYS))
+        self._check(lib().obs_attn_decode(self.ctx, C.byref(L), _ptr(x), _ptr(k_cache), _ptr(v_cache_t), max_len,
+                                          float(eps), float(theta), _ptr(state), _ptr(x1)))
 
     # -- prefill of the layers around the MoE block (forward.rs:114-160) --
     def embed_q4_rows(self, w, s, b, hidden: int, vocab: int, tokens, n_tokens: int, out, group: int = 64) -> None:

@@ -86,17 +86,28 @@ class Model:
         self.moe_cfg = c.moe()
         self.graph: Optional[int] = None
         self._pf: Optional[Dict] = None      # prefill buffers, grown to the largest batch
+        self.use_fused_attention = True      # one-launch attention half where the shape allows
         self.last_seq: List[int] = []        # the tokens whose keys and values the caches hold (run_turn)
         self.last_reused = 0
         self.last_prefilled = 0
 
     # -- the pieces of forward_layer (forward.rs:398-443) ------------------
+    def fused_attention(self) -> bool:
+        """Whether the attention half runs as one launch (obs_attn_decode: the
+        Qwen3-30B-A3B attention shape on a device with 256 CUs)."""
+        c = self.cfg
+        return self.use_fused_attention and (c.hidden, c.n_heads, c.n_kv, c.head_dim) == (2048, 32, 4, 128)
+
     def forward_layer(self, il: int, ids_out=None, w_out=None) -> None:
         """self.x <- layer il of self.x at the state's position (ids_out, w_out:
         optional device buffers for the layer's routing)."""
         c, e, L = self.cfg, self.exe, self.layers[il]
         kc, vc = self.caches[il]
         qd, kvd = c.n_heads * c.head_dim, c.n_kv * c.head_dim
+        if self.fused_attention():  # forward.rs:403-418 in one launch
+            e.attn_decode(L, self.x, kc, vc, c.max_len, c.rms_eps, c.rope_theta, self.state, self.x1)
+            e.moe_decode(self.moe_cfg, L["moe"], self.x1, self.x, residual=self.x1, ids_out=ids_out, w_out=w_out)
+            return
         # input RMSNorm (forward.rs:403) fused into the q/k/v mat-vec
         e.q4_gemv(self.x, c.hidden, [(L["q_w"], L["q_s"], L["q_b"], qd, None, self.q, None),
                                      (L["k_w"], L["k_s"], L["k_b"], kvd, None, self.k, None),

@@ -18,20 +18,30 @@ from obsidian_hip import synth
 
 pytestmark = pytest.mark.gpu
 
-CFG = D.DecoderConfig(n_layers=2, hidden=2048, n_heads=16, n_kv=2, head_dim=128, n_exp=8, top_k=2, inter=256,
-                      vocab=512, max_len=64)
-OCFG = {"hidden": CFG.hidden, "n_heads": CFG.n_heads, "n_kv": CFG.n_kv, "head_dim": CFG.head_dim,
-        "eps": CFG.rms_eps, "theta": CFG.rope_theta, "top_k": CFG.top_k, "norm_topk": CFG.norm_topk,
-        "vocab": CFG.vocab}
+# 16 query heads: the attention half as separate launches; the Qwen3-30B-A3B
+# attention shape (32 / 4 heads): one launch (obs_attn_decode)
+CFGS = {
+    "split": D.DecoderConfig(n_layers=2, hidden=2048, n_heads=16, n_kv=2, head_dim=128, n_exp=8, top_k=2,
+                             inter=256, vocab=512, max_len=64),
+    "fused": D.DecoderConfig(n_layers=2, hidden=2048, n_heads=32, n_kv=4, head_dim=128, n_exp=8, top_k=2,
+                             inter=256, vocab=512, max_len=64),
+}
 
 
-@pytest.fixture(scope="module")
-def model(exe):
-    layers, glob = synth.decoder_weights(3, CFG.n_layers, CFG.hidden, CFG.n_heads, CFG.n_kv, CFG.head_dim,
-                                         CFG.n_exp, CFG.inter, CFG.vocab)
+def _ocfg(c):
+    return {"hidden": c.hidden, "n_heads": c.n_heads, "n_kv": c.n_kv, "head_dim": c.head_dim, "eps": c.rms_eps,
+            "theta": c.rope_theta, "top_k": c.top_k, "norm_topk": c.norm_topk, "vocab": c.vocab}
+
+
+@pytest.fixture(scope="module", params=sorted(CFGS))
+def model(exe, request):
+    cfg = CFGS[request.param]
+    layers, glob = synth.decoder_weights(3, cfg.n_layers, cfg.hidden, cfg.n_heads, cfg.n_kv, cfg.head_dim,
+                                         cfg.n_exp, cfg.inter, cfg.vocab)
     dl, dg = D.upload_weights(exe, layers, glob)
-    m = D.Model(exe, CFG, dl, dg)
-    moes = [O.Layer(t, CFG.n_exp, CFG.hidden, CFG.inter) for t in layers]
+    m = D.Model(exe, cfg, dl, dg)
+    assert m.fused_attention() == (request.param == "fused")
+    moes = [O.Layer(t, cfg.n_exp, cfg.hidden, cfg.inter) for t in layers]
     yield m, layers, glob, moes
     m.close()
 
@@ -50,6 +60,7 @@ def _close(got, want, tol=1e-2):
 
 def test_decoder_stages_match_oracle(exe, model):
     m, layers, glob, moes = model
+    CFG, OCFG = m.cfg, _ocfg(m.cfg)
     caches = [(np.zeros((CFG.n_kv, CFG.max_len, CFG.head_dim), np.uint16),
                np.zeros((CFG.n_kv, CFG.max_len, CFG.head_dim), np.uint16)) for _ in range(CFG.n_layers)]
     ids_buf = exe.alloc(CFG.top_k, np.int32)
@@ -87,6 +98,7 @@ def test_decoder_stages_match_oracle(exe, model):
 
 def test_graph_replay_equals_eager_steps(exe, model):
     m = model[0]
+    CFG = m.cfg
     m.close()
     eager = m.generate(7, 10, 6, graph=False)
     logits_eager = m.logits.download()
@@ -98,6 +110,7 @@ def test_graph_replay_equals_eager_steps(exe, model):
 
 def test_generation_stays_in_the_cache(exe, model):
     m = model[0]
+    CFG = m.cfg
     with pytest.raises(ValueError):
         m.generate(1, CFG.max_len - 2, 5)
     with pytest.raises(ValueError):
