@@ -206,7 +206,8 @@ __global__ void __launch_bounds__(256) q4_gemv_kernel(const uint16_t* __restrict
 // ROWS = false (decode): one token at pos = state[0], one wave per head; the
 // position is read with a vector load issued after the head's loads (a scalar
 // load would be waited for together with the kernel arguments, before any
-// other load). ROWS = true (prefill): one workgroup per token of q (rows of
+// other load). ROWS = true (prefill; cosines and sines from the context's
+// RoPE table, the same values): one workgroup per token of q (rows of
 // q_ld elements holding nh x 128), k, v (rows of kv_ld holding nkv x 128) at
 // position pos0 + token; wave w owns heads w, w + 4, ...
 template <bool ROWS>
@@ -217,7 +218,8 @@ __global__ void __launch_bounds__(256) attn_prep_kernel(uint16_t* __restrict__ q
                                                         uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache_t,
                                                         uint32_t nh, uint32_t nkv, uint32_t max_len, float eps,
                                                         float theta, const int32_t* __restrict__ state, uint32_t pos0,
-                                                        uint32_t n_tok, uint32_t q_ld, uint32_t kv_ld) {
+                                                        uint32_t n_tok, uint32_t q_ld, uint32_t kv_ld,
+                                                        const float* __restrict__ rope) {
   const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
   const uint32_t heads = nh + 2u * nkv;
   const uint32_t tok = ROWS ? blockIdx.x : 0u;
@@ -247,17 +249,34 @@ __global__ void __launch_bounds__(256) attn_prep_kernel(uint16_t* __restrict__ q
   const uint32_t pos = static_cast<uint32_t>(pos_i);
   const bool pos_ok = pos_i >= 0 && pos < max_len;
   float cs[2], sn[2];
+  if (ROWS) {  // the context's table holds exactly these values (rope_table_kernel)
+    const float4 t = *reinterpret_cast<const float4*>(rope + static_cast<size_t>(min(pos, max_len - 1u)) * 128u +
+                                                      4u * (lane & 31u));
+    cs[0] = t.x; sn[0] = t.y; cs[1] = t.z; sn[1] = t.w;
+  } else {
 #pragma unroll
-  for (uint32_t j = 0; j < 2; ++j) {
-    const uint32_t i = (c0 + j) & 63u;  // pair index
-    const float f = static_cast<float>(pow(static_cast<double>(theta), -2.0 * static_cast<double>(i) / 128.0));
-    const float angle = static_cast<float>(pos) * f;
-    cs[j] = static_cast<float>(cos(static_cast<double>(angle)));
-    sn[j] = static_cast<float>(sin(static_cast<double>(angle)));
+    for (uint32_t j = 0; j < 2; ++j) {
+      const uint32_t i = (c0 + j) & 63u;  // pair index
+      const float f = static_cast<float>(pow(static_cast<double>(theta), -2.0 * static_cast<double>(i) / 128.0));
+      const float angle = static_cast<float>(pos) * f;
+      cs[j] = static_cast<float>(cos(static_cast<double>(angle)));
+      sn[j] = static_cast<float>(sin(static_cast<double>(angle)));
+    }
   }
   const bool first = lane < 32u;
-  for (uint32_t head = h_first; head < heads; head += h_step) {
-    const uint32_t xv = head == h_first ? xv0 : *reinterpret_cast<const uint32_t*>(head_src(head) + c0);
+  // heads in groups of 4: the group's loads first (clamped to a valid head;
+  // unused past the last), so a wave waits once per group, not once per head
+  for (uint32_t hb = h_first; hb < heads; hb += 4u * h_step) {
+  uint32_t xvs[4];
+#pragma unroll
+  for (uint32_t j = 0; j < 4; ++j)
+    xvs[j] = j == 0 && hb == h_first ? xv0
+                                     : *reinterpret_cast<const uint32_t*>(head_src(min(hb + j * h_step, heads - 1u)) + c0);
+#pragma unroll
+  for (uint32_t j = 0; j < 4; ++j) {
+    const uint32_t head = hb + j * h_step;
+    if (head >= heads) break;  // wave-uniform
+    const uint32_t xv = xvs[j];
     const bool is_v = head >= nh + nkv, is_q = head < nh;
     const uint32_t hk = is_q ? head : (is_v ? head - nh - nkv : head - nh);
     if (is_v) {  // value head: transposed cache column pos
@@ -290,6 +309,7 @@ __global__ void __launch_bounds__(256) attn_prep_kernel(uint16_t* __restrict__ q
     } else if (pos_ok) {
       *reinterpret_cast<uint32_t*>(k_cache + (static_cast<size_t>(hk) * max_len + pos) * HD + c0) = out;
     }
+  }
   }
 }
 
@@ -633,15 +653,26 @@ __global__ void __launch_bounds__(256, 2) sdpa_prefill_kernel(const uint16_t* __
       }
     }
   };
-  u32x4_t stage[4];
-  load_blk(0u, stage);
-  store_blk(0u, stage);
+  // two register stages in turn (no copies between them): block b + 2's loads
+  // are issued while block b is computed from LDS and block b + 1, loaded an
+  // iteration earlier, goes from registers to the other LDS buffer. Past the
+  // end the last block is loaded again (unused).
+  u32x4_t sa[4], sb[4];
+  load_blk(0u, sa);
+  load_blk(min(1u, nblk - 1u), sb);
+  store_blk(0u, sa);
   __syncthreads();
-  for (uint32_t blk = 0; blk < nblk; ++blk) {
-    load_blk(min(blk + 1u, nblk - 1u), stage);  // past the end: the last block again (unused)
-    run_blk(blk & 1u, blk);
-    store_blk((blk + 1u) & 1u, stage);
+  for (uint32_t blk = 0;;) {
+    load_blk(min(blk + 2u, nblk - 1u), sa);
+    run_blk(0u, blk);
+    store_blk(1u, sb);
     __syncthreads();
+    if (++blk >= nblk) break;
+    load_blk(min(blk + 2u, nblk - 1u), sb);
+    run_blk(1u, blk);
+    store_blk(0u, sa);
+    __syncthreads();
+    if (++blk >= nblk) break;
   }
   // normalise: lane holds O[column 4 g + i][dim 16 nt + col] of each group
 #pragma unroll
@@ -850,7 +881,7 @@ int obs_attn_prep(obs_ctx* ctx, uint16_t* q, const uint16_t* k, const uint16_t* 
   const uint32_t heads = n_heads + 2u * n_kv;
   OBS_LAUNCH(ctx, "attn_prep", attn_prep_kernel<false><<<(heads + 3u) / 4u, 256, 0, ctx->stream>>>(
                                    q, k, v, q_norm, k_norm, k_cache, v_cache_t, n_heads, n_kv, max_len, eps, theta, state,
-                                   0u, 1u, 0u, 0u));
+                                   0u, 1u, 0u, 0u, nullptr));
   return OBS_OK;
 }
 
@@ -938,10 +969,13 @@ int obs_attn_prep_rows(obs_ctx* ctx, uint16_t* q, const uint16_t* k, const uint1
     return obs::set_error(ctx, OBS_E_ALIGN, "obs_attn_prep_rows: q, k, v and the key cache must be 4-byte aligned");
   if (n_tokens == 0) return OBS_OK;
   if (n_tokens > 0x7fffffffu) return obs::set_error(ctx, OBS_E_SHAPE, "obs_attn_prep_rows: too many tokens");
+  const float* rope = nullptr;
+  const int rc = obs::ensure_rope_table(ctx, theta, max_len, &rope);
+  if (rc != OBS_OK) return rc;
   OBS_LAUNCH(ctx, "attn_prep_rows", attn_prep_kernel<true><<<n_tokens, 256, 0,
                                                               ctx->stream>>>(q, k, v, q_norm, k_norm, k_cache, v_cache_t,
                                                                              n_heads, n_kv, max_len, eps, theta, nullptr,
-                                                                             pos0, n_tokens, q_ld, kv_ld));
+                                                                             pos0, n_tokens, q_ld, kv_ld, rope));
   return OBS_OK;
 }
 

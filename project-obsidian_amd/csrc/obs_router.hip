@@ -27,9 +27,10 @@ constexpr int ROUTER_TOKENS_PER_WAVE = 8;
 // grid: x = ceil(n_exp / (4 EPW)) (4 waves per block, EPW expert rows each),
 //       y = ceil(T / ROUTER_TOKENS_PER_WAVE)
 // WPL = packed words per lane (in = 64 lanes * 4 cols * WPL). A wave keeps its
-// EPW rows dequantized in registers and streams its tokens' activations once
-// for all of them: with one row per wave every activation row was read from
-// L2 once per expert (1 GB at T = 2048), which bounded the launch.
+// EPW rows dequantized in registers; the workgroup stages its 8 tokens'
+// activation rows in LDS once for its 4 waves. With one row per wave and no
+// staging every activation row was read from L2 once per expert (1 GB at
+// T = 2048), which bounded the launch.
 template <int WPL, int EPW>
 __global__ void __launch_bounds__(256) q8_gate_logits_kernel(const uint32_t* __restrict__ w8,
                                                              const uint16_t* __restrict__ s,
@@ -39,9 +40,19 @@ __global__ void __launch_bounds__(256) q8_gate_logits_kernel(const uint32_t* __r
                                                              uint32_t in, uint32_t n_exp,
                                                              uint32_t group) {
   constexpr int C = 4 * WPL;  // columns per lane
+  extern __shared__ __attribute__((aligned(16))) uint16_t s_x[];  // [ROUTER_TOKENS_PER_WAVE][in]
   const uint32_t lane = threadIdx.x & 63;
+  const uint32_t t0 = blockIdx.y * ROUTER_TOKENS_PER_WAVE;
+  const uint32_t nt = min(static_cast<uint32_t>(ROUTER_TOKENS_PER_WAVE), T - t0);
+  {
+    const uint32_t row_chunks = in / 8u;  // 16-byte chunks per activation row
+    for (uint32_t c = threadIdx.x; c < nt * row_chunks; c += 256u)
+      *reinterpret_cast<uint4*>(s_x + 8u * c) =
+          *reinterpret_cast<const uint4*>(x + static_cast<uint64_t>(t0 + c / row_chunks) * in + 8u * (c % row_chunks));
+  }
+  __syncthreads();
   const uint32_t e0 = (blockIdx.x * 4 + threadIdx.x / 64) * EPW;
-  if (e0 >= n_exp) return;
+  if (e0 >= n_exp) return;  // wave-uniform; no barrier follows
   const uint32_t words = in / 4, groups = in / group;
   // dequantize this lane's C weights of each row once (exact: byte*scale has <= 16 bits)
   float wv[EPW][C];
@@ -61,9 +72,8 @@ __global__ void __launch_bounds__(256) q8_gate_logits_kernel(const uint32_t* __r
         wv[r][4 * j + q] = __builtin_fmaf(static_cast<float>((word >> (8 * q)) & 0xffu), sc, bi);
     }
   }
-  const uint32_t t0 = blockIdx.y * ROUTER_TOKENS_PER_WAVE;
-  for (uint32_t t = t0; t < t0 + ROUTER_TOKENS_PER_WAVE && t < T; ++t) {
-    const uint16_t* xr = x + static_cast<uint64_t>(t) * in + lane * C;
+  for (uint32_t t = t0; t < t0 + nt; ++t) {
+    const uint16_t* xr = s_x + (t - t0) * in + lane * C;
     float xf[C];
 #pragma unroll
     for (int c = 0; c < C; c += 8) {
@@ -130,11 +140,12 @@ int launch_gate_logits(obs_ctx* ctx, const uint32_t* w8, const uint16_t* s, cons
   // 4 rows per wave (2 at in = 4096, whose rows hold 64 columns per lane)
   const uint32_t ty = (T + ROUTER_TOKENS_PER_WAVE - 1) / ROUTER_TOKENS_PER_WAVE;
   const dim3 grid4((n_exp + 15) / 16, ty), grid2((n_exp + 7) / 8, ty);
+  const size_t lds = sizeof(uint16_t) * ROUTER_TOKENS_PER_WAVE * in;  // 64 KB at in = 4096
   switch (in) {
-    case 512: OBS_LAUNCH(ctx, "q8_gate_logits", q8_gate_logits_kernel<2, 4><<<grid4, 256, 0, ctx->stream>>>(w8, s, b, x, logits, T, in, n_exp, group)); break;
-    case 1024: OBS_LAUNCH(ctx, "q8_gate_logits", q8_gate_logits_kernel<4, 4><<<grid4, 256, 0, ctx->stream>>>(w8, s, b, x, logits, T, in, n_exp, group)); break;
-    case 2048: OBS_LAUNCH(ctx, "q8_gate_logits", q8_gate_logits_kernel<8, 4><<<grid4, 256, 0, ctx->stream>>>(w8, s, b, x, logits, T, in, n_exp, group)); break;
-    default: OBS_LAUNCH(ctx, "q8_gate_logits", q8_gate_logits_kernel<16, 2><<<grid2, 256, 0, ctx->stream>>>(w8, s, b, x, logits, T, in, n_exp, group)); break;
+    case 512: OBS_LAUNCH(ctx, "q8_gate_logits", q8_gate_logits_kernel<2, 4><<<grid4, 256, lds, ctx->stream>>>(w8, s, b, x, logits, T, in, n_exp, group)); break;
+    case 1024: OBS_LAUNCH(ctx, "q8_gate_logits", q8_gate_logits_kernel<4, 4><<<grid4, 256, lds, ctx->stream>>>(w8, s, b, x, logits, T, in, n_exp, group)); break;
+    case 2048: OBS_LAUNCH(ctx, "q8_gate_logits", q8_gate_logits_kernel<8, 4><<<grid4, 256, lds, ctx->stream>>>(w8, s, b, x, logits, T, in, n_exp, group)); break;
+    default: OBS_LAUNCH(ctx, "q8_gate_logits", q8_gate_logits_kernel<16, 2><<<grid2, 256, lds, ctx->stream>>>(w8, s, b, x, logits, T, in, n_exp, group)); break;
   }
   return OBS_OK;
 }
