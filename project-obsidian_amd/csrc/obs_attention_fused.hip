@@ -106,14 +106,16 @@ attn_fused_kernel(AttnArgs a) {
   // launch count first (its round trip gates the first publish), the
   // position, the activations and every weight row, then what depends on the
   // position (the first key/value block, the RoPE cosines and sines)
-  // every workgroup adds 1 to the count as it exits: the quotient counts the
-  // earlier launches (as in decode_fused_kernel). Every thread loads it (the
-  // same address): a load under a branch is waited for at the branch's join.
-  const uint64_t counted = __hip_atomic_load(ctl_count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  const uint32_t err = __hip_atomic_load(ctl_err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  // the position through the scalar cache (its own counter: the key/value
-  // loads that need it wait for it alone, not for the vector loads before them)
-  const int32_t pos_i = a.state[0];
+  // the position, as the first vector load (a per-lane index keeps it off the
+  // scalar cache, whose load the compiler issued late and which returned only
+  // after the flood of row loads): the key/value loads that need it wait for
+  // it alone, the memory counter being in order
+  int32_t pos_i;
+  {
+    uint32_t zero;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(zero));
+    pos_i = a.state[zero];
+  }
   __builtin_amdgcn_sched_barrier(0);
   uint4 xq[4], nq[4];
 #pragma unroll
@@ -189,19 +191,18 @@ attn_fused_kernel(AttnArgs a) {
   load_block(min(b0 + wave, nblk - 1u));
   const f32x4_t csn = *reinterpret_cast<const f32x4_t*>(a.rope + static_cast<size_t>(min(pos, max_len - 1u)) * 128u +
                                                         4u * (lane & 31u));
-  __builtin_amdgcn_sched_barrier(0);
+  // every workgroup adds 1 to the count as it exits: the quotient counts the
+  // earlier launches (as in decode_fused_kernel). One thread per workgroup
+  // loads it, last: these coherent loads go to memory, and from every thread
+  // they made a hot spot of two addresses; under a branch they are waited
+  // for at its join, which here follows every other load.
+  uint64_t counted = 0;
+  uint32_t err = 0;
   if (tid == 0) {
-    s_epoch = static_cast<uint32_t>(counted / ANWG) + 1u;
-    s_abort = err != 0u;
-    s_fail = 0;
+    counted = __hip_atomic_load(ctl_count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    err = __hip_atomic_load(ctl_err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  __syncthreads();
-  const uint32_t epoch = s_epoch;
-  if (s_abort) {  // a previous launch failed: the host must reset first
-    if (tid == 0) __hip_atomic_fetch_add(ctl_count, uint64_t{1}, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return;
-  }
-
+  __builtin_amdgcn_sched_barrier(0);
   OBS_ATTN_MARK(1);
   // ---- 1. q/k/v rows of rmsnorm(x) (obs_rmsnorm's sequence), rounded to bf16
   {
@@ -249,8 +250,21 @@ attn_fused_kernel(AttnArgs a) {
       part = wave_sum_asc(part);
       mine = lane == k ? bf16_to_f32(f32_to_bf16(part)) : mine;
     }
-    if (lane < A_RPW) slot_store(qkv_slots + A_RPW * wave_g + lane, epoch, mine);
+    // the epoch is needed from the first publish on: the barrier sits here,
+    // after the rows' wait, not before the compute
+    if (tid == 0) {
+      s_epoch = static_cast<uint32_t>(counted / ANWG) + 1u;
+      s_abort = err != 0u;
+      s_fail = 0;
+    }
+    __syncthreads();
+    if (s_abort) {  // a previous launch failed: the host must reset first
+      if (tid == 0) __hip_atomic_fetch_add(ctl_count, uint64_t{1}, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return;
+    }
+    if (lane < A_RPW) slot_store(qkv_slots + A_RPW * wave_g + lane, s_epoch, mine);
   }
+  const uint32_t epoch = s_epoch;
   OBS_ATTN_MARK(2);
   if (attends) {  // workgroup-uniform
 
