@@ -23,8 +23,11 @@
 //      publishes them as bf16 pairs;
 //   4. every workgroup polls the 4,096 attention outputs into LDS and each
 //      wave computes 2 rows of x1 = x + W_o attn.
-// All weight, activation and cache loads that do not depend on an exchange
-// are issued at the start, so the exchanges overlap the memory stream.
+// Every weight, activation and cache load that does not depend on an exchange
+// is issued before the first exchange: the q/k/v rows at the start, the first
+// key/value block and the o rows right after the q/k/v publish, so the
+// exchanges overlap the memory stream and the q/k/v rows have the bandwidth
+// to themselves.
 // Every wait is bounded (100 ms of the constant clock); a time-out sets the
 // workspace's error flag, reported and cleared by obs_device_status.
 #include "obs_internal.hpp"
@@ -102,14 +105,16 @@ attn_fused_kernel(AttnArgs a) {
   uint64_t* attn_slots = reinterpret_cast<uint64_t*>(a.ws + AW_ATTN);
 
   OBS_ATTN_MARK(0);
-  // ---- 0. loads that need no exchange, in the order they are used: the
-  // launch count first (its round trip gates the first publish), the
-  // position, the activations and every weight row, then what depends on the
-  // position (the first key/value block, the RoPE cosines and sines)
+  // ---- 0. loads that the q/k/v rows and the RoPE need, in the order they are
+  // used: the position, the activations, the q/k/v rows, then the RoPE cosines
+  // and sines at the position and the launch count. The first key/value block
+  // and the o rows follow the q/k/v publish: issued here they shared the
+  // bandwidth with the q/k/v rows, and the publish (which waits for the count,
+  // loaded last) waited for them too.
   // the position, as the first vector load (a per-lane index keeps it off the
   // scalar cache, whose load the compiler issued late and which returned only
-  // after the flood of row loads): the key/value loads that need it wait for
-  // it alone, the memory counter being in order
+  // after the flood of row loads): the RoPE load that needs it waits for it
+  // alone, the memory counter being in order
   int32_t pos_i;
   {
     uint32_t zero;
@@ -139,18 +144,6 @@ attn_fused_kernel(AttnArgs a) {
   }
   uint4 oq[A_ORPW][2];
   uint16_t osc[A_ORPW][2], obi[A_ORPW][2], ores[A_ORPW];
-#pragma unroll
-  for (uint32_t k = 0; k < A_ORPW; ++k) {
-    const uint32_t r = A_ORPW * wave_g + k;
-#pragma unroll
-    for (uint32_t sg = 0; sg < 2; ++sg) {
-      oq[k][sg] = reinterpret_cast<const uint4*>(a.o_w + static_cast<size_t>(r) * (AQD / 8u) + 256u * sg)[lane];
-      const size_t gi = static_cast<size_t>(r) * (AQD / 64u) + 32u * sg + lane / 2u;
-      osc[k][sg] = a.o_s[gi];
-      obi[k][sg] = a.o_b[gi];
-    }
-    ores[k] = a.x[r];
-  }
   const uint32_t wq = *reinterpret_cast<const uint32_t*>(a.q_norm + 2u * lane);
   const uint32_t wk = *reinterpret_cast<const uint32_t*>(a.k_norm + 2u * lane);
   // this workgroup's split of kv head kv, and the position's loads
@@ -184,11 +177,8 @@ attn_fused_kernel(AttnArgs a) {
       va[nt][1] = *reinterpret_cast<const u32x2_t*>(vr + 16);
     }
   };
-  // the position's loads: the wave's first key/value block (clamped into the
-  // sequence; unused by workgroups that do not attend or waves without a
-  // block) and the lane's RoPE cosines and sines, pairs (2 lane, 2 lane + 1)
-  // mod 64: (cos, sin, cos, sin)
-  load_block(min(b0 + wave, nblk - 1u));
+  // the lane's RoPE cosines and sines at the position, pairs (2 lane,
+  // 2 lane + 1) mod 64: (cos, sin, cos, sin)
   const f32x4_t csn = *reinterpret_cast<const f32x4_t*>(a.rope + static_cast<size_t>(min(pos, max_len - 1u)) * 128u +
                                                         4u * (lane & 31u));
   // every workgroup adds 1 to the count as it exits: the quotient counts the
@@ -263,6 +253,22 @@ attn_fused_kernel(AttnArgs a) {
       return;
     }
     if (lane < A_RPW) slot_store(qkv_slots + A_RPW * wave_g + lane, s_epoch, mine);
+  }
+  // the wave's first key/value block (clamped into the sequence; unused by
+  // workgroups that do not attend or waves without a block)
+  load_block(min(b0 + wave, nblk - 1u));
+  // the o rows and the residual, needed only by the last phase
+#pragma unroll
+  for (uint32_t k = 0; k < A_ORPW; ++k) {
+    const uint32_t r = A_ORPW * wave_g + k;
+#pragma unroll
+    for (uint32_t sg = 0; sg < 2; ++sg) {
+      oq[k][sg] = reinterpret_cast<const uint4*>(a.o_w + static_cast<size_t>(r) * (AQD / 8u) + 256u * sg)[lane];
+      const size_t gi = static_cast<size_t>(r) * (AQD / 64u) + 32u * sg + lane / 2u;
+      osc[k][sg] = a.o_s[gi];
+      obi[k][sg] = a.o_b[gi];
+    }
+    ores[k] = a.x[r];
   }
   const uint32_t epoch = s_epoch;
   OBS_ATTN_MARK(2);
