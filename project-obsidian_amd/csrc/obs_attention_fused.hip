@@ -106,8 +106,8 @@ attn_fused_kernel(AttnArgs a) {
 
   OBS_ATTN_MARK(0);
   // ---- 0. loads that the q/k/v rows and the RoPE need, in the order they are
-  // used: the position, the activations, the q/k/v rows, then the RoPE cosines
-  // and sines at the position and the launch count. The first key/value block
+  // used: the position, the activations, the q/k/v rows, the launch count,
+  // then the RoPE cosines and sines at the position. The first key/value block
   // and the o rows follow the q/k/v publish: issued here they shared the
   // bandwidth with the q/k/v rows, and the publish (which waits for the count,
   // loaded last) waited for them too.
@@ -177,21 +177,26 @@ attn_fused_kernel(AttnArgs a) {
       va[nt][1] = *reinterpret_cast<const u32x2_t*>(vr + 16);
     }
   };
-  // the lane's RoPE cosines and sines at the position, pairs (2 lane,
-  // 2 lane + 1) mod 64: (cos, sin, cos, sin)
-  const f32x4_t csn = *reinterpret_cast<const f32x4_t*>(a.rope + static_cast<size_t>(min(pos, max_len - 1u)) * 128u +
-                                                        4u * (lane & 31u));
+  // every row load above is issued before anything waits for the position
+  // (left alone, the scheduler put that wait ahead of the last row's load)
+  __builtin_amdgcn_sched_barrier(0);
   // every workgroup adds 1 to the count as it exits: the quotient counts the
   // earlier launches (as in decode_fused_kernel). One thread per workgroup
-  // loads it, last: these coherent loads go to memory, and from every thread
-  // they made a hot spot of two addresses; under a branch they are waited
-  // for at its join, which here follows every other load.
+  // loads it, after the rows and before anything that needs the position:
+  // these coherent loads go to memory, and from every thread they made a hot
+  // spot of two addresses; under a branch they are waited for at its join,
+  // which here follows the row loads, needed first anyway.
   uint64_t counted = 0;
   uint32_t err = 0;
   if (tid == 0) {
     counted = __hip_atomic_load(ctl_count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     err = __hip_atomic_load(ctl_err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
+  __builtin_amdgcn_sched_barrier(0);
+  // the lane's RoPE cosines and sines at the position, pairs (2 lane,
+  // 2 lane + 1) mod 64: (cos, sin, cos, sin); needed after the first exchange
+  const f32x4_t csn = *reinterpret_cast<const f32x4_t*>(a.rope + static_cast<size_t>(min(pos, max_len - 1u)) * 128u +
+                                                        4u * (lane & 31u));
   __builtin_amdgcn_sched_barrier(0);
   OBS_ATTN_MARK(1);
   // ---- 1. q/k/v rows of rmsnorm(x) (obs_rmsnorm's sequence), rounded to bf16
