@@ -523,8 +523,9 @@ __device__ __forceinline__ int32_t block_exclusive_scan256(int32_t v, int32_t* s
 
 // Measured cost of one (tile, column block) item by its active 32-row blocks
 // (1..4), in thousands of core cycles (per-wave timestamps at T = 2048 on
-// MI355X, two workgroups per CU): gate/up 74, 81, 91, 108; down (256 columns)
-// 36, 41, 45, 50. Only their ratios matter: they balance the XCDs.
+// MI355X, two workgroups per CU, items in this schedule's order; 2 and 3
+// interpolated): gate/up 66, 82, 98, 114; down (256 columns) 35, 41, 48, 54.
+// Only their ratios matter: they balance the XCDs.
 // Four 16-bit costs in one word: the device extracts one with a shift (a
 // four-entry array, or a select chain the compiler turns into one, would be
 // read from scratch memory).
@@ -538,8 +539,8 @@ constexpr ItemCost item_cost(uint32_t c1, uint32_t c2, uint32_t c3, uint32_t c4)
   return ItemCost{c1 | (static_cast<unsigned long long>(c2) << 16) | (static_cast<unsigned long long>(c3) << 32) |
                   (static_cast<unsigned long long>(c4) << 48)};
 }
-constexpr ItemCost COST_GATEUP = item_cost(74, 81, 91, 108);
-constexpr ItemCost COST_DOWN = item_cost(36, 41, 45, 50);
+constexpr ItemCost COST_GATEUP = item_cost(66, 82, 98, 114);
+constexpr ItemCost COST_DOWN = item_cost(35, 41, 48, 54);
 constexpr uint32_t SCHED_MAX_TILES = 2048;  // tiles the cost-balanced schedule handles (else even split)
 
 // Workgroups a grouped GEMM launch needs for at most max_tiles tiles: an XCD's
@@ -625,7 +626,7 @@ __device__ void work_table_fill(const WorkTable W, uint32_t E, SchedLds& L) {  /
     }
     if (lane == 0) L.over = 0;
     __syncthreads();
-    // XCD of a tile: where its cost starts (32-bit: total <= 2048 tiles x 8 x 108)
+    // XCD of a tile: where its cost starts (32-bit: total <= 2048 tiles x 8 x 114)
     auto xcd_at = [&](uint32_t c) __attribute__((always_inline)) {
       return total ? min(7u, c * 8u / total) : 0u;
     };
