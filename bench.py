@@ -97,6 +97,7 @@ def bench_decode(torch, oh, exe, args):
     for i in range(args.steps):
         exe.graph_launch(graphs[i % n_sets])
     ms = exe.timer_stop()
+    exe.device_status()  # a timed-out wait in a fused launch would make the timing meaningless
     torch.cuda.synchronize()
     ms_step = ms / args.steps
     us_layer = ms_step * 1000.0 / n_layers
@@ -112,6 +113,7 @@ def bench_decode(torch, oh, exe, args):
         sweep(r % n_sets)
         exe.profile_enable(False)
         exe.profile_accumulate()
+    exe.device_status()
     stats = exe.profile_stats()
     exe.profile_clear()
     for g in graphs:
@@ -222,7 +224,9 @@ def bench_decoder(torch, oh, exe, args):
     exe.timer_start()
     model.replay(args.dec_steps)
     ms = exe.timer_stop()
-    pos1, tok = model.read_state()
+    pos1, tok = model.read_state()  # checks the device status of the timed steps
+    if pos1 - pos0 != args.dec_steps:
+        raise RuntimeError(f"decoder: {pos1 - pos0} positions advanced in {args.dec_steps} steps")
     ms_tok = ms / args.dec_steps
     seq_mid = (pos0 + pos1) / 2.0 + 1.0  # mean attended length of the timed steps
     nbytes = decoder_token_bytes(model.cfg, seq_mid)
@@ -234,6 +238,7 @@ def bench_decoder(torch, oh, exe, args):
     model.step()
     exe.profile_enable(False)
     exe.profile_accumulate()
+    exe.device_status()
     stats = exe.profile_stats()
     exe.profile_clear()
     kern = {n: round(1000.0 * t, 1) for n, (t, c) in sorted(stats.items(), key=lambda kv: -kv[1][0])}
@@ -273,7 +278,7 @@ def bench_decoder_prefill(exe, model, args):
     exe.sync()
     exe.timer_start()
     for _ in range(reps):
-        model.prefill(toks, 0)
+        model.prefill(toks, 0)  # each reads its next token back (read_state checks the device status)
     ms = exe.timer_stop() / reps
     exe.profile_clear()
     exe.profile_enable(True)
@@ -352,6 +357,7 @@ def bench_prefill(torch, oh, exe, args):
     for _ in range(reps):
         run()
     ms = exe.timer_stop() / reps
+    exe.device_status()
     exe.profile_clear()
     for _ in range(3):
         exe.stream_hold(20000)
@@ -453,8 +459,11 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "f16",
+        "dtype_detail": ("decode: 4-bit MLX-affine weights against f16 activation operands (v_dot2_f32_f16), "
+                         "fp32 accumulation; prefill: bf16 MFMA operands, fp32 accumulation"),
         "data": "synthetic (seeded random 4-bit weights, bf16 scales/biases, bf16 activations)",
+        "device_status": "ok",  # obs_device_status after every timed region (a failure raises before this line)
         "config": {"workload": "decode MoE layer T=1, top-8 of 128 experts, 48-layer HBM-resident table",
                    "experts": E, "top_k": K, "hidden": H, "moe_inter": I, "group": G,
                    "layers_per_step": args.layers, "parallelism": "none (1 GPU)"},

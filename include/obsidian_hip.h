@@ -153,15 +153,27 @@ int obs_q8_gate_logits(obs_ctx* ctx, const uint32_t* w8, const uint16_t* scales,
                        const uint16_t* biases, const uint16_t* x, float* logits,
                        uint32_t T, uint32_t in, uint32_t n_exp, uint32_t group);
 
-/* Softmax over n_exp logits, top-k by repeated argmax (ties -> lower expert
- * id), optional renormalisation — moe_routing_topk.metal:24-56 and
- * MoeRouter::route_dispatch (router.rs:62-83). ids int32 [T, k], weights fp32 [T, k].
- * n_exp <= 256 (the reference kernel's limit), 1 <= k <= min(n_exp, 64).
+/* Routing rules.
+ * OBS_ROUTE_REF (0, the default of a zeroed obs_moe_config): the reference's
+ *   rule. Each logit is rounded to f16 (round to nearest even), the type
+ *   dequant_matvec_8bit.metal:30 stores it in, before the softmax; the weights
+ *   are f16 values, f16(p) and, renormalised, f16(f16(p) / wsum)
+ *   (moe_routing_topk.metal:47, :55; router.rs:50-54 reads them as f32).
+ * OBS_ROUTE_F32 (1): the same softmax and selection on the fp32 logits, fp32
+ *   weights (no reference counterpart). */
+enum { OBS_ROUTE_REF = 0, OBS_ROUTE_F32 = 1 };
+
+/* Softmax over n_exp logits, top-k by repeated argmax over the probabilities
+ * (ties -> lower expert id), optional renormalisation — moe_routing_topk.metal:24-56
+ * and MoeRouter::route_dispatch (router.rs:62-83). logits fp32 [T, n_exp] (rounded
+ * to f16 inside under OBS_ROUTE_REF), ids int32 [T, k], weights fp32 [T, k].
+ * n_exp <= 256 (the reference kernel's limit), 1 <= k <= min(n_exp, 64);
+ * rule OBS_ROUTE_REF or OBS_ROUTE_F32.
  * A slot with no selectable expert (NaN logits) gets id -1 and weight 0.
  * The synchronous MoeRouter::route (router.rs:25-56) is this call followed by
  * obs_sync + obs_download. */
 int obs_route_topk(obs_ctx* ctx, const float* logits, int32_t* ids, float* weights,
-                   uint32_t T, uint32_t n_exp, uint32_t k, int norm_topk);
+                   uint32_t T, uint32_t n_exp, uint32_t k, int norm_topk, int rule);
 
 /* ------------------------------------------------------------------ */
 /* Elementwise — ops.metal ew_swiglu / ew_scaled_add (forward.rs:370-380) */
@@ -194,6 +206,7 @@ typedef struct obs_moe_config {
   uint32_t group;    /* quantization group size (64) */
   int32_t norm_topk; /* norm_topk_prob (model.rs:22) */
   float rms_eps;     /* rms_norm_eps (model.rs:18); used when layer->norm_w is set */
+  int32_t route_rule; /* OBS_ROUTE_REF (0: the reference's f16 logits and weights) or OBS_ROUTE_F32 */
 } obs_moe_config;
 
 /* One layer's MoE weights, all device pointers, stacked on the expert axis. */
@@ -217,11 +230,13 @@ typedef struct obs_moe_layer {
  * ids_out [top_k] / w_out [top_k] (may be NULL) receive the routing.
  * Workspace comes from the context (allocated once, on first use: make the
  * first call outside a graph capture).
- * For hidden 2048 / inter 768 / top_k 8 / group 64 (Qwen3-30B-A3B) the layer
- * runs as ONE launch of 256 workgroups that exchange data through bounded
- * device-side waits; it needs the GPU's CUs free for that launch (no other
- * kernel holding them). A wait that times out is reported by
- * obs_device_status(). Other shapes run as 4 launches. */
+ * For hidden 2048 / inter 768 / top_k 8 / group 64 (Qwen3-30B-A3B) on a
+ * device with at least 256 CUs the layer runs as ONE launch of 256 workgroups
+ * that exchange data through bounded device-side waits; it needs the GPU's CUs
+ * free for that launch (no other kernel holding them). A wait that times out
+ * is reported by obs_device_status(): call it after a sequence of calls (or a
+ * graph replay) before using their outputs. Other shapes, and devices with
+ * fewer CUs, run as 4 launches. */
 int obs_moe_decode(obs_ctx* ctx, const obs_moe_config* cfg, const obs_moe_layer* layer,
                    const uint16_t* x, const uint16_t* residual, uint16_t* y,
                    int32_t* ids_out, float* w_out);
@@ -240,7 +255,10 @@ int obs_device_status(obs_ctx* ctx);
 size_t obs_moe_prefill_workspace(const obs_moe_config* cfg, uint32_t T);
 
 /* Grouped prefill MoE for T tokens (forward.rs:164-247): routing either
- * computed from X (ids == NULL: router as obs_q8_gate_logits + obs_route_topk)
+ * computed from X (ids == NULL: router as obs_q8_gate_logits + obs_route_topk
+ * with cfg->route_rule; the routing is left in the workspace, ids int32
+ * [T, top_k] at byte 0 and weights fp32 [T, top_k] at byte
+ * (4 * T * top_k + 255) / 256 * 256, where read_route reads it, forward.rs:175-182)
  * or injected (ids, weights [T, top_k] device arrays; ids must be in range and
  * distinct per token). Tokens are permuted into per-expert groups on the GPU,
  * gate/up/down run as grouped dequant-to-LDS bf16 MFMA GEMMs with a SwiGLU

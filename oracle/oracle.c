@@ -241,12 +241,15 @@ int orc_qmatvec_f64(int bits, const uint32_t* w, const uint16_t* s, const uint16
  *   n = rint(x * log2(e)),  r = x - n*ln2 (Cody-Waite: ln2 = hi + lo, each
  *   step one fma), exp(r) by the degree-7 Taylor polynomial in Horner form
  *   (|r| <= ln2/2, truncation < 6e-9 relative), result = p * 2^n.
- * Domain conventions: x < -86 -> +0 (keeps 2^n normal), x > 88.5 -> +inf,
- * NaN -> NaN. Both the HIP kernels and this oracle evaluate exactly these
- * operations, so their results are bit-identical. */
+ * Below the normal range the result underflows gradually, as IEEE exp does:
+ * p * 2^n is formed as (p * 2^(n+64)) * 2^-64 (the first product exact, the
+ * second one rounding into the subnormals).
+ * Domain conventions: x < -104 -> +0 (exp(-104) is below half the smallest
+ * subnormal), x > 88.5 -> +inf, NaN -> NaN. Both the HIP kernels and this
+ * oracle evaluate exactly these operations, so their results are bit-identical. */
 float orc_exp(float x) {
   if (x != x) return x;
-  if (x < -86.0f) return 0.0f;
+  if (x < -104.0f) return 0.0f;
   if (x > 88.5f) return INFINITY;
   const float LOG2E = 1.44269502162933349609375f;   /* fl32(1/ln 2) */
   const float LN2_HI = 0.693145751953125f;           /* ln2 rounded to 16 significant bits */
@@ -264,13 +267,20 @@ float orc_exp(float x) {
   p = fmaf(p, r, 1.0f);
   int ni = (int)n;
   if (ni > 127) { p = p * 2.0f; ni -= 1; }
+  if (ni < -126) return (p * u2f((uint32_t)(ni + 64 + 127) << 23)) * 0x1p-64f;
   return p * u2f((uint32_t)(ni + 127) << 23);
 }
 
-/* moe_routing_topk.metal:31-56 for one token. */
-static void route_one(const float* l, int n, int k, int norm_topk, int sum_order, int emulate_f16,
+static inline float round_f16(float v) { return orc_f16_to_f32(orc_f32_to_f16(v)); }
+
+/* moe_routing_topk.metal:24-56 for one token. Under ORC_ROUTE_REF the logits
+ * are the f16 values dequant_matvec_8bit.metal:30 stores (each rounded RNE),
+ * and the weights are stored as f16 (:47, :55). */
+static void route_one(const float* l_in, int n, int k, int norm_topk, int sum_order, int rule,
                       int32_t* ids, float* w) {
-  float p[1024];
+  float p[1024], l[1024];
+  const int f16 = (rule == ORC_ROUTE_REF);
+  for (int i = 0; i < n; ++i) l[i] = f16 ? round_f16(l_in[i]) : l_in[i];
   float mx = -INFINITY;
   for (int i = 0; i < n; ++i) mx = fmaxf(mx, l[i]);
   for (int i = 0; i < n; ++i) p[i] = orc_exp(l[i] - mx);
@@ -300,7 +310,7 @@ static void route_one(const float* l, int n, int k, int norm_topk, int sum_order
       if (p[i] > best) { best = p[i]; bi = i; }
     if (bi < 0) { ids[kk] = -1; w[kk] = 0.0f; continue; }
     ids[kk] = bi;
-    w[kk] = emulate_f16 ? orc_f16_to_f32(orc_f32_to_f16(best)) : best;
+    w[kk] = f16 ? round_f16(best) : best;
     wsum = wsum + best;
     p[bi] = -INFINITY;
   }
@@ -308,17 +318,18 @@ static void route_one(const float* l, int n, int k, int norm_topk, int sum_order
     for (int kk = 0; kk < k; ++kk) {
       if (ids[kk] < 0) continue;
       const float q = w[kk] / wsum;
-      w[kk] = emulate_f16 ? orc_f16_to_f32(orc_f32_to_f16(q)) : q;
+      w[kk] = f16 ? round_f16(q) : q;
     }
   }
 }
 
 int orc_route_topk(const float* logits, int64_t T, int n_exp, int k, int norm_topk,
-                   int sum_order, int emulate_f16, int32_t* ids, float* w) {
+                   int sum_order, int rule, int32_t* ids, float* w) {
   if (n_exp < 1 || n_exp > 256 || k < 1 || k > n_exp) return -1;
   if (sum_order != ORC_SUM_SERIAL && sum_order != ORC_SUM_WAVE) return -2;
+  if (rule != ORC_ROUTE_REF && rule != ORC_ROUTE_F32) return -3;
   for (int64_t t = 0; t < T; ++t)
-    route_one(logits + t * n_exp, n_exp, k, norm_topk, sum_order, emulate_f16, ids + t * k, w + t * k);
+    route_one(logits + t * n_exp, n_exp, k, norm_topk, sum_order, rule, ids + t * k, w + t * k);
   return 0;
 }
 
@@ -370,7 +381,7 @@ void orc_scaled_add(float* acc, const float* y, float scale, int64_t n) {
 
 static inline double silu_mul_d(double g, double u) { return g / (1.0 + exp(-g)) * u; }
 
-int orc_router(const orc_layer* L, const uint16_t* x_bf16, int64_t T, int k, int norm_topk,
+int orc_router(const orc_layer* L, const uint16_t* x_bf16, int64_t T, int k, int norm_topk, int rule,
                float* logits_out, int32_t* ids, float* w) {
   const int E = L->n_exp, H = L->hidden;
   float* x = (float*)malloc(sizeof(float) * (size_t)H);
@@ -380,7 +391,7 @@ int orc_router(const orc_layer* L, const uint16_t* x_bf16, int64_t T, int k, int
     orc_bf16_to_f32_n(x_bf16 + t * H, x, H);
     rc = orc_qmatvec_lanes(8, L->router_w, L->router_s, L->router_b, ORC_SB_BF16, x, lg + t * E, H, E, L->group, 64);
   }
-  if (!rc) rc = orc_route_topk(lg, T, E, k, norm_topk, ORC_SUM_WAVE, 0, ids, w);
+  if (!rc) rc = orc_route_topk(lg, T, E, k, norm_topk, ORC_SUM_WAVE, rule, ids, w);
   if (!rc && logits_out) memcpy(logits_out, lg, sizeof(float) * (size_t)E * (size_t)T);
   free(x);
   free(lg);
@@ -434,7 +445,7 @@ static void expert_shader_f16(const orc_layer* L, int e, const float* x, float* 
   free(g); free(u); free(h);
 }
 
-int orc_moe_decode(const orc_layer* L, const uint16_t* x_bf16, int64_t T, int k, int norm_topk,
+int orc_moe_decode(const orc_layer* L, const uint16_t* x_bf16, int64_t T, int k, int norm_topk, int rule,
                    const int32_t* ids_in, const float* w_in, int32_t* ids_out, float* w_out,
                    int mode, double* y_out) {
   const int H = L->hidden, E = L->n_exp;
@@ -442,7 +453,7 @@ int orc_moe_decode(const orc_layer* L, const uint16_t* x_bf16, int64_t T, int k,
   const int32_t* ids = ids_in;
   const float* w = w_in;
   if (!ids_in) {
-    int rc = orc_router(L, x_bf16, T, k, norm_topk, NULL, ids_out, w_out);
+    int rc = orc_router(L, x_bf16, T, k, norm_topk, rule, NULL, ids_out, w_out);
     if (rc) return rc;
     ids = ids_out;
     w = w_out;
@@ -596,9 +607,9 @@ int orc_moe_decode_baseline(const orc_layer* L, const uint16_t* x_bf16, int k, i
   float x[8192], lg[256], g[4096], u[4096], h[4096], ye[8192];
   if (H > 8192 || I > 4096 || E > 256) return -1;
   orc_bf16_to_f32_n(x_bf16, x, H);
-  /* dequant_matvec_8bit (serial per row) then moe_routing_topk */
+  /* dequant_matvec_8bit (serial per row, f16 logits) then moe_routing_topk */
   orc_qmatvec_shader(8, L->router_w, L->router_s, L->router_b, ORC_SB_BF16, x, lg, H, E, G);
-  orc_route_topk(lg, 1, E, k, norm_topk, ORC_SUM_SERIAL, 0, ids, w);
+  orc_route_topk(lg, 1, E, k, norm_topk, ORC_SUM_SERIAL, ORC_ROUTE_REF, ids, w);
   for (int o = 0; o < H; ++o) y[o] = 0.0f;
   for (int r = 0; r < k; ++r) {
     const int e = ids[r];

@@ -27,8 +27,9 @@
  *     MLX is absent, so the bf16 value is defined here as one RNE of the exact
  *     fp32 q*s+b;
  *   - Metal fast-math exp and contraction inside the reference shaders: the
- *     reference's f16 logits and routing weights are restated semantically
- *     (orc_route_topk's emulate_f16 mode), not bit for bit.
+ *     routing softmax is restated with an IEEE-style exp (gradual underflow)
+ *     and IEEE division on the f16 logits (orc_route_topk's ORC_ROUTE_REF),
+ *     not with Metal's own exp.
  */
 #ifndef OBSIDIAN_ORACLE_H
 #define OBSIDIAN_ORACLE_H
@@ -81,17 +82,23 @@ int orc_qmatvec_f64(int bits, const uint32_t* w, const uint16_t* s, const uint16
 float orc_exp(float x);
 
 enum { ORC_SUM_SERIAL = 0, ORC_SUM_WAVE = 1 };
+/* ORC_ROUTE_REF: the reference's rule — every logit rounded to f16 first (the
+ * half output of dequant_matvec_8bit.metal:30, read back as float by
+ * moe_routing_topk.metal:24), weights stored as f16: f16(p), renormalised
+ * f16(f16(p) / wsum) (moe_routing_topk.metal:47, :55). ORC_ROUTE_F32: no
+ * rounding of logits or weights. */
+enum { ORC_ROUTE_REF = 0, ORC_ROUTE_F32 = 1 };
 /* logits [T, n_exp] fp32 -> ids [T, k] int32, weights [T, k] fp32.
  * Softmax p = e/S with e = orc_exp(l - max); top-k by repeated argmax over p
  * (strict '>', lowest id wins ties); if norm_topk and wsum > 0, w = p / wsum
- * with wsum the serial fp32 sum of the selected p in selection order.
+ * with wsum the serial fp32 sum of the selected (unrounded) p in selection order.
  * sum_order picks the order of S: serial (the reference kernel) or the wave
  * order of the HIP kernel (lane l sums experts l, l+64, l+128, l+192 in that
- * order, then an xor butterfly over 64 lanes with offsets 1, 2, ..., 32). emulate_f16 = 1 additionally
- * rounds the weights to f16 as moe_routing_topk.metal:49,55 does.
+ * order, then an xor butterfly over 64 lanes with offsets 1, 2, ..., 32).
+ * rule: ORC_ROUTE_REF or ORC_ROUTE_F32 (above).
  * A slot with no selectable expert (NaN probabilities) gets id -1, weight 0. */
 int orc_route_topk(const float* logits, int64_t T, int n_exp, int k, int norm_topk,
-                   int sum_order, int emulate_f16, int32_t* ids, float* w);
+                   int sum_order, int rule, int32_t* ids, float* w);
 
 /* ---- RMSNorm (shaders/rmsnorm.metal:17-35, Model::rmsnorm forward.rs:345-357) ----
  * rows x dim, bf16 in and out. ss = sum of x^2 in the documented lane order
@@ -120,8 +127,9 @@ typedef struct {
 enum { ORC_MODE_F64 = 0, ORC_MODE_SHADER_F16 = 1, ORC_MODE_MFMA_BF16 = 2 };
 
 /* Router for T tokens: logits in the lanes order (64 lanes) then orc_route_topk
- * with the wave sum order. logits_out may be NULL. */
-int orc_router(const orc_layer* L, const uint16_t* x_bf16, int64_t T, int k, int norm_topk,
+ * with the wave sum order and `rule`. logits_out (fp32, before any f16
+ * rounding) may be NULL. */
+int orc_router(const orc_layer* L, const uint16_t* x_bf16, int64_t T, int k, int norm_topk, int rule,
                float* logits_out, int32_t* ids, float* w);
 
 /* Decode MoE half for T tokens (forward.rs:421-441 per token): y[t] = sum_rank w*expert(x[t]).
@@ -130,7 +138,7 @@ int orc_router(const orc_layer* L, const uint16_t* x_bf16, int64_t T, int k, int
  * mode ORC_MODE_SHADER_F16: the reference engine's rounding sequence (f16 g,u,h,y and
  *   an f16 accumulate per rank, serial fp32 dots).
  * y_out [T, H] fp64 (no residual). */
-int orc_moe_decode(const orc_layer* L, const uint16_t* x_bf16, int64_t T, int k, int norm_topk,
+int orc_moe_decode(const orc_layer* L, const uint16_t* x_bf16, int64_t T, int k, int norm_topk, int rule,
                    const int32_t* ids_in, const float* w_in, int32_t* ids_out, float* w_out,
                    int mode, double* y_out);
 

@@ -20,6 +20,7 @@ LIB_PATH = os.path.join(HERE, "liboracle.so")
 
 SB_BF16, SB_F16 = 0, 1
 SUM_SERIAL, SUM_WAVE = 0, 1
+ROUTE_REF, ROUTE_F32 = 0, 1
 MODE_F64, MODE_SHADER_F16, MODE_MFMA_BF16 = 0, 1, 2
 
 
@@ -60,8 +61,8 @@ def lib() -> C.CDLL:
         L.orc_qmatvec_lanes.argtypes = [i32, vp, vp, vp, i32, vp, vp, i64, i64, i32, i32]
         L.orc_qmatvec_f64.argtypes = [i32, vp, vp, vp, i32, vp, vp, vp, i64, i64, i32]
         L.orc_route_topk.argtypes = [vp, i64, i32, i32, i32, i32, i32, vp, vp]
-        L.orc_router.argtypes = [C.POINTER(OrcLayer), vp, i64, i32, i32, vp, vp, vp]
-        L.orc_moe_decode.argtypes = [C.POINTER(OrcLayer), vp, i64, i32, i32, vp, vp, vp, vp, i32, vp]
+        L.orc_router.argtypes = [C.POINTER(OrcLayer), vp, i64, i32, i32, i32, vp, vp, vp]
+        L.orc_moe_decode.argtypes = [C.POINTER(OrcLayer), vp, i64, i32, i32, i32, vp, vp, vp, vp, i32, vp]
         L.orc_group_rows.argtypes = [vp, i64, i32, i32, vp, vp, vp, vp]
         L.orc_moe_prefill.argtypes = [C.POINTER(OrcLayer), vp, i64, i32, vp, vp, i32, vp]
         L.orc_moe_decode_baseline.argtypes = [C.POINTER(OrcLayer), vp, i32, i32, i32, vp, vp, vp]
@@ -156,14 +157,15 @@ def qmatvec(kind: str, bits: int, w, s, b, x_f32, in_f: int, out_f: int, group: 
 
 
 def route_topk(logits, k: int, norm_topk: bool = True, sum_order: int = SUM_WAVE,
-               emulate_f16: bool = False) -> Tuple[np.ndarray, np.ndarray]:
+               rule: int = ROUTE_REF) -> Tuple[np.ndarray, np.ndarray]:
+    """rule ROUTE_REF: the reference's f16 logits and f16 weights; ROUTE_F32: fp32 throughout."""
     lg = _c(logits, np.float32)
     if lg.ndim == 1:
         lg = lg[None, :]
     T, n = lg.shape
     ids = np.empty((T, k), np.int32)
     w = np.empty((T, k), np.float32)
-    _rc(lib().orc_route_topk(_p(lg), T, n, k, int(norm_topk), sum_order, int(emulate_f16), _p(ids), _p(w)),
+    _rc(lib().orc_route_topk(_p(lg), T, n, k, int(norm_topk), sum_order, int(rule), _p(ids), _p(w)),
         "route_topk")
     return ids, w
 
@@ -179,17 +181,20 @@ class Layer:
         self.n_exp, self.hidden, self.inter, self.group = n_exp, hidden, inter, group
 
 
-def router(layer: Layer, x_bf16, k: int, norm_topk: bool = True):
+def router(layer: Layer, x_bf16, k: int, norm_topk: bool = True, rule: int = ROUTE_REF):
+    """(fp32 logits [T, E] before any f16 rounding, ids [T, k], weights [T, k])."""
     x = _c(x_bf16, np.uint16).reshape(-1, layer.hidden)
     T = x.shape[0]
     lg = np.empty((T, layer.n_exp), np.float32)
     ids = np.empty((T, k), np.int32)
     w = np.empty((T, k), np.float32)
-    _rc(lib().orc_router(C.byref(layer.s), _p(x), T, k, int(norm_topk), _p(lg), _p(ids), _p(w)), "router")
+    _rc(lib().orc_router(C.byref(layer.s), _p(x), T, k, int(norm_topk), int(rule), _p(lg), _p(ids), _p(w)),
+        "router")
     return lg, ids, w
 
 
-def moe_decode(layer: Layer, x_bf16, k: int, norm_topk: bool = True, ids=None, w=None, mode: int = MODE_F64):
+def moe_decode(layer: Layer, x_bf16, k: int, norm_topk: bool = True, ids=None, w=None, mode: int = MODE_F64,
+               rule: int = ROUTE_REF):
     x = _c(x_bf16, np.uint16).reshape(-1, layer.hidden)
     T = x.shape[0]
     y = np.empty((T, layer.hidden), np.float64)
@@ -197,8 +202,8 @@ def moe_decode(layer: Layer, x_bf16, k: int, norm_topk: bool = True, ids=None, w
     w_o = np.empty((T, k), np.float32)
     ids_i = None if ids is None else _c(ids, np.int32).reshape(T, k)
     w_i = None if w is None else _c(w, np.float32).reshape(T, k)
-    _rc(lib().orc_moe_decode(C.byref(layer.s), _p(x), T, k, int(norm_topk), _p(ids_i), _p(w_i), _p(ids_o),
-                             _p(w_o), mode, _p(y)), "moe_decode")
+    _rc(lib().orc_moe_decode(C.byref(layer.s), _p(x), T, k, int(norm_topk), int(rule), _p(ids_i), _p(w_i),
+                             _p(ids_o), _p(w_o), mode, _p(y)), "moe_decode")
     if ids is None:
         return y, ids_o, w_o
     return y, ids_i, w_i

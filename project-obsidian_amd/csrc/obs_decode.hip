@@ -20,7 +20,7 @@ int check_router_shape(obs_ctx* ctx, const char* who, uint32_t in, uint32_t n_ex
 int launch_gate_logits(obs_ctx* ctx, const uint32_t* w8, const uint16_t* s, const uint16_t* b,
                        const uint16_t* x, float* logits, uint32_t T, uint32_t in, uint32_t n_exp, uint32_t group);
 int launch_route_topk(obs_ctx* ctx, const float* logits, int32_t* ids, float* w, uint32_t T,
-                      uint32_t n_exp, uint32_t k, int norm_topk);
+                      uint32_t n_exp, uint32_t k, int norm_topk, int rule);
 }  // namespace obs
 
 namespace {
@@ -212,6 +212,8 @@ int check_moe_config(obs_ctx* ctx, const char* who, const obs_moe_config* cfg) {
     return set_error(ctx, OBS_E_SHAPE, "%s: n_exp must be in [1, 256] (got %u)", who, cfg->n_exp);
   if (cfg->top_k == 0 || cfg->top_k > cfg->n_exp || cfg->top_k > 8)
     return set_error(ctx, OBS_E_SHAPE, "%s: top_k must be in [1, min(n_exp, 8)] (got %u)", who, cfg->top_k);
+  if (cfg->route_rule != OBS_ROUTE_REF && cfg->route_rule != OBS_ROUTE_F32)
+    return set_error(ctx, OBS_E_INVALID, "%s: unknown route_rule %d", who, cfg->route_rule);
   return OBS_OK;
 }
 
@@ -264,6 +266,63 @@ int launch_decode_experts(obs_ctx* ctx, const obs_moe_config* cfg, const obs_moe
   return OBS_OK;
 }
 
+// Validates a decode call and picks its path (the one-launch fused kernel, or
+// the 4 launches).
+int decode_plan(obs_ctx* ctx, const char* who, const obs_moe_config* cfg, const obs_moe_layer* layer,
+                const uint16_t* x, const uint16_t* y, bool* fused) {
+  int rc = check_moe_config(ctx, who, cfg);
+  if (rc) return rc;
+  rc = check_moe_layer(ctx, who, layer);
+  if (rc) return rc;
+  if (!x || !y) return set_error(ctx, OBS_E_INVALID, "%s: null x or y", who);
+  if (!aligned(x, 16)) return set_error(ctx, OBS_E_ALIGN, "%s: x must be 16-byte aligned", who);
+  const bool shape_ok = fused_decode_supported(cfg);
+  // the one-launch path spins on values other workgroups publish: all of its
+  // workgroups must be resident at once, one per CU
+  const bool cus_ok = ctx->num_cus >= static_cast<int>(fused_decode_workgroups());
+  if (ctx->decode_path == OBS_DECODE_FUSED && !shape_ok)
+    return set_error(ctx, OBS_E_SHAPE, "%s: the fused path needs hidden 2048, inter 768, top_k 8, group 64, n_exp <= 256",
+                     who);
+  if (ctx->decode_path == OBS_DECODE_FUSED && !cus_ok)
+    return set_error(ctx, OBS_E_UNSUPPORTED, "%s: the fused path needs %u CUs (the device has %d)", who,
+                     fused_decode_workgroups(), ctx->num_cus);
+  *fused = shape_ok && cus_ok && ctx->decode_path != OBS_DECODE_MULTI;
+  return OBS_OK;
+}
+
+// Workspace of the 4-launch path: logits [E] | ids [k] | w [k] | h [k, I] | normed x [H].
+size_t multi_ws_bytes(const obs_moe_config* cfg) {
+  return align256(sizeof(float) * cfg->n_exp) + align256(sizeof(int32_t) * cfg->top_k) +
+         align256(sizeof(float) * cfg->top_k) + align256(sizeof(float) * cfg->top_k * cfg->inter) +
+         align256(sizeof(uint16_t) * cfg->hidden);
+}
+
+// The 4-launch path over a workspace of multi_ws_bytes(cfg) at `base`.
+int decode_multi(obs_ctx* ctx, const obs_moe_config* cfg, const obs_moe_layer* layer, const uint16_t* x,
+                 const uint16_t* residual, uint16_t* y, int32_t* ids_out, float* w_out, char* base) {
+  const uint32_t E = cfg->n_exp, k = cfg->top_k, H = cfg->hidden, I = cfg->inter;
+  const size_t off_ids = align256(sizeof(float) * E);
+  const size_t off_w = off_ids + align256(sizeof(int32_t) * k);
+  const size_t off_h = off_w + align256(sizeof(float) * k);
+  const size_t off_xn = off_h + align256(sizeof(float) * k * I);
+  float* logits = reinterpret_cast<float*>(base);
+  int32_t* ids = ids_out ? ids_out : reinterpret_cast<int32_t*>(base + off_ids);
+  float* w = w_out ? w_out : reinterpret_cast<float*>(base + off_w);
+  float* h = reinterpret_cast<float*>(base + off_h);
+  int rc;
+  if (layer->norm_w) {  // the router and experts see rmsnorm(x) (forward.rs:419-421)
+    uint16_t* xn = reinterpret_cast<uint16_t*>(base + off_xn);
+    rc = launch_rmsnorm(ctx, x, layer->norm_w, xn, 1, H, cfg->rms_eps);
+    if (rc) return rc;
+    x = xn;
+  }
+  rc = launch_gate_logits(ctx, layer->router_w, layer->router_s, layer->router_b, x, logits, 1, H, E, cfg->group);
+  if (rc) return rc;
+  rc = launch_route_topk(ctx, logits, ids, w, 1, E, k, cfg->norm_topk, cfg->route_rule);
+  if (rc) return rc;
+  return launch_decode_experts(ctx, cfg, layer, x, residual, y, ids, w, h);
+}
+
 }  // namespace obs
 
 extern "C" {
@@ -271,43 +330,14 @@ extern "C" {
 int obs_moe_decode(obs_ctx* ctx, const obs_moe_config* cfg, const obs_moe_layer* layer, const uint16_t* x,
                    const uint16_t* residual, uint16_t* y, int32_t* ids_out, float* w_out) {
   if (!ctx) return OBS_E_INVALID;
-  int rc = obs::check_moe_config(ctx, "obs_moe_decode", cfg);
+  bool fused = false;
+  int rc = obs::decode_plan(ctx, "obs_moe_decode", cfg, layer, x, y, &fused);
   if (rc) return rc;
-  rc = obs::check_moe_layer(ctx, "obs_moe_decode", layer);
-  if (rc) return rc;
-  if (!x || !y) return obs::set_error(ctx, OBS_E_INVALID, "obs_moe_decode: null x or y");
-  if (!obs::aligned(x, 16)) return obs::set_error(ctx, OBS_E_ALIGN, "obs_moe_decode: x must be 16-byte aligned");
-  const bool fused_ok = obs::fused_decode_supported(cfg);
-  if (ctx->decode_path == OBS_DECODE_FUSED && !fused_ok)
-    return obs::set_error(ctx, OBS_E_SHAPE, "obs_moe_decode: the fused path needs hidden 2048, inter 768, top_k 8, group 64, n_exp <= 256");
-  if (fused_ok && ctx->decode_path != OBS_DECODE_MULTI)
-    return obs::launch_fused_decode(ctx, cfg, layer, x, residual, y, ids_out, w_out);
-  const uint32_t E = cfg->n_exp, k = cfg->top_k, H = cfg->hidden, I = cfg->inter;
-  // workspace: logits [E] | ids [k] | w [k] | h [k, I] | normed x [H]
-  const size_t off_ids = align256(sizeof(float) * E);
-  const size_t off_w = off_ids + align256(sizeof(int32_t) * k);
-  const size_t off_h = off_w + align256(sizeof(float) * k);
-  const size_t off_xn = off_h + align256(sizeof(float) * k * I);
-  const size_t total = off_xn + align256(sizeof(uint16_t) * H);
+  if (fused) return obs::launch_fused_decode(ctx, cfg, layer, x, residual, y, ids_out, w_out);
   void* ws = nullptr;
-  rc = obs::ensure_decode_ws(ctx, total, &ws);
+  rc = obs::ensure_decode_ws(ctx, obs::multi_ws_bytes(cfg), &ws);
   if (rc) return rc;
-  char* base = static_cast<char*>(ws);
-  float* logits = reinterpret_cast<float*>(base);
-  int32_t* ids = ids_out ? ids_out : reinterpret_cast<int32_t*>(base + off_ids);
-  float* w = w_out ? w_out : reinterpret_cast<float*>(base + off_w);
-  float* h = reinterpret_cast<float*>(base + off_h);
-  if (layer->norm_w) {  // the router and experts see rmsnorm(x) (forward.rs:419-421)
-    uint16_t* xn = reinterpret_cast<uint16_t*>(base + off_xn);
-    rc = obs::launch_rmsnorm(ctx, x, layer->norm_w, xn, 1, H, cfg->rms_eps);
-    if (rc) return rc;
-    x = xn;
-  }
-  rc = obs::launch_gate_logits(ctx, layer->router_w, layer->router_s, layer->router_b, x, logits, 1, H, E, cfg->group);
-  if (rc) return rc;
-  rc = obs::launch_route_topk(ctx, logits, ids, w, 1, E, k, cfg->norm_topk);
-  if (rc) return rc;
-  return obs::launch_decode_experts(ctx, cfg, layer, x, residual, y, ids, w, h);
+  return obs::decode_multi(ctx, cfg, layer, x, residual, y, ids_out, w_out, static_cast<char*>(ws));
 }
 
 int obs_set_decode_path(obs_ctx* ctx, int path) {

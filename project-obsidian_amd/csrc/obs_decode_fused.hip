@@ -71,6 +71,7 @@ struct FusedArgs {
   unsigned char* ws;
   uint32_t n_exp;
   int norm_topk;
+  int route_rule;
 };
 
 __device__ __forceinline__ void raise_error(unsigned char* ws) {
@@ -228,7 +229,7 @@ __global__ void __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 
   if (wave == 0) {
     int32_t id;
     float w;
-    route_wave<NQ>(lg, n_exp, FK, a.norm_topk, lane, &id, &w);
+    route_wave<NQ>(lg, n_exp, FK, a.norm_topk, a.route_rule, lane, &id, &w);
     if (lane < FK) {
       s_ids[lane] = id;
       s_w[lane] = w;
@@ -454,6 +455,8 @@ bool fused_decode_supported(const obs_moe_config* cfg) {
   return cfg->hidden == FH && cfg->inter == FI && cfg->top_k == FK && cfg->group == FG && cfg->n_exp <= MAX_E;
 }
 
+uint32_t fused_decode_workgroups() { return NWG; }
+
 size_t fused_decode_ws_bytes() { return WS_BYTES; }
 
 int launch_fused_decode(obs_ctx* ctx, const obs_moe_config* cfg, const obs_moe_layer* L, const uint16_t* x,
@@ -467,9 +470,14 @@ int launch_fused_decode(obs_ctx* ctx, const obs_moe_config* cfg, const obs_moe_l
     OBS_HIP_TRY(ctx, hipMemset(ctx->fused_ws, 0, WS_BYTES));
     OBS_HIP_TRY(ctx, hipDeviceSynchronize());
   }
+  return launch_fused_decode_ws(ctx, cfg, L, x, residual, y, ids_out, w_out, ctx->fused_ws);
+}
+
+int launch_fused_decode_ws(obs_ctx* ctx, const obs_moe_config* cfg, const obs_moe_layer* L, const uint16_t* x,
+                           const uint16_t* residual, uint16_t* y, int32_t* ids_out, float* w_out, void* ws) {
   FusedArgs a{L->gate_w, L->gate_s, L->gate_b, L->up_w, L->up_s, L->up_b, L->down_w, L->down_s, L->down_b,
               L->router_w, L->router_s, L->router_b, x, residual, y, L->norm_w, cfg->rms_eps, ids_out, w_out,
-              static_cast<unsigned char*>(ctx->fused_ws), cfg->n_exp, cfg->norm_topk};
+              static_cast<unsigned char*>(ws), cfg->n_exp, cfg->norm_topk, cfg->route_rule};
   if (cfg->n_exp <= 128)
     OBS_LAUNCH(ctx, "decode_fused", decode_fused_kernel<2><<<NWG, 256, 0, ctx->stream>>>(a));
   else
@@ -477,13 +485,14 @@ int launch_fused_decode(obs_ctx* ctx, const obs_moe_config* cfg, const obs_moe_l
   return OBS_OK;
 }
 
-int fused_decode_status(obs_ctx* ctx) {
-  if (!ctx->fused_ws) return OBS_OK;
+int fused_decode_status(obs_ctx* ctx) { return ctx->fused_ws ? fused_decode_status_ws(ctx, ctx->fused_ws) : OBS_OK; }
+
+int fused_decode_status_ws(obs_ctx* ctx, void* ws) {
   OBS_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
   uint32_t err = 0;
-  OBS_HIP_TRY(ctx, hipMemcpy(&err, static_cast<unsigned char*>(ctx->fused_ws) + WS_ERR, 4, hipMemcpyDeviceToHost));
+  OBS_HIP_TRY(ctx, hipMemcpy(&err, static_cast<unsigned char*>(ws) + WS_ERR, 4, hipMemcpyDeviceToHost));
   if (err) {
-    OBS_HIP_TRY(ctx, hipMemset(ctx->fused_ws, 0, WS_BYTES));
+    OBS_HIP_TRY(ctx, hipMemset(ws, 0, WS_BYTES));
     OBS_HIP_TRY(ctx, hipDeviceSynchronize());
     return set_error(ctx, OBS_E_HIP,
                      "fused decode: a cross-workgroup wait timed out (were all CUs available?); "

@@ -96,11 +96,18 @@ int launch_rmsnorm(obs_ctx* ctx, const uint16_t* x, const uint16_t* w, uint16_t*
 
 // Fused single-launch decode (obs_decode_fused.hip).
 bool fused_decode_supported(const obs_moe_config* cfg);
+uint32_t fused_decode_workgroups();  // workgroups of one launch (each needs a CU of its own)
 size_t fused_decode_ws_bytes();
 int launch_fused_decode(obs_ctx* ctx, const obs_moe_config* cfg, const obs_moe_layer* L, const uint16_t* x,
                         const uint16_t* residual, uint16_t* y, int32_t* ids_out, float* w_out);
+// The same launch on a caller-provided exchange area of fused_decode_ws_bytes()
+// (zeroed before its first use; never cleared between launches).
+int launch_fused_decode_ws(obs_ctx* ctx, const obs_moe_config* cfg, const obs_moe_layer* L, const uint16_t* x,
+                           const uint16_t* residual, uint16_t* y, int32_t* ids_out, float* w_out, void* ws);
 // Reads and clears the fused path's device error flag (synchronizes).
 int fused_decode_status(obs_ctx* ctx);
+// The same for an exchange area `ws` (resets it when the flag is set).
+int fused_decode_status_ws(obs_ctx* ctx, void* ws);
 
 // Fused attention half of a decode layer (obs_attention_fused.hip): its
 // device error flag, read and cleared (synchronizes).
@@ -141,11 +148,13 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 // exp(x) by Cody-Waite reduction with ln2 = HI + LO and a degree-7 Taylor
 // polynomial (|r| <= ln2/2, truncation error < 6e-9 relative); every step is a
 // correctly rounded fp32 operation, so the result is reproducible bit for bit
-// on any IEEE fp32 machine that evaluates the same sequence. x < -86 -> +0,
-// x > 88.5 -> +inf, NaN -> NaN.
+// on any IEEE fp32 machine that evaluates the same sequence. Results below the
+// normal range underflow gradually, as IEEE exp does: p * 2^n is formed as
+// (p * 2^(n+64)) * 2^-64, one rounding into the subnormals. x < -104 -> +0
+// (exp(-104) is below half the smallest subnormal), x > 88.5 -> +inf, NaN -> NaN.
 __device__ __forceinline__ float exp_det(float x) {
   if (x != x) return x;
-  if (x < -86.0f) return 0.0f;
+  if (x < -104.0f) return 0.0f;
   if (x > 88.5f) return __builtin_huge_valf();
   const float LOG2E = 1.44269502162933349609375f;
   const float LN2_HI = 0.693145751953125f;
@@ -163,8 +172,12 @@ __device__ __forceinline__ float exp_det(float x) {
   p = __builtin_fmaf(p, r, 1.0f);
   int ni = static_cast<int>(n);
   if (ni > 127) { p = p * 2.0f; ni -= 1; }
+  if (ni < -126) return (p * __uint_as_float(static_cast<uint32_t>(ni + 64 + 127) << 23)) * 0x1p-64f;
   return p * __uint_as_float(static_cast<uint32_t>(ni + 127) << 23);
 }
+
+// fp32 -> f16 (round to nearest even) -> fp32: the value a half holds
+__device__ __forceinline__ float round_f16(float v) { return static_cast<float>(static_cast<_Float16>(v)); }
 
 // silu(g) * u with the deterministic exp (ops.metal:21 form).
 __device__ __forceinline__ float silu_mul(float g, float u) { return (g / (1.0f + exp_det(-g))) * u; }
@@ -335,12 +348,16 @@ __device__ __forceinline__ int wave_max_i32(int v) {
              max(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
 }
 
-// Softmax + top-k of one token on one wave (moe_routing_topk.metal:31-56).
+// Softmax + top-k of one token on one wave (moe_routing_topk.metal:24-56).
 // lane l holds the logits of experts l, l+64, l+128, l+192 (absent ones are
-// ignored). m = max logit; e = exp_det(l - m); S = sum of e in the wave order
+// ignored). Under the reference rule (rule == OBS_ROUTE_REF) each logit is
+// first rounded to f16, the type dequant_matvec_8bit.metal:30 stores it in.
+// m = max logit; e = exp_det(l - m); S = sum of e in the wave order
 // (lane-serial over its experts from 0, then wave_sum_asc); p = e / S; k rounds
 // select the largest p (lowest expert id on ties); wsum is the serial sum of
-// the selected p; weights are p / wsum when norm_topk and wsum > 0.
+// the selected p; weights are p / wsum when norm_topk and wsum > 0. Under the
+// reference rule the weights are stored as f16 values: f16(p), renormalised as
+// f16(f16(p) / wsum) (moe_routing_topk.metal:47, :55).
 // Lane kk < k receives slot kk (id -1, weight 0 if nothing is selectable).
 // Must be called with all 64 lanes active. NQ = logit slots per lane
 // (ceil(n_exp / 64), at most 4); selection is branch-free per round.
@@ -348,12 +365,15 @@ __device__ __forceinline__ int wave_max_i32(int v) {
 // key = bit pattern of p = e / S (non-negative, so integer order = p order),
 // -1 for an absent expert, -2 for NaN.
 template <int NQ>
-__device__ __forceinline__ void route_keys(const float (&lg)[NQ], uint32_t n_exp, uint32_t lane, int (&key)[NQ]) {
+__device__ __forceinline__ void route_keys(const float (&lg_in)[NQ], uint32_t n_exp, uint32_t lane, int rule,
+                                           int (&key)[NQ]) {
   bool present[NQ];
+  float lg[NQ];
   float m = -__builtin_huge_valf();
 #pragma unroll
   for (int j = 0; j < NQ; ++j) {
     present[j] = lane + 64u * j < n_exp;
+    lg[j] = rule == OBS_ROUTE_REF ? round_f16(lg_in[j]) : lg_in[j];
     m = present[j] ? __builtin_fmaxf(m, lg[j]) : m;
   }
   m = wave_max_f32(m);
@@ -361,7 +381,7 @@ __device__ __forceinline__ void route_keys(const float (&lg)[NQ], uint32_t n_exp
   float a = 0.0f;
 #pragma unroll
   for (int j = 0; j < NQ; ++j) {
-    e[j] = exp_det(present[j] ? lg[j] - m : -100.0f);  // absent -> 0, not added below
+    e[j] = exp_det(present[j] ? lg[j] - m : -1000.0f);  // absent -> 0, not added below
     a = present[j] ? a + e[j] : a;
   }
   const float S = wave_sum_asc(a);
@@ -372,11 +392,20 @@ __device__ __forceinline__ void route_keys(const float (&lg)[NQ], uint32_t n_exp
   }
 }
 
+// Weight of a selected expert from its p and the sum of the selected p.
+__device__ __forceinline__ float route_weight(float p, float wsum, int norm_topk, int rule) {
+  if (rule == OBS_ROUTE_REF) {
+    const float w = round_f16(p);
+    return (norm_topk && wsum > 0.0f) ? round_f16(w / wsum) : w;
+  }
+  return (norm_topk && wsum > 0.0f) ? p / wsum : p;
+}
+
 template <int NQ>
 __device__ __forceinline__ void route_wave(const float (&lg)[NQ], uint32_t n_exp, uint32_t k, int norm_topk,
-                                           uint32_t lane, int32_t* my_id, float* my_w) {
+                                           int rule, uint32_t lane, int32_t* my_id, float* my_w) {
   int key[NQ];
-  route_keys<NQ>(lg, n_exp, lane, key);
+  route_keys<NQ>(lg, n_exp, lane, rule, key);
   float wsum = 0.0f;
   int32_t sel_id = -1;
   float sel_p = 0.0f;
@@ -400,10 +429,8 @@ __device__ __forceinline__ void route_wave(const float (&lg)[NQ], uint32_t n_exp
 #pragma unroll
     for (int j = 0; j < NQ; ++j) key[j] = (64u * j + lane == bidx) ? -1 : key[j];
   }
-  float w = sel_p;
-  if (norm_topk && wsum > 0.0f && sel_id >= 0) w = sel_p / wsum;
   *my_id = sel_id;
-  *my_w = sel_id >= 0 ? w : 0.0f;
+  *my_w = sel_id >= 0 ? route_weight(sel_p, wsum, norm_topk, rule) : 0.0f;
 }
 
 // Same contract and bit-identical result as route_wave for k = 8, without
@@ -415,11 +442,11 @@ __device__ __forceinline__ void route_wave(const float (&lg)[NQ], uint32_t n_exp
 // Because (key desc, id asc) is a strict total order, this equals k rounds of
 // "largest p, lowest id on ties".
 template <int NQ>
-__device__ __forceinline__ void route_wave_top8(const float (&lg)[NQ], uint32_t n_exp, int norm_topk,
+__device__ __forceinline__ void route_wave_top8(const float (&lg)[NQ], uint32_t n_exp, int norm_topk, int rule,
                                                 uint32_t lane, int32_t* my_id, float* my_w) {
   constexpr int K = 8;
   int key[NQ];
-  route_keys<NQ>(lg, n_exp, lane, key);
+  route_keys<NQ>(lg, n_exp, lane, rule, key);
   // (1) T = largest value with count(key >= T) >= K (0 if fewer than K selectable)
   int T = 0;
 #pragma unroll
@@ -491,10 +518,8 @@ __device__ __forceinline__ void route_wave_top8(const float (&lg)[NQ], uint32_t 
     sel_id = (lane == static_cast<uint32_t>(s)) ? si[s] : sel_id;
     sel_p = (lane == static_cast<uint32_t>(s)) ? ps : sel_p;
   }
-  float w = sel_p;
-  if (norm_topk && wsum > 0.0f && sel_id >= 0) w = sel_p / wsum;
   *my_id = sel_id;
-  *my_w = sel_id >= 0 ? w : 0.0f;
+  *my_w = sel_id >= 0 ? route_weight(sel_p, wsum, norm_topk, rule) : 0.0f;
 }
 
 }  // namespace obsd

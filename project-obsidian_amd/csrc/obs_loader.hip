@@ -860,6 +860,7 @@ int obs_ckpt_config(obs_ckpt* ck, obs_moe_config* cfg, uint32_t* n_layers) {
   cfg->group = static_cast<uint32_t>(group);
   cfg->norm_topk = norm_topk ? 1 : 0;
   cfg->rms_eps = fv[0];
+  cfg->route_rule = OBS_ROUTE_REF;  // the reference engine routes on f16 logits
   if (n_layers) *n_layers = static_cast<uint32_t>(u[0]);
   return OBS_OK;
 }

@@ -35,7 +35,7 @@ int check_moe_layer(obs_ctx* ctx, const char* who, const obs_moe_layer* L);
 int launch_gate_logits(obs_ctx* ctx, const uint32_t* w8, const uint16_t* s, const uint16_t* b,
                        const uint16_t* x, float* logits, uint32_t T, uint32_t in, uint32_t n_exp, uint32_t group);
 int launch_route_topk(obs_ctx* ctx, const float* logits, int32_t* ids, float* w, uint32_t T,
-                      uint32_t n_exp, uint32_t k, int norm_topk);
+                      uint32_t n_exp, uint32_t k, int norm_topk, int rule);
 }  // namespace obs
 
 namespace {
@@ -846,9 +846,10 @@ PrefillWs prefill_layout(const obs_moe_config* cfg, uint32_t T) {
   const size_t R = static_cast<size_t>(T) * cfg->top_k;
   L.max_tiles = static_cast<uint32_t>((R + TM - 1) / TM + cfg->n_exp);
   size_t o = 0;
-  L.logits = o; o += al256(sizeof(float) * T * cfg->n_exp);
+  // the routing first, at the offsets the C ABI documents (read after a computed routing)
   L.ids = o; o += al256(sizeof(int32_t) * R);
   L.w = o; o += al256(sizeof(float) * R);
+  L.logits = o; o += al256(sizeof(float) * T * cfg->n_exp);
   L.counts = o; o += al256(sizeof(int32_t) * cfg->n_exp);
   L.offsets = o; o += al256(sizeof(int32_t) * (cfg->n_exp + 1));
   L.nchunks = (T + GROUP_TOKENS - 1) / GROUP_TOKENS;
@@ -959,7 +960,7 @@ int obs_moe_prefill(obs_ctx* ctx, const obs_moe_config* cfg, const obs_moe_layer
     rc = obs::launch_gate_logits(ctx, layer->router_w, layer->router_s, layer->router_b, Xin,
                                  reinterpret_cast<float*>(base + L.logits), T, H, E, cfg->group);
     if (rc) return rc;
-    rc = obs::launch_route_topk(ctx, reinterpret_cast<float*>(base + L.logits), d_ids, d_w, T, E, k, cfg->norm_topk);
+    rc = obs::launch_route_topk(ctx, reinterpret_cast<float*>(base + L.logits), d_ids, d_w, T, E, k, cfg->norm_topk, cfg->route_rule);
     if (rc) return rc;
     ids = d_ids;
     weights = d_w;

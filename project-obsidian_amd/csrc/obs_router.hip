@@ -9,13 +9,16 @@
 // column order from 0; the lanes are combined by an xor butterfly with
 // offsets 32, 16, 8, 4, 2, 1.
 //
-// Selection (moe_routing_topk.metal:31-56): m = max logit; e_i = exp(l_i - m)
+// Selection (moe_routing_topk.metal:24-56): under the reference rule each
+// logit is first rounded to f16 (dequant_matvec_8bit.metal:30 stores halves);
+// m = max logit; e_i = exp(l_i - m)
 // with the deterministic exp; S = sum e_i where lane l adds e_l, e_{l+64},
 // e_{l+128}, e_{l+192} in that order and the lanes are combined by the xor
 // butterfly; p_i = e_i / S; k rounds of argmax over p (lower id wins ties);
 // wsum = serial sum of the selected p; if norm_topk and wsum > 0 the weights
-// are p / wsum. All steps are correctly rounded fp32 operations, so the ids
-// and weights are bit-identical to the oracle given the same logits.
+// are p / wsum (under the reference rule f16(p) and f16(f16(p) / wsum)). All
+// steps are correctly rounded operations, so the ids and weights are
+// bit-identical to the oracle given the same logits.
 #include "obs_internal.hpp"
 
 namespace {
@@ -98,7 +101,7 @@ __global__ void __launch_bounds__(256) q8_gate_logits_kernel(const uint32_t* __r
 template <int NQ>
 __global__ void __launch_bounds__(256) route_topk_kernel(const float* __restrict__ logits, int32_t* __restrict__ ids,
                                                          float* __restrict__ weights, uint32_t T, uint32_t n_exp,
-                                                         uint32_t k, int norm_topk) {
+                                                         uint32_t k, int norm_topk, int rule) {
   const uint32_t lane = threadIdx.x & 63;
   const uint32_t t = blockIdx.x * 4 + threadIdx.x / 64;
   if (t >= T) return;  // wave-uniform: every lane of a wave shares t
@@ -109,9 +112,9 @@ __global__ void __launch_bounds__(256) route_topk_kernel(const float* __restrict
   int32_t id;
   float w;
   if (k == 8)
-    route_wave_top8<NQ>(l, n_exp, norm_topk, lane, &id, &w);
+    route_wave_top8<NQ>(l, n_exp, norm_topk, rule, lane, &id, &w);
   else
-    route_wave<NQ>(l, n_exp, k, norm_topk, lane, &id, &w);
+    route_wave<NQ>(l, n_exp, k, norm_topk, rule, lane, &id, &w);
   if (lane < k) {
     ids[static_cast<uint64_t>(t) * k + lane] = id;
     weights[static_cast<uint64_t>(t) * k + lane] = w;
@@ -151,13 +154,13 @@ int launch_gate_logits(obs_ctx* ctx, const uint32_t* w8, const uint16_t* s, cons
 }
 
 int launch_route_topk(obs_ctx* ctx, const float* logits, int32_t* ids, float* w, uint32_t T,
-                      uint32_t n_exp, uint32_t k, int norm_topk) {
+                      uint32_t n_exp, uint32_t k, int norm_topk, int rule) {
   if (n_exp <= 64)
-    OBS_LAUNCH(ctx, "route_topk", route_topk_kernel<1><<<(T + 3) / 4, 256, 0, ctx->stream>>>(logits, ids, w, T, n_exp, k, norm_topk));
+    OBS_LAUNCH(ctx, "route_topk", route_topk_kernel<1><<<(T + 3) / 4, 256, 0, ctx->stream>>>(logits, ids, w, T, n_exp, k, norm_topk, rule));
   else if (n_exp <= 128)
-    OBS_LAUNCH(ctx, "route_topk", route_topk_kernel<2><<<(T + 3) / 4, 256, 0, ctx->stream>>>(logits, ids, w, T, n_exp, k, norm_topk));
+    OBS_LAUNCH(ctx, "route_topk", route_topk_kernel<2><<<(T + 3) / 4, 256, 0, ctx->stream>>>(logits, ids, w, T, n_exp, k, norm_topk, rule));
   else
-    OBS_LAUNCH(ctx, "route_topk", route_topk_kernel<4><<<(T + 3) / 4, 256, 0, ctx->stream>>>(logits, ids, w, T, n_exp, k, norm_topk));
+    OBS_LAUNCH(ctx, "route_topk", route_topk_kernel<4><<<(T + 3) / 4, 256, 0, ctx->stream>>>(logits, ids, w, T, n_exp, k, norm_topk, rule));
   return OBS_OK;
 }
 
@@ -180,15 +183,17 @@ int obs_q8_gate_logits(obs_ctx* ctx, const uint32_t* w8, const uint16_t* scales,
 }
 
 int obs_route_topk(obs_ctx* ctx, const float* logits, int32_t* ids, float* weights, uint32_t T,
-                   uint32_t n_exp, uint32_t k, int norm_topk) {
+                   uint32_t n_exp, uint32_t k, int norm_topk, int rule) {
   if (!ctx) return OBS_E_INVALID;
   if (!logits || !ids || !weights) return obs::set_error(ctx, OBS_E_INVALID, "obs_route_topk: null pointer");
   if (n_exp == 0 || n_exp > 256)
     return obs::set_error(ctx, OBS_E_SHAPE, "obs_route_topk: n_exp must be in [1, 256] (got %u)", n_exp);
   if (k == 0 || k > n_exp || k > 64)
     return obs::set_error(ctx, OBS_E_SHAPE, "obs_route_topk: k must be in [1, min(n_exp, 64)] (got %u)", k);
+  if (rule != OBS_ROUTE_REF && rule != OBS_ROUTE_F32)
+    return obs::set_error(ctx, OBS_E_INVALID, "obs_route_topk: unknown rule %d", rule);
   if (T == 0) return OBS_OK;
-  return obs::launch_route_topk(ctx, logits, ids, weights, T, n_exp, k, norm_topk);
+  return obs::launch_route_topk(ctx, logits, ids, weights, T, n_exp, k, norm_topk, rule);
 }
 
 }  // extern "C"

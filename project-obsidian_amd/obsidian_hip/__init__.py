@@ -34,6 +34,8 @@ OBS_E_NOMEM = -5
 OBS_E_UNSUPPORTED = -6
 
 OBS_DECODE_AUTO, OBS_DECODE_MULTI, OBS_DECODE_FUSED = 0, 1, 2
+# routing rules (obs_route_topk, MoeConfig.route_rule)
+ROUTE_REF, ROUTE_F32 = 0, 1
 
 _ERRNAMES = {
     OBS_E_INVALID: "OBS_E_INVALID",
@@ -71,7 +73,7 @@ class ObsError(RuntimeError):
 class ObsMoeConfig(C.Structure):
     _fields_ = [("n_exp", C.c_uint32), ("top_k", C.c_uint32), ("hidden", C.c_uint32),
                 ("inter", C.c_uint32), ("group", C.c_uint32), ("norm_topk", C.c_int32),
-                ("rms_eps", C.c_float)]
+                ("rms_eps", C.c_float), ("route_rule", C.c_int32)]
 
 
 class ObsMoeLayer(C.Structure):
@@ -137,7 +139,7 @@ def lib() -> C.CDLL:
         "obs_q4_matvec": (i32, [vp, vp, vp, vp, vp, vp, vp, u32, u32, u32]),
         "obs_q4_matmul": (i32, [vp, vp, vp, vp, vp, vp, u32, u32, u32, u32]),
         "obs_q8_gate_logits": (i32, [vp, vp, vp, vp, vp, vp, u32, u32, u32, u32]),
-        "obs_route_topk": (i32, [vp, vp, vp, vp, u32, u32, u32, C.c_int]),
+        "obs_route_topk": (i32, [vp, vp, vp, vp, u32, u32, u32, C.c_int, C.c_int]),
         "obs_swiglu": (i32, [vp, vp, vp, vp, u32]),
         "obs_scaled_add": (i32, [vp, vp, vp, f32, u32]),
         "obs_rmsnorm": (i32, [vp, vp, vp, vp, u32, u32, f32]),
@@ -364,9 +366,12 @@ class ObsidianExecutor:
         self._check(lib().obs_q8_gate_logits(self.ctx, _ptr(w), _ptr(s), _ptr(b), _ptr(x), _ptr(logits), T,
                                              in_f, n_exp, group))
 
-    def route_topk(self, logits, ids, weights, T: int, n_exp: int, k: int, norm_topk: bool) -> None:
+    def route_topk(self, logits, ids, weights, T: int, n_exp: int, k: int, norm_topk: bool,
+                   rule: int = None) -> None:
+        """rule: ROUTE_REF (default; the reference's f16 logits and weights) or ROUTE_F32."""
+        rule = ROUTE_REF if rule is None else rule
         self._check(lib().obs_route_topk(self.ctx, _ptr(logits), _ptr(ids), _ptr(weights), T, n_exp, k,
-                                         int(bool(norm_topk))))
+                                         int(bool(norm_topk)), int(rule)))
 
     def swiglu_raw(self, g, u, h, n: int) -> None:
         self._check(lib().obs_swiglu(self.ctx, _ptr(g), _ptr(u), _ptr(h), n))
@@ -443,6 +448,23 @@ class ObsidianExecutor:
         self._check(lib().obs_sdpa_prefill(self.ctx, _ptr(q), _ptr(k_cache), _ptr(v_cache_t), _ptr(out), n_heads,
                                            n_kv, head_dim, max_len, pos0, n_tokens, q_ld))
 
+    def download_raw(self, ptr: int, shape, dtype) -> np.ndarray:
+        """Copies device bytes at `ptr` into a new host array (Buffer::contents after a drain)."""
+        out = np.empty(shape, dtype=dtype)
+        if out.nbytes:
+            self._check(lib().obs_download(self.ctx, out.ctypes.data, ptr, out.nbytes))
+        return out
+
+    def prefill_routing(self, cfg: "MoeConfig", T: int, ws) -> Tuple[np.ndarray, np.ndarray]:
+        """(ids int32 [T, top_k], weights fp32 [T, top_k]) that a moe_prefill
+        with computed routing left at the start of its workspace: the values
+        prefill_batched reads back per token with read_route (forward.rs:175-182)."""
+        R = T * cfg.top_k
+        base = _ptr(ws)
+        ids = self.download_raw(base, (T, cfg.top_k), np.int32)
+        w = self.download_raw(base + (4 * R + 255) // 256 * 256, (T, cfg.top_k), np.float32)
+        return ids, w
+
     def moe_prefill_workspace(self, cfg: "MoeConfig", T: int) -> int:
         c = cfg.to_c()
         return int(lib().obs_moe_prefill_workspace(C.byref(c), T))
@@ -466,10 +488,12 @@ class MoeConfig:
     group: int = 64
     norm_topk: bool = True
     rms_eps: float = 1e-6  # rms_norm_eps (model.rs:18); used when the layer has norm_w
+    # ROUTE_REF: f16 logits and weights, as moe_routing_topk.metal sees them; ROUTE_F32: fp32
+    route_rule: int = 0
 
     def to_c(self) -> ObsMoeConfig:
         return ObsMoeConfig(self.n_exp, self.top_k, self.hidden, self.inter, self.group, int(bool(self.norm_topk)),
-                            float(self.rms_eps))
+                            float(self.rms_eps), int(self.route_rule))
 
 
 PROJ_KEYS = ("gate_w", "gate_s", "gate_b", "up_w", "up_s", "up_b", "down_w", "down_s", "down_b",
@@ -501,13 +525,13 @@ class MoeRouter:
     """router.rs:16-94. `route` = dispatch + drain + read; `route_dispatch`
     returns device buffers; `read_route` reads them after a drain."""
 
-    def __init__(self, n_experts: int, top_k: int, norm_topk: bool):
-        self.n_experts, self.top_k, self.norm_topk = n_experts, top_k, norm_topk
+    def __init__(self, n_experts: int, top_k: int, norm_topk: bool, rule: int = 0):
+        self.n_experts, self.top_k, self.norm_topk, self.rule = n_experts, top_k, norm_topk, rule
 
     def route_dispatch(self, exe: ObsidianExecutor, gate_logits: DeviceBuffer, T: int = 1):
         idx = exe.alloc((T, self.top_k), np.int32)
         w = exe.alloc((T, self.top_k), np.float32)
-        exe.route_topk(gate_logits, idx, w, T, self.n_experts, self.top_k, self.norm_topk)
+        exe.route_topk(gate_logits, idx, w, T, self.n_experts, self.top_k, self.norm_topk, self.rule)
         return idx, w
 
     def read_route(self, idx_buf: DeviceBuffer, w_buf: DeviceBuffer):
@@ -603,7 +627,8 @@ class Checkpoint:
         """(MoeConfig, num_hidden_layers) from config.json."""
         c, n = ObsMoeConfig(), C.c_uint32()
         self._check(lib().obs_ckpt_config(self.h, C.byref(c), C.byref(n)))
-        return MoeConfig(c.n_exp, c.top_k, c.hidden, c.inter, c.group, bool(c.norm_topk), c.rms_eps), n.value
+        return MoeConfig(c.n_exp, c.top_k, c.hidden, c.inter, c.group, bool(c.norm_topk), c.rms_eps,
+                         c.route_rule), n.value
 
     def tensor_info(self, name: str) -> TensorInfo:
         i = ObsTensorInfo()

@@ -148,6 +148,10 @@ class Model:
         self.state.upload(np.array([pos, tok], np.int32))
 
     def read_state(self):
+        """(position, token) after the queued steps; raises if a fused kernel
+        of those steps recorded a device-side failure (a cross-workgroup wait
+        that timed out), whose outputs, and so this token, would be invalid."""
+        self.exe.device_status()
         pos, tok = self.state.download()
         return int(pos), int(tok)
 

@@ -14,10 +14,16 @@ format and of the operators:
   float64 -> float32 conversion rounds it.
 * mat-vec with one-hot x (fused_dequant_matvec_4bit.metal:14-53): y[o] = W[o, j]
   exactly (every other product is an exact zero).
-* top-k routing (moe_routing_topk.metal:31-56): ids are the k largest logits,
-  ties to the lower id; the renormalised weight of a chosen id is
-  exp(l_i - m) / sum over the chosen exp(l_j - m) (the full-softmax
-  denominator cancels), computed in float64. A -inf logit has p = 0 and is
+* top-k routing (moe_routing_topk.metal:24-56), in IEEE fp32 semantics: under
+  the reference rule ("ref") each logit is first rounded to f16, the half that
+  dequant_matvec_8bit.metal:30 stores (numpy's float16 conversion is round to
+  nearest even); e_i = fl32(exp(l_i - m)) with gradual underflow (numpy's
+  float64 -> float32 conversion of the float64 exp), p_i = fl32(e_i / S); the
+  ids are the k largest p, ties (including p that underflowed to 0) to the
+  lower id. Weights: "f32" rule p_i, renormalised exp(l_i - m) / sum over the
+  chosen exp(l_j - m) (the full-softmax denominator cancels, float64); "ref"
+  rule f16(p_i), renormalised f16(f16(p_i) / wsum) with wsum the fp32 sum of
+  the chosen p (moe_routing_topk.metal:47, :55). A -inf logit has p = 0 and is
   still chosen, after every positive p (strict > against a -inf start,
   :44-46). A NaN logit makes the softmax sum NaN (:33-39: max skips it, exp
   does not), so every p is NaN, no comparison succeeds and no id is chosen:
@@ -112,22 +118,36 @@ def onehot_matvec_case():
 
 
 def route_cases():
-    def top(logits, k, norm):
+    def f16(v):
+        return float(np.float16(v))
+
+    def top(logits, k, norm, rule):
         n = len(logits)
         if any(math.isnan(v) for v in logits):
             return [-1] * k, [0.0] * k
-        finite = list(range(n))
-        order = sorted(finite, key=lambda i: (-logits[i], i))  # larger first, lower id on ties
+        lg = [f16(v) for v in logits] if rule == "ref" else list(logits)
+        m = max(lg)
+        ed = [math.exp(v - m) for v in lg]               # float64
+        e32 = [float(np.float32(v)) for v in ed]         # one rounding, gradual underflow
+        S = float(np.float32(sum(e32)))
+        p32 = [float(np.float32(v / S)) for v in e32]
+        order = sorted(range(n), key=lambda i: (-p32[i], i))  # larger p first, lower id on ties
         sel = order[:k]
-        m = max(logits[i] for i in finite)
-        e = {i: math.exp(logits[i] - m) for i in finite}
-        tot = sum(e.values())
         ids = sel + [-1] * (k - len(sel))
-        p = [e[i] / tot for i in sel]
-        if norm:
-            s = sum(p)
-            p = [v / s for v in p] if s > 0 else p
-        return ids, p + [0.0] * (k - len(sel))
+        if rule == "f32":
+            if norm:
+                tot = sum(ed[i] for i in sel)
+                w = [ed[i] / tot for i in sel] if tot > 0 else [p32[i] for i in sel]
+            else:
+                w = [ed[i] / sum(ed) for i in sel]
+        else:
+            wsum = 0.0
+            for i in sel:
+                wsum = float(np.float32(wsum + p32[i]))
+            w = [f16(p32[i]) for i in sel]
+            if norm and wsum > 0:
+                w = [f16(v / wsum) for v in w]
+        return ids, w + [0.0] * (k - len(sel))
 
     cases = []
     base = [0.5, -1.0, 2.0, 2.0, 0.25, 3.0, -7.5, 2.0, 1.0, 0.0, -0.5, 1.5, 2.0, -2.0, 0.75, 3.0]
@@ -143,11 +163,23 @@ def route_cases():
     wide[17] = wide[90] = float(np.float32(max(wide) + 1.0))  # an exact tie at the top
     cases.append(("n128_tie_at_top", wide, 8, True))
     cases.append(("top1", wide, 1, True))
+    # fp32 logits that one f16 rounding makes equal: 2 + 2^-11 (id 9) rounds to 2.0
+    # (id 3), so the lower id goes first under the reference rule and last in fp32
+    near = [0.5, -1.0, 0.25, 2.0, 1.0, -0.5, 0.0, 1.5, -2.0, 2.0 + 2.0 ** -11, 0.75, -0.25, 1.25, -1.5, 0.125, 1.75]
+    cases.append(("f16_rounding_tie", near, 4, True))
+    # one f16 ulp apart at 4.0 (2^-8): still ordered under both rules
+    cases.append(("one_f16_ulp_apart", [4.0, 4.0 + 2.0 ** -8, 3.0, 4.0 - 2.0 ** -9] + [0.0] * 12, 4, True))
+    # logit gaps below -87.3 give subnormal p (ordered by value), below -104 p = 0 (ties by id)
+    cases.append(("subnormal_p", [0.0, -95.0, -90.0, -300.0, -200.0, -100.0] + [-500.0] * 10, 6, False))
+    # spread of the 30B-A3B router at the bench's weight scale (logit sd ~100): several p underflow
+    wide100 = [float(np.float32(v)) for v in np.random.default_rng(5).standard_normal(128) * 100.0]
+    cases.append(("sd100_spread", wide100, 8, True))
     out = []
-    for name, lg, k, norm in cases:
-        ids, w = top(lg, k, norm)
-        out.append({"name": name, "logits": [None if math.isnan(v) else v for v in lg], "k": k,
-                    "norm_topk": norm, "ids": ids, "weights": w})
+    for rule in ("f32", "ref"):
+        for name, lg, k, norm in cases:
+            ids, w = top(lg, k, norm, rule)
+            out.append({"name": f"{name}/{rule}", "rule": rule, "logits": [None if math.isnan(v) else v for v in lg],
+                        "k": k, "norm_topk": norm, "ids": ids, "weights": w})
     return out
 
 

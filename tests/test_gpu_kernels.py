@@ -92,9 +92,10 @@ def test_q8_gate_logits_bit_exact(exe, T):
         assert np.array_equal(got[t].view(np.uint32), ref.view(np.uint32)), f"token {t}"
 
 
+@pytest.mark.parametrize("rule", [O.ROUTE_REF, O.ROUTE_F32], ids=["ref", "f32"])
 @pytest.mark.parametrize("n_exp,k,norm", [(128, 8, True), (128, 8, False), (64, 4, True), (256, 8, True),
                                           (100, 7, True), (16, 16, True), (128, 1, True)])
-def test_route_topk_bit_exact(exe, n_exp, k, norm):
+def test_route_topk_bit_exact(exe, n_exp, k, norm, rule):
     rng = np.random.default_rng(400 + n_exp + k)
     T = 512
     lg = (rng.standard_normal((T, n_exp)) * 3).astype(np.float32)
@@ -105,13 +106,13 @@ def test_route_topk_bit_exact(exe, n_exp, k, norm):
     dl = exe.upload(lg)
     ids = exe.alloc((T, k), np.int32)
     w = exe.alloc((T, k), np.float32)
-    exe.route_topk(dl, ids, w, T, n_exp, k, norm)
+    exe.route_topk(dl, ids, w, T, n_exp, k, norm, rule=rule)
     gi, gw = ids.download(), w.download()
-    ri, rw = O.route_topk(lg, k, norm, O.SUM_WAVE)
+    ri, rw = O.route_topk(lg, k, norm, O.SUM_WAVE, rule=rule)
     assert np.array_equal(gi, ri)
     assert np.array_equal(gw.view(np.uint32), rw.view(np.uint32))
     # the reference's serial softmax order gives the same ids on this data
-    si, _ = O.route_topk(lg, k, norm, O.SUM_SERIAL)
+    si, _ = O.route_topk(lg, k, norm, O.SUM_SERIAL, rule=rule)
     assert np.array_equal(gi, si)
     assert list(gi[0]) == list(range(k))
 

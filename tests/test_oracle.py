@@ -188,14 +188,18 @@ def test_qmatvec_error_bound_vs_fp64(bits, in_f, out_f):
 
 # ---------------------------------------------------------------- exp / silu
 def test_exp_against_libm():
-    xs = np.concatenate([np.linspace(-86.0, 88.5, 200001, dtype=np.float32),
-                         np.float32([0.0, -0.0, 1e-30, -1e-30, 0.5, -0.5])])
+    xs = np.concatenate([np.linspace(-104.0, 88.5, 200001, dtype=np.float32),
+                         np.float32([0.0, -0.0, 1e-30, -1e-30, 0.5, -0.5, -87.3, -87.4, -103.9])])
     got = np.array([O.exp(float(v)) for v in xs[::7]], np.float32)
     ref = np.exp(xs[::7].astype(np.float64)).astype(np.float32)
     ulp = np.abs(got.view(np.int32).astype(np.int64) - ref.view(np.int32).astype(np.int64))
     assert ulp.max() <= 2
     assert O.exp(0.0) == 1.0
-    assert O.exp(-86.5) == 0.0 and O.exp(-1e30) == 0.0 and O.exp(float("-inf")) == 0.0
+    assert O.exp(-104.5) == 0.0 and O.exp(-1e30) == 0.0 and O.exp(float("-inf")) == 0.0
+    # gradual underflow: exp(-90) is the subnormal 2^-149 * round(exp(-90) / 2^-149)
+    sub = np.float32(O.exp(-90.0))
+    assert 0 < sub < np.finfo(np.float32).tiny
+    assert abs(int(sub.view(np.int32)) - int(np.float32(math.exp(-90.0)).view(np.int32))) <= 1
     assert math.isinf(O.exp(88.6)) and math.isnan(O.exp(float("nan")))
     srt = got[np.argsort(xs[::7], kind="stable")]
     assert np.all(np.diff(srt.astype(np.float64)) >= 0)  # monotone on the grid
@@ -270,7 +274,7 @@ def test_silu_mul_closed_form():
 def test_route_topk_matches_sorted_logits(order):
     rng = np.random.default_rng(9)
     lg = rng.standard_normal((64, 128)).astype(np.float32) * 3
-    ids, w = O.route_topk(lg, 8, True, order)
+    ids, w = O.route_topk(lg, 8, True, order, rule=O.ROUTE_F32)
     ref = np.argsort(-lg.astype(np.float64), axis=1, kind="stable")[:, :8]
     assert np.array_equal(ids, ref)
     # closed form of the renormalised weight: e_i / sum_sel e_j (full-softmax S cancels)
@@ -301,14 +305,14 @@ def test_route_topk_permutation_equivariance():
     assert np.array_equal(perm[ids_p[0]], ids[0])
 
 
-def test_route_topk_no_norm_and_f16_emulation():
+def test_route_topk_no_norm_and_f16_weights():
     rng = np.random.default_rng(11)
     lg = rng.standard_normal((4, 128)).astype(np.float32)
-    ids, w = O.route_topk(lg, 8, norm_topk=False)
+    ids, w = O.route_topk(lg, 8, norm_topk=False, rule=O.ROUTE_F32)
     p = np.exp(lg.astype(np.float64) - lg.max(axis=1, keepdims=True))
     p /= p.sum(axis=1, keepdims=True)
     assert np.allclose(w, np.take_along_axis(p, ids, axis=1), rtol=2e-6)
-    _, wf = O.route_topk(lg, 8, True, emulate_f16=True)
+    _, wf = O.route_topk(lg, 8, True)  # the reference rule stores f16 weights
     assert np.array_equal(wf.astype(np.float16).astype(np.float32), wf)
 
 
@@ -318,18 +322,120 @@ def test_route_topk_nan_and_k_equals_n():
     assert list(ids[0]) == [-1, -1, -1] and list(w[0]) == [0.0, 0.0, 0.0]
     rng = np.random.default_rng(12)
     lg = rng.standard_normal((3, 16)).astype(np.float32)
-    ids, w = O.route_topk(lg, 16)
+    ids, w = O.route_topk(lg, 16, rule=O.ROUTE_F32)
     assert all(sorted(r) == list(range(16)) for r in ids)
     assert np.allclose(w.sum(axis=1), 1.0, atol=1e-6)
+    ids, w = O.route_topk(lg, 16)
+    assert all(sorted(r) == list(range(16)) for r in ids)
+    assert np.allclose(w.sum(axis=1), 1.0, atol=16 * 2.0 ** -11)  # 16 f16 roundings
 
 
 def test_route_sum_orders_agree_on_random_data():
     rng = np.random.default_rng(13)
     lg = (rng.standard_normal((512, 128)) * 4).astype(np.float32)
+    a, wa = O.route_topk(lg, 8, True, O.SUM_SERIAL, rule=O.ROUTE_F32)
+    b, wb = O.route_topk(lg, 8, True, O.SUM_WAVE, rule=O.ROUTE_F32)
+    assert np.array_equal(a, b)
+    assert np.allclose(wa, wb, rtol=1e-6)
     a, wa = O.route_topk(lg, 8, True, O.SUM_SERIAL)
     b, wb = O.route_topk(lg, 8, True, O.SUM_WAVE)
     assert np.array_equal(a, b)
-    assert np.allclose(wa, wb, rtol=1e-6)
+    assert np.allclose(wa, wb, rtol=2.0 ** -10)  # f16 weights, at most one step apart
+
+
+def _f16_round(lg):
+    return np.asarray(lg, np.float32).astype(np.float16).astype(np.float32)
+
+
+def test_route_ref_rule_is_f32_rule_on_f16_logits():
+    """The reference rule selects exactly as the fp32 rule does on the logits
+    rounded to f16 (numpy's float16 conversion, round to nearest even), and its
+    weights are f16(p) and f16(f16(p) / wsum) of that rule's p
+    (moe_routing_topk.metal:47, :55), wsum the fp32 sum of the chosen p in rank order."""
+    rng = np.random.default_rng(14)
+    for scale in (0.5, 3.0, 100.0):
+        lg = (rng.standard_normal((400, 128)) * scale).astype(np.float32)
+        ids_r, w_r = O.route_topk(lg, 8, False)
+        ids_f, p = O.route_topk(_f16_round(lg), 8, False, rule=O.ROUTE_F32)
+        assert np.array_equal(ids_r, ids_f)
+        assert np.array_equal(w_r, _f16_round(p))
+        idsn, wn = O.route_topk(lg, 8, True)
+        assert np.array_equal(idsn, ids_r)
+        wsum = np.zeros(400, np.float32)
+        for r in range(8):
+            wsum = (wsum + p[:, r]).astype(np.float32)
+        want = np.where(wsum[:, None] > 0, _f16_round(_f16_round(p) / wsum[:, None]), _f16_round(p))
+        assert np.array_equal(wn, want)
+
+
+def test_route_ref_rule_forced_f16_ties():
+    """fp32 logits less than one f16 step apart round to one half: the lower id
+    then wins, whatever the fp32 order; the fp32 rule keeps the fp32 order."""
+    lg = np.zeros((2, 64), np.float32)
+    lg[0, 40] = 3.0
+    lg[0, 7] = 3.0 - 2.0 ** -12    # rounds up to 3.0 (the f16 step at 3.0 is 2^-9)
+    lg[1] = -1.0
+    lg[1, 40] = 2.0 ** -12 + 2.0 ** -23  # halfway between two halves: rounds to the even one, 2^-12
+    lg[1, 7] = 2.0 ** -12                # (exp(-2^-23) = 1 - 2^-23 keeps them apart in fp32)
+    ids_r, w_r = O.route_topk(lg, 2, True)
+    ids_f, w_f = O.route_topk(lg, 2, True, rule=O.ROUTE_F32)
+    for t in range(2):
+        assert list(ids_r[t]) == [7, 40] and list(ids_f[t]) == [40, 7], t
+        assert w_r[t, 0] == w_r[t, 1] and w_f[t, 0] > w_f[t, 1]
+
+
+def test_route_ref_rule_duplicate_rows_and_router_logits():
+    """Duplicate router rows give equal logits and the lower id wins; a row
+    that differs from another by one 8-bit step in one column gives an fp32
+    logit a little larger (at the higher id): where both round to one f16 they
+    tie under the reference rule (lower id first), while the fp32 rule puts the
+    larger, higher id first."""
+    E, H = 64, 512
+    rng = np.random.default_rng(15)
+    t = synth.moe_layer(31, E, H, 256, 64)
+    rw = t["router_w"].copy()
+    for a, b in ((3, 50), (9, 20)):  # row b copies row a
+        rw[b] = rw[a]
+        t["router_s"][b] = t["router_s"][a]
+        t["router_b"][b] = t["router_b"][a]
+    lo8 = ~np.uint32(0xFF)
+    rw[9, 0] = (rw[9, 0] & lo8) | np.uint32(100)
+    rw[20, 0] = (rw[20, 0] & lo8) | np.uint32(101)  # row 20 = row 9 + one step in column 0
+    t["router_w"] = rw
+    L = O.Layer(t, E, H, 256, 64)
+    x = synth.bf16_normal(rng, (512, H))
+    x[:, 0] = 0x3B80  # bf16 2^-8: row 20's logit exceeds row 9's by about s * 2^-8
+    lg, ids, _ = O.router(L, x, 8, True)
+    _, ids_f, _ = O.router(L, x, 8, True, rule=O.ROUTE_F32)
+    assert np.array_equal(lg[:, 3], lg[:, 50])
+    assert np.all(lg[:, 20] > lg[:, 9])
+    same16 = _f16_round(lg[:, 9]) == _f16_round(lg[:, 20])
+    assert same16.mean() > 0.9
+    seen = 0
+    for t_ in range(512):
+        row, row_f = list(ids[t_]), list(ids_f[t_])
+        if 50 in row:
+            assert 3 in row and row.index(3) == row.index(50) - 1
+        if 20 in row and 9 in row:
+            i9, i20 = row.index(9), row.index(20)
+            assert (i9 == i20 - 1) if same16[t_] else (i20 < i9)
+            seen += int(same16[t_])
+        if 20 in row_f and 9 in row_f and lg[t_].max() - lg[t_, 9] < 80.0:  # p normal: distinct
+            assert row_f.index(20) < row_f.index(9)  # fp32: the larger logit first
+    assert seen > 0  # the f16 tie was exercised
+
+
+def test_route_rule_divergence_rate_is_measured():
+    """The measured rate at which fp32 logits route differently from the
+    reference's f16 logits (router logit sd about 3 and about 100), so the rule
+    is known to matter; both rates are quoted where the rule is documented."""
+    rng = np.random.default_rng(16)
+    for sd in (3.0, 100.0):
+        lg = (rng.standard_normal((3000, 128)) * sd).astype(np.float32)
+        a, _ = O.route_topk(lg, 8, True, O.SUM_SERIAL)
+        b, _ = O.route_topk(lg, 8, True, O.SUM_WAVE, rule=O.ROUTE_F32)
+        rate = np.mean(np.any(a != b, axis=1))
+        assert 0.0 < rate < 0.1, (sd, rate)
 
 
 # ---------------------------------------------------------------- compositions
