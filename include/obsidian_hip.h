@@ -241,6 +241,23 @@ int obs_moe_decode(obs_ctx* ctx, const obs_moe_config* cfg, const obs_moe_layer*
                    const uint16_t* x, const uint16_t* residual, uint16_t* y,
                    int32_t* ids_out, float* w_out);
 
+/* obs_moe_decode without any allocation: the same kernels, results and path
+ * choice, with every intermediate (the fused path's exchange area, the
+ * 4-launch path's logits, routing, h and normalised x) in a file-scope device
+ * array of 272,896 bytes that each GPU holds for the life of the process
+ * (looked up per device by obs_create). It calls no hipMalloc, hipFree or
+ * allocating routine, so it may run under HIP graph capture without a warm-up
+ * call. Every shape obs_moe_decode accepts fits; a larger need would be
+ * rejected with OBS_E_NOMEM. All calls on one GPU share that array: calls that
+ * overlap in time on one GPU (two streams, two contexts, two threads) race and
+ * give wrong results; serialise them. A timed-out wait is reported by
+ * obs_device_status() of the calling context.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * (code under graph capture, tight serving loops, harnesses that forbid it). */
+int obs_moe_decode_static(obs_ctx* ctx, const obs_moe_config* cfg, const obs_moe_layer* layer,
+                          const uint16_t* x, const uint16_t* residual, uint16_t* y,
+                          int32_t* ids_out, float* w_out);
+
 /* Decode path selection (no reference counterpart; like the reference's
  * OBSIDIAN_NO_GEMM switch, forward.rs:125-126, it exists to compare paths). */
 enum { OBS_DECODE_AUTO = 0, OBS_DECODE_MULTI = 1, OBS_DECODE_FUSED = 2 };

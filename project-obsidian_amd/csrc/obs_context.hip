@@ -3,11 +3,51 @@
 // (src/forward.rs:264-286).
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 
 #include "obs_internal.hpp"
 
 namespace {
 thread_local std::string g_create_error;
+
+// The scratch of obs_moe_decode_static (the fused decode's exchange area and
+// the 4-launch path's intermediates), a file-scope device array: every GPU the
+// library runs on holds its own copy until the process ends. Host code never
+// passes `scratch` itself to a kernel (on the host it is only a stand-in for
+// the symbol): obs_create looks up each device's address once, with that
+// device current, and the contexts carry that address.
+static __device__ __align__(256) unsigned char scratch[obs::STATIC_SCRATCH_BYTES];
+
+constexpr int MAX_SCRATCH_DEVICES = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[MAX_SCRATCH_DEVICES] = {};
+
+// The current device's scratch address, looked up (and zeroed) on the first
+// call for that device; null with a message if the lookup fails.
+void* device_scratch(int device, std::string* err) {
+  if (device < 0 || device >= MAX_SCRATCH_DEVICES) {
+    *err = "device index beyond the static scratch table";
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> g(g_scratch_mu);
+  if (!g_scratch_ptr[device]) {
+    void* p = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      *err = std::string("hipGetSymbolAddress(scratch) failed: ") + hipGetErrorString(e);
+      return nullptr;
+    }
+    // the exchange area must start at zero (epoch 0 in every slot, count 0)
+    e = hipMemset(p, 0, obs::STATIC_SCRATCH_BYTES);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+      *err = std::string("clearing the static scratch failed: ") + hipGetErrorString(e);
+      return nullptr;
+    }
+    g_scratch_ptr[device] = p;
+  }
+  return g_scratch_ptr[device];
+}
 
 // Busy-waits `ticks` of the 100 MHz constant clock on one lane; always ends.
 __global__ void hold_kernel(uint64_t ticks) {
@@ -96,6 +136,16 @@ int obs_create(int device, obs_ctx** out) {
     return OBS_E_HIP;
   }
   ctx->stream = ctx->own_stream;
+  std::string serr;
+  ctx->scratch = device_scratch(device, &serr);
+  if (!ctx->scratch) {
+    g_create_error = serr;
+    (void)hipEventDestroy(ctx->ev_start);
+    (void)hipEventDestroy(ctx->ev_stop);
+    (void)hipStreamDestroy(ctx->own_stream);
+    delete ctx;
+    return OBS_E_HIP;
+  }
   *out = ctx;
   return OBS_OK;
 }

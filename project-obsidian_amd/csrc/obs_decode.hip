@@ -340,6 +340,26 @@ int obs_moe_decode(obs_ctx* ctx, const obs_moe_config* cfg, const obs_moe_layer*
   return obs::decode_multi(ctx, cfg, layer, x, residual, y, ids_out, w_out, static_cast<char*>(ws));
 }
 
+int obs_moe_decode_static(obs_ctx* ctx, const obs_moe_config* cfg, const obs_moe_layer* layer, const uint16_t* x,
+                          const uint16_t* residual, uint16_t* y, int32_t* ids_out, float* w_out) {
+  if (!ctx) return OBS_E_INVALID;
+  bool fused = false;
+  int rc = obs::decode_plan(ctx, "obs_moe_decode_static", cfg, layer, x, y, &fused);
+  if (rc) return rc;
+  if (!ctx->scratch)
+    return obs::set_error(ctx, OBS_E_UNSUPPORTED, "obs_moe_decode_static: no static scratch on device %d",
+                          ctx->device);
+  const size_t need = obs::multi_ws_bytes(cfg);
+  if (need > obs::STATIC_MULTI_BYTES)
+    return obs::set_error(ctx, OBS_E_NOMEM,
+                          "obs_moe_decode_static: the shape needs %zu bytes of scratch, the static array holds %zu",
+                          need, obs::STATIC_MULTI_BYTES);
+  ctx->scratch_used = true;
+  char* base = static_cast<char*>(ctx->scratch);
+  if (fused) return obs::launch_fused_decode_ws(ctx, cfg, layer, x, residual, y, ids_out, w_out, base);
+  return obs::decode_multi(ctx, cfg, layer, x, residual, y, ids_out, w_out, base + obs::STATIC_FUSED_BYTES);
+}
+
 int obs_set_decode_path(obs_ctx* ctx, int path) {
   if (!ctx) return OBS_E_INVALID;
   if (path != OBS_DECODE_AUTO && path != OBS_DECODE_MULTI && path != OBS_DECODE_FUSED)
@@ -352,7 +372,8 @@ int obs_device_status(obs_ctx* ctx) {
   if (!ctx) return OBS_E_INVALID;
   const int a = obs::fused_decode_status(ctx);
   const int b = obs::attn_fused_status(ctx);
-  return a != OBS_OK ? a : b;
+  const int c = ctx->scratch_used ? obs::fused_decode_status_ws(ctx, ctx->scratch) : OBS_OK;
+  return a != OBS_OK ? a : b != OBS_OK ? b : c;
 }
 
 }  // extern "C"

@@ -459,6 +459,8 @@ uint32_t fused_decode_workgroups() { return NWG; }
 
 size_t fused_decode_ws_bytes() { return WS_BYTES; }
 
+static_assert(WS_BYTES == STATIC_FUSED_BYTES, "the static scratch holds one exchange area");
+
 int launch_fused_decode(obs_ctx* ctx, const obs_moe_config* cfg, const obs_moe_layer* L, const uint16_t* x,
                         const uint16_t* residual, uint16_t* y, int32_t* ids_out, float* w_out) {
   if (!ctx->fused_ws) {

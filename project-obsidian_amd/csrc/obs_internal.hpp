@@ -38,6 +38,10 @@ struct obs_ctx {
   void* fused_ws = nullptr;
   // fused attention-half workspace (exchange slots + counters), zeroed once
   void* attn_ws = nullptr;
+  // this device's file-scope scratch array (obs_moe_decode_static), looked up
+  // once per device by obs_create; null if the lookup was not possible
+  void* scratch = nullptr;
+  bool scratch_used = false;  // obs_device_status then checks its error flag too
   // RoPE (cos, sin) table [rope_len][64][2] fp32 for rope_theta
   float* rope_table = nullptr;
   uint32_t rope_len = 0;
@@ -55,6 +59,14 @@ struct obs_graph {
 };
 
 namespace obs {
+
+// The scratch of obs_moe_decode_static: one file-scope device array per GPU
+// (obs_context.hip), the fused decode's exchange area followed by the
+// 4-launch path's logits / ids / weights / h / normalised x at the largest
+// shape obs_moe_decode accepts (E 256, top_k 8, inter 2048, hidden 4096).
+constexpr size_t STATIC_FUSED_BYTES = 197632;
+constexpr size_t STATIC_MULTI_BYTES = 1024 + 256 + 256 + 8 * 2048 * 4 + 4096 * 2;
+constexpr size_t STATIC_SCRATCH_BYTES = STATIC_FUSED_BYTES + STATIC_MULTI_BYTES;
 
 int set_error(obs_ctx* ctx, int code, const char* fmt, ...);
 

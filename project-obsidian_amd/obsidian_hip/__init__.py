@@ -52,7 +52,7 @@ EXPORTS = (
     "obs_get_stream", "obs_alloc", "obs_free", "obs_upload", "obs_download", "obs_memset",
     "obs_sync", "obs_timer_start", "obs_timer_stop", "obs_dequant", "obs_q4_matvec",
     "obs_q4_matmul", "obs_q8_gate_logits", "obs_route_topk", "obs_swiglu", "obs_scaled_add", "obs_rmsnorm",
-    "obs_moe_decode", "obs_moe_prefill_workspace", "obs_moe_prefill", "obs_capture_begin",
+    "obs_moe_decode", "obs_moe_decode_static", "obs_moe_prefill_workspace", "obs_moe_prefill", "obs_capture_begin",
     "obs_capture_end", "obs_graph_launch", "obs_graph_destroy", "obs_set_decode_path",
     "obs_device_status", "obs_stream_hold", "obs_profile_enable",
     "obs_profile_accumulate", "obs_profile_count", "obs_profile_stat", "obs_profile_clear",
@@ -144,6 +144,7 @@ def lib() -> C.CDLL:
         "obs_scaled_add": (i32, [vp, vp, vp, f32, u32]),
         "obs_rmsnorm": (i32, [vp, vp, vp, vp, u32, u32, f32]),
         "obs_moe_decode": (i32, [vp, C.POINTER(ObsMoeConfig), C.POINTER(ObsMoeLayer), vp, vp, vp, vp, vp]),
+        "obs_moe_decode_static": (i32, [vp, C.POINTER(ObsMoeConfig), C.POINTER(ObsMoeLayer), vp, vp, vp, vp, vp]),
         "obs_moe_prefill_workspace": (sz, [C.POINTER(ObsMoeConfig), u32]),
         "obs_moe_prefill": (i32, [vp, C.POINTER(ObsMoeConfig), C.POINTER(ObsMoeLayer), vp, vp, vp, u32,
                                   vp, vp, vp, sz]),
@@ -387,6 +388,14 @@ class ObsidianExecutor:
         c, l = cfg.to_c(), layer.to_c()
         self._check(lib().obs_moe_decode(self.ctx, C.byref(c), C.byref(l), _ptr(x), _ptr(residual), _ptr(y),
                                          _ptr(ids_out), _ptr(w_out)))
+
+    def moe_decode_static(self, cfg: "MoeConfig", layer: "MoeLayer", x, y, residual=None, ids_out=None,
+                          w_out=None) -> None:
+        """moe_decode with no allocation (the device's static scratch); calls
+        that overlap in time on one GPU race."""
+        c, l = cfg.to_c(), layer.to_c()
+        self._check(lib().obs_moe_decode_static(self.ctx, C.byref(c), C.byref(l), _ptr(x), _ptr(residual),
+                                                _ptr(y), _ptr(ids_out), _ptr(w_out)))
 
     # -- the rest of a decode step (forward.rs:398-419, :445-462, :552-567) --
     def q4_gemv(self, x, in_f: int, parts: Sequence[Tuple], group: int = 64, norm_w=None, eps: float = 1e-6) -> None:
