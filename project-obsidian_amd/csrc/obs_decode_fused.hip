@@ -92,7 +92,8 @@ __global__ void __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 
   __shared__ uint32_t s_epoch;
   __shared__ int s_abort;
   __shared__ int32_t s_ids[FK];
-  __shared__ float s_w[FK];
+  __shared__ float s_p[FK];
+  __shared__ uint64_t s_comp[MAX_E];  // routing: (p bits << 9) | (511 - id), 0 = not selectable
   __shared__ bool s_ok;
   __shared__ __attribute__((aligned(16))) f16x2_t s_hp[FI / 2];  // h as f16 pairs, dot8_q4_off order
   __shared__ float s_hsum[FI / 32], s_hoff[FI / 32];              // per 32 columns: sum h, sum off*h
@@ -197,12 +198,19 @@ __global__ void __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 
         acc = __builtin_fmaf(wv, xf[c], acc);
       }
       acc = wave_sum_asc(acc);
-      if (lane == 0) slot_store(logit_slots + e, epoch, acc);
+      if (lane == 0) slot_store_xcd(logit_slots + e, epoch, acc);  // polled by this XCD only
     }
   }
 
   OBS_FUSED_MARK(2);
-  // ---- 2. every wave polls its group's logits and routes the token
+  // ---- 2. routing (moe_routing_topk.metal:24-56). Wave 0 polls its group's
+  // logits and turns them into selection keys (route_keys: the softmax p of
+  // each expert, from the f16-rounded logits under the reference rule). The k
+  // argmax rounds of the reference (largest p, lowest id on ties) select the
+  // experts that fewer than k others precede in that order, in that order; so
+  // all 256 threads count, in parallel, how many experts precede each one
+  // (composite keys make the order strict), and the experts with a count below
+  // k take the slot of that count.
   bool ok = true;
   float lg[NQ];
   if (wave == 0) {
@@ -224,25 +232,56 @@ __global__ void __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 
   }
   OBS_FUSED_MARK(9);
   if (!ok && lane == 0) raise_error(a.ws);
-  // one wave per workgroup routes (moe_routing_topk.metal:31-56), then
-  // broadcasts through LDS
   if (wave == 0) {
-    int32_t id;
-    float w;
-    route_wave<NQ>(lg, n_exp, FK, a.norm_topk, a.route_rule, lane, &id, &w);
+    int key[NQ];
+    route_keys<NQ>(lg, n_exp, lane, a.route_rule, key);
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const uint32_t id = lane + 64u * q;
+      s_comp[id] = key[q] >= 0 ? (static_cast<uint64_t>(key[q]) << 9) | (511u - id) : 0ull;
+    }
     if (lane < FK) {
-      s_ids[lane] = id;
-      s_w[lane] = w;
+      s_ids[lane] = -1;
+      s_p[lane] = 0.0f;
       s_ok = ok;
-      if (blockIdx.x == 0) {
-        if (a.ids_out) a.ids_out[lane] = id;
-        if (a.w_out) a.w_out[lane] = w;
-      }
+    }
+  }
+  __syncthreads();
+  {
+    constexpr uint32_t TPE = 4 / NQ;         // threads per expert
+    constexpr uint32_t CMP = 64 * NQ / TPE;  // composites each thread compares against
+    const uint32_t ei = tid / TPE, part = tid % TPE;
+    const uint64_t ci = s_comp[ei];
+    const uint64_t* cj = s_comp + part * CMP;
+    uint32_t c0 = 0, c1 = 0, c2 = 0, c3 = 0;  // four chains: independent adds
+#pragma unroll
+    for (uint32_t c = 0; c < CMP; c += 4) {
+      c0 += cj[c] > ci;
+      c1 += cj[c + 1] > ci;
+      c2 += cj[c + 2] > ci;
+      c3 += cj[c + 3] > ci;
+    }
+    uint32_t rank = (c0 + c1) + (c2 + c3);
+    if constexpr (TPE >= 2) rank += static_cast<uint32_t>(dpp_i32<DPP_XOR1>(static_cast<int>(rank)));
+    if constexpr (TPE >= 4) rank += static_cast<uint32_t>(dpp_i32<DPP_XOR2>(static_cast<int>(rank)));
+    if (part == 0 && ci != 0ull && rank < FK) {
+      s_ids[rank] = static_cast<int32_t>(ei);
+      s_p[rank] = __uint_as_float(static_cast<uint32_t>(ci >> 9));
     }
   }
   __syncthreads();
   ok = ok && s_ok;
-  const float sel_w = lane < FK ? s_w[lane] : 0.0f;  // rank weights in lanes 0..7 (combine)
+  // weights: wsum is the serial sum of the selected p in rank order (empty slots add +0)
+  float wsum = 0.0f;
+#pragma unroll
+  for (uint32_t r = 0; r < FK; ++r) wsum = wsum + s_p[r];
+  const int32_t my_id = lane < FK ? s_ids[lane] : -1;
+  const float sel_w = my_id >= 0 ? route_weight(s_p[lane & (FK - 1u)], wsum, a.norm_topk, a.route_rule)
+                                 : 0.0f;  // rank weights in lanes 0..7 (combine)
+  if (blockIdx.x == 0 && wave == 0 && lane < FK) {
+    if (a.ids_out) a.ids_out[lane] = my_id;
+    if (a.w_out) a.w_out[lane] = sel_w;
+  }
   const int32_t eg = s_ids[g];
   const bool have = ok && eg >= 0 && static_cast<uint32_t>(eg) < n_exp;
   OBS_FUSED_MARK(3);
@@ -328,7 +367,7 @@ __global__ void __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 
     pg = wave_sum_asc(pg);
     pu = wave_sum_asc(pu);
     const float hv = have ? silu_mul(pg, pu) : 0.0f;
-    if (lane == 0) slot_store(h_slots + e0 + 128u * t, epoch, hv);
+    if (lane == 0) slot_store_xcd(h_slots + e0 + 128u * t, epoch, hv);  // polled by this XCD only
   }
 
   OBS_FUSED_MARK(5);

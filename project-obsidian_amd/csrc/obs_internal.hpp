@@ -164,15 +164,16 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 // normal range underflow gradually, as IEEE exp does: p * 2^n is formed as
 // (p * 2^(n+64)) * 2^-64, one rounding into the subnormals. x < -104 -> +0
 // (exp(-104) is below half the smallest subnormal), x > 88.5 -> +inf, NaN -> NaN.
+// Branch-free: the polynomial runs on x clamped into [-104, 88.5] and the
+// special cases are selected at the end (a branch per case made the routing
+// wave diverge and reconverge around every call).
 __device__ __forceinline__ float exp_det(float x) {
-  if (x != x) return x;
-  if (x < -104.0f) return 0.0f;
-  if (x > 88.5f) return __builtin_huge_valf();
+  const float xc = __builtin_fminf(__builtin_fmaxf(x, -104.0f), 88.5f);
   const float LOG2E = 1.44269502162933349609375f;
   const float LN2_HI = 0.693145751953125f;
   const float LN2_LO = 1.428606765330187045e-06f;
-  const float n = __builtin_rintf(x * LOG2E);
-  float r = __builtin_fmaf(-n, LN2_HI, x);
+  const float n = __builtin_rintf(xc * LOG2E);
+  float r = __builtin_fmaf(-n, LN2_HI, xc);
   r = __builtin_fmaf(-n, LN2_LO, r);
   float p = 1.98412698e-04f;
   p = __builtin_fmaf(p, r, 1.38888889e-03f);
@@ -183,9 +184,15 @@ __device__ __forceinline__ float exp_det(float x) {
   p = __builtin_fmaf(p, r, 1.0f);
   p = __builtin_fmaf(p, r, 1.0f);
   int ni = static_cast<int>(n);
-  if (ni > 127) { p = p * 2.0f; ni -= 1; }
-  if (ni < -126) return (p * __uint_as_float(static_cast<uint32_t>(ni + 64 + 127) << 23)) * 0x1p-64f;
-  return p * __uint_as_float(static_cast<uint32_t>(ni + 127) << 23);
+  const bool big = ni > 127;
+  p = big ? p * 2.0f : p;
+  ni = big ? ni - 1 : ni;
+  const bool tiny = ni < -126;  // the result is subnormal: scale by 2^(n+64), then by 2^-64
+  float res = p * __uint_as_float(static_cast<uint32_t>(ni + (tiny ? 64 : 0) + 127) << 23);
+  res = tiny ? res * 0x1p-64f : res;
+  res = x < -104.0f ? 0.0f : res;
+  res = x > 88.5f ? __builtin_huge_valf() : res;
+  return x != x ? x : res;
 }
 
 // fp32 -> f16 (round to nearest even) -> fp32: the value a half holds
@@ -263,6 +270,16 @@ __device__ __forceinline__ float group8_sum(float v) {
 __device__ __forceinline__ void slot_store(uint64_t* p, uint32_t epoch, float v) {
   __hip_atomic_store(p, (static_cast<uint64_t>(epoch) << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
                      __HIP_MEMORY_SCOPE_SYSTEM);
+}
+// Exchange between workgroups of one XCD: a plain store (no write-through)
+// stays in the XCD's L2, where the agent-scope poll of slot_load reads it.
+// Measured on MI355X with two workgroups of one XCD: 0.27 us one way, against
+// 0.40 us for the write-through store; the line never queues behind HBM
+// traffic. Across XCDs such a store is not seen (each XCD has its own L2), so
+// only slots that one XCD both writes and polls use it.
+__device__ __forceinline__ void slot_store_xcd(uint64_t* p, uint32_t epoch, float v) {
+  __hip_atomic_store(p, (static_cast<uint64_t>(epoch) << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_WAVEFRONT);
 }
 __device__ __forceinline__ uint64_t slot_load(const uint64_t* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -342,23 +359,28 @@ __device__ __forceinline__ void f16_pairs8(const float* x, f16x2_t* xp) {
   xp[3] = f16x2_of(x[3], x[7]);
 }
 
-__device__ __forceinline__ float wave_max_f32(float v) {
-  v = __builtin_fmaxf(v, dpp_f32<DPP_XOR1>(v));
-  v = __builtin_fmaxf(v, dpp_f32<DPP_XOR2>(v));
-  v = __builtin_fmaxf(v, dpp_f32<DPP_HALF_MIRROR>(v));
-  v = __builtin_fmaxf(v, dpp_f32<DPP_MIRROR>(v));
-  return __builtin_fmaxf(__builtin_fmaxf(readlane_f32(v, 0), readlane_f32(v, 16)),
-                         __builtin_fmaxf(readlane_f32(v, 32), readlane_f32(v, 48)));
-}
-
+// Maximum over the 64 lanes, returned uniform: the row maxima meet in lane 63
+// through the row broadcasts (one lane read instead of four).
+constexpr int DPP_ROW_BCAST15 = 0x142;  // lane 15 of each row -> the next row (rows 1 and 3 enabled)
+constexpr int DPP_ROW_BCAST31 = 0x143;  // lane 31 -> rows 2 and 3
 __device__ __forceinline__ int wave_max_i32(int v) {
   v = max(v, dpp_i32<DPP_XOR1>(v));
   v = max(v, dpp_i32<DPP_XOR2>(v));
   v = max(v, dpp_i32<DPP_HALF_MIRROR>(v));
   v = max(v, dpp_i32<DPP_MIRROR>(v));
-  return max(max(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
-             max(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+  v = max(v, __builtin_amdgcn_update_dpp(v, v, DPP_ROW_BCAST15, 0xA, 0xF, false));
+  v = max(v, __builtin_amdgcn_update_dpp(v, v, DPP_ROW_BCAST31, 0xC, 0xF, false));
+  return __builtin_amdgcn_readlane(v, 63);
 }
+
+// Order-preserving int image of a float (larger float <-> larger int; NaN
+// maps above +inf).
+__device__ __forceinline__ int f32_order(float f) {
+  const int b = __float_as_int(f);
+  return b >= 0 ? b : b ^ 0x7fffffff;
+}
+__device__ __forceinline__ float f32_unorder(int k) { return __int_as_float(k >= 0 ? k : k ^ 0x7fffffff); }
+
 
 // Softmax + top-k of one token on one wave (moe_routing_topk.metal:24-56).
 // lane l holds the logits of experts l, l+64, l+128, l+192 (absent ones are
@@ -381,14 +403,17 @@ __device__ __forceinline__ void route_keys(const float (&lg_in)[NQ], uint32_t n_
                                            int (&key)[NQ]) {
   bool present[NQ];
   float lg[NQ];
-  float m = -__builtin_huge_valf();
+  int mk = f32_order(-__builtin_huge_valf());
 #pragma unroll
   for (int j = 0; j < NQ; ++j) {
     present[j] = lane + 64u * j < n_exp;
     lg[j] = rule == OBS_ROUTE_REF ? round_f16(lg_in[j]) : lg_in[j];
-    m = present[j] ? __builtin_fmaxf(m, lg[j]) : m;
+    mk = present[j] ? max(mk, f32_order(lg[j])) : mk;
   }
-  m = wave_max_f32(m);
+  // The maximum through the order-preserving int image. A NaN logit becomes
+  // the maximum here where fmaxf would skip it; either way every l - m, e and
+  // S then holds a NaN (a NaN logit's own e is NaN), so no expert is selectable.
+  const float m = f32_unorder(wave_max_i32(mk));
   float e[NQ];
   float a = 0.0f;
 #pragma unroll
@@ -426,18 +451,20 @@ __device__ __forceinline__ void route_wave(const float (&lg)[NQ], uint32_t n_exp
 #pragma unroll
     for (int j = 1; j < NQ; ++j) lm = max(lm, key[j]);
     const int bk = wave_max_i32(lm);
-    if (bk < 0) break;  // keys only decrease: no later slot is selectable either
+    // Branch-free: once nothing is selectable (bk < 0; keys only decrease) no
+    // key equals bk, so no id is taken and the later slots keep id -1.
     // lowest expert id holding bk: slot-major (ids 64j + lane), lowest lane first
     uint32_t bidx = 0xffffffffu;
 #pragma unroll
     for (int j = NQ - 1; j >= 0; --j) {
-      const unsigned long long mj = __ballot(key[j] == bk);
+      const unsigned long long mj = __ballot(key[j] == bk && bk >= 0);
       bidx = mj ? 64u * j + static_cast<uint32_t>(__builtin_ctzll(mj)) : bidx;
     }
     const float p = __int_as_float(bk);
-    sel_id = (lane == kk) ? static_cast<int32_t>(bidx) : sel_id;
-    sel_p = (lane == kk) ? p : sel_p;
-    wsum = wsum + p;
+    const bool take = bk >= 0;
+    sel_id = (lane == kk && take) ? static_cast<int32_t>(bidx) : sel_id;
+    sel_p = (lane == kk && take) ? p : sel_p;
+    wsum = take ? wsum + p : wsum;
 #pragma unroll
     for (int j = 0; j < NQ; ++j) key[j] = (64u * j + lane == bidx) ? -1 : key[j];
   }
