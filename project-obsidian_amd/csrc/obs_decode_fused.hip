@@ -24,9 +24,14 @@
 //      workgroup will need (64 rows x 384 B per workgroup), so the down weights
 //      arrive during the gate/up phase.
 //   3. h = silu(gate.x) * (up.x) goes to the group's h slots; each workgroup
-//      polls all 768 into LDS and finishes its 64 down rows from registers.
+//      polls them into LDS in three blocks, adding each block's terms to its 64
+//      down rows as the block arrives (the down weights are in registers).
 //   4. Group 0 combines: workgroup j polls the 8 ranks' outputs for its 64 rows
 //      and accumulates residual + sum_r w_r * y_r in rank order (forward.rs:440).
+//      (Spreading the combine over all 256 workgroups, 8 rows each, measured
+//      1 us slower per layer: every workgroup then waits on other XCDs.)
+// The logit and h slots are written and polled within one XCD and live in its
+// L2; the y slots cross XCDs and are written through to memory.
 // The epoch is derived from a device-side count of exited workgroups (see the
 // kernel's first lines), so graph replays need no host involvement.
 //
@@ -94,10 +99,10 @@ __global__ void __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 
   __shared__ int32_t s_ids[FK];
   __shared__ float s_p[FK];
   __shared__ uint64_t s_comp[MAX_E];  // routing: (p bits << 9) | (511 - id), 0 = not selectable
+  __shared__ float s_y[FK][64];
   __shared__ bool s_ok;
   __shared__ __attribute__((aligned(16))) f16x2_t s_hp[FI / 2];  // h as f16 pairs, dot8_q4_off order
   __shared__ float s_hsum[FI / 32], s_hoff[FI / 32];              // per 32 columns: sum h, sum off*h
-  __shared__ float s_y[FK][64];
   __shared__ __attribute__((aligned(16))) uint16_t s_sc[4][1536];  // per wave: staged scales (see phase 3)
 
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
@@ -371,84 +376,78 @@ __global__ void __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 
   }
 
   OBS_FUSED_MARK(5);
-  // ---- 5. poll the group's 768 h values; store them to LDS as f16 in the pair
-  // order of dot8_q4_off, with the sum and the offset sum of every 32 columns
-  // (32 consecutive columns sit in one half-wave)
+  // ---- 5/6. h arrives in three 256-column blocks. Block L = h[256L, 256L + 256)
+  // holds every workgroup's rows t = 2L and 2L + 1, which it finishes before
+  // its later rows, so the blocks become visible in order. The workgroup polls
+  // one block at a time (one slot per thread), stores it to LDS as f16 in the
+  // pair order of dot8_q4_off with the sum and the offset sum of every 32
+  // columns (32 consecutive columns sit in one half-wave), and adds the block's
+  // terms to its 64 down rows (of expert e_g, unscaled by w_g) while the later
+  // blocks are still being computed. The terms are added in block order, as a
+  // single pass over the row would add them.
+  reinterpret_cast<u32x4_t*>(s_sc[wave])[128u + lane] = scq2;  // down scales; chunks 176..191: padding
+  float part[2] = {0.0f, 0.0f};
   {
-    bool wave_ok = ok;
-    float hv[FI / 256];
-    const uint64_t t0 = wall_clock64();
-    while (wave_ok) {
-      bool ready = true;
-#pragma unroll
-      for (uint32_t u = 0; u < FI / 256; ++u) {
-        const uint64_t v = slot_load(h_slots + tid + 256u * u);
-        hv[u] = slot_val(v);
-        ready = ready && slot_ready(v, epoch);
-      }
-      if (__all(ready)) break;
-      if (wall_clock64() - t0 > WAIT_TICKS) {
-        wave_ok = false;
-        if (lane == 0) raise_error(a.ws);
-      }
-    }
-    ok = ok && wave_ok;
     _Float16* hp16 = reinterpret_cast<_Float16*>(s_hp);
-#pragma unroll
-    for (uint32_t u = 0; u < FI / 256; ++u) {
-      const uint32_t idx = tid + 256u * u, jn = idx & 7u;  // column idx = 8 * word + jn
-      hp16[(idx & ~7u) + 2u * (jn & 3u) + (jn >> 2)] = static_cast<_Float16>(hv[u]);
-      // offsets of dot8_q4_off: 1024 at even nibble positions, 64 at odd ones;
-      // the sums use the f16-rounded values the dot products see
-      const float hr = static_cast<float>(static_cast<_Float16>(hv[u]));
-      const float sum = half_wave_sum(hr);
-      const float off = half_wave_sum(hr * ((jn & 1u) ? 64.0f : 1024.0f));
-      if ((idx & 31u) == 0u) {
-        s_hsum[idx >> 5] = sum;
-        s_hoff[idx >> 5] = off;
-      }
-    }
-  }
-  __syncthreads();
-
-  OBS_FUSED_MARK(6);
-  // ---- 6. this workgroup's 64 down rows of expert e_g (unscaled by w_g)
-  reinterpret_cast<u32x4_t*>(s_sc[wave])[128u + lane] = scq2;  // chunks 176..191: padding
-  {
-    // the lane's 96 columns: blocks [256L + 32m, +32), L = 0..2
-    f16x2_t hp[48];
-    float hsum[3], hoff[3];
+    const uint64_t t0 = wall_clock64();
 #pragma unroll
     for (uint32_t L = 0; L < 3; ++L) {
+      float hv = 0.0f;
+      bool wave_ok = ok;
+      while (wave_ok) {
+        const uint64_t v = slot_load(h_slots + tid + 256u * L);
+        hv = slot_val(v);
+        if (__all(slot_ready(v, epoch))) break;
+        if (wall_clock64() - t0 > WAIT_TICKS) {
+          wave_ok = false;
+          if (lane == 0) raise_error(a.ws);
+        }
+      }
+      ok = ok && wave_ok;
+      {
+        const uint32_t idx = tid + 256u * L, jn = idx & 7u;  // column idx = 8 * word + jn
+        hp16[(idx & ~7u) + 2u * (jn & 3u) + (jn >> 2)] = static_cast<_Float16>(hv);
+        // offsets of dot8_q4_off: 1024 at even nibble positions, 64 at odd ones;
+        // the sums use the f16-rounded values the dot products see
+        const float hr = static_cast<float>(static_cast<_Float16>(hv));
+        const float sum = half_wave_sum(hr);
+        const float off = half_wave_sum(hr * ((jn & 1u) ? 64.0f : 1024.0f));
+        if ((idx & 31u) == 0u) {
+          s_hsum[idx >> 5] = sum;
+          s_hoff[idx >> 5] = off;
+        }
+      }
+      __syncthreads();
+      if (L == 0) OBS_FUSED_MARK(6);
+      // the lane's columns of block L: [256L + 32m, +32)
+      f16x2_t hp[16];
 #pragma unroll
       for (uint32_t c = 0; c < 16; c += 4) {
         const uint4 v = *reinterpret_cast<const uint4*>(s_hp + 128u * L + 16u * m + c);
-        hp[16 * L + c] = as_f16x2(v.x); hp[16 * L + c + 1] = as_f16x2(v.y);
-        hp[16 * L + c + 2] = as_f16x2(v.z); hp[16 * L + c + 3] = as_f16x2(v.w);
+        hp[c] = as_f16x2(v.x); hp[c + 1] = as_f16x2(v.y);
+        hp[c + 2] = as_f16x2(v.z); hp[c + 3] = as_f16x2(v.w);
       }
-      hsum[L] = s_hsum[8u * L + m];
-      hoff[L] = s_hoff[8u * L + m];
-    }
-#pragma unroll
-    for (uint32_t p = 0; p < 2; ++p) {
-      float part = 0.0f;
+      const float hsum = s_hsum[8u * L + m], hoff = s_hoff[8u * L + m];
       if (have) {
-        const uint16_t* dsb = sc16 + 1024u + 12u * (8u * p + r8);
 #pragma unroll
-        for (uint32_t L = 0; L < 3; ++L) {
+        for (uint32_t p = 0; p < 2; ++p) {
+          const uint16_t* dsb = sc16 + 1024u + 12u * (8u * p + r8);
           float acc = 0.0f;
-          acc = dot8_q4_off(dq[p][L].x, hp + 16u * L + 0, acc);
-          acc = dot8_q4_off(dq[p][L].y, hp + 16u * L + 4, acc);
-          acc = dot8_q4_off(dq[p][L].z, hp + 16u * L + 8, acc);
-          acc = dot8_q4_off(dq[p][L].w, hp + 16u * L + 12, acc);
+          acc = dot8_q4_off(dq[p][L].x, hp + 0, acc);
+          acc = dot8_q4_off(dq[p][L].y, hp + 4, acc);
+          acc = dot8_q4_off(dq[p][L].z, hp + 8, acc);
+          acc = dot8_q4_off(dq[p][L].w, hp + 12, acc);
           const uint32_t gi = 4u * L + m / 2u;  // quantization group of block L
-          part = part + __builtin_fmaf(bf16_to_f32(dsb[gi]), acc - hoff[L], bf16_to_f32(dsb[192u + gi]) * hsum[L]);
+          part[p] = part[p] + __builtin_fmaf(bf16_to_f32(dsb[gi]), acc - hoff, bf16_to_f32(dsb[192u + gi]) * hsum);
         }
       }
-      part = group8_sum(part);
-      const uint32_t row = dn_row0 + 8u * p + r8;
-      if (m == 0) slot_store(y_slots + size_t(g) * FH + row, epoch, part);
     }
+  }
+#pragma unroll
+  for (uint32_t p = 0; p < 2; ++p) {
+    const float v = group8_sum(part[p]);
+    const uint32_t row = dn_row0 + 8u * p + r8;
+    if (m == 0) slot_store(y_slots + size_t(g) * FH + row, epoch, v);
   }
 
   OBS_FUSED_MARK(7);
