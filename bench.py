@@ -133,13 +133,52 @@ def bench_decode(torch, oh, exe, args):
         name = None
     if name is not None:
         ach = nbytes / (us * 1e-6) / 1e9
+        traffic, prov = measured_traffic(name)
         roof = {"kernel": name, "bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
-                "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": measured_traffic(name),
+                "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic, "traffic_source": prov,
                 "bytes_per_launch": nbytes, "avg_launch_us": round(us, 3),
                 "event_pair_us": round(kernels[name]["avg_us"], 3)}
     del table, xs, ys
     torch.cuda.empty_cache()
     return {"ms_step": ms_step, "us_layer": us_layer, "gbs": gbs, "kernels": kernels, "roofline": roof}
+
+
+def bench_router(torch, oh, exe, reps=200):
+    """BASELINE config 1 on the GPU: 8-bit gate logits + softmax/top-8 for T = 1
+    and T = 512 tokens (gate_gpu + MoeRouter.route_dispatch, forward.rs:386-397,
+    router.rs:62-83). Each T's two launches are captured `reps` times in one
+    graph; the time per call is the replay time over reps."""
+    t = gpu_table(torch, 1, 555)[0]
+    w8, s8, b8 = (t[k].data_ptr() for k in ("router_w", "router_s", "router_b"))
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(11)
+    out = {}
+    for T in (1, 512):
+        x = torch.randn((T, H), device="cuda", generator=gen).to(torch.bfloat16)
+        lg = torch.empty((T, E), dtype=torch.float32, device="cuda")
+        ids = torch.empty((T, K), dtype=torch.int32, device="cuda")
+        w = torch.empty((T, K), dtype=torch.float32, device="cuda")
+        torch.cuda.synchronize()
+
+        def call():
+            exe.q8_gate_logits(w8, s8, b8, x.data_ptr(), lg.data_ptr(), T, H, E)
+            exe.route_topk(lg.data_ptr(), ids.data_ptr(), w.data_ptr(), T, E, K, True)
+
+        call()
+        exe.sync()
+        exe.capture_begin()
+        for _ in range(reps):
+            call()
+        g = exe.capture_end()
+        exe.graph_launch(g)
+        exe.sync()
+        exe.timer_start()
+        exe.graph_launch(g)
+        ms = exe.timer_stop()
+        exe.graph_destroy(g)
+        out[f"T{T}_us"] = round(1000.0 * ms / reps, 2)
+    del t
+    return out
 
 
 def gpu_decoder(torch, oh, D, exe, n_layers, max_len, seed):
@@ -294,16 +333,24 @@ def bench_decoder_prefill(exe, model, args):
 
 
 def measured_traffic(kernel):
-    """HBM bytes per launch of `kernel` from the committed counter summary
-    (rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE passes, each scaled by the same
-    counter over a plain device copy of known size); None when not measured."""
+    """(HBM bytes per launch of `kernel`, provenance) from the committed counter
+    summary (rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE passes, each scaled by
+    the same counter over a plain device copy of known size). The figure counts
+    only while the digest of the kernel's sources it was measured at matches
+    the sources now (obsidian_hip.profiles.source_digest); otherwise None."""
+    from obsidian_hip import profiles
     path = os.path.join(ROOT, "profiles", "hbm_traffic.json")
     try:
         with open(path) as f:
             rec = json.load(f).get(kernel)
     except (OSError, ValueError):
-        return None
-    return None if rec is None else rec.get("traffic_bytes_per_launch")
+        return None, "not measured"
+    if rec is None:
+        return None, "not measured"
+    now = profiles.source_digest(kernel)
+    if rec.get("source_sha") != now:
+        return None, f"stale: measured at sources {rec.get('source_sha')}, sources now {now}"
+    return rec.get("traffic_bytes_per_launch"), f"profiles/hbm_traffic.json (sources {now})"
 
 
 def calibrate_copy(torch, mib):
@@ -380,32 +427,72 @@ def bench_prefill(torch, oh, exe, args):
     return out
 
 
-def cpu_baseline(seconds, n_threads):
-    """The reference's CPU path: shader-semantics C rendering of the decode MoE
-    layer (router + 8 experts, serial fp32 per output row), OpenMP over rows."""
+def _median_us(fn, reps):
+    """Median wall time of `reps` calls of fn, in microseconds (one untimed call first)."""
+    fn()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    ts.sort()
+    return 1e6 * ts[len(ts) // 2]
+
+
+def cpu_baseline(n_threads, pf_sample=256):
+    """The reference's CPU path on this host, per BASELINE configuration: the
+    oracle's C rendering of the Metal shaders' semantics (serial fp32 dot per
+    output row, OpenMP over rows; kind "port") and the NumPy replica of
+    validate_dequant.py:24-30 with numpy's BLAS for the products. Medians of 20
+    repetitions (3 for the prefill, on a sample of its tokens)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import numpy as np
 
     import oracle as O
     from obsidian_hip import synth
 
+    O.set_threads(n_threads)
     t = synth.moe_layer(77, E, H, I, G)
     L = O.Layer(t, E, H, I, G)
     rng = np.random.default_rng(5)
     xs = synth.bf16_normal(rng, (64, H))
-    O.moe_decode_baseline(L, xs[0], K, True, n_threads)  # warm
-    n, t0 = 0, time.perf_counter()
-    while True:
-        O.moe_decode_baseline(L, xs[n % len(xs)], K, True, n_threads)
-        n += 1
-        el = time.perf_counter() - t0
-        if el >= seconds:
-            break
-    per_layer = el / n
-    return {"value": round(LAYER_BYTES / per_layer / 1e9, 3), "unit": "GB/s",
-            "us_per_layer": round(per_layer * 1e6, 1), "cores": n_threads, "kind": "port",
-            "sample": f"{n} decode MoE layers (T=1, top-8 of 128, one resident layer, "
-                      f"64 rotating inputs) in {el:.1f} s"}
+    W, S, B = t["down_w"][0], t["down_s"][0], t["down_b"][0]
+    xd = synth.bf16_bits_to_f32(synth.bf16_normal(rng, I))
+    Sf, Bf = synth.bf16_bits_to_f32(S), synth.bf16_bits_to_f32(B)
+    X512 = synth.bf16_normal(rng, (512, H))
+    ids, w = synth.zipf_routing(PREFILL_T, E, K, 1.1, seed=0)
+    Xp = synth.bf16_normal(rng, (PREFILL_T, H))
+    n = min(pf_sample, PREFILL_T)
+    it = iter(range(10 ** 9))
+    # the C rendering first, then the NumPy replica (so neither's idle threads spin during the other)
+    c = {"0": _median_us(lambda: O.qmatvec("shader", 4, W, S, B, xd, I, H), 20),
+         "1a": _median_us(lambda: O.router_baseline(L, xs[:1], K, True, n_threads), 20),
+         "1b": _median_us(lambda: O.router_baseline(L, X512, K, True, n_threads), 20),
+         "2": _median_us(lambda: O.moe_decode_baseline(L, xs[next(it) % 64], K, True, n_threads), 20),
+         "3": _median_us(lambda: O.moe_prefill_baseline(L, Xp[:n], ids[:n], w[:n], n_threads), 3)}
+    npy = {"0": _median_us(lambda: O.dequant_numpy(W, Sf, Bf) @ xd, 20),
+           "1a": _median_us(lambda: O.router_numpy(t, xs[:1], K, True), 20),
+           "1b": _median_us(lambda: O.router_numpy(t, X512, K, True), 20),
+           "2": _median_us(lambda: O.decode_layer_numpy(t, xs[next(it) % 64], K), 20),
+           "3": _median_us(lambda: O.prefill_numpy(t, Xp[:n], ids[:n], w[:n]), 3)}
+    out = {"0_down_proj_matvec": {"c_us": round(c["0"], 1), "numpy_us": round(npy["0"], 1)},
+           "1_router": {"T1": {"c_us": round(c["1a"], 1), "numpy_us": round(npy["1a"], 1)},
+                        "T512": {"c_us": round(c["1b"], 1), "numpy_us": round(npy["1b"], 1)}},
+           "2_decode_layer": {"c_us": round(c["2"], 1), "numpy_us": round(npy["2"], 1)},
+           "3_prefill": {"sample_tokens": n, "c_ms_sample": round(c["3"] / 1000, 1),
+                         "numpy_ms_sample": round(npy["3"] / 1000, 1),
+                         "c_ms_T2048_est": round(c["3"] / 1000 * PREFILL_T / n, 1)}}
+    c2 = c["2"]
+    try:
+        from threadpoolctl import threadpool_info
+        blas = sorted({d.get("num_threads") for d in threadpool_info() if d.get("user_api") == "blas"})
+    except Exception:  # threadpoolctl missing: report unknown
+        blas = []
+    return {"value": round(LAYER_BYTES / (c2 * 1e-6) / 1e9, 3), "unit": "GB/s", "us_per_layer": round(c2, 1),
+            "cores": n_threads, "kind": "port",
+            "sample": ("median of 20 decode MoE layers (T=1, top-8 of 128, one resident layer, rotating inputs), "
+                       "C rendering of the shader semantics, OpenMP over rows"),
+            "host_cpus": len(os.sched_getaffinity(0)), "numpy_blas_threads": blas, "configs": out}
 
 
 def main():
@@ -416,7 +503,6 @@ def main():
     ap.add_argument("--layers", type=int, default=48)
     ap.add_argument("--input-sets", type=int, default=4)
     ap.add_argument("--prof-reps", type=int, default=5)
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-decoder", action="store_true")
@@ -440,12 +526,17 @@ def main():
 
     exe = oh.ObsidianExecutor(0)
     dec = bench_decode(torch, oh, exe, args)
+    rtr = bench_router(torch, oh, exe)
     pre = None if args.no_prefill else bench_prefill(torch, oh, exe, args)
     dcd = None if args.no_decoder else bench_decoder(torch, oh, exe, args)
     cpu = None
     if not args.no_cpu:
-        threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(os.cpu_count() or 1, 16)
-        cpu = cpu_baseline(args.cpu_seconds, threads)
+        # every core this process may run on, capped by OMP_NUM_THREADS where it is set (the
+        # host's CPU share per GPU)
+        threads = len(os.sched_getaffinity(0))
+        if os.environ.get("OMP_NUM_THREADS", "").isdigit() and int(os.environ["OMP_NUM_THREADS"]) > 0:
+            threads = min(threads, int(os.environ["OMP_NUM_THREADS"]))
+        cpu = cpu_baseline(threads)
     exe.close()
 
     line = {
@@ -471,6 +562,8 @@ def main():
         "decode_frac_of_hbm_peak": round(dec["gbs"] / HBM_PEAK_GBS, 4),
         "decode_kernels": {n: round(v["avg_us"], 3) for n, v in dec["kernels"].items()},
         "roofline": dec["roofline"],
+        "router": dict(rtr, workload="8-bit gate [128 x 2048] + softmax/top-8 (f16 logits), 2 launches per call, "
+                                      "graph of 200 calls"),
         "prefill": None if pre is None else {
             "T": pre["T"], "ms": round(pre["ms"], 4), "tflops": round(pre["tflops"], 1),
             "gemm_us": round(pre["gemm_us"], 2),

@@ -623,6 +623,86 @@ int orc_moe_decode_baseline(const orc_layer* L, const uint16_t* x_bf16, int k, i
   return 0;
 }
 
+/* CPU baseline, router of T tokens (dequant_matvec_8bit.metal: one serial
+ * fp32 dot per logit, rounded to f16; moe_routing_topk.metal on those halves),
+ * OpenMP over tokens. */
+int orc_router_baseline(const orc_layer* L, const uint16_t* x_bf16, int64_t T, int k, int norm_topk,
+                        int nthreads, int32_t* ids, float* w) {
+#ifdef _OPENMP
+  if (nthreads > 0) omp_set_num_threads(nthreads);
+#else
+  (void)nthreads;
+#endif
+  const int H = L->hidden, E = L->n_exp, G = L->group;
+  if (H > 8192 || E > 256) return -1;
+  const int64_t words = H / 4, groups = H / G;
+#pragma omp parallel for schedule(static)
+  for (int64_t t = 0; t < T; ++t) {
+    float x[8192], lg[256];
+    orc_bf16_to_f32_n(x_bf16 + t * H, x, H);
+    for (int e = 0; e < E; ++e)
+      lg[e] = row_dot_shader(8, L->router_w + e * words, L->router_s + e * groups, L->router_b + e * groups,
+                             ORC_SB_BF16, x, H, G);
+    route_one(lg, E, k, norm_topk, ORC_SUM_SERIAL, ORC_ROUTE_REF, ids + t * k, w + t * k);
+  }
+  return 0;
+}
+
+/* CPU baseline, grouped prefill MoE (forward.rs:200-232 with
+ * matmul_dequant_4bit.metal: one serial fp32 dot per (row, output), the same
+ * order as the mat-vec), for T tokens with given routing: gate and up, SwiGLU,
+ * down, then the rank-order combine into y [T, H] (fp32). OpenMP over the
+ * (token, rank) rows. */
+int orc_moe_prefill_baseline(const orc_layer* L, const uint16_t* x_bf16, int64_t T, int k, const int32_t* ids,
+                             const float* w, int nthreads, float* y) {
+#ifdef _OPENMP
+  if (nthreads > 0) omp_set_num_threads(nthreads);
+#else
+  (void)nthreads;
+#endif
+  const int H = L->hidden, I = L->inter, E = L->n_exp, G = L->group;
+  if (H > 8192 || I > 4096) return -1;
+  const size_t gw = (size_t)I * H / 8, gs = (size_t)I * H / G, dw = (size_t)H * I / 8, ds = (size_t)H * I / G;
+  float* ye = (float*)malloc(sizeof(float) * (size_t)T * k * H);
+  if (!ye) return -2;
+#pragma omp parallel for schedule(dynamic, 4)
+  for (int64_t row = 0; row < T * k; ++row) {
+    float x[8192], g[4096], u[4096], h[4096];
+    const int e = ids[row];
+    float* out = ye + row * H;
+    if (e < 0 || e >= E) {
+      for (int o = 0; o < H; ++o) out[o] = 0.0f;
+      continue;
+    }
+    orc_bf16_to_f32_n(x_bf16 + (row / k) * H, x, H);
+    for (int i = 0; i < I; ++i) {
+      g[i] = row_dot_shader(4, L->gate_w + e * gw + (size_t)i * (H / 8), L->gate_s + e * gs + (size_t)i * (H / G),
+                            L->gate_b + e * gs + (size_t)i * (H / G), ORC_SB_BF16, x, H, G);
+      u[i] = row_dot_shader(4, L->up_w + e * gw + (size_t)i * (H / 8), L->up_s + e * gs + (size_t)i * (H / G),
+                            L->up_b + e * gs + (size_t)i * (H / G), ORC_SB_BF16, x, H, G);
+    }
+    orc_swiglu(g, u, h, I);
+    for (int o = 0; o < H; ++o)
+      out[o] = row_dot_shader(4, L->down_w + e * dw + (size_t)o * (I / 8), L->down_s + e * ds + (size_t)o * (I / G),
+                              L->down_b + e * ds + (size_t)o * (I / G), ORC_SB_BF16, h, I, G);
+  }
+  for (int64_t t = 0; t < T; ++t) {
+    float* yt = y + t * H;
+    for (int o = 0; o < H; ++o) yt[o] = 0.0f;
+    for (int r = 0; r < k; ++r) orc_scaled_add(yt, ye + (t * k + r) * H, w[t * k + r], H);
+  }
+  free(ye);
+  return 0;
+}
+
+void orc_set_threads(int n) {
+#ifdef _OPENMP
+  if (n > 0) omp_set_num_threads(n);
+#else
+  (void)n;
+#endif
+}
+
 int orc_omp_max_threads(void) {
 #ifdef _OPENMP
   return omp_get_max_threads();

@@ -184,7 +184,22 @@ int64_t orc_argmax(const float* x, int64_t n);
 int orc_moe_decode_baseline(const orc_layer* L, const uint16_t* x_bf16, int k, int norm_topk,
                             int nthreads, int32_t* ids, float* w, float* y);
 
+/* CPU baseline: the router of T tokens in the reference's shader semantics
+ * (serial fp32 dot per logit, f16 logits, serial softmax/top-k), OpenMP over
+ * tokens (nthreads <= 0: all). Returns 0. */
+int orc_router_baseline(const orc_layer* L, const uint16_t* x_bf16, int64_t T, int k, int norm_topk,
+                        int nthreads, int32_t* ids, float* w);
+
+/* CPU baseline: the grouped prefill MoE of T tokens with given routing in the
+ * shader semantics of matmul_dequant_4bit.metal (serial fp32 dot per (row,
+ * output)), rank-order combine into y [T, H] fp32; OpenMP over (token, rank)
+ * rows. Returns 0. */
+int orc_moe_prefill_baseline(const orc_layer* L, const uint16_t* x_bf16, int64_t T, int k, const int32_t* ids,
+                             const float* w, int nthreads, float* y);
+
 int orc_omp_max_threads(void);
+/* Threads of the OpenMP loops above (n <= 0: unchanged). */
+void orc_set_threads(int n);
 
 #ifdef __cplusplus
 }

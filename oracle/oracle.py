@@ -66,6 +66,8 @@ def lib() -> C.CDLL:
         L.orc_group_rows.argtypes = [vp, i64, i32, i32, vp, vp, vp, vp]
         L.orc_moe_prefill.argtypes = [C.POINTER(OrcLayer), vp, i64, i32, vp, vp, i32, vp]
         L.orc_moe_decode_baseline.argtypes = [C.POINTER(OrcLayer), vp, i32, i32, i32, vp, vp, vp]
+        L.orc_router_baseline.argtypes = [C.POINTER(OrcLayer), vp, i64, i32, i32, i32, vp, vp]
+        L.orc_moe_prefill_baseline.argtypes = [C.POINTER(OrcLayer), vp, i64, i32, vp, vp, i32, vp]
         L.orc_rmsnorm.argtypes = [vp, vp, C.c_float, i64, i64, vp]
         L.orc_rope_neox.argtypes = [vp, i64, i64, i64, C.c_float]
         L.orc_sdpa_decode.argtypes = [vp, vp, vp, i64, i64, i64, i64, i64, C.c_double, vp]
@@ -73,6 +75,7 @@ def lib() -> C.CDLL:
         L.orc_argmax.argtypes = [vp, i64]
         L.orc_f32_to_bf16_n.argtypes = [vp, vp, i64]
         L.orc_omp_max_threads.restype = C.c_int
+        L.orc_set_threads.argtypes = [C.c_int]
         _L = L
     return _L
 
@@ -241,8 +244,34 @@ def moe_decode_baseline(layer: Layer, x_bf16, k: int, norm_topk: bool = True, nt
     return ids, w, y
 
 
+def router_baseline(layer: Layer, x_bf16, k: int, norm_topk: bool = True, nthreads: int = 0):
+    """The router of T tokens in shader semantics (f16 logits), OpenMP over tokens."""
+    x = _c(x_bf16, np.uint16).reshape(-1, layer.hidden)
+    T = x.shape[0]
+    ids = np.empty((T, k), np.int32)
+    w = np.empty((T, k), np.float32)
+    _rc(lib().orc_router_baseline(C.byref(layer.s), _p(x), T, k, int(norm_topk), nthreads, _p(ids), _p(w)),
+        "router_baseline")
+    return ids, w
+
+
+def moe_prefill_baseline(layer: Layer, X_bf16, ids, w, nthreads: int = 0) -> np.ndarray:
+    """Grouped prefill in the shader semantics of matmul_dequant_4bit.metal -> y fp32 [T, H]."""
+    X = _c(X_bf16, np.uint16).reshape(-1, layer.hidden)
+    ids, w = _c(ids, np.int32), _c(w, np.float32)
+    T, k = ids.shape
+    y = np.empty((T, layer.hidden), np.float32)
+    _rc(lib().orc_moe_prefill_baseline(C.byref(layer.s), _p(X), T, k, _p(ids), _p(w), nthreads, _p(y)),
+        "prefill_baseline")
+    return y
+
+
 def omp_max_threads() -> int:
     return lib().orc_omp_max_threads()
+
+
+def set_threads(n: int) -> None:
+    lib().orc_set_threads(int(n))
 
 
 # ---- attention half and the whole decoder (forward.rs:398-443, :552-567) ----
@@ -372,3 +401,74 @@ def dequant_numpy(W: np.ndarray, S_f32: np.ndarray, B_f32: np.ndarray, group: in
     in_f = Wn.shape[1] * 8
     nib = np.stack([(Wn >> (4 * j)) & 0xF for j in range(8)], -1).reshape(out_f, in_f).astype(np.float32)
     return nib * np.repeat(S_f32, group, axis=1) + np.repeat(B_f32, group, axis=1)
+
+
+# ---- NumPy replica of the reference's CPU path (validate_dequant.py:24-30) --------
+# The reference checks its dequant with a NumPy shift/mask unpack (nibble j of a
+# uint32 word = (word >> 4j) & 0xF, value = nibble * scale + bias in fp32);
+# these functions run the MoE hot path on that replica with numpy's BLAS for the
+# products. They time the reference's CPU path; results agree with the oracle to
+# fp32 rounding (the routing softmax uses numpy's exp).
+def _bf16f(a) -> np.ndarray:
+    return (np.asarray(a, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def dequant8_numpy(W, S_f32, B_f32, group: int = 64) -> np.ndarray:
+    """8-bit MLX affine: byte c % 4 of word c // 4 (little-endian), value = byte * scale + bias."""
+    Wb = np.ascontiguousarray(W, np.uint32).view(np.uint8).astype(np.float32)
+    return Wb * np.repeat(S_f32, group, axis=1) + np.repeat(B_f32, group, axis=1)
+
+
+def _route_numpy(lg, k: int, norm_topk: bool):
+    """moe_routing_topk.metal on f16 logits: softmax, k largest p (lower id on ties), f16 weights."""
+    l16 = np.asarray(lg, np.float32).astype(np.float16).astype(np.float32)
+    e = np.exp(l16 - l16.max(axis=-1, keepdims=True))
+    p = (e / e.sum(axis=-1, keepdims=True)).astype(np.float32)
+    ids = np.argsort(-p, axis=-1, kind="stable")[..., :k]
+    sel = np.take_along_axis(p, ids, axis=-1)
+    w = sel.astype(np.float16).astype(np.float32)
+    if norm_topk:
+        ws = sel.sum(axis=-1, keepdims=True, dtype=np.float32)
+        w = np.where(ws > 0, (w / ws).astype(np.float16).astype(np.float32), w)
+    return ids.astype(np.int32), w
+
+
+def router_numpy(t: Dict[str, np.ndarray], X_bf16, k: int, norm_topk: bool = True):
+    """Router of T tokens: 8-bit dequant + X @ W^T, then the f16 routing rule."""
+    Wr = dequant8_numpy(t["router_w"], _bf16f(t["router_s"]), _bf16f(t["router_b"]))
+    return _route_numpy(_bf16f(X_bf16).reshape(-1, Wr.shape[1]) @ Wr.T, k, norm_topk)
+
+
+def _expert_mats(t, e):
+    g = dequant_numpy(t["gate_w"][e], _bf16f(t["gate_s"][e]), _bf16f(t["gate_b"][e]))
+    u = dequant_numpy(t["up_w"][e], _bf16f(t["up_s"][e]), _bf16f(t["up_b"][e]))
+    d = dequant_numpy(t["down_w"][e], _bf16f(t["down_s"][e]), _bf16f(t["down_b"][e]))
+    return g, u, d
+
+
+def decode_layer_numpy(t: Dict[str, np.ndarray], x_bf16, k: int, norm_topk: bool = True) -> np.ndarray:
+    """The decode MoE half for one token: router, then per chosen expert the
+    dequantized gate/up/down products and SwiGLU, weighted sum in rank order."""
+    x = _bf16f(x_bf16).reshape(-1)
+    ids, w = router_numpy(t, x_bf16, k, norm_topk)
+    y = np.zeros(x.shape[0], np.float32)
+    for e, we in zip(ids[0], w[0]):
+        g, u, d = _expert_mats(t, e)
+        gv, uv = g @ x, u @ x
+        y += we * (d @ (gv / (1.0 + np.exp(-gv)) * uv))
+    return y
+
+
+def prefill_numpy(t: Dict[str, np.ndarray], X_bf16, ids, w) -> np.ndarray:
+    """Grouped prefill with given routing: per expert, its tokens' rows through
+    the dequantized gate/up/down products, then the rank-order combine."""
+    X = _bf16f(X_bf16).reshape(ids.shape[0], -1)
+    T, k = ids.shape
+    Ye = np.zeros((T, k, X.shape[1]), np.float32)
+    for e in np.unique(ids):
+        rows = np.nonzero(ids == e)
+        g, u, d = _expert_mats(t, e)
+        Xe = X[rows[0]]
+        G, U = Xe @ g.T, Xe @ u.T
+        Ye[rows] = (G / (1.0 + np.exp(-G)) * U) @ d.T
+    return np.einsum("tk,tkh->th", w, Ye, optimize=False)

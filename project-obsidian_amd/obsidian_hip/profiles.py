@@ -1,0 +1,191 @@
+"""Summaries of rocprofv3 runs for the repository's profiles/ folder.
+
+    python -m obsidian_hip.profiles traffic --fetch F.csv --write W.csv \\
+        --copy-fetch CF.csv --copy-write CW.csv [--out DIR]
+    python -m obsidian_hip.profiles stats --stats S.csv [--line bench.json] [--out DIR]
+
+`traffic` turns two `rocprofv3 --pmc` runs of bench.py (FETCH_SIZE, then
+WRITE_SIZE, KiB per dispatch) into HBM bytes per launch, each counter scaled by
+what it reads for a plain device copy of known size (bench.py --calibrate-copy),
+and records for each kernel a digest of the sources it is built from, so a
+reader (bench.py) can tell whether the figure still describes the code.
+`stats` turns a `rocprofv3 --kernel-trace --stats` CSV into a Markdown table.
+"""
+from __future__ import annotations
+
+import argparse
+import collections
+import csv
+import hashlib
+import json
+import os
+import re
+import sys
+from typing import Dict, Optional, Tuple
+
+PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+# kernel -> (pattern of its rocprofv3 name, the sources it is compiled from)
+KERNELS = {
+    "decode_fused": (r"decode_fused_kernel<2>", ("csrc/obs_decode_fused.hip", "csrc/obs_internal.hpp")),
+    "grouped_gemm_gateup": (r"grouped_gemm_kernel<1u, 3u>", ("csrc/obs_prefill.hip", "csrc/obs_internal.hpp")),
+    "grouped_gemm_down": (r"grouped_gemm_kernel<2u, 5u>", ("csrc/obs_prefill.hip", "csrc/obs_internal.hpp")),
+    "moe_group_count": (r"group_count_kernel", ("csrc/obs_prefill.hip",)),
+    "moe_group_scan": (r"group_scan_kernel", ("csrc/obs_prefill.hip",)),
+    "moe_group_rank": (r"group_rank_kernel", ("csrc/obs_prefill.hip",)),
+    "moe_combine": (r"combine_kernel", ("csrc/obs_prefill.hip",)),
+}
+COPY = r"copyBuffer"
+
+# algorithmic bytes per launch at the bench's shapes (H 2048, I 768, 128 experts, top-8, T 2048)
+_PROJ = 768 * 2048 // 2 + 2 * 2 * (768 * 2048 // 64)
+ALGORITHMIC = {
+    "decode_fused": 8 * 3 * _PROJ + (128 * 2048 + 2 * 2 * (128 * 2048 // 64)) + 2 * 2 * 2048,
+    "grouped_gemm_gateup": 128 * 2 * _PROJ + 2048 * 2048 * 2 + 2048 * 8 * 768 * 2,
+    "grouped_gemm_down": 128 * _PROJ + 2048 * 8 * 768 * 2 + 2048 * 8 * 2048 * 2,
+}
+
+
+def source_digest(kernel: str) -> Optional[str]:
+    """sha256 (first 16 hex digits) over the sources `kernel` is built from."""
+    if kernel not in KERNELS:
+        return None
+    h = hashlib.sha256()
+    for rel in KERNELS[kernel][1]:
+        with open(os.path.join(PKG, rel), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()[:16]
+
+
+def _short(name: str) -> Optional[str]:
+    if re.search(COPY, name):
+        return "__copy"
+    for k, (pat, _) in KERNELS.items():
+        if re.search(re.escape(pat) if "<" in pat else pat, name):
+            return k
+    return None
+
+
+def pmc_per_dispatch(path: str, counter: str, first: int = 0) -> Dict[str, Tuple[float, int]]:
+    """(mean counter value per dispatch, dispatches) per known kernel; with
+    first > 0 only each kernel's first `first` dispatches count."""
+    per = collections.defaultdict(dict)
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            if r["Counter_Name"] != counter:
+                continue
+            k = _short(r["Kernel_Name"])
+            if k is None:
+                continue
+            d = per[k]
+            d[r["Dispatch_Id"]] = d.get(r["Dispatch_Id"], 0.0) + float(r["Counter_Value"])
+    out = {}
+    for k, d in per.items():
+        ids = sorted(d, key=int)
+        vals = [d[i] for i in ids]
+        if k == "__copy":  # the big copies only (a small readback copy runs too)
+            vals = [v for v in vals if v >= 0.5 * max(vals)]
+        elif first:
+            vals = vals[:first]
+        out[k] = (sum(vals) / len(vals), len(vals))
+    return out
+
+
+def traffic(fetch: str, write: str, copy_fetch: str, copy_write: str, copy_bytes: int, first: int = 0) -> Dict:
+    cf = pmc_per_dispatch(copy_fetch, "FETCH_SIZE")["__copy"][0]
+    cw = pmc_per_dispatch(copy_write, "WRITE_SIZE")["__copy"][0]
+    fs, ws = copy_bytes / 1024 / cf, copy_bytes / 1024 / cw
+    fe, wr = pmc_per_dispatch(fetch, "FETCH_SIZE", first), pmc_per_dispatch(write, "WRITE_SIZE", first)
+    res = {"_calibration": {"copy_bytes": copy_bytes, "fetch_kib_per_copy": cf, "write_kib_per_copy": cw,
+                            "fetch_scale": fs, "write_scale": ws}}
+    for k in KERNELS:
+        if k not in fe or k not in wr:
+            continue
+        f, n = fe[k]
+        w, _ = wr[k]
+        t = int(round(f * 1024 * fs + w * 1024 * ws))
+        e = {"dispatches": n, "fetch_kib_per_dispatch": round(f, 1), "write_kib_per_dispatch": round(w, 1),
+             "traffic_bytes_per_launch": t, "source_sha": source_digest(k)}
+        if k in ALGORITHMIC:
+            e["algorithmic_bytes_per_launch"] = ALGORITHMIC[k]
+            e["traffic_over_algorithmic"] = round(t / ALGORITHMIC[k], 3)
+        res[k] = e
+    return res
+
+
+def traffic_md(res: Dict, cmds) -> str:
+    c = res["_calibration"]
+    md = ["# HBM traffic per launch — rocprofv3 FETCH_SIZE / WRITE_SIZE", "",
+          "Workloads: decode MoE layer T=1 (top-8 of 128 experts, H=2048, I=768, 48-layer table) and grouped "
+          "prefill T=2048 (Zipf s=1.1 routing, seed 0), as run by `bench.py`.", "",
+          "Commands (each counter in its own run, from the repository root):", "", "```", *cmds, "```", "",
+          f"Calibration: a plain {c['copy_bytes'] >> 20} MiB device copy reads FETCH_SIZE = {c['fetch_kib_per_copy']:.0f} "
+          f"KiB and WRITE_SIZE = {c['write_kib_per_copy']:.0f} KiB per dispatch for {c['copy_bytes'] >> 10:,} KiB moved "
+          f"each way, so bytes = FETCH_SIZE x 1024 x {c['fetch_scale']:.4f} and WRITE_SIZE x 1024 x "
+          f"{c['write_scale']:.4f}.", "",
+          "| kernel | dispatches | FETCH_SIZE KiB | WRITE_SIZE KiB | traffic bytes / launch | algorithmic bytes / "
+          "launch | ratio | source digest |", "|---|---|---|---|---|---|---|---|"]
+    for k, e in res.items():
+        if k.startswith("_"):
+            continue
+        a = e.get("algorithmic_bytes_per_launch")
+        md.append(f"| {k} | {e['dispatches']} | {e['fetch_kib_per_dispatch']:,.1f} | {e['write_kib_per_dispatch']:,.1f} "
+                  f"| {e['traffic_bytes_per_launch']:,} | {'' if a is None else format(a, ',')} | "
+                  f"{e.get('traffic_over_algorithmic', '')} | `{e['source_sha']}` |")
+    md += ["", "Algorithmic bytes: decode = 8 experts x 2,654,208 + router 278,528 + 8,192 activations; gate/up GEMM = "
+           "128 experts x 2 x 884,736 (weights, scales, biases) + X 8 MiB + H 24 MiB written; down GEMM = 128 x 884,736 "
+           "+ H 24 MiB + Yp 64 MiB written. FETCH_SIZE counts L2-to-fabric reads, so Infinity Cache hits count too. "
+           "The source digest is `obsidian_hip.profiles.source_digest` of the kernel's sources at measurement time; "
+           "bench.py reports the traffic only while it matches."]
+    return "\n".join(md) + "\n"
+
+
+def stats_md(path: str, line: Optional[str], cmd: str) -> str:
+    with open(path) as f:
+        rows = list(csv.DictReader(f))
+    md = ["# Kernel durations — rocprofv3 --kernel-trace --stats", "", "Command (from the repository root):", "",
+          "```", cmd, "```", "", "| kernel | calls | average µs | min µs | max µs | % of traced time |",
+          "|---|---|---|---|---|---|"]
+    for r in rows:
+        nm = re.sub(r"\(.*", "", r["Name"].replace("(anonymous namespace)::", "").replace("void ", ""))[:60]
+        md.append(f"| `{nm}` | {r['Calls']} | {float(r['AverageNs']) / 1000:.2f} | {float(r['MinNs']) / 1000:.2f} | "
+                  f"{float(r['MaxNs']) / 1000:.2f} | {float(r['Percentage']):.2f} |")
+    if line:
+        md += ["", "bench.py's line from the same run:", "", "```json", line.strip(), "```"]
+    return "\n".join(md) + "\n"
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(prog="python -m obsidian_hip.profiles")
+    sub = ap.add_subparsers(dest="what", required=True)
+    t = sub.add_parser("traffic")
+    for a in ("fetch", "write", "copy-fetch", "copy-write"):
+        t.add_argument("--" + a, required=True)
+    t.add_argument("--copy-mib", type=int, default=1024)
+    t.add_argument("--first", type=int, default=0, help="count only each kernel's first N dispatches")
+    t.add_argument("--cmd", action="append", default=[], help="a command that made the CSVs (for the summary)")
+    t.add_argument("--out", default="profiles")
+    s = sub.add_parser("stats")
+    s.add_argument("--stats", required=True)
+    s.add_argument("--line", help="a file holding bench.py's JSON line from the same run")
+    s.add_argument("--cmd", required=True)
+    s.add_argument("--name", default="kernel_stats_bench.md")
+    s.add_argument("--out", default="profiles")
+    args = ap.parse_args(argv)
+    os.makedirs(args.out, exist_ok=True)
+    if args.what == "traffic":
+        res = traffic(args.fetch, args.write, args.copy_fetch, args.copy_write, args.copy_mib << 20, args.first)
+        with open(os.path.join(args.out, "hbm_traffic.json"), "w") as f:
+            json.dump(res, f, indent=1)
+        with open(os.path.join(args.out, "hbm_traffic.md"), "w") as f:
+            f.write(traffic_md(res, args.cmd))
+        print(json.dumps({k: v.get("traffic_over_algorithmic") for k, v in res.items() if not k.startswith("_")}))
+    else:
+        line = open(args.line).read().strip().splitlines()[-1] if args.line else None
+        with open(os.path.join(args.out, args.name), "w") as f:
+            f.write(stats_md(args.stats, line, args.cmd))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -661,3 +661,38 @@ def test_prefill_layer_major_equals_token_by_token():
         assert np.array_equal(k1[:, keep], k0[:, keep]) and np.array_equal(v1[:, keep], v0[:, keep])
         assert not np.array_equal(k1[:, pos0:pos0 + len(toks)], k0[:, pos0:pos0 + len(toks)])
     assert rows.shape == (len(toks), H)
+
+
+# ---------------------------------------------------------------- CPU baselines
+def test_router_baseline_is_the_shader_order_router():
+    """orc_router_baseline = the serial (shader-order) 8-bit dot per logit,
+    then the reference rule with the serial softmax sum."""
+    E, H = 64, 512
+    t = synth.moe_layer(40, E, H, 256, 64)
+    L = O.Layer(t, E, H, 256, 64)
+    x = synth.bf16_normal(np.random.default_rng(41), (16, H))
+    ids, w = O.router_baseline(L, x, 4, True, 2)
+    xf = synth.bf16_bits_to_f32(x)
+    lg = np.stack([O.qmatvec("shader", 8, t["router_w"], t["router_s"], t["router_b"], xf[i], H, E) for i in range(16)])
+    ri, rw = O.route_topk(lg, 4, True, O.SUM_SERIAL)
+    assert np.array_equal(ids, ri) and np.array_equal(w, rw)
+
+
+def test_prefill_baseline_and_numpy_replica_match_fp64():
+    """The C shader-semantics prefill and the NumPy replica both agree with the
+    fp64 oracle to fp32 rounding; the NumPy decode layer agrees with the C
+    decode baseline."""
+    E, H, I = 16, 512, 256
+    t = synth.moe_layer(42, E, H, I, 64)
+    L = O.Layer(t, E, H, I, 64)
+    rng = np.random.default_rng(43)
+    X = synth.bf16_normal(rng, (24, H))
+    ids, w = synth.zipf_routing(24, E, 4, 1.1, seed=1)
+    y64 = O.moe_prefill(L, X, ids, w, O.MODE_F64)
+    for y in (O.moe_prefill_baseline(L, X, ids, w, 2), O.prefill_numpy(t, X, ids, w)):
+        assert np.linalg.norm(y - y64) / np.linalg.norm(y64) < 1e-5
+    ib, wb, yb = O.moe_decode_baseline(L, X[0], 4, True, 2)
+    yn = O.decode_layer_numpy(t, X[0], 4)
+    assert np.linalg.norm(yn - yb) / np.linalg.norm(yb) < 1e-5
+    ni, nw = O.router_numpy(t, X, 4, True)
+    assert np.mean(np.all(ni == O.router_baseline(L, X, 4, True, 2)[0], axis=1)) >= 0.9
