@@ -266,6 +266,10 @@ def bench_decoder(torch, oh, exe, args):
     pos1, tok = model.read_state()  # checks the device status of the timed steps
     if pos1 - pos0 != args.dec_steps:
         raise RuntimeError(f"decoder: {pos1 - pos0} positions advanced in {args.dec_steps} steps")
+    import numpy as np
+    lg = model.logits.download()
+    if not bool(np.all(np.isfinite(lg))) or not 0 <= tok < model.cfg.vocab:
+        raise RuntimeError("decoder: the last timed step produced non-finite logits or an invalid token")
     ms_tok = ms / args.dec_steps
     seq_mid = (pos0 + pos1) / 2.0 + 1.0  # mean attended length of the timed steps
     nbytes = decoder_token_bytes(model.cfg, seq_mid)

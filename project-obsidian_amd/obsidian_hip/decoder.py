@@ -13,12 +13,13 @@ Every kernel runs through libobsidian_hip; there is no CPU path.
 """
 from __future__ import annotations
 
+import os
 from dataclasses import dataclass
 from typing import Dict, List, Optional
 
 import numpy as np
 
-from . import DeviceBuffer, MoeConfig, MoeLayer, ObsidianExecutor, _ptr, lib
+from . import DeviceBuffer, MoeConfig, MoeLayer, ObsError, ObsidianExecutor, _ptr, lib
 
 
 @dataclass
@@ -90,6 +91,7 @@ class Model:
         self.last_seq: List[int] = []        # the tokens whose keys and values the caches hold (run_turn)
         self.last_reused = 0
         self.last_prefilled = 0
+        self.last_fallback: Optional[str] = None  # why the last turn's batched prefill fell back, if it did
 
     # -- the pieces of forward_layer (forward.rs:398-443) ------------------
     def fused_attention(self) -> bool:
@@ -319,9 +321,17 @@ class Model:
             lcp += 1
         lcp = min(lcp, len(prompt) - 1)
         suffix = prompt[lcp:]
-        if len(suffix) >= batch_min:
-            nxt = self.prefill(suffix, lcp)
-        else:
+        # batched from batch_min tokens unless OBSIDIAN_NO_BATCH is set; a failed
+        # batched prefill falls back to per-token steps (forward.rs:494-507),
+        # which write the same cache positions again
+        self.last_fallback = None
+        nxt = None
+        if len(suffix) >= batch_min and "OBSIDIAN_NO_BATCH" not in os.environ:
+            try:
+                nxt = self.prefill(suffix, lcp)
+            except ObsError as e:
+                self.last_fallback = str(e)
+        if nxt is None:
             for i, tk in enumerate(suffix[:-1]):
                 self.fill_kv(tk, lcp + i)
             nxt = self.run_one_token(suffix[-1], len(prompt) - 1)

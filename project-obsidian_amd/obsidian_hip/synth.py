@@ -195,13 +195,26 @@ def norm_weight(rng: np.random.Generator, n: int) -> np.ndarray:
 def decoder_weights(seed: int, n_layers: int, hidden: int, n_heads: int, n_kv: int, head_dim: int, n_exp: int,
                     inter: int, vocab: int, group: int = 64):
     """Seeded random weights of a Qwen3-MoE decoder (host arrays): per layer the
-    attention tensors (centred 4-bit q/k/v/o, norm weights) and the MoE tables
-    of moe_layer(); globally the embedding, final norm and lm_head."""
+    attention tensors (centred 4-bit q/k/v/o, norm weights), the router of
+    moe_layer() and centred expert tables; globally the embedding, final norm
+    and lm_head.
+
+    The experts are centred too: moe_layer()'s all-positive tables give every
+    expert output one common direction, which the residual stream accumulates
+    until the SwiGLU intermediates leave the f16 range the kernels carry them
+    in (|h| > 65504 within six tokens of two layers), where a trained model's
+    stay small."""
     rng = np.random.default_rng(seed)
     layers = []
     qd, kvd = n_heads * head_dim, n_kv * head_dim
     for il in range(n_layers):
         t = moe_layer(seed * 1000 + il, n_exp, hidden, inter, group)
+        for proj, (r, c), sd in (("gate", (inter, hidden), 0.02), ("up", (inter, hidden), 0.02),
+                                 ("down", (hidden, inter), 0.01)):
+            w, s, b = centered_quant(rng, n_exp * r, c, group, sd)
+            t[f"{proj}_w"] = w.reshape(n_exp, r, c // 8)
+            t[f"{proj}_s"] = s.reshape(n_exp, r, c // group)
+            t[f"{proj}_b"] = b.reshape(n_exp, r, c // group)
         for name, (r, c) in (("q", (qd, hidden)), ("k", (kvd, hidden)), ("v", (kvd, hidden)), ("o", (hidden, qd))):
             t[name + "_w"], t[name + "_s"], t[name + "_b"] = centered_quant(rng, r, c, group)
         t["in_norm"] = norm_weight(rng, hidden)

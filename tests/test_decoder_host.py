@@ -5,6 +5,7 @@ token is fed at, and eos. The device calls are replaced by a recorder whose
 'next token' is a fixed function of (token, position)."""
 import pytest
 
+import obsidian_hip as oh
 from obsidian_hip import decoder as D
 
 V = 1000
@@ -18,12 +19,17 @@ class Rec(D.Model):
     def __init__(self, max_len):  # no device: only the host fields run_turn uses
         self.cfg = D.DecoderConfig(max_len=max_len)
         self.last_seq, self.last_reused, self.last_prefilled = [], 0, 0
+        self.fail_prefill = False
         self.fed = {}      # position -> token whose keys/values it holds
         self.calls = []
         self._state = (0, 0)
 
     def prefill(self, tokens, pos0):
         self.calls.append(("prefill", pos0, len(tokens)))
+        if self.fail_prefill:  # as a failing library call would, after writing part of the caches
+            for i, t in enumerate(tokens[: len(tokens) // 2]):
+                self.fed[pos0 + i] = -1
+            raise oh.ObsError(oh.OBS_E_NOMEM, "obs_moe_prefill: workspace too small")
         for i, t in enumerate(tokens):
             self.fed[pos0 + i] = t
         self._state = (pos0 + len(tokens), nxt(tokens[-1], pos0 + len(tokens) - 1))
@@ -115,3 +121,21 @@ def test_overflowing_prompt_keeps_its_tail():
     assert max(m.fed) < 64
     with pytest.raises(ValueError, match="no room"):
         Rec(8).run_turn([1, 2], 8, eos=-1)
+
+
+def test_failed_batched_prefill_falls_back_to_token_steps(monkeypatch):
+    """forward.rs:497-507: a batched prefill that fails is redone token by
+    token from the reused prefix (the same positions, rewritten), and the
+    turn's tokens are those of the per-token path."""
+    m = Rec(4096)
+    m.fail_prefill = True
+    p = list(range(200, 240))
+    g = m.run_turn(p, 3, eos=-1)
+    assert g == expected(p, 3, -1) and "workspace" in m.last_fallback
+    assert m.calls[0] == ("prefill", 0, 40) and m.calls[1:40] == [("fill", i) for i in range(39)]
+    assert m.calls[40] == ("one", 39)
+    assert all(m.fed[i] == t for i, t in enumerate(m.last_seq))
+    m2 = Rec(4096)
+    monkeypatch.setenv("OBSIDIAN_NO_BATCH", "1")  # the reference's switch: per-token only
+    assert m2.run_turn(p, 2, eos=-1) == expected(p, 2, -1) and m2.calls[0] == ("fill", 0)
+    assert m2.last_fallback is None

@@ -99,26 +99,39 @@ def test_sdpa_prefill_rejects_bad_shapes(exe):
         exe.attn_prep_rows(x, x, x, x, x, x, x, 32, 4, 128, 64, EPS, THETA, 64, 1)
 
 
-CFG = D.DecoderConfig(n_layers=2, hidden=2048, n_heads=16, n_kv=2, head_dim=128, n_exp=8, top_k=2, inter=256,
-                      vocab=512, max_len=64)
-OCFG = {"hidden": CFG.hidden, "n_heads": CFG.n_heads, "n_kv": CFG.n_kv, "head_dim": CFG.head_dim,
-        "eps": CFG.rms_eps, "theta": CFG.rope_theta, "top_k": CFG.top_k, "norm_topk": CFG.norm_topk,
-        "vocab": CFG.vocab}
+# "split": 16 query heads, 8 experts, top-2 (the separate attention launches
+# and the 4-launch MoE path in the decode steps); "q30": the Qwen3-30B-A3B
+# attention and expert shapes (32 / 4 heads, inter 768, top-8) with 16
+# experts, whose decode steps run the one-launch attention and MoE kernels.
+CFGS = {
+    "split": D.DecoderConfig(n_layers=2, hidden=2048, n_heads=16, n_kv=2, head_dim=128, n_exp=8, top_k=2, inter=256,
+                             vocab=512, max_len=64),
+    "q30": D.DecoderConfig(n_layers=2, hidden=2048, n_heads=32, n_kv=4, head_dim=128, n_exp=16, top_k=8, inter=768,
+                           vocab=512, max_len=64),
+}
 
 
-@pytest.fixture(scope="module")
-def small(exe):
+def _ocfg(c):
+    return {"hidden": c.hidden, "n_heads": c.n_heads, "n_kv": c.n_kv, "head_dim": c.head_dim, "eps": c.rms_eps,
+            "theta": c.rope_theta, "top_k": c.top_k, "norm_topk": c.norm_topk, "vocab": c.vocab}
+
+
+@pytest.fixture(scope="module", params=sorted(CFGS))
+def small(exe, request):
+    CFG = CFGS[request.param]
     layers, glob = synth.decoder_weights(5, CFG.n_layers, CFG.hidden, CFG.n_heads, CFG.n_kv, CFG.head_dim,
                                          CFG.n_exp, CFG.inter, CFG.vocab)
     dl, dg = D.upload_weights(exe, layers, glob)
     olayers = [(t, O.Layer(t, CFG.n_exp, CFG.hidden, CFG.inter)) for t in layers]
-    return dl, dg, layers, glob, olayers
+    return dl, dg, layers, glob, olayers, CFG
 
 
 def _model_with_caches(exe, small, host_caches):
-    dl, dg = small[0], small[1]
+    dl, dg, CFG = small[0], small[1], small[5]
     caches = [(exe.upload(k), exe.upload(np.ascontiguousarray(v.transpose(0, 2, 1)))) for k, v in host_caches]
-    return D.Model(exe, CFG, dl, dg, caches)
+    m = D.Model(exe, CFG, dl, dg, caches)
+    assert m.fused_attention() == (CFG.n_heads == 32)
+    return m
 
 
 def _close(got, want, tol, floor_mult=1.0, elem_tol=None):
@@ -141,6 +154,8 @@ def test_prefill_vs_oracle(exe, small, pos0, toks):
     cache entries, its row after attention and after the MoE block within 1e-2
     of the fp64 oracle; then the last token's logits from the GPU's last row,
     and the greedy token."""
+    CFG = small[5]
+    OCFG = _ocfg(CFG)
     rng = np.random.default_rng(1400 + pos0 + len(toks))
     host = [(synth.bf16_normal(rng, (CFG.n_kv, CFG.max_len, CFG.head_dim)),
              synth.bf16_normal(rng, (CFG.n_kv, CFG.max_len, CFG.head_dim))) for _ in range(CFG.n_layers)]
@@ -199,6 +214,7 @@ def test_prefill_then_decode_matches_token_steps(exe, small):
     entries (exact inputs on both paths) agree within 1e-2, and the next
     token agrees unless the logits' top two are within the paths' tolerance
     (later layers can route a token to another expert on a near tie)."""
+    CFG = small[5]
     toks = [9, 300, 4, 4, 77, 123, 5, 6, 200, 11, 12]
     zero = [(np.zeros((CFG.n_kv, CFG.max_len, CFG.head_dim), np.uint16),) * 2 for _ in range(CFG.n_layers)]
     a, b = _model_with_caches(exe, small, zero), _model_with_caches(exe, small, zero)
@@ -219,6 +235,7 @@ def test_prefill_then_decode_matches_token_steps(exe, small):
 
 
 def test_run_turn_reuses_the_cached_prefix(exe, small):
+    CFG = small[5]
     zero = [(np.zeros((CFG.n_kv, CFG.max_len, CFG.head_dim), np.uint16),) * 2 for _ in range(CFG.n_layers)]
     m = _model_with_caches(exe, small, zero)
     fresh = _model_with_caches(exe, small, zero)
