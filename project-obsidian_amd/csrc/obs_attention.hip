@@ -794,24 +794,27 @@ uint32_t sdpa_splits(uint32_t max_len) {
 namespace obs {
 
 int ensure_rope_table(obs_ctx* ctx, float theta, uint32_t max_len, const float** out) {
-  if (!ctx->rope_table || ctx->rope_theta != theta || ctx->rope_len < max_len) {
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    OBS_HIP_TRY(ctx, hipStreamIsCapturing(ctx->stream, &cs));
-    if (cs != hipStreamCaptureStatusNone)
-      return set_error(ctx, OBS_E_INVALID, "RoPE table: run once before capturing (table for theta %g, %u positions)",
-                       static_cast<double>(theta), max_len);
-    OBS_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
-    if (ctx->rope_table) OBS_HIP_TRY(ctx, hipFree(ctx->rope_table));
-    ctx->rope_table = nullptr;
-    ctx->rope_len = 0;
-    OBS_HIP_TRY(ctx, hipMalloc(&ctx->rope_table, sizeof(float) * 128u * max_len));
-    rope_table_kernel<<<(max_len * 64u + 255u) / 256u, 256, 0, ctx->stream>>>(ctx->rope_table, max_len, theta);
-    OBS_HIP_TRY(ctx, hipGetLastError());
-    OBS_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
-    ctx->rope_len = max_len;
-    ctx->rope_theta = theta;
+  for (const auto& r : ctx->rope_tables)
+    if (r.theta == theta && r.len >= max_len) {
+      *out = r.table;
+      return OBS_OK;
+    }
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  OBS_HIP_TRY(ctx, hipStreamIsCapturing(ctx->stream, &cs));
+  if (cs != hipStreamCaptureStatusNone)
+    return set_error(ctx, OBS_E_INVALID, "RoPE table: run once before capturing (table for theta %g, %u positions)",
+                     static_cast<double>(theta), max_len);
+  float* t = nullptr;
+  OBS_HIP_TRY(ctx, hipMalloc(&t, sizeof(float) * 128u * max_len));
+  rope_table_kernel<<<(max_len * 64u + 255u) / 256u, 256, 0, ctx->stream>>>(t, max_len, theta);
+  hipError_t e = hipGetLastError();
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) {
+    (void)hipFree(t);
+    return set_error(ctx, OBS_E_HIP, "RoPE table: %s", hipGetErrorString(e));
   }
-  *out = ctx->rope_table;
+  ctx->rope_tables.push_back({t, max_len, theta});
+  *out = t;
   return OBS_OK;
 }
 

@@ -87,9 +87,12 @@ int prof_end(obs_ctx* ctx) {
 
 int ensure_decode_ws(obs_ctx* ctx, size_t bytes, void** out) {
   if (ctx->decode_ws_bytes < bytes) {
-    if (ctx->decode_ws) {
-      OBS_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
-      OBS_HIP_TRY(ctx, hipFree(ctx->decode_ws));
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    OBS_HIP_TRY(ctx, hipStreamIsCapturing(ctx->stream, &cs));
+    if (cs != hipStreamCaptureStatusNone)
+      return set_error(ctx, OBS_E_INVALID, "decode workspace: run this shape once before capturing (%zu bytes)", bytes);
+    if (ctx->decode_ws) {  // kept: graphs captured with it may still run
+      ctx->retired.push_back(ctx->decode_ws);
       ctx->decode_ws = nullptr;
       ctx->decode_ws_bytes = 0;
     }
@@ -158,7 +161,8 @@ void obs_destroy(obs_ctx* ctx) {
   if (ctx->decode_ws) (void)hipFree(ctx->decode_ws);
   if (ctx->fused_ws) (void)hipFree(ctx->fused_ws);
   if (ctx->attn_ws) (void)hipFree(ctx->attn_ws);
-  if (ctx->rope_table) (void)hipFree(ctx->rope_table);
+  for (const auto& r : ctx->rope_tables) (void)hipFree(r.table);
+  for (void* p : ctx->retired) (void)hipFree(p);
   if (ctx->ev_start) (void)hipEventDestroy(ctx->ev_start);
   if (ctx->ev_stop) (void)hipEventDestroy(ctx->ev_stop);
   if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);

@@ -42,10 +42,17 @@ struct obs_ctx {
   // once per device by obs_create; null if the lookup was not possible
   void* scratch = nullptr;
   bool scratch_used = false;  // obs_device_status then checks its error flag too
-  // RoPE (cos, sin) table [rope_len][64][2] fp32 for rope_theta
-  float* rope_table = nullptr;
-  uint32_t rope_len = 0;
-  float rope_theta = 0.0f;
+  // RoPE (cos, sin) tables [len][64][2] fp32, one per (theta, length) built;
+  // a graph captured with one keeps reading it, so none is freed before
+  // obs_destroy (a call uses the first table of its theta that is long enough)
+  struct rope_entry {
+    float* table;
+    uint32_t len;
+    float theta;
+  };
+  std::vector<rope_entry> rope_tables;
+  // decode workspaces replaced by larger ones, kept for the same reason
+  std::vector<void*> retired;
   int decode_path = 0;  // OBS_DECODE_AUTO / _MULTI / _FUSED
   // in-stream kernel timing
   bool prof_on = false;

@@ -112,6 +112,26 @@ def test_graph_replay_equals_eager_steps(exe, model):
     print("tokens", eager)
 
 
+def test_graph_survives_another_models_rope_table(exe, model):
+    """A second model on the same executor with another RoPE theta (and a
+    longer cache) builds its own table; the first model's captured graph keeps
+    its table and still replays equal to eager steps."""
+    import dataclasses
+    m = model[0]
+    m.close()
+    eager = m.generate(7, 10, 6, graph=False)
+    logits_eager = m.logits.download()
+    assert m.generate(7, 10, 6, graph=True) == eager
+    for theta, max_len in ((5e5, m.cfg.max_len), (1e6, 2 * m.cfg.max_len)):
+        m2 = D.Model(exe, dataclasses.replace(m.cfg, rope_theta=theta, max_len=max_len), m.layers, m.glob)
+        m2.generate(7, 10, 6, graph=False)
+        assert not np.array_equal(m2.logits.download(), logits_eager)  # theta reaches the result
+        m2.close()
+        assert m.generate(7, 10, 6, graph=True) == eager
+        assert np.array_equal(m.logits.download(), logits_eager)
+    m.close()
+
+
 def test_generation_stays_in_the_cache(exe, model):
     m = model[0]
     CFG = m.cfg
