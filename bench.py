@@ -183,10 +183,12 @@ def bench_router(torch, oh, exe, reps=200):
 
 def gpu_decoder(torch, oh, D, exe, n_layers, max_len, seed):
     """A Qwen3-30B-A3B-shaped decoder with seeded random
-    weights generated on the GPU: centred 4-bit attention matrices, norm
-    weights around 1, the MoE tables of gpu_table, a 4-bit embedding and
-    lm_head; KV caches filled with random bf16 (the positions before the timed
-    ones stand for an earlier context)."""
+    weights generated on the GPU: centred 4-bit attention and expert matrices
+    (uncentred experts all push the residual stream one way until the SwiGLU
+    intermediates leave the f16 range within a few tokens), norm weights
+    around 1, an 8-bit router, a 4-bit embedding and lm_head; KV caches filled
+    with random bf16 (the positions before the timed ones stand for an earlier
+    context)."""
     c = D.DecoderConfig(n_layers=n_layers, max_len=max_len)
     gen = torch.Generator(device="cuda")
     gen.manual_seed(seed)
@@ -202,7 +204,18 @@ def gpu_decoder(torch, oh, D, exe, n_layers, max_len, seed):
     def norm(n):
         return (1.0 + 0.1 * torch.randn(n, device="cuda", generator=gen)).to(torch.bfloat16)
 
-    moe = gpu_table(torch, n_layers, seed + 1)
+    def moe_table():
+        t = {}
+        for p, (r, cols), std in (("gate", (I, H), 0.02), ("up", (I, H), 0.02), ("down", (H, I), 0.01)):
+            w, sc, b = quant(E * r, cols, std)
+            t[p + "_w"], t[p + "_s"], t[p + "_b"] = (w.view(E, r, cols // 8), sc.view(E, r, cols // G),
+                                                     b.view(E, r, cols // G))
+        t["router_w"] = torch.randint(-2**31, 2**31, (E, H // 4), dtype=torch.int32, device="cuda", generator=gen)
+        t["router_s"] = (torch.randn((E, H // G), device="cuda", generator=gen) * 0.02).abs().to(torch.bfloat16)
+        t["router_b"] = (torch.randn((E, H // G), device="cuda", generator=gen) * 0.01).to(torch.bfloat16)
+        return t
+
+    moe = [moe_table() for _ in range(n_layers)]
     keep, layers, caches = [], [], []
     qd, kvd = c.n_heads * c.head_dim, c.n_kv * c.head_dim
     for il in range(n_layers):
