@@ -8,21 +8,33 @@
 // less, and a launch boundary with its fences and first memory round trip
 // cost about as much as their work. Here 256 workgroups (one per CU) pass the
 // few values that cross workgroups through epoch-tagged slots (see
-// slot_store), as decode_fused_kernel does for the MoE half:
-//   1. every wave computes 5 of the 5,120 q/k/v rows (RMSNorm of x fused) and
-//      publishes them;
-//   2. workgroup b < 128 is (kv head b % 4, split b / 4 of 32): it polls
-//      the 8 query heads and the key/value head of its kv head, applies the
-//      per-head RMSNorm and NeoX RoPE, appends the key and value at pos to the
-//      caches (the workgroup whose split holds pos) and runs the split's
-//      attention with the decode kernel's MFMA block math (its own key/value
-//      at pos spliced in from registers); the 4 waves' partials are merged in
-//      LDS and published (32 splits, not 64: the same one block per wave at a
-//      4,096-token context, and half the partials to exchange);
-//   3. workgroup j combines the 32 splits of head j / 8 for 16 of its dims and
-//      publishes them as bf16 pairs;
-//   4. every workgroup polls the 4,096 attention outputs into LDS and each
-//      wave computes 2 rows of x1 = x + W_o attn.
+// slot_store), as decode_fused_kernel does for the MoE half.
+//
+// Work split. Workgroup b belongs to group g = b % 8, which the dispatcher
+// places on one XCD (consecutive workgroups go round-robin over the 8 XCDs),
+// and has index j = b / 8 in it. Group g serves kv head g / 2 and its query
+// heads 8 (g / 2) + 4 (g % 2) .. + 3, over the whole sequence, so every
+// exchange but the last stays inside the group and its L2:
+//   1. each of the group's 128 waves computes 6 of its 768 q/k/v rows (4 query
+//      heads, the key and the value head; RMSNorm of x fused) and publishes
+//      them to the group's slots (both groups of a kv head compute its key and
+//      value rows, bit-identically);
+//   2. workgroup j takes split j of 32 of the sequence: it polls the group's
+//      rows, applies the per-head RMSNorm and NeoX RoPE, appends the key and
+//      value at pos to the caches (the even group's split holding pos) and runs
+//      the split's attention with the decode kernel's MFMA block math (its own
+//      key/value at pos spliced in from registers); the 4 waves' partials are
+//      merged in LDS and published;
+//   3. workgroup j combines query head j / 8 of the group, 16 dims, over the
+//      32 splits and publishes them as bf16 pairs;
+//   4. every workgroup polls the group's 512 attention outputs into LDS and
+//      computes, for its 64 rows of W_o, the partial product over the group's
+//      512 columns, published across XCDs;
+//   5. group 0 sums the 8 groups' partials per row with the residual:
+//      x1 = x + sum_g partial_g, in group order, rounded once to bf16.
+// (The earlier split of the same work over the whole grid exchanged q/k/v,
+// the split partials and the attention outputs across XCDs, three round trips
+// through memory that cost 1.5-3.3 us each.)
 // Every weight, activation and cache load that does not depend on an exchange
 // is issued before the first exchange: the q/k/v rows at the start, the first
 // key/value block and the o rows right after the q/k/v publish, so the
@@ -47,22 +59,25 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
 constexpr uint32_t AH = 2048, ANH = 32, ANKV = 4, AHD = 128, AG = ANH / ANKV;  // G = 8
-constexpr uint32_t AQD = ANH * AHD, AKVD = ANKV * AHD, AQKV = AQD + 2 * AKVD;  // 4096, 512, 5120
-constexpr uint32_t ANWG = 256, ANWAVE = ANWG * 4;
-constexpr uint32_t A_RPW = AQKV / ANWAVE;       // q/k/v rows per wave: 5
-constexpr uint32_t A_ORPW = AH / ANWAVE;        // o rows per wave: 2
-constexpr uint32_t A_NSPLIT = 32;               // splits per kv head (workgroups 0..127 attend)
-constexpr uint32_t A_NATT = A_NSPLIT * ANKV;    // attending workgroups: 128
-constexpr uint32_t A_CDIM = AQD / ANWG;         // combined outputs per workgroup: 16
-constexpr uint32_t A_NEED = AG * AHD + 2 * AHD; // slots a split polls: its 8 query heads, k, v
-constexpr uint32_t A_PART = AG * (AHD + 2);     // a split's partial: 8 heads x (O[128], m, l)
-static_assert(A_RPW * ANWAVE == AQKV && A_ORPW * ANWAVE == AH && A_CDIM * ANWG == AQD, "shape");
+constexpr uint32_t AQD = ANH * AHD, AKVD = ANKV * AHD;                          // 4096, 512
+constexpr uint32_t ANGRP = 8, AWPG = 32, ANWG = ANGRP * AWPG;                   // groups, WGs per group
+constexpr uint32_t AQPG = ANH / ANGRP;           // query heads per group: 4
+constexpr uint32_t AGQD = AQPG * AHD;            // the group's attention outputs: 512
+constexpr uint32_t AGR = AGQD + 2 * AHD;         // q/k/v rows per group: 768
+constexpr uint32_t A_RPW = AGR / (AWPG * 4);     // q/k/v rows per wave: 6
+constexpr uint32_t A_NSPLIT = AWPG;              // splits of the sequence per group: 32
+constexpr uint32_t A_CDIM = AGQD / AWPG;         // combined outputs per workgroup: 16
+constexpr uint32_t A_PART = AQPG * (AHD + 2);    // a split's partial: 4 heads x (O[128], m, l)
+constexpr uint32_t A_ORWG = AH / AWPG;           // W_o rows per workgroup: 64
+constexpr uint32_t A_ORW = A_ORWG / 4;           // per wave: 16, in two passes of 8 (8 lanes per row)
+static_assert(A_RPW * AWPG * 4 == AGR && A_CDIM * AWPG == AGQD && AQPG * ANGRP == ANH, "shape");
 
 constexpr size_t AW_COUNT = 0, AW_ERR = 256;
-constexpr size_t AW_QKV = 1024;                                // [5120] slots
-constexpr size_t AW_PART = AW_QKV + size_t(AQKV) * 8;           // [128][1040] slots
-constexpr size_t AW_ATTN = AW_PART + size_t(A_NATT) * A_PART * 8; // [2048] slots: bf16 pairs
-constexpr size_t AW_BYTES = AW_ATTN + size_t(AQD / 2) * 8;
+constexpr size_t AW_QKV = 1024;                                              // [8][768] slots
+constexpr size_t AW_PART = AW_QKV + size_t(ANGRP) * AGR * 8;                 // [8][32][520] slots
+constexpr size_t AW_ATTN = AW_PART + size_t(ANGRP) * A_NSPLIT * A_PART * 8;  // [8][256] slots: bf16 pairs
+constexpr size_t AW_Y = AW_ATTN + size_t(ANGRP) * (AGQD / 2) * 8;            // [8][2048] slots
+constexpr size_t AW_BYTES = AW_Y + size_t(ANGRP) * AH * 8;
 constexpr uint64_t A_WAIT_TICKS = 10000000ull;  // 100 ms at 100 MHz
 
 struct AttnArgs {
@@ -83,26 +98,48 @@ struct AttnArgs {
 __device__ __forceinline__ float shfl_f(float v, int src) { return __shfl(v, src, 64); }
 __device__ __forceinline__ float shfl_xor_f(float v, int m) { return __shfl_xor(v, m, 64); }
 
+// Poll n_u slots per thread (slot tid + 256 u of src) until all carry the
+// epoch or the wait times out; values in vals. Returns false on a time-out.
+template <int NU>
+__device__ __forceinline__ bool poll_slots(const uint64_t* src, uint32_t epoch, float (&vals)[NU]) {
+  const uint64_t t0 = wall_clock64();
+  while (true) {
+    bool ready = true;
+#pragma unroll
+    for (int u = 0; u < NU; ++u) {
+      const uint64_t v = slot_load(src + threadIdx.x + 256u * u);
+      vals[u] = slot_val(v);
+      ready = ready && slot_ready(v, epoch);
+    }
+    if (__all(ready)) return true;
+    if (wall_clock64() - t0 > A_WAIT_TICKS) return false;
+  }
+}
+
 __global__ void __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 1)))
 attn_fused_kernel(AttnArgs a) {
   __shared__ uint32_t s_epoch;
   __shared__ int s_abort, s_fail;
-  __shared__ float s_qkv[A_NEED];                                    // the split's q (8 heads), k, v
-  __shared__ __attribute__((aligned(16))) uint16_t s_rot[AG + 2][AHD];  // rotated q heads, k, then v (bf16)
+  __shared__ float s_qkv[AGR];                                          // the group's q (4 heads), k, v
+  __shared__ __attribute__((aligned(16))) uint16_t s_rot[AQPG + 2][AHD];  // rotated q heads, k, then v (bf16)
   __shared__ float s_pm[4][16], s_pl[4][16];
-  __shared__ float s_po[4][AG][AHD];
+  __shared__ float s_po[4][AQPG][AHD];
   __shared__ float s_cm[A_NSPLIT], s_cl[A_NSPLIT], s_co[A_NSPLIT][A_CDIM];
   __shared__ float s_rl[16][A_CDIM], s_ra[16][A_CDIM];
-  __shared__ __attribute__((aligned(16))) f16x2_t s_ap[AQD / 2];    // attention output as f16 pairs
-  __shared__ float s_asum[AQD / 32], s_aoff[AQD / 32];
+  __shared__ __attribute__((aligned(16))) f16x2_t s_ap[AGQD / 2];   // the group's attention output, f16 pairs
+  __shared__ float s_asum[AGQD / 32], s_aoff[AGQD / 32];
+  __shared__ float s_y[ANGRP][A_ORWG];
 
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-  const uint32_t wave_g = __builtin_amdgcn_readfirstlane(blockIdx.x * 4u + wave);
+  const uint32_t g = blockIdx.x % ANGRP, j = blockIdx.x / ANGRP;
+  const uint32_t kv = g / 2u, hq0 = AG * kv + AQPG * (g % 2u);  // kv head, first query head
+  const uint32_t wl = __builtin_amdgcn_readfirstlane(4u * j + wave);  // wave within the group
   uint64_t* ctl_count = reinterpret_cast<uint64_t*>(a.ws + AW_COUNT);
   uint32_t* ctl_err = reinterpret_cast<uint32_t*>(a.ws + AW_ERR);
-  uint64_t* qkv_slots = reinterpret_cast<uint64_t*>(a.ws + AW_QKV);
-  uint64_t* part_slots = reinterpret_cast<uint64_t*>(a.ws + AW_PART);
-  uint64_t* attn_slots = reinterpret_cast<uint64_t*>(a.ws + AW_ATTN);
+  uint64_t* qkv_slots = reinterpret_cast<uint64_t*>(a.ws + AW_QKV) + size_t(g) * AGR;
+  uint64_t* part_slots = reinterpret_cast<uint64_t*>(a.ws + AW_PART) + size_t(g) * A_NSPLIT * A_PART;
+  uint64_t* attn_slots = reinterpret_cast<uint64_t*>(a.ws + AW_ATTN) + size_t(g) * (AGQD / 2);
+  uint64_t* y_slots = reinterpret_cast<uint64_t*>(a.ws + AW_Y);
 
   OBS_ATTN_MARK(0);
   // ---- 0. loads that the q/k/v rows and the RoPE need, in the order they are
@@ -128,13 +165,14 @@ attn_fused_kernel(AttnArgs a) {
     xq[i] = reinterpret_cast<const uint4*>(a.x + 32u * lane)[i];
     nq[i] = reinterpret_cast<const uint4*>(a.in_norm + 32u * lane)[i];
   }
+  // the wave's rows r = 6 wl + k of the group's [q heads | key head | value head]
   uint4 rq[A_RPW];
   uint16_t rsc[A_RPW], rbi[A_RPW];
 #pragma unroll
   for (uint32_t k = 0; k < A_RPW; ++k) {
-    const uint32_t r = A_RPW * wave_g + k;  // wave-uniform
-    const bool is_q = r < AQD, is_k = !is_q && r < AQD + AKVD;
-    const uint32_t rr = is_q ? r : (is_k ? r - AQD : r - AQD - AKVD);
+    const uint32_t r = A_RPW * wl + k;  // wave-uniform
+    const bool is_q = r < AGQD, is_k = !is_q && r < AGQD + AHD;
+    const uint32_t rr = is_q ? AHD * hq0 + r : AHD * kv + (is_k ? r - AGQD : r - AGQD - AHD);
     const uint32_t* w = is_q ? a.q_w : (is_k ? a.k_w : a.v_w);
     const uint16_t* sp = is_q ? a.q_s : (is_k ? a.k_s : a.v_s);
     const uint16_t* bp = is_q ? a.q_b : (is_k ? a.k_b : a.v_b);
@@ -142,37 +180,33 @@ attn_fused_kernel(AttnArgs a) {
     rsc[k] = sp[static_cast<size_t>(rr) * (AH / 64u) + lane / 2u];
     rbi[k] = bp[static_cast<size_t>(rr) * (AH / 64u) + lane / 2u];
   }
-  uint4 oq[A_ORPW][2];
-  uint16_t osc[A_ORPW][2], obi[A_ORPW][2], ores[A_ORPW];
   const uint32_t wq = *reinterpret_cast<const uint32_t*>(a.q_norm + 2u * lane);
   const uint32_t wk = *reinterpret_cast<const uint32_t*>(a.k_norm + 2u * lane);
-  // this workgroup's split of kv head kv, and the position's loads
-  const bool attends = blockIdx.x < A_NATT;  // uniform
-  const uint32_t kv = blockIdx.x % ANKV, sp = min(blockIdx.x / ANKV, A_NSPLIT - 1u);
+  // this workgroup's split of the sequence, and the position's loads
   const uint32_t max_len = a.max_len;
   const uint32_t pos = static_cast<uint32_t>(pos_i);
   const bool pos_ok = pos_i >= 0 && pos < max_len;
   const uint32_t seq = static_cast<uint32_t>(min(max(pos_i + 1, 1), static_cast<int32_t>(max_len)));
   const uint32_t nblk = (seq + 31u) / 32u, per = (nblk + A_NSPLIT - 1u) / A_NSPLIT;
-  const uint32_t b0 = sp * per, b1 = min(nblk, b0 + per);
-  const uint32_t col = lane & 15u, g = lane >> 4;
+  const uint32_t b0 = j * per, b1 = min(nblk, b0 + per);
+  const uint32_t col = lane & 15u, gq = lane >> 4;
   const uint16_t* kb = a.k_cache + static_cast<size_t>(kv) * max_len * AHD;
   const uint16_t* vb = a.v_cache_t + static_cast<size_t>(kv) * AHD * max_len;
   // wave w runs blocks b0 + w, b0 + w + 4, ...; its first block's loads go out
-  // now (clamped into the sequence when it has none; unused then)
+  // after the q/k/v publish (clamped into the sequence when it has none; unused then)
   u32x4_t ka[2][4];
   u32x2_t va[8][2];
   auto load_block = [&](uint32_t blk) __attribute__((always_inline)) {
     const uint32_t t0 = 32u * blk;
 #pragma unroll
     for (uint32_t tt = 0; tt < 2; ++tt) {
-      const uint16_t* kr = kb + static_cast<size_t>(t0 + 16u * tt + col) * AHD + 8u * g;
+      const uint16_t* kr = kb + static_cast<size_t>(t0 + 16u * tt + col) * AHD + 8u * gq;
 #pragma unroll
       for (uint32_t ks = 0; ks < 4; ++ks) ka[tt][ks] = *reinterpret_cast<const u32x4_t*>(kr + 32u * ks);
     }
 #pragma unroll
     for (uint32_t nt = 0; nt < 8; ++nt) {
-      const uint16_t* vr = vb + static_cast<size_t>(16u * nt + col) * max_len + t0 + 4u * g;
+      const uint16_t* vr = vb + static_cast<size_t>(16u * nt + col) * max_len + t0 + 4u * gq;
       va[nt][0] = *reinterpret_cast<const u32x2_t*>(vr);
       va[nt][1] = *reinterpret_cast<const u32x2_t*>(vr + 16);
     }
@@ -206,9 +240,9 @@ attn_fused_kernel(AttnArgs a) {
     for (int i = 0; i < 4; ++i) {
       const uint32_t wd[4] = {xq[i].x, xq[i].y, xq[i].z, xq[i].w};
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        xf[8 * i + 2 * j] = bf16lo(wd[j]);
-        xf[8 * i + 2 * j + 1] = bf16hi(wd[j]);
+      for (int jj = 0; jj < 4; ++jj) {
+        xf[8 * i + 2 * jj] = bf16lo(wd[jj]);
+        xf[8 * i + 2 * jj + 1] = bf16hi(wd[jj]);
       }
     }
     float ss = 0.0f;
@@ -219,9 +253,9 @@ attn_fused_kernel(AttnArgs a) {
     for (int i = 0; i < 4; ++i) {
       const uint32_t wd[4] = {nq[i].x, nq[i].y, nq[i].z, nq[i].w};
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        xf[8 * i + 2 * j] = bf16_to_f32(f32_to_bf16((xf[8 * i + 2 * j] * inv) * bf16lo(wd[j])));
-        xf[8 * i + 2 * j + 1] = bf16_to_f32(f32_to_bf16((xf[8 * i + 2 * j + 1] * inv) * bf16hi(wd[j])));
+      for (int jj = 0; jj < 4; ++jj) {
+        xf[8 * i + 2 * jj] = bf16_to_f32(f32_to_bf16((xf[8 * i + 2 * jj] * inv) * bf16lo(wd[jj])));
+        xf[8 * i + 2 * jj + 1] = bf16_to_f32(f32_to_bf16((xf[8 * i + 2 * jj + 1] * inv) * bf16hi(wd[jj])));
       }
     }
     float xs = 0.0f;
@@ -257,66 +291,47 @@ attn_fused_kernel(AttnArgs a) {
       if (tid == 0) __hip_atomic_fetch_add(ctl_count, uint64_t{1}, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       return;
     }
-    if (lane < A_RPW) slot_store(qkv_slots + A_RPW * wave_g + lane, s_epoch, mine);
+    if (lane < A_RPW) slot_store_xcd(qkv_slots + A_RPW * wl + lane, s_epoch, mine);  // polled by this XCD only
   }
-  // the wave's first key/value block (clamped into the sequence; unused by
-  // workgroups that do not attend or waves without a block)
+  // the wave's first key/value block
   load_block(min(b0 + wave, nblk - 1u));
-  // the o rows and the residual, needed only by the last phase
+  // the o rows of this wave (rows 64 j + 16 wave + 8 p + lane / 8), lane's 64
+  // of the group's 512 columns (the quantization group 2 hq0 + lane % 8), and
+  // for group 0 the residual of the rows it finishes
+  const uint32_t orow0 = A_ORWG * j + A_ORW * wave + lane / 8u, oc = lane & 7u;
+  uint4 oq[2][2];
+  uint16_t osc[2], obi[2];
 #pragma unroll
-  for (uint32_t k = 0; k < A_ORPW; ++k) {
-    const uint32_t r = A_ORPW * wave_g + k;
-#pragma unroll
-    for (uint32_t sg = 0; sg < 2; ++sg) {
-      oq[k][sg] = reinterpret_cast<const uint4*>(a.o_w + static_cast<size_t>(r) * (AQD / 8u) + 256u * sg)[lane];
-      const size_t gi = static_cast<size_t>(r) * (AQD / 64u) + 32u * sg + lane / 2u;
-      osc[k][sg] = a.o_s[gi];
-      obi[k][sg] = a.o_b[gi];
-    }
-    ores[k] = a.x[r];
+  for (uint32_t p = 0; p < 2; ++p) {
+    const size_t r = orow0 + 8u * p;
+    const uint4* op = reinterpret_cast<const uint4*>(a.o_w + r * (AQD / 8u) + (AHD * hq0 + 64u * oc) / 8u);
+    oq[p][0] = op[0];
+    oq[p][1] = op[1];
+    const size_t gi = r * (AQD / 64u) + 2u * hq0 + oc;
+    osc[p] = a.o_s[gi];
+    obi[p] = a.o_b[gi];
   }
+  const uint16_t ores = a.x[A_ORWG * j + (lane & 63u)];  // group 0, wave 0: row 64 j + lane
   const uint32_t epoch = s_epoch;
   OBS_ATTN_MARK(2);
-  if (attends) {  // workgroup-uniform
 
-  // ---- 2. this workgroup's split of kv head kv: poll the split's q heads
-  // (rows 1024 kv ..), k (4096 + 128 kv ..) and v (4608 + 128 kv ..)
+  // ---- 2. this workgroup's split: poll the group's q heads, key and value
   {
-    float vals[5];
-    const uint64_t t0 = wall_clock64();
-    bool ok = true;
-    while (true) {
-      bool ready = true;
+    float vals[3];
+    if (!poll_slots<3>(qkv_slots, epoch, vals) && lane == 0) s_fail = 1;
 #pragma unroll
-      for (uint32_t u = 0; u < 5; ++u) {
-        const uint32_t i = tid + 256u * u;
-        const uint32_t row = i < AG * AHD ? kv * AG * AHD + i
-                                          : (i < AG * AHD + AHD ? AQD + kv * AHD + (i - AG * AHD)
-                                                                : AQD + AKVD + kv * AHD + (i - AG * AHD - AHD));
-        const uint64_t v = slot_load(qkv_slots + row);
-        vals[u] = slot_val(v);
-        ready = ready && slot_ready(v, epoch);
-      }
-      if (__all(ready)) break;
-      if (wall_clock64() - t0 > A_WAIT_TICKS) {
-        ok = false;
-        break;
-      }
-    }
-    if (!ok && lane == 0) s_fail = 1;
-#pragma unroll
-    for (uint32_t u = 0; u < 5; ++u) s_qkv[tid + 256u * u] = vals[u];
+    for (uint32_t u = 0; u < 3; ++u) s_qkv[tid + 256u * u] = vals[u];
   }
   __syncthreads();
   OBS_ATTN_MARK(3);
   // per-head RMSNorm + NeoX RoPE (attn_prep_kernel's sequence): wave w owns
-  // heads w, w + 4 (query heads) and, for wave 0, head 8 = the key head
+  // query head w and, for wave 0, head 4 = the key head
   {
     const float cs[2] = {csn[0], csn[2]}, sn[2] = {csn[1], csn[3]};
     const bool first = lane < 32u;
-    for (uint32_t h = wave; h <= AG; h += 4u) {
+    for (uint32_t h = wave; h <= AQPG; h += 4u) {
       const float x0 = s_qkv[h * AHD + 2u * lane], x1 = s_qkv[h * AHD + 2u * lane + 1u];
-      const uint32_t wv = h < AG ? wq : wk;
+      const uint32_t wv = h < AQPG ? wq : wk;
       float ss = __builtin_fmaf(x0, x0, 0.0f);
       ss = __builtin_fmaf(x1, x1, ss);
       const float inv = 1.0f / __builtin_sqrtf(wave_sum_asc(ss) / static_cast<float>(AHD) + a.eps);
@@ -325,36 +340,38 @@ attn_fused_kernel(AttnArgs a) {
       const float p0 = shfl_xor_f(n0, 32), p1 = shfl_xor_f(n1, 32);
       float r[2];
 #pragma unroll
-      for (uint32_t j = 0; j < 2; ++j) {
-        const float own = j ? n1 : n0, other = j ? p1 : p0;
-        const float aa = own * cs[j], bb = other * sn[j];
-        r[j] = first ? aa - bb : aa + bb;
+      for (uint32_t jj = 0; jj < 2; ++jj) {
+        const float own = jj ? n1 : n0, other = jj ? p1 : p0;
+        const float aa = own * cs[jj], bb = other * sn[jj];
+        r[jj] = first ? aa - bb : aa + bb;
       }
       *reinterpret_cast<uint32_t*>(&s_rot[h][2u * lane]) = pack_bf16x2(r[0], r[1]);
     }
     if (wave == 1) {  // the value head, as bf16
-      *reinterpret_cast<uint32_t*>(&s_rot[AG + 1][2u * lane]) =
-          pack_bf16x2(s_qkv[(AG + 1) * AHD + 2u * lane], s_qkv[(AG + 1) * AHD + 2u * lane + 1u]);
+      *reinterpret_cast<uint32_t*>(&s_rot[AQPG + 1][2u * lane]) =
+          pack_bf16x2(s_qkv[(AQPG + 1) * AHD + 2u * lane], s_qkv[(AQPG + 1) * AHD + 2u * lane + 1u]);
     }
   }
   __syncthreads();
   OBS_ATTN_MARK(4);
   const uint32_t pblk = pos / 32u;
-  const bool own_pos = pos_ok && pblk >= b0 && pblk < b1;  // this split holds pos: append it
+  // the even group of the kv head appends it (the odd one computes the same
+  // key and value and splices them in from registers, like every split does)
+  const bool own_pos = pos_ok && pblk >= b0 && pblk < b1 && (g % 2u) == 0u;
   if (own_pos && wave == 0) {
     *reinterpret_cast<uint32_t*>(a.k_cache + (static_cast<size_t>(kv) * max_len + pos) * AHD + 2u * lane) =
-        *reinterpret_cast<const uint32_t*>(&s_rot[AG][2u * lane]);
+        *reinterpret_cast<const uint32_t*>(&s_rot[AQPG][2u * lane]);
   } else if (own_pos && wave == 1) {
     uint16_t* dst = a.v_cache_t + (static_cast<size_t>(kv) * AHD + 2u * lane) * max_len + pos;
-    dst[0] = s_rot[AG + 1][2u * lane];
-    dst[max_len] = s_rot[AG + 1][2u * lane + 1u];
+    dst[0] = s_rot[AQPG + 1][2u * lane];
+    dst[max_len] = s_rot[AQPG + 1][2u * lane + 1u];
   }
-  // query slices: B operand, head col (zero for the padding columns 8..15)
+  // query slices: B operand, head col (zero for the padding columns 4..15)
   bf16x8_t qb[4];
 #pragma unroll
   for (uint32_t ks = 0; ks < 4; ++ks) {
-    u32x4_t v = *reinterpret_cast<const u32x4_t*>(&s_rot[min(col, AG - 1u)][32u * ks + 8u * g]);
-    if (col >= AG) v = u32x4_t{0u, 0u, 0u, 0u};
+    u32x4_t v = *reinterpret_cast<const u32x4_t*>(&s_rot[min(col, AQPG - 1u)][32u * ks + 8u * gq]);
+    if (col >= AQPG) v = u32x4_t{0u, 0u, 0u, 0u};
     qb[ks] = __builtin_bit_cast(bf16x8_t, v);
   }
   float m_run = -__builtin_huge_valf(), l_run = 0.0f;
@@ -370,13 +387,13 @@ attn_fused_kernel(AttnArgs a) {
         if (t0 + 16u * tt + col == pos)
 #pragma unroll
           for (uint32_t ks = 0; ks < 4; ++ks)
-            ka[tt][ks] = *reinterpret_cast<const u32x4_t*>(&s_rot[AG][32u * ks + 8u * g]);
+            ka[tt][ks] = *reinterpret_cast<const u32x4_t*>(&s_rot[AQPG][32u * ks + 8u * gq]);
 #pragma unroll
       for (uint32_t nt = 0; nt < 8; ++nt) {
-        const uint32_t vv = s_rot[AG + 1][16u * nt + col];
+        const uint32_t vv = s_rot[AQPG + 1][16u * nt + col];
 #pragma unroll
         for (uint32_t hh = 0; hh < 2; ++hh) {
-          const uint32_t ta = t0 + 16u * hh + 4u * g;  // positions ta .. ta + 3 in two words
+          const uint32_t ta = t0 + 16u * hh + 4u * gq;  // positions ta .. ta + 3 in two words
           if (pos >= ta && pos < ta + 4u) {
             const uint32_t e = pos - ta, sh = 16u * (e & 1u);
             uint32_t wd = (e >> 1) ? va[nt][hh].y : va[nt][hh].x;
@@ -400,7 +417,7 @@ attn_fused_kernel(AttnArgs a) {
     for (uint32_t tt = 0; tt < 2; ++tt)
 #pragma unroll
       for (uint32_t i = 0; i < 4; ++i) {
-        const uint32_t t = t0 + 16u * tt + 4u * g + i;
+        const uint32_t t = t0 + 16u * tt + 4u * gq + i;
         sv[4 * tt + i] = t < seq ? s[tt][i] * a.scale_log2 : -__builtin_huge_valf();
       }
     float bm = sv[0];
@@ -418,9 +435,9 @@ attn_fused_kernel(AttnArgs a) {
     }
     l_run = l_run * corr + psum;
     m_run = m_new;
-    float oc[4];
+    float ocr[4];
 #pragma unroll
-    for (uint32_t i = 0; i < 4; ++i) oc[i] = shfl_f(corr, static_cast<int>(4u * g + i));
+    for (uint32_t i = 0; i < 4; ++i) ocr[i] = shfl_f(corr, static_cast<int>(4u * gq + i));
     const bf16x8_t pa = __builtin_bit_cast(
         bf16x8_t, u32x4_t{pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]), pack_bf16x2(p[4], p[5]),
                           pack_bf16x2(p[6], p[7])});
@@ -430,7 +447,7 @@ attn_fused_kernel(AttnArgs a) {
       u32x2_t v0 = va[nt][0], v1 = va[nt][1];
       if (tail) {
         auto keep = [&](uint32_t w, uint32_t t) { return t >= seq ? 0u : (t + 1u >= seq ? (w & 0xffffu) : w); };
-        const uint32_t ta = t0 + 4u * g, tb = ta + 16u;
+        const uint32_t ta = t0 + 4u * gq, tb = ta + 16u;
         v0.x = keep(v0.x, ta);
         v0.y = keep(v0.y, ta + 2u);
         v1.x = keep(v1.x, tb);
@@ -438,29 +455,30 @@ attn_fused_kernel(AttnArgs a) {
       }
       const bf16x8_t vbf = __builtin_bit_cast(bf16x8_t, u32x4_t{v0.x, v0.y, v1.x, v1.y});
 #pragma unroll
-      for (uint32_t i = 0; i < 4; ++i) o[nt][i] *= oc[i];
+      for (uint32_t i = 0; i < 4; ++i) o[nt][i] *= ocr[i];
       o[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, vbf, o[nt], 0, 0, 0);
     }
   }
   OBS_ATTN_MARK(5);
-  // the wave's partial: m, l per head column (l summed over the four g lanes), O rows 4 g + i
+  // the wave's partial: m, l per head column (l summed over the four gq lanes), O rows 4 gq + i
   l_run += shfl_xor_f(l_run, 16);
   l_run += shfl_xor_f(l_run, 32);
   if (lane < 16u) {
     s_pm[wave][lane] = m_run;
     s_pl[wave][lane] = l_run;
   }
-  if (g < 2u) {
+  if (gq == 0u) {
 #pragma unroll
     for (uint32_t nt = 0; nt < 8; ++nt)
 #pragma unroll
-      for (uint32_t i = 0; i < 4; ++i) s_po[wave][4u * g + i][16u * nt + col] = o[nt][i];
+      for (uint32_t i = 0; i < 4; ++i) s_po[wave][i][16u * nt + col] = o[nt][i];
   }
   __syncthreads();
-  // merge the four waves (a wave without blocks has m = -inf, l = 0, O = 0) and publish
+  // merge the four waves (a wave without blocks has m = -inf, l = 0, O = 0) and
+  // publish: thread (head h, dims d0 .. d0 + 1)
   {
-    uint64_t* dst = part_slots + static_cast<size_t>(blockIdx.x) * A_PART;
-    const uint32_t h = tid / 32u, d0 = 4u * (tid % 32u);
+    uint64_t* dst = part_slots + static_cast<size_t>(j) * A_PART;
+    const uint32_t h = tid / 64u, d0 = 2u * (tid % 64u);
     float M = s_pm[0][h];
 #pragma unroll
     for (uint32_t w = 1; w < 4; ++w) M = fmaxf(M, s_pm[w][h]);
@@ -471,26 +489,23 @@ attn_fused_kernel(AttnArgs a) {
       L = __builtin_fmaf(s_pl[w][h], wt[w], L);
     }
 #pragma unroll
-    for (uint32_t d = 0; d < 4; ++d) {
+    for (uint32_t d = 0; d < 2; ++d) {
       float acc = 0.0f;
 #pragma unroll
       for (uint32_t w = 0; w < 4; ++w) acc = __builtin_fmaf(s_po[w][h][d0 + d], wt[w], acc);
-      slot_store(dst + h * (AHD + 2u) + d0 + d, epoch, acc);
+      slot_store_xcd(dst + h * (AHD + 2u) + d0 + d, epoch, acc);
     }
-    if (tid % 32u == 0u) {
-      slot_store(dst + h * (AHD + 2u) + AHD, epoch, M);
-      slot_store(dst + h * (AHD + 2u) + AHD + 1u, epoch, L);
+    if (tid % 64u == 0u) {
+      slot_store_xcd(dst + h * (AHD + 2u) + AHD, epoch, M);
+      slot_store_xcd(dst + h * (AHD + 2u) + AHD + 1u, epoch, L);
     }
   }
-
-  }  // attends
   OBS_ATTN_MARK(6);
-  // ---- 3. combine head j / 8, dims 16 (j % 8) .. + 16 over the 32 splits
+  // ---- 3. combine query head j / 8 of the group, dims 16 (j % 8) .. + 16, over the 32 splits
   {
-    const uint32_t h = blockIdx.x / 8u, d0 = A_CDIM * (blockIdx.x % 8u);
-    const uint32_t ckv = h / AG, hh = h % AG;
+    const uint32_t hh = j / 8u, d0 = A_CDIM * (j % 8u);
     const uint32_t s = tid / 8u, q8 = tid % 8u;  // split s, dims d0 + 2 q8, + 1
-    const uint64_t* src = part_slots + static_cast<size_t>(s * ANKV + ckv) * A_PART + hh * (AHD + 2u);
+    const uint64_t* src = part_slots + static_cast<size_t>(s) * A_PART + hh * (AHD + 2u);
     float v[4];
     const uint64_t t0 = wall_clock64();
     bool ok = s_fail == 0;
@@ -542,94 +557,103 @@ attn_fused_kernel(AttnArgs a) {
       const uint32_t mine = f32_to_bf16(acc / L);
       const uint32_t next = __shfl_xor(static_cast<int>(mine), 1, 64);
       if (lane < A_CDIM && (lane & 1u) == 0u)
-        slot_store(attn_slots + (h * AHD + d0 + lane) / 2u, epoch, __uint_as_float(mine | (next << 16)));
+        slot_store_xcd(attn_slots + (hh * AHD + d0 + lane) / 2u, epoch, __uint_as_float(mine | (next << 16)));
     }
   }
   OBS_ATTN_MARK(8);
 
-  // ---- 4. x1 = x + W_o attn: the attention output into LDS as f16 pairs in
+  // ---- 4. the group's 512 attention outputs into LDS as f16 pairs in
   // dot8_q4_off order, with the sum and the offset sum of every 32 columns
   {
-    // the 2,048 bf16 pairs (the loop decisions are workgroup-uniform)
-    bool ok = s_fail == 0;
-    const uint64_t t0 = wall_clock64();
-    uint32_t pv[AQD / 512];
-    while (ok) {
-      bool ready = true;
-#pragma unroll
-      for (uint32_t u = 0; u < AQD / 512; ++u) {
-        const uint64_t x = slot_load(attn_slots + tid + 256u * u);
-        pv[u] = static_cast<uint32_t>(x);
-        ready = ready && slot_ready(x, epoch);
-      }
-      const int late = wall_clock64() - t0 > A_WAIT_TICKS;
-      if (__syncthreads_and(ready)) break;
-      if (__syncthreads_or(late)) ok = false;
-    }
-    if (!ok && tid == 0) s_fail = 1;
+    float pvf[1];
+    const bool ok = s_fail == 0 && poll_slots<1>(attn_slots, epoch, pvf);
+    if (!ok && lane == 0) s_fail = 1;
+    const uint32_t pv = __float_as_uint(pvf[0]);
     _Float16* ap16 = reinterpret_cast<_Float16*>(s_ap);
-#pragma unroll
-    for (uint32_t u = 0; u < AQD / 512; ++u) {
-      const uint32_t k = tid + 256u * u, i0 = 2u * k;  // columns i0 (low half), i0 + 1
-      const _Float16 h0 = static_cast<_Float16>(bf16lo(pv[u])), h1 = static_cast<_Float16>(bf16hi(pv[u]));
-      const uint32_t j0 = i0 & 7u, j1 = j0 + 1u;
-      ap16[(i0 & ~7u) + 2u * (j0 & 3u) + (j0 >> 2)] = h0;
-      ap16[(i0 & ~7u) + 2u * (j1 & 3u) + (j1 >> 2)] = h1;
-      // per 32 columns = 16 consecutive lanes: the sum and the offset sum of
-      // dot8_q4_off (1024 at even positions, 64 at odd ones) over the f16 values
-      float sum = static_cast<float>(h0) + static_cast<float>(h1);
-      float off = static_cast<float>(h0) * 1024.0f + static_cast<float>(h1) * 64.0f;
-      sum = sum + dpp_f32<DPP_XOR1>(sum);
-      sum = sum + dpp_f32<DPP_XOR2>(sum);
-      sum = sum + dpp_f32<DPP_HALF_MIRROR>(sum);
-      sum = sum + dpp_f32<DPP_MIRROR>(sum);
-      off = off + dpp_f32<DPP_XOR1>(off);
-      off = off + dpp_f32<DPP_XOR2>(off);
-      off = off + dpp_f32<DPP_HALF_MIRROR>(off);
-      off = off + dpp_f32<DPP_MIRROR>(off);
-      if ((k & 15u) == 0u) {
-        s_asum[k >> 4] = sum;
-        s_aoff[k >> 4] = off;
-      }
+    const uint32_t i0 = 2u * tid;  // columns i0 (low half), i0 + 1
+    const _Float16 h0 = static_cast<_Float16>(bf16lo(pv)), h1 = static_cast<_Float16>(bf16hi(pv));
+    const uint32_t j0 = i0 & 7u, j1 = j0 + 1u;
+    ap16[(i0 & ~7u) + 2u * (j0 & 3u) + (j0 >> 2)] = h0;
+    ap16[(i0 & ~7u) + 2u * (j1 & 3u) + (j1 >> 2)] = h1;
+    // per 32 columns = 16 consecutive lanes: the sum and the offset sum of
+    // dot8_q4_off (1024 at even positions, 64 at odd ones) over the f16 values
+    float sum = static_cast<float>(h0) + static_cast<float>(h1);
+    float off = static_cast<float>(h0) * 1024.0f + static_cast<float>(h1) * 64.0f;
+    sum = sum + dpp_f32<DPP_XOR1>(sum);
+    sum = sum + dpp_f32<DPP_XOR2>(sum);
+    sum = sum + dpp_f32<DPP_HALF_MIRROR>(sum);
+    sum = sum + dpp_f32<DPP_MIRROR>(sum);
+    off = off + dpp_f32<DPP_XOR1>(off);
+    off = off + dpp_f32<DPP_XOR2>(off);
+    off = off + dpp_f32<DPP_HALF_MIRROR>(off);
+    off = off + dpp_f32<DPP_MIRROR>(off);
+    if ((tid & 15u) == 0u) {
+      s_asum[tid >> 4] = sum;
+      s_aoff[tid >> 4] = off;
     }
   }
   __syncthreads();
   OBS_ATTN_MARK(9);
+  // partial W_o rows over the group's columns: lane (row 8 p + lane / 8, 64
+  // columns 64 (lane % 8) .. of the group's 512 = one quantization group), then
+  // the 8 lanes of a row summed
   {
     f16x2_t ah[2][16];
-    float asum[2], aoff[2];
 #pragma unroll
     for (uint32_t sg = 0; sg < 2; ++sg) {
-      const uint32_t c0 = 2048u * sg + 32u * lane;
+      const uint32_t c0 = 64u * oc + 32u * sg;
 #pragma unroll
       for (uint32_t i = 0; i < 4; ++i) {
         const uint4 w4 = *reinterpret_cast<const uint4*>(&s_ap[c0 / 2u + 4u * i]);
         ah[sg][4 * i] = as_f16x2(w4.x); ah[sg][4 * i + 1] = as_f16x2(w4.y);
         ah[sg][4 * i + 2] = as_f16x2(w4.z); ah[sg][4 * i + 3] = as_f16x2(w4.w);
       }
-      asum[sg] = s_asum[c0 / 32u];
-      aoff[sg] = s_aoff[c0 / 32u];
     }
-    float mine = 0.0f;  // lane k keeps row k
+    const float asum = s_asum[2u * oc] + s_asum[2u * oc + 1u], aoff = s_aoff[2u * oc] + s_aoff[2u * oc + 1u];
 #pragma unroll
-    for (uint32_t k = 0; k < A_ORPW; ++k) {
-      float part = 0.0f;
+    for (uint32_t p = 0; p < 2; ++p) {
+      float acc = 0.0f;
 #pragma unroll
       for (uint32_t sg = 0; sg < 2; ++sg) {
-        float acc = 0.0f;
-        acc = dot8_q4_off(oq[k][sg].x, ah[sg] + 0, acc);
-        acc = dot8_q4_off(oq[k][sg].y, ah[sg] + 4, acc);
-        acc = dot8_q4_off(oq[k][sg].z, ah[sg] + 8, acc);
-        acc = dot8_q4_off(oq[k][sg].w, ah[sg] + 12, acc);
-        part = part + __builtin_fmaf(bf16_to_f32(osc[k][sg]), acc - aoff[sg], bf16_to_f32(obi[k][sg]) * asum[sg]);
+        acc = dot8_q4_off(oq[p][sg].x, ah[sg] + 0, acc);
+        acc = dot8_q4_off(oq[p][sg].y, ah[sg] + 4, acc);
+        acc = dot8_q4_off(oq[p][sg].z, ah[sg] + 8, acc);
+        acc = dot8_q4_off(oq[p][sg].w, ah[sg] + 12, acc);
       }
-      part = wave_sum_asc(part);
-      mine = lane == k ? bf16_to_f32(ores[k]) + part : mine;
+      const float part = group8_sum(__builtin_fmaf(bf16_to_f32(osc[p]), acc - aoff, bf16_to_f32(obi[p]) * asum));
+      if (oc == 0u) slot_store(y_slots + size_t(g) * AH + orow0 + 8u * p, epoch, part);  // polled by group 0
     }
-    if (lane < A_ORPW) a.x1[A_ORPW * wave_g + lane] = f32_to_bf16(mine);
+  }
+  OBS_ATTN_MARK(10);
+  // ---- 5. group 0: x1 = x + sum of the 8 groups' partials, rows 64 j .. + 64
+  if (g == 0) {
+    bool ok = s_fail == 0;
+    const uint64_t t0 = wall_clock64();
+    while (ok) {
+      bool ready = true;
+#pragma unroll
+      for (uint32_t u = 0; u < 2; ++u) {
+        const uint32_t sidx = tid + 256u * u;  // group sidx / 64, row sidx % 64
+        const uint64_t v = slot_load(y_slots + size_t(sidx >> 6) * AH + A_ORWG * j + (sidx & 63u));
+        s_y[sidx >> 6][sidx & 63u] = slot_val(v);
+        ready = ready && slot_ready(v, epoch);
+      }
+      if (__all(ready)) break;
+      if (wall_clock64() - t0 > A_WAIT_TICKS) {
+        ok = false;
+        if (lane == 0) s_fail = 1;
+      }
+    }
+    __syncthreads();
+    if (wave == 0) {
+      float acc = bf16_to_f32(ores);
+#pragma unroll
+      for (uint32_t q = 0; q < ANGRP; ++q) acc += s_y[q][lane];
+      a.x1[A_ORWG * j + lane] = f32_to_bf16(acc);
+    }
   }
   __syncthreads();
-  OBS_ATTN_MARK(10);
+  OBS_ATTN_MARK(11);
   if (tid == 0) {
     if (s_fail) __hip_atomic_store(ctl_err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     __hip_atomic_fetch_add(ctl_count, uint64_t{1}, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
