@@ -352,7 +352,8 @@ int obs_argmax(obs_ctx* ctx, const float* x, uint32_t n, int32_t* state, void* w
  * fused norm) + obs_attn_prep + obs_sdpa_decode + obs_q4_gemv (o, residual)
  * compute, in one launch of 256 workgroups that exchange values through a
  * context-owned area (allocated on the first call: run one before a graph
- * capture). Needs all 256 CUs; other shapes use the separate calls. */
+ * capture). Needs all 256 CUs; other shapes use the separate calls. x, the
+ * weight rows and both caches must be 16-byte aligned (OBS_E_ALIGN). */
 typedef struct obs_attn_layer {
   const uint32_t* q_w; const uint16_t* q_s; const uint16_t* q_b;  /* [4096, 2048/8], [4096, 32] */
   const uint32_t* k_w; const uint16_t* k_s; const uint16_t* k_b;  /* [512, ...] */

@@ -35,11 +35,13 @@
 // (The earlier split of the same work over the whole grid exchanged q/k/v,
 // the split partials and the attention outputs across XCDs, three round trips
 // through memory that cost 1.5-3.3 us each.)
-// Every weight, activation and cache load that does not depend on an exchange
-// is issued before the first exchange: the q/k/v rows at the start, the first
-// key/value block and the o rows right after the q/k/v publish, so the
-// exchanges overlap the memory stream and the q/k/v rows have the bandwidth
-// to themselves.
+// Load order. A wave's loads complete in issue order, and a CU accepts them
+// only as fast as memory drains them, so each batch sits where it delays
+// nothing more urgent: the q/k/v rows at the start (they have the bandwidth
+// to themselves), the first key/value block right after the q/k/v poll (issued
+// before it, the poll waited for the block's data; issued at the start, the
+// rows shared their bandwidth), and the o rows after the attention blocks,
+// where their latency overlaps the two exchanges that precede their use.
 // Every wait is bounded (100 ms of the constant clock); a time-out sets the
 // workspace's error flag, reported and cleared by obs_device_status.
 #include "obs_internal.hpp"
@@ -144,10 +146,8 @@ attn_fused_kernel(AttnArgs a) {
   OBS_ATTN_MARK(0);
   // ---- 0. loads that the q/k/v rows and the RoPE need, in the order they are
   // used: the position, the activations, the q/k/v rows, the launch count,
-  // then the RoPE cosines and sines at the position. The first key/value block
-  // and the o rows follow the q/k/v publish: issued here they shared the
-  // bandwidth with the q/k/v rows, and the publish (which waits for the count,
-  // loaded last) waited for them too.
+  // then the RoPE cosines and sines at the position (the key/value blocks and
+  // the o rows come later; see the load order above).
   // the position, as the first vector load (a per-lane index keeps it off the
   // scalar cache, whose load the compiler issued late and which returned only
   // after the flood of row loads): the RoPE load that needs it waits for it
@@ -193,23 +193,26 @@ attn_fused_kernel(AttnArgs a) {
   const uint16_t* kb = a.k_cache + static_cast<size_t>(kv) * max_len * AHD;
   const uint16_t* vb = a.v_cache_t + static_cast<size_t>(kv) * AHD * max_len;
   // wave w runs blocks b0 + w, b0 + w + 4, ...; its first block's loads go out
-  // after the q/k/v publish (clamped into the sequence when it has none; unused then)
+  // after the q/k/v poll. Row r of score tile tt (the MFMA's A rows) is
+  // position t0 + 8 (r / 4) + 4 tt + r % 4 of the 32-position block, so lane
+  // (col, gq) ends with the scores of positions t0 + 8 gq .. + 7 and reads
+  // their values as one 16-byte run of the transposed value cache.
   u32x4_t ka[2][4];
-  u32x2_t va[8][2];
+  u32x4_t va[8];
+  auto kpos = [&](uint32_t t0, uint32_t tt) __attribute__((always_inline)) {
+    return t0 + 8u * (col >> 2) + 4u * tt + (col & 3u);
+  };
   auto load_block = [&](uint32_t blk) __attribute__((always_inline)) {
     const uint32_t t0 = 32u * blk;
 #pragma unroll
     for (uint32_t tt = 0; tt < 2; ++tt) {
-      const uint16_t* kr = kb + static_cast<size_t>(t0 + 16u * tt + col) * AHD + 8u * gq;
+      const uint16_t* kr = kb + static_cast<size_t>(kpos(t0, tt)) * AHD + 8u * gq;
 #pragma unroll
       for (uint32_t ks = 0; ks < 4; ++ks) ka[tt][ks] = *reinterpret_cast<const u32x4_t*>(kr + 32u * ks);
     }
 #pragma unroll
-    for (uint32_t nt = 0; nt < 8; ++nt) {
-      const uint16_t* vr = vb + static_cast<size_t>(16u * nt + col) * max_len + t0 + 4u * gq;
-      va[nt][0] = *reinterpret_cast<const u32x2_t*>(vr);
-      va[nt][1] = *reinterpret_cast<const u32x2_t*>(vr + 16);
-    }
+    for (uint32_t nt = 0; nt < 8; ++nt)
+      va[nt] = *reinterpret_cast<const u32x4_t*>(vb + static_cast<size_t>(16u * nt + col) * max_len + t0 + 8u * gq);
   };
   // every row load above is issued before anything waits for the position
   // (left alone, the scheduler put that wait ahead of the last row's load)
@@ -293,25 +296,12 @@ attn_fused_kernel(AttnArgs a) {
     }
     if (lane < A_RPW) slot_store_xcd(qkv_slots + A_RPW * wl + lane, s_epoch, mine);  // polled by this XCD only
   }
-  // the wave's first key/value block
-  load_block(min(b0 + wave, nblk - 1u));
-  // the o rows of this wave (rows 64 j + 16 wave + 8 p + lane / 8), lane's 64
-  // of the group's 512 columns (the quantization group 2 hq0 + lane % 8), and
-  // for group 0 the residual of the rows it finishes
+  // the o rows of this wave: rows 64 j + 16 wave + 8 p + lane / 8, the lane's
+  // 64 of the group's 512 columns (the quantization group 2 hq0 + lane % 8);
+  // loaded after the attention blocks
   const uint32_t orow0 = A_ORWG * j + A_ORW * wave + lane / 8u, oc = lane & 7u;
   uint4 oq[2][2];
   uint16_t osc[2], obi[2];
-#pragma unroll
-  for (uint32_t p = 0; p < 2; ++p) {
-    const size_t r = orow0 + 8u * p;
-    const uint4* op = reinterpret_cast<const uint4*>(a.o_w + r * (AQD / 8u) + (AHD * hq0 + 64u * oc) / 8u);
-    oq[p][0] = op[0];
-    oq[p][1] = op[1];
-    const size_t gi = r * (AQD / 64u) + 2u * hq0 + oc;
-    osc[p] = a.o_s[gi];
-    obi[p] = a.o_b[gi];
-  }
-  const uint16_t ores = a.x[A_ORWG * j + (lane & 63u)];  // group 0, wave 0: row 64 j + lane
   const uint32_t epoch = s_epoch;
   OBS_ATTN_MARK(2);
 
@@ -323,6 +313,9 @@ attn_fused_kernel(AttnArgs a) {
     for (uint32_t u = 0; u < 3; ++u) s_qkv[tid + 256u * u] = vals[u];
   }
   __syncthreads();
+  // the wave's first key/value block (clamped into the sequence when it has
+  // none; unused then), now that no poll waits behind it
+  load_block(min(b0 + wave, nblk - 1u));
   OBS_ATTN_MARK(3);
   // per-head RMSNorm + NeoX RoPE (attn_prep_kernel's sequence): wave w owns
   // query head w and, for wave 0, head 4 = the key head
@@ -384,22 +377,22 @@ attn_fused_kernel(AttnArgs a) {
     if (pblk == blk) {  // uniform: splice this token's key and value (the cache held the old ones)
 #pragma unroll
       for (uint32_t tt = 0; tt < 2; ++tt)
-        if (t0 + 16u * tt + col == pos)
+        if (kpos(t0, tt) == pos)
 #pragma unroll
           for (uint32_t ks = 0; ks < 4; ++ks)
             ka[tt][ks] = *reinterpret_cast<const u32x4_t*>(&s_rot[AQPG][32u * ks + 8u * gq]);
+      const uint32_t ta = t0 + 8u * gq;  // this lane's positions ta .. ta + 7, two per word
+      if (pos >= ta && pos < ta + 8u) {
+        const uint32_t e = pos - ta, wi = e >> 1, sh = 16u * (e & 1u);
 #pragma unroll
-      for (uint32_t nt = 0; nt < 8; ++nt) {
-        const uint32_t vv = s_rot[AQPG + 1][16u * nt + col];
-#pragma unroll
-        for (uint32_t hh = 0; hh < 2; ++hh) {
-          const uint32_t ta = t0 + 16u * hh + 4u * gq;  // positions ta .. ta + 3 in two words
-          if (pos >= ta && pos < ta + 4u) {
-            const uint32_t e = pos - ta, sh = 16u * (e & 1u);
-            uint32_t wd = (e >> 1) ? va[nt][hh].y : va[nt][hh].x;
-            wd = (wd & ~(0xffffu << sh)) | (vv << sh);
-            if (e >> 1) va[nt][hh].y = wd; else va[nt][hh].x = wd;
-          }
+        for (uint32_t nt = 0; nt < 8; ++nt) {
+          const uint32_t vv = s_rot[AQPG + 1][16u * nt + col];
+          uint32_t wd = wi == 0u ? va[nt].x : (wi == 1u ? va[nt].y : (wi == 2u ? va[nt].z : va[nt].w));
+          wd = (wd & ~(0xffffu << sh)) | (vv << sh);
+          va[nt].x = wi == 0u ? wd : va[nt].x;
+          va[nt].y = wi == 1u ? wd : va[nt].y;
+          va[nt].z = wi == 2u ? wd : va[nt].z;
+          va[nt].w = wi == 3u ? wd : va[nt].w;
         }
       }
     }
@@ -417,7 +410,7 @@ attn_fused_kernel(AttnArgs a) {
     for (uint32_t tt = 0; tt < 2; ++tt)
 #pragma unroll
       for (uint32_t i = 0; i < 4; ++i) {
-        const uint32_t t = t0 + 16u * tt + 4u * gq + i;
+        const uint32_t t = t0 + 8u * gq + 4u * tt + i;
         sv[4 * tt + i] = t < seq ? s[tt][i] * a.scale_log2 : -__builtin_huge_valf();
       }
     float bm = sv[0];
@@ -444,21 +437,34 @@ attn_fused_kernel(AttnArgs a) {
     const bool tail = t0 + 32u > seq;  // positions past seq read zero values
 #pragma unroll
     for (uint32_t nt = 0; nt < 8; ++nt) {
-      u32x2_t v0 = va[nt][0], v1 = va[nt][1];
+      u32x4_t v = va[nt];
       if (tail) {
         auto keep = [&](uint32_t w, uint32_t t) { return t >= seq ? 0u : (t + 1u >= seq ? (w & 0xffffu) : w); };
-        const uint32_t ta = t0 + 4u * gq, tb = ta + 16u;
-        v0.x = keep(v0.x, ta);
-        v0.y = keep(v0.y, ta + 2u);
-        v1.x = keep(v1.x, tb);
-        v1.y = keep(v1.y, tb + 2u);
+        const uint32_t ta = t0 + 8u * gq;
+        v.x = keep(v.x, ta);
+        v.y = keep(v.y, ta + 2u);
+        v.z = keep(v.z, ta + 4u);
+        v.w = keep(v.w, ta + 6u);
       }
-      const bf16x8_t vbf = __builtin_bit_cast(bf16x8_t, u32x4_t{v0.x, v0.y, v1.x, v1.y});
+      const bf16x8_t vbf = __builtin_bit_cast(bf16x8_t, v);
 #pragma unroll
       for (uint32_t i = 0; i < 4; ++i) o[nt][i] *= ocr[i];
       o[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, vbf, o[nt], 0, 0, 0);
     }
   }
+  // the o rows (used after two more exchanges) and, for group 0, the residual
+  // of the rows it finishes
+#pragma unroll
+  for (uint32_t p = 0; p < 2; ++p) {
+    const size_t r = orow0 + 8u * p;
+    const uint4* op = reinterpret_cast<const uint4*>(a.o_w + r * (AQD / 8u) + (AHD * hq0 + 64u * oc) / 8u);
+    oq[p][0] = op[0];
+    oq[p][1] = op[1];
+    const size_t gi = r * (AQD / 64u) + 2u * hq0 + oc;
+    osc[p] = a.o_s[gi];
+    obi[p] = a.o_b[gi];
+  }
+  const uint16_t ores = a.x[A_ORWG * j + (lane & 63u)];  // group 0, wave 0: row 64 j + lane
   OBS_ATTN_MARK(5);
   // the wave's partial: m, l per head column (l summed over the four gq lanes), O rows 4 gq + i
   l_run += shfl_xor_f(l_run, 16);
@@ -699,8 +705,8 @@ int obs_attn_decode(obs_ctx* ctx, const obs_attn_layer* L, const uint16_t* x, ui
   if (!obs::aligned(x, 16) || !obs::aligned(L->in_norm, 16) || !obs::aligned(L->q_w, 16) ||
       !obs::aligned(L->k_w, 16) || !obs::aligned(L->v_w, 16) || !obs::aligned(L->o_w, 16) ||
       !obs::aligned(L->q_norm, 4) || !obs::aligned(L->k_norm, 4) || !obs::aligned(k_cache, 16) ||
-      !obs::aligned(v_cache_t, 8))
-    return obs::set_error(ctx, OBS_E_ALIGN, "obs_attn_decode: weights, x and the key cache must be 16-byte aligned");
+      !obs::aligned(v_cache_t, 16))
+    return obs::set_error(ctx, OBS_E_ALIGN, "obs_attn_decode: weights, x and the caches must be 16-byte aligned");
   if (ctx->num_cus < static_cast<int>(ANWG))
     return obs::set_error(ctx, OBS_E_UNSUPPORTED, "obs_attn_decode: needs %u CUs (the device has %d)", ANWG,
                           ctx->num_cus);
