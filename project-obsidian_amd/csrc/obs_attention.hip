@@ -580,23 +580,33 @@ __global__ void __launch_bounds__(256, 2) sdpa_prefill_kernel(const uint16_t* __
       r[2 + h] = *reinterpret_cast<const u32x4_t*>(vb + static_cast<size_t>(c / 4u) * max_len + t0 + 8u * (c % 4u));
     }
   };
-  auto store_blk = [&](uint32_t buf, const u32x4_t* r) __attribute__((always_inline)) {
+  // Values at or past seq (the block past the workgroup's longest sequence) are
+  // stored as zero: their scores are masked, and the cache may hold anything there.
+  auto store_blk = [&](uint32_t buf, const u32x4_t* r, uint32_t blk) __attribute__((always_inline)) {
+    const bool tail = 32u * blk + 32u > seq;  // uniform
 #pragma unroll
     for (uint32_t h = 0; h < 2; ++h) {
       const uint32_t c = tid + 256u * h;
       *reinterpret_cast<u32x4_t*>(&s_blk[buf][(c / 16u) * PF_KROW + 8u * (c % 16u)]) = r[h];
+      u32x4_t v = r[2 + h];
+      if (tail) {
+        const uint32_t ta = 32u * blk + 8u * (c % 4u);  // positions ta .. ta + 7, two per word
+        auto m = [&](uint32_t w, uint32_t t) { return t >= seq ? 0u : (t + 1u >= seq ? (w & 0xffffu) : w); };
+        v = u32x4_t{m(v.x, ta), m(v.y, ta + 2u), m(v.z, ta + 4u), m(v.w, ta + 6u)};
+      }
       // a transposed value row of 32 positions is 4 chunks; rows are 72 bytes, so
       // each chunk is stored as two 8-byte halves (8-byte alignment)
       uint16_t* vr = &s_blk[buf][32u * PF_KROW + (c / 4u) * PF_VROW + 8u * (c % 4u)];
-      *reinterpret_cast<u32x2_t*>(vr) = u32x2_t{r[2 + h].x, r[2 + h].y};
-      *reinterpret_cast<u32x2_t*>(vr + 4) = u32x2_t{r[2 + h].z, r[2 + h].w};
+      *reinterpret_cast<u32x2_t*>(vr) = u32x2_t{v.x, v.y};
+      *reinterpret_cast<u32x2_t*>(vr + 4) = u32x2_t{v.z, v.w};
     }
   };
+  // A column's rescale by its correction factor is skipped while no column's
+  // maximum moved (the factor is then exactly 1).
   auto run_blk = [&](uint32_t buf, uint32_t blk) __attribute__((always_inline)) {
     const uint32_t t0 = 32u * blk;
     const uint16_t* sk = s_blk[buf];
     const uint16_t* sv = s_blk[buf] + 32u * PF_KROW;
-    const u32x4_t vm = value_masks(t0 + 4u * g, seq);
 #pragma unroll
     for (uint32_t cg = 0; cg < 2; ++cg) {
       f32x4_t sc[2];
@@ -626,29 +636,34 @@ __global__ void __launch_bounds__(256, 2) sdpa_prefill_kernel(const uint16_t* __
       // finite: block 0 holds position 0 of every column, so m_run is finite after it
       const float m_new = fmaxf(m_run[cg], bm);
       const float corr = __builtin_amdgcn_exp2f(m_run[cg] - m_new);
-      float p[8], psum = 0.0f;
+      // p rounded to bf16 (v_cvt_pk_bf16_f32, round to nearest even); the sum uses the rounded values
+      uint32_t pk[4];
+      float psum = 0.0f;
 #pragma unroll
-      for (uint32_t i = 0; i < 8; ++i) {
-        p[i] = bf16_to_f32(f32_to_bf16(__builtin_amdgcn_exp2f(svl[i] - m_new)));
-        psum += p[i];
+      for (uint32_t i = 0; i < 4; ++i) {
+        pk[i] = pack_bf16_pair_rne(__builtin_amdgcn_exp2f(svl[2 * i] - m_new),
+                                   __builtin_amdgcn_exp2f(svl[2 * i + 1] - m_new));
+        psum += __uint_as_float(pk[i] << 16);
+        psum += __uint_as_float(pk[i] & 0xffff0000u);
       }
       l_run[cg] = l_run[cg] * corr + psum;
       m_run[cg] = m_new;
-      float oc[4];
+      if (__any(corr != 1.0f)) {  // wave-uniform
+        float oc[4];
 #pragma unroll
-      for (uint32_t i = 0; i < 4; ++i) oc[i] = __shfl(corr, static_cast<int>(4u * g + i), 64);
-      const bf16x8_t pa = __builtin_bit_cast(
-          bf16x8_t, u32x4_t{pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]), pack_bf16x2(p[4], p[5]),
-                            pack_bf16x2(p[6], p[7])});
+        for (uint32_t i = 0; i < 4; ++i) oc[i] = __shfl(corr, static_cast<int>(4u * g + i), 64);
+#pragma unroll
+        for (uint32_t nt = 0; nt < 8; ++nt)
+#pragma unroll
+          for (uint32_t i = 0; i < 4; ++i) o[cg][nt][i] *= oc[i];
+      }
+      const bf16x8_t pa = __builtin_bit_cast(bf16x8_t, u32x4_t{pk[0], pk[1], pk[2], pk[3]});
 #pragma unroll
       for (uint32_t nt = 0; nt < 8; ++nt) {
         const uint16_t* vr = sv + (16u * nt + col) * PF_VROW + 4u * g;
         const u32x2_t v0 = *reinterpret_cast<const u32x2_t*>(vr);
         const u32x2_t v1 = *reinterpret_cast<const u32x2_t*>(vr + 16);
-        const bf16x8_t vbf =
-            __builtin_bit_cast(bf16x8_t, u32x4_t{v0.x & vm.x, v0.y & vm.y, v1.x & vm.z, v1.y & vm.w});
-#pragma unroll
-        for (uint32_t i = 0; i < 4; ++i) o[cg][nt][i] *= oc[i];
+        const bf16x8_t vbf = __builtin_bit_cast(bf16x8_t, u32x4_t{v0.x, v0.y, v1.x, v1.y});
         o[cg][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, vbf, o[cg][nt], 0, 0, 0);
       }
     }
@@ -660,17 +675,17 @@ __global__ void __launch_bounds__(256, 2) sdpa_prefill_kernel(const uint16_t* __
   u32x4_t sa[4], sb[4];
   load_blk(0u, sa);
   load_blk(min(1u, nblk - 1u), sb);
-  store_blk(0u, sa);
+  store_blk(0u, sa, 0u);
   __syncthreads();
   for (uint32_t blk = 0;;) {
     load_blk(min(blk + 2u, nblk - 1u), sa);
     run_blk(0u, blk);
-    store_blk(1u, sb);
+    store_blk(1u, sb, min(blk + 1u, nblk - 1u));
     __syncthreads();
     if (++blk >= nblk) break;
     load_blk(min(blk + 2u, nblk - 1u), sb);
     run_blk(1u, blk);
-    store_blk(0u, sa);
+    store_blk(0u, sa, min(blk + 1u, nblk - 1u));
     __syncthreads();
     if (++blk >= nblk) break;
   }

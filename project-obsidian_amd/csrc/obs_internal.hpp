@@ -7,6 +7,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <string>
+#include <type_traits>
 #include <vector>
 
 #include "../../include/obsidian_hip.h"
@@ -162,6 +163,14 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
 }
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
+}
+// The same pair with one v_cvt_pk_bf16_f32 (round to nearest even, as
+// f32_to_bf16 for every value that is not a NaN).
+__device__ __forceinline__ uint32_t pack_bf16_pair_rne(float lo, float hi) {
+  typedef __bf16 bf16x2_v __attribute__((ext_vector_type(2)));
+  typedef float f32x2_v __attribute__((ext_vector_type(2)));
+  const f32x2_v f = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2_v));
 }
 
 // exp(x) by Cody-Waite reduction with ln2 = HI + LO and a degree-7 Taylor

@@ -77,14 +77,8 @@ struct GemmArgs {
   uint32_t K, N;
 };
 
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-typedef float f32x2_t __attribute__((ext_vector_type(2)));
-
 // Two fp32 values -> one packed bf16 pair (RNE, v_cvt_pk_bf16_f32).
-__device__ __forceinline__ uint32_t pack_bf16_rne(float lo, float hi) {
-  const f32x2_t f = {lo, hi};
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2_t));
-}
+__device__ __forceinline__ uint32_t pack_bf16_rne(float lo, float hi) { return pack_bf16_pair_rne(lo, hi); }
 
 // fp32 fma(h, s, b) where h is the low (HI = 0) or high (HI = 1) f16 half of v
 // (v_fma_mix_f32: the f16 operand converts exactly to fp32 inside the fma).
