@@ -524,8 +524,7 @@ __global__ void __launch_bounds__(512) sdpa_combine_kernel(const float* __restri
 // tokens instead of once per TPG. The next block's loads are in flight while
 // a block is computed (registers, then the other LDS buffer). A column's
 // scores past its token's position are masked; values at or past the
-// workgroup's longest sequence read as zero. Workgroups of the latest tokens,
-// the longest sequences, are dispatched first.
+// workgroup's longest sequence read as zero.
 constexpr uint32_t PF_KROW = HD + 8u;  // padded key row (bf16): 272 bytes
 constexpr uint32_t PF_VROW = 32u + 4u; // padded transposed value row (bf16): 72 bytes
 constexpr uint32_t PF_BUF = 32u * PF_KROW + HD * PF_VROW;  // bf16 elements per staged block
@@ -540,7 +539,11 @@ __global__ void __launch_bounds__(256, 2) sdpa_prefill_kernel(const uint16_t* __
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   const uint32_t G = nh / nkv, TPG = 16u / G, TPWG = 8u * TPG;
   const uint32_t n_wg_tok = (n_tok + TPWG - 1u) / TPWG;
-  const uint32_t kv = blockIdx.x % nkv, tb = (n_wg_tok - 1u - blockIdx.x / nkv) * TPWG;  // first token
+  // tiles in launch order: the longer half of the tiles from the longest down,
+  // then the shorter half from the shortest up, so the two workgroups that
+  // share a CU tend to be a long and a short one
+  const uint32_t kv = blockIdx.x % nkv, r = blockIdx.x / nkv, half = (n_wg_tok + 1u) / 2u;
+  const uint32_t tb = (r < half ? n_wg_tok - 1u - r : r - half) * TPWG;  // first token
   const uint32_t col = lane & 15u, g = lane >> 4;
   const uint32_t cj = col / G, ci = col % G;
   const uint32_t seq = pos0 + min(tb + TPWG, n_tok);  // the workgroup's longest sequence
