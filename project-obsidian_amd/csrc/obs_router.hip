@@ -7,7 +7,8 @@
 // (token, expert row) one wave of 64 lanes; lane l owns the in/64 contiguous
 // columns [l*in/64, (l+1)*in/64) and accumulates acc = fma(w_c, x_c, acc) in
 // column order from 0; the lanes are combined by an xor butterfly with
-// offsets 32, 16, 8, 4, 2, 1.
+// offsets 1, 2, 4, ..., 32 (wave_sum_asc; the prefill kernel below adds the
+// same pairs in LDS).
 //
 // Selection (moe_routing_topk.metal:24-56): under the reference rule each
 // logit is first rounded to f16 (dequant_matvec_8bit.metal:30 stores halves);
@@ -33,7 +34,10 @@ constexpr int ROUTER_TOKENS_PER_WAVE = 8;
 // EPW rows dequantized in registers; the workgroup stages its 8 tokens'
 // activation rows in LDS once for its 4 waves. With one row per wave and no
 // staging every activation row was read from L2 once per expert (1 GB at
-// T = 2048), which bounded the launch.
+// T = 2048), which bounded the launch. Each lane's partial sum of every
+// (token, row) pair goes to LDS, and one thread per pair adds the 64 partials
+// in the butterfly's order: a wave reduction per pair (DPP steps and lane
+// reads, ~20 dependent instructions) had cost as much as the pair's fmas.
 template <int WPL, int EPW>
 __global__ void __launch_bounds__(256) q8_gate_logits_kernel(const uint32_t* __restrict__ w8,
                                                              const uint16_t* __restrict__ s,
@@ -43,6 +47,10 @@ __global__ void __launch_bounds__(256) q8_gate_logits_kernel(const uint32_t* __r
                                                              uint32_t in, uint32_t n_exp,
                                                              uint32_t group) {
   constexpr int C = 4 * WPL;  // columns per lane
+  // lane partials, 68 floats per pair: a thread's 16-byte reads of its pair hit
+  // distinct banks across 16 consecutive threads
+  constexpr uint32_t PART_STRIDE = 68;
+  __shared__ __attribute__((aligned(16))) float s_part[ROUTER_TOKENS_PER_WAVE * 4 * EPW * PART_STRIDE];
   extern __shared__ __attribute__((aligned(16))) uint16_t s_x[];  // [ROUTER_TOKENS_PER_WAVE][in]
   const uint32_t lane = threadIdx.x & 63;
   const uint32_t t0 = blockIdx.y * ROUTER_TOKENS_PER_WAVE;
@@ -54,8 +62,8 @@ __global__ void __launch_bounds__(256) q8_gate_logits_kernel(const uint32_t* __r
           *reinterpret_cast<const uint4*>(x + static_cast<uint64_t>(t0 + c / row_chunks) * in + 8u * (c % row_chunks));
   }
   __syncthreads();
-  const uint32_t e0 = (blockIdx.x * 4 + threadIdx.x / 64) * EPW;
-  if (e0 >= n_exp) return;  // wave-uniform; no barrier follows
+  const uint32_t wave = threadIdx.x / 64u;
+  const uint32_t e0 = (blockIdx.x * 4 + wave) * EPW;
   const uint32_t words = in / 4, groups = in / group;
   // dequantize this lane's C weights of each row once (exact: byte*scale has <= 16 bits)
   float wv[EPW][C];
@@ -75,25 +83,47 @@ __global__ void __launch_bounds__(256) q8_gate_logits_kernel(const uint32_t* __r
         wv[r][4 * j + q] = __builtin_fmaf(static_cast<float>((word >> (8 * q)) & 0xffu), sc, bi);
     }
   }
-  for (uint32_t t = t0; t < t0 + nt; ++t) {
-    const uint16_t* xr = s_x + (t - t0) * in + lane * C;
-    float xf[C];
+  // the lane partials (serial fma over the lane's columns) of every (token, row)
+  // pair go to LDS, pair-major
+  if (e0 < n_exp) {  // wave-uniform
+    for (uint32_t t = 0; t < nt; ++t) {
+      const uint16_t* xr = s_x + t * in + lane * C;
+      float xf[C];
 #pragma unroll
-    for (int c = 0; c < C; c += 8) {
-      const uint4 xv = *reinterpret_cast<const uint4*>(xr + c);
-      xf[c + 0] = bf16lo(xv.x); xf[c + 1] = bf16hi(xv.x); xf[c + 2] = bf16lo(xv.y); xf[c + 3] = bf16hi(xv.y);
-      xf[c + 4] = bf16lo(xv.z); xf[c + 5] = bf16hi(xv.z); xf[c + 6] = bf16lo(xv.w); xf[c + 7] = bf16hi(xv.w);
+      for (int c = 0; c < C; c += 8) {
+        const uint4 xv = *reinterpret_cast<const uint4*>(xr + c);
+        xf[c + 0] = bf16lo(xv.x); xf[c + 1] = bf16hi(xv.x); xf[c + 2] = bf16lo(xv.y); xf[c + 3] = bf16hi(xv.y);
+        xf[c + 4] = bf16lo(xv.z); xf[c + 5] = bf16hi(xv.z); xf[c + 6] = bf16lo(xv.w); xf[c + 7] = bf16hi(xv.w);
+      }
+#pragma unroll
+      for (int r = 0; r < EPW; ++r) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int c = 0; c < C; ++c) acc = __builtin_fmaf(wv[r][c], xf[c], acc);
+        s_part[((t * 4u + wave) * EPW + r) * PART_STRIDE + lane] = acc;
+      }
     }
-    float mine = 0.0f;  // lane r keeps row r's logit
+  }
+  __syncthreads();
+  // one thread per pair: its 64 lane partials summed in the xor-butterfly order
+  // (at step off, lane l adds lane l ^ off; lane 0's value is the sum over
+  // aligned blocks, pairwise in index order), as wave_sum_asc does in registers
+  const uint32_t pairs = nt * 4u * EPW;
+  for (uint32_t pr = threadIdx.x; pr < pairs; pr += 256u) {
+    const uint32_t r = pr % EPW, w = (pr / EPW) % 4u, t = pr / (4u * EPW);
+    const uint32_t e = (blockIdx.x * 4 + w) * EPW + r;
+    float v[64];
+    const float4* src = reinterpret_cast<const float4*>(s_part + pr * PART_STRIDE);
 #pragma unroll
-    for (int r = 0; r < EPW; ++r) {
-      float acc = 0.0f;
-#pragma unroll
-      for (int c = 0; c < C; ++c) acc = __builtin_fmaf(wv[r][c], xf[c], acc);
-      acc = wave_sum_asc(acc);
-      mine = lane == static_cast<uint32_t>(r) ? acc : mine;
+    for (int i = 0; i < 16; ++i) {
+      const float4 q = src[i];
+      v[4 * i] = q.x; v[4 * i + 1] = q.y; v[4 * i + 2] = q.z; v[4 * i + 3] = q.w;
     }
-    if (lane < static_cast<uint32_t>(EPW) && e0 + lane < n_exp) logits[static_cast<uint64_t>(t) * n_exp + e0 + lane] = mine;
+#pragma unroll
+    for (int off = 1; off < 64; off *= 2)
+#pragma unroll
+      for (int l = 0; l < 64; l += 2 * off) v[l] = v[l] + v[l + off];
+    if (e < n_exp) logits[static_cast<uint64_t>(t0 + t) * n_exp + e] = v[0];
   }
 }
 

@@ -92,6 +92,22 @@ def test_q8_gate_logits_bit_exact(exe, T):
         assert np.array_equal(got[t].view(np.uint32), ref.view(np.uint32)), f"token {t}"
 
 
+@pytest.mark.parametrize("H,E,T", [(512, 60, 9), (1024, 128, 17), (4096, 256, 11), (4096, 37, 3)])
+def test_q8_gate_logits_other_widths_bit_exact(exe, H, E, T):
+    """The router kernel's other row widths (4, 16 or 64 columns per lane) and
+    expert counts that leave a workgroup's rows partly past the last expert."""
+    rng = np.random.default_rng(310 + H + E)
+    w, s, b = synth.quant_tensor(rng, E, H, 8, 64)
+    x = synth.bf16_normal(rng, (T, H))
+    lg = exe.alloc((T, E), np.float32)
+    exe.q8_gate_logits(exe.upload(w), exe.upload(s), exe.upload(b), exe.upload(x), lg, T, H, E, 64)
+    got = lg.download()
+    xf = _f32(x)
+    for t in range(T):
+        ref = O.qmatvec("lanes", 8, w, s, b, xf[t], H, E, lanes=64)
+        assert np.array_equal(got[t].view(np.uint32), ref.view(np.uint32)), f"token {t}"
+
+
 @pytest.mark.parametrize("rule", [O.ROUTE_REF, O.ROUTE_F32], ids=["ref", "f32"])
 @pytest.mark.parametrize("n_exp,k,norm", [(128, 8, True), (128, 8, False), (64, 4, True), (256, 8, True),
                                           (100, 7, True), (16, 16, True), (128, 1, True)])
