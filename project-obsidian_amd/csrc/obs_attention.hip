@@ -209,7 +209,12 @@ __global__ void __launch_bounds__(256) q4_gemv_kernel(const uint16_t* __restrict
 // other load). ROWS = true (prefill; cosines and sines from the context's
 // RoPE table, the same values): one workgroup per token of q (rows of
 // q_ld elements holding nh x 128), k, v (rows of kv_ld holding nkv x 128) at
-// position pos0 + token; wave w owns heads w, w + 4, ...
+// position pos0 + token; wave w owns heads w, w + 4, ... of the query and key
+// heads. The value heads go through LDS instead: workgroups n_tok.. each take
+// (kv head, 64 consecutive tokens), read the 64 value rows and write each of
+// the 128 transposed cache rows as one 128-byte run (a 2-byte store per
+// token and dim, from the token's workgroup, cost as much as the rest).
+constexpr uint32_t PREP_VTOK = 64;  // tokens per value-transposing workgroup
 template <bool ROWS>
 __global__ void __launch_bounds__(256) attn_prep_kernel(uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
                                                         const uint16_t* __restrict__ v,
@@ -221,7 +226,28 @@ __global__ void __launch_bounds__(256) attn_prep_kernel(uint16_t* __restrict__ q
                                                         uint32_t n_tok, uint32_t q_ld, uint32_t kv_ld,
                                                         const float* __restrict__ rope) {
   const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-  const uint32_t heads = nh + 2u * nkv;
+  if (ROWS && blockIdx.x >= n_tok) {  // uniform: a value-transposing workgroup
+    __shared__ uint32_t s_v[PREP_VTOK][HD / 2 + 1];  // token rows of dim pairs (+1 word: bank spread)
+    const uint32_t vi = blockIdx.x - n_tok, kvh = vi % nkv, t0 = (vi / nkv) * PREP_VTOK;
+    const uint32_t nt = min(PREP_VTOK, n_tok - t0);
+#pragma unroll
+    for (uint32_t i = 0; i < PREP_VTOK * HD / 2u / 256u; ++i) {
+      const uint32_t idx = threadIdx.x + 256u * i, tt = idx / (HD / 2u), dp = idx % (HD / 2u);
+      if (tt < nt)
+        s_v[tt][dp] = *reinterpret_cast<const uint32_t*>(v + static_cast<size_t>(t0 + tt) * kv_ld + kvh * HD + 2u * dp);
+    }
+    __syncthreads();
+    const uint32_t tt = threadIdx.x % PREP_VTOK;  // lanes: consecutive positions of one dim
+    if (tt < nt) {
+      uint16_t* dst = v_cache_t + static_cast<size_t>(kvh) * HD * max_len + pos0 + t0 + tt;
+      for (uint32_t d = threadIdx.x / PREP_VTOK; d < HD; d += 256u / PREP_VTOK) {
+        const uint32_t wd = s_v[tt][d / 2u];
+        dst[static_cast<size_t>(d) * max_len] = static_cast<uint16_t>((d & 1u) ? wd >> 16 : wd & 0xffffu);
+      }
+    }
+    return;
+  }
+  const uint32_t heads = ROWS ? nh + nkv : nh + 2u * nkv;  // with ROWS the value heads are transposed above
   const uint32_t tok = ROWS ? blockIdx.x : 0u;
   const uint32_t h_first = ROWS ? wave : blockIdx.x * 4u + wave, h_step = ROWS ? 4u : heads;
   if (tok >= n_tok || h_first >= heads) return;  // wave-uniform
@@ -993,7 +1019,9 @@ int obs_attn_prep_rows(obs_ctx* ctx, uint16_t* q, const uint16_t* k, const uint1
   const float* rope = nullptr;
   const int rc = obs::ensure_rope_table(ctx, theta, max_len, &rope);
   if (rc != OBS_OK) return rc;
-  OBS_LAUNCH(ctx, "attn_prep_rows", attn_prep_kernel<true><<<n_tokens, 256, 0,
+  const uint64_t grid = static_cast<uint64_t>(n_tokens) + static_cast<uint64_t>(n_kv) * ((n_tokens + PREP_VTOK - 1u) / PREP_VTOK);
+  if (grid > 0x7fffffffull) return obs::set_error(ctx, OBS_E_SHAPE, "obs_attn_prep_rows: too many tokens");
+  OBS_LAUNCH(ctx, "attn_prep_rows", attn_prep_kernel<true><<<static_cast<uint32_t>(grid), 256, 0,
                                                               ctx->stream>>>(q, k, v, q_norm, k_norm, k_cache, v_cache_t,
                                                                              n_heads, n_kv, max_len, eps, theta, nullptr,
                                                                              pos0, n_tokens, q_ld, kv_ld, rope));

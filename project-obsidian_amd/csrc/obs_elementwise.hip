@@ -20,6 +20,20 @@ __global__ void __launch_bounds__(256) scaled_add_kernel(uint16_t* __restrict__ 
   const uint32_t i = blockIdx.x * 256 + threadIdx.x;
   if (i < n) acc[i] = f32_to_bf16(__builtin_fmaf(scale, bf16_to_f32(y[i]), bf16_to_f32(acc[i])));
 }
+// The same, 8 elements (16 bytes) per thread: both arrays 16-byte aligned, n8 = n / 8.
+__global__ void __launch_bounds__(256) scaled_add8_kernel(uint16_t* __restrict__ acc, const uint16_t* __restrict__ y,
+                                                          float scale, uint32_t n8) {
+  const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= n8) return;
+  const uint4 a = reinterpret_cast<const uint4*>(acc)[i], b = reinterpret_cast<const uint4*>(y)[i];
+  const uint32_t aw[4] = {a.x, a.y, a.z, a.w}, bw[4] = {b.x, b.y, b.z, b.w};
+  uint32_t o[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    o[j] = pack_bf16x2(__builtin_fmaf(scale, bf16lo(bw[j]), bf16lo(aw[j])),
+                       __builtin_fmaf(scale, bf16hi(bw[j]), bf16hi(aw[j])));
+  reinterpret_cast<uint4*>(acc)[i] = make_uint4(o[0], o[1], o[2], o[3]);
+}
 // One wave per row; lane l owns the dim/64 contiguous columns [l*c, (l+1)*c).
 // sum(x^2): serial fma over the lane's columns, then wave_sum_asc (the xor
 // butterfly 1..32); inv = 1/sqrt(sum/dim + eps) with IEEE sqrt and division
@@ -35,9 +49,11 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(const uint16_t* x, const u
   const uint16_t* xr = x + static_cast<size_t>(row) * dim + c0;
   uint16_t* orow = out + static_cast<size_t>(row) * dim + c0;
   if constexpr (C != 0) {
-    uint4 xv[C / 8];
+    uint4 xv[C / 8], wv[C / 8];  // the weights load with x: no second round trip after the reduction
 #pragma unroll
     for (uint32_t i = 0; i < C / 8; ++i) xv[i] = reinterpret_cast<const uint4*>(xr)[i];
+#pragma unroll
+    for (uint32_t i = 0; i < C / 8; ++i) wv[i] = reinterpret_cast<const uint4*>(w + c0)[i];
     float acc = 0.0f;
 #pragma unroll
     for (uint32_t i = 0; i < C / 8; ++i) {
@@ -52,8 +68,7 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(const uint16_t* x, const u
     const float inv = 1.0f / __builtin_sqrtf(wave_sum_asc(acc) / static_cast<float>(dim) + eps);
 #pragma unroll
     for (uint32_t i = 0; i < C / 8; ++i) {
-      const uint4 wv = reinterpret_cast<const uint4*>(w + c0)[i];
-      const uint32_t xd[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w}, wdd[4] = {wv.x, wv.y, wv.z, wv.w};
+      const uint32_t xd[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w}, wdd[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
       uint32_t o[4];
 #pragma unroll
       for (uint32_t j = 0; j < 4; ++j)
@@ -115,7 +130,12 @@ int obs_scaled_add(obs_ctx* ctx, uint16_t* acc, const uint16_t* y, float scale, 
   if (!ctx) return OBS_E_INVALID;
   if (!acc || !y) return obs::set_error(ctx, OBS_E_INVALID, "obs_scaled_add: null pointer");
   if (n == 0) return OBS_OK;
-  OBS_LAUNCH(ctx, "scaled_add", scaled_add_kernel<<<(n + 255) / 256, 256, 0, ctx->stream>>>(acc, y, scale, n));
+  if (n % 8u == 0 && obs::aligned(acc, 16) && obs::aligned(y, 16)) {
+    const uint32_t n8 = n / 8u;
+    OBS_LAUNCH(ctx, "scaled_add", scaled_add8_kernel<<<(n8 + 255) / 256, 256, 0, ctx->stream>>>(acc, y, scale, n8));
+  } else {
+    OBS_LAUNCH(ctx, "scaled_add", scaled_add_kernel<<<(n + 255) / 256, 256, 0, ctx->stream>>>(acc, y, scale, n));
+  }
   return OBS_OK;
 }
 

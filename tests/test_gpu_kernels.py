@@ -173,12 +173,13 @@ def test_swiglu_and_scaled_add(exe):
     exe.swiglu_raw(exe.upload(g), exe.upload(u), h, n)
     ref = np.array([O.f32_to_bf16(O.silu_mul(float(a), float(c))) for a, c in zip(_f32(g), _f32(u))], np.uint16)
     assert np.array_equal(h.download(), ref)
-    acc = synth.bf16_normal(rng, n)
-    y = synth.bf16_normal(rng, n)
-    da = exe.upload(acc)
-    exe.scaled_add_raw(da, exe.upload(y), 0.37, n)
-    exact = np.float32(0.37).astype(np.float64) * _f32(y).astype(np.float64) + _f32(acc).astype(np.float64)
-    assert np.array_equal(da.download(), synth.f32_to_bf16_bits(exact.astype(np.float32)))
+    for m in (n, 1001):  # 16-byte vector path, then the one-element path (n % 8 != 0)
+        acc = synth.bf16_normal(rng, m)
+        y = synth.bf16_normal(rng, m)
+        da = exe.upload(acc)
+        exe.scaled_add_raw(da, exe.upload(y), 0.37, m)
+        exact = np.float32(0.37).astype(np.float64) * _f32(y).astype(np.float64) + _f32(acc).astype(np.float64)
+        assert np.array_equal(da.download(), synth.f32_to_bf16_bits(exact.astype(np.float32))), m
 
 
 @pytest.mark.parametrize("rows,dim", [(1, 2048), (7, 2048), (300, 2048), (5, 1024), (3, 4096), (4, 192)])

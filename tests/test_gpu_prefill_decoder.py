@@ -40,7 +40,7 @@ def test_embed_q4_rows_bit_exact(exe):
         assert np.array_equal(got[i], want), i
 
 
-@pytest.mark.parametrize("pos0,T", [(0, 1), (0, 7), (100, 33), (4000, 96)])
+@pytest.mark.parametrize("pos0,T", [(0, 1), (0, 7), (100, 33), (4000, 96), (3, 130), (4001, 95)])
 def test_attn_prep_rows_vs_oracle(exe, pos0, T):
     nh, nkv, hd, ml = 32, 4, 128, 4096
     rng = np.random.default_rng(1200 + T)
