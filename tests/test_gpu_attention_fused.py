@@ -67,7 +67,9 @@ def _separate(exe, d, x, kc, vc, state):
     return x1
 
 
-@pytest.mark.parametrize("pos", [0, 1, 33, 1000, 4063, 4095])
+# positions 0..7 put the new token in each of the four value words a lane
+# splices (and keep the context short enough that a wrong splice shows)
+@pytest.mark.parametrize("pos", [0, 1, 2, 4, 6, 7, 33, 1000, 4063, 4095])
 def test_attn_decode_vs_oracle_and_separate_launches(exe, layer, pos):
     t, d, kc0, vc0 = layer
     rng = np.random.default_rng(2100 + pos)
