@@ -20,9 +20,10 @@
 //      logits; wave 0 of every workgroup runs softmax + top-8 on them and
 //      shares the result through LDS.
 //   2. Group g serves routing rank g: expert e_g = ids[g]. Its 128 waves stream
-//      the 768 gate and up rows (6 each) and, at the same time, the down rows the
-//      workgroup will need (64 rows x 384 B per workgroup), so the down weights
-//      arrive during the gate/up phase.
+//      the 768 gate and up rows (6 each) and, at the same time, the first third
+//      of the down rows the workgroup will need (64 rows x 384 B per workgroup);
+//      the other two thirds are issued once the first block of h is in (below),
+//      so they do not compete with the gate/up rows.
 //   3. h = silu(gate.x) * (up.x) goes to the group's h slots; each workgroup
 //      polls them into LDS in three blocks, adding each block's terms to its 64
 //      down rows as the block arrives (the down weights are in registers).
@@ -291,7 +292,7 @@ __global__ void __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 
   const bool have = ok && eg >= 0 && static_cast<uint32_t>(eg) < n_exp;
   OBS_FUSED_MARK(3);
 
-  // ---- 3. issue every weight load this wave needs: 6 gate + 6 up rows, 2x3 down blocks.
+  // ---- 3. issue the weight loads: 6 gate + 6 up rows, the first of 3 down blocks (x2).
   // Wide loads only: each gate/up row is one coalesced 1 KB load; the down rows
   // are read a 128-byte line per 8 lanes (lane (r8, m) takes bytes
   // [128L + 16m, +16) of row r8, L = 0..2: columns [256L + 32m, +32)); the
@@ -300,6 +301,7 @@ __global__ void __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 
   // through the wave's own LDS area, not one 2-byte load per value.
   uint4 gq[GU_ROWS], uq[GU_ROWS];
   uint4 dq[2][3];
+  const uint4* dpp[2];
   const uint32_t m = lane & 7u;   // down: 16-byte chunk within each 128-byte line
   const uint32_t r8 = lane >> 3;  // down: row within an 8-row pass
   const uint32_t dn_row0 = DN_ROWS_WG * j + 16u * wave;  // the wave's 16 down rows
@@ -336,9 +338,8 @@ __global__ void __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 
 #pragma unroll
     for (uint32_t p = 0; p < 2; ++p) {
       const size_t row = size_t(el) * FH + dn_row0 + 8u * p + r8;
-      const uint4* dp = reinterpret_cast<const uint4*>(a.down_w + row * (FI / 8)) + m;
-#pragma unroll
-      for (uint32_t L = 0; L < 3; ++L) dq[p][L] = dp[8u * L];
+      dpp[p] = reinterpret_cast<const uint4*>(a.down_w + row * (FI / 8)) + m;
+      dq[p][0] = dpp[p][0];
     }
   }
   // the wave's staged scales: gate/up segment sg = 4t + {gate_s, gate_b, up_s,
@@ -418,7 +419,18 @@ __global__ void __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 
         }
       }
       __syncthreads();
-      if (L == 0) OBS_FUSED_MARK(6);
+      if (L == 0) {
+        OBS_FUSED_MARK(6);
+        // the down rows' other two blocks, now: issued with the gate/up rows they
+        // competed with them (the median workgroup stored h ~0.8 us later), and
+        // issued before this first poll the poll would have waited for their
+        // data (a wave's loads complete in issue order); 14.23 -> 13.93 us
+#pragma unroll
+        for (uint32_t p = 0; p < 2; ++p) {
+          dq[p][1] = dpp[p][8];
+          dq[p][2] = dpp[p][16];
+        }
+      }
       // the lane's columns of block L: [256L + 32m, +32)
       f16x2_t hp[16];
 #pragma unroll
