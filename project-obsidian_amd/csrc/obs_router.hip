@@ -7,8 +7,8 @@
 // (token, expert row) one wave of 64 lanes; lane l owns the in/64 contiguous
 // columns [l*in/64, (l+1)*in/64) and accumulates acc = fma(w_c, x_c, acc) in
 // column order from 0; the lanes are combined by an xor butterfly with
-// offsets 1, 2, 4, ..., 32 (wave_sum_asc; the prefill kernel below adds the
-// same pairs in LDS).
+// offsets 1, 2, 4, ..., 32 (wave_sum_asc in the decode kernels;
+// q8_gate_logits_kernel below adds the same pairs in LDS).
 //
 // Selection (moe_routing_topk.metal:24-56): under the reference rule each
 // logit is first rounded to f16 (dequant_matvec_8bit.metal:30 stores halves);
