@@ -655,7 +655,7 @@ __global__ void __launch_bounds__(256, 2) sdpa_prefill_kernel(const uint16_t* __
 #pragma unroll
         for (uint32_t i = 0; i < 4; ++i) {
           const uint32_t t = t0 + 16u * tt + 4u * g + i;
-          svl[4 * tt + i] = t < lim[cg] ? sc[tt][i] * scale_log2 : -__builtin_huge_valf();
+          svl[4 * tt + i] = t < lim[cg] ? sc[tt][i] : -__builtin_huge_valf();
         }
       float bm = svl[0];
 #pragma unroll
@@ -663,17 +663,21 @@ __global__ void __launch_bounds__(256, 2) sdpa_prefill_kernel(const uint16_t* __
       bm = fmaxf(bm, shfl_xor_f(bm, 16));
       bm = fmaxf(bm, shfl_xor_f(bm, 32));
       // finite: block 0 holds position 0 of every column, so m_run is finite after it
-      const float m_new = fmaxf(m_run[cg], bm);
+      const float m_new = fmaxf(m_run[cg], bm * scale_log2);
       const float corr = __builtin_amdgcn_exp2f(m_run[cg] - m_new);
-      // p rounded to bf16 (v_cvt_pk_bf16_f32, round to nearest even); the sum uses the rounded values
+      // p = 2^(s * scale - m), the scale folded into one fma (the maximum is taken
+      // over the unscaled scores: scaling by a positive factor keeps their
+      // order), rounded to bf16 (v_cvt_pk_bf16_f32, round to nearest even); the
+      // row sum adds the rounded pairs with v_dot2c_f32_bf16 against (1, 1)
+      typedef __bf16 bf16x2_v __attribute__((ext_vector_type(2)));
+      const bf16x2_v ones2 = __builtin_bit_cast(bf16x2_v, 0x3f803f80u);
       uint32_t pk[4];
       float psum = 0.0f;
 #pragma unroll
       for (uint32_t i = 0; i < 4; ++i) {
-        pk[i] = pack_bf16_pair_rne(__builtin_amdgcn_exp2f(svl[2 * i] - m_new),
-                                   __builtin_amdgcn_exp2f(svl[2 * i + 1] - m_new));
-        psum += __uint_as_float(pk[i] << 16);
-        psum += __uint_as_float(pk[i] & 0xffff0000u);
+        pk[i] = pack_bf16_pair_rne(__builtin_amdgcn_exp2f(__builtin_fmaf(svl[2 * i], scale_log2, -m_new)),
+                                   __builtin_amdgcn_exp2f(__builtin_fmaf(svl[2 * i + 1], scale_log2, -m_new)));
+        psum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_v, pk[i]), ones2, psum, false);
       }
       l_run[cg] = l_run[cg] * corr + psum;
       m_run[cg] = m_new;
