@@ -114,3 +114,21 @@ def test_attn_decode_consecutive_launches(exe, layer):
         _close(_f(x1.download()), _f(x1_s.download()))
     assert np.array_equal(kc_f.download(), kc_s.download()) and np.array_equal(vc_f.download(), vc_s.download())
     exe.device_status()  # raises if a cross-workgroup wait timed out
+
+
+def test_attn_decode_rejects_misaligned_caches(exe, layer):
+    """Each lane reads its 8 value positions as one 16-byte load, so a value
+    cache (or key cache, or x) off a 16-byte boundary is refused before any
+    launch, and nothing is written."""
+    import obsidian_hip as oh
+    t, d, kc0, vc0 = layer
+    vt0 = np.ascontiguousarray(vc0.transpose(0, 2, 1))
+    kc, vc = exe.upload(kc0), exe.upload(vt0)
+    x = exe.upload(synth.bf16_normal(np.random.default_rng(2300), H, 0.5))
+    state = exe.upload(np.array([100, 0], np.int32))
+    x1 = exe.alloc(H, np.uint16)
+    for args in ((x, kc, vc.ptr + 8), (x, kc.ptr + 8, vc), (x.ptr + 8, kc, vc)):
+        with pytest.raises(oh.ObsError) as ei:
+            exe.attn_decode(d, args[0], args[1], args[2], ML, EPS, THETA, state, x1)
+        assert ei.value.code == oh.OBS_E_ALIGN
+    assert np.array_equal(kc.download(), kc0) and np.array_equal(vc.download(), vt0)
