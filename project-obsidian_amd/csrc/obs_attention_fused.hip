@@ -73,6 +73,7 @@ constexpr uint32_t A_PART = AQPG * (AHD + 2);    // a split's partial: 4 heads x
 constexpr uint32_t A_ORWG = AH / AWPG;           // W_o rows per workgroup: 64
 constexpr uint32_t A_ORW = A_ORWG / 4;           // per wave: 16, in two passes of 8 (8 lanes per row)
 static_assert(A_RPW * AWPG * 4 == AGR && A_CDIM * AWPG == AGQD && AQPG * ANGRP == ANH, "shape");
+static_assert(A_RPW == 6, "the q/k/v rows of a wave are reduced six at a time");
 
 constexpr size_t AW_COUNT = 0, AW_ERR = 256;
 constexpr size_t AW_QKV = 1024;                                              // [8][768] slots
@@ -270,7 +271,7 @@ attn_fused_kernel(AttnArgs a) {
     float xoff = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) xoff = dot8_off_only(xh + 4 * i, xoff);
-    float mine = 0.0f;  // lane k keeps row k
+    float part[A_RPW];
 #pragma unroll
     for (uint32_t k = 0; k < A_RPW; ++k) {
       float acc = 0.0f;
@@ -278,10 +279,12 @@ attn_fused_kernel(AttnArgs a) {
       acc = dot8_q4_off(rq[k].y, xh + 4, acc);
       acc = dot8_q4_off(rq[k].z, xh + 8, acc);
       acc = dot8_q4_off(rq[k].w, xh + 12, acc);
-      float part = __builtin_fmaf(bf16_to_f32(rsc[k]), acc - xoff, bf16_to_f32(rbi[k]) * xs);
-      part = wave_sum_asc(part);
-      mine = lane == k ? bf16_to_f32(f32_to_bf16(part)) : mine;
+      part[k] = __builtin_fmaf(bf16_to_f32(rsc[k]), acc - xoff, bf16_to_f32(rbi[k]) * xs);
     }
+    // the six 64-lane sums in wave_sum_asc's order (bit-identical to the
+    // per-head launches), row my_row in lane l < 8
+    const float mine = bf16_to_f32(f32_to_bf16(wave_sum6_scatter(part, lane)));
+    const int my_row = lane < 8u ? row6_of_lane(lane) : -1;
     // the epoch is needed from the first publish on: the barrier sits here,
     // after the rows' wait, not before the compute
     if (tid == 0) {
@@ -294,7 +297,7 @@ attn_fused_kernel(AttnArgs a) {
       if (tid == 0) __hip_atomic_fetch_add(ctl_count, uint64_t{1}, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       return;
     }
-    if (lane < A_RPW) slot_store_xcd(qkv_slots + A_RPW * wl + lane, s_epoch, mine);  // polled by this XCD only
+    if (my_row >= 0) slot_store_xcd(qkv_slots + A_RPW * wl + my_row, s_epoch, mine);  // polled by this XCD only
   }
   // the o rows of this wave: rows 64 j + 16 wave + 8 p + lane / 8, the lane's
   // 64 of the group's 512 columns (the quantization group 2 hq0 + lane % 8);

@@ -84,6 +84,59 @@ __device__ __forceinline__ void raise_error(unsigned char* ws) {
   __hip_atomic_store(reinterpret_cast<uint32_t*>(ws + WS_ERR), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
+// Gate/up rows whose lane partials are reduced together.
+#ifndef GU_BATCH_ROWS
+#define GU_BATCH_ROWS 2
+#endif
+constexpr uint32_t GU_BATCH = GU_BATCH_ROWS;
+static_assert(GU_BATCH == 2 || GU_BATCH == 6, "batches of 2 or 6 rows");
+
+// The 64-lane sums of a wave's lane partials of R gate rows (pg) and R up rows
+// (pu), reduced together, and silu(gate) * up of each row. Instead of a full
+// butterfly per value (12 of them cost ~150 instructions plus their DPP
+// hazards, and each row's silu), the values are reduce-scattered over the
+// lanes of a 16-lane row: at each step two lanes that hold the same set of
+// values split it, each keeping half and adding its partner's copy of that
+// half, until every lane of the row holds the row's sum of one value. The
+// pairings are the row mirror (lane bit 3 splits gate from up), the half-row
+// mirror (bit 2) and the quad xors (bits 1, 0); lanes paired at one step agree
+// in every bit split before. An xor by 16 and a swap of the wave's halves then
+// add the four rows. Gate row r ends up in a lane with bit 3 clear and its up
+// row 8 lanes higher, so one row rotation brings them together; `row` is the
+// batch row a lane of 0..7 holds (-1 for the other lanes, and for padding).
+// Rows: R = 2: lanes 0, 4 -> rows 0, 1. R = 6: lane bits 2..0 = 000 -> 0,
+// 001 -> 2, 010 -> 1, 100 -> 3, 101 -> 5, 110 -> 4, 011 and 111 padding.
+template <uint32_t R>
+__device__ __forceinline__ float gateup_reduce(const float (&pg)[R], const float (&pu)[R], uint32_t lane, int& row) {
+  const bool s1 = (lane & 8u) != 0u, s2 = (lane & 4u) != 0u;
+  float a[R];
+#pragma unroll
+  for (uint32_t i = 0; i < R; ++i) a[i] = (s1 ? pu[i] : pg[i]) + dpp_f32<DPP_MIRROR>(s1 ? pg[i] : pu[i]);
+  float d;
+  if constexpr (R == 2) {
+    d = (s2 ? a[1] : a[0]) + dpp_f32<DPP_HALF_MIRROR>(s2 ? a[0] : a[1]);
+    d = d + dpp_f32<DPP_XOR2>(d);
+    d = d + dpp_f32<DPP_XOR1>(d);
+    row = lane < 8u && (lane & 3u) == 0u ? (s2 ? 1 : 0) : -1;
+  } else {
+    const bool s3 = (lane & 2u) != 0u, s4 = (lane & 1u) != 0u;
+    float b[3];
+#pragma unroll
+    for (uint32_t i = 0; i < 3; ++i) b[i] = (s2 ? a[3 + i] : a[i]) + dpp_f32<DPP_HALF_MIRROR>(s2 ? a[i] : a[3 + i]);
+    const float c0 = (s3 ? b[1] : b[0]) + dpp_f32<DPP_XOR2>(s3 ? b[0] : b[1]);
+    const float c1 = (s3 ? 0.0f : b[2]) + dpp_f32<DPP_XOR2>(s3 ? b[2] : 0.0f);
+    d = (s4 ? c1 : c0) + dpp_f32<DPP_XOR1>(s4 ? c0 : c1);
+    const int i = s4 ? (s3 ? -1 : 2) : (s3 ? 1 : 0);
+    row = lane < 8u && i >= 0 ? (s2 ? 3 : 0) + i : -1;
+  }
+  d = d + __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(d), 0x401F));  // lanes i, i ^ 16
+  {
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(d), __float_as_uint(d), false, false);
+    d = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);  // lanes i, i ^ 32
+  }
+  return silu_mul(d, dpp_f32<DPP_ROW_ROR8>(d));
+}
+
 __device__ __forceinline__ void unpack_bf16x8(const uint4& v, float* f) {
   f[0] = bf16lo(v.x); f[1] = bf16hi(v.x); f[2] = bf16lo(v.y); f[3] = bf16hi(v.y);
   f[4] = bf16lo(v.z); f[5] = bf16hi(v.z); f[6] = bf16lo(v.w); f[7] = bf16hi(v.w);
@@ -354,26 +407,31 @@ __global__ void __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 
     sc[64u + lane] = scq1;  // chunks 96..127: padding
   }
 #pragma unroll
-  for (uint32_t t = 0; t < GU_ROWS; ++t) {
-    float pg = 0.0f, pu = 0.0f;
-    if (have) {
-      float ag = 0.0f, au = 0.0f;
-      ag = dot8_q4_off(gq[t].x, xh + 0, ag);
-      ag = dot8_q4_off(gq[t].y, xh + 4, ag);
-      ag = dot8_q4_off(gq[t].z, xh + 8, ag);
-      ag = dot8_q4_off(gq[t].w, xh + 12, ag);
-      au = dot8_q4_off(uq[t].x, xh + 0, au);
-      au = dot8_q4_off(uq[t].y, xh + 4, au);
-      au = dot8_q4_off(uq[t].z, xh + 8, au);
-      au = dot8_q4_off(uq[t].w, xh + 12, au);
-      const uint16_t* sg = sc16 + 128u * t + lane / 2u;  // this lane's group of row t
-      pg = __builtin_fmaf(bf16_to_f32(sg[0]), ag - xoff, bf16_to_f32(sg[32]) * xs);
-      pu = __builtin_fmaf(bf16_to_f32(sg[64]), au - xoff, bf16_to_f32(sg[96]) * xs);
+  for (uint32_t t0 = 0; t0 < GU_ROWS; t0 += GU_BATCH) {
+    float pg[GU_BATCH], pu[GU_BATCH];
+#pragma unroll
+    for (uint32_t i = 0; i < GU_BATCH; ++i) {
+      const uint32_t t = t0 + i;
+      pg[i] = 0.0f;
+      pu[i] = 0.0f;
+      if (have) {
+        float ag = 0.0f, au = 0.0f;
+        ag = dot8_q4_off(gq[t].x, xh + 0, ag);
+        ag = dot8_q4_off(gq[t].y, xh + 4, ag);
+        ag = dot8_q4_off(gq[t].z, xh + 8, ag);
+        ag = dot8_q4_off(gq[t].w, xh + 12, ag);
+        au = dot8_q4_off(uq[t].x, xh + 0, au);
+        au = dot8_q4_off(uq[t].y, xh + 4, au);
+        au = dot8_q4_off(uq[t].z, xh + 8, au);
+        au = dot8_q4_off(uq[t].w, xh + 12, au);
+        const uint16_t* sg = sc16 + 128u * t + lane / 2u;  // this lane's group of row t
+        pg[i] = __builtin_fmaf(bf16_to_f32(sg[0]), ag - xoff, bf16_to_f32(sg[32]) * xs);
+        pu[i] = __builtin_fmaf(bf16_to_f32(sg[64]), au - xoff, bf16_to_f32(sg[96]) * xs);
+      }
     }
-    pg = wave_sum_asc(pg);
-    pu = wave_sum_asc(pu);
-    const float hv = have ? silu_mul(pg, pu) : 0.0f;
-    if (lane == 0) slot_store_xcd(h_slots + e0 + 128u * t, epoch, hv);  // polled by this XCD only
+    int row;
+    const float hv = gateup_reduce<GU_BATCH>(pg, pu, lane, row);  // silu(0) * 0 = 0 without an expert
+    if (row >= 0) slot_store_xcd(h_slots + e0 + 128u * (t0 + row), epoch, hv);  // polled by this XCD only
   }
 
   OBS_FUSED_MARK(5);

@@ -268,6 +268,45 @@ __device__ __forceinline__ float wave_sum_asc(float v) {
   return (r0 + r1) + (r2 + r3);
 }
 
+constexpr int DPP_ROW_SHL4 = 0x104;  // lane i <- lane i + 4 within the row
+constexpr int DPP_ROW_SHR4 = 0x114;  // lane i <- lane i - 4 within the row
+constexpr int DPP_ROW_ROR8 = 0x128;  // lane i <- lane (i + 8) mod 16 within the row: an xor by 8
+
+// Lane i ^ 4's value on any data (the half-row mirror pairs the same lanes
+// only on quad-uniform data): banks 0 and 2 of each row (lanes 0-3, 8-11)
+// read 4 lanes up, banks 1 and 3 read 4 lanes down.
+__device__ __forceinline__ float dpp_xor4_f32(float v) {
+  int r = __builtin_amdgcn_update_dpp(0, __float_as_int(v), DPP_ROW_SHL4, 0xF, 0x5, false);
+  r = __builtin_amdgcn_update_dpp(r, __float_as_int(v), DPP_ROW_SHR4, 0xF, 0xA, false);
+  return __int_as_float(r);
+}
+
+// The wave_sum_asc of six values at once, bit for bit: the same pairs are
+// added in the same order (xor 1, 2, 4, 8 within a row, then the four row sums
+// as (r0 + r1) + (r2 + r3)), but at the first three steps the two lanes of a
+// pair split the values they hold (each keeps half and adds its partner's
+// copy of that half) instead of both adding all of them: 3 + 2 + 1 + 1 + 1 + 1
+// additions per lane instead of 6 x 6, and no scalar reads. Lane l < 8 returns
+// the sum of value row6_of_lane(l) (lanes 6 and 7 hold padding).
+__device__ __forceinline__ int row6_of_lane(uint32_t lane) {
+  const uint32_t b0 = lane & 1u, b1 = (lane >> 1) & 1u, b2 = (lane >> 2) & 1u;
+  const int i = b1 ? (b2 ? -1 : 1) : (b2 ? 2 : 0);
+  return i < 0 ? -1 : static_cast<int>(3u * b0) + i;
+}
+__device__ __forceinline__ float wave_sum6_scatter(const float (&v)[6], uint32_t lane) {
+  const bool b0 = (lane & 1u) != 0u, b1 = (lane & 2u) != 0u, b2 = (lane & 4u) != 0u;
+  float a[3];
+#pragma unroll
+  for (int i = 0; i < 3; ++i) a[i] = (b0 ? v[3 + i] : v[i]) + dpp_f32<DPP_XOR1>(b0 ? v[i] : v[3 + i]);
+  const float c0 = (b1 ? a[1] : a[0]) + dpp_f32<DPP_XOR2>(b1 ? a[0] : a[1]);
+  const float c1 = (b1 ? 0.0f : a[2]) + dpp_f32<DPP_XOR2>(b1 ? a[2] : 0.0f);
+  float d = (b2 ? c1 : c0) + dpp_xor4_f32(b2 ? c0 : c1);
+  d = d + dpp_f32<DPP_ROW_ROR8>(d);
+  d = d + __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(d), 0x401F));  // lanes i, i ^ 16
+  const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(d), __float_as_uint(d), false, false);
+  return __uint_as_float(sw[0]) + __uint_as_float(sw[1]);  // lanes i, i ^ 32
+}
+
 // Sum over each aligned group of 8 lanes (xor offsets 1, 2, 4); uniform in the group.
 __device__ __forceinline__ float group8_sum(float v) {
   v = v + dpp_f32<DPP_XOR1>(v);
@@ -339,13 +378,21 @@ __device__ __forceinline__ f16x2_t f16x2_of(float a, float b) {  // round to nea
   return r;
 }
 
-// (w & mask) | magic in one v_and_or_b32: the compiler splits it into an AND and
-// an OR because VOP3 here takes no literal, so the mask rides in a VGPR and the
-// magic in an SGPR (one constant-bus read).
+// A constant the compiler must keep in a VGPR (an empty asm it cannot see
+// through; identical ones are merged, so each constant is materialized once).
+__device__ __forceinline__ uint32_t vgpr_const(uint32_t c) {
+  asm("" : "+v"(c));
+  return c;
+}
+
+// (w & mask) | magic in one v_and_or_b32. VOP3 here takes no literal, so with
+// both constants as literals the compiler splits it into an AND and an OR; with
+// the mask in a VGPR and the magic in an SGPR (one constant-bus read) it emits
+// the single instruction. (An inline-asm v_and_or_b32 did too, but the
+// compiler then assumes the worst of it: a wait state before every dot product
+// that reads its result, and no reordering around it.)
 __device__ __forceinline__ uint32_t and_or(uint32_t w, uint32_t mask, uint32_t magic) {
-  uint32_t r;
-  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(w), "v"(mask), "s"(magic));
-  return r;
+  return (w & vgpr_const(mask)) | magic;
 }
 
 // xp[0..3] = (x0,x4), (x1,x5), (x2,x6), (x3,x7) of the word's eight columns
