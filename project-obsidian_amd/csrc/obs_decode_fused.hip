@@ -134,7 +134,7 @@ __device__ __forceinline__ float gateup_reduce(const float (&pg)[R], const float
     const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(d), __float_as_uint(d), false, false);
     d = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);  // lanes i, i ^ 32
   }
-  return silu_mul(d, dpp_f32<DPP_ROW_ROR8>(d));
+  return silu_mul_fast(d, dpp_f32<DPP_ROW_ROR8>(d));  // h is rounded to f16 for the down rows
 }
 
 __device__ __forceinline__ void unpack_bf16x8(const uint4& v, float* f) {
@@ -406,31 +406,35 @@ __global__ void __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 
     sc[lane] = scq0;
     sc[64u + lane] = scq1;  // chunks 96..127: padding
   }
+  // this lane's group's scale and bias of every row, read at once (one LDS wait)
+  uint16_t rsb[GU_ROWS][4];
+#pragma unroll
+  for (uint32_t t = 0; t < GU_ROWS; ++t) {
+    const uint16_t* sg = sc16 + 128u * t + lane / 2u;
+#pragma unroll
+    for (uint32_t q = 0; q < 4; ++q) rsb[t][q] = sg[32u * q];  // gate s, gate b, up s, up b
+  }
 #pragma unroll
   for (uint32_t t0 = 0; t0 < GU_ROWS; t0 += GU_BATCH) {
     float pg[GU_BATCH], pu[GU_BATCH];
 #pragma unroll
     for (uint32_t i = 0; i < GU_BATCH; ++i) {
       const uint32_t t = t0 + i;
-      pg[i] = 0.0f;
-      pu[i] = 0.0f;
-      if (have) {
-        float ag = 0.0f, au = 0.0f;
-        ag = dot8_q4_off(gq[t].x, xh + 0, ag);
-        ag = dot8_q4_off(gq[t].y, xh + 4, ag);
-        ag = dot8_q4_off(gq[t].z, xh + 8, ag);
-        ag = dot8_q4_off(gq[t].w, xh + 12, ag);
-        au = dot8_q4_off(uq[t].x, xh + 0, au);
-        au = dot8_q4_off(uq[t].y, xh + 4, au);
-        au = dot8_q4_off(uq[t].z, xh + 8, au);
-        au = dot8_q4_off(uq[t].w, xh + 12, au);
-        const uint16_t* sg = sc16 + 128u * t + lane / 2u;  // this lane's group of row t
-        pg[i] = __builtin_fmaf(bf16_to_f32(sg[0]), ag - xoff, bf16_to_f32(sg[32]) * xs);
-        pu[i] = __builtin_fmaf(bf16_to_f32(sg[64]), au - xoff, bf16_to_f32(sg[96]) * xs);
-      }
+      float ag = 0.0f, au = 0.0f;
+      ag = dot8_q4_off(gq[t].x, xh + 0, ag);
+      ag = dot8_q4_off(gq[t].y, xh + 4, ag);
+      ag = dot8_q4_off(gq[t].z, xh + 8, ag);
+      ag = dot8_q4_off(gq[t].w, xh + 12, ag);
+      au = dot8_q4_off(uq[t].x, xh + 0, au);
+      au = dot8_q4_off(uq[t].y, xh + 4, au);
+      au = dot8_q4_off(uq[t].z, xh + 8, au);
+      au = dot8_q4_off(uq[t].w, xh + 12, au);
+      pg[i] = __builtin_fmaf(bf16_to_f32(rsb[t][0]), ag - xoff, bf16_to_f32(rsb[t][1]) * xs);
+      pu[i] = __builtin_fmaf(bf16_to_f32(rsb[t][2]), au - xoff, bf16_to_f32(rsb[t][3]) * xs);
     }
     int row;
-    const float hv = gateup_reduce<GU_BATCH>(pg, pu, lane, row);  // silu(0) * 0 = 0 without an expert
+    float hv = gateup_reduce<GU_BATCH>(pg, pu, lane, row);
+    hv = have ? hv : 0.0f;  // without an expert the rows are expert 0's, loaded but not used
     if (row >= 0) slot_store_xcd(h_slots + e0 + 128u * (t0 + row), epoch, hv);  // polled by this XCD only
   }
 

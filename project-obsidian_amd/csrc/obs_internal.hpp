@@ -217,6 +217,14 @@ __device__ __forceinline__ float round_f16(float v) { return static_cast<float>(
 // silu(g) * u with the deterministic exp (ops.metal:21 form).
 __device__ __forceinline__ float silu_mul(float g, float u) { return (g / (1.0f + exp_det(-g))) * u; }
 
+// silu(g) * u with the hardware exp2 and reciprocal (about 2 ulp in fp32), for
+// results rounded to bf16 or f16 right after: the grouped GEMM's epilogue and
+// the fused decode's h.
+__device__ __forceinline__ float silu_mul_fast(float g, float u) {
+  const float e = __builtin_amdgcn_exp2f(-g * 1.44269504088896341f);
+  return (g * __builtin_amdgcn_rcpf(1.0f + e)) * u;
+}
+
 // Sum over the 8 nibbles of `w` of q_j * x[j] (nibble j = (w >> 4j) & 15),
 // fp32 fma chain in nibble order. The nibbles are split into the bytes of two
 // words so each converts with one byte-to-float instruction.

@@ -124,13 +124,6 @@ __device__ __forceinline__ bf16x8_t dequant_word_mix(uint32_t w, const MixScale&
   return __builtin_bit_cast(bf16x8_t, r);
 }
 
-// silu(g) * u for the GEMM epilogue with the hardware exp2 and reciprocal
-// (about 2 ulp in fp32; the result is rounded to bf16 right after).
-__device__ __forceinline__ float silu_mul_fast(float g, float u) {
-  const float e = __builtin_amdgcn_exp2f(-g * 1.44269504088896341f);
-  return (g * __builtin_amdgcn_rcpf(1.0f + e)) * u;
-}
-
 // A staged scale|bias word whose scale is beyond dequant_word_mix's range
 // (|s| > 2^100, inf, NaN): bf16 exponent field above 127 + 100.
 __device__ __forceinline__ bool scale_out_of_mix_range(uint32_t packed_sb) {
