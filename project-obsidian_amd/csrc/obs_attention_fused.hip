@@ -258,8 +258,11 @@ attn_fused_kernel(AttnArgs a) {
       const uint32_t wd[4] = {nq[i].x, nq[i].y, nq[i].z, nq[i].w};
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) {
-        xf[8 * i + 2 * jj] = bf16_to_f32(f32_to_bf16((xf[8 * i + 2 * jj] * inv) * bf16lo(wd[jj])));
-        xf[8 * i + 2 * jj + 1] = bf16_to_f32(f32_to_bf16((xf[8 * i + 2 * jj + 1] * inv) * bf16hi(wd[jj])));
+        // rounded to bf16 in pairs (v_cvt_pk_bf16_f32: f32_to_bf16 but for NaN payloads)
+        const uint32_t pr = pack_bf16_pair_rne((xf[8 * i + 2 * jj] * inv) * bf16lo(wd[jj]),
+                                               (xf[8 * i + 2 * jj + 1] * inv) * bf16hi(wd[jj]));
+        xf[8 * i + 2 * jj] = bf16lo(pr);
+        xf[8 * i + 2 * jj + 1] = bf16hi(pr);
       }
     }
     float xs = 0.0f;
@@ -331,8 +334,8 @@ attn_fused_kernel(AttnArgs a) {
       float ss = __builtin_fmaf(x0, x0, 0.0f);
       ss = __builtin_fmaf(x1, x1, ss);
       const float inv = 1.0f / __builtin_sqrtf(wave_sum_asc(ss) / static_cast<float>(AHD) + a.eps);
-      const float n0 = bf16_to_f32(f32_to_bf16((x0 * inv) * bf16lo(wv)));
-      const float n1 = bf16_to_f32(f32_to_bf16((x1 * inv) * bf16hi(wv)));
+      const uint32_t npr = pack_bf16_pair_rne((x0 * inv) * bf16lo(wv), (x1 * inv) * bf16hi(wv));
+      const float n0 = bf16lo(npr), n1 = bf16hi(npr);
       const float p0 = shfl_xor_f(n0, 32), p1 = shfl_xor_f(n1, 32);
       float r[2];
 #pragma unroll
@@ -425,10 +428,13 @@ attn_fused_kernel(AttnArgs a) {
     const float corr = __builtin_amdgcn_exp2f(m_run - m_new);
     float p[8], psum = 0.0f;
 #pragma unroll
-    for (uint32_t i = 0; i < 8; ++i) {
-      p[i] = bf16_to_f32(f32_to_bf16(__builtin_amdgcn_exp2f(sv[i] - m_new)));
-      psum += p[i];
+    for (uint32_t i = 0; i < 8; i += 2) {  // rounded to bf16 in pairs
+      const uint32_t pr = pack_bf16_pair_rne(__builtin_amdgcn_exp2f(sv[i] - m_new), __builtin_amdgcn_exp2f(sv[i + 1] - m_new));
+      p[i] = bf16lo(pr);
+      p[i + 1] = bf16hi(pr);
     }
+#pragma unroll
+    for (uint32_t i = 0; i < 8; ++i) psum += p[i];
     l_run = l_run * corr + psum;
     m_run = m_new;
     float ocr[4];

@@ -228,7 +228,11 @@ __global__ void __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 
 #pragma unroll
     for (int i = 0; i < 4; ++i) unpack_bf16x8(nq[i], wf + 8 * i);
 #pragma unroll
-    for (int c = 0; c < 32; ++c) xf[c] = bf16_to_f32(f32_to_bf16((xf[c] * inv) * wf[c]));
+    for (int c = 0; c < 32; c += 2) {  // rounded to bf16 in pairs (v_cvt_pk_bf16_f32: f32_to_bf16 but for NaN payloads)
+      const uint32_t pr = pack_bf16_pair_rne((xf[c] * inv) * wf[c], (xf[c + 1] * inv) * wf[c + 1]);
+      xf[c] = bf16lo(pr);
+      xf[c + 1] = bf16hi(pr);
+    }
   }
   float xs = 0.0f;
 #pragma unroll
