@@ -99,7 +99,6 @@ struct AttnArgs {
 };
 
 __device__ __forceinline__ float shfl_f(float v, int src) { return __shfl(v, src, 64); }
-__device__ __forceinline__ float shfl_xor_f(float v, int m) { return __shfl_xor(v, m, 64); }
 
 // Poll n_u slots per thread (slot tid + 256 u of src) until all carry the
 // epoch or the wait times out; values in vals. Returns false on a time-out.
@@ -324,19 +323,29 @@ attn_fused_kernel(AttnArgs a) {
   load_block(min(b0 + wave, nblk - 1u));
   OBS_ATTN_MARK(3);
   // per-head RMSNorm + NeoX RoPE (attn_prep_kernel's sequence): wave w owns
-  // query head w and, for wave 0, head 4 = the key head
+  // query head w, and wave 0 the key head (head 4) too. Every wave computes the
+  // key head beside its own, the two chains interleaved (one after the other,
+  // wave 0's dependent reductions and exchanges set this phase's length), and
+  // only wave 0 stores it.
   {
     const float cs[2] = {csn[0], csn[2]}, sn[2] = {csn[1], csn[3]};
     const bool first = lane < 32u;
-    for (uint32_t h = wave; h <= AQPG; h += 4u) {
-      const float x0 = s_qkv[h * AHD + 2u * lane], x1 = s_qkv[h * AHD + 2u * lane + 1u];
-      const uint32_t wv = h < AQPG ? wq : wk;
-      float ss = __builtin_fmaf(x0, x0, 0.0f);
-      ss = __builtin_fmaf(x1, x1, ss);
-      const float inv = 1.0f / __builtin_sqrtf(wave_sum_asc(ss) / static_cast<float>(AHD) + a.eps);
-      const uint32_t npr = pack_bf16_pair_rne((x0 * inv) * bf16lo(wv), (x1 * inv) * bf16hi(wv));
+    float xv[2][2], ss[2];
+#pragma unroll
+    for (uint32_t u = 0; u < 2; ++u) {
+      const uint32_t h = u ? AQPG : wave;
+      xv[u][0] = s_qkv[h * AHD + 2u * lane];
+      xv[u][1] = s_qkv[h * AHD + 2u * lane + 1u];
+      ss[u] = __builtin_fmaf(xv[u][1], xv[u][1], __builtin_fmaf(xv[u][0], xv[u][0], 0.0f));
+    }
+    const float tot[2] = {wave_sum_asc(ss[0]), wave_sum_asc(ss[1])};
+#pragma unroll
+    for (uint32_t u = 0; u < 2; ++u) {
+      const uint32_t h = u ? AQPG : wave, wv = u ? wk : wq;
+      const float inv = 1.0f / __builtin_sqrtf(tot[u] / static_cast<float>(AHD) + a.eps);
+      const uint32_t npr = pack_bf16_pair_rne((xv[u][0] * inv) * bf16lo(wv), (xv[u][1] * inv) * bf16hi(wv));
       const float n0 = bf16lo(npr), n1 = bf16hi(npr);
-      const float p0 = shfl_xor_f(n0, 32), p1 = shfl_xor_f(n1, 32);
+      const float p0 = lane_xor32_f32(n0, lane), p1 = lane_xor32_f32(n1, lane);
       float r[2];
 #pragma unroll
       for (uint32_t jj = 0; jj < 2; ++jj) {
@@ -344,11 +353,11 @@ attn_fused_kernel(AttnArgs a) {
         const float aa = own * cs[jj], bb = other * sn[jj];
         r[jj] = first ? aa - bb : aa + bb;
       }
-      *reinterpret_cast<uint32_t*>(&s_rot[h][2u * lane]) = pack_bf16x2(r[0], r[1]);
+      if (u == 0 || wave == 0) *reinterpret_cast<uint32_t*>(&s_rot[h][2u * lane]) = pack_bf16_pair_rne(r[0], r[1]);
     }
     if (wave == 1) {  // the value head, as bf16
       *reinterpret_cast<uint32_t*>(&s_rot[AQPG + 1][2u * lane]) =
-          pack_bf16x2(s_qkv[(AQPG + 1) * AHD + 2u * lane], s_qkv[(AQPG + 1) * AHD + 2u * lane + 1u]);
+          pack_bf16_pair_rne(s_qkv[(AQPG + 1) * AHD + 2u * lane], s_qkv[(AQPG + 1) * AHD + 2u * lane + 1u]);
     }
   }
   __syncthreads();
@@ -422,27 +431,28 @@ attn_fused_kernel(AttnArgs a) {
     float bm = sv[0];
 #pragma unroll
     for (uint32_t i = 1; i < 8; ++i) bm = fmaxf(bm, sv[i]);
-    bm = fmaxf(bm, shfl_xor_f(bm, 16));
-    bm = fmaxf(bm, shfl_xor_f(bm, 32));
+    bm = fmaxf(bm, lane_xor16_f32(bm, lane));
+    bm = fmaxf(bm, lane_xor32_f32(bm, lane));
     const float m_new = fmaxf(m_run, bm);  // finite: every block holds a position < seq
     const float corr = __builtin_amdgcn_exp2f(m_run - m_new);
-    float p[8], psum = 0.0f;
+    uint32_t pw[4];  // p rounded to bf16, in pairs: the A operand of P V as it stands
+    float psum = 0.0f;
 #pragma unroll
-    for (uint32_t i = 0; i < 8; i += 2) {  // rounded to bf16 in pairs
-      const uint32_t pr = pack_bf16_pair_rne(__builtin_amdgcn_exp2f(sv[i] - m_new), __builtin_amdgcn_exp2f(sv[i + 1] - m_new));
-      p[i] = bf16lo(pr);
-      p[i + 1] = bf16hi(pr);
+    for (uint32_t i = 0; i < 4; ++i) {
+      pw[i] = pack_bf16_pair_rne(__builtin_amdgcn_exp2f(sv[2 * i] - m_new), __builtin_amdgcn_exp2f(sv[2 * i + 1] - m_new));
+      psum += bf16lo(pw[i]);
+      psum += bf16hi(pw[i]);
     }
-#pragma unroll
-    for (uint32_t i = 0; i < 8; ++i) psum += p[i];
     l_run = l_run * corr + psum;
     m_run = m_new;
-    float ocr[4];
+    // the rescale of O; on the wave's first block O is still zero (and corr = 0)
+    const bool rescale = blk != b0 + wave;  // uniform
+    float ocr[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+    if (rescale) {
 #pragma unroll
-    for (uint32_t i = 0; i < 4; ++i) ocr[i] = shfl_f(corr, static_cast<int>(4u * gq + i));
-    const bf16x8_t pa = __builtin_bit_cast(
-        bf16x8_t, u32x4_t{pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]), pack_bf16x2(p[4], p[5]),
-                          pack_bf16x2(p[6], p[7])});
+      for (uint32_t i = 0; i < 4; ++i) ocr[i] = shfl_f(corr, static_cast<int>(4u * gq + i));
+    }
+    const bf16x8_t pa = __builtin_bit_cast(bf16x8_t, u32x4_t{pw[0], pw[1], pw[2], pw[3]});
     const bool tail = t0 + 32u > seq;  // positions past seq read zero values
 #pragma unroll
     for (uint32_t nt = 0; nt < 8; ++nt) {
@@ -456,8 +466,10 @@ attn_fused_kernel(AttnArgs a) {
         v.w = keep(v.w, ta + 6u);
       }
       const bf16x8_t vbf = __builtin_bit_cast(bf16x8_t, v);
+      if (rescale) {
 #pragma unroll
-      for (uint32_t i = 0; i < 4; ++i) o[nt][i] *= ocr[i];
+        for (uint32_t i = 0; i < 4; ++i) o[nt][i] *= ocr[i];
+      }
       o[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, vbf, o[nt], 0, 0, 0);
     }
   }
@@ -476,8 +488,8 @@ attn_fused_kernel(AttnArgs a) {
   const uint16_t ores = a.x[A_ORWG * j + (lane & 63u)];  // group 0, wave 0: row 64 j + lane
   OBS_ATTN_MARK(5);
   // the wave's partial: m, l per head column (l summed over the four gq lanes), O rows 4 gq + i
-  l_run += shfl_xor_f(l_run, 16);
-  l_run += shfl_xor_f(l_run, 32);
+  l_run += lane_xor16_f32(l_run, lane);
+  l_run += lane_xor32_f32(l_run, lane);
   if (lane < 16u) {
     s_pm[wave][lane] = m_run;
     s_pl[wave][lane] = l_run;
@@ -570,7 +582,7 @@ attn_fused_kernel(AttnArgs a) {
         acc += s_ra[q][lane & 15u];
       }
       const uint32_t mine = f32_to_bf16(acc / L);
-      const uint32_t next = __shfl_xor(static_cast<int>(mine), 1, 64);
+      const uint32_t next = static_cast<uint32_t>(dpp_i32<DPP_XOR1>(static_cast<int>(mine)));  // lane ^ 1
       if (lane < A_CDIM && (lane & 1u) == 0u)
         slot_store_xcd(attn_slots + (hh * AHD + d0 + lane) / 2u, epoch, __uint_as_float(mine | (next << 16)));
     }

@@ -289,6 +289,20 @@ __device__ __forceinline__ float dpp_xor4_f32(float v) {
   return __int_as_float(r);
 }
 
+// Lane i ^ 32's and lane i ^ 16's values through the VALU's half and row swaps
+// (v_permlane32_swap, v_permlane16_swap) instead of a ds_bpermute round trip
+// through the LDS crossbar. With both operands v, the swap returns v with its
+// upper half (odd rows) replaced by the lower half (even rows), and v with its
+// lower half (even rows) replaced by the upper half (odd rows).
+__device__ __forceinline__ float lane_xor32_f32(float v, uint32_t lane) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(lane < 32u ? r[1] : r[0]);
+}
+__device__ __forceinline__ float lane_xor16_f32(float v, uint32_t lane) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float((lane & 16u) ? r[0] : r[1]);
+}
+
 // The wave_sum_asc of six values at once, bit for bit: the same pairs are
 // added in the same order (xor 1, 2, 4, 8 within a row, then the four row sums
 // as (r0 + r1) + (r2 + r3)), but at the first three steps the two lanes of a
