@@ -22,8 +22,8 @@
 //   2. Group g serves routing rank g: expert e_g = ids[g]. Its 128 waves stream
 //      the 768 gate and up rows (6 each) and, at the same time, the first third
 //      of the down rows the workgroup will need (64 rows x 384 B per workgroup);
-//      the other two thirds are issued once the first block of h is in (below),
-//      so they do not compete with the gate/up rows.
+//      the other two thirds are issued once most of the gate/up rows are in
+//      (below), so they do not compete with them.
 //   3. h = silu(gate.x) * (up.x) goes to the group's h slots; each workgroup
 //      polls them into LDS in three blocks, adding each block's terms to its 64
 //      down rows as the block arrives (the down weights are in registers).
@@ -440,6 +440,20 @@ __global__ void __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 
     float hv = gateup_reduce<GU_BATCH>(pg, pu, lane, row);
     hv = have ? hv : 0.0f;  // without an expert the rows are expert 0's, loaded but not used
     if (row >= 0) slot_store_xcd(h_slots + e0 + 128u * (t0 + row), epoch, hv);  // polled by this XCD only
+    if (t0 == 2u) {
+      // The down rows' other two blocks, between the second and the last gate/up
+      // batch. Issued with the gate/up rows they competed with them for
+      // bandwidth; the h polls below wait for them (a wave's loads complete in
+      // issue order), so issued here they are in flight during the last batch
+      // and the exchange. Per layer (48-layer sweep, timing build): after the
+      // first h poll 13.40 us, after the first batch 13.43, after the last
+      // 13.35, here 13.17.
+#pragma unroll
+      for (uint32_t p = 0; p < 2; ++p) {
+        dq[p][1] = dpp[p][8];
+        dq[p][2] = dpp[p][16];
+      }
+    }
   }
 
   OBS_FUSED_MARK(5);
@@ -485,18 +499,7 @@ __global__ void __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 
         }
       }
       __syncthreads();
-      if (L == 0) {
-        OBS_FUSED_MARK(6);
-        // the down rows' other two blocks, now: issued with the gate/up rows they
-        // competed with them (the median workgroup stored h ~0.8 us later), and
-        // issued before this first poll the poll would have waited for their
-        // data (a wave's loads complete in issue order); 14.23 -> 13.93 us
-#pragma unroll
-        for (uint32_t p = 0; p < 2; ++p) {
-          dq[p][1] = dpp[p][8];
-          dq[p][2] = dpp[p][16];
-        }
-      }
+      if (L == 0) OBS_FUSED_MARK(6);
       // the lane's columns of block L: [256L + 32m, +32)
       f16x2_t hp[16];
 #pragma unroll
