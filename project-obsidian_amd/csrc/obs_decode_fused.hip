@@ -20,10 +20,10 @@
 //      logits; wave 0 of every workgroup runs softmax + top-8 on them and
 //      shares the result through LDS.
 //   2. Group g serves routing rank g: expert e_g = ids[g]. Its 128 waves stream
-//      the 768 gate and up rows (6 each) and, at the same time, the first third
-//      of the down rows the workgroup will need (64 rows x 384 B per workgroup);
-//      the other two thirds are issued once most of the gate/up rows are in
-//      (below), so they do not compete with them.
+//      the 768 gate and up rows (6 each) and the scales of the down rows the
+//      workgroup will need (64 rows x 384 B per workgroup); the down rows
+//      themselves are issued once most of the gate/up rows are in (below), so
+//      they do not compete with them.
 //   3. h = silu(gate.x) * (up.x) goes to the group's h slots; each workgroup
 //      polls them into LDS in three blocks, adding each block's terms to its 64
 //      down rows as the block arrives (the down weights are in registers).
@@ -349,7 +349,8 @@ __global__ void __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 
   const bool have = ok && eg >= 0 && static_cast<uint32_t>(eg) < n_exp;
   OBS_FUSED_MARK(3);
 
-  // ---- 3. issue the weight loads: 6 gate + 6 up rows, the first of 3 down blocks (x2).
+  // ---- 3. issue the weight loads: 6 gate + 6 up rows and the down scales (the
+  // down rows follow in phase 4).
   // Wide loads only: each gate/up row is one coalesced 1 KB load; the down rows
   // are read a 128-byte line per 8 lanes (lane (r8, m) takes bytes
   // [128L + 16m, +16) of row r8, L = 0..2: columns [256L + 32m, +32)); the
@@ -369,8 +370,9 @@ __global__ void __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 
     const uint32_t el = have ? static_cast<uint32_t>(eg) : 0u;
     const size_t eoff_gu = size_t(el) * FI;
     // Loads in the order they are consumed (the memory counter is in order): the
-    // gate/up scales and rows, then the down scales and rows. Lanes past the
-    // last chunk reload a valid one, so no load is predicated.
+    // gate/up scales and rows, then the down scales (the down rows' addresses
+    // are set here, their loads issued in phase 4). Lanes past the last chunk
+    // reload a valid one, so no load is predicated.
 #pragma unroll
     for (uint32_t i = 0; i < 2; ++i) {  // chunk c = 16 bytes of segment c/4 = (row t, array)
       const uint32_t c = min(lane + 64u * i, GU_ROWS * 16u - 1u), sg = c / 4u, t = sg / 4u, arr = sg % 4u;
@@ -396,7 +398,6 @@ __global__ void __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 
     for (uint32_t p = 0; p < 2; ++p) {
       const size_t row = size_t(el) * FH + dn_row0 + 8u * p + r8;
       dpp[p] = reinterpret_cast<const uint4*>(a.down_w + row * (FI / 8)) + m;
-      dq[p][0] = dpp[p][0];
     }
   }
   // the wave's staged scales: gate/up segment sg = 4t + {gate_s, gate_b, up_s,
@@ -441,15 +442,17 @@ __global__ void __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 
     hv = have ? hv : 0.0f;  // without an expert the rows are expert 0's, loaded but not used
     if (row >= 0) slot_store_xcd(h_slots + e0 + 128u * (t0 + row), epoch, hv);  // polled by this XCD only
     if (t0 == 2u) {
-      // The down rows' other two blocks, between the second and the last gate/up
-      // batch. Issued with the gate/up rows they competed with them for
-      // bandwidth; the h polls below wait for them (a wave's loads complete in
-      // issue order), so issued here they are in flight during the last batch
-      // and the exchange. Per layer (48-layer sweep, timing build): after the
-      // first h poll 13.40 us, after the first batch 13.43, after the last
-      // 13.35, here 13.17.
+      // The down rows, between the second and the last gate/up batch: issued
+      // with the gate/up rows they competed with them for bandwidth, and the h
+      // polls below wait for them (a wave's loads complete in issue order), so
+      // issued here they are in flight during the last batch and the exchange.
+      // Per layer (48-layer sweep, timing build, graph replay): blocks 1 and 2
+      // after the first h poll and block 0 with the gate/up rows 13.40 us;
+      // blocks 1 and 2 here 13.17; all three here 12.93 (after the first batch
+      // 13.12; the down scales here too 13.02).
 #pragma unroll
       for (uint32_t p = 0; p < 2; ++p) {
+        dq[p][0] = dpp[p][0];
         dq[p][1] = dpp[p][8];
         dq[p][2] = dpp[p][16];
       }
