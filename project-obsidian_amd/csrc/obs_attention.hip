@@ -97,7 +97,7 @@ __global__ void __launch_bounds__(256) q4_gemv_kernel(const uint16_t* __restrict
     const uint16_t* rp = pick(pi, a.p[0].residual, a.p[1].residual, a.p[2].residual);
 #pragma unroll
     for (uint32_t sg = 0; sg < SEG; ++sg) {
-      q[k][sg] = reinterpret_cast<const uint4*>(w + static_cast<size_t>(rr) * (IN / 8u) + 256u * sg)[lane];
+      q[k][sg] = load_stream(reinterpret_cast<const uint4*>(w + static_cast<size_t>(rr) * (IN / 8u) + 256u * sg) + lane);
       const size_t gi = static_cast<size_t>(rr) * GROUPS + 32u * sg + lane / 2u;
       sc[k][sg] = sp[gi];
       bi[k][sg] = bp[gi];
@@ -135,10 +135,9 @@ __global__ void __launch_bounds__(256) q4_gemv_kernel(const uint16_t* __restrict
         for (uint32_t j = 0; j < 4; ++j) {
           float& e0 = xf[sg][8 * i + 2 * j];
           float& e1 = xf[sg][8 * i + 2 * j + 1];
-          const float n0 = bf16_to_f32(f32_to_bf16((e0 * inv) * bf16lo(wd[j])));
-          const float n1 = bf16_to_f32(f32_to_bf16((e1 * inv) * bf16hi(wd[j])));
-          e0 = use_norm ? n0 : e0;
-          e1 = use_norm ? n1 : e1;
+          const uint32_t npr = pack_bf16_pair_rne((e0 * inv) * bf16lo(wd[j]), (e1 * inv) * bf16hi(wd[j]));
+          e0 = use_norm ? bf16lo(npr) : e0;
+          e1 = use_norm ? bf16hi(npr) : e1;
         }
       }
   }

@@ -176,7 +176,7 @@ attn_fused_kernel(AttnArgs a) {
     const uint32_t* w = is_q ? a.q_w : (is_k ? a.k_w : a.v_w);
     const uint16_t* sp = is_q ? a.q_s : (is_k ? a.k_s : a.v_s);
     const uint16_t* bp = is_q ? a.q_b : (is_k ? a.k_b : a.v_b);
-    rq[k] = reinterpret_cast<const uint4*>(w + static_cast<size_t>(rr) * (AH / 8u))[lane];
+    rq[k] = load_stream(reinterpret_cast<const uint4*>(w + static_cast<size_t>(rr) * (AH / 8u)) + lane);
     rsc[k] = sp[static_cast<size_t>(rr) * (AH / 64u) + lane / 2u];
     rbi[k] = bp[static_cast<size_t>(rr) * (AH / 64u) + lane / 2u];
   }
@@ -202,17 +202,19 @@ attn_fused_kernel(AttnArgs a) {
   auto kpos = [&](uint32_t t0, uint32_t tt) __attribute__((always_inline)) {
     return t0 + 8u * (col >> 2) + 4u * tt + (col & 3u);
   };
+  // (keys and values are loaded non-temporally, like the weight rows: a step
+  // reads each once, and cached they pushed out what the MoE half reads again)
   auto load_block = [&](uint32_t blk) __attribute__((always_inline)) {
     const uint32_t t0 = 32u * blk;
 #pragma unroll
     for (uint32_t tt = 0; tt < 2; ++tt) {
       const uint16_t* kr = kb + static_cast<size_t>(kpos(t0, tt)) * AHD + 8u * gq;
 #pragma unroll
-      for (uint32_t ks = 0; ks < 4; ++ks) ka[tt][ks] = *reinterpret_cast<const u32x4_t*>(kr + 32u * ks);
+      for (uint32_t ks = 0; ks < 4; ++ks) ka[tt][ks] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(kr + 32u * ks));
     }
 #pragma unroll
     for (uint32_t nt = 0; nt < 8; ++nt)
-      va[nt] = *reinterpret_cast<const u32x4_t*>(vb + static_cast<size_t>(16u * nt + col) * max_len + t0 + 8u * gq);
+      va[nt] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(vb + static_cast<size_t>(16u * nt + col) * max_len + t0 + 8u * gq));
   };
   // every row load above is issued before anything waits for the position
   // (left alone, the scheduler put that wait ahead of the last row's load)
@@ -479,8 +481,8 @@ attn_fused_kernel(AttnArgs a) {
   for (uint32_t p = 0; p < 2; ++p) {
     const size_t r = orow0 + 8u * p;
     const uint4* op = reinterpret_cast<const uint4*>(a.o_w + r * (AQD / 8u) + (AHD * hq0 + 64u * oc) / 8u);
-    oq[p][0] = op[0];
-    oq[p][1] = op[1];
+    oq[p][0] = load_stream(op);
+    oq[p][1] = load_stream(op + 1);
     const size_t gi = r * (AQD / 64u) + 2u * hq0 + oc;
     osc[p] = a.o_s[gi];
     obi[p] = a.o_b[gi];

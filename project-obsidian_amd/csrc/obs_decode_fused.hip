@@ -377,21 +377,22 @@ __global__ void __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 
     for (uint32_t i = 0; i < 2; ++i) {  // chunk c = 16 bytes of segment c/4 = (row t, array)
       const uint32_t c = min(lane + 64u * i, GU_ROWS * 16u - 1u), sg = c / 4u, t = sg / 4u, arr = sg % 4u;
       const uint16_t* base = arr == 0u ? a.gate_s : arr == 1u ? a.gate_b : arr == 2u ? a.up_s : a.up_b;
-      const u32x4_t v = *reinterpret_cast<const u32x4_t*>(base + (eoff_gu + e0 + 128u * t) * (FH / FG) + 8u * (c % 4u));
-      if (i == 0) scq0 = v; else scq1 = v;
+      const uint4 v = load_stream(base + (eoff_gu + e0 + 128u * t) * (FH / FG) + 8u * (c % 4u));
+      if (i == 0) scq0 = u32x4_t{v.x, v.y, v.z, v.w}; else scq1 = u32x4_t{v.x, v.y, v.z, v.w};
     }
     __builtin_amdgcn_sched_barrier(0);  // keep the issue order (see above)
 #pragma unroll
     for (uint32_t t = 0; t < GU_ROWS; ++t) {
       const size_t row = eoff_gu + e0 + 128u * t;
-      gq[t] = reinterpret_cast<const uint4*>(a.gate_w + row * (FH / 8))[lane];
-      uq[t] = reinterpret_cast<const uint4*>(a.up_w + row * (FH / 8))[lane];
+      gq[t] = load_stream(reinterpret_cast<const uint4*>(a.gate_w + row * (FH / 8)) + lane);
+      uq[t] = load_stream(reinterpret_cast<const uint4*>(a.up_w + row * (FH / 8)) + lane);
     }
     __builtin_amdgcn_sched_barrier(0);
     {  // down scales (chunks 0..23) and biases (24..47) of the wave's 16 rows
       const uint32_t c = min(lane, 47u);
-      scq2 = *reinterpret_cast<const u32x4_t*>((c < 24u ? a.down_s : a.down_b) +
-                                               (size_t(el) * FH + dn_row0) * (FI / FG) + 8u * (c % 24u));
+      const uint4 v = load_stream((c < 24u ? a.down_s : a.down_b) + (size_t(el) * FH + dn_row0) * (FI / FG) +
+                                  8u * (c % 24u));
+      scq2 = u32x4_t{v.x, v.y, v.z, v.w};
     }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -452,9 +453,9 @@ __global__ void __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 
       // 13.12; the down scales here too 13.02).
 #pragma unroll
       for (uint32_t p = 0; p < 2; ++p) {
-        dq[p][0] = dpp[p][0];
-        dq[p][1] = dpp[p][8];
-        dq[p][2] = dpp[p][16];
+        dq[p][0] = load_stream(dpp[p]);
+        dq[p][1] = load_stream(dpp[p] + 8);
+        dq[p][2] = load_stream(dpp[p] + 16);
       }
     }
   }
