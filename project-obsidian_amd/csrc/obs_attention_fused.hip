@@ -38,10 +38,11 @@
 // Load order. A wave's loads complete in issue order, and a CU accepts them
 // only as fast as memory drains them, so each batch sits where it delays
 // nothing more urgent: the q/k/v rows at the start (they have the bandwidth
-// to themselves), the first key/value block right after the q/k/v poll (issued
+// to themselves), the first block's keys right after the q/k/v poll (issued
 // before it, the poll waited for the block's data; issued at the start, the
-// rows shared their bandwidth), and the o rows after the attention blocks,
-// where their latency overlaps the two exchanges that precede their use.
+// rows shared their bandwidth) and its values after the RoPE, and the o rows
+// after the attention blocks, where their latency overlaps the two exchanges
+// that precede their use.
 // Every wait is bounded (100 ms of the constant clock); a time-out sets the
 // workspace's error flag, reported and cleared by obs_device_status.
 #include "obs_internal.hpp"
@@ -204,7 +205,7 @@ attn_fused_kernel(AttnArgs a) {
   };
   // (keys and values are loaded non-temporally, like the weight rows: a step
   // reads each once, and cached they pushed out what the MoE half reads again)
-  auto load_block = [&](uint32_t blk) __attribute__((always_inline)) {
+  auto load_keys = [&](uint32_t blk) __attribute__((always_inline)) {
     const uint32_t t0 = 32u * blk;
 #pragma unroll
     for (uint32_t tt = 0; tt < 2; ++tt) {
@@ -212,9 +213,16 @@ attn_fused_kernel(AttnArgs a) {
 #pragma unroll
       for (uint32_t ks = 0; ks < 4; ++ks) ka[tt][ks] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(kr + 32u * ks));
     }
+  };
+  auto load_values = [&](uint32_t blk) __attribute__((always_inline)) {
+    const uint32_t t0 = 32u * blk;
 #pragma unroll
     for (uint32_t nt = 0; nt < 8; ++nt)
       va[nt] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(vb + static_cast<size_t>(16u * nt + col) * max_len + t0 + 8u * gq));
+  };
+  auto load_block = [&](uint32_t blk) __attribute__((always_inline)) {
+    load_keys(blk);
+    load_values(blk);
   };
   // every row load above is issued before anything waits for the position
   // (left alone, the scheduler put that wait ahead of the last row's load)
@@ -320,9 +328,12 @@ attn_fused_kernel(AttnArgs a) {
     for (uint32_t u = 0; u < 3; ++u) s_qkv[tid + 256u * u] = vals[u];
   }
   __syncthreads();
-  // the wave's first key/value block (clamped into the sequence when it has
-  // none; unused then), now that no poll waits behind it
-  load_block(min(b0 + wave, nblk - 1u));
+  // the keys of the wave's first block (clamped into the sequence when it has
+  // none; unused then), now that no poll waits behind them; its values follow
+  // the RoPE: a wave stalls while the memory queue takes its loads, and the
+  // RoPE needs none of them (decoder 724 -> 729 tokens/s; all 16 loads after
+  // the RoPE: 718)
+  load_keys(min(b0 + wave, nblk - 1u));
   OBS_ATTN_MARK(3);
   // per-head RMSNorm + NeoX RoPE (attn_prep_kernel's sequence): wave w owns
   // query head w, and wave 0 the key head (head 4) too. Every wave computes the
@@ -362,6 +373,7 @@ attn_fused_kernel(AttnArgs a) {
           pack_bf16_pair_rne(s_qkv[(AQPG + 1) * AHD + 2u * lane], s_qkv[(AQPG + 1) * AHD + 2u * lane + 1u]);
     }
   }
+  load_values(min(b0 + wave, nblk - 1u));
   __syncthreads();
   OBS_ATTN_MARK(4);
   const uint32_t pblk = pos / 32u;
