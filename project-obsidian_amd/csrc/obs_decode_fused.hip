@@ -84,51 +84,33 @@ __device__ __forceinline__ void raise_error(unsigned char* ws) {
   __hip_atomic_store(reinterpret_cast<uint32_t*>(ws + WS_ERR), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
-// Gate/up rows whose lane partials are reduced together.
-#ifndef GU_BATCH_ROWS
-#define GU_BATCH_ROWS 2
-#endif
-constexpr uint32_t GU_BATCH = GU_BATCH_ROWS;
-static_assert(GU_BATCH == 2 || GU_BATCH == 6, "batches of 2 or 6 rows");
+// Gate/up rows whose lane partials are reduced together (a batch of 6 made h
+// visible all at once and measured slower: blocks of h then arrive together).
+constexpr uint32_t GU_BATCH = 2;
 
-// The 64-lane sums of a wave's lane partials of R gate rows (pg) and R up rows
+// The 64-lane sums of a wave's lane partials of 2 gate rows (pg) and 2 up rows
 // (pu), reduced together, and silu(gate) * up of each row. Instead of a full
-// butterfly per value (12 of them cost ~150 instructions plus their DPP
-// hazards, and each row's silu), the values are reduce-scattered over the
-// lanes of a 16-lane row: at each step two lanes that hold the same set of
-// values split it, each keeping half and adding its partner's copy of that
+// butterfly per value (4 of them cost ~60 instructions plus their DPP hazards
+// and readlanes, and each row's silu), the values are reduce-scattered over
+// the lanes of a 16-lane row: at each step two lanes that hold the same set
+// of values split it, each keeping half and adding its partner's copy of that
 // half, until every lane of the row holds the row's sum of one value. The
-// pairings are the row mirror (lane bit 3 splits gate from up), the half-row
-// mirror (bit 2) and the quad xors (bits 1, 0); lanes paired at one step agree
-// in every bit split before. An xor by 16 and a swap of the wave's halves then
-// add the four rows. Gate row r ends up in a lane with bit 3 clear and its up
-// row 8 lanes higher, so one row rotation brings them together; `row` is the
-// batch row a lane of 0..7 holds (-1 for the other lanes, and for padding).
-// Rows: R = 2: lanes 0, 4 -> rows 0, 1. R = 6: lane bits 2..0 = 000 -> 0,
-// 001 -> 2, 010 -> 1, 100 -> 3, 101 -> 5, 110 -> 4, 011 and 111 padding.
-template <uint32_t R>
-__device__ __forceinline__ float gateup_reduce(const float (&pg)[R], const float (&pu)[R], uint32_t lane, int& row) {
+// pairings are the row mirror (lane bit 3 splits gate from up) and the
+// half-row mirror (bit 2 splits the two rows); lanes paired at one step agree
+// in every bit split before. Two quad xors, an xor by 16 and a swap of the
+// wave's halves then add the rest. Gate row r ends up in the lanes with bit 3
+// clear and bit 2 = r, its up row 8 lanes higher, so one row rotation brings
+// them together; `row` is the batch row lanes 0 and 4 hold (-1 elsewhere).
+__device__ __forceinline__ float gateup_reduce(const float (&pg)[GU_BATCH], const float (&pu)[GU_BATCH], uint32_t lane,
+                                               int& row) {
   const bool s1 = (lane & 8u) != 0u, s2 = (lane & 4u) != 0u;
-  float a[R];
+  float a[GU_BATCH];
 #pragma unroll
-  for (uint32_t i = 0; i < R; ++i) a[i] = (s1 ? pu[i] : pg[i]) + dpp_f32<DPP_MIRROR>(s1 ? pg[i] : pu[i]);
-  float d;
-  if constexpr (R == 2) {
-    d = (s2 ? a[1] : a[0]) + dpp_f32<DPP_HALF_MIRROR>(s2 ? a[0] : a[1]);
-    d = d + dpp_f32<DPP_XOR2>(d);
-    d = d + dpp_f32<DPP_XOR1>(d);
-    row = lane < 8u && (lane & 3u) == 0u ? (s2 ? 1 : 0) : -1;
-  } else {
-    const bool s3 = (lane & 2u) != 0u, s4 = (lane & 1u) != 0u;
-    float b[3];
-#pragma unroll
-    for (uint32_t i = 0; i < 3; ++i) b[i] = (s2 ? a[3 + i] : a[i]) + dpp_f32<DPP_HALF_MIRROR>(s2 ? a[i] : a[3 + i]);
-    const float c0 = (s3 ? b[1] : b[0]) + dpp_f32<DPP_XOR2>(s3 ? b[0] : b[1]);
-    const float c1 = (s3 ? 0.0f : b[2]) + dpp_f32<DPP_XOR2>(s3 ? b[2] : 0.0f);
-    d = (s4 ? c1 : c0) + dpp_f32<DPP_XOR1>(s4 ? c0 : c1);
-    const int i = s4 ? (s3 ? -1 : 2) : (s3 ? 1 : 0);
-    row = lane < 8u && i >= 0 ? (s2 ? 3 : 0) + i : -1;
-  }
+  for (uint32_t i = 0; i < GU_BATCH; ++i) a[i] = (s1 ? pu[i] : pg[i]) + dpp_f32<DPP_MIRROR>(s1 ? pg[i] : pu[i]);
+  float d = (s2 ? a[1] : a[0]) + dpp_f32<DPP_HALF_MIRROR>(s2 ? a[0] : a[1]);
+  d = d + dpp_f32<DPP_XOR2>(d);
+  d = d + dpp_f32<DPP_XOR1>(d);
+  row = lane < 8u && (lane & 3u) == 0u ? (s2 ? 1 : 0) : -1;
   d = d + __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(d), 0x401F));  // lanes i, i ^ 16
   {
     const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(d), __float_as_uint(d), false, false);
@@ -430,7 +412,7 @@ __global__ void __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 
       pu[i] = __builtin_fmaf(bf16_to_f32(rsb[t][2]), au - xoff, bf16_to_f32(rsb[t][3]) * xs);
     }
     int row;
-    float hv = gateup_reduce<GU_BATCH>(pg, pu, lane, row);
+    float hv = gateup_reduce(pg, pu, lane, row);
     hv = have ? hv : 0.0f;  // without an expert the rows are expert 0's, loaded but not used
     if (row >= 0) slot_store_xcd(h_slots + e0 + 128u * (t0 + row), epoch, hv);  // polled by this XCD only
     if (t0 == 2u) {
