@@ -76,9 +76,11 @@ def test_q4_matvec_one_hot(exe):
         assert np.array_equal(yf.download(), W[:, j])
 
 
-@pytest.mark.parametrize("T", [1, 7, 512])
+@pytest.mark.parametrize("T", [1, 7, 512, 1100, 2048])
 def test_q8_gate_logits_bit_exact(exe, T):
-    """Config 1: router gate [128, 2048] 8-bit, T = 1 and 512."""
+    """Config 1: router gate [128, 2048] 8-bit, T = 1 and 512; at 1,100 and
+    2,048 tokens a workgroup runs several 8-token chunks (1,100: a partial
+    last chunk)."""
     E, H = 128, 2048
     rng = np.random.default_rng(300 + T)
     w, s, b = synth.quant_tensor(rng, E, H, 8, 64)
