@@ -144,7 +144,7 @@ def bench_decode(torch, oh, exe, args):
 
 
 def bench_router(torch, oh, exe, reps=200):
-    """BASELINE config 1 on the GPU: 8-bit gate logits + softmax/top-8 for T = 1
+    """The router on the GPU: 8-bit gate logits + softmax/top-8 for T = 1
     and T = 512 tokens (gate_gpu + MoeRouter.route_dispatch, forward.rs:386-397,
     router.rs:62-83). Each T's two launches are captured `reps` times in one
     graph; the time per call is the replay time over reps."""
@@ -182,7 +182,7 @@ def bench_router(torch, oh, exe, reps=200):
 
 
 def gpu_decoder(torch, oh, D, exe, n_layers, max_len, seed):
-    """A Qwen3-30B-A3B-shaped decoder with seeded random
+    """A Qwen3-30B-A3B-shaped decoder (48 layers, vocab 151,936) with seeded random
     weights generated on the GPU: centred 4-bit attention and expert matrices
     (uncentred experts all push the residual stream one way until the SwiGLU
     intermediates leave the f16 range within a few tokens), norm weights
@@ -259,7 +259,7 @@ def decoder_token_bytes(c, seq):
 
 
 def bench_decoder(torch, oh, exe, args):
-    """greedy decode steps of the 48-layer decoder around
+    """Greedy decode steps of the 48-layer decoder around
     context 4096, one captured graph per step, replayed back to back."""
     from obsidian_hip import decoder as D
     ctx = 4096
@@ -457,7 +457,7 @@ def _median_us(fn, reps):
 
 
 def cpu_baseline(n_threads, pf_sample=256):
-    """The reference's CPU path on this host, per BASELINE configuration: the
+    """The reference's CPU path on this host, per benched workload: the
     oracle's C rendering of the Metal shaders' semantics (serial fp32 dot per
     output row, OpenMP over rows; kind "port") and the NumPy replica of
     validate_dequant.py:24-30 with numpy's BLAS for the products. Medians of 20

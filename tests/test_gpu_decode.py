@@ -1,4 +1,4 @@
-"""GPU parity of the decode MoE half (forward.rs:421-441; config 2 shapes):
+"""GPU parity of the decode MoE half (forward.rs:421-441; the 30B-A3B decode layer shapes):
 router ids/weights bit-exact with the oracle, layer output within 1e-2
 relative of the oracle's fp64 evaluation on the same routing."""
 import numpy as np

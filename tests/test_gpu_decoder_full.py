@@ -1,5 +1,5 @@
-"""The benched decoder step at its full Qwen3-30B-A3B shape (BASELINE config
-4): one layer of hidden 2048, 32 query / 4 kv heads of 128, a 128-expert top-8
+"""The benched decoder step at its full Qwen3-30B-A3B shape: one layer of
+hidden 2048, 32 query / 4 kv heads of 128, a 128-expert top-8
 MoE block of inter 768 with its post-attention norm, a KV cache of 4,096
 positions already holding 4,000, and the 151,936-row 4-bit lm_head. The step
 runs the same one-launch attention and MoE kernels as the benched 48-layer

@@ -46,7 +46,7 @@ def test_dequant_known_answer_word(exe):
 
 @pytest.mark.parametrize("in_f,out_f", [(768, 2048), (2048, 768), (512, 5)])
 def test_q4_matvec_within_fp32_bound(exe, in_f, out_f):
-    """Config 0 shape (down_proj [2048, 768]) and the gate/up shape."""
+    """The down_proj shape [2048, 768] and the gate/up shape."""
     rng = np.random.default_rng(200 + in_f)
     w, s, b = synth.quant_tensor(rng, out_f, in_f, 4, 64)
     x = synth.bf16_normal(rng, in_f)
@@ -78,7 +78,7 @@ def test_q4_matvec_one_hot(exe):
 
 @pytest.mark.parametrize("T", [1, 7, 512, 1100, 2048])
 def test_q8_gate_logits_bit_exact(exe, T):
-    """Config 1: router gate [128, 2048] 8-bit, T = 1 and 512; at 1,100 and
+    """The router gate [128, 2048] 8-bit, T = 1 and 512; at 1,100 and
     2,048 tokens a workgroup runs several 8-token chunks (1,100: a partial
     last chunk)."""
     E, H = 128, 2048

@@ -1,4 +1,4 @@
-"""GPU parity of the grouped prefill MoE (forward.rs:164-247, config 3 shapes)
+"""GPU parity of the grouped prefill MoE (forward.rs:164-247, T = 2,048 Zipf shapes)
 and of the per-expert batched dequant matmul (matmul_raw, forward.rs:313-321).
 
 Bars: outputs within 1e-2 relative (north-star bf16 tolerance) of the
@@ -181,7 +181,7 @@ def test_moe_prefill_with_post_attention_norm(exe, qwen):
 
 
 def test_moe_prefill_t2048_matches_decode(exe, qwen):
-    """Config 3 size: every token of a T=2048 prefill (routing computed on the
+    """Full size: every token of a T=2048 prefill (routing computed on the
     GPU) equals the fused decode of that token, within tolerance."""
     t, layer, L = qwen
     cfg = oh.MoeConfig(E, K, H, I, 64, True)
@@ -204,7 +204,7 @@ def test_moe_prefill_t2048_matches_decode(exe, qwen):
 
 
 def test_moe_prefill_t2048_zipf_linearity(exe, qwen):
-    """Config 3 routing at full size: scaling every routing weight by 2 doubles
+    """Zipf routing at full size: scaling every routing weight by 2 doubles
     the output (linearity of the combine), and a second run is bit-identical
     (deterministic grouping and rank-order combine)."""
     t, layer, L = qwen
