@@ -227,8 +227,12 @@ attn_fused_kernel(AttnArgs a) {
   // every row load above is issued before anything waits for the position
   // (left alone, the scheduler put that wait ahead of the last row's load)
   __builtin_amdgcn_sched_barrier(0);
-  // every workgroup adds 1 to the count as it exits: the quotient counts the
-  // earlier launches (as in decode_fused_kernel). One thread per workgroup
+  // workgroup 0 adds 1 to the count as it exits, after every workgroup of its
+  // launch has read it: it exits after the residual add, which waits for the
+  // output partials of workgroup 0 of every group, each of which waited for
+  // the attention outputs of every workgroup of its group, each of which read
+  // the count before its first publish. So the count is the number of earlier
+  // launches (as in decode_fused_kernel). One thread per workgroup
   // loads it, after the rows and before anything that needs the position:
   // these coherent loads go to memory, and from every thread they made a hot
   // spot of two addresses; under a branch they are waited for at its join,
@@ -300,13 +304,14 @@ attn_fused_kernel(AttnArgs a) {
     // the epoch is needed from the first publish on: the barrier sits here,
     // after the rows' wait, not before the compute
     if (tid == 0) {
-      s_epoch = static_cast<uint32_t>(counted / ANWG) + 1u;
+      s_epoch = static_cast<uint32_t>(counted) + 1u;
       s_abort = err != 0u;
       s_fail = 0;
     }
     __syncthreads();
     if (s_abort) {  // a previous launch failed: the host must reset first
-      if (tid == 0) __hip_atomic_fetch_add(ctl_count, uint64_t{1}, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (tid == 0 && blockIdx.x == 0)
+        __hip_atomic_fetch_add(ctl_count, uint64_t{1}, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       return;
     }
     if (my_row >= 0) slot_store_xcd(qkv_slots + A_RPW * wl + my_row, s_epoch, mine);  // polled by this XCD only
@@ -697,7 +702,9 @@ attn_fused_kernel(AttnArgs a) {
   OBS_ATTN_MARK(11);
   if (tid == 0) {
     if (s_fail) __hip_atomic_store(ctl_err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-    __hip_atomic_fetch_add(ctl_count, uint64_t{1}, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // one add per launch (256 adds on one address at the end of a launch
+    // delay the next launch by over a microsecond)
+    if (blockIdx.x == 0) __hip_atomic_fetch_add(ctl_count, uint64_t{1}, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
