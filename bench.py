@@ -432,7 +432,8 @@ def bench_prefill(torch, oh, exe, args):
     stats = exe.profile_stats()
     exe.profile_clear()
     kernels = {n: {"avg_us": 1000.0 * tt / c, "launches": c} for n, (tt, c) in stats.items()}
-    gemm_us = sum(v["avg_us"] for n, v in kernels.items() if n.startswith("grouped_gemm"))
+    # both GEMMs: one moe_ffn launch, or grouped_gemm_gateup + grouped_gemm_down
+    gemm_us = sum(v["avg_us"] for n, v in kernels.items() if n.startswith("grouped_gemm") or n == "moe_ffn")
     ys = Y.float().cpu()
     if not bool(torch.isfinite(ys).all()):
         raise RuntimeError("prefill produced non-finite outputs")

@@ -132,6 +132,7 @@ int fused_decode_status_ws(obs_ctx* ctx, void* ws);
 // Fused attention half of a decode layer (obs_attention_fused.hip): its
 // device error flag, read and cleared (synchronizes).
 int attn_fused_status(obs_ctx* ctx);
+int ffn_status(obs_ctx* ctx);  // the one-launch prefill FFN's wait flag
 
 // The context's RoPE table for (theta, max_len) (obs_attention.hip): entry
 // [p][i] = (cos, sin) of fl32(p * fl32(theta^(-2i/128))), each evaluated in

@@ -27,6 +27,8 @@
 //   - v_mfma_f32_32x32x16_bf16 accumulates in fp32. The MFMA's 16 k-slots of
 //     K-step s map to columns k0 + 32h + 8s + j (h = lane half, j = 0..7), for
 //     A and B alike, so each lane's 16-byte load feeds all four K-steps.
+#include <algorithm>
+
 #include "obs_internal.hpp"
 
 namespace obs {
@@ -318,13 +320,14 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, uint16_t (&sA)[2][T
 // Two workgroups per CU (at most 256 registers per lane): the co-resident
 // workgroup hides each one's load, LDS and barrier latency.
 template <uint32_t MODE, uint32_t FLAGS>
+__device__ __forceinline__ void gemm_item(const GemmArgs& a, uint32_t e, uint32_t row0, uint32_t nrows, uint32_t n0,
+                                          uint16_t (&sA)[2][TM * LDS_STRIDE], int32_t* s_orow, uint32_t* s_sb);
+
+template <uint32_t MODE, uint32_t FLAGS>
 __global__ void __launch_bounds__(256, 2) grouped_gemm_kernel(GemmArgs a) {
-  constexpr bool TWO = MODE != MODE_NARROW;
   __shared__ uint16_t sA[2][TM * LDS_STRIDE];
   __shared__ int32_t s_orow[TM];
   extern __shared__ uint32_t s_sb[];  // [matrix][group][SB_STRIDE]: scale | bias << 16
-  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-  const uint32_t K = a.K, groups = K / GK;
   // The work item: one load from the grouping's per-workgroup table, or, for
   // dense rows, arithmetic on the launch index.
   uint32_t e, row0, nrows, n0;
@@ -347,6 +350,17 @@ __global__ void __launch_bounds__(256, 2) grouped_gemm_kernel(GemmArgs a) {
     nrows = min(TM, a.dense_rows - row0);
     n0 = item % ncb * mode_cols(MODE);
   }
+  gemm_item<MODE, FLAGS>(a, e, row0, nrows, n0, sA, s_orow, s_sb);
+}
+
+// One work item: rows [row0, row0 + nrows) of expert e's group (at most TM),
+// output columns from n0 (mode_cols(MODE) of them).
+template <uint32_t MODE, uint32_t FLAGS>
+__device__ __forceinline__ void gemm_item(const GemmArgs& a, uint32_t e, uint32_t row0, uint32_t nrows, uint32_t n0,
+                                          uint16_t (&sA)[2][TM * LDS_STRIDE], int32_t* s_orow, uint32_t* s_sb) {
+  constexpr bool TWO = MODE != MODE_NARROW;
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  const uint32_t K = a.K, groups = K / GK;
 
   // Every load that depends on the work item alone is issued before any is
   // waited for: this thread's A row ids, the output row map, the tile's scales
@@ -455,6 +469,59 @@ __global__ void __launch_bounds__(256, 2) grouped_gemm_kernel(GemmArgs a) {
   }
 }
 
+// ---- the expert FFN of a prefill in one launch: the gate/up items, then the
+// down items, of each XCD. Workgroup l = 8p + x runs XCD x's p-th item: its
+// gate/up items first (p < g.work_count[x]), then its down items. Both
+// lists cover the same tiles per XCD (the tables split the tiles by their
+// combined cost), so a tile's H rows are written and read through one L2: a
+// gate/up item counts itself in tile_done[row0] once its H stores are
+// complete, and a down item starts when all ncb_gu of its tile's items have
+// counted. The dispatcher hands out workgroups in index order, so a waiting
+// down item waits only for gate/up items already running; the down items of
+// the first tiles fill the slots the last gate/up items leave idle. The wait
+// is bounded: a time-out sets g_ffn_err (read by obs_device_status) and the
+// item runs anyway, so the grid always drains.
+struct FfnSync {
+  int32_t* tile_done;  // per tile, at its first grouped row: gate/up items done
+  uint32_t ncb_gu;     // gate/up items per tile
+};
+__device__ uint32_t g_ffn_err;
+constexpr uint64_t FFN_WAIT_TICKS = 10000000ull;  // 100 ms of wall_clock64 (100 MHz)
+
+template <uint32_t MODE_DN>
+__global__ void __launch_bounds__(256, 2) moe_ffn_kernel(GemmArgs g, GemmArgs d, FfnSync sy) {
+  __shared__ uint16_t sA[2][TM * LDS_STRIDE];
+  __shared__ int32_t s_orow[TM];
+  extern __shared__ uint32_t s_sb[];
+  const uint32_t x = blockIdx.x % 8u, p = blockIdx.x / 8u, tid = threadIdx.x;
+  const uint32_t ngu = static_cast<uint32_t>(g.work_count[x]), ndn = static_cast<uint32_t>(d.work_count[x]);
+  if (p < ngu) {
+    const int4 w = g.work[blockIdx.x];
+    gemm_item<MODE_SWIGLU, F_WORK | F_AROWS>(g, static_cast<uint32_t>(w.x), static_cast<uint32_t>(w.y),
+                                             static_cast<uint32_t>(w.z), static_cast<uint32_t>(w.w), sA, s_orow, s_sb);
+    // this thread's H stores are complete (on gfx9 the vector memory counter
+    // counts stores too); then one add for the workgroup, in this XCD's L2
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    __syncthreads();
+    if (tid == 0) __hip_atomic_fetch_add(sy.tile_done + w.y, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  } else if (p - ngu < ndn) {
+    const int4 w = d.work[8u * (p - ngu) + x];
+    if (tid == 0) {
+      const uint64_t t0 = wall_clock64();
+      while (__hip_atomic_load(sy.tile_done + w.y, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) <
+             static_cast<int32_t>(sy.ncb_gu)) {
+        if (wall_clock64() - t0 > FFN_WAIT_TICKS) {
+          __hip_atomic_store(&g_ffn_err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+          break;
+        }
+      }
+    }
+    __syncthreads();
+    gemm_item<MODE_DN, F_WORK | F_OROWS>(d, static_cast<uint32_t>(w.x), static_cast<uint32_t>(w.y),
+                                         static_cast<uint32_t>(w.z), static_cast<uint32_t>(w.w), sA, s_orow, s_sb);
+  }
+}
+
 // ---- grouping: rows of expert e are its routed (token, rank) pairs in
 // ascending token order (forward.rs:203-204). Three launches: per 64-token
 // chunk counts, one scan, per chunk ranks + scatter.
@@ -528,10 +595,19 @@ constexpr ItemCost item_cost(uint32_t c1, uint32_t c2, uint32_t c3, uint32_t c4)
 }
 constexpr ItemCost COST_GATEUP = item_cost(66, 82, 98, 114);
 constexpr ItemCost COST_DOWN = item_cost(35, 41, 48, 54);
+// Per-tile cost of a tile's items in one GEMM (ncb of them), or in both GEMMs.
+constexpr ItemCost tile_cost(const ItemCost& c, uint32_t ncb) {
+  return item_cost(c.of(1) * ncb, c.of(2) * ncb, c.of(3) * ncb, c.of(4) * ncb);
+}
+constexpr ItemCost tile_cost2(const ItemCost& a, uint32_t na, const ItemCost& b, uint32_t nb) {
+  return item_cost(a.of(1) * na + b.of(1) * nb, a.of(2) * na + b.of(2) * nb, a.of(3) * na + b.of(3) * nb,
+                   a.of(4) * na + b.of(4) * nb);
+}
 constexpr uint32_t SCHED_MAX_TILES = 2048;  // tiles the cost-balanced schedule handles (else even split)
 
 // Workgroups a grouped GEMM launch needs for at most max_tiles tiles: an XCD's
-// cost share (total / 8) holds at most max_tiles * cmax / (8 * cmin) + 1 tiles.
+// cost share (total / 8) holds at most max_tiles * cmax / (8 * cmin) + 1 tiles
+// (cost: the per-tile cost the tiles are split by).
 uint32_t sched_grid(uint32_t max_tiles, uint32_t ncb, const ItemCost& cost) {
   const uint64_t cmin = cost.of(1), cmax = cost.of(4);
   const uint64_t per_xcd = (static_cast<uint64_t>(max_tiles) * cmax + 8u * cmin - 1u) / (8u * cmin) + 1u;
@@ -545,7 +621,8 @@ struct WorkTable {
   int4* work;
   int32_t* count;
   uint32_t grid, ncb, cols;
-  ItemCost cost;
+  ItemCost split;       // per-tile cost the tiles are split over the XCDs by
+  int32_t* tile_done;   // when set: zeroed at each tile's first row (the one-launch FFN's counters)
 };
 
 // Exclusive prefix sum over the wave (64 lanes) and the wave total.
@@ -583,7 +660,7 @@ struct SchedLds {
 __device__ void work_table_fill(const WorkTable W, uint32_t E, SchedLds& L) {  // by value: no scratch copy
   const uint32_t lane = threadIdx.x & 63u, T_all = static_cast<uint32_t>(L.toff[E]), slots = W.grid / 8u;
   const uint32_t ncb = W.ncb;
-  auto cost = [&](uint32_t nb) __attribute__((always_inline)) { return W.cost.of(nb) * ncb; };
+  auto cost = [&](uint32_t nb) __attribute__((always_inline)) { return W.split.of(nb); };
   auto item_of = [&](uint32_t e, uint32_t q, uint32_t cb) __attribute__((always_inline)) {
     const int32_t r0 = static_cast<int32_t>(q * TM);
     return make_int4(static_cast<int32_t>(e), L.roff[e] + r0, min(static_cast<int32_t>(TM), L.cnt[e] - r0),
@@ -613,7 +690,7 @@ __device__ void work_table_fill(const WorkTable W, uint32_t E, SchedLds& L) {  /
     }
     if (lane == 0) L.over = 0;
     __syncthreads();
-    // XCD of a tile: where its cost starts (32-bit: total <= 2048 tiles x 8 x 114)
+    // XCD of a tile: where its cost starts (32-bit: total <= 2048 tiles x 1,116)
     auto xcd_at = [&](uint32_t c) __attribute__((always_inline)) {
       return total ? min(7u, c * 8u / total) : 0u;
     };
@@ -644,6 +721,7 @@ __device__ void work_table_fill(const WorkTable W, uint32_t E, SchedLds& L) {  /
         uint32_t pos = field(v, nb) - field(lo, nb);  // same block count, earlier in this XCD
         for (uint32_t w = nb + 1u; w <= 4u; ++w) pos += field(hi, w) - field(lo, w);
         for (uint32_t cb = 0; cb < ncb; ++cb) W.work[8u * (pos * ncb + cb) + x] = item_of(e, q, cb);
+        if (W.tile_done) W.tile_done[L.roff[e] + static_cast<int32_t>(q * TM)] = 0;
         c += cost(nb);
         v += unit(nb);
       }
@@ -823,9 +901,11 @@ uint32_t gemm_grid(uint32_t tiles, uint32_t N, uint32_t mode) {
 }
 
 struct PrefillWs {
-  size_t logits, ids, w, counts, offsets, chunk_cnt, row_token, row_slot, work_gu, work_dn, work_cnt, H, Yp, Xn,
-      total;
+  size_t logits, ids, w, counts, offsets, chunk_cnt, row_token, row_slot, work_gu, work_dn, work_cnt, tile_done, H,
+      Yp, Xn, total;
   uint32_t max_tiles, nchunks, grid_gu, grid_dn;
+  bool ffn_one_launch;  // both GEMMs in moe_ffn_kernel (the tables then split tiles by their combined cost)
+  ItemCost split_gu, split_dn;
 };
 
 PrefillWs prefill_layout(const obs_moe_config* cfg, uint32_t T) {
@@ -843,11 +923,20 @@ PrefillWs prefill_layout(const obs_moe_config* cfg, uint32_t T) {
   L.chunk_cnt = o; o += al256(sizeof(int32_t) * L.nchunks * cfg->n_exp);
   L.row_token = o; o += al256(sizeof(int32_t) * R);
   L.row_slot = o; o += al256(sizeof(int32_t) * R);
-  L.grid_gu = sched_grid(L.max_tiles, cfg->inter / mode_cols(gemm_mode(true, cfg->inter)), COST_GATEUP);
-  L.grid_dn = sched_grid(L.max_tiles, cfg->hidden / mode_cols(gemm_mode(false, cfg->hidden)), COST_DOWN);
+  const uint32_t ncb_gu = cfg->inter / mode_cols(gemm_mode(true, cfg->inter));
+  const uint32_t ncb_dn = cfg->hidden / mode_cols(gemm_mode(false, cfg->hidden));
+  // One launch for both GEMMs needs the cost-balanced schedule for both tables
+  // (the even split would put a tile's down items on other XCDs than its
+  // gate/up items) and per-tile costs within 16 bits.
+  L.ffn_one_launch = L.max_tiles <= SCHED_MAX_TILES && COST_GATEUP.of(4) * ncb_gu + COST_DOWN.of(4) * ncb_dn < 65536u;
+  L.split_gu = L.ffn_one_launch ? tile_cost2(COST_GATEUP, ncb_gu, COST_DOWN, ncb_dn) : tile_cost(COST_GATEUP, ncb_gu);
+  L.split_dn = L.ffn_one_launch ? L.split_gu : tile_cost(COST_DOWN, ncb_dn);
+  L.grid_gu = sched_grid(L.max_tiles, ncb_gu, L.split_gu);
+  L.grid_dn = sched_grid(L.max_tiles, ncb_dn, L.split_dn);
   L.work_gu = o; o += al256(sizeof(int4) * L.grid_gu);
   L.work_dn = o; o += al256(sizeof(int4) * L.grid_dn);
   L.work_cnt = o; o += 256;  // items per XCD, gate/up then down
+  L.tile_done = o; o += al256(sizeof(int32_t) * R);  // by a tile's first row
   L.H = o; o += al256(sizeof(uint16_t) * R * cfg->inter);
   L.Yp = o; o += al256(sizeof(uint16_t) * R * cfg->hidden);
   L.Xn = o; o += al256(sizeof(uint16_t) * static_cast<size_t>(T) * cfg->hidden);  // rmsnorm(X) when layer->norm_w
@@ -904,7 +993,49 @@ int launch_gemm(obs_ctx* ctx, GemmArgs a, uint32_t grid, uint32_t mode) {
   return OBS_OK;
 }
 
+// The expert FFN of a grouped prefill in one launch (moe_ffn_kernel): the
+// gate/up items of g.work, then the down items of d.work, per XCD.
+int launch_ffn(obs_ctx* ctx, GemmArgs g, GemmArgs d, int32_t* tile_done, uint32_t ncb_gu, uint32_t grid,
+               uint32_t mode_dn) {
+  if (mode_dn == MODE_WIDE) {
+    d.w1 = d.w0 + static_cast<size_t>(TN) * (d.K / 8u);
+    d.s1 = d.s0 + static_cast<size_t>(TN) * (d.K / GK);
+    d.b1 = d.b0 + static_cast<size_t>(TN) * (d.K / GK);
+  }
+  const size_t lds = std::max(gemm_sb_bytes(MODE_SWIGLU, g.K), gemm_sb_bytes(mode_dn, d.K));
+  const void* fn = mode_dn == MODE_WIDE ? reinterpret_cast<const void*>(&moe_ffn_kernel<MODE_WIDE>)
+                                        : reinterpret_cast<const void*>(&moe_ffn_kernel<MODE_NARROW>);
+  static bool lds_raised[2] = {};
+  const int v = mode_dn == MODE_WIDE ? 0 : 1;
+  if (!lds_raised[v]) {
+    OBS_HIP_TRY(ctx, hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, SB_LDS_MAX));
+    lds_raised[v] = true;
+  }
+  FfnSync sy{tile_done, ncb_gu};
+  void* args[] = {&g, &d, &sy};
+  OBS_LAUNCH(ctx, "moe_ffn", OBS_HIP_TRY(ctx, hipLaunchKernel(fn, dim3(grid), dim3(256), args, lds, ctx->stream)));
+  return OBS_OK;
+}
+
 }  // namespace
+
+namespace obs {
+
+// The one-launch FFN's wait flag: reported (and cleared) like the fused
+// decode's time-outs.
+int ffn_status(obs_ctx* ctx) {
+  uint32_t err = 0;
+  OBS_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+  OBS_HIP_TRY(ctx, hipMemcpyFromSymbol(&err, HIP_SYMBOL(g_ffn_err), sizeof(err)));
+  if (err) {
+    const uint32_t zero = 0;
+    OBS_HIP_TRY(ctx, hipMemcpyToSymbol(HIP_SYMBOL(g_ffn_err), &zero, sizeof(zero)));
+    return set_error(ctx, OBS_E_HIP, "grouped prefill: a down item's wait for its tile timed out; its output is invalid");
+  }
+  return OBS_OK;
+}
+
+}  // namespace obs
 
 extern "C" {
 
@@ -966,8 +1097,10 @@ int obs_moe_prefill(obs_ctx* ctx, const obs_moe_config* cfg, const obs_moe_layer
              group_scan_kernel<<<1, 256, 0, ctx->stream>>>(L.nchunks, E, chunk_cnt, counts, offsets));
   const uint32_t cols_dn = mode_cols(gemm_mode(false, H));
   int32_t* work_cnt = reinterpret_cast<int32_t*>(base + L.work_cnt);
-  const WorkTable wt_gu{work_gu, work_cnt, L.grid_gu, I / TN, TN, COST_GATEUP};
-  const WorkTable wt_dn{work_dn, work_cnt + 8, L.grid_dn, H / cols_dn, cols_dn, COST_DOWN};
+  int32_t* tile_done = reinterpret_cast<int32_t*>(base + L.tile_done);
+  const WorkTable wt_gu{work_gu, work_cnt, L.grid_gu, I / TN, TN, L.split_gu, nullptr};
+  const WorkTable wt_dn{work_dn, work_cnt + 8, L.grid_dn, H / cols_dn, cols_dn, L.split_dn,
+                        L.ffn_one_launch ? tile_done : nullptr};
   OBS_LAUNCH(ctx, "moe_group_rank",
              group_rank_kernel<<<L.nchunks + 2u, 64, 0, ctx->stream>>>(ids, T, k, E, chunk_cnt, row_token, row_slot,
                                                                        counts, offsets, wt_gu, wt_dn));
@@ -978,16 +1111,21 @@ int obs_moe_prefill(obs_ctx* ctx, const obs_moe_config* cfg, const obs_moe_layer
   g.out = Hbuf; g.out_rows = nullptr;
   g.work = work_gu; g.work_count = work_cnt;
   g.K = H; g.N = I;
-  rc = launch_gemm(ctx, g, L.grid_gu, MODE_SWIGLU);
-  if (rc) return rc;
   GemmArgs d{};
   d.A = Hbuf; d.a_rows = nullptr; d.a_rows_total = T * k;
   d.w0 = layer->down_w; d.s0 = layer->down_s; d.b0 = layer->down_b;
   d.out = Yp; d.out_rows = row_slot;
   d.work = work_dn; d.work_count = work_cnt + 8;
   d.K = I; d.N = H;
-  rc = launch_gemm(ctx, d, L.grid_dn, gemm_mode(false, H));
-  if (rc) return rc;
+  if (L.ffn_one_launch) {
+    rc = launch_ffn(ctx, g, d, tile_done, I / TN, L.grid_gu + L.grid_dn, gemm_mode(false, H));
+    if (rc) return rc;
+  } else {
+    rc = launch_gemm(ctx, g, L.grid_gu, MODE_SWIGLU);
+    if (rc) return rc;
+    rc = launch_gemm(ctx, d, L.grid_dn, gemm_mode(false, H));
+    if (rc) return rc;
+  }
   OBS_LAUNCH(ctx, "moe_combine", combine_kernel<<<T, H / 8u, 0, ctx->stream>>>(Yp, ids, weights, residual, Y, k, H, E));
   return OBS_OK;
 }

@@ -30,6 +30,7 @@ KERNELS = {
     "decode_fused": (r"decode_fused_kernel<2>", ("csrc/obs_decode_fused.hip", "csrc/obs_internal.hpp")),
     "grouped_gemm_gateup": (r"grouped_gemm_kernel<1u, 3u>", ("csrc/obs_prefill.hip", "csrc/obs_internal.hpp")),
     "grouped_gemm_down": (r"grouped_gemm_kernel<2u, 5u>", ("csrc/obs_prefill.hip", "csrc/obs_internal.hpp")),
+    "moe_ffn": (r"moe_ffn_kernel<2u>", ("csrc/obs_prefill.hip", "csrc/obs_internal.hpp")),
     "moe_group_count": (r"group_count_kernel", ("csrc/obs_prefill.hip",)),
     "moe_group_scan": (r"group_scan_kernel", ("csrc/obs_prefill.hip",)),
     "moe_group_rank": (r"group_rank_kernel", ("csrc/obs_prefill.hip",)),
@@ -44,6 +45,8 @@ ALGORITHMIC = {
     "grouped_gemm_gateup": 128 * 2 * _PROJ + 2048 * 2048 * 2 + 2048 * 8 * 768 * 2,
     "grouped_gemm_down": 128 * _PROJ + 2048 * 8 * 768 * 2 + 2048 * 8 * 2048 * 2,
 }
+# both GEMMs in one launch: the same bytes (H is still written once and read once)
+ALGORITHMIC["moe_ffn"] = ALGORITHMIC["grouped_gemm_gateup"] + ALGORITHMIC["grouped_gemm_down"]
 
 
 def source_digest(kernel: str) -> Optional[str]:
