@@ -264,8 +264,9 @@ enum { OBS_DECODE_AUTO = 0, OBS_DECODE_MULTI = 1, OBS_DECODE_FUSED = 2 };
 int obs_set_decode_path(obs_ctx* ctx, int path);
 
 /* Waits for the stream, then reports (OBS_E_HIP + message) and clears a
- * device-side failure of the fused decode path (a bounded wait that timed
- * out); OBS_OK otherwise. The reference never checks GPU status. */
+ * device-side failure: a bounded wait that timed out in the fused decode
+ * path, the fused attention half or the grouped prefill's one-launch expert
+ * FFN; OBS_OK otherwise. The reference never checks GPU status. */
 int obs_device_status(obs_ctx* ctx);
 
 /* Workspace bytes obs_moe_prefill needs for T tokens. */
@@ -279,7 +280,10 @@ size_t obs_moe_prefill_workspace(const obs_moe_config* cfg, uint32_t T);
  * or injected (ids, weights [T, top_k] device arrays; ids must be in range and
  * distinct per token). Tokens are permuted into per-expert groups on the GPU,
  * gate/up/down run as grouped dequant-to-LDS bf16 MFMA GEMMs with a SwiGLU
- * epilogue, and outputs are combined per token in rank order in fp32.
+ * epilogue (up to 2,048 row tiles both GEMMs share one launch whose down
+ * items wait, bounded, for their tile's gate/up items: obs_device_status
+ * reports a time-out), and outputs are combined per token in rank order in
+ * fp32.
  * X, Y bf16 [T, hidden]; residual (nullable) and layer->norm_w as in
  * obs_moe_decode (the norm runs as one more launch into the workspace).
  * ws: caller-owned device workspace of obs_moe_prefill_workspace() bytes. */
