@@ -27,10 +27,11 @@
 //   3. h = silu(gate.x) * (up.x) goes to the group's h slots; each workgroup
 //      polls them into LDS in three blocks, adding each block's terms to its 64
 //      down rows as the block arrives (the down weights are in registers).
-//   4. Group 0 combines: workgroup j polls the 8 ranks' outputs for its 64 rows
+//   4. Every workgroup combines 8 rows: it polls the 8 ranks' outputs for them
 //      and accumulates residual + sum_r w_r * y_r in rank order (forward.rs:440).
-//      (Spreading the combine over all 256 workgroups, 8 rows each, measured
-//      1 us slower per layer: every workgroup then waits on other XCDs.)
+//      (Group 0 alone, 64 rows per workgroup, measured 0.2 us slower per layer
+//      once the launch count took one atomic instead of 256; with 256 exit
+//      atomics at once the spread combine had been 1 us slower.)
 // The logit and h slots are written and polled within one XCD and live in its
 // L2; the y slots cross XCDs and are written through to memory.
 // The epoch is derived from a device-side count of exited workgroups (see the
@@ -525,28 +526,28 @@ __global__ void __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 
   }
 
   OBS_FUSED_MARK(7);
-  // ---- 7. group 0: combine the 8 ranks for rows [64j, 64j + 64) in rank order
-  if (g == 0) {
+  // ---- 7. every workgroup combines the 8 ranks for its 8 rows 256 g + 8 j ..
+  // in rank order (wave 0: lane 8 r + i polls rank r's row i). Group 0 alone,
+  // 64 rows per workgroup: 10.87 against 10.66 us per layer.
+  if (wave == 0) {
+    const uint32_t row0c = 256u * g + 8u * j;
     bool wave_ok = ok;
     const uint64_t t0 = wall_clock64();
+    float yv = 0.0f;
     while (wave_ok) {
-      bool ready = true;
-#pragma unroll
-      for (uint32_t u = 0; u < 2; ++u) {
-        const uint32_t s = tid + 256u * u;  // rank s/64, row s%64
-        const uint64_t v = slot_load(y_slots + size_t(s >> 6) * FH + DN_ROWS_WG * j + (s & 63u));
-        s_y[s >> 6][s & 63u] = slot_val(v);
-        ready = ready && slot_ready(v, epoch);
-      }
-      if (__all(ready)) break;
+      const uint64_t v = slot_load(y_slots + size_t(lane >> 3) * FH + row0c + (lane & 7u));  // rank lane/8, row lane%8
+      yv = slot_val(v);
+      if (__all(slot_ready(v, epoch))) break;
       if (wall_clock64() - t0 > WAIT_TICKS) {
         wave_ok = false;
         if (lane == 0) raise_error(a.ws);
       }
     }
-    __syncthreads();
-    if (wave == 0) {
-      const uint32_t o = DN_ROWS_WG * j + lane;
+    s_y[lane >> 3][lane & 7u] = yv;
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    if (lane < 8u) {
+      const uint32_t o = row0c + lane;
       float acc = a.residual ? bf16_to_f32(a.residual[o]) : 0.0f;
 #pragma unroll
       for (uint32_t r = 0; r < FK; ++r) acc = __builtin_fmaf(readlane_f32(sel_w, static_cast<int>(r)), s_y[r][lane], acc);
