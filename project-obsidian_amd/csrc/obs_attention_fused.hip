@@ -30,7 +30,7 @@
 //   4. every workgroup polls the group's 512 attention outputs into LDS and
 //      computes, for its 64 rows of W_o, the partial product over the group's
 //      512 columns, published across XCDs;
-//   5. group 0 sums the 8 groups' partials per row with the residual:
+//   5. every workgroup sums the 8 groups' partials of 8 rows with the residual:
 //      x1 = x + sum_g partial_g, in group order, rounded once to bf16.
 // (The earlier split of the same work over the whole grid exchanged q/k/v,
 // the split partials and the attention outputs across XCDs, three round trips
@@ -492,8 +492,8 @@ attn_fused_kernel(AttnArgs a) {
       o[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, vbf, o[nt], 0, 0, 0);
     }
   }
-  // the o rows (used after two more exchanges) and, for group 0, the residual
-  // of the rows it finishes
+  // the o rows (used after two more exchanges) and the residual of the 8 rows
+  // it finishes
 #pragma unroll
   for (uint32_t p = 0; p < 2; ++p) {
     const size_t r = orow0 + 8u * p;
@@ -504,7 +504,7 @@ attn_fused_kernel(AttnArgs a) {
     osc[p] = a.o_s[gi];
     obi[p] = a.o_b[gi];
   }
-  const uint16_t ores = a.x[A_ORWG * j + (lane & 63u)];  // group 0, wave 0: row 64 j + lane
+  const uint16_t ores = a.x[256u * g + 8u * j + (lane & 7u)];  // wave 0, lanes 0-7: row 256 g + 8 j + lane
   OBS_ATTN_MARK(5);
   // the wave's partial: m, l per head column (l summed over the four gq lanes), O rows 4 gq + i
   l_run += lane_xor16_f32(l_run, lane);
@@ -667,35 +667,36 @@ attn_fused_kernel(AttnArgs a) {
         acc = dot8_q4_off(oq[p][sg].w, ah[sg] + 12, acc);
       }
       const float part = group8_sum(__builtin_fmaf(bf16_to_f32(osc[p]), acc - aoff, bf16_to_f32(obi[p]) * asum));
-      if (oc == 0u) slot_store(y_slots + size_t(g) * AH + orow0 + 8u * p, epoch, part);  // polled by group 0
+      if (oc == 0u) slot_store(y_slots + size_t(g) * AH + orow0 + 8u * p, epoch, part);  // polled across XCDs
     }
   }
   OBS_ATTN_MARK(10);
-  // ---- 5. group 0: x1 = x + sum of the 8 groups' partials, rows 64 j .. + 64
-  if (g == 0) {
+  // ---- 5. x1 = x + sum of the 8 groups' partials, rows 256 g + 8 j .. + 8, in
+  // every workgroup (wave 0: lane 8 q + i polls group q's row i). Group 0
+  // alone, 64 rows per workgroup: decoder 810-811 against 816 tokens/s.
+  static_assert(AH == ANGRP * AWPG * 8u, "8 residual rows per workgroup");
+  if (wave == 0) {
+    const uint32_t row0c = 256u * g + 8u * j;
     bool ok = s_fail == 0;
     const uint64_t t0 = wall_clock64();
+    float yv = 0.0f;
     while (ok) {
-      bool ready = true;
-#pragma unroll
-      for (uint32_t u = 0; u < 2; ++u) {
-        const uint32_t sidx = tid + 256u * u;  // group sidx / 64, row sidx % 64
-        const uint64_t v = slot_load(y_slots + size_t(sidx >> 6) * AH + A_ORWG * j + (sidx & 63u));
-        s_y[sidx >> 6][sidx & 63u] = slot_val(v);
-        ready = ready && slot_ready(v, epoch);
-      }
-      if (__all(ready)) break;
+      const uint64_t v = slot_load(y_slots + size_t(lane >> 3) * AH + row0c + (lane & 7u));  // group lane/8, row lane%8
+      yv = slot_val(v);
+      if (__all(slot_ready(v, epoch))) break;
       if (wall_clock64() - t0 > A_WAIT_TICKS) {
         ok = false;
         if (lane == 0) s_fail = 1;
       }
     }
-    __syncthreads();
-    if (wave == 0) {
+    s_y[lane >> 3][lane & 7u] = yv;
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    if (lane < 8u) {
       float acc = bf16_to_f32(ores);
 #pragma unroll
       for (uint32_t q = 0; q < ANGRP; ++q) acc += s_y[q][lane];
-      a.x1[A_ORWG * j + lane] = f32_to_bf16(acc);
+      a.x1[row0c + lane] = f32_to_bf16(acc);
     }
   }
   __syncthreads();
