@@ -269,6 +269,30 @@ int obs_set_decode_path(obs_ctx* ctx, int path);
  * FFN; OBS_OK otherwise. The reference never checks GPU status. */
 int obs_device_status(obs_ctx* ctx);
 
+/* Dispatch facts and the one-launch paths they allow (no reference
+ * counterpart: the reference's executor setup, executor.rs:39-58, probes
+ * nothing). obs_create runs two small probe kernels: one records the XCD each
+ * workgroup of a 256-workgroup grid runs on (the fused kernels keep each
+ * group of 32 workgroups, those with one b % 8, inside one XCD's L2, and the
+ * 8 groups on 8 XCDs), one checks that each XCD starts its workgroups in index order (the
+ * one-launch prefill FFN's down items wait for lower-index gate/up items).
+ * obs_dispatch_gate is the pure rule (no device needed): the OBS_PATH_* bits
+ * a device with num_cus CUs and those facts may take; the other paths run as
+ * separate launches. obs_set_dispatch_facts overrides the probed facts
+ * (tests; a caller that knows better). */
+enum { OBS_PATH_FUSED_DECODE = 1, OBS_PATH_FUSED_ATTN = 2, OBS_PATH_FFN_ONE_LAUNCH = 4 };
+uint32_t obs_dispatch_gate(int num_cus, int xcd_map_ok, int inorder_ok);
+int obs_dispatch_info(const obs_ctx* ctx, int* num_cus, int* xcd_map_ok, int* inorder_ok);
+int obs_set_dispatch_facts(obs_ctx* ctx, int xcd_map_ok, int inorder_ok);
+
+/* Testing hook (no reference counterpart): makes the one-launch prefill FFN's
+ * down items of this context wait for extra_count more counts than their
+ * tile's gate/up items give, with a wait limit of wait_us (1..100,000 us), so
+ * the bounded wait's time-out report can be exercised from the host: every
+ * kernel still exits normally, obs_device_status then reports OBS_E_HIP once
+ * and clears the flag. extra_count 0 and wait_us 100000 restore the defaults. */
+int obs_debug_ffn_wait(obs_ctx* ctx, uint32_t extra_count, uint32_t wait_us);
+
 /* Workspace bytes obs_moe_prefill needs for T tokens. */
 size_t obs_moe_prefill_workspace(const obs_moe_config* cfg, uint32_t T);
 
@@ -279,11 +303,12 @@ size_t obs_moe_prefill_workspace(const obs_moe_config* cfg, uint32_t T);
  * (4 * T * top_k + 255) / 256 * 256, where read_route reads it, forward.rs:175-182)
  * or injected (ids, weights [T, top_k] device arrays; ids must be in range and
  * distinct per token). Tokens are permuted into per-expert groups on the GPU,
- * gate/up/down run as grouped dequant-to-LDS bf16 MFMA GEMMs with a SwiGLU
- * epilogue (up to 2,048 row tiles both GEMMs share one launch whose down
- * items wait, bounded, for their tile's gate/up items: obs_device_status
- * reports a time-out), and outputs are combined per token in rank order in
- * fp32.
+ * gate/up/down run as grouped bf16 MFMA GEMMs (the gathered activation rows
+ * staged in LDS; the 4-bit weights dequantized in registers, bf16 =
+ * RNE(fp32(q*s + b))) with a SwiGLU epilogue (up to 2,048 row tiles both
+ * GEMMs share one launch whose down items wait, bounded, for their tile's
+ * gate/up items: obs_device_status of the calling context reports a
+ * time-out), and outputs are combined per token in rank order in fp32.
  * X, Y bf16 [T, hidden]; residual (nullable) and layer->norm_w as in
  * obs_moe_decode (the norm runs as one more launch into the workspace).
  * ws: caller-owned device workspace of obs_moe_prefill_workspace() bytes. */

@@ -62,7 +62,7 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
 constexpr uint32_t AH = 2048, ANH = 32, ANKV = 4, AHD = 128, AG = ANH / ANKV;  // G = 8
-constexpr uint32_t AQD = ANH * AHD, AKVD = ANKV * AHD;                          // 4096, 512
+constexpr uint32_t AQD = ANH * AHD;                                              // 4096
 constexpr uint32_t ANGRP = 8, AWPG = 32, ANWG = ANGRP * AWPG;                   // groups, WGs per group
 constexpr uint32_t AQPG = ANH / ANGRP;           // query heads per group: 4
 constexpr uint32_t AGQD = AQPG * AHD;            // the group's attention outputs: 512
@@ -730,6 +730,10 @@ int attn_fused_status(obs_ctx* ctx) {
 
 }  // namespace obs
 
+namespace obs {
+uint32_t fused_attn_workgroups() { return ANWG; }
+}  // namespace obs
+
 extern "C" {
 
 int obs_attn_decode(obs_ctx* ctx, const obs_attn_layer* L, const uint16_t* x, uint16_t* k_cache,
@@ -750,9 +754,11 @@ int obs_attn_decode(obs_ctx* ctx, const obs_attn_layer* L, const uint16_t* x, ui
       !obs::aligned(L->q_norm, 4) || !obs::aligned(L->k_norm, 4) || !obs::aligned(k_cache, 16) ||
       !obs::aligned(v_cache_t, 16))
     return obs::set_error(ctx, OBS_E_ALIGN, "obs_attn_decode: weights, x and the caches must be 16-byte aligned");
-  if (ctx->num_cus < static_cast<int>(ANWG))
-    return obs::set_error(ctx, OBS_E_UNSUPPORTED, "obs_attn_decode: needs %u CUs (the device has %d)", ANWG,
-                          ctx->num_cus);
+  if (!(obs::dispatch_gate(ctx->num_cus, ctx->xcd_map_ok, ctx->inorder_ok) & OBS_PATH_FUSED_ATTN))
+    return obs::set_error(ctx, OBS_E_UNSUPPORTED,
+                          "obs_attn_decode: needs %u CUs, one workgroup per CU, each group b %% 8 on one XCD "
+                          "(the device has %d CUs; XCD map %s)",
+                          ANWG, ctx->num_cus, ctx->xcd_map_ok ? "as expected" : "not as expected");
   if (!ctx->attn_ws) {
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     OBS_HIP_TRY(ctx, hipStreamIsCapturing(ctx->stream, &cs));

@@ -55,6 +55,40 @@ __global__ void hold_kernel(uint64_t ticks) {
   const uint64_t t0 = wall_clock64();
   while (wall_clock64() - t0 < ticks) __builtin_amdgcn_s_sleep(64);
 }
+
+// Dispatch probes (obs_create). xcd_probe_kernel: workgroup b of a grid shaped
+// like the fused kernels' (256 workgroups of 256 threads, one per CU) records
+// the XCD it runs on (the hardware XCC_ID register, an index below 32).
+constexpr uint32_t PROBE_XCD_GRID = 256;
+__global__ void __launch_bounds__(256, 1) xcd_probe_kernel(uint32_t* xcc) {
+  if (threadIdx.x != 0) return;
+  uint32_t id;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(id));
+  xcc[blockIdx.x] = id & 0xfu;
+}
+
+// order_probe_kernel: a grid of many more workgroups than can be resident at
+// once. Workgroup b marks itself started, then waits (bounded) until
+// workgroup b - 8, the previous one of its XCD under the round-robin deal, has
+// started. When the dispatcher starts each XCD's workgroups in index order the
+// predecessor is always running or done and every wait ends at once; when a
+// workgroup could hold a slot its predecessor needs, the wait runs out and the
+// grid reports it.
+constexpr uint32_t PROBE_ORDER_GRID = 8192;
+constexpr uint64_t PROBE_WAIT_TICKS = 1000000ull;  // 10 ms of the 100 MHz clock
+__global__ void __launch_bounds__(256) order_probe_kernel(uint32_t* started, uint32_t* late) {
+  if (threadIdx.x != 0) return;
+  const uint32_t b = blockIdx.x;
+  __hip_atomic_store(started + b, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  if (b < 8u) return;
+  const uint64_t t0 = wall_clock64();
+  while (__hip_atomic_load(started + b - 8u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u) {
+    if (wall_clock64() - t0 > PROBE_WAIT_TICKS) {
+      __hip_atomic_store(late, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      break;
+    }
+  }
+}
 }  // namespace
 
 namespace obs {
@@ -82,6 +116,48 @@ int prof_begin(obs_ctx* ctx, const char* name) {
 int prof_end(obs_ctx* ctx) {
   if (!ctx->prof_on || ctx->prof_pairs.empty()) return OBS_OK;
   OBS_HIP_TRY(ctx, hipEventRecord(ctx->prof_pairs.back().e1, ctx->stream));
+  return OBS_OK;
+}
+
+uint32_t dispatch_gate(int num_cus, bool xcd_map_ok, bool inorder_ok) {
+  uint32_t paths = 0;
+  if (num_cus >= static_cast<int>(fused_decode_workgroups()) && xcd_map_ok) paths |= OBS_PATH_FUSED_DECODE;
+  if (num_cus >= static_cast<int>(fused_attn_workgroups()) && xcd_map_ok) paths |= OBS_PATH_FUSED_ATTN;
+  if (xcd_map_ok && inorder_ok) paths |= OBS_PATH_FFN_ONE_LAUNCH;
+  return paths;
+}
+
+int probe_dispatch(obs_ctx* ctx) {
+  ctx->xcd_map_ok = ctx->inorder_ok = false;
+  uint32_t* d = nullptr;
+  const size_t words = PROBE_XCD_GRID + PROBE_ORDER_GRID + 64;
+  OBS_HIP_TRY(ctx, hipMalloc(&d, words * sizeof(uint32_t)));
+  uint32_t* xcc = d;
+  uint32_t* started = d + PROBE_XCD_GRID;
+  uint32_t* late = started + PROBE_ORDER_GRID;
+  std::vector<uint32_t> h(PROBE_XCD_GRID + 1);
+  hipError_t e = hipMemsetAsync(d, 0, words * sizeof(uint32_t), ctx->stream);
+  if (e == hipSuccess) {
+    xcd_probe_kernel<<<PROBE_XCD_GRID, 256, 0, ctx->stream>>>(xcc);
+    order_probe_kernel<<<PROBE_ORDER_GRID, 256, 0, ctx->stream>>>(started, late);
+    e = hipGetLastError();
+  }
+  if (e == hipSuccess) e = hipMemcpyAsync(h.data(), xcc, PROBE_XCD_GRID * sizeof(uint32_t), hipMemcpyDeviceToHost, ctx->stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(h.data() + PROBE_XCD_GRID, late, sizeof(uint32_t), hipMemcpyDeviceToHost, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  (void)hipFree(d);
+  if (e != hipSuccess) return set_error(ctx, OBS_E_HIP, "dispatch probe failed: %s", hipGetErrorString(e));
+  // The fused kernels need each group (workgroups b with one b % 8) inside one
+  // XCD, and the 8 groups on 8 different XCDs. Which XCD takes group 0 may
+  // change from launch to launch (the dispatcher's round-robin continues from
+  // the previous dispatch), so only that structure is checked.
+  bool map = true;
+  uint32_t seen = 0;
+  for (uint32_t b = 0; b < PROBE_XCD_GRID; ++b) map = map && h[b] == h[b % 8u] && h[b] < 32u;
+  for (uint32_t g = 0; g < 8u && map; ++g) seen |= 1u << h[g];
+  map = map && __builtin_popcount(seen) == 8;
+  ctx->xcd_map_ok = map;
+  ctx->inorder_ok = h[PROBE_XCD_GRID] == 0u;
   return OBS_OK;
 }
 
@@ -141,13 +217,20 @@ int obs_create(int device, obs_ctx** out) {
   ctx->stream = ctx->own_stream;
   std::string serr;
   ctx->scratch = device_scratch(device, &serr);
-  if (!ctx->scratch) {
-    g_create_error = serr;
-    (void)hipEventDestroy(ctx->ev_start);
-    (void)hipEventDestroy(ctx->ev_stop);
-    (void)hipStreamDestroy(ctx->own_stream);
-    delete ctx;
-    return OBS_E_HIP;
+  int rc = ctx->scratch ? OBS_OK : OBS_E_HIP;
+  if (rc == OBS_OK) {
+    if (hipMalloc(&ctx->status_dev, obs::CTX_ST_WORDS * sizeof(uint32_t)) != hipSuccess ||
+        hipMemset(ctx->status_dev, 0, obs::CTX_ST_WORDS * sizeof(uint32_t)) != hipSuccess) {
+      serr = "status words: hipMalloc/hipMemset failed";
+      rc = OBS_E_HIP;
+    }
+  }
+  if (rc == OBS_OK) rc = obs::probe_dispatch(ctx);
+  if (rc == OBS_OK) rc = obs::prefill_init(ctx);
+  if (rc != OBS_OK) {
+    g_create_error = serr.empty() ? ctx->err : serr;
+    obs_destroy(ctx);
+    return rc;
   }
   *out = ctx;
   return OBS_OK;
@@ -161,6 +244,7 @@ void obs_destroy(obs_ctx* ctx) {
   if (ctx->decode_ws) (void)hipFree(ctx->decode_ws);
   if (ctx->fused_ws) (void)hipFree(ctx->fused_ws);
   if (ctx->attn_ws) (void)hipFree(ctx->attn_ws);
+  if (ctx->status_dev) (void)hipFree(ctx->status_dev);
   for (const auto& r : ctx->rope_tables) (void)hipFree(r.table);
   for (void* p : ctx->retired) (void)hipFree(p);
   if (ctx->ev_start) (void)hipEventDestroy(ctx->ev_start);
@@ -323,6 +407,34 @@ int obs_profile_stat(const obs_ctx* ctx, int i, const char** name, double* total
   if (name) *name = s.name;
   if (total_ms) *total_ms = s.total_ms;
   if (launches) *launches = s.launches;
+  return OBS_OK;
+}
+
+uint32_t obs_dispatch_gate(int num_cus, int xcd_map_ok, int inorder_ok) {
+  return obs::dispatch_gate(num_cus, xcd_map_ok != 0, inorder_ok != 0);
+}
+
+int obs_dispatch_info(const obs_ctx* ctx, int* num_cus, int* xcd_map_ok, int* inorder_ok) {
+  if (!ctx) return OBS_E_INVALID;
+  if (num_cus) *num_cus = ctx->num_cus;
+  if (xcd_map_ok) *xcd_map_ok = ctx->xcd_map_ok ? 1 : 0;
+  if (inorder_ok) *inorder_ok = ctx->inorder_ok ? 1 : 0;
+  return OBS_OK;
+}
+
+int obs_set_dispatch_facts(obs_ctx* ctx, int xcd_map_ok, int inorder_ok) {
+  if (!ctx) return OBS_E_INVALID;
+  ctx->xcd_map_ok = xcd_map_ok != 0;
+  ctx->inorder_ok = inorder_ok != 0;
+  return OBS_OK;
+}
+
+int obs_debug_ffn_wait(obs_ctx* ctx, uint32_t extra_count, uint32_t wait_us) {
+  if (!ctx) return OBS_E_INVALID;
+  if (wait_us == 0u || wait_us > 100000u)
+    return obs::set_error(ctx, OBS_E_INVALID, "obs_debug_ffn_wait: wait_us must be 1..100000 (got %u)", wait_us);
+  ctx->ffn_extra_count = extra_count;
+  ctx->ffn_wait_ticks = static_cast<uint64_t>(wait_us) * 100u;  // the constant clock runs at 100 MHz
   return OBS_OK;
 }
 

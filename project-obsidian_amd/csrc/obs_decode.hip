@@ -278,14 +278,16 @@ int decode_plan(obs_ctx* ctx, const char* who, const obs_moe_config* cfg, const 
   if (!aligned(x, 16)) return set_error(ctx, OBS_E_ALIGN, "%s: x must be 16-byte aligned", who);
   const bool shape_ok = fused_decode_supported(cfg);
   // the one-launch path spins on values other workgroups publish: all of its
-  // workgroups must be resident at once, one per CU
-  const bool cus_ok = ctx->num_cus >= static_cast<int>(fused_decode_workgroups());
+  // workgroups must be resident at once, one per CU, and each group of 32 must
+  // share an XCD (its L2) as the probe at obs_create found
+  const bool cus_ok = (dispatch_gate(ctx->num_cus, ctx->xcd_map_ok, ctx->inorder_ok) & OBS_PATH_FUSED_DECODE) != 0u;
   if (ctx->decode_path == OBS_DECODE_FUSED && !shape_ok)
     return set_error(ctx, OBS_E_SHAPE, "%s: the fused path needs hidden 2048, inter 768, top_k 8, group 64, n_exp <= 256",
                      who);
   if (ctx->decode_path == OBS_DECODE_FUSED && !cus_ok)
-    return set_error(ctx, OBS_E_UNSUPPORTED, "%s: the fused path needs %u CUs (the device has %d)", who,
-                     fused_decode_workgroups(), ctx->num_cus);
+    return set_error(ctx, OBS_E_UNSUPPORTED,
+                     "%s: the fused path needs %u CUs with each group b %% 8 on one XCD (the device has %d CUs; XCD map %s)",
+                     who, fused_decode_workgroups(), ctx->num_cus, ctx->xcd_map_ok ? "as expected" : "not as expected");
   *fused = shape_ok && cus_ok && ctx->decode_path != OBS_DECODE_MULTI;
   return OBS_OK;
 }

@@ -133,11 +133,11 @@ __global__ void __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 
   constexpr int RT = NQ / 2;  // router rows per wave
   __shared__ uint32_t s_epoch;
   __shared__ int s_abort;
-  __shared__ int32_t s_ids[FK];
-  __shared__ float s_p[FK];
-  __shared__ uint64_t s_comp[MAX_E];  // routing: (p bits << 9) | (511 - id), 0 = not selectable
   __shared__ float s_y[FK][64];
-  __shared__ bool s_ok;
+  __shared__ __attribute__((aligned(16))) uint64_t s_ck[4][MAX_E / 4];  // routing: each wave's share of the keys
+  __shared__ uint32_t s_cnt[4][MAX_E];                                // routing: each wave's partial counts
+  __shared__ int32_t s_sel_id[FK];                                    // routing: expert of each rank (-1: none)
+  __shared__ float s_sel_p[FK];                                       // routing: its p
   __shared__ __attribute__((aligned(16))) f16x2_t s_hp[FI / 2];  // h as f16 pairs, dot8_q4_off order
   __shared__ float s_hsum[FI / 32], s_hoff[FI / 32];              // per 32 columns: sum h, sum off*h
   __shared__ __attribute__((aligned(16))) uint16_t s_sc[4][1536];  // per wave: staged scales (see phase 3)
@@ -177,6 +177,7 @@ __global__ void __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 
     rs[t] = a.router_s[size_t(e) * (FH / FG) + lane / 2u];
     rb[t] = a.router_b[size_t(e) * (FH / FG) + lane / 2u];
   }
+  if (tid < FK) s_sel_id[tid] = -1;
   // after the activation and router loads, so its two reads overlap them
   if (tid == 0) {
     // Workgroup 0 adds 1 to the count as it exits, and only after every
@@ -220,18 +221,6 @@ __global__ void __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 
       xf[c + 1] = bf16hi(pr);
     }
   }
-  float xs = 0.0f;
-#pragma unroll
-  for (int c = 0; c < 32; ++c) xs = xs + xf[c];
-  // the lane's 32 activations as f16 pairs for the expert rows, and the offset
-  // part of dot8_q4_off over them (shared by every row)
-  f16x2_t xh[16];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) f16_pairs8(xf + 8 * i, xh + 4 * i);
-  float xoff = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) xoff = dot8_off_only(xh + 4 * i, xoff);
-
   // ---- 1. router logits (order of obs_q8_gate_logits: serial fma, then wave_sum_asc)
 #pragma unroll
   for (int t = 0; t < RT; ++t) {
@@ -250,21 +239,36 @@ __global__ void __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 
       if (lane == 0) slot_store_xcd(logit_slots + e, epoch, acc);  // polled by this XCD only
     }
   }
+  // While the logits travel: the lane's 32 activations as f16 pairs for the
+  // expert rows, their sum and the offset part of dot8_q4_off over them
+  // (shared by every row).
+  float xs = 0.0f;
+#pragma unroll
+  for (int c = 0; c < 32; ++c) xs = xs + xf[c];
+  f16x2_t xh[16];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) f16_pairs8(xf + 8 * i, xh + 4 * i);
+  float xoff = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) xoff = dot8_off_only(xh + 4 * i, xoff);
 
   OBS_FUSED_MARK(2);
-  // ---- 2. routing (moe_routing_topk.metal:24-56). Wave 0 polls its group's
-  // logits and turns them into selection keys (route_keys: the softmax p of
-  // each expert, from the f16-rounded logits under the reference rule). The k
-  // argmax rounds of the reference (largest p, lowest id on ties) select the
-  // experts that fewer than k others precede in that order, in that order; so
-  // all 256 threads count, in parallel, how many experts precede each one
-  // (composite keys make the order strict), and the experts with a count below
-  // k take the slot of that count. (Every wave computing the keys into its own
-  // LDS copy, to spare the barrier between keys and count, measured 0.07 us
-  // slower per layer.)
+  // ---- 2. routing (moe_routing_topk.metal:24-56). Every wave polls its
+  // group's logits and turns them into selection keys itself (route_keys: the
+  // softmax p of each expert, from the f16-rounded logits under the reference
+  // rule), so all four waves hold the same keys without an exchange. The k
+  // argmax rounds of the reference (largest p, lowest id on ties) select
+  // exactly the experts that fewer than k others precede in that order, in
+  // that order; composite keys (p << 9) | (511 - id) make the order strict.
+  // Each wave counts, for all experts (NQ per lane), the composites that
+  // exceed theirs among its quarter of the experts (read back from its own LDS
+  // area as broadcasts), and one barrier adds the four partial counts. (All
+  // 256 threads counting one expert against half of all keys was bound by the
+  // LDS broadcast reads, 0.70 us; eight argmax rounds on one wave were bound by
+  // their serial latency, ~1 us.)
   bool ok = true;
   float lg[NQ];
-  if (wave == 0) {
+  {
     const uint64_t t0 = wall_clock64();
     while (true) {
       // all slot loads in flight together (clamped index, no per-load branch)
@@ -283,46 +287,44 @@ __global__ void __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 
   }
   OBS_FUSED_MARK(9);
   if (!ok && lane == 0) raise_error(a.ws);
-  if (wave == 0) {
-    int key[NQ];
-    route_keys<NQ>(lg, n_exp, lane, a.route_rule, key);
+  int key[NQ];
+  route_keys<NQ>(lg, n_exp, lane, a.route_rule, key);
+  constexpr uint32_t QW = 16u * NQ;  // experts per wave's share: [QW * wave, QW * (wave + 1))
+  uint64_t ck[NQ];
 #pragma unroll
-    for (int q = 0; q < NQ; ++q) {
-      const uint32_t id = lane + 64u * q;
-      s_comp[id] = key[q] >= 0 ? (static_cast<uint64_t>(key[q]) << 9) | (511u - id) : 0ull;
-    }
-    if (lane < FK) {
-      s_ids[lane] = -1;
-      s_p[lane] = 0.0f;
-      s_ok = ok;
-    }
+  for (int q = 0; q < NQ; ++q) {
+    const uint32_t id = lane + 64u * q;
+    ck[q] = key[q] >= 0 ? (static_cast<uint64_t>(key[q]) << 9) | (511u - id) : 0ull;
+    if (id / QW == wave) s_ck[wave][id % QW] = ck[q];
   }
-  __syncthreads();
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");  // the wave's own LDS stores before its reads
+  __builtin_amdgcn_wave_barrier();
   {
-    constexpr uint32_t TPE = 4 / NQ;         // threads per expert
-    constexpr uint32_t CMP = 64 * NQ / TPE;  // composites each thread compares against
-    const uint32_t ei = tid / TPE, part = tid % TPE;
-    const uint64_t ci = s_comp[ei];
-    const uint64_t* cj = s_comp + part * CMP;
-    uint32_t c0 = 0, c1 = 0, c2 = 0, c3 = 0;  // four chains: independent adds
+    uint32_t c[NQ];
 #pragma unroll
-    for (uint32_t c = 0; c < CMP; c += 4) {
-      c0 += cj[c] > ci;
-      c1 += cj[c + 1] > ci;
-      c2 += cj[c + 2] > ci;
-      c3 += cj[c + 3] > ci;
+    for (int q = 0; q < NQ; ++q) c[q] = 0;
+    const uint4* cw = reinterpret_cast<const uint4*>(s_ck[wave]);
+#pragma unroll
+    for (uint32_t i = 0; i < QW / 2; ++i) {
+      const uint4 v = cw[i];
+      const uint64_t c0 = (static_cast<uint64_t>(v.y) << 32) | v.x, c1 = (static_cast<uint64_t>(v.w) << 32) | v.z;
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) c[q] += static_cast<uint32_t>(c0 > ck[q]) + static_cast<uint32_t>(c1 > ck[q]);
     }
-    uint32_t rank = (c0 + c1) + (c2 + c3);
-    if constexpr (TPE >= 2) rank += static_cast<uint32_t>(dpp_i32<DPP_XOR1>(static_cast<int>(rank)));
-    if constexpr (TPE >= 4) rank += static_cast<uint32_t>(dpp_i32<DPP_XOR2>(static_cast<int>(rank)));
-    if (part == 0 && ci != 0ull && rank < FK) {
-      s_ids[rank] = static_cast<int32_t>(ei);
-      s_p[rank] = __uint_as_float(static_cast<uint32_t>(ci >> 9));
-    }
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) s_cnt[wave][lane + 64u * q] = c[q];
   }
   __syncthreads();
-  ok = ok && s_ok;
-  const int32_t eg = s_ids[g];
+  // rank of each of the lane's experts; the group's expert has rank g
+  uint32_t rank[NQ];
+  int32_t eg = -1;
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    const uint32_t id = lane + 64u * q;
+    rank[q] = (s_cnt[0][id] + s_cnt[1][id]) + (s_cnt[2][id] + s_cnt[3][id]);
+    const unsigned long long m = __ballot(ck[q] != 0ull && rank[q] == g);
+    eg = m ? static_cast<int32_t>(64u * q + static_cast<uint32_t>(__builtin_ctzll(m))) : eg;
+  }
   const bool have = ok && eg >= 0 && static_cast<uint32_t>(eg) < n_exp;
   OBS_FUSED_MARK(3);
 
@@ -382,6 +384,19 @@ __global__ void __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 
   // up_b} at [32 sg], down scales at [1024 + 12 r], down biases at [1216 + 12 r]
   const uint16_t* sc16 = s_sc[wave];
 
+  // The selected experts and their p, by rank, for the combine's weights: the
+  // lane of wave 0 holding a selected expert writes it (read after the h
+  // exchange's barriers; the ranks no expert takes keep the -1 set at the start).
+  if (wave == 0) {
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      if (ck[q] != 0ull && rank[q] < FK) {
+        s_sel_id[rank[q]] = static_cast<int32_t>(lane + 64u * q);
+        s_sel_p[rank[q]] = __int_as_float(key[q]);
+      }
+    }
+  }
+
   OBS_FUSED_MARK(4);
   // ---- 4. gate/up rows -> h slots (factored per group: s*sum(q x) + b*sum(x))
   {  // the wave's own LDS area: no barrier (its LDS accesses run in order)
@@ -437,19 +452,6 @@ __global__ void __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 
     }
   }
 
-  // The routing weights, needed by the combine only: computed here, while h
-  // travels, instead of before the weight loads (0.2 us on the critical path).
-  // wsum is the serial sum of the selected p in rank order (empty slots add +0).
-  float wsum = 0.0f;
-#pragma unroll
-  for (uint32_t r = 0; r < FK; ++r) wsum = wsum + s_p[r];
-  const int32_t my_id = lane < FK ? s_ids[lane] : -1;
-  const float sel_w = my_id >= 0 ? route_weight(s_p[lane & (FK - 1u)], wsum, a.norm_topk, a.route_rule)
-                                 : 0.0f;  // rank weights in lanes 0..7 (combine)
-  if (blockIdx.x == 0 && wave == 0 && lane < FK) {
-    if (a.ids_out) a.ids_out[lane] = my_id;
-    if (a.w_out) a.w_out[lane] = sel_w;
-  }
   OBS_FUSED_MARK(5);
   // ---- 5/6. h arrives in three 256-column blocks. Block L = h[256L, 256L + 256)
   // holds every workgroup's rows t = 2L and 2L + 1, which it finishes before
@@ -530,6 +532,18 @@ __global__ void __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 
   // in rank order (wave 0: lane 8 r + i polls rank r's row i). Group 0 alone,
   // 64 rows per workgroup: 10.87 against 10.66 us per layer.
   if (wave == 0) {
+    // the routing weights (moe_routing_topk.metal:47-55): lane r < 8 holds rank
+    // r's; wsum is the serial sum of the selected p in rank order
+    const int32_t sel_id = lane < FK ? s_sel_id[lane] : -1;
+    float wsum = 0.0f;
+#pragma unroll
+    for (uint32_t r = 0; r < FK; ++r) wsum = s_sel_id[r] >= 0 ? wsum + s_sel_p[r] : wsum;
+    const float sel_w =
+        sel_id >= 0 ? route_weight(s_sel_p[lane & (FK - 1u)], wsum, a.norm_topk, a.route_rule) : 0.0f;
+    if (blockIdx.x == 0 && lane < FK) {
+      if (a.ids_out) a.ids_out[lane] = sel_id;
+      if (a.w_out) a.w_out[lane] = sel_w;
+    }
     const uint32_t row0c = 256u * g + 8u * j;
     bool wave_ok = ok;
     const uint64_t t0 = wall_clock64();

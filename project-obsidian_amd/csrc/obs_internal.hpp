@@ -55,6 +55,19 @@ struct obs_ctx {
   // decode workspaces replaced by larger ones, kept for the same reason
   std::vector<void*> retired;
   int decode_path = 0;  // OBS_DECODE_AUTO / _MULTI / _FUSED
+  // Context-owned device status words (obs::CTX_ST_*), zeroed by obs_create,
+  // read and cleared by obs_device_status: the one-launch prefill FFN's flags.
+  uint32_t* status_dev = nullptr;
+  // Dispatch facts the one-launch kernels build on, probed by obs_create
+  // (obs::probe_dispatch): the workgroups b of one b % 8 share an XCD (8
+  // groups, 8 XCDs), and an XCD starts its workgroups in index order.
+  bool xcd_map_ok = false;
+  bool inorder_ok = false;
+  // Test hook (obs_debug_ffn_wait): counts the one-launch FFN's down items
+  // wait for beyond their tile's gate/up items, and their wait limit (ticks of
+  // the 100 MHz constant clock).
+  uint32_t ffn_extra_count = 0;
+  uint64_t ffn_wait_ticks = 10000000ull;
   // in-stream kernel timing
   bool prof_on = false;
   std::vector<obs_prof_pair> prof_pairs;
@@ -77,6 +90,23 @@ constexpr size_t STATIC_MULTI_BYTES = 1024 + 256 + 256 + 8 * 2048 * 4 + 4096 * 2
 constexpr size_t STATIC_SCRATCH_BYTES = STATIC_FUSED_BYTES + STATIC_MULTI_BYTES;
 
 int set_error(obs_ctx* ctx, int code, const char* fmt, ...);
+
+// Words of obs_ctx::status_dev.
+enum : uint32_t {
+  CTX_ST_FFN_WAIT = 0,   // a one-launch FFN down item's wait for its tile timed out
+  CTX_ST_FFN_SCHED = 1,  // a one-launch FFN work table did not fit its launch
+  CTX_ST_WORDS = 64
+};
+
+// Which one-launch paths a device may take (OBS_PATH_* bits of
+// obs_dispatch_gate): the fused decode and fused attention need all 256 of
+// their workgroups resident, one per CU, and each group b % 8 on one XCD; the
+// one-launch prefill FFN needs the XCD map and in-order dispatch per XCD.
+uint32_t dispatch_gate(int num_cus, bool xcd_map_ok, bool inorder_ok);
+// Runs the dispatch probe kernels on the context's device and records the facts.
+int probe_dispatch(obs_ctx* ctx);
+// Per-context setup of the grouped GEMM kernels (LDS limits raised once).
+int prefill_init(obs_ctx* ctx);
 
 // Kernel bracketing for obs_profile_*: call prof_begin before a launch and
 // prof_end after it; both are no-ops unless profiling is enabled.
@@ -117,6 +147,7 @@ int launch_rmsnorm(obs_ctx* ctx, const uint16_t* x, const uint16_t* w, uint16_t*
 // Fused single-launch decode (obs_decode_fused.hip).
 bool fused_decode_supported(const obs_moe_config* cfg);
 uint32_t fused_decode_workgroups();  // workgroups of one launch (each needs a CU of its own)
+uint32_t fused_attn_workgroups();    // the same for the fused attention half (obs_attention_fused.hip)
 size_t fused_decode_ws_bytes();
 int launch_fused_decode(obs_ctx* ctx, const obs_moe_config* cfg, const obs_moe_layer* L, const uint16_t* x,
                         const uint16_t* residual, uint16_t* y, int32_t* ids_out, float* w_out);

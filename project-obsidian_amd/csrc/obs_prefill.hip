@@ -367,12 +367,15 @@ __device__ __forceinline__ void gemm_item(const GemmArgs& a, uint32_t e, uint32_
   // and biases, B groups 0 and 1. A group 0 follows as soon as its row ids are
   // in. All of them are unconditional (indices clamped into the tile, results
   // selected afterwards), so the waits count exactly the loads they need.
+  // Padding rows (r >= nrows) repeat the tile's last row: row i of an MFMA
+  // product depends on row i of A only, and the epilogue discards them. They
+  // never name a row outside the tile: in the one-launch FFN the A of a down
+  // item is H, and only its own tile's rows are complete once its wait passes.
   int32_t arow[4];
 #pragma unroll
   for (uint32_t i = 0; i < 4; ++i) {
-    const uint32_t r = tid / 8u + 32u * i;
-    arow[i] = (FLAGS & F_AROWS) ? a.a_rows[row0 + min(r, nrows - 1u)] : static_cast<int32_t>(row0 + r);
-    if (r >= nrows) arow[i] = -1;
+    const uint32_t r = min(tid / 8u + 32u * i, nrows - 1u);
+    arow[i] = (FLAGS & F_AROWS) ? a.a_rows[row0 + r] : static_cast<int32_t>(row0 + r);
   }
   // threads t and t + 128 load and store the same entry (an unconditional store
   // keeps the load from sinking under a branch)
@@ -440,11 +443,11 @@ __device__ __forceinline__ void gemm_item(const GemmArgs& a, uint32_t e, uint32_
   u32x4_t ras[4];
 #pragma unroll
   for (uint32_t i = 0; i < 4; ++i) {
-    // Padding rows (no A row) stage row 0: row i of an MFMA product depends on
-    // row i of A only, and the epilogue discards padding rows.
-    const int32_t r = arow[i] >= 0 && static_cast<uint32_t>(arow[i]) < a.a_rows_total ? arow[i] : 0;
+    // clamped into A: a corrupt row map (the grouping never writes one) reads
+    // a wrong row instead of faulting
+    const int32_t r = min(max(arow[i], 0), static_cast<int32_t>(a.a_rows_total) - 1);
     in.aptr[i] = a.A + static_cast<size_t>(r) * K + ac;
-    ras[i] = *reinterpret_cast<const u32x4_t*>(in.aptr[i]);  // A group 0 (rows of unused blocks: row 0)
+    ras[i] = *reinterpret_cast<const u32x4_t*>(in.aptr[i]);  // A group 0 (rows of unused blocks too)
   }
   // every load above is issued before the first wait below: left alone, the
   // scheduler moves the scale stores (and their waits) ahead of the B and A loads
@@ -479,14 +482,15 @@ __device__ __forceinline__ void gemm_item(const GemmArgs& a, uint32_t e, uint32_
 // counted. The dispatcher hands out workgroups in index order, so a waiting
 // down item waits only for gate/up items already running; the down items of
 // the first tiles fill the slots the last gate/up items leave idle. The wait
-// is bounded: a time-out sets g_ffn_err (read by obs_device_status) and the
-// item runs anyway, so the grid always drains.
+// is bounded: a time-out sets the calling context's status word (read and
+// cleared by obs_device_status of that context) and the item runs anyway, so
+// the grid always drains.
 struct FfnSync {
   int32_t* tile_done;  // per tile, at its first grouped row: gate/up items done
-  uint32_t ncb_gu;     // gate/up items per tile
+  int32_t need;        // counts a down item waits for: the tile's gate/up items (more only under a test hook)
+  uint64_t ticks;      // wait limit in ticks of wall_clock64 (100 MHz); 100 ms unless a test shortens it
+  uint32_t* err;       // the context's status words (obs::CTX_ST_FFN_WAIT)
 };
-__device__ uint32_t g_ffn_err;
-constexpr uint64_t FFN_WAIT_TICKS = 10000000ull;  // 100 ms of wall_clock64 (100 MHz)
 
 template <uint32_t MODE_DN>
 __global__ void __launch_bounds__(256, 2) moe_ffn_kernel(GemmArgs g, GemmArgs d, FfnSync sy) {
@@ -508,10 +512,9 @@ __global__ void __launch_bounds__(256, 2) moe_ffn_kernel(GemmArgs g, GemmArgs d,
     const int4 w = d.work[8u * (p - ngu) + x];
     if (tid == 0) {
       const uint64_t t0 = wall_clock64();
-      while (__hip_atomic_load(sy.tile_done + w.y, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) <
-             static_cast<int32_t>(sy.ncb_gu)) {
-        if (wall_clock64() - t0 > FFN_WAIT_TICKS) {
-          __hip_atomic_store(&g_ffn_err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      while (__hip_atomic_load(sy.tile_done + w.y, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < sy.need) {
+        if (wall_clock64() - t0 > sy.ticks) {
+          __hip_atomic_store(sy.err + obs::CTX_ST_FFN_WAIT, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
           break;
         }
       }
@@ -623,6 +626,7 @@ struct WorkTable {
   uint32_t grid, ncb, cols;
   ItemCost split;       // per-tile cost the tiles are split over the XCDs by
   int32_t* tile_done;   // when set: zeroed at each tile's first row (the one-launch FFN's counters)
+  uint32_t* err;        // with tile_done: the context's status words (obs::CTX_ST_FFN_SCHED)
 };
 
 // Exclusive prefix sum over the wave (64 lanes) and the wave total.
@@ -729,6 +733,12 @@ __device__ void work_table_fill(const WorkTable W, uint32_t E, SchedLds& L) {  /
       return;
     }
   }
+  // The one-launch FFN needs the cost-balanced split (a tile's items on one
+  // XCD, its counters zeroed); its launch is sized so that split always fits
+  // (sched_grid), so this is never reached with tile_done set. Should it be,
+  // the context's status word says the launch's outputs are invalid.
+  if (W.tile_done && lane == 0)
+    __hip_atomic_store(W.err + obs::CTX_ST_FFN_SCHED, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
   // even split by count: XCD x runs items [x * chunk, (x + 1) * chunk) in item order
   const uint32_t n_items = T_all * ncb, chunk = (n_items + 7u) / 8u;
   for (uint32_t i = lane; i < n_items; i += 64u) {
@@ -908,7 +918,9 @@ struct PrefillWs {
   ItemCost split_gu, split_dn;
 };
 
-PrefillWs prefill_layout(const obs_moe_config* cfg, uint32_t T) {
+// one_launch_ok: the device's dispatch allows the one-launch FFN (the workspace
+// size does not depend on it).
+PrefillWs prefill_layout(const obs_moe_config* cfg, uint32_t T, bool one_launch_ok) {
   PrefillWs L{};
   const size_t R = static_cast<size_t>(T) * cfg->top_k;
   L.max_tiles = static_cast<uint32_t>((R + TM - 1) / TM + cfg->n_exp);
@@ -928,7 +940,8 @@ PrefillWs prefill_layout(const obs_moe_config* cfg, uint32_t T) {
   // One launch for both GEMMs needs the cost-balanced schedule for both tables
   // (the even split would put a tile's down items on other XCDs than its
   // gate/up items) and per-tile costs within 16 bits.
-  L.ffn_one_launch = L.max_tiles <= SCHED_MAX_TILES && COST_GATEUP.of(4) * ncb_gu + COST_DOWN.of(4) * ncb_dn < 65536u;
+  L.ffn_one_launch = one_launch_ok && L.max_tiles <= SCHED_MAX_TILES &&
+                     COST_GATEUP.of(4) * ncb_gu + COST_DOWN.of(4) * ncb_dn < 65536u;
   L.split_gu = L.ffn_one_launch ? tile_cost2(COST_GATEUP, ncb_gu, COST_DOWN, ncb_dn) : tile_cost(COST_GATEUP, ncb_gu);
   L.split_dn = L.ffn_one_launch ? L.split_gu : tile_cost(COST_DOWN, ncb_dn);
   L.grid_gu = sched_grid(L.max_tiles, ncb_gu, L.split_gu);
@@ -977,17 +990,12 @@ int launch_gemm(obs_ctx* ctx, GemmArgs a, uint32_t grid, uint32_t mode) {
       {MODE_WIDE, 0, reinterpret_cast<const void*>(&grouped_gemm_kernel<MODE_WIDE, 0>), "q4_matmul"},
       {MODE_NARROW, 0, reinterpret_cast<const void*>(&grouped_gemm_kernel<MODE_NARROW, 0>), "q4_matmul"},
   };
-  static bool lds_raised[sizeof(variants) / sizeof(variants[0])] = {};
   int v = -1;
   for (int i = 0; i < static_cast<int>(sizeof(variants) / sizeof(variants[0])); ++i)
     if (variants[i].mode == mode && variants[i].flags == flags) v = i;
   if (v < 0) return obs::set_error(ctx, OBS_E_INVALID, "grouped GEMM: unsupported launch (mode %u, flags %u)", mode, flags);
   const void* fn = variants[v].fn;
   const char* name = variants[v].name;
-  if (!lds_raised[v]) {  // the staged scales can take the block past 64 KB of LDS (gfx950 has 160 KB)
-    OBS_HIP_TRY(ctx, hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, SB_LDS_MAX));
-    lds_raised[v] = true;
-  }
   void* args[] = {&a};
   OBS_LAUNCH(ctx, name, OBS_HIP_TRY(ctx, hipLaunchKernel(fn, dim3(grid), dim3(256), args, lds, ctx->stream)));
   return OBS_OK;
@@ -1005,13 +1013,7 @@ int launch_ffn(obs_ctx* ctx, GemmArgs g, GemmArgs d, int32_t* tile_done, uint32_
   const size_t lds = std::max(gemm_sb_bytes(MODE_SWIGLU, g.K), gemm_sb_bytes(mode_dn, d.K));
   const void* fn = mode_dn == MODE_WIDE ? reinterpret_cast<const void*>(&moe_ffn_kernel<MODE_WIDE>)
                                         : reinterpret_cast<const void*>(&moe_ffn_kernel<MODE_NARROW>);
-  static bool lds_raised[2] = {};
-  const int v = mode_dn == MODE_WIDE ? 0 : 1;
-  if (!lds_raised[v]) {
-    OBS_HIP_TRY(ctx, hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, SB_LDS_MAX));
-    lds_raised[v] = true;
-  }
-  FfnSync sy{tile_done, ncb_gu};
+  FfnSync sy{tile_done, static_cast<int32_t>(ncb_gu + ctx->ffn_extra_count), ctx->ffn_wait_ticks, ctx->status_dev};
   void* args[] = {&g, &d, &sy};
   OBS_LAUNCH(ctx, "moe_ffn", OBS_HIP_TRY(ctx, hipLaunchKernel(fn, dim3(grid), dim3(256), args, lds, ctx->stream)));
   return OBS_OK;
@@ -1021,17 +1023,36 @@ int launch_ffn(obs_ctx* ctx, GemmArgs g, GemmArgs d, int32_t* tile_done, uint32_
 
 namespace obs {
 
-// The one-launch FFN's wait flag: reported (and cleared) like the fused
-// decode's time-outs.
+// The one-launch FFN's flags in the context's status words: reported (and
+// cleared) like the fused decode's time-outs.
 int ffn_status(obs_ctx* ctx) {
-  uint32_t err = 0;
+  uint32_t st[2] = {0, 0};
   OBS_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
-  OBS_HIP_TRY(ctx, hipMemcpyFromSymbol(&err, HIP_SYMBOL(g_ffn_err), sizeof(err)));
-  if (err) {
-    const uint32_t zero = 0;
-    OBS_HIP_TRY(ctx, hipMemcpyToSymbol(HIP_SYMBOL(g_ffn_err), &zero, sizeof(zero)));
+  OBS_HIP_TRY(ctx, hipMemcpy(st, ctx->status_dev, sizeof(st), hipMemcpyDeviceToHost));
+  if (st[CTX_ST_FFN_WAIT] || st[CTX_ST_FFN_SCHED]) {
+    OBS_HIP_TRY(ctx, hipMemset(ctx->status_dev, 0, sizeof(st)));
+    OBS_HIP_TRY(ctx, hipDeviceSynchronize());
+    if (st[CTX_ST_FFN_SCHED])
+      return set_error(ctx, OBS_E_HIP, "grouped prefill: a one-launch work table did not fit its launch; outputs invalid");
     return set_error(ctx, OBS_E_HIP, "grouped prefill: a down item's wait for its tile timed out; its output is invalid");
   }
+  return OBS_OK;
+}
+
+// The staged scales can take a grouped GEMM workgroup past 64 KB of LDS
+// (gfx950 has 160 KB per CU): every variant's limit is raised once per
+// context, at creation, so no launch sets a kernel attribute.
+int prefill_init(obs_ctx* ctx) {
+  const void* fns[] = {
+      reinterpret_cast<const void*>(&grouped_gemm_kernel<MODE_SWIGLU, F_WORK | F_AROWS>),
+      reinterpret_cast<const void*>(&grouped_gemm_kernel<MODE_WIDE, F_WORK | F_OROWS>),
+      reinterpret_cast<const void*>(&grouped_gemm_kernel<MODE_NARROW, F_WORK | F_OROWS>),
+      reinterpret_cast<const void*>(&grouped_gemm_kernel<MODE_WIDE, 0>),
+      reinterpret_cast<const void*>(&grouped_gemm_kernel<MODE_NARROW, 0>),
+      reinterpret_cast<const void*>(&moe_ffn_kernel<MODE_WIDE>),
+      reinterpret_cast<const void*>(&moe_ffn_kernel<MODE_NARROW>)};
+  for (const void* fn : fns)
+    OBS_HIP_TRY(ctx, hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, SB_LDS_MAX));
   return OBS_OK;
 }
 
@@ -1041,7 +1062,8 @@ extern "C" {
 
 size_t obs_moe_prefill_workspace(const obs_moe_config* cfg, uint32_t T) {
   if (!cfg || T == 0) return 0;
-  return prefill_layout(cfg, T).total;
+  // the larger of the two layouts (the work tables are sized by the schedule the device allows)
+  return std::max(prefill_layout(cfg, T, false).total, prefill_layout(cfg, T, true).total);
 }
 
 int obs_moe_prefill(obs_ctx* ctx, const obs_moe_config* cfg, const obs_moe_layer* layer, const uint16_t* X,
@@ -1059,7 +1081,8 @@ int obs_moe_prefill(obs_ctx* ctx, const obs_moe_config* cfg, const obs_moe_layer
   const uint32_t E = cfg->n_exp, k = cfg->top_k, H = cfg->hidden, I = cfg->inter;
   if (H % TN != 0 || I % TN != 0)
     return obs::set_error(ctx, OBS_E_SHAPE, "obs_moe_prefill: hidden and inter must be multiples of %u", TN);
-  const PrefillWs L = prefill_layout(cfg, T);
+  const PrefillWs L = prefill_layout(cfg, T, (obs::dispatch_gate(ctx->num_cus, ctx->xcd_map_ok, ctx->inorder_ok) &
+                                               OBS_PATH_FFN_ONE_LAUNCH) != 0u);
   if (ws_bytes < L.total)
     return obs::set_error(ctx, OBS_E_NOMEM, "obs_moe_prefill: workspace %zu bytes < %zu needed", ws_bytes, L.total);
   if (!obs::aligned(X, 16) || !obs::aligned(Y, 16) || (residual && !obs::aligned(residual, 16)) || !obs::aligned(ws, 256))
@@ -1098,9 +1121,9 @@ int obs_moe_prefill(obs_ctx* ctx, const obs_moe_config* cfg, const obs_moe_layer
   const uint32_t cols_dn = mode_cols(gemm_mode(false, H));
   int32_t* work_cnt = reinterpret_cast<int32_t*>(base + L.work_cnt);
   int32_t* tile_done = reinterpret_cast<int32_t*>(base + L.tile_done);
-  const WorkTable wt_gu{work_gu, work_cnt, L.grid_gu, I / TN, TN, L.split_gu, nullptr};
+  const WorkTable wt_gu{work_gu, work_cnt, L.grid_gu, I / TN, TN, L.split_gu, nullptr, nullptr};
   const WorkTable wt_dn{work_dn, work_cnt + 8, L.grid_dn, H / cols_dn, cols_dn, L.split_dn,
-                        L.ffn_one_launch ? tile_done : nullptr};
+                        L.ffn_one_launch ? tile_done : nullptr, ctx->status_dev};
   OBS_LAUNCH(ctx, "moe_group_rank",
              group_rank_kernel<<<L.nchunks + 2u, 64, 0, ctx->stream>>>(ids, T, k, E, chunk_cnt, row_token, row_slot,
                                                                        counts, offsets, wt_gu, wt_dn));

@@ -34,6 +34,7 @@ OBS_E_NOMEM = -5
 OBS_E_UNSUPPORTED = -6
 
 OBS_DECODE_AUTO, OBS_DECODE_MULTI, OBS_DECODE_FUSED = 0, 1, 2
+OBS_PATH_FUSED_DECODE, OBS_PATH_FUSED_ATTN, OBS_PATH_FFN_ONE_LAUNCH = 1, 2, 4  # obs_dispatch_gate bits
 # routing rules (obs_route_topk, MoeConfig.route_rule)
 ROUTE_REF, ROUTE_F32 = 0, 1
 
@@ -60,7 +61,7 @@ EXPORTS = (
     "obs_ckpt_read", "obs_moe_layer_bytes", "obs_ckpt_load_moe_layer", "obs_ckpt_load_tensor",
     "obs_q4_gemv", "obs_attn_prep", "obs_sdpa_workspace", "obs_sdpa_decode", "obs_embed_q4",
     "obs_argmax_workspace", "obs_argmax", "obs_embed_q4_rows", "obs_attn_prep_rows", "obs_sdpa_prefill",
-    "obs_attn_decode",
+    "obs_attn_decode", "obs_dispatch_gate", "obs_dispatch_info", "obs_set_dispatch_facts", "obs_debug_ffn_wait",
 )
 
 
@@ -154,6 +155,10 @@ def lib() -> C.CDLL:
         "obs_graph_destroy": (None, [vp]),
         "obs_set_decode_path": (i32, [vp, C.c_int]),
         "obs_device_status": (i32, [vp]),
+        "obs_dispatch_gate": (u32, [C.c_int, C.c_int, C.c_int]),
+        "obs_dispatch_info": (i32, [vp, C.POINTER(C.c_int), C.POINTER(C.c_int), C.POINTER(C.c_int)]),
+        "obs_set_dispatch_facts": (i32, [vp, C.c_int, C.c_int]),
+        "obs_debug_ffn_wait": (i32, [vp, u32, u32]),
         "obs_stream_hold": (i32, [vp, u32]),
         "obs_profile_enable": (i32, [vp, C.c_int]),
         "obs_profile_accumulate": (i32, [vp]),
@@ -292,8 +297,27 @@ class ObsidianExecutor:
         self._check(lib().obs_set_decode_path(self.ctx, int(path)))
 
     def device_status(self) -> None:
-        """Raise if the fused decode path recorded a device-side failure."""
+        """Raise if a one-launch kernel of this context recorded a device-side
+        failure (a bounded wait that timed out); the flag is cleared."""
         self._check(lib().obs_device_status(self.ctx))
+
+    def dispatch_info(self) -> Tuple[int, bool, bool]:
+        """(CUs, each group b % 8 of workgroups on one XCD, in-order dispatch per XCD) as the
+        probe at context creation found them."""
+        n, xm, io = C.c_int(), C.c_int(), C.c_int()
+        self._check(lib().obs_dispatch_info(self.ctx, C.byref(n), C.byref(xm), C.byref(io)))
+        return n.value, bool(xm.value), bool(io.value)
+
+    def set_dispatch_facts(self, xcd_map_ok: bool, inorder_ok: bool) -> None:
+        self._check(lib().obs_set_dispatch_facts(self.ctx, int(xcd_map_ok), int(inorder_ok)))
+
+    def paths(self) -> int:
+        """The OBS_PATH_* one-launch paths this context's device may take."""
+        n, xm, io = self.dispatch_info()
+        return int(lib().obs_dispatch_gate(n, int(xm), int(io)))
+
+    def debug_ffn_wait(self, extra_count: int, wait_us: int) -> None:
+        self._check(lib().obs_debug_ffn_wait(self.ctx, int(extra_count), int(wait_us)))
 
     # -- graph capture / replay ------------------------------------------
     def capture_begin(self) -> None:

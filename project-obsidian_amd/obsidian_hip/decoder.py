@@ -19,7 +19,7 @@ from typing import Dict, List, Optional
 
 import numpy as np
 
-from . import DeviceBuffer, MoeConfig, MoeLayer, ObsError, ObsidianExecutor, _ptr, lib
+from . import OBS_PATH_FUSED_ATTN, DeviceBuffer, MoeConfig, MoeLayer, ObsError, ObsidianExecutor, _ptr, lib
 
 
 @dataclass
@@ -96,9 +96,11 @@ class Model:
     # -- the pieces of forward_layer (forward.rs:398-443) ------------------
     def fused_attention(self) -> bool:
         """Whether the attention half runs as one launch (obs_attn_decode: the
-        Qwen3-30B-A3B attention shape on a device with 256 CUs)."""
+        Qwen3-30B-A3B attention shape on a device whose dispatch allows it: 256
+        CUs, each group b % 8 of workgroups on one XCD)."""
         c = self.cfg
-        return self.use_fused_attention and (c.hidden, c.n_heads, c.n_kv, c.head_dim) == (2048, 32, 4, 128)
+        return (self.use_fused_attention and (c.hidden, c.n_heads, c.n_kv, c.head_dim) == (2048, 32, 4, 128)
+                and bool(self.exe.paths() & OBS_PATH_FUSED_ATTN))
 
     def forward_layer(self, il: int, ids_out=None, w_out=None) -> None:
         """self.x <- layer il of self.x at the state's position (ids_out, w_out:

@@ -59,7 +59,7 @@ def test_null_context_is_rejected_before_any_device_work():
     host_only = {"obs_create", "obs_create_error", "obs_destroy", "obs_last_error", "obs_get_stream",
                  "obs_graph_destroy", "obs_moe_prefill_workspace", "obs_profile_count",
                  "obs_ckpt_close", "obs_ckpt_error", "obs_moe_layer_bytes", "obs_sdpa_workspace",
-                 "obs_argmax_workspace"}
+                 "obs_argmax_workspace", "obs_dispatch_gate"}
     for name in declared_functions():
         if name in host_only:
             continue
@@ -109,3 +109,19 @@ def test_create_without_a_gpu_reports_unsupported():
     with pytest.raises(oh.ObsError) as ei:
         oh.ObsidianExecutor(0)
     assert ei.value.code == oh.OBS_E_UNSUPPORTED
+
+
+def test_dispatch_gate_rule():
+    """The one-launch paths a device may take, from its CU count and the two
+    dispatch facts obs_create probes (pure host rule, no device)."""
+    L = oh.lib()
+    D, A, F = oh.OBS_PATH_FUSED_DECODE, oh.OBS_PATH_FUSED_ATTN, oh.OBS_PATH_FFN_ONE_LAUNCH
+    assert L.obs_dispatch_gate(256, 1, 1) == D | A | F
+    assert L.obs_dispatch_gate(304, 1, 1) == D | A | F
+    # the fused decode / attention need 256 CUs (one workgroup each) and the XCD map
+    assert L.obs_dispatch_gate(255, 1, 1) == F
+    assert L.obs_dispatch_gate(32, 1, 1) == F
+    assert L.obs_dispatch_gate(256, 0, 1) == 0
+    assert L.obs_dispatch_gate(256, 1, 0) == D | A
+    assert L.obs_dispatch_gate(0, 0, 0) == 0
+    assert L.obs_dispatch_gate(100, 1, 0) == 0

@@ -47,7 +47,10 @@ def _close(y, ref, tol, elem_tol=None):
 BF_NORM, BF_ELEM = 5e-3, 1e-2
 
 
-def _prefill(exe, cfg, layer, X, ids=None, w=None, residual=None):
+def _prefill(exe, cfg, layer, X, ids=None, w=None, residual=None, kernels=None):
+    """obs_moe_prefill of X; the device status is checked after every call (a
+    bounded wait of the one-launch FFN that timed out fails the test that
+    caused it). kernels: a dict that receives {kernel name: (ms, launches)}."""
     T = X.shape[0]
     ws_bytes = exe.moe_prefill_workspace(cfg, T)
     ws = exe.alloc(ws_bytes, np.uint8)
@@ -55,8 +58,17 @@ def _prefill(exe, cfg, layer, X, ids=None, w=None, residual=None):
     d_ids = exe.upload(np.ascontiguousarray(ids, np.int32)) if ids is not None else None
     d_w = exe.upload(np.ascontiguousarray(w, np.float32)) if w is not None else None
     d_res = exe.upload(residual) if residual is not None else None
-    exe.moe_prefill(cfg, layer, exe.upload(X), Y, T, ids=d_ids, weights=d_w, residual=d_res, ws=ws,
-                    ws_bytes=ws_bytes)
+    dX = exe.upload(X)
+    if kernels is not None:
+        exe.profile_clear()
+        exe.profile_enable(True)
+    exe.moe_prefill(cfg, layer, dX, Y, T, ids=d_ids, weights=d_w, residual=d_res, ws=ws, ws_bytes=ws_bytes)
+    if kernels is not None:
+        exe.profile_enable(False)
+        exe.profile_accumulate()
+        kernels.update(exe.profile_stats())
+        exe.profile_clear()
+    exe.device_status()
     out = Y.download()
     for b in (ws, Y, d_ids, d_w, d_res):
         if b is not None:
@@ -218,10 +230,48 @@ def test_moe_prefill_t2048_zipf_linearity(exe, qwen):
     assert np.array_equal(y1, y1b)
     y2 = _prefill(exe, cfg, layer, X, ids, 2 * w)
     assert np.array_equal(_f32(y2), 2 * _f32(y1))  # *2 is exact in fp32 and bf16
-    # spot-check a few tokens against the oracle
-    sel = np.array([0, 1, 777, 2047])
+
+
+def test_moe_prefill_t2048_zipf_vs_oracle(exe, qwen):
+    """The benched prefill (T = 2,048, Zipf(1.1) routing, seed 0) through the
+    one-launch expert FFN, against the oracle evaluated with the GEMM's
+    operand roundings (forward.rs:199-232: grouping, rank-order scatter):
+    (a) every row of the largest expert (1,839 rows in 15 tiles: the deepest
+    chain of down items waiting on their tiles' gate/up items). Its rank's
+    routing weight is set to 1 and the other ranks' to 0, so each of its
+    tokens' outputs is that expert's output row alone (the grouping, the
+    tiles and the schedule are those of the real routing), and the oracle
+    runs that one rank per token; every other token's output is exactly 0.
+    (b) 256 tokens with the real weights, at least one per expert."""
+    t, layer, L = qwen
+    if not exe.paths() & oh.OBS_PATH_FFN_ONE_LAUNCH:
+        pytest.skip("this device's dispatch does not allow the one-launch FFN")
+    cfg = oh.MoeConfig(E, K, H, I, 64, True)
+    rng = np.random.default_rng(961)
+    T = 2048
+    X = synth.bf16_normal(rng, (T, H))
+    ids, w = synth.zipf_routing(T, E, K, 1.1, seed=0)
+    counts = np.bincount(ids.ravel(), minlength=E)
+    big = int(np.argmax(counts))
+    assert counts[big] == 1839
+    tok, rank = np.nonzero(ids == big)  # a token routes to an expert at most once
+    w1 = np.zeros_like(w)
+    w1[tok, rank] = 1.0
+    kern = {}
+    y1 = _f32(_prefill(exe, cfg, layer, X, ids, w1, kernels=kern))
+    assert "moe_ffn" in kern and not any(n.startswith("grouped_gemm") for n in kern), sorted(kern)
+    ref1 = O.moe_prefill(L, X[tok], ids[tok, rank][:, None], np.ones((tok.size, 1), np.float32), O.MODE_MFMA_BF16)
+    rel1 = _close(y1[tok], ref1, BF_NORM, BF_ELEM)
+    rest = np.setdiff1d(np.arange(T), tok)
+    assert np.all(y1[rest] == 0.0)
+    # (b): one token per expert (the first routed to it), then random others
+    first = np.array([int(np.nonzero((ids == e).any(1))[0][0]) for e in range(E)])
+    sel = np.union1d(first, rng.choice(T, 256, replace=False))[:384]
+    assert np.array_equal(np.unique(ids[sel]), np.arange(E)) and sel.size >= 256
+    y = _f32(_prefill(exe, cfg, layer, X, ids, w))
     ref = O.moe_prefill(L, X[sel], ids[sel], w[sel], O.MODE_MFMA_BF16)
-    _close(_f32(y1[sel]), ref, BF_NORM, BF_ELEM)
+    rel = _close(y[sel], ref, BF_NORM, BF_ELEM)
+    print(f"T=2048 Zipf: largest expert ({tok.size} rows) rel {rel1:.2e}; {sel.size}-token sample rel {rel:.2e}")
 
 
 def test_moe_prefill_invalid_and_duplicate_ids_are_skipped(exe, qwen):
