@@ -141,15 +141,21 @@ __global__ void __launch_bounds__(256) q4_gemv_kernel(const uint16_t* __restrict
         }
       }
   }
-  // f16 pairs, their sum and the offset part, per segment
+  // f16 pairs, their sum and the offset part, per segment; the f16 range per
+  // segment (the lane's 32 columns scaled by 2^-k at 2^15 and beyond, the
+  // segment's dot products by 2^k; k = 0 below)
   f16x2_t xh[SEG][16];
-  float xs[SEG], xoff[SEG];
+  float xs[SEG], xoff[SEG], xup[SEG];
 #pragma unroll
   for (uint32_t sg = 0; sg < SEG; ++sg) {
     float sum = 0.0f;
 #pragma unroll
     for (uint32_t c = 0; c < 32; ++c) sum = sum + xf[sg][c];
     xs[sg] = sum;
+    const F16Range xr = f16_range(lane_absmax<32>(xf[sg]));
+    xup[sg] = xr.up;
+#pragma unroll
+    for (uint32_t c = 0; c < 32; ++c) xf[sg][c] = xf[sg][c] * xr.down;
 #pragma unroll
     for (uint32_t i = 0; i < 4; ++i) f16_pairs8(xf[sg] + 8 * i, xh[sg] + 4 * i);
     float off = 0.0f;
@@ -169,7 +175,7 @@ __global__ void __launch_bounds__(256) q4_gemv_kernel(const uint16_t* __restrict
       acc = dot8_q4_off(q[k][sg].y, xh[sg] + 4, acc);
       acc = dot8_q4_off(q[k][sg].z, xh[sg] + 8, acc);
       acc = dot8_q4_off(q[k][sg].w, xh[sg] + 12, acc);
-      part = part + __builtin_fmaf(bf16_to_f32(sc[k][sg]), acc - xoff[sg], bf16_to_f32(bi[k][sg]) * xs[sg]);
+      part = part + __builtin_fmaf(bf16_to_f32(sc[k][sg]), (acc - xoff[sg]) * xup[sg], bf16_to_f32(bi[k][sg]) * xs[sg]);
     }
     part = wave_sum_asc(part);
     const float y = bf16_to_f32(res[k]) + part;  // used only where the part has a residual

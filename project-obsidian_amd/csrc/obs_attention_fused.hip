@@ -131,6 +131,7 @@ attn_fused_kernel(AttnArgs a) {
   __shared__ float s_rl[16][A_CDIM], s_ra[16][A_CDIM];
   __shared__ __attribute__((aligned(16))) f16x2_t s_ap[AGQD / 2];   // the group's attention output, f16 pairs
   __shared__ float s_asum[AGQD / 32], s_aoff[AGQD / 32];
+  __shared__ float s_aup[AGQD / 64];  // the f16 range factor 2^k of each 64 output columns
   __shared__ float s_y[ANGRP][A_ORWG];
 
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
@@ -281,6 +282,11 @@ attn_fused_kernel(AttnArgs a) {
     float xs = 0.0f;
 #pragma unroll
     for (int c = 0; c < 32; ++c) xs = xs + xf[c];
+    // the f16 range: the lane's 32 columns scaled by 2^-k at 2^15 and beyond,
+    // the rows' dot products by 2^k (k = 0 below)
+    const F16Range xr = f16_range(lane_absmax<32>(xf));
+#pragma unroll
+    for (int c = 0; c < 32; ++c) xf[c] = xf[c] * xr.down;
     f16x2_t xh[16];
 #pragma unroll
     for (int i = 0; i < 4; ++i) f16_pairs8(xf + 8 * i, xh + 4 * i);
@@ -295,7 +301,7 @@ attn_fused_kernel(AttnArgs a) {
       acc = dot8_q4_off(rq[k].y, xh + 4, acc);
       acc = dot8_q4_off(rq[k].z, xh + 8, acc);
       acc = dot8_q4_off(rq[k].w, xh + 12, acc);
-      part[k] = __builtin_fmaf(bf16_to_f32(rsc[k]), acc - xoff, bf16_to_f32(rbi[k]) * xs);
+      part[k] = __builtin_fmaf(bf16_to_f32(rsc[k]), (acc - xoff) * xr.up, bf16_to_f32(rbi[k]) * xs);
     }
     // the six 64-lane sums in wave_sum_asc's order (bit-identical to the
     // per-head launches), row my_row in lane l < 8
@@ -617,7 +623,12 @@ attn_fused_kernel(AttnArgs a) {
     const uint32_t pv = __float_as_uint(pvf[0]);
     _Float16* ap16 = reinterpret_cast<_Float16*>(s_ap);
     const uint32_t i0 = 2u * tid;  // columns i0 (low half), i0 + 1
-    const _Float16 h0 = static_cast<_Float16>(bf16lo(pv)), h1 = static_cast<_Float16>(bf16hi(pv));
+    // the f16 range per 64 columns (one quantization group of W_o, 32 lanes):
+    // the outputs scaled by 2^-k at 2^15 and beyond, the group's terms by 2^k
+    const F16Range asc = f16_range(half_wave_absmax(__builtin_fmaxf(__builtin_fabsf(bf16lo(pv)),
+                                                                     __builtin_fabsf(bf16hi(pv)))));
+    const _Float16 h0 = static_cast<_Float16>(bf16lo(pv) * asc.down), h1 = static_cast<_Float16>(bf16hi(pv) * asc.down);
+    if ((tid & 31u) == 0u) s_aup[tid >> 5] = asc.up;
     const uint32_t j0 = i0 & 7u, j1 = j0 + 1u;
     ap16[(i0 & ~7u) + 2u * (j0 & 3u) + (j0 >> 2)] = h0;
     ap16[(i0 & ~7u) + 2u * (j1 & 3u) + (j1 >> 2)] = h1;
@@ -666,7 +677,9 @@ attn_fused_kernel(AttnArgs a) {
         acc = dot8_q4_off(oq[p][sg].z, ah[sg] + 8, acc);
         acc = dot8_q4_off(oq[p][sg].w, ah[sg] + 12, acc);
       }
-      const float part = group8_sum(__builtin_fmaf(bf16_to_f32(osc[p]), acc - aoff, bf16_to_f32(obi[p]) * asum));
+      // asum and aoff are sums of the scaled values: the 2^k factor takes the whole term
+      const float part =
+          group8_sum(s_aup[oc] * __builtin_fmaf(bf16_to_f32(osc[p]), acc - aoff, bf16_to_f32(obi[p]) * asum));
       if (oc == 0u) slot_store(y_slots + size_t(g) * AH + orow0 + 8u * p, epoch, part);  // polled across XCDs
     }
   }

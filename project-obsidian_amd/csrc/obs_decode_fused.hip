@@ -242,10 +242,17 @@ __global__ void __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 
   // While the logits travel: the lane's 32 activations as f16 pairs for the
   // expert rows, their sum and the offset part of dot8_q4_off over them
   // (shared by every row).
+  // (The f16 range: the lane's 32 columns are scaled by 2^-k when their
+  // largest magnitude reaches 2^15, and the rows' dot products by 2^k.)
   float xs = 0.0f;
 #pragma unroll
   for (int c = 0; c < 32; ++c) xs = xs + xf[c];
+  const F16Range xr = f16_range(lane_absmax<32>(xf));
   f16x2_t xh[16];
+  if (__any(xr.down != 1.0f)) {
+#pragma unroll
+    for (int c = 0; c < 32; ++c) xf[c] = xf[c] * xr.down;
+  }
 #pragma unroll
   for (int i = 0; i < 4; ++i) f16_pairs8(xf + 8 * i, xh + 4 * i);
   float xoff = 0.0f;
@@ -427,8 +434,8 @@ __global__ void __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 
       au = dot8_q4_off(uq[t].y, xh + 4, au);
       au = dot8_q4_off(uq[t].z, xh + 8, au);
       au = dot8_q4_off(uq[t].w, xh + 12, au);
-      pg[i] = __builtin_fmaf(bf16_to_f32(rsb[t][0]), ag - xoff, bf16_to_f32(rsb[t][1]) * xs);
-      pu[i] = __builtin_fmaf(bf16_to_f32(rsb[t][2]), au - xoff, bf16_to_f32(rsb[t][3]) * xs);
+      pg[i] = __builtin_fmaf(bf16_to_f32(rsb[t][0]), (ag - xoff) * xr.up, bf16_to_f32(rsb[t][1]) * xs);
+      pu[i] = __builtin_fmaf(bf16_to_f32(rsb[t][2]), (au - xoff) * xr.up, bf16_to_f32(rsb[t][3]) * xs);
     }
     int row;
     float hv = gateup_reduce(pg, pu, lane, row);
@@ -483,10 +490,11 @@ __global__ void __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 
       ok = ok && wave_ok;
       {
         const uint32_t idx = tid + 256u * L, jn = idx & 7u;  // column idx = 8 * word + jn
-        hp16[(idx & ~7u) + 2u * (jn & 3u) + (jn >> 2)] = static_cast<_Float16>(hv);
+        const _Float16 h16 = static_cast<_Float16>(hv);
+        hp16[(idx & ~7u) + 2u * (jn & 3u) + (jn >> 2)] = h16;
         // offsets of dot8_q4_off: 1024 at even nibble positions, 64 at odd ones;
         // the sums use the f16-rounded values the dot products see
-        const float hr = static_cast<float>(static_cast<_Float16>(hv));
+        const float hr = static_cast<float>(h16);
         const float sum = half_wave_sum(hr);
         const float off = half_wave_sum(hr * ((jn & 1u) ? 64.0f : 1024.0f));
         if ((idx & 31u) == 0u) {
@@ -516,6 +524,48 @@ __global__ void __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 
           acc = dot8_q4_off(dq[p][L].w, hp + 12, acc);
           const uint32_t gi = 4u * L + m / 2u;  // quantization group of block L
           part[p] = part[p] + __builtin_fmaf(bf16_to_f32(dsb[gi]), acc - hoff, bf16_to_f32(dsb[192u + gi]) * hsum);
+        }
+      }
+    }
+  }
+  // The f16 range of h. An h of 2^15 or more may round to an infinite f16,
+  // which makes its rows' sums NaN (inf - inf). A wave holding such a sum
+  // recomputes its two rows without the LDS copy: each lane reads its 32
+  // columns of every block from the h slots (this launch's values, already
+  // seen complete), scales them by 2^-k below 2^15 (f16_range), and adds the
+  // block's terms times 2^k. Checking the sums once here keeps the blocks'
+  // exchange path as it is (a check per block measured 0.07 us per layer).
+  if (__any(!__builtin_isfinite(part[0]) || !__builtin_isfinite(part[1]))) {
+    part[0] = part[1] = 0.0f;
+#pragma unroll
+    for (uint32_t L = 0; L < 3; ++L) {
+      float hc[32];
+#pragma unroll
+      for (uint32_t c = 0; c < 32; ++c) hc[c] = slot_val(slot_load(h_slots + 256u * L + 32u * m + c));
+      const F16Range r = f16_range(lane_absmax<32>(hc));
+      float hsum = 0.0f;
+#pragma unroll
+      for (uint32_t c = 0; c < 32; ++c) {
+        hc[c] = static_cast<float>(static_cast<_Float16>(hc[c] * r.down));  // the f16 values the dot products see
+        hsum = hsum + hc[c];
+      }
+      f16x2_t hp[16];
+#pragma unroll
+      for (uint32_t i = 0; i < 4; ++i) f16_pairs8(hc + 8 * i, hp + 4 * i);
+      float hoff = 0.0f;
+#pragma unroll
+      for (uint32_t i = 0; i < 4; ++i) hoff = dot8_off_only(hp + 4 * i, hoff);
+      if (have) {
+#pragma unroll
+        for (uint32_t p = 0; p < 2; ++p) {
+          const uint16_t* dsb = sc16 + 1024u + 12u * (8u * p + r8);
+          float acc = 0.0f;
+          acc = dot8_q4_off(dq[p][L].x, hp + 0, acc);
+          acc = dot8_q4_off(dq[p][L].y, hp + 4, acc);
+          acc = dot8_q4_off(dq[p][L].z, hp + 8, acc);
+          acc = dot8_q4_off(dq[p][L].w, hp + 12, acc);
+          const uint32_t gi = 4u * L + m / 2u;
+          part[p] = part[p] + r.up * __builtin_fmaf(bf16_to_f32(dsb[gi]), acc - hoff, bf16_to_f32(dsb[192u + gi]) * hsum);
         }
       }
     }

@@ -480,6 +480,42 @@ __device__ __forceinline__ float dot8_off_only(const f16x2_t* xp, float acc) {
   return acc;
 }
 
+// ---- The range of the f16 operands ----------------------------------------
+// dot8_q4_off takes its activations as f16, which holds magnitudes up to
+// 65504. A block of values whose largest magnitude amax is 2^15 or more is
+// scaled by 2^-k before the conversion, exactly (a power of two; values
+// 2^25 below amax may lose bits as f16 subnormals), with k the smallest that
+// brings amax below 2^15; the block's fp32 dot products are multiplied by 2^k
+// afterwards, also exactly. For amax below 2^15 (and for a non-finite amax,
+// whose inf or NaN propagates anyway) k = 0 and both factors are 1.0, so the
+// results there are the unscaled ones bit for bit.
+struct F16Range {
+  float up;    // 2^k: multiplies the block's dot products
+  float down;  // 2^-k: multiplies the block's values before the f16 conversion
+};
+__device__ __forceinline__ F16Range f16_range(float amax) {
+  const uint32_t e = (__float_as_uint(amax) >> 23) & 0xffu;   // biased exponent: amax < 2^(e - 126)
+  const uint32_t k = (e >= 142u && e < 255u) ? e - 141u : 0u;  // amax * 2^-k < 2^15
+  return F16Range{__uint_as_float((127u + k) << 23), __uint_as_float((127u - k) << 23)};
+}
+// Largest magnitude over each aligned group of 32 lanes (every lane gets it).
+__device__ __forceinline__ float half_wave_absmax(float v) {
+  v = __builtin_fabsf(v);
+  v = __builtin_fmaxf(v, dpp_f32<DPP_XOR1>(v));
+  v = __builtin_fmaxf(v, dpp_f32<DPP_XOR2>(v));
+  v = __builtin_fmaxf(v, dpp_f32<DPP_HALF_MIRROR>(v));  // quad-uniform data: pairs quads 0-1, 2-3
+  v = __builtin_fmaxf(v, dpp_f32<DPP_MIRROR>(v));       // 8-uniform data: pairs the half-rows
+  return __builtin_fmaxf(v, __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F)));  // lanes i, i ^ 16
+}
+// Largest magnitude of n values held by one lane.
+template <int N>
+__device__ __forceinline__ float lane_absmax(const float* v) {
+  float m = 0.0f;
+#pragma unroll
+  for (int i = 0; i < N; ++i) m = __builtin_fmaxf(m, __builtin_fabsf(v[i]));
+  return m;
+}
+
 // f16 pairs of eight consecutive fp32 values in the order dot8_q4_off expects
 __device__ __forceinline__ void f16_pairs8(const float* x, f16x2_t* xp) {
   xp[0] = f16x2_of(x[0], x[4]);
