@@ -445,6 +445,44 @@ def bench_prefill(torch, oh, exe, args):
     return out
 
 
+def bench_peaks(torch, exe, read_bytes=2 << 30, mfma_iters=50000, reps=5):
+    """The achievable peaks on this device (obs_measure_read / obs_measure_mfma):
+    a cold read of read_bytes (8x the 256 MB Infinity Cache) with the fused
+    decode's 16-byte non-temporal loads, and bf16 MFMAs with nothing else to do,
+    with the core clock they ran at. Best of `reps` launches each."""
+    buf = torch.empty(read_bytes, dtype=torch.uint8, device="cuda")
+    sink = torch.zeros(4, dtype=torch.int32, device="cuda")
+    clocks = torch.zeros(2, dtype=torch.int64, device="cuda")
+    torch.cuda.synchronize()
+    exe.measure_read(buf.data_ptr(), read_bytes, sink.data_ptr())
+    best = None
+    for _ in range(reps):
+        exe.timer_start()
+        exe.measure_read(buf.data_ptr(), read_bytes, sink.data_ptr())
+        ms = exe.timer_stop()
+        best = ms if best is None else min(best, ms)
+    read_gbs = read_bytes / (best * 1e-3) / 1e9
+    flops = exe.measure_mfma(mfma_iters // 10, sink.data_ptr(), clocks.data_ptr())
+    best, clk = None, None
+    for _ in range(reps):
+        exe.timer_start()
+        flops = exe.measure_mfma(mfma_iters, sink.data_ptr(), clocks.data_ptr())
+        ms = exe.timer_stop()
+        cyc, ticks = (int(v) for v in clocks.cpu())
+        if best is None or ms < best:
+            best, clk = ms, cyc / (ticks / 1e8) / 1e9
+    del buf
+    torch.cuda.empty_cache()
+    tf = flops / (best * 1e-3) / 1e12
+    return {"hbm_read_gbs": round(read_gbs, 1), "hbm_read_bytes": read_bytes,
+            "hbm_read_frac_of_peak": round(read_gbs / HBM_PEAK_GBS, 4),
+            "mfma_bf16_tflops": round(tf, 1), "mfma_clock_ghz": round(clk, 3),
+            "mfma_frac_of_peak": round(tf / BF16_PEAK_TFLOPS, 4),
+            "method": ("obs_measure_read: 2 GiB read once with 16-byte non-temporal loads, 8 workgroups per CU; "
+                       "obs_measure_mfma: v_mfma_f32_32x32x16_bf16 only, 4 chains per wave, 8 waves per CU; "
+                       "best of 5 launches each, HIP events on the context's stream")}
+
+
 def _median_us(fn, reps):
     """Median wall time of `reps` calls of fn, in microseconds (one untimed call first)."""
     fn()
@@ -547,6 +585,10 @@ def main():
     rtr = bench_router(torch, oh, exe)
     pre = None if args.no_prefill else bench_prefill(torch, oh, exe, args)
     dcd = None if args.no_decoder else bench_decoder(torch, oh, exe, args)
+    peaks = bench_peaks(torch, exe)
+    if dec["roofline"] is not None:
+        dec["roofline"]["achievable_peak"] = peaks["hbm_read_gbs"]
+        dec["roofline"]["frac_of_achievable"] = round(dec["roofline"]["achieved"] / peaks["hbm_read_gbs"], 4)
     cpu = None
     if not args.no_cpu:
         # every core this process may run on, capped by OMP_NUM_THREADS where it is set (the
@@ -587,7 +629,10 @@ def main():
             "gemm_us": round(pre["gemm_us"], 2),
             "gemm_tflops": None if pre["gemm_tflops"] is None else round(pre["gemm_tflops"], 1),
             "frac_of_bf16_peak": None if pre["gemm_tflops"] is None else round(pre["gemm_tflops"] / BF16_PEAK_TFLOPS, 4),
+            "frac_of_achievable_mfma": None if pre["gemm_tflops"] is None else
+            round(pre["gemm_tflops"] / peaks["mfma_bf16_tflops"], 4),
             "kernels": {n: round(v["avg_us"], 2) for n, v in pre["kernels"].items()}},
+        "achievable": peaks,
         "decoder": None if dcd is None else {
             "workload": f"greedy decode, {args.layers}-layer Qwen3-30B-A3B shape, bf16 KV cache, "
                         f"positions {dcd['positions'][0]}-{dcd['positions'][1]} (context ~4096)",

@@ -113,6 +113,20 @@ int obs_profile_count(const obs_ctx* ctx);
 int obs_profile_stat(const obs_ctx* ctx, int i, const char** name, double* total_ms, int64_t* launches);
 int obs_profile_clear(obs_ctx* ctx);
 
+/* Achievable peaks (no reference counterpart; the reference's harness is a
+ * wall-clock token timer, main.rs:99-116): the ceilings the roofline
+ * fractions are read against, measured on the device itself. Both launch on
+ * the context's stream and are timed by the caller (obs_timer_*).
+ * obs_measure_read: every 16-byte chunk of [src, src + bytes) read once with
+ * the fused decode's non-temporal 16-byte loads (8 workgroups per CU); sink is
+ * a 4-byte device word the kernel never writes in practice. obs_measure_mfma:
+ * v_mfma_f32_32x32x16_bf16 only, 4 independent chains per wave, 8 waves per
+ * CU, `iters` steps; *flops (host) receives the flop count of the launch and
+ * clocks[0..1] (device) the core clock cycles and 100 MHz constant-clock
+ * ticks of one wave's loop, whose ratio is the clock the MFMAs ran at. */
+int obs_measure_read(obs_ctx* ctx, const void* src, size_t bytes, uint32_t* sink);
+int obs_measure_mfma(obs_ctx* ctx, uint32_t iters, float* sink, uint64_t* clocks, double* flops);
+
 /* ------------------------------------------------------------------ */
 /* Quantized tensor kernels                                            */
 /* ------------------------------------------------------------------ */

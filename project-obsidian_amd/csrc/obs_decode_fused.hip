@@ -126,9 +126,10 @@ __device__ __forceinline__ void unpack_bf16x8(const uint4& v, float* f) {
 }
 
 // NQ = router logit slots per lane: 2 for up to 128 experts, 4 for up to 256.
-// One workgroup per CU, so one wave per SIMD: the compiler is told so and need
-// not trade waits for registers.
-template <int NQ>
+// NORM: the layer has a post-attention norm weight (rmsnorm of the input
+// first). One workgroup per CU, so one wave per SIMD: the compiler is told so
+// and need not trade waits for registers.
+template <int NQ, bool NORM>
 __global__ void __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) decode_fused_kernel(FusedArgs a) {
   constexpr int RT = NQ / 2;  // router rows per wave
   __shared__ uint32_t s_epoch;
@@ -158,11 +159,11 @@ __global__ void __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 
     const uint4* xp = reinterpret_cast<const uint4*>(a.x + 32u * lane);
 #pragma unroll
     for (int i = 0; i < 4; ++i) xq[i] = xp[i];
-    // unconditional (x again when there is no norm, unused then): a load under
-    // a branch makes the compiler wait for every load in flight at the join
-    const uint4* np = reinterpret_cast<const uint4*>((a.norm_w ? a.norm_w : a.x) + 32u * lane);
+    if constexpr (NORM) {
+      const uint4* np = reinterpret_cast<const uint4*>(a.norm_w + 32u * lane);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) nq[i] = np[i];
+      for (int i = 0; i < 4; ++i) nq[i] = np[i];
+    }
   }
   // router rows of this wave: e = 4j + wave (+128)
   const uint32_t e0 = 4u * j + wave;
@@ -203,7 +204,7 @@ __global__ void __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 
   float xf[32];
 #pragma unroll
   for (int i = 0; i < 4; ++i) unpack_bf16x8(xq[i], xf + 8 * i);
-  if (a.norm_w) {
+  if constexpr (NORM) {
     // RMSNorm in obs_rmsnorm's sequence (the lane owns 2048/64 contiguous
     // columns): serial fma of x^2, wave butterfly, 1/sqrt(ss/2048 + eps), then
     // x*inv*w rounded to bf16 — bit-identical to the standalone kernel.
@@ -660,10 +661,20 @@ int launch_fused_decode_ws(obs_ctx* ctx, const obs_moe_config* cfg, const obs_mo
   FusedArgs a{L->gate_w, L->gate_s, L->gate_b, L->up_w, L->up_s, L->up_b, L->down_w, L->down_s, L->down_b,
               L->router_w, L->router_s, L->router_b, x, residual, y, L->norm_w, cfg->rms_eps, ids_out, w_out,
               static_cast<unsigned char*>(ws), cfg->n_exp, cfg->norm_topk, cfg->route_rule};
-  if (cfg->n_exp <= 128)
-    OBS_LAUNCH(ctx, "decode_fused", decode_fused_kernel<2><<<NWG, 256, 0, ctx->stream>>>(a));
-  else
-    OBS_LAUNCH(ctx, "decode_fused", decode_fused_kernel<4><<<NWG, 256, 0, ctx->stream>>>(a));
+  // the layer with a post-attention norm (the decoder's) and without (the
+  // bare MoE block) are two instantiations, so each is timed under its own name
+  const bool norm = L->norm_w != nullptr;
+  if (cfg->n_exp <= 128) {
+    if (norm)
+      OBS_LAUNCH(ctx, "decode_fused_norm", decode_fused_kernel<2, true><<<NWG, 256, 0, ctx->stream>>>(a));
+    else
+      OBS_LAUNCH(ctx, "decode_fused", decode_fused_kernel<2, false><<<NWG, 256, 0, ctx->stream>>>(a));
+  } else {
+    if (norm)
+      OBS_LAUNCH(ctx, "decode_fused_norm", decode_fused_kernel<4, true><<<NWG, 256, 0, ctx->stream>>>(a));
+    else
+      OBS_LAUNCH(ctx, "decode_fused", decode_fused_kernel<4, false><<<NWG, 256, 0, ctx->stream>>>(a));
+  }
   return OBS_OK;
 }
 

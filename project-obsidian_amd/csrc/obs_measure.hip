@@ -1,0 +1,99 @@
+// obs_measure.hip — the achievable peaks the roofline fractions are read
+// against, measured on the device that runs the kernels: a cold streaming read
+// (HBM bytes per second a read-only kernel of this library's load shape gets)
+// and a bf16 MFMA-only loop (TFLOP/s of v_mfma_f32_32x32x16_bf16 with nothing
+// else to do, and the core clock it ran at). No reference counterpart: the
+// reference's harness is a wall-clock token timer (main.rs:99-116).
+#include "obs_internal.hpp"
+
+namespace {
+
+using namespace obsd;
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16_t;
+
+// Every 16-byte chunk of [src, src + n16) read once with a non-temporal
+// 16-byte load (the expert weights' load in the fused decode), four chunks in
+// flight per thread per step, the workgroups striding the buffer. The XOR of
+// what a thread read is stored only if it equals a value no input of the
+// benchmark produces, so the loads stay and nothing is written.
+__global__ void __launch_bounds__(256) peak_read_kernel(const uint4* __restrict__ src, size_t n16,
+                                                        uint32_t* __restrict__ sink) {
+  const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+  size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  uint32_t acc = 0;
+  for (; i + 3 * stride < n16; i += 4 * stride) {
+    const uint4 a = load_stream(src + i), b = load_stream(src + i + stride);
+    const uint4 c = load_stream(src + i + 2 * stride), d = load_stream(src + i + 3 * stride);
+    acc ^= (a.x ^ a.y ^ a.z ^ a.w) ^ (b.x ^ b.y ^ b.z ^ b.w) ^ (c.x ^ c.y ^ c.z ^ c.w) ^ (d.x ^ d.y ^ d.z ^ d.w);
+  }
+  for (; i < n16; i += stride) {
+    const uint4 a = load_stream(src + i);
+    acc ^= a.x ^ a.y ^ a.z ^ a.w;
+  }
+  if (acc == 0x9e3779b9u) sink[0] = acc;
+}
+
+// MFMA_CHAINS independent accumulators per wave, each advanced `iters` times
+// by v_mfma_f32_32x32x16_bf16 (32,768 flop each); two workgroups of four waves
+// per CU, so two waves share each SIMD's matrix core. Workgroup 0's first wave
+// records the core clock cycles (s_memtime) and the 100 MHz constant clock
+// ticks (s_memrealtime) its loop took, so clock = cycles / (ticks / 1e8).
+constexpr int MFMA_CHAINS = 4;
+__global__ void __launch_bounds__(256) peak_mfma_kernel(uint32_t iters, float* __restrict__ sink,
+                                                        uint64_t* __restrict__ clocks) {
+  const uint32_t lane = threadIdx.x & 63u;
+  typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+  const u32x4_t av = {0x3f803f80u + lane, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u ^ lane};
+  const bf16x8_t a = __builtin_bit_cast(bf16x8_t, av);
+  const bf16x8_t b = __builtin_bit_cast(bf16x8_t, u32x4_t{0x3c003c00u, 0x3c003c00u + lane, 0x3c003c00u, 0x3c003c00u});
+  f32x16_t c[MFMA_CHAINS];
+#pragma unroll
+  for (int k = 0; k < MFMA_CHAINS; ++k)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) c[k][v] = 0.0f;
+  const uint64_t t0 = __builtin_amdgcn_s_memtime(), r0 = __builtin_amdgcn_s_memrealtime();
+  for (uint32_t it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int k = 0; k < MFMA_CHAINS; ++k) c[k] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c[k], 0, 0, 0);
+  }
+  const uint64_t t1 = __builtin_amdgcn_s_memtime(), r1 = __builtin_amdgcn_s_memrealtime();
+  float s = 0.0f;
+#pragma unroll
+  for (int k = 0; k < MFMA_CHAINS; ++k)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) s += c[k][v];
+  if (s == 1234.5f) sink[0] = s;
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    clocks[0] = t1 - t0;
+    clocks[1] = r1 - r0;
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int obs_measure_read(obs_ctx* ctx, const void* src, size_t bytes, uint32_t* sink) {
+  if (!ctx) return OBS_E_INVALID;
+  if (!src || !sink) return obs::set_error(ctx, OBS_E_INVALID, "obs_measure_read: null pointer");
+  if (bytes == 0 || bytes % 16 != 0 || !obs::aligned(src, 16))
+    return obs::set_error(ctx, OBS_E_ALIGN, "obs_measure_read: bytes must be a positive multiple of 16 at a 16-byte boundary");
+  const uint32_t grid = static_cast<uint32_t>(ctx->num_cus) * 8u;
+  OBS_LAUNCH(ctx, "peak_read", peak_read_kernel<<<grid, 256, 0, ctx->stream>>>(static_cast<const uint4*>(src), bytes / 16,
+                                                                                 sink));
+  return OBS_OK;
+}
+
+int obs_measure_mfma(obs_ctx* ctx, uint32_t iters, float* sink, uint64_t* clocks, double* flops) {
+  if (!ctx) return OBS_E_INVALID;
+  if (!sink || !clocks) return obs::set_error(ctx, OBS_E_INVALID, "obs_measure_mfma: null pointer");
+  if (iters == 0) return obs::set_error(ctx, OBS_E_INVALID, "obs_measure_mfma: iters must be positive");
+  const uint32_t grid = static_cast<uint32_t>(ctx->num_cus) * 2u;
+  OBS_LAUNCH(ctx, "peak_mfma", peak_mfma_kernel<<<grid, 256, 0, ctx->stream>>>(iters, sink, clocks));
+  if (flops) *flops = static_cast<double>(grid) * 4.0 * MFMA_CHAINS * iters * (2.0 * 32 * 32 * 16);
+  return OBS_OK;
+}
+
+}  // extern "C"

@@ -62,6 +62,7 @@ EXPORTS = (
     "obs_q4_gemv", "obs_attn_prep", "obs_sdpa_workspace", "obs_sdpa_decode", "obs_embed_q4",
     "obs_argmax_workspace", "obs_argmax", "obs_embed_q4_rows", "obs_attn_prep_rows", "obs_sdpa_prefill",
     "obs_attn_decode", "obs_dispatch_gate", "obs_dispatch_info", "obs_set_dispatch_facts", "obs_debug_ffn_wait",
+    "obs_measure_read", "obs_measure_mfma",
 )
 
 
@@ -159,6 +160,8 @@ def lib() -> C.CDLL:
         "obs_dispatch_info": (i32, [vp, C.POINTER(C.c_int), C.POINTER(C.c_int), C.POINTER(C.c_int)]),
         "obs_set_dispatch_facts": (i32, [vp, C.c_int, C.c_int]),
         "obs_debug_ffn_wait": (i32, [vp, u32, u32]),
+        "obs_measure_read": (i32, [vp, vp, sz, vp]),
+        "obs_measure_mfma": (i32, [vp, u32, vp, vp, C.POINTER(C.c_double)]),
         "obs_stream_hold": (i32, [vp, u32]),
         "obs_profile_enable": (i32, [vp, C.c_int]),
         "obs_profile_accumulate": (i32, [vp]),
@@ -315,6 +318,16 @@ class ObsidianExecutor:
         """The OBS_PATH_* one-launch paths this context's device may take."""
         n, xm, io = self.dispatch_info()
         return int(lib().obs_dispatch_gate(n, int(xm), int(io)))
+
+    def measure_read(self, src, nbytes: int, sink) -> None:
+        """Launch the streaming-read peak kernel over nbytes at src (time it with timer_start/stop)."""
+        self._check(lib().obs_measure_read(self.ctx, _ptr(src), int(nbytes), _ptr(sink)))
+
+    def measure_mfma(self, iters: int, sink, clocks) -> float:
+        """Launch the MFMA-only peak kernel; returns its flop count."""
+        f = C.c_double()
+        self._check(lib().obs_measure_mfma(self.ctx, int(iters), _ptr(sink), _ptr(clocks), C.byref(f)))
+        return f.value
 
     def debug_ffn_wait(self, extra_count: int, wait_us: int) -> None:
         self._check(lib().obs_debug_ffn_wait(self.ctx, int(extra_count), int(wait_us)))

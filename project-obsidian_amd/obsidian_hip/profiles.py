@@ -27,7 +27,8 @@ PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 # kernel -> (pattern of its rocprofv3 name, the sources it is compiled from)
 KERNELS = {
-    "decode_fused": (r"decode_fused_kernel<2>", ("csrc/obs_decode_fused.hip", "csrc/obs_internal.hpp")),
+    "decode_fused": (r"decode_fused_kernel<2, false>", ("csrc/obs_decode_fused.hip", "csrc/obs_internal.hpp")),
+    "decode_fused_norm": (r"decode_fused_kernel<2, true>", ("csrc/obs_decode_fused.hip", "csrc/obs_internal.hpp")),
     "grouped_gemm_gateup": (r"grouped_gemm_kernel<1u, 3u>", ("csrc/obs_prefill.hip", "csrc/obs_internal.hpp")),
     "grouped_gemm_down": (r"grouped_gemm_kernel<2u, 5u>", ("csrc/obs_prefill.hip", "csrc/obs_internal.hpp")),
     "moe_ffn": (r"moe_ffn_kernel<2u>", ("csrc/obs_prefill.hip", "csrc/obs_internal.hpp")),
@@ -42,6 +43,8 @@ COPY = r"copyBuffer"
 _PROJ = 768 * 2048 // 2 + 2 * 2 * (768 * 2048 // 64)
 ALGORITHMIC = {
     "decode_fused": 8 * 3 * _PROJ + (128 * 2048 + 2 * 2 * (128 * 2048 // 64)) + 2 * 2 * 2048,
+    # with the post-attention norm: its 2048 bf16 weights are read too
+    "decode_fused_norm": 8 * 3 * _PROJ + (128 * 2048 + 2 * 2 * (128 * 2048 // 64)) + 2 * 2 * 2048 + 2 * 2048,
     "grouped_gemm_gateup": 128 * 2 * _PROJ + 2048 * 2048 * 2 + 2048 * 8 * 768 * 2,
     "grouped_gemm_down": 128 * _PROJ + 2048 * 8 * 768 * 2 + 2048 * 8 * 2048 * 2,
 }
@@ -154,8 +157,32 @@ def stats_md(path: str, line: Optional[str], cmd: str) -> str:
         md.append(f"| `{nm}` | {r['Calls']} | {float(r['AverageNs']) / 1000:.2f} | {float(r['MinNs']) / 1000:.2f} | "
                   f"{float(r['MaxNs']) / 1000:.2f} | {float(r['Percentage']):.2f} |")
     if line:
+        md += _roofline_check(rows, json.loads(line))
         md += ["", "bench.py's line from the same run:", "", "```json", line.strip(), "```"]
     return "\n".join(md) + "\n"
+
+
+def _roofline_check(rows, line: Dict):
+    """The line's decode roofline against this run's rocprof average of the
+    kernel it names (the MoE sweep's launches alone: the decoder's MoE half is
+    the `decode_fused_norm` instantiation, timed under its own name)."""
+    rf = line.get("roofline") or {}
+    k = rf.get("kernel")
+    if k not in KERNELS or not line.get("config", {}).get("layers_per_step"):
+        return []
+    hit = [r for r in rows if _short(r["Name"]) == k]
+    if not hit:
+        return []
+    avg_us = float(hit[0]["AverageNs"]) / 1000
+    n = int(line["config"]["layers_per_step"])
+    frac = rf["bytes_per_launch"] / (avg_us * 1e-6) / (rf["peak"] * 1e9)
+    return ["", f"Roofline check for `{k}` ({hit[0]['Calls']} launches of the {n}-layer sweep):", "",
+            f"- {n} x {avg_us:.3f} µs (rocprof average) = {n * avg_us / 1000:.4f} ms, against the line's "
+            f"ms_per_step {line['ms_per_step']:.4f} (the rest is the gap between launches: "
+            f"{(line['ms_per_step'] * 1000 / n - avg_us):.3f} µs per launch);",
+            f"- {rf['bytes_per_launch']:,} B / {avg_us:.3f} µs / {rf['peak']:.0f} GB/s = frac {frac:.4f} against the "
+            f"line's {rf['frac']:.4f}, which the timed region gives launch gaps included "
+            f"({line['decode_us_per_layer']:.3f} µs per layer)."]
 
 
 def main(argv=None) -> int:

@@ -17,7 +17,7 @@ def _csv(path, rows):
 
 
 def test_traffic_scales_by_the_copy_calibration(tmp_path):
-    k = "void (anonymous namespace)::decode_fused_kernel<2>(FusedArgs)"
+    k = "void (anonymous namespace)::decode_fused_kernel<2, false>(FusedArgs)"
     cp = "__amd_rocclr_copyBuffer"
     _csv(tmp_path / "f.csv", [{"Dispatch_Id": i, "Kernel_Name": k, "Counter_Name": "FETCH_SIZE", "Counter_Value": 10000 + i}
                               for i in (1, 2)])
