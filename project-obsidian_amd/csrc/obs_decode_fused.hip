@@ -135,7 +135,7 @@ __global__ void __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 
   __shared__ uint32_t s_epoch;
   __shared__ int s_abort;
   __shared__ float s_y[FK][64];
-  __shared__ __attribute__((aligned(16))) uint64_t s_ck[4][MAX_E / 4];  // routing: each wave's share of the keys
+  __shared__ __attribute__((aligned(16))) double s_ck[4][MAX_E / 4];  // routing: each wave's share of the keys
   __shared__ uint32_t s_cnt[4][MAX_E];                                // routing: each wave's partial counts
   __shared__ int32_t s_sel_id[FK];                                    // routing: expert of each rank (-1: none)
   __shared__ float s_sel_p[FK];                                       // routing: its p
@@ -270,10 +270,11 @@ __global__ void __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 
   // that order; composite keys (p << 9) | (511 - id) make the order strict.
   // Each wave counts, for all experts (NQ per lane), the composites that
   // exceed theirs among its quarter of the experts (read back from its own LDS
-  // area as broadcasts), and one barrier adds the four partial counts. (All
-  // 256 threads counting one expert against half of all keys was bound by the
-  // LDS broadcast reads, 0.70 us; eight argmax rounds on one wave were bound by
-  // their serial latency, ~1 us.)
+  // area as broadcasts), and one barrier adds the four partial counts. The
+  // composites (< 2^40) are held as doubles, so one exact fp64 subtraction and
+  // its sign bit compare a pair: no compare writes a lane mask that the next
+  // instruction must wait for (64-bit integer compares into a mask and a
+  // carry-add took 0.65 us for the count, this 0.4 us).
   bool ok = true;
   float lg[NQ];
   {
@@ -298,11 +299,11 @@ __global__ void __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 
   int key[NQ];
   route_keys<NQ>(lg, n_exp, lane, a.route_rule, key);
   constexpr uint32_t QW = 16u * NQ;  // experts per wave's share: [QW * wave, QW * (wave + 1))
-  uint64_t ck[NQ];
+  double ck[NQ];  // (p << 9) | (511 - id), or 0 for an absent expert and a NaN p
 #pragma unroll
   for (int q = 0; q < NQ; ++q) {
     const uint32_t id = lane + 64u * q;
-    ck[q] = key[q] >= 0 ? (static_cast<uint64_t>(key[q]) << 9) | (511u - id) : 0ull;
+    ck[q] = key[q] >= 0 ? __builtin_fma(static_cast<double>(key[q]), 512.0, static_cast<double>(511u - id)) : 0.0;
     if (id / QW == wave) s_ck[wave][id % QW] = ck[q];
   }
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");  // the wave's own LDS stores before its reads
@@ -311,13 +312,13 @@ __global__ void __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 
     uint32_t c[NQ];
 #pragma unroll
     for (int q = 0; q < NQ; ++q) c[q] = 0;
-    const uint4* cw = reinterpret_cast<const uint4*>(s_ck[wave]);
+    const double2* cw = reinterpret_cast<const double2*>(s_ck[wave]);
 #pragma unroll
     for (uint32_t i = 0; i < QW / 2; ++i) {
-      const uint4 v = cw[i];
-      const uint64_t c0 = (static_cast<uint64_t>(v.y) << 32) | v.x, c1 = (static_cast<uint64_t>(v.w) << 32) | v.z;
+      const double2 v = cw[i];
 #pragma unroll
-      for (int q = 0; q < NQ; ++q) c[q] += static_cast<uint32_t>(c0 > ck[q]) + static_cast<uint32_t>(c1 > ck[q]);
+      for (int q = 0; q < NQ; ++q)  // ck - v is exact and negative exactly when v > ck
+        c[q] += static_cast<uint32_t>(__double2hiint(ck[q] - v.x) < 0) + static_cast<uint32_t>(__double2hiint(ck[q] - v.y) < 0);
     }
 #pragma unroll
     for (int q = 0; q < NQ; ++q) s_cnt[wave][lane + 64u * q] = c[q];
@@ -325,12 +326,15 @@ __global__ void __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 
   __syncthreads();
   // rank of each of the lane's experts; the group's expert has rank g
   uint32_t rank[NQ];
-  int32_t eg = -1;
 #pragma unroll
   for (int q = 0; q < NQ; ++q) {
     const uint32_t id = lane + 64u * q;
     rank[q] = (s_cnt[0][id] + s_cnt[1][id]) + (s_cnt[2][id] + s_cnt[3][id]);
-    const unsigned long long m = __ballot(ck[q] != 0ull && rank[q] == g);
+  }
+  int32_t eg = -1;
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    const unsigned long long m = __ballot(ck[q] != 0.0 && rank[q] == g);
     eg = m ? static_cast<int32_t>(64u * q + static_cast<uint32_t>(__builtin_ctzll(m))) : eg;
   }
   const bool have = ok && eg >= 0 && static_cast<uint32_t>(eg) < n_exp;
@@ -398,7 +402,7 @@ __global__ void __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 
   if (wave == 0) {
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
-      if (ck[q] != 0ull && rank[q] < FK) {
+      if (ck[q] != 0.0 && rank[q] < FK) {
         s_sel_id[rank[q]] = static_cast<int32_t>(lane + 64u * q);
         s_sel_p[rank[q]] = __int_as_float(key[q]);
       }
