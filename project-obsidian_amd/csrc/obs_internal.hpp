@@ -292,18 +292,6 @@ __device__ __forceinline__ float readlane_f32(float v, int lane) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }
 
-// Bitwise OR over the 64 lanes, returned uniform (the row mirrors pair the
-// lanes an xor by 4, then 8, would on quad-, then half-row-uniform data).
-__device__ __forceinline__ uint32_t wave_or_u32(uint32_t v) {
-  int r = static_cast<int>(v);
-  r |= dpp_i32<DPP_XOR1>(r);
-  r |= dpp_i32<DPP_XOR2>(r);
-  r |= dpp_i32<DPP_HALF_MIRROR>(r);
-  r |= dpp_i32<DPP_MIRROR>(r);
-  return static_cast<uint32_t>((__builtin_amdgcn_readlane(r, 0) | __builtin_amdgcn_readlane(r, 16)) |
-                               (__builtin_amdgcn_readlane(r, 32) | __builtin_amdgcn_readlane(r, 48)));
-}
-
 // Xor-butterfly sum over 64 lanes with ascending offsets 1, 2, 4, 8, 16, 32;
 // the result is returned on every lane. Offsets 1 and 2 are quad
 // permutations; on quad-uniform (then half-row-uniform) data the half-row and
