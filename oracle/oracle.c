@@ -39,6 +39,11 @@
  *                                 through distinct kv heads; a numpy restatement.
  *   orc_argmax .................. ties -> first index, NaN skipped, all -inf -> 0,
  *                                 numpy argmax where no NaN.
+ *   attention_half (oracle.py) .. against an fp64 restatement of forward.rs:403-418
+ *                                 written from the reference (own dequant, norms,
+ *                                 RoPE, attention); the restatement with the RoPE
+ *                                 before the q/k norms or with the append after the
+ *                                 attention lands far outside the tolerance.
  */
 #include "oracle.h"
 

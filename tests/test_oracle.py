@@ -663,6 +663,107 @@ def test_prefill_layer_major_equals_token_by_token():
     assert rows.shape == (len(toks), H)
 
 
+def _deq4_f64(w, s, b, group=64):
+    """validate_dequant.py:26-30 in fp64: nibble j of word i is column 8i + j
+    (low bits first), w = s * q + b per 64-column group."""
+    w = np.asarray(w, np.uint32)
+    q = np.stack([(w >> (4 * j)) & 0xF for j in range(8)], axis=-1).reshape(w.shape[0], -1).astype(np.float64)
+    sf = np.repeat(_b2f(np.asarray(s)), group, axis=-1)
+    bf = np.repeat(_b2f(np.asarray(b)), group, axis=-1)
+    return sf * q + bf
+
+
+def _rms64(x, w, eps):
+    return x / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps) * w
+
+
+def _to_bf16_f64(x):
+    return _b2f(synth.f32_to_bf16_bits(np.asarray(x, np.float32)))
+
+
+def _attention_half_f64(P, x_bits, k_cache, v_cache, pos, cfg, *, rope_first=False, append_after=False):
+    """forward.rs:403-418 restated from the reference in fp64, with the stored
+    activations rounded to bf16 where the reference stores them (xn, q, k, v
+    after each kernel, the attention output, o, x1): input RMSNorm
+    (rmsnorm.metal), the three projections, the per-head q and k RMSNorm, the
+    NeoX RoPE (rope.metal: angle = pos * theta^(-2i/d), pairs (i, i + d/2)),
+    k and v appended at pos, single-query GQA attention over 0..pos
+    (sdpa_decode.metal: query head h reads kv head h / (n_heads / n_kv), scale
+    1/sqrt(d)), the o projection and the residual. The two flags plant the
+    order mistakes this restatement exists to catch."""
+    H, nh, nkv, hd, eps, theta = cfg["hidden"], cfg["n_heads"], cfg["n_kv"], cfg["head_dim"], cfg["eps"], cfg["theta"]
+    x = _b2f(x_bits)
+    xn = _to_bf16_f64(_rms64(x, _b2f(P["in_norm"]), eps))
+    proj = lambda n: _deq4_f64(P[n + "_w"], P[n + "_s"], P[n + "_b"]) @ xn
+    q = _to_bf16_f64(proj("q")).reshape(nh, hd)
+    k = _to_bf16_f64(proj("k")).reshape(nkv, hd)
+    v = _to_bf16_f64(proj("v")).reshape(nkv, hd)
+    i = np.arange(hd // 2)
+    ang = pos * theta ** (-2.0 * i / hd)
+    c, sn = np.cos(ang), np.sin(ang)
+
+    def rope(t):
+        a, b = t[:, :hd // 2], t[:, hd // 2:]
+        return np.concatenate([a * c - b * sn, b * c + a * sn], axis=1)
+
+    def norm(t, wname):
+        return _rms64(t, _b2f(P[wname]), eps)
+
+    if rope_first:
+        q = _to_bf16_f64(norm(_to_bf16_f64(rope(q)), "q_norm"))
+        k = _to_bf16_f64(norm(_to_bf16_f64(rope(k)), "k_norm"))
+    else:
+        q = _to_bf16_f64(rope(_to_bf16_f64(norm(q, "q_norm"))))
+        k = _to_bf16_f64(rope(_to_bf16_f64(norm(k, "k_norm"))))
+    kc, vc = _b2f(k_cache), _b2f(v_cache)
+    if not append_after:
+        kc[:, pos], vc[:, pos] = k, v
+    out = np.empty((nh, hd))
+    for h in range(nh):
+        g = h // (nh // nkv)
+        sc = kc[g, :pos + 1] @ q[h] / math.sqrt(hd)
+        p_ = np.exp(sc - sc.max())
+        out[h] = (p_ / p_.sum()) @ vc[g, :pos + 1]
+    attn = _to_bf16_f64(out.reshape(-1))
+    o = _to_bf16_f64(_deq4_f64(P["o_w"], P["o_s"], P["o_b"]) @ attn)
+    return _to_bf16_f64(x + o)
+
+
+def test_attention_half_composition_against_fp64_restatement():
+    """O.attention_half (forward.rs:403-418) against the fp64 restatement above,
+    written from the reference without the oracle's kernels, within 1e-2 in
+    the 2-norm and a few bf16 steps per element (the two round the stored
+    activations at the same points, from fp32 / fp64 sums that differ in the
+    last bits). The restatement with the RoPE before the q/k norms, or with
+    k and v appended after the attention, lands far outside that: the
+    composition is pinned, not only its primitives. Checked at position 0
+    (the token attends to itself alone, so its own v must be in the cache
+    first) and at position 5 over cached entries."""
+    H, nh, nkv, hd, E, I, V, ml = 256, 4, 2, 64, 4, 128, 64, 16
+    cfg = {"hidden": H, "n_heads": nh, "n_kv": nkv, "head_dim": hd, "eps": 1e-6, "theta": 1e4}
+    lays, _ = synth.decoder_weights(21, 1, H, nh, nkv, hd, E, I, V)
+    P = lays[0]
+    P["q_norm"] = synth.f32_to_bf16_bits(np.linspace(0.3, 2.5, hd).astype(np.float32))  # far from uniform
+    P["k_norm"] = synth.f32_to_bf16_bits(np.linspace(2.0, 0.4, hd).astype(np.float32))
+    rng = np.random.default_rng(22)
+    x = synth.bf16_normal(rng, H)
+    for pos in (0, 5):
+        kc = synth.bf16_normal(rng, (nkv, ml, hd))
+        vc = synth.bf16_normal(rng, (nkv, ml, hd))
+        ref = _attention_half_f64(P, x, kc, vc, pos, cfg)
+        got = _b2f(O.attention_half(P, x, kc.copy(), vc.copy(), pos, cfg))
+        delta = ref - _b2f(x)  # the attention's contribution, where the orders show
+        d = got - ref
+        rel = np.linalg.norm(d) / np.linalg.norm(delta)
+        assert rel < 1e-2, (pos, rel)
+        assert np.all(np.abs(d) <= 4 * np.abs(ref) * 2.0 ** -8 + 1e-2 * np.sqrt(np.mean(delta ** 2))), pos
+        for plant in ({"rope_first": True}, {"append_after": True}):
+            if pos == 0 and "rope_first" in plant:
+                continue  # the rotation at position 0 is the identity: the orders agree there
+            bad = _attention_half_f64(P, x, kc, vc, pos, cfg, **plant)
+            assert np.linalg.norm(bad - got) / np.linalg.norm(delta) > 0.1, (pos, plant)  # 0.26 and 0.44 at pos 5
+
+
 # ---------------------------------------------------------------- CPU baselines
 def test_router_baseline_is_the_shader_order_router():
     """orc_router_baseline = the serial (shader-order) 8-bit dot per logit,
