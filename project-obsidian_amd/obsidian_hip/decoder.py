@@ -237,8 +237,12 @@ class Model:
         q/k/v as 4-bit GEMMs, q/k norm + RoPE + cache appends at pos0 + t,
         causal attention, o as a GEMM plus the residual, and the MoE prefill
         (post-attention norm, GPU routing and grouping, grouped GEMMs,
-        rank-order combine with the residual). Returns the buffer holding the
-        last layer's output rows [T, hidden]. trace: a list that receives, per
+        rank-order combine with the residual). With OBSIDIAN_NO_GEMM set
+        (forward.rs:124-126, read per call like the reference's switch) the MoE
+        half runs token by token through the decode path instead of the
+        grouped GEMMs (forward.rs:233-247), the anchor the grouped path is
+        checked against at full size. Returns the buffer holding the last
+        layer's output rows [T, hidden]. trace: a list that receives, per
         layer, host copies (input rows, rows after attention, output rows)."""
         c, e, g = self.cfg, self.exe, self.glob
         toks = np.ascontiguousarray(tokens, dtype=np.int32).reshape(-1)
@@ -247,6 +251,7 @@ class Model:
             raise ValueError("empty prompt")
         if pos0 < 0 or pos0 + T > c.max_len:
             raise ValueError(f"context overflow: positions {pos0}..{pos0 + T} past max_len {c.max_len}")
+        no_gemm = "OBSIDIAN_NO_GEMM" in os.environ
         B = self._prefill_buffers(T)
         e._check(lib().obs_upload(e.ctx, B["tokens"].ptr, toks.ctypes.data, toks.nbytes))
         qd, kvd, H = c.n_heads * c.head_dim, c.n_kv * c.head_dim, c.hidden
@@ -276,7 +281,12 @@ class Model:
             e.scaled_add_raw(x, B["o"], 1.0, T * H)                                             # x1 = x + o
             if trace is not None:
                 stages.append(x.download()[:T].copy())
-            e.moe_prefill(self.moe_cfg, L["moe"], x, x2, T, residual=x, ws=B["ws"])             # :162-238
+            if no_gemm:  # per-token expert mat-vecs (forward.rs:233-247): one decode MoE call per row
+                for t in range(T):
+                    off = t * H * 2
+                    e.moe_decode(self.moe_cfg, L["moe"], x.ptr + off, x2.ptr + off, residual=x.ptr + off)
+            else:
+                e.moe_prefill(self.moe_cfg, L["moe"], x, x2, T, residual=x, ws=B["ws"])         # :162-238
             x, x2 = x2, x
             if trace is not None:
                 trace.append(tuple(stages) + (x.download()[:T].copy(),))

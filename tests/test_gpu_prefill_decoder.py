@@ -208,6 +208,45 @@ def test_prefill_vs_oracle(exe, small, pos0, toks):
     print(f"prefill pos0 {pos0} T {T}: worst stage error {worst:.2e}")
 
 
+def test_prefill_no_gemm_switch(exe, small, monkeypatch):
+    """OBSIDIAN_NO_GEMM (forward.rs:124-126, :233-247): the prefill's MoE half
+    runs per token through the decode path instead of the grouped GEMMs. Each
+    layer's MoE output on that path is within 1e-2 of the fp64 oracle on the
+    GPU's own post-attention rows (routing from those rows), and the first
+    layer's output, whose input is the same on both paths, is within 1e-2 of
+    the grouped path's: the switch is the full-size anchor of the grouped
+    GEMM that the reference keeps."""
+    CFG = small[5]
+    OCFG = _ocfg(CFG)
+    toks, pos0 = [7, 1, 500, 7, 20, 64], 3
+    rng = np.random.default_rng(1777)
+    host = [(synth.bf16_normal(rng, (CFG.n_kv, CFG.max_len, CFG.head_dim)),
+             synth.bf16_normal(rng, (CFG.n_kv, CFG.max_len, CFG.head_dim))) for _ in range(CFG.n_layers)]
+    traces = {}
+    for mode in ("gemm", "no_gemm"):
+        if mode == "no_gemm":
+            monkeypatch.setenv("OBSIDIAN_NO_GEMM", "1")
+        else:
+            monkeypatch.delenv("OBSIDIAN_NO_GEMM", raising=False)
+        m = _model_with_caches(exe, small, host)
+        try:
+            traces[mode] = []
+            m.prefill_layers(toks, pos0, traces[mode])
+            exe.device_status()
+        finally:
+            m.close()
+    monkeypatch.delenv("OBSIDIAN_NO_GEMM", raising=False)
+    for il, ((P, moe), (x_in, x1, x_out)) in enumerate(zip(small[4], traces["no_gemm"])):
+        x1n = O.rmsnorm(x1, P["post_norm"], OCFG["eps"])
+        _, ids, w = O.router(moe, x1n, CFG.top_k, CFG.norm_topk)
+        ref64 = O.moe_prefill(moe, x1n, ids, w, O.MODE_F64) + _f(x1)
+        _close(_f(x_out), ref64, 1e-2, 2.0)
+    g0, n0 = traces["gemm"][0], traces["no_gemm"][0]
+    assert np.array_equal(g0[0], n0[0]) and np.array_equal(g0[1], n0[1])  # same input and attention half
+    rel = _close(_f(n0[2]), _f(g0[2]), 1e-2, 2.0)
+    print(f"no-GEMM prefill: layer 0 MoE output vs the grouped path rel {rel:.2e}")
+
+
 def test_prefill_then_decode_matches_token_steps(exe, small):
     """The same prompt through prefill (GEMMs, batch attention) and through
     per-token steps (mat-vecs, decode attention): the first layer's cache
