@@ -3,6 +3,7 @@
     python -m obsidian_hip.profiles traffic --fetch F.csv --write W.csv \\
         --copy-fetch CF.csv --copy-write CW.csv [--out DIR]
     python -m obsidian_hip.profiles stats --stats S.csv [--line bench.json] [--out DIR]
+    python -m obsidian_hip.profiles mfma --pmc P.csv [--kernel moe_ffn] [--out DIR]
 
 `traffic` turns two `rocprofv3 --pmc` runs of bench.py (FETCH_SIZE, then
 WRITE_SIZE, KiB per dispatch) into HBM bytes per launch, each counter scaled by
@@ -10,6 +11,8 @@ what it reads for a plain device copy of known size (bench.py --calibrate-copy),
 and records for each kernel a digest of the sources it is built from, so a
 reader (bench.py) can tell whether the figure still describes the code.
 `stats` turns a `rocprofv3 --kernel-trace --stats` CSV into a Markdown table.
+`mfma` turns a `rocprofv3 --pmc` run of the MFMA counters into the matrix
+and vector pipes' busy fractions of one kernel.
 """
 from __future__ import annotations
 
@@ -185,6 +188,68 @@ def _roofline_check(rows, line: Dict):
             f"({line['decode_us_per_layer']:.3f} µs per layer)."]
 
 
+MFMA_COUNTERS = ("SQ_VALU_MFMA_BUSY_CYCLES", "SQ_INSTS_MFMA", "SQ_INSTS_VALU", "SQ_ACTIVE_INST_VALU",
+                 "SQ_VALU_MFMA_COEXEC_CYCLES", "SQ_WAVE_CYCLES", "SQ_WAIT_INST_ANY", "GRBM_GUI_ACTIVE")
+# flop of one prefill FFN launch at T = 2048, top-8: gate/up 2 x T k x 2 I x H, down 2 x T k x H x I
+PREFILL_FFN_FLOP = 2 * 2048 * 8 * (2 * 768) * 2048 + 2 * 2048 * 8 * 2048 * 768
+
+
+def mfma_util(path: str, kernel: str, first: int = 10, simds: int = 1024, xcds: int = 8) -> Dict:
+    """Per-dispatch means of the MFMA counters for `kernel`'s first `first`
+    dispatches of a `rocprofv3 --pmc` CSV, and the figures derived from them.
+    GRBM_GUI_ACTIVE is summed over the XCDs, so per XCD it is / xcds; a SIMD's
+    busy fractions are counter / (cycles x simds); SQ_ACTIVE_INST_VALU counts
+    in units of 4 cycles."""
+    per = collections.defaultdict(lambda: collections.defaultdict(float))
+    span = {}
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            if _short(r["Kernel_Name"]) != kernel:
+                continue
+            d = int(r["Dispatch_Id"])
+            per[d][r["Counter_Name"]] += float(r["Counter_Value"])
+            if "Start_Timestamp" in r and r.get("End_Timestamp"):
+                span[d] = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000.0
+    ids = sorted(per)[:first]
+    if not ids:
+        raise ValueError(f"no dispatches of {kernel} in {path}")
+    m = {c: sum(per[i].get(c, 0.0) for i in ids) / len(ids) for c in MFMA_COUNTERS}
+    us = sum(span.get(i, 0.0) for i in ids) / len(ids)
+    cyc = m["GRBM_GUI_ACTIVE"] / xcds
+    mfma = m["SQ_VALU_MFMA_BUSY_CYCLES"] / (cyc * simds)
+    valu = 4.0 * m["SQ_ACTIVE_INST_VALU"] / (cyc * simds)
+    both = m["SQ_VALU_MFMA_COEXEC_CYCLES"] / (cyc * simds)
+    return {"dispatches": len(ids), "us": us, "clock_ghz": cyc / us / 1e3 if us else None,
+            "mfma_insts": m["SQ_INSTS_MFMA"], "mfma_util": mfma, "valu_per_mfma": m["SQ_INSTS_VALU"] / m["SQ_INSTS_MFMA"],
+            "valu_busy": valu, "coexec": both, "neither": 1.0 - (mfma + valu - both),
+            "tflops": PREFILL_FFN_FLOP / us / 1e6 if us else None,
+            "padded_tflops": m["SQ_INSTS_MFMA"] * 32768 / us / 1e6 if us else None}
+
+
+def mfma_md(res: Dict, kernel: str, cmd: str) -> str:
+    md = ["# MFMA utilisation — the prefill's expert FFN (rocprofv3 --pmc)", "",
+          "Workload: `bench.py` prefill, T=2048 tokens, top-8 of 128 experts with Zipf(s=1.1) routing (seed 0), "
+          "gate/up [768, 2048] and down [2048, 768] 4-bit experts, both GEMMs in one launch.", "",
+          "Command (from the repository root), then the summary:", "", "```", cmd,
+          f"cd project-obsidian_amd && python -m obsidian_hip.profiles mfma --pmc ../gpurun_out/pmc_mfma/bench_counter_collection.csv --kernel {kernel} --out ../profiles",
+          "```", "",
+          "MfmaUtil = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE per XCD x 1024 SIMDs), rocprofv3's own MfmaUtil "
+          "expression (one v_mfma_f32_32x32x16_bf16 keeps a SIMD's matrix unit busy 32 cycles). VALU busy = 4 x "
+          "SQ_ACTIVE_INST_VALU over the same cycles; both = SQ_VALU_MFMA_COEXEC_CYCLES; neither = 1 - (MFMA + VALU - "
+          "both). The clock is GRBM_GUI_ACTIVE per XCD / duration.", "",
+          "| kernel | dispatches | duration µs | clock GHz | MFMA instructions | MfmaUtil | VALU instr / MFMA | VALU busy "
+          "| both busy | neither busy | algorithmic TFLOP/s | padded-MFMA TFLOP/s |",
+          "|---|---|---|---|---|---|---|---|---|---|---|---|",
+          f"| {kernel} | {res['dispatches']} | {res['us']:.1f} | {res['clock_ghz']:.2f} | {res['mfma_insts']:,.0f} | "
+          f"{100 * res['mfma_util']:.1f}% | {res['valu_per_mfma']:.1f} | {100 * res['valu_busy']:.1f}% | "
+          f"{100 * res['coexec']:.1f}% | {100 * res['neither']:.1f}% | {res['tflops']:.0f} | {res['padded_tflops']:.0f} |", "",
+          "Rows: the kernel's first dispatches, which are the Zipf prefill section of the bench. SQ_INSTS_VALU counts "
+          "the MFMAs too. The padded-MFMA rate counts every issued MFMA (rows padded to 32 per expert tile); the "
+          "algorithmic rate counts 2 x rows x N x K only. Durations are the dispatch timestamps of the counter run, "
+          "whose clock runs below the 2.30 GHz the MFMA-only loop reaches (`achievable` in bench.py's line)."]
+    return "\n".join(md) + "\n"
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(prog="python -m obsidian_hip.profiles")
     sub = ap.add_subparsers(dest="what", required=True)
@@ -201,6 +266,14 @@ def main(argv=None) -> int:
     s.add_argument("--cmd", required=True)
     s.add_argument("--name", default="kernel_stats_bench.md")
     s.add_argument("--out", default="profiles")
+    mm = sub.add_parser("mfma")
+    mm.add_argument("--pmc", required=True)
+    mm.add_argument("--kernel", default="moe_ffn")
+    mm.add_argument("--first", type=int, default=10)
+    mm.add_argument("--cmd", default="rocprofv3 --pmc " + " ".join(MFMA_COUNTERS) + " --kernel-include-regex moe_ffn "
+                    "-d gpurun_out/pmc_mfma -o bench --output-format csv -- python3 bench.py --no-cpu --no-decoder "
+                    "--steps 2 --warmup 1 --prof-reps 2")
+    mm.add_argument("--out", default="profiles")
     args = ap.parse_args(argv)
     os.makedirs(args.out, exist_ok=True)
     if args.what == "traffic":
@@ -210,6 +283,11 @@ def main(argv=None) -> int:
         with open(os.path.join(args.out, "hbm_traffic.md"), "w") as f:
             f.write(traffic_md(res, args.cmd))
         print(json.dumps({k: v.get("traffic_over_algorithmic") for k, v in res.items() if not k.startswith("_")}))
+    elif args.what == "mfma":
+        res = mfma_util(args.pmc, args.kernel, args.first)
+        with open(os.path.join(args.out, "mfma_util_prefill.md"), "w") as f:
+            f.write(mfma_md(res, args.kernel, args.cmd))
+        print(json.dumps({k: (round(v, 4) if isinstance(v, float) else v) for k, v in res.items()}))
     else:
         line = open(args.line).read().strip().splitlines()[-1] if args.line else None
         with open(os.path.join(args.out, args.name), "w") as f:

@@ -37,3 +37,29 @@ def test_digest_follows_the_sources():
     assert a == P.source_digest("grouped_gemm_down")  # one source file holds both
     assert a != P.source_digest("decode_fused") and P.source_digest("nope") is None
     assert all(os.path.exists(os.path.join(P.PKG, f)) for _, fs in P.KERNELS.values() for f in fs)
+
+
+def test_mfma_util_fractions(tmp_path):
+    """Busy fractions per SIMD from the counters: 8 XCDs x 1,000 cycles each,
+    1,024 SIMDs; MFMA busy 40%, VALU busy 50% (SQ_ACTIVE_INST_VALU counts 4
+    cycles), both 15%, so neither 25%."""
+    k = "void (anonymous namespace)::moe_ffn_kernel<2u>(GemmArgs, GemmArgs, FfnSync)"
+    cyc, simds = 1000.0, 1024
+    vals = {"GRBM_GUI_ACTIVE": 8 * cyc, "SQ_VALU_MFMA_BUSY_CYCLES": 0.4 * cyc * simds,
+            "SQ_ACTIVE_INST_VALU": 0.5 * cyc * simds / 4, "SQ_VALU_MFMA_COEXEC_CYCLES": 0.15 * cyc * simds,
+            "SQ_INSTS_MFMA": 0.4 * cyc * simds / 32, "SQ_INSTS_VALU": 3.0 * 0.4 * cyc * simds / 32,
+            "SQ_WAVE_CYCLES": 1.0, "SQ_WAIT_INST_ANY": 1.0}
+    path = tmp_path / "m.csv"
+    with open(path, "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=["Dispatch_Id", "Kernel_Name", "Counter_Name", "Counter_Value",
+                                          "Start_Timestamp", "End_Timestamp"])
+        w.writeheader()
+        for d in (5, 9):
+            for c, v in vals.items():
+                w.writerow({"Dispatch_Id": d, "Kernel_Name": k, "Counter_Name": c, "Counter_Value": v,
+                            "Start_Timestamp": 0, "End_Timestamp": 500})  # 0.5 us: 2 GHz
+    r = P.mfma_util(str(path), "moe_ffn")
+    assert r["dispatches"] == 2 and abs(r["clock_ghz"] - 2.0) < 1e-9
+    assert abs(r["mfma_util"] - 0.4) < 1e-9 and abs(r["valu_busy"] - 0.5) < 1e-9
+    assert abs(r["coexec"] - 0.15) < 1e-9 and abs(r["neither"] - 0.25) < 1e-9 and abs(r["valu_per_mfma"] - 3.0) < 1e-9
+    assert "| moe_ffn | 2 |" in P.mfma_md(r, "moe_ffn", "cmd")
