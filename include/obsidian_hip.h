@@ -435,7 +435,8 @@ int obs_attn_prep_rows(obs_ctx* ctx, uint16_t* q, const uint16_t* k, const uint1
  * positions [0, pos0 + t]; the batch's keys and values must be in the caches
  * (obs_attn_prep_rows first). q bf16 rows of q_ld elements (a multiple of 8;
  * 0 = dense) holding [n_heads, head_dim]; out bf16 [n_tokens, n_heads,
- * head_dim]; head_dim 128, query heads per kv head a divisor of 16. */
+ * head_dim]; head_dim 128, query heads per kv head a divisor of 16; q, out
+ * and both caches 16-byte aligned (OBS_E_ALIGN). */
 int obs_sdpa_prefill(obs_ctx* ctx, const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache_t,
                      uint16_t* out, uint32_t n_heads, uint32_t n_kv, uint32_t head_dim, uint32_t max_len,
                      uint32_t pos0, uint32_t n_tokens, uint32_t q_ld);

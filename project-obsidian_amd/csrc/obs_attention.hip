@@ -545,36 +545,45 @@ __global__ void __launch_bounds__(512) sdpa_combine_kernel(const float* __restri
 // Tokens [0, n_tok) of q (rows of q_ld elements holding nh x 128) sit at
 // positions pos0 + token and attend to cache positions [0, pos0 + token]; the
 // batch's own keys and values are in the caches already (attn_prep over the
-// rows runs first). A workgroup (4 waves) serves one kv head and 8 column groups of 16 MFMA
-// columns, a column being (token, query head) = TPG = 16 / G tokens x the
-// G query heads of the kv head; wave w owns groups 2w and 2w + 1. Per
-// 32-position block the workgroup stages the keys [32][128] and the
-// transposed values [128][32] in LDS once (rows padded against bank
-// conflicts), and every wave runs sdpa_split_kernel's block math on both of
-// its groups from there, so each key/value byte leaves L2 once per 8 TPG
-// tokens instead of once per TPG. The next block's loads are in flight while
-// a block is computed (registers, then the other LDS buffer). A column's
+// rows runs first). A workgroup serves one kv head and 8 column groups of 16
+// MFMA columns, a column being (token, query head) = TPG = 16 / G tokens x
+// the G query heads of the kv head. It has two sets of 4 waves that split the
+// 32-position blocks: set s runs blocks s, s + 2, s + 4, ..., and wave w of
+// each set owns column groups 2w and 2w + 1, so a tile's chain of dependent
+// blocks is half as long (the longest tiles of a prompt set the launch's
+// length). Per block a set stages the keys [32][128] and the transposed
+// values [128][32] in LDS once (rows padded against bank conflicts), and each
+// of its waves runs sdpa_split_kernel's block math on both of its groups from
+// there, so each key/value byte leaves L2 once per 8 TPG tokens instead of
+// once per TPG. The next block's loads are in flight while a block is
+// computed (registers, then the other LDS buffer). At the end the second set
+// hands its (m, l, O) to the first through LDS, which merges them. A column's
 // scores past its token's position are masked; values at or past the
-// workgroup's longest sequence read as zero.
+// workgroup's longest sequence read as zero. Tiles are launched longest first.
 constexpr uint32_t PF_KROW = HD + 8u;  // padded key row (bf16): 272 bytes
 constexpr uint32_t PF_VROW = 32u + 4u; // padded transposed value row (bf16): 72 bytes
 constexpr uint32_t PF_BUF = 32u * PF_KROW + HD * PF_VROW;  // bf16 elements per staged block
 
-__global__ void __launch_bounds__(256, 2) sdpa_prefill_kernel(const uint16_t* __restrict__ q,
-                                                             const uint16_t* __restrict__ k_cache,
-                                                             const uint16_t* __restrict__ v_cache_t,
-                                                             uint16_t* __restrict__ out, uint32_t nh, uint32_t nkv,
-                                                             uint32_t max_len, uint32_t pos0, uint32_t n_tok,
-                                                             uint32_t q_ld, float scale_log2) {
-  __shared__ __attribute__((aligned(16))) uint16_t s_blk[2][PF_BUF];
-  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+constexpr uint32_t PF_THREADS = 512;  // two sets of 4 waves
+
+__global__ void __launch_bounds__(PF_THREADS, 1) sdpa_prefill_kernel(const uint16_t* __restrict__ q,
+                                                                    const uint16_t* __restrict__ k_cache,
+                                                                    const uint16_t* __restrict__ v_cache_t,
+                                                                    uint16_t* __restrict__ out, uint32_t nh,
+                                                                    uint32_t nkv, uint32_t max_len, uint32_t pos0,
+                                                                    uint32_t n_tok, uint32_t q_ld, float scale_log2) {
+  // per set, two staging buffers; after the block loop the second set's
+  // (m, l, O) pass through them to the first
+  __shared__ __attribute__((aligned(16))) uint16_t s_blk[2][2][PF_BUF];
+  const uint32_t tid = threadIdx.x, lane = tid & 63u;
+  const uint32_t set = tid >> 8, stid = tid & 255u, wave = stid >> 6;  // wave within its set
   const uint32_t G = nh / nkv, TPG = 16u / G, TPWG = 8u * TPG;
   const uint32_t n_wg_tok = (n_tok + TPWG - 1u) / TPWG;
-  // tiles in launch order: the longer half of the tiles from the longest down,
-  // then the shorter half from the shortest up, so the two workgroups that
-  // share a CU tend to be a long and a short one
-  const uint32_t kv = blockIdx.x % nkv, r = blockIdx.x / nkv, half = (n_wg_tok + 1u) / 2u;
-  const uint32_t tb = (r < half ? n_wg_tok - 1u - r : r - half) * TPWG;  // first token
+  // tiles in launch order from the longest (last tokens) down: one workgroup
+  // fills a CU, so the dispatcher hands the shorter tiles to the CUs that free
+  // up first
+  const uint32_t kv = blockIdx.x % nkv, r = blockIdx.x / nkv;
+  const uint32_t tb = (n_wg_tok - 1u - r) * TPWG;  // first token
   const uint32_t col = lane & 15u, g = lane >> 4;
   const uint32_t cj = col / G, ci = col % G;
   const uint32_t seq = pos0 + min(tb + TPWG, n_tok);  // the workgroup's longest sequence
@@ -602,14 +611,14 @@ __global__ void __launch_bounds__(256, 2) sdpa_prefill_kernel(const uint16_t* __
     for (uint32_t nt = 0; nt < 8; ++nt) o[cg][nt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
   const uint16_t* kb = k_cache + static_cast<size_t>(kv) * max_len * HD;
   const uint16_t* vb = v_cache_t + static_cast<size_t>(kv) * HD * max_len;
-  // staging: thread t moves 16-byte chunks t and t + 256 of the key block
-  // (row c / 16, column 8 (c % 16)) and of the transposed value block (row
-  // c / 4, column 8 (c % 4))
+  // staging: thread t of a set moves 16-byte chunks t and t + 256 of the key
+  // block (row c / 16, column 8 (c % 16)) and of the transposed value block
+  // (row c / 4, column 8 (c % 4))
   auto load_blk = [&](uint32_t blk, u32x4_t* r) __attribute__((always_inline)) {
     const uint32_t t0 = 32u * blk;
 #pragma unroll
     for (uint32_t h = 0; h < 2; ++h) {
-      const uint32_t c = tid + 256u * h;
+      const uint32_t c = stid + 256u * h;
       r[h] = *reinterpret_cast<const u32x4_t*>(kb + static_cast<size_t>(t0 + c / 16u) * HD + 8u * (c % 16u));
       r[2 + h] = *reinterpret_cast<const u32x4_t*>(vb + static_cast<size_t>(c / 4u) * max_len + t0 + 8u * (c % 4u));
     }
@@ -620,8 +629,8 @@ __global__ void __launch_bounds__(256, 2) sdpa_prefill_kernel(const uint16_t* __
     const bool tail = 32u * blk + 32u > seq;  // uniform
 #pragma unroll
     for (uint32_t h = 0; h < 2; ++h) {
-      const uint32_t c = tid + 256u * h;
-      *reinterpret_cast<u32x4_t*>(&s_blk[buf][(c / 16u) * PF_KROW + 8u * (c % 16u)]) = r[h];
+      const uint32_t c = stid + 256u * h;
+      *reinterpret_cast<u32x4_t*>(&s_blk[set][buf][(c / 16u) * PF_KROW + 8u * (c % 16u)]) = r[h];
       u32x4_t v = r[2 + h];
       if (tail) {
         const uint32_t ta = 32u * blk + 8u * (c % 4u);  // positions ta .. ta + 7, two per word
@@ -630,7 +639,7 @@ __global__ void __launch_bounds__(256, 2) sdpa_prefill_kernel(const uint16_t* __
       }
       // a transposed value row of 32 positions is 4 chunks; rows are 72 bytes, so
       // each chunk is stored as two 8-byte halves (8-byte alignment)
-      uint16_t* vr = &s_blk[buf][32u * PF_KROW + (c / 4u) * PF_VROW + 8u * (c % 4u)];
+      uint16_t* vr = &s_blk[set][buf][32u * PF_KROW + (c / 4u) * PF_VROW + 8u * (c % 4u)];
       *reinterpret_cast<u32x2_t*>(vr) = u32x2_t{v.x, v.y};
       *reinterpret_cast<u32x2_t*>(vr + 4) = u32x2_t{v.z, v.w};
     }
@@ -639,37 +648,79 @@ __global__ void __launch_bounds__(256, 2) sdpa_prefill_kernel(const uint16_t* __
   // maximum moved (the factor is then exactly 1).
   auto run_blk = [&](uint32_t buf, uint32_t blk) __attribute__((always_inline)) {
     const uint32_t t0 = 32u * blk;
-    const uint16_t* sk = s_blk[buf];
-    const uint16_t* sv = s_blk[buf] + 32u * PF_KROW;
+    const uint16_t* sk = s_blk[set][buf];
+    const uint16_t* sv = s_blk[set][buf] + 32u * PF_KROW;
+    // the scores of both column groups: each key fragment is read from LDS
+    // once and feeds both groups' MFMAs (the LDS reads, not the MFMAs, set the
+    // block's time)
+    bf16x8_t kf[2][4];  // all 8 key fragments in flight at once
+#pragma unroll
+    for (uint32_t tt = 0; tt < 2; ++tt)
+#pragma unroll
+      for (uint32_t ks = 0; ks < 4; ++ks)
+        kf[tt][ks] = __builtin_bit_cast(
+            bf16x8_t, *reinterpret_cast<const u32x4_t*>(sk + (16u * tt + col) * PF_KROW + 8u * g + 32u * ks));
+    __builtin_amdgcn_sched_barrier(0);
+    f32x4_t sc[2][2];
+#pragma unroll
+    for (uint32_t tt = 0; tt < 2; ++tt) {
+      f32x4_t acc[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
+#pragma unroll
+      for (uint32_t ks = 0; ks < 4; ++ks)
+#pragma unroll
+        for (uint32_t cg = 0; cg < 2; ++cg) acc[cg] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[tt][ks], qb[cg][ks], acc[cg], 0, 0, 0);
+      sc[0][tt] = acc[0];
+      sc[1][tt] = acc[1];
+    }
+    // the value slices (dim 16 nt + col, the lane's 8 positions), read now so
+    // that their LDS latency passes during the softmax (pinned here: left
+    // alone, each read sank to its MFMAs and waited there)
+    bf16x8_t vf[8];
+#pragma unroll
+    for (uint32_t nt = 0; nt < 8; ++nt) {
+      const uint16_t* vr = sv + (16u * nt + col) * PF_VROW + 4u * g;
+      const u32x2_t v0 = *reinterpret_cast<const u32x2_t*>(vr);
+      const u32x2_t v1 = *reinterpret_cast<const u32x2_t*>(vr + 16);
+      vf[nt] = __builtin_bit_cast(bf16x8_t, u32x4_t{v0.x, v0.y, v1.x, v1.y});
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // the scores as the softmax sees them: a block wholly below every column's
+    // position (all but the last few of a long tile) needs no mask
+    float svl[2][8];
+    if (t0 + 32u <= pos0 + tb + 1u) {  // uniform
+#pragma unroll
+      for (uint32_t cg = 0; cg < 2; ++cg)
+#pragma unroll
+        for (uint32_t tt = 0; tt < 2; ++tt)
+#pragma unroll
+          for (uint32_t i = 0; i < 4; ++i) svl[cg][4 * tt + i] = sc[cg][tt][i];
+    } else {
+#pragma unroll
+      for (uint32_t cg = 0; cg < 2; ++cg)
+#pragma unroll
+        for (uint32_t tt = 0; tt < 2; ++tt)
+#pragma unroll
+          for (uint32_t i = 0; i < 4; ++i) {
+            const uint32_t t = t0 + 16u * tt + 4u * g + i;
+            svl[cg][4 * tt + i] = t < lim[cg] ? sc[cg][tt][i] : -__builtin_huge_valf();
+          }
+    }
+    // both groups' steps side by side (independent chains), one rescale for both
+    bf16x8_t pa[2];
+    float corr[2];
 #pragma unroll
     for (uint32_t cg = 0; cg < 2; ++cg) {
-      f32x4_t sc[2];
+      float bm = svl[cg][0];
 #pragma unroll
-      for (uint32_t tt = 0; tt < 2; ++tt) {
-        f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
-        const uint16_t* kr = sk + (16u * tt + col) * PF_KROW + 8u * g;
-#pragma unroll
-        for (uint32_t ks = 0; ks < 4; ++ks)
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-              __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4_t*>(kr + 32u * ks)), qb[cg][ks], acc, 0, 0, 0);
-        sc[tt] = acc;
-      }
-      float svl[8];
-#pragma unroll
-      for (uint32_t tt = 0; tt < 2; ++tt)
-#pragma unroll
-        for (uint32_t i = 0; i < 4; ++i) {
-          const uint32_t t = t0 + 16u * tt + 4u * g + i;
-          svl[4 * tt + i] = t < lim[cg] ? sc[tt][i] : -__builtin_huge_valf();
-        }
-      float bm = svl[0];
-#pragma unroll
-      for (uint32_t i = 1; i < 8; ++i) bm = fmaxf(bm, svl[i]);
-      bm = fmaxf(bm, shfl_xor_f(bm, 16));
-      bm = fmaxf(bm, shfl_xor_f(bm, 32));
-      // finite: block 0 holds position 0 of every column, so m_run is finite after it
+      for (uint32_t i = 1; i < 8; ++i) bm = fmaxf(bm, svl[cg][i]);
+      bm = fmaxf(bm, lane_xor16_f32(bm, lane));
+      bm = fmaxf(bm, lane_xor32_f32(bm, lane));
+      // -inf while none of the set's blocks so far held a position of the
+      // column (the second set starts at block 1): its p and corr are then
+      // taken against 0, so they are 0 and l and O stay 0 (not NaN)
       const float m_new = fmaxf(m_run[cg], bm * scale_log2);
-      const float corr = __builtin_amdgcn_exp2f(m_run[cg] - m_new);
+      const float m_use = m_new == -__builtin_huge_valf() ? 0.0f : m_new;
+      corr[cg] = __builtin_amdgcn_exp2f(m_run[cg] - m_use);
       // p = 2^(s * scale - m), the scale folded into one fma (the maximum is taken
       // over the unscaled scores: scaling by a positive factor keeps their
       // order), rounded to bf16 (v_cvt_pk_bf16_f32, round to nearest even); the
@@ -680,67 +731,104 @@ __global__ void __launch_bounds__(256, 2) sdpa_prefill_kernel(const uint16_t* __
       float psum = 0.0f;
 #pragma unroll
       for (uint32_t i = 0; i < 4; ++i) {
-        pk[i] = pack_bf16_pair_rne(__builtin_amdgcn_exp2f(__builtin_fmaf(svl[2 * i], scale_log2, -m_new)),
-                                   __builtin_amdgcn_exp2f(__builtin_fmaf(svl[2 * i + 1], scale_log2, -m_new)));
+        pk[i] = pack_bf16_pair_rne(__builtin_amdgcn_exp2f(__builtin_fmaf(svl[cg][2 * i], scale_log2, -m_use)),
+                                   __builtin_amdgcn_exp2f(__builtin_fmaf(svl[cg][2 * i + 1], scale_log2, -m_use)));
         psum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_v, pk[i]), ones2, psum, false);
       }
-      l_run[cg] = l_run[cg] * corr + psum;
+      l_run[cg] = l_run[cg] * corr[cg] + psum;
       m_run[cg] = m_new;
-      if (__any(corr != 1.0f)) {  // wave-uniform
-        float oc[4];
+      pa[cg] = __builtin_bit_cast(bf16x8_t, u32x4_t{pk[0], pk[1], pk[2], pk[3]});
+    }
+    if (__any(corr[0] != 1.0f || corr[1] != 1.0f)) {  // wave-uniform; a lane's O entries are all of its own column
 #pragma unroll
-        for (uint32_t i = 0; i < 4; ++i) oc[i] = __shfl(corr, static_cast<int>(4u * g + i), 64);
+      for (uint32_t cg = 0; cg < 2; ++cg)
 #pragma unroll
         for (uint32_t nt = 0; nt < 8; ++nt)
 #pragma unroll
-          for (uint32_t i = 0; i < 4; ++i) o[cg][nt][i] *= oc[i];
-      }
-      const bf16x8_t pa = __builtin_bit_cast(bf16x8_t, u32x4_t{pk[0], pk[1], pk[2], pk[3]});
-#pragma unroll
-      for (uint32_t nt = 0; nt < 8; ++nt) {
-        const uint16_t* vr = sv + (16u * nt + col) * PF_VROW + 4u * g;
-        const u32x2_t v0 = *reinterpret_cast<const u32x2_t*>(vr);
-        const u32x2_t v1 = *reinterpret_cast<const u32x2_t*>(vr + 16);
-        const bf16x8_t vbf = __builtin_bit_cast(bf16x8_t, u32x4_t{v0.x, v0.y, v1.x, v1.y});
-        o[cg][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, vbf, o[cg][nt], 0, 0, 0);
-      }
+          for (uint32_t i = 0; i < 4; ++i) o[cg][nt][i] *= corr[cg];
     }
+    // O^T += V^T P of both groups: the value slice is the A operand and the
+    // lane's own probabilities the B operand, so the lane ends with
+    // O[column col][dims 16 nt + 4 g .. + 3] and every factor it applies
+    // (correction, merge, 1 / l) is its own column's: no lane exchanges
+#pragma unroll
+    for (uint32_t nt = 0; nt < 8; ++nt)
+#pragma unroll
+      for (uint32_t cg = 0; cg < 2; ++cg) o[cg][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[nt], pa[cg], o[cg][nt], 0, 0, 0);
   };
-  // two register stages in turn (no copies between them): block b + 2's loads
-  // are issued while block b is computed from LDS and block b + 1, loaded an
-  // iteration earlier, goes from registers to the other LDS buffer. Past the
-  // end the last block is loaded again (unused).
+  // Iteration i computes block 2 i + set (none past the end: the second set's
+  // last iteration when nblk is odd), with two register stages in turn (no
+  // copies between them): the set's block two iterations ahead is loaded while
+  // the current one is computed from LDS and the next one, loaded an iteration
+  // earlier, goes from registers to the other LDS buffer. Past the end the
+  // last block is loaded again (unused). Both sets run the same iterations, so
+  // all 8 waves meet every barrier.
+  const uint32_t nit = (nblk + 1u) / 2u;
+  auto blk_of = [&](uint32_t i) __attribute__((always_inline)) { return min(2u * i + set, nblk - 1u); };
   u32x4_t sa[4], sb[4];
-  load_blk(0u, sa);
-  load_blk(min(1u, nblk - 1u), sb);
-  store_blk(0u, sa, 0u);
+  load_blk(blk_of(0u), sa);
+  load_blk(blk_of(1u), sb);
+  store_blk(0u, sa, blk_of(0u));
   __syncthreads();
-  for (uint32_t blk = 0;;) {
-    load_blk(min(blk + 2u, nblk - 1u), sa);
-    run_blk(0u, blk);
-    store_blk(1u, sb, min(blk + 1u, nblk - 1u));
+  for (uint32_t i = 0;;) {
+    load_blk(blk_of(i + 2u), sa);
+    if (2u * i + set < nblk) run_blk(0u, 2u * i + set);  // uniform per set
+    store_blk(1u, sb, blk_of(i + 1u));
     __syncthreads();
-    if (++blk >= nblk) break;
-    load_blk(min(blk + 2u, nblk - 1u), sb);
-    run_blk(1u, blk);
-    store_blk(0u, sa, min(blk + 1u, nblk - 1u));
+    if (++i >= nit) break;
+    load_blk(blk_of(i + 2u), sb);
+    if (2u * i + set < nblk) run_blk(1u, 2u * i + set);
+    store_blk(0u, sa, blk_of(i + 1u));
     __syncthreads();
-    if (++blk >= nblk) break;
+    if (++i >= nit) break;
   }
-  // normalise: lane holds O[column 4 g + i][dim 16 nt + col] of each group
+  // The second set's (m, l, O) go to the first through the staging buffers,
+  // free after the last barrier: value k of thread stid at s_mo[k][stid]
+  // (m and l of both groups, then the 64 O values).
+  float* const s_mo = reinterpret_cast<float*>(&s_blk[0][0][0]);
+  static_assert((4u + 64u) * 256u * sizeof(float) <= sizeof(s_blk), "the merge fits the staging buffers");
+  if (set == 1u) {
+#pragma unroll
+    for (uint32_t cg = 0; cg < 2; ++cg) {
+      s_mo[cg * 256u + stid] = m_run[cg];
+      s_mo[(2u + cg) * 256u + stid] = l_run[cg];
+#pragma unroll
+      for (uint32_t nt = 0; nt < 8; ++nt)
+#pragma unroll
+        for (uint32_t i = 0; i < 4; ++i) s_mo[(4u + 32u * cg + 4u * nt + i) * 256u + stid] = o[cg][nt][i];
+    }
+  }
+  __syncthreads();
+  if (set == 1u) return;
+  // merge: m = max of the two; each side's l and O scaled by 2^(its m - m)
+  // (the second set's factor is 0 where it saw no position of the column)
+#pragma unroll
+  for (uint32_t cg = 0; cg < 2; ++cg) {
+    const float m1 = s_mo[cg * 256u + stid], l1 = s_mo[(2u + cg) * 256u + stid];
+    const float m = fmaxf(m_run[cg], m1);  // finite: block 0 holds position 0 of every column
+    const float f0 = __builtin_amdgcn_exp2f(m_run[cg] - m), f1 = __builtin_amdgcn_exp2f(m1 - m);
+    l_run[cg] = __builtin_fmaf(l1, f1, l_run[cg] * f0);
+#pragma unroll
+    for (uint32_t nt = 0; nt < 8; ++nt)
+#pragma unroll
+      for (uint32_t i = 0; i < 4; ++i)
+        o[cg][nt][i] = __builtin_fmaf(s_mo[(4u + 32u * cg + 4u * nt + i) * 256u + stid], f1, o[cg][nt][i] * f0);
+  }
+  // normalise: lane holds O[column col][dims 16 nt + 4 g .. + 3] of each
+  // group; l summed over the column's four lanes
 #pragma unroll
   for (uint32_t cg = 0; cg < 2; ++cg) {
     float l = l_run[cg];
-    l += shfl_xor_f(l, 16);
-    l += shfl_xor_f(l, 32);
+    l += lane_xor16_f32(l, lane);
+    l += lane_xor32_f32(l, lane);
+    const float inv = 1.0f / l;
+    const uint32_t t = tb + (2u * wave + cg) * TPG + cj;
+    if (t < n_tok) {
+      uint16_t* orow = out + (static_cast<size_t>(t) * nh + kv * G + ci) * HD + 4u * g;
 #pragma unroll
-    for (uint32_t i = 0; i < 4; ++i) {
-      const float inv = 1.0f / __shfl(l, static_cast<int>(4u * g + i), 64);
-      const uint32_t c = 4u * g + i, t = tb + (2u * wave + cg) * TPG + c / G, hh = c % G;
-      if (t < n_tok) {
-        uint16_t* orow = out + (static_cast<size_t>(t) * nh + kv * G + hh) * HD;
-#pragma unroll
-        for (uint32_t nt = 0; nt < 8; ++nt) orow[16u * nt + col] = f32_to_bf16(o[cg][nt][i] * inv);
+      for (uint32_t nt = 0; nt < 8; ++nt) {
+        *reinterpret_cast<u32x2_t*>(orow + 16u * nt) =
+            u32x2_t{pack_bf16x2(o[cg][nt][0] * inv, o[cg][nt][1] * inv), pack_bf16x2(o[cg][nt][2] * inv, o[cg][nt][3] * inv)};
       }
     }
   }
@@ -1054,14 +1142,14 @@ int obs_sdpa_prefill(obs_ctx* ctx, const uint16_t* q, const uint16_t* k_cache, c
   if (q_ld < n_heads * head_dim || q_ld % 8u != 0)
     return obs::set_error(ctx, OBS_E_SHAPE, "obs_sdpa_prefill: q row stride %u must be a multiple of 8 holding a row",
                           q_ld);
-  if (!obs::aligned(q, 16) || !obs::aligned(k_cache, 16) || !obs::aligned(v_cache_t, 16))
-    return obs::set_error(ctx, OBS_E_ALIGN, "obs_sdpa_prefill: q and the caches must be 16-byte aligned");
+  if (!obs::aligned(q, 16) || !obs::aligned(k_cache, 16) || !obs::aligned(v_cache_t, 16) || !obs::aligned(out, 16))
+    return obs::set_error(ctx, OBS_E_ALIGN, "obs_sdpa_prefill: q, the caches and out must be 16-byte aligned");
   if (n_tokens == 0) return OBS_OK;
   const uint32_t tpwg = 8u * (16u / (n_heads / n_kv));  // tokens per workgroup
   const uint64_t wgs = static_cast<uint64_t>(n_kv) * ((n_tokens + tpwg - 1u) / tpwg);
   if (wgs > 0x7fffffffull) return obs::set_error(ctx, OBS_E_SHAPE, "obs_sdpa_prefill: too many tokens");
   const float scale_log2 = 1.4426950408889634f / __builtin_sqrtf(static_cast<float>(HD));
-  OBS_LAUNCH(ctx, "sdpa_prefill", sdpa_prefill_kernel<<<static_cast<uint32_t>(wgs), 256, 0, ctx->stream>>>(
+  OBS_LAUNCH(ctx, "sdpa_prefill", sdpa_prefill_kernel<<<static_cast<uint32_t>(wgs), PF_THREADS, 0, ctx->stream>>>(
                                       q, k_cache, v_cache_t, out, n_heads, n_kv, max_len, pos0, n_tokens, q_ld,
                                       scale_log2));
   return OBS_OK;
