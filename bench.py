@@ -146,8 +146,10 @@ def bench_decode(torch, oh, exe, args):
 def bench_router(torch, oh, exe, reps=200):
     """The router on the GPU: 8-bit gate logits + softmax/top-8 for T = 1
     and T = 512 tokens (gate_gpu + MoeRouter.route_dispatch, forward.rs:386-397,
-    router.rs:62-83). Each T's two launches are captured `reps` times in one
-    graph; the time per call is the replay time over reps."""
+    router.rs:62-83), as one launch (obs_route: T{T}_us) and as the two calls
+    (obs_q8_gate_logits + obs_route_topk: T{T}_us_two_launches). Each form is
+    captured `reps` times in one graph; the time per call is the replay time
+    over reps."""
     t = gpu_table(torch, 1, 555)[0]
     w8, s8, b8 = (t[k].data_ptr() for k in ("router_w", "router_s", "router_b"))
     gen = torch.Generator(device="cuda")
@@ -160,23 +162,28 @@ def bench_router(torch, oh, exe, reps=200):
         w = torch.empty((T, K), dtype=torch.float32, device="cuda")
         torch.cuda.synchronize()
 
-        def call():
+        def two_calls():
             exe.q8_gate_logits(w8, s8, b8, x.data_ptr(), lg.data_ptr(), T, H, E)
             exe.route_topk(lg.data_ptr(), ids.data_ptr(), w.data_ptr(), T, E, K, True)
 
-        call()
-        exe.sync()
-        exe.capture_begin()
-        for _ in range(reps):
+        def one_launch():
+            exe.route(w8, s8, b8, x.data_ptr(), lg.data_ptr(), ids.data_ptr(), w.data_ptr(), T, H, E, K, True)
+
+        for name, call in ((f"T{T}_us_two_launches", two_calls), (f"T{T}_us", one_launch)):
             call()
-        g = exe.capture_end()
-        exe.graph_launch(g)
-        exe.sync()
-        exe.timer_start()
-        exe.graph_launch(g)
-        ms = exe.timer_stop()
-        exe.graph_destroy(g)
-        out[f"T{T}_us"] = round(1000.0 * ms / reps, 2)
+            exe.sync()
+            exe.capture_begin()
+            for _ in range(reps):
+                call()
+            g = exe.capture_end()
+            exe.graph_launch(g)
+            exe.sync()
+            exe.timer_start()
+            exe.graph_launch(g)
+            ms = exe.timer_stop()
+            exe.graph_destroy(g)
+            out[name] = round(1000.0 * ms / reps, 2)
+        exe.device_status()
     del t
     return out
 
@@ -622,8 +629,8 @@ def main():
         "decode_frac_of_hbm_peak": round(dec["gbs"] / HBM_PEAK_GBS, 4),
         "decode_kernels": {n: round(v["avg_us"], 3) for n, v in dec["kernels"].items()},
         "roofline": dec["roofline"],
-        "router": dict(rtr, workload="8-bit gate [128 x 2048] + softmax/top-8 (f16 logits), 2 launches per call, "
-                                      "graph of 200 calls"),
+        "router": dict(rtr, workload="8-bit gate [128 x 2048] + softmax/top-8 (f16 logits): one launch per call "
+                                      "(T*_us) and the two-launch form (T*_us_two_launches), graph of 200 calls"),
         "prefill": None if pre is None else {
             "T": pre["T"], "ms": round(pre["ms"], 4), "tflops": round(pre["tflops"], 1),
             "gemm_us": round(pre["gemm_us"], 2),

@@ -189,6 +189,18 @@ enum { OBS_ROUTE_REF = 0, OBS_ROUTE_F32 = 1 };
 int obs_route_topk(obs_ctx* ctx, const float* logits, int32_t* ids, float* weights,
                    uint32_t T, uint32_t n_exp, uint32_t k, int norm_topk, int rule);
 
+/* obs_q8_gate_logits followed by obs_route_topk: the router step of
+ * MoeRouter::route_dispatch as forward.rs:386-397 and router.rs:62-83 run it
+ * (gate_gpu, then the routing kernel). logits, ids and weights are written as
+ * by the two calls, bit for bit. Up to 8 tokens it is one launch whose
+ * workgroups share one XCD (on a device where obs_create's dispatch probe
+ * found workgroup b on XCD b % 8), using a context counter that each launch
+ * leaves at zero, so such calls on one context must not overlap (issue them
+ * on one stream); otherwise the two launches. */
+int obs_route(obs_ctx* ctx, const uint32_t* w8, const uint16_t* scales, const uint16_t* biases,
+              const uint16_t* x, float* logits, int32_t* ids, float* weights, uint32_t T,
+              uint32_t in, uint32_t n_exp, uint32_t group, uint32_t k, int norm_topk, int rule);
+
 /* ------------------------------------------------------------------ */
 /* Elementwise — ops.metal ew_swiglu / ew_scaled_add (forward.rs:370-380) */
 /* ------------------------------------------------------------------ */

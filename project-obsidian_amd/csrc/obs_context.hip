@@ -225,6 +225,14 @@ int obs_create(int device, obs_ctx** out) {
       rc = OBS_E_HIP;
     }
   }
+  if (rc == OBS_OK) {
+    if (hipMalloc(&ctx->route_cnt, obs::ROUTE_CNT_WORDS * sizeof(uint32_t)) != hipSuccess ||
+        hipMemsetAsync(ctx->route_cnt, 0, obs::ROUTE_CNT_WORDS * sizeof(uint32_t), ctx->stream) != hipSuccess ||
+        hipStreamSynchronize(ctx->stream) != hipSuccess) {
+      serr = "router counters: hipMalloc/hipMemset failed";
+      rc = OBS_E_HIP;
+    }
+  }
   if (rc == OBS_OK) rc = obs::probe_dispatch(ctx);
   if (rc == OBS_OK) rc = obs::prefill_init(ctx);
   if (rc != OBS_OK) {
@@ -245,6 +253,7 @@ void obs_destroy(obs_ctx* ctx) {
   if (ctx->fused_ws) (void)hipFree(ctx->fused_ws);
   if (ctx->attn_ws) (void)hipFree(ctx->attn_ws);
   if (ctx->status_dev) (void)hipFree(ctx->status_dev);
+  if (ctx->route_cnt) (void)hipFree(ctx->route_cnt);
   for (const auto& r : ctx->rope_tables) (void)hipFree(r.table);
   for (void* p : ctx->retired) (void)hipFree(p);
   if (ctx->ev_start) (void)hipEventDestroy(ctx->ev_start);

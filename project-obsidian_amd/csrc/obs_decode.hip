@@ -17,10 +17,9 @@
 
 namespace obs {
 int check_router_shape(obs_ctx* ctx, const char* who, uint32_t in, uint32_t n_exp, uint32_t group);
-int launch_gate_logits(obs_ctx* ctx, const uint32_t* w8, const uint16_t* s, const uint16_t* b,
-                       const uint16_t* x, float* logits, uint32_t T, uint32_t in, uint32_t n_exp, uint32_t group);
-int launch_route_topk(obs_ctx* ctx, const float* logits, int32_t* ids, float* w, uint32_t T,
-                      uint32_t n_exp, uint32_t k, int norm_topk, int rule);
+int launch_route(obs_ctx* ctx, const uint32_t* w8, const uint16_t* s, const uint16_t* b, const uint16_t* x,
+                 float* logits, int32_t* ids, float* w, uint32_t T, uint32_t in, uint32_t n_exp, uint32_t group,
+                 uint32_t k, int norm_topk, int rule);
 }  // namespace obs
 
 namespace {
@@ -318,9 +317,8 @@ int decode_multi(obs_ctx* ctx, const obs_moe_config* cfg, const obs_moe_layer* l
     if (rc) return rc;
     x = xn;
   }
-  rc = launch_gate_logits(ctx, layer->router_w, layer->router_s, layer->router_b, x, logits, 1, H, E, cfg->group);
-  if (rc) return rc;
-  rc = launch_route_topk(ctx, logits, ids, w, 1, E, k, cfg->norm_topk, cfg->route_rule);
+  rc = launch_route(ctx, layer->router_w, layer->router_s, layer->router_b, x, logits, ids, w, 1, H, E, cfg->group, k,
+                    cfg->norm_topk, cfg->route_rule);
   if (rc) return rc;
   return launch_decode_experts(ctx, cfg, layer, x, residual, y, ids, w, h);
 }

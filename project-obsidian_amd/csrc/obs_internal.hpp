@@ -58,6 +58,9 @@ struct obs_ctx {
   // Context-owned device status words (obs::CTX_ST_*), zeroed by obs_create,
   // read and cleared by obs_device_status: the one-launch prefill FFN's flags.
   uint32_t* status_dev = nullptr;
+  // The one-launch router's counter (obs_route), zeroed by obs_create; the
+  // workgroup that routes sets it back to 0.
+  uint32_t* route_cnt = nullptr;
   // Dispatch facts the one-launch kernels build on, probed by obs_create
   // (obs::probe_dispatch): the workgroups b of one b % 8 share an XCD (8
   // groups, 8 XCDs), and an XCD starts its workgroups in index order.
@@ -97,6 +100,9 @@ enum : uint32_t {
   CTX_ST_FFN_SCHED = 1,  // a one-launch FFN work table did not fit its launch
   CTX_ST_WORDS = 64
 };
+// Words of the one-launch router's counter block in the context (word 0 is
+// the count of its working workgroups).
+constexpr uint32_t ROUTE_CNT_WORDS = 64;
 
 // Which one-launch paths a device may take (OBS_PATH_* bits of
 // obs_dispatch_gate): the fused decode and fused attention need all 256 of

@@ -34,10 +34,9 @@
 namespace obs {
 int check_moe_config(obs_ctx* ctx, const char* who, const obs_moe_config* cfg);
 int check_moe_layer(obs_ctx* ctx, const char* who, const obs_moe_layer* L);
-int launch_gate_logits(obs_ctx* ctx, const uint32_t* w8, const uint16_t* s, const uint16_t* b,
-                       const uint16_t* x, float* logits, uint32_t T, uint32_t in, uint32_t n_exp, uint32_t group);
-int launch_route_topk(obs_ctx* ctx, const float* logits, int32_t* ids, float* w, uint32_t T,
-                      uint32_t n_exp, uint32_t k, int norm_topk, int rule);
+int launch_route(obs_ctx* ctx, const uint32_t* w8, const uint16_t* s, const uint16_t* b, const uint16_t* x,
+                 float* logits, int32_t* ids, float* w, uint32_t T, uint32_t in, uint32_t n_exp, uint32_t group,
+                 uint32_t k, int norm_topk, int rule);
 }  // namespace obs
 
 namespace {
@@ -1098,10 +1097,9 @@ int obs_moe_prefill(obs_ctx* ctx, const obs_moe_config* cfg, const obs_moe_layer
   int32_t* d_ids = reinterpret_cast<int32_t*>(base + L.ids);
   float* d_w = reinterpret_cast<float*>(base + L.w);
   if (!ids) {
-    rc = obs::launch_gate_logits(ctx, layer->router_w, layer->router_s, layer->router_b, Xin,
-                                 reinterpret_cast<float*>(base + L.logits), T, H, E, cfg->group);
-    if (rc) return rc;
-    rc = obs::launch_route_topk(ctx, reinterpret_cast<float*>(base + L.logits), d_ids, d_w, T, E, k, cfg->norm_topk, cfg->route_rule);
+    rc = obs::launch_route(ctx, layer->router_w, layer->router_s, layer->router_b, Xin,
+                           reinterpret_cast<float*>(base + L.logits), d_ids, d_w, T, H, E, cfg->group, k,
+                           cfg->norm_topk, cfg->route_rule);
     if (rc) return rc;
     ids = d_ids;
     weights = d_w;

@@ -52,7 +52,7 @@ EXPORTS = (
     "obs_create", "obs_destroy", "obs_last_error", "obs_create_error", "obs_set_stream",
     "obs_get_stream", "obs_alloc", "obs_free", "obs_upload", "obs_download", "obs_memset",
     "obs_sync", "obs_timer_start", "obs_timer_stop", "obs_dequant", "obs_q4_matvec",
-    "obs_q4_matmul", "obs_q8_gate_logits", "obs_route_topk", "obs_swiglu", "obs_scaled_add", "obs_rmsnorm",
+    "obs_q4_matmul", "obs_q8_gate_logits", "obs_route_topk", "obs_route", "obs_swiglu", "obs_scaled_add", "obs_rmsnorm",
     "obs_moe_decode", "obs_moe_decode_static", "obs_moe_prefill_workspace", "obs_moe_prefill", "obs_capture_begin",
     "obs_capture_end", "obs_graph_launch", "obs_graph_destroy", "obs_set_decode_path",
     "obs_device_status", "obs_stream_hold", "obs_profile_enable",
@@ -142,6 +142,7 @@ def lib() -> C.CDLL:
         "obs_q4_matmul": (i32, [vp, vp, vp, vp, vp, vp, u32, u32, u32, u32]),
         "obs_q8_gate_logits": (i32, [vp, vp, vp, vp, vp, vp, u32, u32, u32, u32]),
         "obs_route_topk": (i32, [vp, vp, vp, vp, u32, u32, u32, C.c_int, C.c_int]),
+        "obs_route": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, u32, u32, u32, u32, u32, C.c_int, C.c_int]),
         "obs_swiglu": (i32, [vp, vp, vp, vp, u32]),
         "obs_scaled_add": (i32, [vp, vp, vp, f32, u32]),
         "obs_rmsnorm": (i32, [vp, vp, vp, vp, u32, u32, f32]),
@@ -410,6 +411,13 @@ class ObsidianExecutor:
         rule = ROUTE_REF if rule is None else rule
         self._check(lib().obs_route_topk(self.ctx, _ptr(logits), _ptr(ids), _ptr(weights), T, n_exp, k,
                                          int(bool(norm_topk)), int(rule)))
+
+    def route(self, w8, scales, biases, x, logits, ids, weights, T: int, in_dim: int, n_exp: int, k: int,
+              norm_topk: bool, group: int = 64, rule: int = None) -> None:
+        """q8_gate_logits + route_topk in one launch (obs_route); logits is written as well."""
+        rule = ROUTE_REF if rule is None else rule
+        self._check(lib().obs_route(self.ctx, _ptr(w8), _ptr(scales), _ptr(biases), _ptr(x), _ptr(logits), _ptr(ids),
+                                    _ptr(weights), T, in_dim, n_exp, group, k, int(bool(norm_topk)), int(rule)))
 
     def swiglu_raw(self, g, u, h, n: int) -> None:
         self._check(lib().obs_swiglu(self.ctx, _ptr(g), _ptr(u), _ptr(h), n))

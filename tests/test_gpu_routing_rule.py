@@ -149,3 +149,44 @@ def test_prefill_computed_routing_forced_ties(exe, tie_model):
     ref = O.moe_prefill(L, X[sel], ri[sel], rw[sel], O.MODE_F64)
     rel = float(np.linalg.norm(y[sel] - ref) / np.linalg.norm(ref))
     assert rel < 1e-2, rel
+
+
+@pytest.mark.parametrize("T", [1, 7, 64, 65, 512, 1100, 3000])
+def test_one_launch_router_matches_the_two_calls(exe, T):
+    """obs_route (up to 8 tokens one launch whose last workgroup routes, else
+    the two launches) against obs_q8_gate_logits + obs_route_topk and the
+    oracle: logits, ids and weights bit-exact, under both rules, on a router
+    with forced f16 ties; two calls in a row (the launch leaves its counter at
+    zero for the next)."""
+    t = _tie_layer(78, 1.0)
+    w8, s8, b8 = (exe.upload(t[k]) for k in ("router_w", "router_s", "router_b"))
+    x = _inputs(92 + T, T)
+    dx = exe.upload(x)
+    lg2 = exe.alloc((T, E), np.float32)
+    exe.q8_gate_logits(w8, s8, b8, dx, lg2, T, H, E)
+    ref_lg = lg2.download()
+    sel = list(range(0, T, max(1, T // 40)))
+    xf = synth.bf16_bits_to_f32(x)
+    want_lg = np.stack([O.qmatvec("lanes", 8, t["router_w"], t["router_s"], t["router_b"], xf[i], H, E) for i in sel])
+    assert np.array_equal(ref_lg[sel].view(np.uint32), want_lg.view(np.uint32))
+    for rule in (O.ROUTE_REF, O.ROUTE_F32):
+        ids2, w2 = exe.alloc((T, K), np.int32), exe.alloc((T, K), np.float32)
+        exe.route_topk(lg2, ids2, w2, T, E, K, True, rule=rule)
+        ri, rw = O.route_topk(ref_lg, K, True, O.SUM_WAVE, rule=rule)
+        assert np.array_equal(ids2.download(), ri)
+        for rep in range(2):
+            lg1 = exe.alloc((T, E), np.float32)
+            ids1, w1 = exe.alloc((T, K), np.int32), exe.alloc((T, K), np.float32)
+            exe.route(w8, s8, b8, dx, lg1, ids1, w1, T, H, E, K, True, rule=rule)
+            exe.device_status()
+            assert np.array_equal(lg1.download().view(np.uint32), ref_lg.view(np.uint32)), (rule, rep)
+            assert np.array_equal(ids1.download(), ri), (rule, rep)
+            assert np.array_equal(w1.download().view(np.uint32), rw.view(np.uint32)), (rule, rep)
+
+
+def test_one_launch_router_rejects_bad_arguments(exe):
+    x = exe.alloc(64, np.uint16)
+    with pytest.raises(oh.ObsError, match="k must be"):
+        exe.route(x, x, x, x, x, x, x, 1, H, E, 0, True)
+    with pytest.raises(oh.ObsError, match="OBS_E_SHAPE"):
+        exe.route(x, x, x, x, x, x, x, 1, 1000, E, K, True)
