@@ -121,7 +121,7 @@ int obs_profile_clear(obs_ctx* ctx);
  * the fused decode's non-temporal 16-byte loads (8 workgroups per CU); sink is
  * a 4-byte device word the kernel never writes in practice. obs_measure_mfma:
  * v_mfma_f32_32x32x16_bf16 only, 4 independent chains per wave, 8 waves per
- * CU, `iters` steps; *flops (host) receives the flop count of the launch and
+ * CU, `iters` steps (1 to 2^24); *flops (host) receives the flop count of the launch and
  * clocks[0..1] (device) the core clock cycles and 100 MHz constant-clock
  * ticks of one wave's loop, whose ratio is the clock the MFMAs ran at. */
 int obs_measure_read(obs_ctx* ctx, const void* src, size_t bytes, uint32_t* sink);

@@ -89,7 +89,9 @@ int obs_measure_read(obs_ctx* ctx, const void* src, size_t bytes, uint32_t* sink
 int obs_measure_mfma(obs_ctx* ctx, uint32_t iters, float* sink, uint64_t* clocks, double* flops) {
   if (!ctx) return OBS_E_INVALID;
   if (!sink || !clocks) return obs::set_error(ctx, OBS_E_INVALID, "obs_measure_mfma: null pointer");
-  if (iters == 0) return obs::set_error(ctx, OBS_E_INVALID, "obs_measure_mfma: iters must be positive");
+  // at most 2^24 steps: about 0.5 s at 2.4 GHz, so a wrong count cannot hold the device for minutes
+  if (iters == 0 || iters > (1u << 24))
+    return obs::set_error(ctx, OBS_E_INVALID, "obs_measure_mfma: iters must be in [1, 2^24] (got %u)", iters);
   const uint32_t grid = static_cast<uint32_t>(ctx->num_cus) * 2u;
   OBS_LAUNCH(ctx, "peak_mfma", peak_mfma_kernel<<<grid, 256, 0, ctx->stream>>>(iters, sink, clocks));
   if (flops) *flops = static_cast<double>(grid) * 4.0 * MFMA_CHAINS * iters * (2.0 * 32 * 32 * 16);

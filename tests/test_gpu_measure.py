@@ -55,3 +55,5 @@ def test_measure_rejects_bad_arguments(exe):
         exe.measure_read(buf, 0, sink)
     with pytest.raises(oh.ObsError):
         exe.measure_mfma(0, sink, sink)
+    with pytest.raises(oh.ObsError):
+        exe.measure_mfma((1 << 24) + 1, sink, sink)
