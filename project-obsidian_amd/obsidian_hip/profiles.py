@@ -289,7 +289,9 @@ def main(argv=None) -> int:
             f.write(mfma_md(res, args.kernel, args.cmd))
         print(json.dumps({k: (round(v, 4) if isinstance(v, float) else v) for k, v in res.items()}))
     else:
-        line = open(args.line).read().strip().splitlines()[-1] if args.line else None
+        # the bench's JSON line: the last line that is one (rocprofv3 logs after it)
+        objs = [ln for ln in open(args.line).read().splitlines() if ln.lstrip().startswith("{")] if args.line else []
+        line = objs[-1] if objs else None
         with open(os.path.join(args.out, args.name), "w") as f:
             f.write(stats_md(args.stats, line, args.cmd))
     return 0
