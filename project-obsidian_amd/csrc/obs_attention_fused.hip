@@ -38,11 +38,12 @@
 // Load order. A wave's loads complete in issue order, and a CU accepts them
 // only as fast as memory drains them, so each batch sits where it delays
 // nothing more urgent: the q/k/v rows at the start (they have the bandwidth
-// to themselves), the first block's keys right after the q/k/v poll (issued
-// before it, the poll waited for the block's data; issued at the start, the
-// rows shared their bandwidth) and its values after the RoPE, and the o rows
-// after the attention blocks, where their latency overlaps the two exchanges
-// that precede their use.
+// to themselves), the first block's keys right behind them (they arrive while
+// the rows are computed and exchanged, before the data of the poll that waits
+// behind them; issued ahead of the rows, they shared the rows' bandwidth), its
+// values right after the poll (issued before it, the poll waited for them),
+// and the o rows after the attention blocks, where their latency overlaps the
+// two exchanges that precede their use.
 // Every wait is bounded (100 ms of the constant clock); a time-out sets the
 // workspace's error flag, reported and cleared by obs_device_status.
 #include "obs_internal.hpp"
@@ -194,8 +195,8 @@ attn_fused_kernel(AttnArgs a) {
   const uint32_t col = lane & 15u, gq = lane >> 4;
   const uint16_t* kb = a.k_cache + static_cast<size_t>(kv) * max_len * AHD;
   const uint16_t* vb = a.v_cache_t + static_cast<size_t>(kv) * AHD * max_len;
-  // wave w runs blocks b0 + w, b0 + w + 4, ...; its first block's loads go out
-  // after the q/k/v poll. Row r of score tile tt (the MFMA's A rows) is
+  // wave w runs blocks b0 + w, b0 + w + 4, ...; its first block's keys go out
+  // behind the q/k/v rows, its values after the poll. Row r of score tile tt (the MFMA's A rows) is
   // position t0 + 8 (r / 4) + 4 tt + r % 4 of the 32-position block, so lane
   // (col, gq) ends with the scores of positions t0 + 8 gq .. + 7 and reads
   // their values as one 16-byte run of the transposed value cache.
@@ -249,6 +250,10 @@ attn_fused_kernel(AttnArgs a) {
   // 2 lane + 1) mod 64: (cos, sin, cos, sin); needed after the first exchange
   const f32x4_t csn = *reinterpret_cast<const f32x4_t*>(a.rope + static_cast<size_t>(min(pos, max_len - 1u)) * 128u +
                                                         4u * (lane & 31u));
+  // the keys of the wave's first block (clamped into the sequence when it has
+  // none; unused then), behind the rows: they arrive while the q/k/v rows are
+  // computed and exchanged, before the poll that waits behind them returns
+  load_keys(min(b0 + wave, nblk - 1u));
   __builtin_amdgcn_sched_barrier(0);
   OBS_ATTN_MARK(1);
   // ---- 1. q/k/v rows of rmsnorm(x) (obs_rmsnorm's sequence), rounded to bf16
@@ -339,12 +344,8 @@ attn_fused_kernel(AttnArgs a) {
     for (uint32_t u = 0; u < 3; ++u) s_qkv[tid + 256u * u] = vals[u];
   }
   __syncthreads();
-  // the keys of the wave's first block (clamped into the sequence when it has
-  // none; unused then), now that no poll waits behind them; its values follow
-  // the RoPE: a wave stalls while the memory queue takes its loads, and the
-  // RoPE needs none of them (decoder 724 -> 729 tokens/s; all 16 loads after
-  // the RoPE: 718)
-  load_keys(min(b0 + wave, nblk - 1u));
+  // the first block's values, now that no poll waits behind them
+  load_values(min(b0 + wave, nblk - 1u));
   OBS_ATTN_MARK(3);
   // per-head RMSNorm + NeoX RoPE (attn_prep_kernel's sequence): wave w owns
   // query head w, and wave 0 the key head (head 4) too. Every wave computes the
@@ -384,7 +385,6 @@ attn_fused_kernel(AttnArgs a) {
           pack_bf16_pair_rne(s_qkv[(AQPG + 1) * AHD + 2u * lane], s_qkv[(AQPG + 1) * AHD + 2u * lane + 1u]);
     }
   }
-  load_values(min(b0 + wave, nblk - 1u));
   __syncthreads();
   OBS_ATTN_MARK(4);
   const uint32_t pblk = pos / 32u;
