@@ -271,10 +271,13 @@ __global__ void __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 
   // Each wave counts, for all experts (NQ per lane), the composites that
   // exceed theirs among its quarter of the experts (read back from its own LDS
   // area as broadcasts), and one barrier adds the four partial counts. The
-  // composites (< 2^40) are held as doubles, so one exact fp64 subtraction and
-  // its sign bit compare a pair: no compare writes a lane mask that the next
-  // instruction must wait for (64-bit integer compares into a mask and a
-  // carry-add took 0.65 us for the count, this 0.4 us).
+  // composites are integers below 2^40 held as doubles, so v - ck is exact and
+  // at least 1 when v > ck: the subtraction with the output clamp to [0, 1] is
+  // the compare's 0 or 1, and a second fp64 add counts it. No compare writes a
+  // lane mask that the next instruction must wait for (64-bit integer compares
+  // into a mask and a carry-add: 0.65 us for the count; the sign bit of the
+  // subtraction, shifted and added: 2.5 instructions a compare, 0.08 us per
+  // layer slower than these 2).
   bool ok = true;
   float lg[NQ];
   {
@@ -309,19 +312,21 @@ __global__ void __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");  // the wave's own LDS stores before its reads
   __builtin_amdgcn_wave_barrier();
   {
-    uint32_t c[NQ];
+    double c[NQ][2];  // two sums per expert, so each add chain is half as long
 #pragma unroll
-    for (int q = 0; q < NQ; ++q) c[q] = 0;
+    for (int q = 0; q < NQ; ++q) c[q][0] = c[q][1] = -0.0;  // -0.0 + x is x: the first add folds away
     const double2* cw = reinterpret_cast<const double2*>(s_ck[wave]);
 #pragma unroll
     for (uint32_t i = 0; i < QW / 2; ++i) {
       const double2 v = cw[i];
 #pragma unroll
-      for (int q = 0; q < NQ; ++q)  // ck - v is exact and negative exactly when v > ck
-        c[q] += static_cast<uint32_t>(__double2hiint(ck[q] - v.x) < 0) + static_cast<uint32_t>(__double2hiint(ck[q] - v.y) < 0);
+      for (int q = 0; q < NQ; ++q) {  // min/max with 0 and 1 fold into v_add_f64's clamp
+        c[q][0] += __builtin_fmin(__builtin_fmax(v.x - ck[q], 0.0), 1.0);
+        c[q][1] += __builtin_fmin(__builtin_fmax(v.y - ck[q], 0.0), 1.0);
+      }
     }
 #pragma unroll
-    for (int q = 0; q < NQ; ++q) s_cnt[wave][lane + 64u * q] = c[q];
+    for (int q = 0; q < NQ; ++q) s_cnt[wave][lane + 64u * q] = static_cast<uint32_t>(c[q][0] + c[q][1]);
   }
   __syncthreads();
   // rank of each of the lane's experts; the group's expert has rank g
@@ -467,11 +472,14 @@ __global__ void __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 
   OBS_FUSED_MARK(5);
   // ---- 5/6. h arrives in three 256-column blocks. Block L = h[256L, 256L + 256)
   // holds every workgroup's rows t = 2L and 2L + 1, which it finishes before
-  // its later rows, so the blocks become visible in order. The workgroup polls
-  // one block at a time (one slot per thread), stores it to LDS as f16 in the
+  // its later rows, so the blocks become visible in order. The first poll of
+  // all three blocks is issued at once (one slot per thread and block), so a
+  // workgroup whose blocks are all complete by then, the last one of its group
+  // among them, spends one round trip on them instead of three; a block not yet
+  // complete is polled again on its own. Each block goes to LDS as f16 in the
   // pair order of dot8_q4_off with the sum and the offset sum of every 32
-  // columns (32 consecutive columns sit in one half-wave), and adds the block's
-  // terms to its 64 down rows (of expert e_g, unscaled by w_g) while the later
+  // columns (32 consecutive columns sit in one half-wave), and its terms are
+  // added to the workgroup's 64 down rows (of expert e_g, unscaled by w_g) while the later
   // blocks are still being computed. The terms are added in block order, as a
   // single pass over the row would add them.
   reinterpret_cast<u32x4_t*>(s_sc[wave])[128u + lane] = scq2;  // down scales; chunks 176..191: padding
@@ -479,19 +487,21 @@ __global__ void __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 
   {
     _Float16* hp16 = reinterpret_cast<_Float16*>(s_hp);
     const uint64_t t0 = wall_clock64();
+    uint64_t hq[3];
+#pragma unroll
+    for (uint32_t L = 0; L < 3; ++L) hq[L] = slot_load(h_slots + tid + 256u * L);
 #pragma unroll
     for (uint32_t L = 0; L < 3; ++L) {
-      float hv = 0.0f;
+      uint64_t v = hq[L];
       bool wave_ok = ok;
-      while (wave_ok) {
-        const uint64_t v = slot_load(h_slots + tid + 256u * L);
-        hv = slot_val(v);
-        if (__all(slot_ready(v, epoch))) break;
+      while (wave_ok && !__all(slot_ready(v, epoch))) {
         if (wall_clock64() - t0 > WAIT_TICKS) {
           wave_ok = false;
           if (lane == 0) raise_error(a.ws);
         }
+        v = slot_load(h_slots + tid + 256u * L);
       }
+      const float hv = slot_val(v);
       ok = ok && wave_ok;
       {
         const uint32_t idx = tid + 256u * L, jn = idx & 7u;  // column idx = 8 * word + jn
