@@ -54,6 +54,16 @@ def test_python_binding_covers_exactly_the_header():
     oh.lib()  # every signature binds
 
 
+def test_rust_binding_in_integration_covers_exactly_the_header():
+    """INTEGRATION.md's `extern "C"` block declares every export once, and
+    nothing the header does not."""
+    text = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    block = text.split("```rust", 1)[1].split("```", 1)[0]
+    fns = re.findall(r"\bpub fn (obs_\w+)\s*\(", block)
+    assert len(fns) == len(set(fns)), sorted(n for n in set(fns) if fns.count(n) > 1)
+    assert set(fns) == set(declared_functions())
+
+
 def test_null_context_is_rejected_before_any_device_work():
     L = oh.lib()
     host_only = {"obs_create", "obs_create_error", "obs_destroy", "obs_last_error", "obs_get_stream",
