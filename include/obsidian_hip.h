@@ -420,6 +420,21 @@ int obs_attn_decode(obs_ctx* ctx, const obs_attn_layer* layer, const uint16_t* x
                     uint16_t* v_cache_t, uint32_t max_len, float eps, float theta, const int32_t* state,
                     uint16_t* x1);
 
+/* A whole decode layer, Model::forward_layer (forward.rs:398-443), in one
+ * launch at the Qwen3-30B-A3B shape: obs_attn_decode (x -> x1, the caches
+ * appended at state[0]) and then obs_moe_decode with the layer's
+ * post-attention norm (moe->norm_w, required) and x1 as its input and
+ * residual (x1 -> y, ids_out / w_out as obs_moe_decode writes them), with the
+ * same results bit for bit, without the kernel boundary between the halves.
+ * Needs what both calls need (256 CUs, the dispatch obs_create probed, the
+ * MoE shape of the fused decode); a context-owned exchange area is allocated
+ * on the first call (run one before a graph capture); obs_device_status
+ * reports its bounded waits' time-outs. */
+int obs_layer_decode(obs_ctx* ctx, const obs_attn_layer* attn, const obs_moe_config* cfg,
+                     const obs_moe_layer* moe, const uint16_t* x, uint16_t* k_cache, uint16_t* v_cache_t,
+                     uint32_t max_len, float eps, float theta, const int32_t* state, uint16_t* x1,
+                     uint16_t* y, int32_t* ids_out, float* w_out);
+
 /* ------------------------------------------------------------------ */
 /* Prefill of the layers around the MoE block for a batch of tokens     */
 /* (Model::prefill_batched, forward.rs:114-160, :240-261)               */

@@ -252,6 +252,7 @@ void obs_destroy(obs_ctx* ctx) {
   if (ctx->decode_ws) (void)hipFree(ctx->decode_ws);
   if (ctx->fused_ws) (void)hipFree(ctx->fused_ws);
   if (ctx->attn_ws) (void)hipFree(ctx->attn_ws);
+  if (ctx->layer_ws) (void)hipFree(ctx->layer_ws);
   if (ctx->status_dev) (void)hipFree(ctx->status_dev);
   if (ctx->route_cnt) (void)hipFree(ctx->route_cnt);
   for (const auto& r : ctx->rope_tables) (void)hipFree(r.table);

@@ -374,7 +374,8 @@ int obs_device_status(obs_ctx* ctx) {
   const int b = obs::attn_fused_status(ctx);
   const int c = ctx->scratch_used ? obs::fused_decode_status_ws(ctx, ctx->scratch) : OBS_OK;
   const int f = obs::ffn_status(ctx);
-  return a != OBS_OK ? a : b != OBS_OK ? b : c != OBS_OK ? c : f;
+  const int l = obs::layer_fused_status(ctx);
+  return a != OBS_OK ? a : b != OBS_OK ? b : c != OBS_OK ? c : f != OBS_OK ? f : l;
 }
 
 }  // extern "C"

@@ -39,6 +39,9 @@ struct obs_ctx {
   void* fused_ws = nullptr;
   // fused attention-half workspace (exchange slots + counters), zeroed once
   void* attn_ws = nullptr;
+  // one-launch decode layer workspace (both halves' slots, the x1 slots and
+  // one launch counter), zeroed once
+  void* layer_ws = nullptr;
   // this device's file-scope scratch array (obs_moe_decode_static), looked up
   // once per device by obs_create; null if the lookup was not possible
   void* scratch = nullptr;
@@ -170,6 +173,16 @@ int fused_decode_status_ws(obs_ctx* ctx, void* ws);
 // device error flag, read and cleared (synchronizes).
 int attn_fused_status(obs_ctx* ctx);
 int ffn_status(obs_ctx* ctx);  // the one-launch prefill FFN's wait flag
+// The one-launch attention half's arguments (obs_attn_decode, obs_layer_decode).
+int check_attn_decode(obs_ctx* ctx, const char* who, const obs_attn_layer* L, const uint16_t* x,
+                      const uint16_t* k_cache, const uint16_t* v_cache_t, const int32_t* state, const uint16_t* x1,
+                      uint32_t max_len);
+// The MoE half's configuration and layer tensors (obs_decode.hip).
+int check_moe_config(obs_ctx* ctx, const char* who, const obs_moe_config* cfg);
+int check_moe_layer(obs_ctx* ctx, const char* who, const obs_moe_layer* L);
+// One-launch decode layer (obs_layer_fused.hip): its device error flags, read
+// and cleared (synchronizes).
+int layer_fused_status(obs_ctx* ctx);
 
 // The context's RoPE table for (theta, max_len) (obs_attention.hip): entry
 // [p][i] = (cos, sin) of fl32(p * fl32(theta^(-2i/128))), each evaluated in

@@ -61,7 +61,7 @@ EXPORTS = (
     "obs_ckpt_read", "obs_moe_layer_bytes", "obs_ckpt_load_moe_layer", "obs_ckpt_load_tensor",
     "obs_q4_gemv", "obs_attn_prep", "obs_sdpa_workspace", "obs_sdpa_decode", "obs_embed_q4",
     "obs_argmax_workspace", "obs_argmax", "obs_embed_q4_rows", "obs_attn_prep_rows", "obs_sdpa_prefill",
-    "obs_attn_decode", "obs_dispatch_gate", "obs_dispatch_info", "obs_set_dispatch_facts", "obs_debug_ffn_wait",
+    "obs_attn_decode", "obs_layer_decode", "obs_dispatch_gate", "obs_dispatch_info", "obs_set_dispatch_facts", "obs_debug_ffn_wait",
     "obs_measure_read", "obs_measure_mfma",
 )
 
@@ -191,6 +191,8 @@ def lib() -> C.CDLL:
                                      u32]),
         "obs_sdpa_prefill": (i32, [vp, vp, vp, vp, vp, u32, u32, u32, u32, u32, u32, u32]),
         "obs_attn_decode": (i32, [vp, C.POINTER(ObsAttnLayer), vp, vp, vp, u32, f32, f32, vp, vp]),
+        "obs_layer_decode": (i32, [vp, C.POINTER(ObsAttnLayer), C.POINTER(ObsMoeConfig), C.POINTER(ObsMoeLayer), vp,
+                                   vp, vp, u32, f32, f32, vp, vp, vp, vp, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -247,6 +249,7 @@ class ObsidianExecutor:
         if rc != OBS_OK:
             raise ObsError(rc, L.obs_create_error().decode())
         self.ctx = ctx.value
+        self.decode_path = OBS_DECODE_AUTO  # as obs_set_decode_path last set it
         self._bufs: List[DeviceBuffer] = []
 
     # -- errors ----------------------------------------------------------
@@ -299,6 +302,7 @@ class ObsidianExecutor:
 
     def set_decode_path(self, path: int) -> None:
         self._check(lib().obs_set_decode_path(self.ctx, int(path)))
+        self.decode_path = int(path)
 
     def device_status(self) -> None:
         """Raise if a one-launch kernel of this context recorded a device-side
@@ -483,6 +487,17 @@ class ObsidianExecutor:
         L = ObsAttnLayer(*(_ptr(layer[k]) for k in ObsAttnLayer.KEYS))
         self._check(lib().obs_attn_decode(self.ctx, C.byref(L), _ptr(x), _ptr(k_cache), _ptr(v_cache_t), max_len,
                                           float(eps), float(theta), _ptr(state), _ptr(x1)))
+
+    def layer_decode(self, layer: Dict, cfg: "MoeConfig", moe: "MoeLayer", x, k_cache, v_cache_t, max_len: int,
+                     eps: float, theta: float, state, x1, y, ids_out=None, w_out=None) -> None:
+        """forward_layer (forward.rs:398-443) in one launch: attn_decode
+        (x -> x1) then moe_decode with the post-attention norm (x1 -> y, x1 the
+        residual), bit for bit."""
+        L = ObsAttnLayer(*(_ptr(layer[k]) for k in ObsAttnLayer.KEYS))
+        c, m = cfg.to_c(), moe.to_c()
+        self._check(lib().obs_layer_decode(self.ctx, C.byref(L), C.byref(c), C.byref(m), _ptr(x), _ptr(k_cache),
+                                           _ptr(v_cache_t), max_len, float(eps), float(theta), _ptr(state), _ptr(x1),
+                                           _ptr(y), _ptr(ids_out), _ptr(w_out)))
 
     # -- prefill of the layers around the MoE block (forward.rs:114-160) --
     def embed_q4_rows(self, w, s, b, hidden: int, vocab: int, tokens, n_tokens: int, out, group: int = 64) -> None:

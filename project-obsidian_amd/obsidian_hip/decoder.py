@@ -19,7 +19,8 @@ from typing import Dict, List, Optional
 
 import numpy as np
 
-from . import OBS_PATH_FUSED_ATTN, DeviceBuffer, MoeConfig, MoeLayer, ObsError, ObsidianExecutor, _ptr, lib
+from . import (OBS_DECODE_MULTI, OBS_PATH_FUSED_ATTN, OBS_PATH_FUSED_DECODE, DeviceBuffer, MoeConfig, MoeLayer,
+               ObsError, ObsidianExecutor, _ptr, lib)
 
 
 @dataclass
@@ -88,6 +89,7 @@ class Model:
         self.graph: Optional[int] = None
         self._pf: Optional[Dict] = None      # prefill buffers, grown to the largest batch
         self.use_fused_attention = True      # one-launch attention half where the shape allows
+        self.use_fused_layer = True          # ... and both halves of a layer in one launch
         self.last_seq: List[int] = []        # the tokens whose keys and values the caches hold (run_turn)
         self.last_reused = 0
         self.last_prefilled = 0
@@ -102,12 +104,25 @@ class Model:
         return (self.use_fused_attention and (c.hidden, c.n_heads, c.n_kv, c.head_dim) == (2048, 32, 4, 128)
                 and bool(self.exe.paths() & OBS_PATH_FUSED_ATTN))
 
+    def fused_moe(self) -> bool:
+        """Whether the MoE half can share the attention half's launch
+        (obs_layer_decode): the one-launch MoE shape (hidden 2048, inter 768,
+        top-8, group 64, at most 256 experts) on a device whose dispatch allows
+        the one-launch decode, unless the context is set to the 4-launch path."""
+        m = self.moe_cfg
+        return ((m.hidden, m.inter, m.top_k, m.group) == (2048, 768, 8, 64) and m.n_exp <= 256
+                and bool(self.exe.paths() & OBS_PATH_FUSED_DECODE) and self.exe.decode_path != OBS_DECODE_MULTI)
+
     def forward_layer(self, il: int, ids_out=None, w_out=None) -> None:
         """self.x <- layer il of self.x at the state's position (ids_out, w_out:
         optional device buffers for the layer's routing)."""
         c, e, L = self.cfg, self.exe, self.layers[il]
         kc, vc = self.caches[il]
         qd, kvd = c.n_heads * c.head_dim, c.n_kv * c.head_dim
+        if self.fused_attention() and self.use_fused_layer and self.fused_moe():  # forward.rs:398-443, one launch
+            e.layer_decode(L, self.moe_cfg, L["moe"], self.x, kc, vc, c.max_len, c.rms_eps, c.rope_theta, self.state,
+                           self.x1, self.x, ids_out=ids_out, w_out=w_out)
+            return
         if self.fused_attention():  # forward.rs:403-418 in one launch
             e.attn_decode(L, self.x, kc, vc, c.max_len, c.rms_eps, c.rope_theta, self.state, self.x1)
             e.moe_decode(self.moe_cfg, L["moe"], self.x1, self.x, residual=self.x1, ids_out=ids_out, w_out=w_out)
