@@ -30,8 +30,13 @@ PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 # kernel -> (pattern of its rocprofv3 name, the sources it is compiled from)
 KERNELS = {
-    "decode_fused": (r"decode_fused_kernel<2, false>", ("csrc/obs_decode_fused.hip", "csrc/obs_internal.hpp")),
-    "decode_fused_norm": (r"decode_fused_kernel<2, true>", ("csrc/obs_decode_fused.hip", "csrc/obs_internal.hpp")),
+    "decode_fused": (r"decode_fused_kernel<2, false>",
+                     ("csrc/obs_decode_fused.hip", "csrc/obs_moe_half.hpp", "csrc/obs_internal.hpp")),
+    "decode_fused_norm": (r"decode_fused_kernel<2, true>",
+                          ("csrc/obs_decode_fused.hip", "csrc/obs_moe_half.hpp", "csrc/obs_internal.hpp")),
+    "layer_fused": (r"layer_fused_kernel<2>",
+                    ("csrc/obs_layer_fused.hip", "csrc/obs_attn_half.hpp", "csrc/obs_moe_half.hpp",
+                     "csrc/obs_internal.hpp")),
     "grouped_gemm_gateup": (r"grouped_gemm_kernel<1u, 3u>", ("csrc/obs_prefill.hip", "csrc/obs_internal.hpp")),
     "grouped_gemm_down": (r"grouped_gemm_kernel<2u, 5u>", ("csrc/obs_prefill.hip", "csrc/obs_internal.hpp")),
     "moe_ffn": (r"moe_ffn_kernel<2u>", ("csrc/obs_prefill.hip", "csrc/obs_internal.hpp")),
